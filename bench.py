@@ -1,0 +1,260 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X-native OxideForge compute core (one GPU).
+
+Headline (BASELINE.json metric, configs[2]): f32 GEMM C = A * B at
+M = N = K = 4096, TFLOP/s, with its fraction of the fp32-MFMA peak.  A "step"
+is one GEMM launch over inputs already resident in HBM; the timed region is
+bracketed by synchronisation and timed with HIP events on the stream the
+kernel runs on.  Secondary figures in the same JSON line: the 8192x1024x4096
+GEMM, the [8192,4096] transpose and the C2 row / elementwise kernels (GB/s,
+rotating over >= 512 MiB of buffers so the 256 MiB MALL cannot serve them),
+and the transformer executors when built.
+
+The CPU baseline is the oracle (oracle/oxforge_oracle.c, f64-accumulate
+GEMM) on a bounded sample of the same workload, multithreaded on the host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+       [--no-secondary] [--sweep]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "oxide-forge_amd"))
+sys.path.insert(0, ROOT)
+
+METRIC = "f32 GEMM TFLOP/s (% fp32-MFMA peak); transformer layer tokens/sec, 1 GPU"
+PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_launches(rt, fn, steps: int, warmup: int, stream=None) -> float:
+    """Average milliseconds of fn(i) over `steps` launches (events on stream)."""
+    for i in range(warmup):
+        fn(i)
+    rt.sync(stream)
+    e0, e1 = rt.event(), rt.event()
+    rt.record(e0, stream)
+    for i in range(steps):
+        fn(i)
+    rt.record(e1, stream)
+    ms = rt.elapsed_ms(e0, e1)
+    rt.sync(stream)
+    rt.event_destroy(e0)
+    rt.event_destroy(e1)
+    return ms / steps
+
+
+def load_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    summary (profiles/traffic.json), scaled by the copy-kernel calibration
+    factor recorded there; None if it has not been measured."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        data = json.load(open(path))
+        k = data["kernels"][kernel]
+        return int(round((k["fetch_kib"] + k["write_kib"]) * 1024 * data.get("copy_factor", 1.0)))
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def gemm_tflops(rt, orc, M, N, K, steps, warmup, seed=3):
+    A = orc.uniform((M, K), seed)
+    B = orc.uniform((K, N), seed + 1)
+    dA, dB, dC = rt.array(A), rt.array(B), rt.empty((M, N))
+    ms = time_launches(rt, lambda i: rt.gemm(dA, dB, dC, M, N, K), steps, warmup)
+    for d in (dA, dB, dC):
+        d.recycle()
+    return 2.0 * M * N * K / (ms * 1e-3) / 1e12, ms
+
+
+def rotating(rt, orc, shape, sets, seed):
+    base = rt.array(orc.normal(shape, seed))
+    bufs = [base]
+    for _ in range(sets - 1):
+        b = rt.empty(shape)
+        rt.copy(b, base)
+        bufs.append(b)
+    return bufs
+
+
+def secondary(rt, orc, steps, warmup, extended):
+    import oxforge
+
+    out = {}
+    log("gemm 8192x1024x4096")
+    t, ms = gemm_tflops(rt, orc, 8192, 1024, 4096, steps, warmup)
+    out["gemm_8192x1024x4096"] = {"tflops": round(t, 2), "ms": round(ms, 4),
+                                  "frac_mfma_peak": round(t / PEAK_FP32_MFMA_TFLOPS, 4)}
+
+    log("transpose 8192x4096")
+    R, C = 8192, 4096
+    xs = rotating(rt, orc, (R, C), 2, 21)
+    ys = [rt.empty((C, R)) for _ in range(2)]
+    ms = time_launches(rt, lambda i: rt.transpose(xs[i % 2], ys[i % 2], R, C), steps, warmup)
+    out["transpose_8192x4096"] = {"gbs": round(2 * R * C * 4 / (ms * 1e-3) / 1e9, 1),
+                                  "ms": round(ms, 4)}
+    for b in xs + ys:
+        b.recycle()
+
+    # C2: X [4096, 1024]; 32 rotating sets = 512 MiB per operand.
+    rows, cols, sets = 4096, 1024, 32
+    X = 4 * rows * cols
+    log("row ops 4096x1024")
+    xs = rotating(rt, orc, (rows, cols), sets, 2)
+    gs = rotating(rt, orc, (rows, cols), sets, 3)
+    ds = [rt.empty((rows, cols)) for _ in range(sets)]
+    gam = rt.array(orc.normal((cols,), 4, 1.0, 0.1))
+    bet = rt.array(orc.normal((cols,), 5, 0.0, 0.1))
+    dgam, dbet = rt.empty((cols,)), rt.empty((cols,))
+    rvec = rt.array(orc.normal((cols,), 6))
+    rsum = rt.empty((rows,))
+    cases = {
+        "softmax_fwd": (2 * X, lambda i: rt.softmax_rows(xs[i % sets], rows, cols)),
+        "layer_norm_fwd": (2 * X, lambda i: rt.layer_norm(xs[i % sets], rows, cols, gam, bet)),
+        "rms_norm_fwd": (2 * X, lambda i: rt.rms_norm(xs[i % sets], rows, cols, gam)),
+        "softmax_bwd": (3 * X, lambda i: rt.softmax_rows_bwd(xs[i % sets], gs[i % sets],
+                                                             ds[i % sets], rows, cols)),
+        "layer_norm_bwd": (3 * X, lambda i: rt.layer_norm_bwd(xs[i % sets], gs[i % sets],
+                                                              ds[i % sets], rows, cols, gam,
+                                                              dgam, dbet)),
+        "rms_norm_bwd": (3 * X, lambda i: rt.rms_norm_bwd(xs[i % sets], gs[i % sets],
+                                                          ds[i % sets], rows, cols, gam, dgam)),
+        "binary_add": (3 * X, lambda i: rt.binary(xs[i % sets], gs[i % sets], ds[i % sets],
+                                                  oxforge.ADD)),
+        "map_scale": (2 * X, lambda i: rt.map(ds[i % sets], oxforge.MAP_SCALE, 1.0)),
+        "by_rows_add": (2 * X, lambda i: rt.binary_assign_by_rows(ds[i % sets], rvec, rows, cols,
+                                                                  oxforge.ADD)),
+        "sum_rows": (X, lambda i: rt.sum_rows(xs[i % sets], rsum, rows, cols)),
+    }
+    if extended:
+        cases["map_gelu"] = (2 * X, lambda i: rt.map(ds[i % sets], oxforge.MAP_GELU))
+        cases["sum_cols"] = (X, lambda i: rt.sum_cols(xs[i % sets], dgam, rows, cols))
+    for name, (nbytes, fn) in cases.items():
+        ms = time_launches(rt, fn, max(steps, sets), warmup)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[f"{name}_4096x1024"] = {"gbs": round(gbs, 1), "us": round(ms * 1e3, 2),
+                                    "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+    for b in xs + gs + ds:
+        b.recycle()
+    return out
+
+
+def sweep(rt, orc, steps, warmup):
+    """Times every plain GEMM tile instance on the two C3 shapes."""
+    import oxforge
+    from oxforge import _lib
+
+    lib = oxforge.load()
+    res = {}
+    for (M, N, K) in [(4096, 4096, 4096), (8192, 1024, 4096)]:
+        A = orc.uniform((M, K), 3)
+        B = orc.uniform((K, N), 4)
+        dA, dB, dC = rt.array(A), rt.array(B), rt.empty((M, N))
+        for tag in ["128x128x16_2x2", "128x128x32_2x2", "128x64x16_2x2", "256x128x16_2x2",
+                    "128x256x16_2x2", "256x128x16_4x2"]:
+            key = f"{M}x{N}x{K}:{tag}"
+
+            def fn(i, tag=tag.encode()):
+                _lib.check(lib.forge_gemm_f32_tile(rt.handle, None, tag, dA.slice, dB.slice,
+                                                   dC.slice, M, N, K), "forge_gemm_f32_tile")
+
+            try:
+                ms = time_launches(rt, fn, steps, warmup)
+            except oxforge.ForgeError as e:
+                res[key] = f"error: {e}"
+                continue
+            res[key] = round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 2)
+            log(f"sweep {key}: {res[key]}")
+        for d in (dA, dB, dC):
+            d.recycle()
+    return res
+
+
+def cpu_baseline(orc, M, N, K):
+    """Oracle GEMM (f64 accumulate, all host threads up to 16) on 256 of the
+    M rows; scaled to TFLOP/s of the same workload."""
+    threads = min(16, os.cpu_count() or 1)
+    orc.set_threads(threads)
+    rows = 256
+    A = orc.uniform((rows, K), 3)
+    B = orc.uniform((K, N), 4)
+    t0 = time.perf_counter()
+    orc.gemm(A, B)
+    dt = time.perf_counter() - t0
+    return {"value": round(2.0 * rows * N * K / dt / 1e12, 5), "unit": "TFLOP/s",
+            "cores": threads, "kind": "port",
+            "sample": f"{rows} of {M} rows of the {M}x{N}x{K} GEMM (oracle, f64 accumulate), "
+                      f"{dt:.2f} s"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--extended", action="store_true")
+    ap.add_argument("--sweep", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE "
+              f"{world}); this build has no multi-GPU path.", file=sys.stderr)
+        return 2
+
+    import oxforge
+    from oracle import oracle as orc
+
+    rt = oxforge.Runtime(0)
+    props = rt.props()
+    log(f"device {props}")
+    M = N = K = 4096
+    log("gemm 4096^3")
+    tflops, ms = gemm_tflops(rt, orc, M, N, K, args.steps, args.warmup)
+    kernel = "forge_gemm_nn_128x128x16_2x2"
+    traffic = load_traffic(kernel)
+    line = {
+        "metric": METRIC,
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (SplitMix64 uniform(-1,1), seeds 3/4)",
+        "config": {"workload": "f32 GEMM C=A*B, M=N=K=4096, row-major (BASELINE configs[2])",
+                   "kernel": kernel, "device": props.get("arch")},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 3),
+                     "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": traffic},
+    }
+    if not args.no_secondary:
+        line["secondary"] = secondary(rt, orc, args.steps, args.warmup, args.extended)
+    if args.sweep:
+        line["sweep"] = sweep(rt, orc, args.steps, args.warmup)
+    if not args.no_cpu:
+        log("cpu baseline")
+        line["cpu_baseline"] = cpu_baseline(orc, M, N, K)
+    rt.close()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,313 @@
+/*
+ * oxforge.h -- C ABI of the MI355X-native OxideForge compute core.
+ *
+ * This is the drop-in boundary that replaces the cuda-oxide context, module
+ * and stream routing of the reference (src/cuda.rs, src/cuda/runtime.rs,
+ * src/cuda/span.rs and the #[cuda_module] kernel module
+ * src/cuda/device/module.rs:6-263).  Host code above it (the C++ classes in
+ * oxide-forge_amd/csrc/net, or a Rust shim) keeps the reference's
+ * CudaRuntime / Matrix / Vector / executor signatures.
+ *
+ * Conventions
+ *   - Every entry point returns forge_status; nothing aborts inside the
+ *     library.  forge_last_error() gives a thread-local detail string.
+ *   - Buffers are f32, contiguous, row-major, passed as forge_slice
+ *     {ptr,len} by value -- the #[repr(C)] DeviceSliceDescriptor /
+ *     DeviceSliceMutDescriptor of span.rs:7-11,45-49.  A slice shorter than
+ *     the shape it is used with is FORGE_EINVAL (the reference kernels
+ *     silently skip out-of-range indices instead).
+ *   - Kernel launches are asynchronous on `stream`; stream == NULL means the
+ *     runtime's primary stream (CudaRuntime::stream, runtime.rs:116-118).
+ *   - A runtime is not thread-safe; serialise calls on one runtime.
+ *   - Device code is loaded from a gfx950 code object with hipModuleLoad and
+ *     launched with hipModuleLaunchKernel.
+ */
+#ifndef OXFORGE_H
+#define OXFORGE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum forge_status {
+    FORGE_OK = 0,
+    FORGE_EINVAL = 1,    /* shape / argument precondition violated       */
+    FORGE_ENOMEM = 2,    /* device or host allocation failed             */
+    FORGE_EHIP = 3,      /* a HIP runtime call failed                    */
+    FORGE_ENOMODULE = 4, /* code object missing or a kernel not found    */
+    FORGE_ENODEV = 5     /* no HIP device / requested device absent      */
+} forge_status;
+
+typedef struct forge_runtime forge_runtime;
+typedef struct forge_stream forge_stream;
+
+/* span.rs:45-49 DeviceSliceMutDescriptor<f32> / span.rs:7-11
+ * DeviceSliceDescriptor<f32>; const-ness is by convention of each entry. */
+typedef struct forge_slice {
+    float *ptr;
+    size_t len;
+} forge_slice;
+
+/* BinaryOp, #[repr(u8)] (cuda.rs:3-10). */
+typedef enum forge_binary_op {
+    FORGE_ADD = 0,
+    FORGE_SUB = 1,
+    FORGE_MUL = 2,
+    FORGE_DIV = 3
+} forge_binary_op;
+
+/* The closures the reference passes to slice_for_each (module.rs:56-64),
+ * one device functor each.  p0 is the captured scalar where there is one. */
+typedef enum forge_map_op {
+    FORGE_MAP_SCALE = 0,     /* x * p0           matrix.rs:31, span.rs:282 */
+    FORGE_MAP_ADD = 1,       /* x + p0           matrix.rs:35              */
+    FORGE_MAP_GELU = 2,      /* Activation::Gelu.forward   linear.rs:30-33 */
+    FORGE_MAP_GELU_D = 3,    /* Activation::Gelu.derivative linear.rs:49-56 */
+    FORGE_MAP_RELU = 4,      /* linear.rs:34-40 */
+    FORGE_MAP_RELU_D = 5,    /* linear.rs:57-63 */
+    FORGE_MAP_SILU = 6,      /* linear.rs:41    */
+    FORGE_MAP_SILU_D = 7,    /* linear.rs:64-67 */
+    FORGE_MAP_EXP_SHIFT = 8, /* exp(x - p0)      vector.rs:50              */
+    FORGE_MAP_HALF_SQ = 9,   /* 0.5 * x * x      linear.rs:327             */
+    FORGE_MAP_IDENTITY = 10  /* x                linear.rs:29              */
+} forge_map_op;
+
+/* Activation applied in a GEMM epilogue (Activation, linear.rs:12-19). */
+typedef enum forge_activation {
+    FORGE_ACT_IDENTITY = 0,
+    FORGE_ACT_GELU = 1,
+    FORGE_ACT_RELU = 2,
+    FORGE_ACT_SILU = 3
+} forge_activation;
+
+/* ------------------------------------------------------------ lifecycle */
+
+/* CudaRuntime::new (runtime.rs:34-45): selects `device`, creates the primary
+ * non-blocking stream and loads the code object.  module_path NULL means
+ * the code object next to this library (oxforge_kernels.hsaco) or the path
+ * in $OXFORGE_KERNELS. */
+forge_status forge_runtime_create(int device, const char *module_path,
+                                  forge_runtime **out);
+/* Drop of CudaRuntime: frees pooled buffers, streams and the module. */
+forge_status forge_runtime_destroy(forge_runtime *rt);
+/* CudaRuntime::sync (runtime.rs:112-114); stream NULL = primary. */
+forge_status forge_sync(forge_runtime *rt, forge_stream *stream);
+/* Number of HIP devices visible (0 on a host without a GPU). */
+forge_status forge_device_count(int *count);
+/* Human-readable status and the last error detail of this thread. */
+const char *forge_status_string(forge_status status);
+const char *forge_last_error(void);
+/* Device properties used by the bench: CU count, LDS bytes per workgroup,
+ * peak clock in kHz and the architecture name (e.g. "gfx950"). */
+forge_status forge_device_props(forge_runtime *rt, int *cu_count,
+                                size_t *lds_bytes, int *clock_khz,
+                                char *arch, size_t arch_len);
+
+/* -------------------------------------------------------------- streams */
+
+/* create_extra_streams (runtime.rs:188-192): n new streams, each forked
+ * from the primary (they wait for everything queued on it so far). */
+forge_status forge_streams_create(forge_runtime *rt, size_t n,
+                                  forge_stream **out);
+/* fork_streams (runtime.rs:196-200): each stream waits on the primary. */
+forge_status forge_streams_fork(forge_runtime *rt, size_t n,
+                                forge_stream *const *streams);
+/* join_streams (runtime.rs:202-206): the primary waits on each stream. */
+forge_status forge_streams_join(forge_runtime *rt, size_t n,
+                                forge_stream *const *streams);
+/* CudaStream::join(other) as used at linear.rs:126 and matrix.rs:128:
+ * `waiter` waits for everything queued on `signaler` (NULL = primary).
+ * An event dependency; the host does not block. */
+forge_status forge_stream_wait(forge_runtime *rt, forge_stream *waiter,
+                               forge_stream *signaler);
+forge_status forge_stream_destroy(forge_runtime *rt, forge_stream *stream);
+
+/* --------------------------------------------------------------- events */
+
+/* Device-side timing on a stream.  No reference counterpart: the reference
+ * times with host wall clock around runtime.sync() (main.rs:54-65).  Used by
+ * the benchmark to time kernels on the stream they are launched on. */
+typedef struct forge_event forge_event;
+forge_status forge_event_create(forge_runtime *rt, forge_event **out);
+forge_status forge_event_record(forge_runtime *rt, forge_stream *stream,
+                                forge_event *ev);
+/* Milliseconds between two recorded events; waits for `end`. */
+forge_status forge_event_elapsed_ms(forge_runtime *rt, forge_event *start,
+                                    forge_event *end, float *ms);
+forge_status forge_event_destroy(forge_runtime *rt, forge_event *ev);
+
+/* --------------------------------------------------------------- memory */
+
+/* get_uninit_buffer (runtime.rs:47-55): pops an exact-size buffer from the
+ * pool or allocates one.  n == 0 yields {NULL, 0}. */
+forge_status forge_alloc(forge_runtime *rt, size_t n, forge_slice *out);
+/* get_zerod_buffer (runtime.rs:67-71): as forge_alloc, then zero-filled on
+ * the primary stream. */
+forge_status forge_alloc_zeroed(forge_runtime *rt, size_t n, forge_slice *out);
+/* recycle_buffer (runtime.rs:98-110): returns a buffer to the exact-size
+ * pool; pending uses must be ordered on the primary stream. */
+forge_status forge_recycle(forge_runtime *rt, forge_slice buf);
+/* Drop of a DeviceBuffer: releases the memory to the device. */
+forge_status forge_free(forge_runtime *rt, forge_slice buf);
+/* reserve_buffers (runtime.rs:75-91). */
+forge_status forge_reserve(forge_runtime *rt, size_t n, size_t count);
+/* Buffers currently held by the pool for size n (for tests). */
+forge_status forge_pool_count(forge_runtime *rt, size_t n, size_t *count);
+
+/* DeviceBuffer::from_host (matrix.rs:107): host -> device, ordered on the
+ * primary stream; returns once the host buffer may be reused. */
+forge_status forge_memcpy_h2d(forge_runtime *rt, forge_slice dst,
+                              const float *src, size_t n);
+/* to_host_vec (matrix.rs:11-13): device -> host; blocks until done. */
+forge_status forge_memcpy_d2h(forge_runtime *rt, float *dst, forge_slice src,
+                              size_t n);
+/* memcpy_dtod_async (runtime.rs:160-167, span.rs:450-457). */
+forge_status forge_memcpy_d2d(forge_runtime *rt, forge_stream *stream,
+                              forge_slice dst, forge_slice src, size_t n);
+/* zero_async (runtime.rs:69): a fill kernel, never hipMemsetAsync, so the
+ * call is safe inside a captured graph. */
+forge_status forge_fill(forge_runtime *rt, forge_stream *stream,
+                        forge_slice x, float value);
+
+/* -------------------------------------------------------------- kernels */
+
+/* matrix_multiply / matrix_multiply_into_on (matrix.rs:113-176, kernel
+ * gemm.rs:202-373): C[M,N] = A[M,K] * B[K,N], row-major, C overwritten.
+ * True fp32 (v_mfma_f32_32x32x2_f32), not the reference's TF32.  Any
+ * M, N, K >= 0 (the reference asserts multiples of 16). */
+forge_status forge_gemm_f32(forge_runtime *rt, forge_stream *stream,
+                            forge_slice A, forge_slice B, forge_slice C,
+                            size_t M, size_t N, size_t K);
+
+/* Fused GEMM used by the executors (no reference counterpart as one call;
+ * it fuses the launch sequence of Linear::affine_on + activate_on,
+ * linear.rs:185-230, and of Linear::learn_on, linear.rs:393-415):
+ *   op(A) = trans_a ? A^T (A stored [K,M]) : A (stored [M,K])
+ *   op(B) = trans_b ? B^T (B stored [N,K]) : B (stored [K,N])
+ *   Z = alpha * op(A) op(B)
+ *   if bias:     Z = Z + bias[col]           (by-rows add, rows.rs:8-42)
+ *   if residual: Z = Z + residual            (binary_assign, matrix.rs:38)
+ *   if aux_mul:  Z = Z * aux_mul             (gradient * act'(z), linear.rs:264)
+ *   if pre_out:  pre_out = Z
+ *   Y = act(Z)
+ *   if update:   C = C - update_scale * Y    (SGD, linear.rs:383-384)
+ *   else         C = Y
+ * Every optional operand is a slice with ptr == NULL when absent.  Each step
+ * is one rounded f32 operation, so the result is bit-identical to the
+ * reference's separate launches given the same product. */
+typedef struct forge_gemm_epilogue {
+    float alpha;           /* 1.0f for a plain product                     */
+    forge_slice bias;      /* [N] or {NULL,0}                              */
+    forge_slice residual;  /* [M,N] or {NULL,0}                            */
+    forge_slice aux_mul;   /* [M,N] or {NULL,0}                            */
+    forge_slice pre_out;   /* [M,N] or {NULL,0}: stores Z before act       */
+    int activation;        /* forge_activation                            */
+    int update;            /* 0: C = Y; 1: C = C - update_scale * Y        */
+    float update_scale;    /* learning rate for update == 1                */
+} forge_gemm_epilogue;
+
+forge_status forge_gemm_ex_f32(forge_runtime *rt, forge_stream *stream,
+                               int trans_a, int trans_b, forge_slice A,
+                               forge_slice B, forge_slice C, size_t M,
+                               size_t N, size_t K,
+                               const forge_gemm_epilogue *epilogue);
+
+/* Tuning entry point (no reference counterpart): forge_gemm_f32 with an
+ * explicit plain tile instance, tile_tag "<BM>x<BN>x<BK>_<WM>x<WN>" (for
+ * example "128x128x16_2x2").  Unguarded tiles require M % BM == N % BN ==
+ * K % BK == 0 and 16-byte aligned operands; anything else is FORGE_EINVAL.
+ * Used by the benchmark's tile sweep. */
+forge_status forge_gemm_f32_tile(forge_runtime *rt, forge_stream *stream,
+                                 const char *tile_tag, forge_slice A,
+                                 forge_slice B, forge_slice C, size_t M,
+                                 size_t N, size_t K);
+
+/* matrix_transpose (convert.rs:17-63 -> layout.rs:8-55):
+ * out[c,r] = in[r,c]; in is [rows,cols]. Bit-exact. */
+forge_status forge_transpose_f32(forge_runtime *rt, forge_stream *stream,
+                                 forge_slice in, forge_slice out, size_t rows,
+                                 size_t cols);
+
+/* Matrix::softmax_rows (norm.rs:8-24 -> row.rs:55-113), in place. */
+forge_status forge_softmax_rows(forge_runtime *rt, forge_stream *stream,
+                                forge_slice x, size_t rows, size_t cols);
+/* softmax_rows_backward (norm.rs:73-101 -> row.rs:193-237):
+ * dx = p * (g - sum(p * g)).  dx may not alias p or g. */
+forge_status forge_softmax_rows_bwd(forge_runtime *rt, forge_stream *stream,
+                                    forge_slice p, forge_slice g,
+                                    forge_slice dx, size_t rows, size_t cols);
+
+/* Matrix::layer_norm (norm.rs:26-48 -> row.rs:115-177), in place.
+ * gamma/beta ({NULL,0} = reference path) are the affine extension. */
+forge_status forge_layer_norm_rows(forge_runtime *rt, forge_stream *stream,
+                                   forge_slice x, forge_slice gamma,
+                                   forge_slice beta, size_t rows, size_t cols,
+                                   float eps);
+/* layer_norm_backward (norm.rs:103-127 -> row.rs:239-347).  dgamma/dbeta
+ * ({NULL,0} to skip) receive column sums over all rows. */
+forge_status forge_layer_norm_bwd(forge_runtime *rt, forge_stream *stream,
+                                  forge_slice x, forge_slice dy,
+                                  forge_slice gamma, forge_slice dx,
+                                  forge_slice dgamma, forge_slice dbeta,
+                                  size_t rows, size_t cols, float eps);
+/* Matrix::rms_norm (norm.rs:50-69 -> row.rs:349-396), in place. */
+forge_status forge_rms_norm_rows(forge_runtime *rt, forge_stream *stream,
+                                 forge_slice x, forge_slice gamma, size_t rows,
+                                 size_t cols, float eps);
+/* rms_norm_backward (norm.rs:129-158 -> row.rs:398-468). */
+forge_status forge_rms_norm_bwd(forge_runtime *rt, forge_stream *stream,
+                                forge_slice x, forge_slice dy,
+                                forge_slice gamma, forge_slice dx,
+                                forge_slice dgamma, size_t rows, size_t cols,
+                                float eps);
+
+/* matrix_binary / vector_binary (matrix.rs:194-219 -> elementwise.rs:45-56):
+ * o = l op r over n elements.  Bit-exact. */
+forge_status forge_binary(forge_runtime *rt, forge_stream *stream,
+                          forge_slice l, forge_slice r, forge_slice o,
+                          size_t n, forge_binary_op op);
+/* binary_assign (matrix.rs:38-64 -> elementwise.rs:58-68): t = t op r. */
+forge_status forge_binary_assign(forge_runtime *rt, forge_stream *stream,
+                                 forge_slice t, forge_slice r, size_t n,
+                                 forge_binary_op op);
+/* binary_assign_by_rows (rows.rs:8-42 -> row.rs:179-191):
+ * M[i] = M[i] op row[i mod cols]. */
+forge_status forge_binary_assign_by_rows(forge_runtime *rt,
+                                         forge_stream *stream, forge_slice m,
+                                         forge_slice row, size_t rows,
+                                         size_t cols, forge_binary_op op);
+/* for_each (span.rs:261-279 -> elementwise.rs:70-79): x = f(x). */
+forge_status forge_map(forge_runtime *rt, forge_stream *stream, forge_slice x,
+                       size_t n, forge_map_op op, float p0);
+
+/* matrix_sum_rows (rows.rs:45-88 -> row.rs:16-53): out[r] = sum_j M[r,j]. */
+forge_status forge_sum_rows(forge_runtime *rt, forge_stream *stream,
+                            forge_slice m, forge_slice out, size_t rows,
+                            size_t cols);
+/* Column sums, replacing the transpose + sum_rows pair of the bias
+ * gradient (linear.rs:267-272): out[c] = sum_r M[r,c]. */
+forge_status forge_sum_cols(forge_runtime *rt, forge_stream *stream,
+                            forge_slice m, forge_slice out, size_t rows,
+                            size_t cols);
+/* Vector::sum / Vector::max (span.rs:301-333 -> reduction.rs:4-41,93-130):
+ * full reduction of x into out[0] on the device (no host round trip; the
+ * caller reads it back when it needs the scalar). */
+forge_status forge_reduce_sum(forge_runtime *rt, forge_stream *stream,
+                              forge_slice x, size_t n, forge_slice out);
+forge_status forge_reduce_max(forge_runtime *rt, forge_stream *stream,
+                              forge_slice x, size_t n, forge_slice out);
+
+/* slice_set_seq (elementwise.rs:23-34): i (ascending) or n - i. */
+forge_status forge_fill_seq(forge_runtime *rt, forge_stream *stream,
+                            forge_slice x, size_t n, int ascending);
+/* Matrix::causal_mask (matrix.rs:79-92 -> row.rs:5-14). */
+forge_status forge_causal_mask(forge_runtime *rt, forge_stream *stream,
+                               forge_slice m, size_t rows, size_t cols);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,236 @@
+"""numpy front end of the CPU oracle (oracle/oxforge_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: the parity checker for the HIP path and the timed
+CPU baseline of bench.py.  Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may import this module; the product (oxide-forge_amd/) never
+does.  See oxforge_oracle.h for the reference lines each function restates.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_double, c_float, c_int, c_size_t, c_uint64
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "liboxforge_oracle.so")
+
+ADD, SUB, MUL, DIV = 0, 1, 2, 3
+MAP_SCALE, MAP_ADD, MAP_GELU, MAP_GELU_D, MAP_RELU, MAP_RELU_D = 0, 1, 2, 3, 4, 5
+MAP_SILU, MAP_SILU_D, MAP_EXP_SHIFT, MAP_HALF_SQ, MAP_IDENTITY = 6, 7, 8, 9, 10
+
+_F = POINTER(c_float)
+_D = POINTER(c_double)
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError(f"{LIB_PATH} missing: run `make -C oracle`")
+        L = ctypes.CDLL(LIB_PATH)
+        sig = {
+            "orc_set_threads": ([c_int], None),
+            "orc_get_threads": ([], c_int),
+            "orc_gemm": ([_F, _F, _F, c_size_t, c_size_t, c_size_t, c_int, c_int], None),
+            "orc_gemm_f64": ([_F, _F, _D, c_size_t, c_size_t, c_size_t, c_int, c_int], None),
+            "orc_transpose": ([_F, _F, c_size_t, c_size_t], None),
+            "orc_softmax_rows": ([_F, c_size_t, c_size_t], None),
+            "orc_softmax_rows_backward": ([_F, _F, _F, c_size_t, c_size_t], None),
+            "orc_layer_norm_rows": ([_F, _F, _F, c_size_t, c_size_t, c_float], None),
+            "orc_layer_norm_backward": ([_F, _F, _F, _F, _F, _F, c_size_t, c_size_t, c_float], None),
+            "orc_rms_norm_rows": ([_F, _F, c_size_t, c_size_t, c_float], None),
+            "orc_rms_norm_backward": ([_F, _F, _F, _F, _F, c_size_t, c_size_t, c_float], None),
+            "orc_binary": ([_F, _F, _F, c_size_t, c_int], None),
+            "orc_binary_assign": ([_F, _F, c_size_t, c_int], None),
+            "orc_binary_assign_by_rows": ([_F, _F, c_size_t, c_size_t, c_int], None),
+            "orc_map": ([_F, c_size_t, c_int, c_float], None),
+            "orc_sum_rows": ([_F, _F, c_size_t, c_size_t], None),
+            "orc_sum_cols": ([_F, _F, c_size_t, c_size_t], None),
+            "orc_reduce_sum": ([_F, c_size_t], c_float),
+            "orc_reduce_max": ([_F, c_size_t], c_float),
+            "orc_fill_seq": ([_F, c_size_t, c_int], None),
+            "orc_causal_mask": ([_F, c_size_t, c_size_t], None),
+            "orc_fill_uniform": ([_F, c_size_t, c_uint64, c_float, c_float], None),
+            "orc_fill_normal": ([_F, c_size_t, c_uint64, c_float, c_float], None),
+        }
+        for name, (args, res) in sig.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray):
+    if a is None:
+        return None
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_F)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def set_threads(n: int) -> None:
+    lib().orc_set_threads(int(n))
+
+
+# ------------------------------------------------------------- synthetic data
+def uniform(shape, seed: int, lo: float = -1.0, hi: float = 1.0) -> np.ndarray:
+    out = np.empty(shape, dtype=np.float32)
+    lib().orc_fill_uniform(_p(out), out.size, seed, lo, hi)
+    return out
+
+
+def normal(shape, seed: int, mu: float = 0.0, sigma: float = 1.0) -> np.ndarray:
+    out = np.empty(shape, dtype=np.float32)
+    lib().orc_fill_normal(_p(out), out.size, seed, mu, sigma)
+    return out
+
+
+def xavier(fan_in: int, fan_out: int, seed: int) -> np.ndarray:
+    """Xavier-uniform U(+-sqrt(6/(fan_in+fan_out))) of shape [fan_in, fan_out]."""
+    lim = float(np.sqrt(6.0 / (fan_in + fan_out)))
+    return uniform((fan_in, fan_out), seed, -lim, lim)
+
+
+# ------------------------------------------------------------------- kernels
+def gemm(A, B, trans_a=False, trans_b=False) -> np.ndarray:
+    A, B = _f32(A), _f32(B)
+    M = A.shape[1] if trans_a else A.shape[0]
+    K = A.shape[0] if trans_a else A.shape[1]
+    N = B.shape[0] if trans_b else B.shape[1]
+    C = np.empty((M, N), dtype=np.float32)
+    lib().orc_gemm(_p(A), _p(B), _p(C), M, N, K, int(trans_a), int(trans_b))
+    return C
+
+
+def gemm_f64(A, B, trans_a=False, trans_b=False) -> np.ndarray:
+    A, B = _f32(A), _f32(B)
+    M = A.shape[1] if trans_a else A.shape[0]
+    K = A.shape[0] if trans_a else A.shape[1]
+    N = B.shape[0] if trans_b else B.shape[1]
+    C = np.empty((M, N), dtype=np.float64)
+    lib().orc_gemm_f64(_p(A), _p(B), C.ctypes.data_as(_D), M, N, K, int(trans_a), int(trans_b))
+    return C
+
+
+def transpose(x) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty((x.shape[1], x.shape[0]), dtype=np.float32)
+    lib().orc_transpose(_p(x), _p(out), x.shape[0], x.shape[1])
+    return out
+
+
+def softmax_rows(x) -> np.ndarray:
+    y = _f32(x).copy()
+    lib().orc_softmax_rows(_p(y), y.shape[0], y.shape[1])
+    return y
+
+
+def softmax_rows_backward(p, g) -> np.ndarray:
+    p, g = _f32(p), _f32(g)
+    dx = np.empty_like(p)
+    lib().orc_softmax_rows_backward(_p(p), _p(g), _p(dx), p.shape[0], p.shape[1])
+    return dx
+
+
+def layer_norm(x, gamma=None, beta=None, eps=1e-5) -> np.ndarray:
+    y = _f32(x).copy()
+    g = None if gamma is None else _f32(gamma)
+    b = None if beta is None else _f32(beta)
+    lib().orc_layer_norm_rows(_p(y), _p(g), _p(b), y.shape[0], y.shape[1], eps)
+    return y
+
+
+def layer_norm_backward(x, dy, gamma=None, eps=1e-5, want_params=False):
+    x, dy = _f32(x), _f32(dy)
+    g = None if gamma is None else _f32(gamma)
+    dx = np.empty_like(x)
+    dg = np.empty(x.shape[1], np.float32) if want_params else None
+    db = np.empty(x.shape[1], np.float32) if want_params else None
+    lib().orc_layer_norm_backward(_p(x), _p(dy), _p(g), _p(dx), _p(dg), _p(db), x.shape[0],
+                                  x.shape[1], eps)
+    return (dx, dg, db) if want_params else dx
+
+
+def rms_norm(x, gamma=None, eps=1e-5) -> np.ndarray:
+    y = _f32(x).copy()
+    g = None if gamma is None else _f32(gamma)
+    lib().orc_rms_norm_rows(_p(y), _p(g), y.shape[0], y.shape[1], eps)
+    return y
+
+
+def rms_norm_backward(x, dy, gamma=None, eps=1e-5, want_params=False):
+    x, dy = _f32(x), _f32(dy)
+    g = None if gamma is None else _f32(gamma)
+    dx = np.empty_like(x)
+    dg = np.empty(x.shape[1], np.float32) if want_params else None
+    lib().orc_rms_norm_backward(_p(x), _p(dy), _p(g), _p(dx), _p(dg), x.shape[0], x.shape[1],
+                                eps)
+    return (dx, dg) if want_params else dx
+
+
+def binary(l, r, op) -> np.ndarray:
+    l, r = _f32(l), _f32(r)
+    o = np.empty_like(l)
+    lib().orc_binary(_p(l), _p(r), _p(o), l.size, op)
+    return o
+
+
+def binary_assign(t, r, op) -> np.ndarray:
+    t = _f32(t).copy()
+    lib().orc_binary_assign(_p(t), _p(_f32(r)), t.size, op)
+    return t
+
+
+def binary_assign_by_rows(m, row, op) -> np.ndarray:
+    m = _f32(m).copy()
+    lib().orc_binary_assign_by_rows(_p(m), _p(_f32(row)), m.shape[0], m.shape[1], op)
+    return m
+
+
+def map_(x, op, p0=0.0) -> np.ndarray:
+    y = _f32(x).copy()
+    lib().orc_map(_p(y), y.size, op, p0)
+    return y
+
+
+def sum_rows(m) -> np.ndarray:
+    m = _f32(m)
+    out = np.empty(m.shape[0], np.float32)
+    lib().orc_sum_rows(_p(m), _p(out), m.shape[0], m.shape[1])
+    return out
+
+
+def sum_cols(m) -> np.ndarray:
+    m = _f32(m)
+    out = np.empty(m.shape[1], np.float32)
+    lib().orc_sum_cols(_p(m), _p(out), m.shape[0], m.shape[1])
+    return out
+
+
+def reduce_sum(x) -> float:
+    x = _f32(x)
+    return float(lib().orc_reduce_sum(_p(x), x.size))
+
+
+def reduce_max(x) -> float:
+    x = _f32(x)
+    return float(lib().orc_reduce_max(_p(x), x.size))
+
+
+def fill_seq(n, ascending=True) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().orc_fill_seq(_p(out), n, int(ascending))
+    return out
+
+
+def causal_mask(m) -> np.ndarray:
+    m = _f32(m).copy()
+    lib().orc_causal_mask(_p(m), m.shape[0], m.shape[1])
+    return m

@@ -1,0 +1,492 @@
+/*
+ * oxforge_oracle.c -- CPU restatement of the OxideForge compute-core math.
+ *
+ * TEST INFRASTRUCTURE ONLY (see oxforge_oracle.h): the parity checker and
+ * the timed CPU baseline.  Built with -ffp-contract=off so every f32
+ * expression rounds after each operation, like the reference's scalar code.
+ */
+#include "oxforge_oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+static int g_threads = 1;
+
+void orc_set_threads(int threads) { g_threads = threads < 1 ? 1 : threads; }
+int orc_get_threads(void) { return g_threads; }
+
+/* ---------------------------------------------------------------- threads */
+
+typedef void (*row_fn)(void *ctx, size_t begin, size_t end);
+
+typedef struct {
+    row_fn fn;
+    void *ctx;
+    size_t begin, end;
+} row_job;
+
+static void *row_job_main(void *arg) {
+    row_job *job = (row_job *)arg;
+    job->fn(job->ctx, job->begin, job->end);
+    return NULL;
+}
+
+/* Splits [0,n) into contiguous chunks, one per thread. */
+static void parallel_rows(size_t n, row_fn fn, void *ctx) {
+    int t = g_threads;
+    if ((size_t)t > n) t = (int)n;
+    if (t <= 1) {
+        fn(ctx, 0, n);
+        return;
+    }
+    pthread_t tid[256];
+    row_job jobs[256];
+    if (t > 256) t = 256;
+    size_t chunk = (n + (size_t)t - 1) / (size_t)t;
+    int launched = 0;
+    for (int i = 0; i < t; i++) {
+        size_t b = (size_t)i * chunk, e = b + chunk;
+        if (b >= n) break;
+        if (e > n) e = n;
+        jobs[i].fn = fn;
+        jobs[i].ctx = ctx;
+        jobs[i].begin = b;
+        jobs[i].end = e;
+        if (pthread_create(&tid[i], NULL, row_job_main, &jobs[i]) != 0) {
+            fn(ctx, b, e); /* run inline if a thread cannot start */
+            jobs[i].fn = NULL;
+        }
+        launched = i + 1;
+    }
+    for (int i = 0; i < launched; i++)
+        if (jobs[i].fn) pthread_join(tid[i], NULL);
+}
+
+/* ------------------------------------------------------------------- GEMM */
+
+typedef struct {
+    const float *A, *B;
+    float *C;
+    double *C64;
+    size_t M, N, K;
+    int ta, tb;
+} gemm_ctx;
+
+/* C[i,j] = sum_k opA[i,k] * opB[k,j], f64 accumulate.  The reference kernel
+ * (gemm.rs:15-129 strict fp32; gemm.rs:202-373 TF32) overwrites C with the
+ * product and takes no alpha/beta (gemm.rs:117-128, 362-372). */
+static void gemm_rows(void *p, size_t i0, size_t i1) {
+    gemm_ctx *g = (gemm_ctx *)p;
+    const size_t M = g->M, N = g->N, K = g->K;
+    double *acc = (double *)malloc(N * sizeof(double));
+    if (!acc) abort();
+    for (size_t i = i0; i < i1; i++) {
+        if (!g->tb) {
+            /* i-k-j order: a contiguous sweep over a row of B. */
+            memset(acc, 0, N * sizeof(double));
+            for (size_t k = 0; k < K; k++) {
+                double a = g->ta ? (double)g->A[k * M + i]
+                                 : (double)g->A[i * K + k];
+                const float *brow = g->B + k * N;
+                for (size_t j = 0; j < N; j++) acc[j] += a * (double)brow[j];
+            }
+        } else {
+            /* B stored [N,K]: each output is a contiguous dot product. */
+            for (size_t j = 0; j < N; j++) {
+                const float *bcol = g->B + j * K;
+                double s = 0.0;
+                if (!g->ta) {
+                    const float *arow = g->A + i * K;
+                    for (size_t k = 0; k < K; k++)
+                        s += (double)arow[k] * (double)bcol[k];
+                } else {
+                    for (size_t k = 0; k < K; k++)
+                        s += (double)g->A[k * M + i] * (double)bcol[k];
+                }
+                acc[j] = s;
+            }
+        }
+        if (g->C)
+            for (size_t j = 0; j < N; j++) g->C[i * N + j] = (float)acc[j];
+        if (g->C64)
+            for (size_t j = 0; j < N; j++) g->C64[i * N + j] = acc[j];
+    }
+    free(acc);
+}
+
+void orc_gemm(const float *A, const float *B, float *C, size_t M, size_t N,
+              size_t K, int trans_a, int trans_b) {
+    gemm_ctx g = {A, B, C, NULL, M, N, K, trans_a, trans_b};
+    parallel_rows(M, gemm_rows, &g);
+}
+
+void orc_gemm_f64(const float *A, const float *B, double *C, size_t M,
+                  size_t N, size_t K, int trans_a, int trans_b) {
+    gemm_ctx g = {A, B, NULL, C, M, N, K, trans_a, trans_b};
+    parallel_rows(M, gemm_rows, &g);
+}
+
+/* -------------------------------------------------------------- transpose */
+
+void orc_transpose(const float *in, float *out, size_t rows, size_t cols) {
+    /* layout.rs:29,46-51: out[c * rows + r] = in[r * cols + c]. */
+    for (size_t r = 0; r < rows; r++)
+        for (size_t c = 0; c < cols; c++) out[c * rows + r] = in[r * cols + c];
+}
+
+/* --------------------------------------------------------------- row ops */
+
+typedef struct {
+    float *x;
+    const float *a, *b, *g;
+    float *out;
+    size_t cols;
+    float eps;
+} row_ctx;
+
+/* row.rs:55-113: m = max_j x_j (identity f32::MIN for inactive lanes);
+ * e_j = exp(x_j - m); y_j = e_j / sum(e). */
+static void softmax_rows_fn(void *p, size_t r0, size_t r1) {
+    row_ctx *c = (row_ctx *)p;
+    for (size_t r = r0; r < r1; r++) {
+        float *x = c->x + r * c->cols;
+        double m = -FLT_MAX;
+        for (size_t j = 0; j < c->cols; j++)
+            if ((double)x[j] > m) m = (double)x[j];
+        double s = 0.0;
+        for (size_t j = 0; j < c->cols; j++) s += exp((double)x[j] - m);
+        for (size_t j = 0; j < c->cols; j++)
+            x[j] = (float)(exp((double)x[j] - m) / s);
+    }
+}
+
+void orc_softmax_rows(float *x, size_t rows, size_t cols) {
+    row_ctx c = {x, NULL, NULL, NULL, NULL, cols, 0.f};
+    parallel_rows(rows, softmax_rows_fn, &c);
+}
+
+/* row.rs:193-237: s = sum_j p_j g_j; dx_j = p_j (g_j - s). */
+static void softmax_bwd_fn(void *p, size_t r0, size_t r1) {
+    row_ctx *c = (row_ctx *)p;
+    for (size_t r = r0; r < r1; r++) {
+        const float *pr = c->a + r * c->cols, *gr = c->b + r * c->cols;
+        float *dx = c->out + r * c->cols;
+        double s = 0.0;
+        for (size_t j = 0; j < c->cols; j++) s += (double)pr[j] * (double)gr[j];
+        for (size_t j = 0; j < c->cols; j++)
+            dx[j] = (float)((double)pr[j] * ((double)gr[j] - s));
+    }
+}
+
+void orc_softmax_rows_backward(const float *p, const float *g, float *dx,
+                               size_t rows, size_t cols) {
+    row_ctx c = {NULL, p, g, NULL, dx, cols, 0.f};
+    parallel_rows(rows, softmax_bwd_fn, &c);
+}
+
+/* Mean and 1/sqrt(var + eps) of one row, as row.rs:130-170 computes them. */
+static void ln_stats(const float *x, size_t n, float eps, double *mean,
+                     double *rstd) {
+    double s = 0.0;
+    for (size_t j = 0; j < n; j++) s += (double)x[j];
+    double mu = s / (double)n;
+    double v = 0.0;
+    for (size_t j = 0; j < n; j++) {
+        double d = (double)x[j] - mu;
+        v += d * d;
+    }
+    *mean = mu;
+    *rstd = 1.0 / sqrt(v / (double)n + (double)eps);
+}
+
+/* row.rs:115-177; extension y = gamma_j * xhat_j + beta_j. */
+static void layer_norm_fn(void *p, size_t r0, size_t r1) {
+    row_ctx *c = (row_ctx *)p;
+    for (size_t r = r0; r < r1; r++) {
+        float *x = c->x + r * c->cols;
+        double mu, rs;
+        ln_stats(x, c->cols, c->eps, &mu, &rs);
+        for (size_t j = 0; j < c->cols; j++) {
+            double y = ((double)x[j] - mu) * rs;
+            if (c->g) y *= (double)c->g[j];
+            if (c->b) y += (double)c->b[j];
+            x[j] = (float)y;
+        }
+    }
+}
+
+void orc_layer_norm_rows(float *x, const float *gamma, const float *beta,
+                         size_t rows, size_t cols, float eps) {
+    row_ctx c = {x, NULL, beta, gamma, NULL, cols, eps};
+    parallel_rows(rows, layer_norm_fn, &c);
+}
+
+/* row.rs:239-347: recompute mu, r, xhat; A = sum g; B = sum g*xhat;
+ * dx = r/n * (n*g - A - xhat*B), where g = dy (reference) or dy*gamma. */
+static void layer_norm_bwd_fn(void *p, size_t r0, size_t r1) {
+    row_ctx *c = (row_ctx *)p;
+    const size_t n = c->cols;
+    for (size_t r = r0; r < r1; r++) {
+        const float *x = c->a + r * n, *dy = c->b + r * n;
+        float *dx = c->out + r * n;
+        double mu, rs;
+        ln_stats(x, n, c->eps, &mu, &rs);
+        double A = 0.0, B = 0.0;
+        for (size_t j = 0; j < n; j++) {
+            double g = (double)dy[j] * (c->g ? (double)c->g[j] : 1.0);
+            double xh = ((double)x[j] - mu) * rs;
+            A += g;
+            B += g * xh;
+        }
+        for (size_t j = 0; j < n; j++) {
+            double g = (double)dy[j] * (c->g ? (double)c->g[j] : 1.0);
+            double xh = ((double)x[j] - mu) * rs;
+            dx[j] = (float)(rs / (double)n * ((double)n * g - A - xh * B));
+        }
+    }
+}
+
+void orc_layer_norm_backward(const float *x, const float *dy,
+                             const float *gamma, float *dx, float *dgamma,
+                             float *dbeta, size_t rows, size_t cols,
+                             float eps) {
+    row_ctx c = {NULL, x, dy, gamma, dx, cols, eps};
+    parallel_rows(rows, layer_norm_bwd_fn, &c);
+    if (dgamma || dbeta) {
+        /* dgamma_j = sum_rows dy * xhat; dbeta_j = sum_rows dy. */
+        double *sg = (double *)calloc(cols, sizeof(double));
+        double *sb = (double *)calloc(cols, sizeof(double));
+        if (!sg || !sb) abort();
+        for (size_t r = 0; r < rows; r++) {
+            double mu, rs;
+            ln_stats(x + r * cols, cols, eps, &mu, &rs);
+            for (size_t j = 0; j < cols; j++) {
+                double d = (double)dy[r * cols + j];
+                sg[j] += d * ((double)x[r * cols + j] - mu) * rs;
+                sb[j] += d;
+            }
+        }
+        for (size_t j = 0; j < cols; j++) {
+            if (dgamma) dgamma[j] = (float)sg[j];
+            if (dbeta) dbeta[j] = (float)sb[j];
+        }
+        free(sg);
+        free(sb);
+    }
+}
+
+static double rms_of(const float *x, size_t n, float eps) {
+    double q = 0.0;
+    for (size_t j = 0; j < n; j++) q += (double)x[j] * (double)x[j];
+    return sqrt(q / (double)n + (double)eps);
+}
+
+/* row.rs:349-396: y = x / sqrt(sum(x^2)/n + eps) -- a division by the
+ * root; extension y = gamma_j * (x_j / rms). */
+static void rms_norm_fn(void *p, size_t r0, size_t r1) {
+    row_ctx *c = (row_ctx *)p;
+    for (size_t r = r0; r < r1; r++) {
+        float *x = c->x + r * c->cols;
+        double rms = rms_of(x, c->cols, c->eps);
+        for (size_t j = 0; j < c->cols; j++) {
+            double y = (double)x[j] / rms;
+            if (c->g) y *= (double)c->g[j];
+            x[j] = (float)y;
+        }
+    }
+}
+
+void orc_rms_norm_rows(float *x, const float *gamma, size_t rows, size_t cols,
+                       float eps) {
+    row_ctx c = {x, NULL, NULL, gamma, NULL, cols, eps};
+    parallel_rows(rows, rms_norm_fn, &c);
+}
+
+/* row.rs:398-468: q = sum x^2, d = sum x*g; inv = 1/sqrt(q/n + eps);
+ * dx = g*inv - x * (d/n * inv^3), with g = dy (reference) or dy*gamma. */
+static void rms_norm_bwd_fn(void *p, size_t r0, size_t r1) {
+    row_ctx *c = (row_ctx *)p;
+    const size_t n = c->cols;
+    for (size_t r = r0; r < r1; r++) {
+        const float *x = c->a + r * n, *dy = c->b + r * n;
+        float *dx = c->out + r * n;
+        double inv = 1.0 / rms_of(x, n, c->eps);
+        double d = 0.0;
+        for (size_t j = 0; j < n; j++)
+            d += (double)x[j] * (double)dy[j] * (c->g ? (double)c->g[j] : 1.0);
+        double corr = d / (double)n * inv * inv * inv;
+        for (size_t j = 0; j < n; j++) {
+            double g = (double)dy[j] * (c->g ? (double)c->g[j] : 1.0);
+            dx[j] = (float)(g * inv - (double)x[j] * corr);
+        }
+    }
+}
+
+void orc_rms_norm_backward(const float *x, const float *dy, const float *gamma,
+                           float *dx, float *dgamma, size_t rows, size_t cols,
+                           float eps) {
+    row_ctx c = {NULL, x, dy, gamma, dx, cols, eps};
+    parallel_rows(rows, rms_norm_bwd_fn, &c);
+    if (dgamma) {
+        /* dgamma_j = sum_rows dy * x / rms. */
+        double *sg = (double *)calloc(cols, sizeof(double));
+        if (!sg) abort();
+        for (size_t r = 0; r < rows; r++) {
+            double inv = 1.0 / rms_of(x + r * cols, cols, eps);
+            for (size_t j = 0; j < cols; j++)
+                sg[j] += (double)dy[r * cols + j] * (double)x[r * cols + j] * inv;
+        }
+        for (size_t j = 0; j < cols; j++) dgamma[j] = (float)sg[j];
+        free(sg);
+    }
+}
+
+/* ------------------------------------------------------------ elementwise */
+
+/* apply_binary (elementwise.rs:5-13), one f32 operation. */
+static float apply_binary(float l, float r, int op) {
+    switch (op) {
+    case ORC_ADD: return l + r;
+    case ORC_SUB: return l - r;
+    case ORC_MUL: return l * r;
+    default: return l / r;
+    }
+}
+
+void orc_binary(const float *l, const float *r, float *o, size_t n, int op) {
+    for (size_t i = 0; i < n; i++) o[i] = apply_binary(l[i], r[i], op);
+}
+
+void orc_binary_assign(float *t, const float *r, size_t n, int op) {
+    for (size_t i = 0; i < n; i++) t[i] = apply_binary(t[i], r[i], op);
+}
+
+/* row.rs:179-191: M[i] = M[i] op row[i mod cols]. */
+void orc_binary_assign_by_rows(float *m, const float *row, size_t rows,
+                               size_t cols, int op) {
+    for (size_t i = 0; i < rows * cols; i++)
+        m[i] = apply_binary(m[i], row[i % cols], op);
+}
+
+/* Activation constants (linear.rs:22-24), kept as the f32 values Rust uses. */
+static const float GELU_SCALE = 0.7978846f;
+static const float GELU_CUBIC = 0.044715f;
+
+static float map_one(float x, int op, float p0) {
+    double xd = (double)x;
+    switch (op) {
+    case ORC_MAP_SCALE: return x * p0;
+    case ORC_MAP_ADD: return x + p0;
+    case ORC_MAP_GELU: { /* linear.rs:30-33 */
+        double inner = (double)GELU_SCALE * (xd + (double)GELU_CUBIC * xd * xd * xd);
+        return (float)(0.5 * xd * (1.0 + tanh(inner)));
+    }
+    case ORC_MAP_GELU_D: { /* linear.rs:49-56 */
+        double inner = (double)GELU_SCALE * (xd + (double)GELU_CUBIC * xd * xd * xd);
+        double t = tanh(inner);
+        double dq = (double)GELU_SCALE * 3.0 * (double)GELU_CUBIC;
+        double inner_d = (double)GELU_SCALE + dq * xd * xd;
+        return (float)(0.5 * (1.0 + t) + 0.5 * xd * (1.0 - t * t) * inner_d);
+    }
+    case ORC_MAP_RELU: return x > 0.f ? x : 0.f;      /* linear.rs:34-40 */
+    case ORC_MAP_RELU_D: return x > 0.f ? 1.f : 0.f;  /* linear.rs:57-63 */
+    case ORC_MAP_SILU: return (float)(xd / (1.0 + exp(-xd))); /* linear.rs:41 */
+    case ORC_MAP_SILU_D: { /* linear.rs:64-67 */
+        double e = exp(-xd);
+        return (float)(1.0 / (1.0 + e) + xd * e / ((1.0 + e) * (1.0 + e)));
+    }
+    case ORC_MAP_EXP_SHIFT: return (float)exp(xd - (double)p0); /* vector.rs:50 */
+    case ORC_MAP_HALF_SQ: return 0.5f * x * x;  /* linear.rs:327, f32 as written */
+    default: return x;                          /* Identity, linear.rs:29 */
+    }
+}
+
+void orc_map(float *x, size_t n, int op, float p0) {
+    for (size_t i = 0; i < n; i++) x[i] = map_one(x[i], op, p0);
+}
+
+/* ------------------------------------------------------------- reductions */
+
+void orc_sum_rows(const float *m, float *out, size_t rows, size_t cols) {
+    /* row.rs:16-53: s_r = sum_j M[r, j]. */
+    for (size_t r = 0; r < rows; r++) {
+        double s = 0.0;
+        for (size_t j = 0; j < cols; j++) s += (double)m[r * cols + j];
+        out[r] = (float)s;
+    }
+}
+
+void orc_sum_cols(const float *m, float *out, size_t rows, size_t cols) {
+    /* Column sums; the reference computes them as transpose followed by
+     * sum_rows (linear.rs:267-272). */
+    double *acc = (double *)calloc(cols ? cols : 1, sizeof(double));
+    if (!acc) abort();
+    for (size_t r = 0; r < rows; r++)
+        for (size_t j = 0; j < cols; j++) acc[j] += (double)m[r * cols + j];
+    for (size_t j = 0; j < cols; j++) out[j] = (float)acc[j];
+    free(acc);
+}
+
+float orc_reduce_sum(const float *x, size_t n) {
+    /* reduction.rs:4-41 with the host loop of span.rs:361-385; an empty span
+     * sums to 0 (span.rs:302-304). */
+    double s = 0.0;
+    for (size_t i = 0; i < n; i++) s += (double)x[i];
+    return (float)s;
+}
+
+float orc_reduce_max(const float *x, size_t n) {
+    /* reduction.rs:93-130; identity f32::MIN, also for an empty span
+     * (span.rs:319-321). */
+    float m = -FLT_MAX;
+    for (size_t i = 0; i < n; i++)
+        if (x[i] > m) m = x[i];
+    return m;
+}
+
+/* ------------------------------------------------------------------ fills */
+
+void orc_fill_seq(float *x, size_t n, int ascending) {
+    /* elementwise.rs:23-34: i (Sequence) or len - i (Reserve). */
+    for (size_t i = 0; i < n; i++)
+        x[i] = ascending ? (float)i : (float)(n - i);
+}
+
+void orc_causal_mask(float *m, size_t rows, size_t cols) {
+    /* row.rs:5-14: M[r, c] = -inf for c > r. */
+    for (size_t r = 0; r < rows; r++)
+        for (size_t c = r + 1; c < cols; c++) m[r * cols + c] = -INFINITY;
+}
+
+/* --------------------------------------------------------- synthetic data */
+
+static uint64_t splitmix64(uint64_t *state) {
+    uint64_t z = (*state += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+void orc_fill_uniform(float *x, size_t n, uint64_t seed, float lo, float hi) {
+    uint64_t s = seed;
+    for (size_t i = 0; i < n; i++) {
+        double u = (double)(splitmix64(&s) >> 40) * (1.0 / 16777216.0);
+        x[i] = (float)((double)lo + ((double)hi - (double)lo) * u);
+    }
+}
+
+void orc_fill_normal(float *x, size_t n, uint64_t seed, float mu, float sigma) {
+    uint64_t s = seed;
+    const double two_pi = 6.283185307179586476925;
+    for (size_t i = 0; i < n; i += 2) {
+        double u1 = ((double)(splitmix64(&s) >> 11) + 1.0) * (1.0 / 9007199254740993.0);
+        double u2 = (double)(splitmix64(&s) >> 11) * (1.0 / 9007199254740992.0);
+        double rad = sqrt(-2.0 * log(u1));
+        x[i] = (float)((double)mu + (double)sigma * rad * cos(two_pi * u2));
+        if (i + 1 < n)
+            x[i + 1] = (float)((double)mu + (double)sigma * rad * sin(two_pi * u2));
+    }
+}

@@ -1,0 +1,108 @@
+// common.hpp -- shared device helpers for the gfx950 (CDNA4) kernels.
+//
+// Wavefronts are 64 lanes.  Cross-lane reductions use DPP row operations
+// (quad_perm, row_half_mirror, row_mirror) to reduce inside each 16-lane row,
+// then v_readlane to combine the four rows into a wave-uniform scalar.  Every
+// lane of a row ends with the same bits (float addition and fmax are
+// commutative, and each step pairs the same two partial values), so the
+// result is deterministic and identical in every lane.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define FORGE_KERNEL extern "C" __global__
+
+namespace forge {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// DPP control words (GFX9 encoding).
+constexpr int DPP_QUAD_1032 = 0xB1;      // quad_perm:[1,0,3,2]
+constexpr int DPP_QUAD_2301 = 0x4E;      // quad_perm:[2,3,0,1]
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;
+constexpr int DPP_ROW_MIRROR = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(
+        0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float readlane(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Sum over the 64 lanes; the result is wave-uniform.
+__device__ __forceinline__ float wave_sum(float v) {
+    v = v + dpp_mov<DPP_QUAD_1032>(v);
+    v = v + dpp_mov<DPP_QUAD_2301>(v);
+    v = v + dpp_mov<DPP_ROW_HALF_MIRROR>(v);
+    v = v + dpp_mov<DPP_ROW_MIRROR>(v);
+    return (readlane(v, 0) + readlane(v, 16)) +
+           (readlane(v, 32) + readlane(v, 48));
+}
+
+// Max over the 64 lanes; the result is wave-uniform.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp_mov<DPP_QUAD_1032>(v));
+    v = fmaxf(v, dpp_mov<DPP_QUAD_2301>(v));
+    v = fmaxf(v, dpp_mov<DPP_ROW_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_mov<DPP_ROW_MIRROR>(v));
+    return fmaxf(fmaxf(readlane(v, 0), readlane(v, 16)),
+                 fmaxf(readlane(v, 32), readlane(v, 48)));
+}
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+// BinaryOp (cuda.rs:3-10) applied as one rounded f32 operation
+// (elementwise.rs:5-13).
+enum BinOp { OP_ADD = 0, OP_SUB = 1, OP_MUL = 2, OP_DIV = 3 };
+
+template <int OP>
+__device__ __forceinline__ float apply_binary(float l, float r) {
+    if constexpr (OP == OP_ADD) return l + r;
+    else if constexpr (OP == OP_SUB) return l - r;
+    else if constexpr (OP == OP_MUL) return l * r;
+    else return l / r;
+}
+
+// Activation (linear.rs:21-70).  The expression order follows the reference
+// so that, with contraction disabled, only tanhf/expf rounding differs.
+constexpr float GELU_SCALE = 0.7978846f;
+constexpr float GELU_CUBIC = 0.044715f;
+constexpr float GELU_DERIVATIVE_QUADRATIC = GELU_SCALE * 3.0f * GELU_CUBIC;
+
+enum Act { ACT_IDENTITY = 0, ACT_GELU = 1, ACT_RELU = 2, ACT_SILU = 3 };
+
+__device__ __forceinline__ float gelu(float x) {
+    float inner = GELU_SCALE * (x + GELU_CUBIC * x * x * x);
+    return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+__device__ __forceinline__ float gelu_derivative(float x) {
+    float inner = GELU_SCALE * (x + GELU_CUBIC * x * x * x);
+    float t = tanhf(inner);
+    float inner_derivative = GELU_SCALE + GELU_DERIVATIVE_QUADRATIC * x * x;
+    return 0.5f * (1.0f + t) + 0.5f * x * (1.0f - t * t) * inner_derivative;
+}
+
+__device__ __forceinline__ float relu(float x) { return x > 0.0f ? x : 0.0f; }
+__device__ __forceinline__ float relu_derivative(float x) {
+    return x > 0.0f ? 1.0f : 0.0f;
+}
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float silu_derivative(float x) {
+    float e = expf(-x);
+    return 1.0f / (1.0f + e) + x * e / ((1.0f + e) * (1.0f + e));
+}
+
+__device__ __forceinline__ float activate(int act, float x) {
+    switch (act) {
+    case ACT_GELU: return gelu(x);
+    case ACT_RELU: return relu(x);
+    case ACT_SILU: return silu(x);
+    default: return x;
+    }
+}
+
+}  // namespace forge

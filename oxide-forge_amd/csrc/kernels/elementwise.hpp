@@ -1,0 +1,298 @@
+// elementwise.hpp -- bandwidth kernels: binary ops, row broadcast, maps,
+// fills, column/row sums, full reductions and the transpose.
+//
+// The reference launches one thread per element with 1024-thread blocks and
+// no vectorisation (runtime.rs:124-130 get_launch_config).  Here every
+// streaming kernel is grid-stride over 128-bit (float4) accesses with a
+// scalar tail; the VEC=false instances serve unaligned slices.
+#pragma once
+#include <float.h>
+#include "common.hpp"
+
+namespace forge {
+
+constexpr int EW_THREADS = 256;
+
+// ---------------------------------------------------------------- binary
+
+template <int OP, bool VEC>
+__device__ __forceinline__ void binary_body(const float* __restrict__ l,
+                                            const float* __restrict__ r,
+                                            float* __restrict__ o, long long n) {
+    const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    if constexpr (VEC) {
+        const long long n4 = n / 4;
+        for (long long i = tid; i < n4; i += stride) {
+            const float4 a = reinterpret_cast<const float4*>(l)[i];
+            const float4 b = reinterpret_cast<const float4*>(r)[i];
+            float4 c;
+            c.x = apply_binary<OP>(a.x, b.x);
+            c.y = apply_binary<OP>(a.y, b.y);
+            c.z = apply_binary<OP>(a.z, b.z);
+            c.w = apply_binary<OP>(a.w, b.w);
+            reinterpret_cast<float4*>(o)[i] = c;
+        }
+        for (long long i = n4 * 4 + tid; i < n; i += stride)
+            o[i] = apply_binary<OP>(l[i], r[i]);
+    } else {
+        for (long long i = tid; i < n; i += stride) o[i] = apply_binary<OP>(l[i], r[i]);
+    }
+}
+
+// In-place variant (target aliases the left operand); no __restrict__.
+template <int OP, bool VEC>
+__device__ __forceinline__ void binary_assign_body(float* t, const float* r,
+                                                   long long n) {
+    const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    if constexpr (VEC) {
+        const long long n4 = n / 4;
+        for (long long i = tid; i < n4; i += stride) {
+            float4 a = reinterpret_cast<float4*>(t)[i];
+            const float4 b = reinterpret_cast<const float4*>(r)[i];
+            a.x = apply_binary<OP>(a.x, b.x);
+            a.y = apply_binary<OP>(a.y, b.y);
+            a.z = apply_binary<OP>(a.z, b.z);
+            a.w = apply_binary<OP>(a.w, b.w);
+            reinterpret_cast<float4*>(t)[i] = a;
+        }
+        for (long long i = n4 * 4 + tid; i < n; i += stride)
+            t[i] = apply_binary<OP>(t[i], r[i]);
+    } else {
+        for (long long i = tid; i < n; i += stride) t[i] = apply_binary<OP>(t[i], r[i]);
+    }
+}
+
+// M[r, c] = M[r, c] op row[c] (row.rs:179-191).  Column tiles on
+// blockIdx.x keep the broadcast row in registers; rows are grid-stride on
+// blockIdx.y.
+template <int OP, bool VEC>
+__device__ __forceinline__ void by_rows_body(float* m, const float* __restrict__ row,
+                                             int rows, int cols) {
+    if constexpr (VEC) {
+        const int c4 = blockIdx.x * blockDim.x + threadIdx.x;
+        if (c4 * 4 >= cols) return;
+        const float4 b = reinterpret_cast<const float4*>(row)[c4];
+        for (int r = blockIdx.y; r < rows; r += gridDim.y) {
+            float4* p = reinterpret_cast<float4*>(m + (long long)r * cols) + c4;
+            float4 a = *p;
+            a.x = apply_binary<OP>(a.x, b.x);
+            a.y = apply_binary<OP>(a.y, b.y);
+            a.z = apply_binary<OP>(a.z, b.z);
+            a.w = apply_binary<OP>(a.w, b.w);
+            *p = a;
+        }
+    } else {
+        const int c = blockIdx.x * blockDim.x + threadIdx.x;
+        if (c >= cols) return;
+        const float b = row[c];
+        for (int r = blockIdx.y; r < rows; r += gridDim.y) {
+            float* p = m + (long long)r * cols + c;
+            *p = apply_binary<OP>(*p, b);
+        }
+    }
+}
+
+// ------------------------------------------------------------------ maps
+
+enum MapOp {
+    MAP_SCALE = 0, MAP_ADD = 1, MAP_GELU = 2, MAP_GELU_D = 3, MAP_RELU = 4,
+    MAP_RELU_D = 5, MAP_SILU = 6, MAP_SILU_D = 7, MAP_EXP_SHIFT = 8,
+    MAP_HALF_SQ = 9, MAP_IDENTITY = 10
+};
+
+template <int OP>
+__device__ __forceinline__ float map_one(float x, float p0) {
+    if constexpr (OP == MAP_SCALE) return x * p0;
+    else if constexpr (OP == MAP_ADD) return x + p0;
+    else if constexpr (OP == MAP_GELU) return gelu(x);
+    else if constexpr (OP == MAP_GELU_D) return gelu_derivative(x);
+    else if constexpr (OP == MAP_RELU) return relu(x);
+    else if constexpr (OP == MAP_RELU_D) return relu_derivative(x);
+    else if constexpr (OP == MAP_SILU) return silu(x);
+    else if constexpr (OP == MAP_SILU_D) return silu_derivative(x);
+    else if constexpr (OP == MAP_EXP_SHIFT) return expf(x - p0);
+    else if constexpr (OP == MAP_HALF_SQ) return 0.5f * x * x;
+    else return x;
+}
+
+template <int OP, bool VEC>
+__device__ __forceinline__ void map_body(float* x, long long n, float p0) {
+    const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    if constexpr (VEC) {
+        const long long n4 = n / 4;
+        for (long long i = tid; i < n4; i += stride) {
+            float4 a = reinterpret_cast<float4*>(x)[i];
+            a.x = map_one<OP>(a.x, p0);
+            a.y = map_one<OP>(a.y, p0);
+            a.z = map_one<OP>(a.z, p0);
+            a.w = map_one<OP>(a.w, p0);
+            reinterpret_cast<float4*>(x)[i] = a;
+        }
+        for (long long i = n4 * 4 + tid; i < n; i += stride) x[i] = map_one<OP>(x[i], p0);
+    } else {
+        for (long long i = tid; i < n; i += stride) x[i] = map_one<OP>(x[i], p0);
+    }
+}
+
+// ----------------------------------------------------------------- fills
+
+template <bool VEC>
+__device__ __forceinline__ void fill_body(float* x, long long n, float v) {
+    const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    if constexpr (VEC) {
+        const long long n4 = n / 4;
+        const float4 f = make_float4(v, v, v, v);
+        for (long long i = tid; i < n4; i += stride) reinterpret_cast<float4*>(x)[i] = f;
+        for (long long i = n4 * 4 + tid; i < n; i += stride) x[i] = v;
+    } else {
+        for (long long i = tid; i < n; i += stride) x[i] = v;
+    }
+}
+
+// elementwise.rs:23-34: index as f32 (ascending) or (len - index) as f32.
+__device__ __forceinline__ void fill_seq_body(float* x, long long n, int ascending) {
+    const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    for (long long i = tid; i < n; i += stride)
+        x[i] = ascending ? (float)(unsigned long long)i
+                         : (float)(unsigned long long)(n - i);
+}
+
+// row.rs:5-14: M[r, c] = -inf for c > r.
+__device__ __forceinline__ void causal_mask_body(float* m, int rows, int cols) {
+    for (int r = blockIdx.y; r < rows; r += gridDim.y)
+        for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < cols;
+             c += gridDim.x * blockDim.x)
+            if (c > r) m[(long long)r * cols + c] = -INFINITY;
+}
+
+// ------------------------------------------------------------ reductions
+
+// Column sums of a [rows, cols] matrix over the row range of chunk
+// blockIdx.y, written to out[blockIdx.y * cols + c].  One thread per column
+// sums its chunk in row order (coalesced across the wave, deterministic);
+// the host reduces the chunk rows with a second launch of the same kernel.
+__device__ __forceinline__ void sum_cols_body(const float* __restrict__ m,
+                                              float* __restrict__ out, int rows,
+                                              int cols, int rows_per_chunk) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= cols) return;
+    const int r0 = blockIdx.y * rows_per_chunk;
+    const int r1 = min(rows, r0 + rows_per_chunk);
+    float s = 0.0f;
+    for (int r = r0; r < r1; r++) s += m[(long long)r * cols + c];
+    out[(long long)blockIdx.y * cols + c] = s;
+}
+
+// Row sums: one wave per row (row.rs:16-53).
+template <bool VEC>
+__device__ __forceinline__ void sum_rows_body(const float* __restrict__ m,
+                                              float* __restrict__ out, int rows,
+                                              int cols) {
+    const int lane = lane_id();
+    const int wave = threadIdx.x >> 6;
+    const int waves = blockDim.x >> 6;
+    for (int r = blockIdx.x * waves + wave; r < rows; r += gridDim.x * waves) {
+        const float* p = m + (long long)r * cols;
+        float s = 0.0f;
+        if constexpr (VEC) {
+            for (int c4 = lane; c4 < cols / 4; c4 += 64) {
+                const float4 a = reinterpret_cast<const float4*>(p)[c4];
+                s += (a.x + a.y) + (a.z + a.w);
+            }
+        } else {
+            for (int c = lane; c < cols; c += 64) s += p[c];
+        }
+        s = wave_sum(s);
+        if (lane == 0) out[r] = s;
+    }
+}
+
+// Block-level reduction to one value per workgroup (partials), grid-stride.
+// IS_MAX selects max with identity -FLT_MAX (reduction.rs:93-130) instead of
+// the sum (reduction.rs:4-41).
+template <bool IS_MAX>
+__device__ __forceinline__ void reduce_body(const float* __restrict__ x, long long n,
+                                            float* __restrict__ out) {
+    __shared__ float part[EW_THREADS / 64];
+    const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    float acc = IS_MAX ? -FLT_MAX : 0.0f;
+    for (long long i = tid; i < n; i += stride)
+        acc = IS_MAX ? fmaxf(acc, x[i]) : acc + x[i];
+    acc = IS_MAX ? wave_max(acc) : wave_sum(acc);
+    const int wave = threadIdx.x >> 6;
+    if (lane_id() == 0) part[wave] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float t = part[0];
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++)
+            t = IS_MAX ? fmaxf(t, part[w]) : t + part[w];
+        out[blockIdx.x] = t;
+    }
+}
+
+// ------------------------------------------------------------- transpose
+
+// out[c, r] = in[r, c] for in [rows, cols] (layout.rs:8-55).  64x64 tiles
+// through LDS with a 65-float pitch: the float4 row loads and the column
+// reads that assemble each float4 store are both bank-conflict free.
+constexpr int TR_TILE = 64;
+constexpr int TR_PITCH = TR_TILE + 1;
+
+template <bool GUARD>
+__device__ __forceinline__ void transpose_body(const float* __restrict__ in,
+                                               float* __restrict__ out, int rows,
+                                               int cols) {
+    __shared__ float tile[TR_TILE * TR_PITCH];
+    const int t = threadIdx.x;  // 256 threads
+    const int tiles_c = (cols + TR_TILE - 1) / TR_TILE;
+    const int tr = blockIdx.x / tiles_c, tc = blockIdx.x % tiles_c;
+    const int r0 = tr * TR_TILE, c0 = tc * TR_TILE;
+    const int sub = t & 15;  // float4 slot inside a 64-wide tile row
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int lr = (t >> 4) + 16 * i;
+        const int r = r0 + lr, c = c0 + sub * 4;
+        float4 v;
+        if constexpr (!GUARD) {
+            v = *reinterpret_cast<const float4*>(in + (long long)r * cols + c);
+        } else {
+            const float* p = in + (long long)r * cols + c;
+            const bool ok = r < rows;
+            v.x = (ok && c + 0 < cols) ? p[0] : 0.0f;
+            v.y = (ok && c + 1 < cols) ? p[1] : 0.0f;
+            v.z = (ok && c + 2 < cols) ? p[2] : 0.0f;
+            v.w = (ok && c + 3 < cols) ? p[3] : 0.0f;
+        }
+        float* s = tile + lr * TR_PITCH + sub * 4;
+        s[0] = v.x; s[1] = v.y; s[2] = v.z; s[3] = v.w;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int lc = (t >> 4) + 16 * i;  // input column = output row
+        const int lr = sub * 4;            // first of four input rows
+        float4 v;
+        v.x = tile[(lr + 0) * TR_PITCH + lc];
+        v.y = tile[(lr + 1) * TR_PITCH + lc];
+        v.z = tile[(lr + 2) * TR_PITCH + lc];
+        v.w = tile[(lr + 3) * TR_PITCH + lc];
+        const int orow = c0 + lc, ocol = r0 + lr;
+        if constexpr (!GUARD) {
+            *reinterpret_cast<float4*>(out + (long long)orow * rows + ocol) = v;
+        } else if (orow < cols) {
+            float* p = out + (long long)orow * rows + ocol;
+            if (ocol + 0 < rows) p[0] = v.x;
+            if (ocol + 1 < rows) p[1] = v.y;
+            if (ocol + 2 < rows) p[2] = v.z;
+            if (ocol + 3 < rows) p[3] = v.w;
+        }
+    }
+}
+
+}  // namespace forge

@@ -1,0 +1,142 @@
+// oxforge_kernels.hip -- the gfx950 code object loaded by forge_runtime_create
+// (hipModuleLoad) and launched by name with hipModuleLaunchKernel.  It plays
+// the role of the reference's #[cuda_module] mod kernels
+// (src/cuda/device/module.rs:6-263): one extern "C" entry per kernel
+// instance; the host picks the instance from the shape and alignment.
+#include "common.hpp"
+#include "elementwise.hpp"
+#include "gemm.hpp"
+#include "rows.hpp"
+
+using namespace forge;
+
+// ------------------------------------------------------------------- GEMM
+// forge_gemm_<ab>_<BM>x<BN>x<BK>_<WARPS_M>x<WARPS_N>[_g][_e]
+//   ab: n/t for A then B (t = operand stored transposed)
+//   _g: bounds-guarded (any shape, any alignment); _e: fused epilogue.
+#define GEMM_KERNEL(NAME, BM, BN, BK, WMW, WNW, TA, TB, GUARD, EPI)          \
+    FORGE_KERNEL void __launch_bounds__(WMW * WNW * 64) NAME(GemmArgs p) {   \
+        gemm_body<BM, BN, BK, WMW, WNW, TA, TB, GUARD, EPI>(p);              \
+    }
+
+#define GEMM_FAMILY(AB, TA, TB)                                                   \
+    GEMM_KERNEL(forge_gemm_##AB##_128x128x16_2x2_e, 128, 128, 16, 2, 2, TA, TB, false, true) \
+    GEMM_KERNEL(forge_gemm_##AB##_128x64x16_2x2_e, 128, 64, 16, 2, 2, TA, TB, false, true)   \
+    GEMM_KERNEL(forge_gemm_##AB##_256x128x16_2x2_e, 256, 128, 16, 2, 2, TA, TB, false, true) \
+    GEMM_KERNEL(forge_gemm_##AB##_64x64x16_2x2_g_e, 64, 64, 16, 2, 2, TA, TB, true, true)
+
+GEMM_FAMILY(nn, false, false)
+GEMM_FAMILY(nt, false, true)
+GEMM_FAMILY(tn, true, false)
+GEMM_FAMILY(tt, true, true)
+
+// Plain C = A * B instances (forge_gemm_f32) and the tile-shape candidates
+// measured by the bench sweep.
+GEMM_KERNEL(forge_gemm_nn_128x128x16_2x2, 128, 128, 16, 2, 2, false, false, false, false)
+GEMM_KERNEL(forge_gemm_nn_128x128x32_2x2, 128, 128, 32, 2, 2, false, false, false, false)
+GEMM_KERNEL(forge_gemm_nn_128x64x16_2x2, 128, 64, 16, 2, 2, false, false, false, false)
+GEMM_KERNEL(forge_gemm_nn_256x128x16_2x2, 256, 128, 16, 2, 2, false, false, false, false)
+GEMM_KERNEL(forge_gemm_nn_128x256x16_2x2, 128, 256, 16, 2, 2, false, false, false, false)
+GEMM_KERNEL(forge_gemm_nn_256x128x16_4x2, 256, 128, 16, 4, 2, false, false, false, false)
+GEMM_KERNEL(forge_gemm_nn_64x64x16_2x2_g, 64, 64, 16, 2, 2, false, false, true, false)
+
+// ------------------------------------------------------------------- rows
+#define ROW_KERNEL(NAME, OP, VPT, PARTIALS) \
+    FORGE_KERNEL void __launch_bounds__(256) NAME(RowArgs a) { row_kernel_reg<OP, VPT, PARTIALS>(a); }
+#define ROW_KERNELS(OPNAME, OP)                                   \
+    ROW_KERNEL(forge_row_##OPNAME##_v1, OP, 1, false)             \
+    ROW_KERNEL(forge_row_##OPNAME##_v2, OP, 2, false)             \
+    ROW_KERNEL(forge_row_##OPNAME##_v4, OP, 4, false)             \
+    ROW_KERNEL(forge_row_##OPNAME##_v8, OP, 8, false)             \
+    ROW_KERNEL(forge_row_##OPNAME##_v16, OP, 16, false)           \
+    FORGE_KERNEL void __launch_bounds__(256) forge_row_##OPNAME##_loop(RowArgs a) { row_kernel_loop<OP>(a); }
+// Norm backward instances that also emit per-workgroup dgamma/dbeta partials.
+#define ROW_PARTIAL_KERNELS(OPNAME, OP)                           \
+    ROW_KERNEL(forge_row_##OPNAME##_v1_p, OP, 1, true)            \
+    ROW_KERNEL(forge_row_##OPNAME##_v2_p, OP, 2, true)            \
+    ROW_KERNEL(forge_row_##OPNAME##_v4_p, OP, 4, true)            \
+    ROW_KERNEL(forge_row_##OPNAME##_v8_p, OP, 8, true)
+
+ROW_KERNELS(softmax, ROW_SOFTMAX)
+ROW_KERNELS(layer_norm, ROW_LAYER_NORM)
+ROW_KERNELS(rms_norm, ROW_RMS_NORM)
+ROW_KERNELS(softmax_bwd, ROW_SOFTMAX_BWD)
+ROW_KERNELS(layer_norm_bwd, ROW_LAYER_NORM_BWD)
+ROW_KERNELS(rms_norm_bwd, ROW_RMS_NORM_BWD)
+ROW_PARTIAL_KERNELS(layer_norm_bwd, ROW_LAYER_NORM_BWD)
+ROW_PARTIAL_KERNELS(rms_norm_bwd, ROW_RMS_NORM_BWD)
+
+// ------------------------------------------------------------ elementwise
+#define BINARY_KERNELS(OPNAME, OP)                                                          \
+    FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_binary_##OPNAME##_v(              \
+        const float* l, const float* r, float* o, long long n) { binary_body<OP, true>(l, r, o, n); } \
+    FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_binary_##OPNAME##_s(              \
+        const float* l, const float* r, float* o, long long n) { binary_body<OP, false>(l, r, o, n); } \
+    FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_binary_assign_##OPNAME##_v(       \
+        float* t, const float* r, long long n) { binary_assign_body<OP, true>(t, r, n); }     \
+    FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_binary_assign_##OPNAME##_s(       \
+        float* t, const float* r, long long n) { binary_assign_body<OP, false>(t, r, n); }    \
+    FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_by_rows_##OPNAME##_v(             \
+        float* m, const float* row, int rows, int cols) { by_rows_body<OP, true>(m, row, rows, cols); } \
+    FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_by_rows_##OPNAME##_s(             \
+        float* m, const float* row, int rows, int cols) { by_rows_body<OP, false>(m, row, rows, cols); }
+
+BINARY_KERNELS(add, OP_ADD)
+BINARY_KERNELS(sub, OP_SUB)
+BINARY_KERNELS(mul, OP_MUL)
+BINARY_KERNELS(div, OP_DIV)
+
+#define MAP_KERNELS(OPNAME, OP)                                                     \
+    FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_map_##OPNAME##_v(         \
+        float* x, long long n, float p0) { map_body<OP, true>(x, n, p0); }          \
+    FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_map_##OPNAME##_s(         \
+        float* x, long long n, float p0) { map_body<OP, false>(x, n, p0); }
+
+MAP_KERNELS(scale, MAP_SCALE)
+MAP_KERNELS(add, MAP_ADD)
+MAP_KERNELS(gelu, MAP_GELU)
+MAP_KERNELS(gelu_d, MAP_GELU_D)
+MAP_KERNELS(relu, MAP_RELU)
+MAP_KERNELS(relu_d, MAP_RELU_D)
+MAP_KERNELS(silu, MAP_SILU)
+MAP_KERNELS(silu_d, MAP_SILU_D)
+MAP_KERNELS(exp_shift, MAP_EXP_SHIFT)
+MAP_KERNELS(half_sq, MAP_HALF_SQ)
+MAP_KERNELS(identity, MAP_IDENTITY)
+
+FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_fill_v(float* x, long long n, float v) {
+    fill_body<true>(x, n, v);
+}
+FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_fill_s(float* x, long long n, float v) {
+    fill_body<false>(x, n, v);
+}
+FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_fill_seq(float* x, long long n, int asc) {
+    fill_seq_body(x, n, asc);
+}
+FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_causal_mask(float* m, int rows, int cols) {
+    causal_mask_body(m, rows, cols);
+}
+FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_sum_cols(const float* m, float* out, int rows,
+                                                               int cols, int rows_per_chunk) {
+    sum_cols_body(m, out, rows, cols, rows_per_chunk);
+}
+FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_sum_rows_v(const float* m, float* out, int rows,
+                                                                 int cols) {
+    sum_rows_body<true>(m, out, rows, cols);
+}
+FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_sum_rows_s(const float* m, float* out, int rows,
+                                                                 int cols) {
+    sum_rows_body<false>(m, out, rows, cols);
+}
+FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_reduce_sum(const float* x, long long n, float* out) {
+    reduce_body<false>(x, n, out);
+}
+FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_reduce_max(const float* x, long long n, float* out) {
+    reduce_body<true>(x, n, out);
+}
+FORGE_KERNEL void __launch_bounds__(256) forge_transpose(const float* in, float* out, int rows, int cols) {
+    transpose_body<false>(in, out, rows, cols);
+}
+FORGE_KERNEL void __launch_bounds__(256) forge_transpose_g(const float* in, float* out, int rows, int cols) {
+    transpose_body<true>(in, out, rows, cols);
+}

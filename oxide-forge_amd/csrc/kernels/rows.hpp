@@ -1,0 +1,407 @@
+// rows.hpp -- row-wise kernels: softmax, LayerNorm, RMSNorm (forward and
+// backward) and row sums.
+//
+// The reference runs one 1024-thread block per row with two-level warp-32
+// shuffle trees through shared memory and asserts cols <= 1024
+// (row.rs:16-468, norm.rs:12,30,54).  Here one 64-lane wavefront owns a row:
+//   - register path: the row is held in VGPRs as VPT float4 per lane
+//     (cols <= 256*VPT, cols % 4 == 0, 16-byte aligned rows), read once and
+//     written once -- the HBM minimum;
+//   - looping path: any cols and alignment; the row is streamed from global
+//     memory once per reduction pass.
+// Reductions are the DPP wave reductions of common.hpp, so there is no LDS
+// traffic and no barrier.  Rows are walked grid-stride so the backward
+// kernels can keep per-column dgamma/dbeta partials in registers across the
+// rows a wave visits; partials are combined per workgroup in LDS and written
+// as one row per workgroup, then summed by the column-sum kernel.
+#pragma once
+#include <float.h>
+#include "common.hpp"
+
+namespace forge {
+
+constexpr int ROW_WAVES = 4;  // wavefronts (rows in flight) per workgroup
+
+struct RowArgs {
+    const float* x;      // input (forward: in/out when y == x)
+    float* y;            // output
+    const float* dy;     // upstream gradient (backward)
+    const float* gamma;  // [cols] or null
+    const float* beta;   // [cols] or null
+    float* pgamma;       // [gridDim.x, cols] partial dgamma or null
+    float* pbeta;        // [gridDim.x, cols] partial dbeta or null
+    int rows, cols;
+    float eps;
+};
+
+enum RowOp {
+    ROW_SOFTMAX = 0,
+    ROW_LAYER_NORM = 1,
+    ROW_RMS_NORM = 2,
+    ROW_SOFTMAX_BWD = 3,
+    ROW_LAYER_NORM_BWD = 4,
+    ROW_RMS_NORM_BWD = 5
+};
+
+__device__ __forceinline__ float sum4(float4 a) { return (a.x + a.y) + (a.z + a.w); }
+__device__ __forceinline__ float max4(float4 a) {
+    return fmaxf(fmaxf(a.x, a.y), fmaxf(a.z, a.w));
+}
+
+#define F4_APPLY(dst, a, EXPR_X, EXPR_Y, EXPR_Z, EXPR_W) \
+    do { dst.x = (EXPR_X); dst.y = (EXPR_Y); dst.z = (EXPR_Z); dst.w = (EXPR_W); } while (0)
+
+// Register path.  VPT float4 per lane; lane l holds columns
+// 4*(64*i + l) .. +3 for i < VPT.
+template <int OP, int VPT, bool PARTIALS>
+__device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
+    const int lane = lane_id();
+    const int wave = threadIdx.x >> 6;
+    const int cols = a.cols;
+    const float n = (float)cols;
+    constexpr bool BWD = OP >= ROW_SOFTMAX_BWD;
+    static_assert(!PARTIALS || OP == ROW_LAYER_NORM_BWD || OP == ROW_RMS_NORM_BWD,
+                  "only the norm backward kernels produce column partials");
+
+    float4 pg[PARTIALS ? VPT : 1], pb[PARTIALS ? VPT : 1];
+    if constexpr (PARTIALS) {
+#pragma unroll
+        for (int i = 0; i < VPT; i++) {
+            pg[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            pb[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+
+    for (int row = blockIdx.x * ROW_WAVES + wave; row < a.rows;
+         row += gridDim.x * ROW_WAVES) {
+        const long long base = (long long)row * cols;
+        float4 v[VPT], g[BWD ? VPT : 1];
+        bool ok[VPT];
+#pragma unroll
+        for (int i = 0; i < VPT; i++) {
+            const int c = (i * 64 + lane) * 4;
+            ok[i] = c < cols;
+            const float fill = (OP == ROW_SOFTMAX) ? -FLT_MAX : 0.0f;
+            v[i] = ok[i] ? *reinterpret_cast<const float4*>(a.x + base + c)
+                         : make_float4(fill, fill, fill, fill);
+            if constexpr (BWD)
+                g[i] = ok[i] ? *reinterpret_cast<const float4*>(a.dy + base + c)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+
+        if constexpr (OP == ROW_SOFTMAX) {
+            // row.rs:64-112: max, exp(x - max), sum, divide.
+            float m = -FLT_MAX;
+#pragma unroll
+            for (int i = 0; i < VPT; i++) m = fmaxf(m, max4(v[i]));
+            m = wave_max(m);
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < VPT; i++) {
+                if (ok[i]) {
+                    F4_APPLY(v[i], v[i], expf(v[i].x - m), expf(v[i].y - m),
+                             expf(v[i].z - m), expf(v[i].w - m));
+                    s += sum4(v[i]);
+                }
+            }
+            s = wave_sum(s);
+#pragma unroll
+            for (int i = 0; i < VPT; i++) {
+                if (ok[i]) {
+                    float4 o;
+                    F4_APPLY(o, v[i], v[i].x / s, v[i].y / s, v[i].z / s, v[i].w / s);
+                    *reinterpret_cast<float4*>(a.y + base + (i * 64 + lane) * 4) = o;
+                }
+            }
+        } else if constexpr (OP == ROW_LAYER_NORM || OP == ROW_LAYER_NORM_BWD) {
+            // row.rs:130-170 (forward) and row.rs:260-300 (backward):
+            // mean, then population variance of (x - mean), r = 1/sqrt(v+eps).
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < VPT; i++) s += sum4(v[i]);
+            const float mean = wave_sum(s) / n;
+            float q = 0.0f;
+#pragma unroll
+            for (int i = 0; i < VPT; i++) {
+                if (ok[i]) {
+                    const float dx0 = v[i].x - mean, dx1 = v[i].y - mean;
+                    const float dx2 = v[i].z - mean, dx3 = v[i].w - mean;
+                    v[i] = make_float4(dx0, dx1, dx2, dx3);
+                    q += (dx0 * dx0 + dx1 * dx1) + (dx2 * dx2 + dx3 * dx3);
+                }
+            }
+            const float rstd = 1.0f / sqrtf(wave_sum(q) / n + a.eps);
+            if constexpr (OP == ROW_LAYER_NORM) {
+#pragma unroll
+                for (int i = 0; i < VPT; i++) {
+                    if (!ok[i]) continue;
+                    const int c = (i * 64 + lane) * 4;
+                    float4 o;
+                    F4_APPLY(o, v[i], v[i].x * rstd, v[i].y * rstd, v[i].z * rstd,
+                             v[i].w * rstd);
+                    if (a.gamma) {
+                        const float4 gm = *reinterpret_cast<const float4*>(a.gamma + c);
+                        F4_APPLY(o, o, o.x * gm.x, o.y * gm.y, o.z * gm.z, o.w * gm.w);
+                    }
+                    if (a.beta) {
+                        const float4 bt = *reinterpret_cast<const float4*>(a.beta + c);
+                        F4_APPLY(o, o, o.x + bt.x, o.y + bt.y, o.z + bt.z, o.w + bt.w);
+                    }
+                    *reinterpret_cast<float4*>(a.y + base + c) = o;
+                }
+            } else {
+                // row.rs:302-346: A = sum g, B = sum g*xhat,
+                // dx = r/n * (n*g - A - xhat*B), g = dy (* gamma).  v holds
+                // x - mean; xhat and g are recomputed per use to keep the
+                // register footprint at two row copies.
+                float sa = 0.0f, sb = 0.0f;
+#pragma unroll
+                for (int i = 0; i < VPT; i++) {
+                    if (!ok[i]) continue;
+                    const int c = (i * 64 + lane) * 4;
+                    float4 gg = g[i];
+                    if (a.gamma) {
+                        const float4 gm = *reinterpret_cast<const float4*>(a.gamma + c);
+                        F4_APPLY(gg, g[i], g[i].x * gm.x, g[i].y * gm.y, g[i].z * gm.z,
+                                 g[i].w * gm.w);
+                    }
+                    sa += sum4(gg);
+                    sb += (gg.x * (v[i].x * rstd) + gg.y * (v[i].y * rstd)) +
+                          (gg.z * (v[i].z * rstd) + gg.w * (v[i].w * rstd));
+                }
+                sa = wave_sum(sa);
+                sb = wave_sum(sb);
+                const float scale = rstd / n;
+#pragma unroll
+                for (int i = 0; i < VPT; i++) {
+                    if (!ok[i]) continue;
+                    const int c = (i * 64 + lane) * 4;
+                    float4 gg = g[i];
+                    if (a.gamma) {
+                        const float4 gm = *reinterpret_cast<const float4*>(a.gamma + c);
+                        F4_APPLY(gg, g[i], g[i].x * gm.x, g[i].y * gm.y, g[i].z * gm.z,
+                                 g[i].w * gm.w);
+                    }
+                    float4 xh;
+                    F4_APPLY(xh, v[i], v[i].x * rstd, v[i].y * rstd, v[i].z * rstd,
+                             v[i].w * rstd);
+                    float4 o;
+                    F4_APPLY(o, xh, scale * (n * gg.x - sa - xh.x * sb),
+                             scale * (n * gg.y - sa - xh.y * sb),
+                             scale * (n * gg.z - sa - xh.z * sb),
+                             scale * (n * gg.w - sa - xh.w * sb));
+                    *reinterpret_cast<float4*>(a.y + base + c) = o;
+                    if constexpr (PARTIALS) {
+                        pg[i].x += g[i].x * xh.x; pg[i].y += g[i].y * xh.y;
+                        pg[i].z += g[i].z * xh.z; pg[i].w += g[i].w * xh.w;
+                        pb[i].x += g[i].x; pb[i].y += g[i].y;
+                        pb[i].z += g[i].z; pb[i].w += g[i].w;
+                    }
+                }
+            }
+        } else if constexpr (OP == ROW_RMS_NORM) {
+            // row.rs:364-395: y = x / sqrt(sum(x^2)/n + eps).
+            float q = 0.0f;
+#pragma unroll
+            for (int i = 0; i < VPT; i++)
+                q += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
+            const float rms = sqrtf(wave_sum(q) / n + a.eps);
+#pragma unroll
+            for (int i = 0; i < VPT; i++) {
+                if (!ok[i]) continue;
+                const int c = (i * 64 + lane) * 4;
+                float4 o;
+                F4_APPLY(o, v[i], v[i].x / rms, v[i].y / rms, v[i].z / rms, v[i].w / rms);
+                if (a.gamma) {
+                    const float4 gm = *reinterpret_cast<const float4*>(a.gamma + c);
+                    F4_APPLY(o, o, o.x * gm.x, o.y * gm.y, o.z * gm.z, o.w * gm.w);
+                }
+                *reinterpret_cast<float4*>(a.y + base + c) = o;
+            }
+        } else if constexpr (OP == ROW_SOFTMAX_BWD) {
+            // row.rs:216-236: s = sum p*g; dx = p * (g - s).
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < VPT; i++)
+                s += (v[i].x * g[i].x + v[i].y * g[i].y) + (v[i].z * g[i].z + v[i].w * g[i].w);
+            s = wave_sum(s);
+#pragma unroll
+            for (int i = 0; i < VPT; i++) {
+                if (!ok[i]) continue;
+                float4 o;
+                F4_APPLY(o, v[i], v[i].x * (g[i].x - s), v[i].y * (g[i].y - s),
+                         v[i].z * (g[i].z - s), v[i].w * (g[i].w - s));
+                *reinterpret_cast<float4*>(a.y + base + (i * 64 + lane) * 4) = o;
+            }
+        } else if constexpr (OP == ROW_RMS_NORM_BWD) {
+            // row.rs:416-467: inv = 1/sqrt(q/n + eps), c = d/n*inv^3,
+            // dx = g*inv - x*c, g = dy (* gamma).
+            float q = 0.0f, d = 0.0f;
+#pragma unroll
+            for (int i = 0; i < VPT; i++) {
+                const int c = (i * 64 + lane) * 4;
+                float4 gg = g[i];
+                if (a.gamma && ok[i]) {
+                    const float4 gm = *reinterpret_cast<const float4*>(a.gamma + c);
+                    F4_APPLY(gg, g[i], g[i].x * gm.x, g[i].y * gm.y, g[i].z * gm.z,
+                             g[i].w * gm.w);
+                }
+                q += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
+                d += (v[i].x * gg.x + v[i].y * gg.y) + (v[i].z * gg.z + v[i].w * gg.w);
+            }
+            q = wave_sum(q);
+            d = wave_sum(d);
+            const float rms = sqrtf(q / n + a.eps);
+            const float inv = 1.0f / rms;
+            const float corr = d / n * inv * inv * inv;
+#pragma unroll
+            for (int i = 0; i < VPT; i++) {
+                if (!ok[i]) continue;
+                const int c = (i * 64 + lane) * 4;
+                float4 gg = g[i];
+                if (a.gamma) {
+                    const float4 gm = *reinterpret_cast<const float4*>(a.gamma + c);
+                    F4_APPLY(gg, g[i], g[i].x * gm.x, g[i].y * gm.y, g[i].z * gm.z,
+                             g[i].w * gm.w);
+                }
+                float4 o;
+                F4_APPLY(o, v[i], gg.x * inv - v[i].x * corr, gg.y * inv - v[i].y * corr,
+                         gg.z * inv - v[i].z * corr, gg.w * inv - v[i].w * corr);
+                *reinterpret_cast<float4*>(a.y + base + c) = o;
+                if constexpr (PARTIALS) {
+                    pg[i].x += g[i].x * (v[i].x * inv); pg[i].y += g[i].y * (v[i].y * inv);
+                    pg[i].z += g[i].z * (v[i].z * inv); pg[i].w += g[i].w * (v[i].w * inv);
+                }
+            }
+        }
+    }
+
+    if constexpr (PARTIALS) {
+        // Combine the ROW_WAVES waves of this workgroup in LDS, then write one
+        // partial row per workgroup.
+        if (!a.pgamma && !a.pbeta) return;
+        extern __shared__ float4 red[];  // [ROW_WAVES][cols/4]
+        const int c4n = cols / 4;
+        for (int pass = 0; pass < 2; pass++) {
+            float* dst = pass == 0 ? a.pgamma : a.pbeta;
+            if (!dst) continue;  // uniform across the workgroup
+#pragma unroll
+            for (int i = 0; i < VPT; i++) {
+                const int c4 = i * 64 + lane;
+                if (c4 < c4n) red[wave * c4n + c4] = pass == 0 ? pg[i] : pb[i];
+            }
+            __syncthreads();
+            for (int c4 = threadIdx.x; c4 < c4n; c4 += blockDim.x) {
+                float4 t = red[c4];
+                for (int w = 1; w < ROW_WAVES; w++) {
+                    const float4 u = red[w * c4n + c4];
+                    t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+                }
+                reinterpret_cast<float4*>(dst + (long long)blockIdx.x * cols)[c4] = t;
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// Looping path: any cols and alignment, scalar accesses, one wave per row.
+template <int OP>
+__device__ __forceinline__ void row_kernel_loop(const RowArgs& a) {
+    const int lane = lane_id();
+    const int wave = threadIdx.x >> 6;
+    const int cols = a.cols;
+    const float n = (float)cols;
+    constexpr bool PARTIALS = (OP == ROW_LAYER_NORM_BWD || OP == ROW_RMS_NORM_BWD);
+    // Partials of the looping path are written per wave: row index
+    // blockIdx.x * ROW_WAVES + wave of the partial buffer.
+    const long long prow = (long long)(blockIdx.x * ROW_WAVES + wave) * cols;
+    if constexpr (PARTIALS) {
+        for (int c = lane; c < cols; c += 64) {
+            if (a.pgamma) a.pgamma[prow + c] = 0.0f;
+            if (a.pbeta) a.pbeta[prow + c] = 0.0f;
+        }
+    }
+    for (int row = blockIdx.x * ROW_WAVES + wave; row < a.rows;
+         row += gridDim.x * ROW_WAVES) {
+        const float* x = a.x + (long long)row * cols;
+        float* y = a.y + (long long)row * cols;
+        const float* dy = a.dy ? a.dy + (long long)row * cols : nullptr;
+        if constexpr (OP == ROW_SOFTMAX) {
+            float m = -FLT_MAX;
+            for (int c = lane; c < cols; c += 64) m = fmaxf(m, x[c]);
+            m = wave_max(m);
+            float s = 0.0f;
+            for (int c = lane; c < cols; c += 64) s += expf(x[c] - m);
+            s = wave_sum(s);
+            for (int c = lane; c < cols; c += 64) y[c] = expf(x[c] - m) / s;
+        } else if constexpr (OP == ROW_LAYER_NORM || OP == ROW_LAYER_NORM_BWD) {
+            float s = 0.0f;
+            for (int c = lane; c < cols; c += 64) s += x[c];
+            const float mean = wave_sum(s) / n;
+            float q = 0.0f;
+            for (int c = lane; c < cols; c += 64) {
+                const float d = x[c] - mean;
+                q += d * d;
+            }
+            const float rstd = 1.0f / sqrtf(wave_sum(q) / n + a.eps);
+            if constexpr (OP == ROW_LAYER_NORM) {
+                for (int c = lane; c < cols; c += 64) {
+                    float o = (x[c] - mean) * rstd;
+                    if (a.gamma) o = o * a.gamma[c];
+                    if (a.beta) o = o + a.beta[c];
+                    y[c] = o;
+                }
+            } else {
+                float sa = 0.0f, sb = 0.0f;
+                for (int c = lane; c < cols; c += 64) {
+                    const float gg = a.gamma ? dy[c] * a.gamma[c] : dy[c];
+                    sa += gg;
+                    sb += gg * ((x[c] - mean) * rstd);
+                }
+                sa = wave_sum(sa);
+                sb = wave_sum(sb);
+                const float scale = rstd / n;
+                for (int c = lane; c < cols; c += 64) {
+                    const float xh = (x[c] - mean) * rstd;
+                    const float gg = a.gamma ? dy[c] * a.gamma[c] : dy[c];
+                    y[c] = scale * (n * gg - sa - xh * sb);
+                    if (a.pgamma) a.pgamma[prow + c] += dy[c] * xh;
+                    if (a.pbeta) a.pbeta[prow + c] += dy[c];
+                }
+            }
+        } else if constexpr (OP == ROW_RMS_NORM) {
+            float q = 0.0f;
+            for (int c = lane; c < cols; c += 64) q += x[c] * x[c];
+            const float rms = sqrtf(wave_sum(q) / n + a.eps);
+            for (int c = lane; c < cols; c += 64) {
+                float o = x[c] / rms;
+                if (a.gamma) o = o * a.gamma[c];
+                y[c] = o;
+            }
+        } else if constexpr (OP == ROW_SOFTMAX_BWD) {
+            float s = 0.0f;
+            for (int c = lane; c < cols; c += 64) s += x[c] * dy[c];
+            s = wave_sum(s);
+            for (int c = lane; c < cols; c += 64) y[c] = x[c] * (dy[c] - s);
+        } else if constexpr (OP == ROW_RMS_NORM_BWD) {
+            float q = 0.0f, d = 0.0f;
+            for (int c = lane; c < cols; c += 64) {
+                const float gg = a.gamma ? dy[c] * a.gamma[c] : dy[c];
+                q += x[c] * x[c];
+                d += x[c] * gg;
+            }
+            q = wave_sum(q);
+            d = wave_sum(d);
+            const float rms = sqrtf(q / n + a.eps);
+            const float inv = 1.0f / rms;
+            const float corr = d / n * inv * inv * inv;
+            for (int c = lane; c < cols; c += 64) {
+                const float gg = a.gamma ? dy[c] * a.gamma[c] : dy[c];
+                y[c] = gg * inv - x[c] * corr;
+                if (a.pgamma) a.pgamma[prow + c] += dy[c] * (x[c] * inv);
+            }
+        }
+    }
+}
+
+}  // namespace forge

@@ -1,0 +1,1009 @@
+// runtime.cpp -- implementation of the C ABI in include/oxforge.h.
+//
+// Replaces the cuda-oxide routing of the reference (src/cuda.rs,
+// src/cuda/runtime.rs, src/cuda/span.rs): a HIP device context, a primary
+// non-blocking stream, extra streams joined by events, an exact-size buffer
+// pool, and kernel launches by name from the gfx950 code object through
+// hipModuleLaunchKernel.  Kernel instances are chosen here from shape and
+// alignment (the reference chooses its launch geometry in the container
+// layer, e.g. matrix.rs:133-176 and norm.rs:8-24).
+#include "oxforge.h"
+
+#include <hip/hip_runtime_api.h>
+#include <dlfcn.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+namespace {
+
+thread_local std::string g_last_error;
+
+forge_status fail(forge_status st, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return st;
+}
+
+#define HIP_TRY(expr)                                                          \
+    do {                                                                       \
+        hipError_t e_ = (expr);                                                \
+        if (e_ != hipSuccess)                                                  \
+            return fail(FORGE_EHIP, "%s failed: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+#define FORGE_TRY(expr)                                                        \
+    do {                                                                       \
+        forge_status s_ = (expr);                                              \
+        if (s_ != FORGE_OK) return s_;                                         \
+    } while (0)
+
+// Must match forge::GemmArgs in csrc/kernels/gemm.hpp.
+struct GemmArgs {
+    const float* A;
+    const float* B;
+    float* C;
+    int M, N, K;
+    long long lda, ldb, ldc;
+    float alpha;
+    const float* bias;
+    const float* residual;
+    const float* aux;
+    float* pre_out;
+    int act;
+    int update;
+    float update_scale;
+};
+
+// Must match forge::RowArgs in csrc/kernels/rows.hpp.
+struct RowArgs {
+    const float* x;
+    float* y;
+    const float* dy;
+    const float* gamma;
+    const float* beta;
+    float* pgamma;
+    float* pbeta;
+    int rows, cols;
+    float eps;
+};
+
+constexpr int ROW_WAVES = 4;   // rows.hpp ROW_WAVES
+constexpr int EW_THREADS = 256;  // elementwise.hpp EW_THREADS
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+// Per-stream scratch for multi-pass kernels (column partials, reduction
+// partials).  Each stream owns one so concurrent streams never share it.
+struct Workspace {
+    float* ptr = nullptr;
+    size_t len = 0;
+};
+
+struct forge_stream {
+    hipStream_t stream = nullptr;
+    hipEvent_t event = nullptr;
+    Workspace ws;
+};
+
+struct forge_runtime {
+    int device = 0;
+    forge_stream primary;
+    hipModule_t module = nullptr;
+    std::unordered_map<std::string, hipFunction_t> functions;
+    std::unordered_map<size_t, std::vector<float*>> pool;
+    std::vector<forge_stream*> streams;
+    int cu_count = 0;
+    size_t lds_bytes = 0;
+    int clock_khz = 0;
+    char arch[256] = {0};
+};
+
+namespace {
+
+forge_stream* pick(forge_runtime* rt, forge_stream* s) { return s ? s : &rt->primary; }
+
+forge_status get_function(forge_runtime* rt, const char* name, hipFunction_t* out) {
+    auto it = rt->functions.find(name);
+    if (it != rt->functions.end()) {
+        *out = it->second;
+        return FORGE_OK;
+    }
+    hipFunction_t f = nullptr;
+    hipError_t e = hipModuleGetFunction(&f, rt->module, name);
+    if (e != hipSuccess)
+        return fail(FORGE_ENOMODULE, "kernel %s not found in code object: %s", name,
+                    hipGetErrorString(e));
+    rt->functions.emplace(name, f);
+    *out = f;
+    return FORGE_OK;
+}
+
+// Launches `name` with the given argument addresses (kernelParams form).
+forge_status launch(forge_runtime* rt, forge_stream* s, const char* name, dim3 grid,
+                    dim3 block, size_t shmem, void** args) {
+    if (grid.x == 0 || grid.y == 0 || grid.z == 0) return FORGE_OK;
+    hipFunction_t f;
+    FORGE_TRY(get_function(rt, name, &f));
+    HIP_TRY(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z,
+                                  (unsigned)shmem, pick(rt, s)->stream, args, nullptr));
+    return FORGE_OK;
+}
+
+template <typename... T>
+forge_status launch_args(forge_runtime* rt, forge_stream* s, const char* name, dim3 grid,
+                         dim3 block, size_t shmem, T... values) {
+    void* args[] = {static_cast<void*>(&values)...};
+    return launch(rt, s, name, grid, block, shmem, args);
+}
+
+forge_status workspace(forge_runtime* rt, forge_stream* s, size_t n, float** out) {
+    forge_stream* st = pick(rt, s);
+    if (st->ws.len < n) {
+        if (st->ws.ptr) {
+            // Work queued on this stream may still read the old buffer.
+            HIP_TRY(hipStreamSynchronize(st->stream));
+            HIP_TRY(hipFree(st->ws.ptr));
+            st->ws = Workspace{};
+        }
+        size_t len = std::max<size_t>(n, 1 << 20);
+        void* p = nullptr;
+        if (hipMalloc(&p, len * sizeof(float)) != hipSuccess)
+            return fail(FORGE_ENOMEM, "workspace allocation of %zu floats failed", len);
+        st->ws.ptr = static_cast<float*>(p);
+        st->ws.len = len;
+    }
+    *out = st->ws.ptr;
+    return FORGE_OK;
+}
+
+forge_status need(const forge_slice& s, size_t n, const char* what) {
+    if (n > 0 && (s.ptr == nullptr || s.len < n))
+        return fail(FORGE_EINVAL, "%s: slice of %zu elements (ptr %p) is too short for %zu",
+                    what, s.len, (void*)s.ptr, n);
+    return FORGE_OK;
+}
+
+forge_status need_opt(const forge_slice& s, size_t n, const char* what) {
+    if (s.ptr == nullptr) return FORGE_OK;
+    return need(s, n, what);
+}
+
+bool fits_int(size_t v) { return v <= 0x7fffffffu; }
+
+unsigned grid_for(long long work_items, long long per_block, unsigned cap) {
+    long long g = (work_items + per_block - 1) / per_block;
+    if (g < 1) g = 1;
+    if (g > cap) g = cap;
+    return (unsigned)g;
+}
+
+std::string default_module_path() {
+    if (const char* env = getenv("OXFORGE_KERNELS")) return env;
+    Dl_info info;
+    if (dladdr(reinterpret_cast<void*>(&forge_runtime_create), &info) && info.dli_fname) {
+        std::string p(info.dli_fname);
+        size_t slash = p.rfind('/');
+        std::string dir = slash == std::string::npos ? "." : p.substr(0, slash);
+        return dir + "/oxforge_kernels.hsaco";
+    }
+    return "oxforge_kernels.hsaco";
+}
+
+}  // namespace
+
+// ================================================================ lifecycle
+
+extern "C" forge_status forge_device_count(int* count) {
+    if (!count) return fail(FORGE_EINVAL, "count is null");
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+    *count = n;
+    return FORGE_OK;
+}
+
+extern "C" const char* forge_status_string(forge_status s) {
+    switch (s) {
+    case FORGE_OK: return "ok";
+    case FORGE_EINVAL: return "invalid argument";
+    case FORGE_ENOMEM: return "out of memory";
+    case FORGE_EHIP: return "HIP runtime error";
+    case FORGE_ENOMODULE: return "code object or kernel missing";
+    case FORGE_ENODEV: return "no HIP device";
+    }
+    return "unknown status";
+}
+
+extern "C" const char* forge_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" forge_status forge_runtime_create(int device, const char* module_path,
+                                             forge_runtime** out) {
+    if (!out) return fail(FORGE_EINVAL, "out is null");
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+        return fail(FORGE_ENODEV, "no HIP device is visible");
+    if (device < 0 || device >= n)
+        return fail(FORGE_ENODEV, "device %d requested, %d visible", device, n);
+    std::string path = module_path ? module_path : default_module_path();
+    FILE* f = fopen(path.c_str(), "rb");
+    if (!f) return fail(FORGE_ENOMODULE, "code object %s not found", path.c_str());
+    fclose(f);
+
+    HIP_TRY(hipSetDevice(device));
+    auto* rt = new forge_runtime();
+    rt->device = device;
+    hipError_t e = hipModuleLoad(&rt->module, path.c_str());
+    if (e != hipSuccess) {
+        delete rt;
+        return fail(FORGE_ENOMODULE, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e));
+    }
+    if (hipStreamCreateWithFlags(&rt->primary.stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&rt->primary.event, hipEventDisableTiming) != hipSuccess) {
+        (void)hipModuleUnload(rt->module);
+        delete rt;
+        return fail(FORGE_EHIP, "primary stream creation failed");
+    }
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess) {
+        rt->cu_count = prop.multiProcessorCount;
+        rt->lds_bytes = prop.sharedMemPerBlock;
+        rt->clock_khz = prop.clockRate;
+        snprintf(rt->arch, sizeof rt->arch, "%s", prop.gcnArchName);
+    }
+    *out = rt;
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_runtime_destroy(forge_runtime* rt) {
+    if (!rt) return FORGE_OK;
+    (void)hipSetDevice(rt->device);
+    (void)hipDeviceSynchronize();
+    for (auto& kv : rt->pool)
+        for (float* p : kv.second) (void)hipFree(p);
+    for (forge_stream* s : rt->streams) {
+        if (s->ws.ptr) (void)hipFree(s->ws.ptr);
+        (void)hipEventDestroy(s->event);
+        (void)hipStreamDestroy(s->stream);
+        delete s;
+    }
+    if (rt->primary.ws.ptr) (void)hipFree(rt->primary.ws.ptr);
+    (void)hipEventDestroy(rt->primary.event);
+    (void)hipStreamDestroy(rt->primary.stream);
+    (void)hipModuleUnload(rt->module);
+    delete rt;
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_sync(forge_runtime* rt, forge_stream* s) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    HIP_TRY(hipStreamSynchronize(pick(rt, s)->stream));
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_device_props(forge_runtime* rt, int* cu_count, size_t* lds_bytes,
+                                           int* clock_khz, char* arch, size_t arch_len) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    if (cu_count) *cu_count = rt->cu_count;
+    if (lds_bytes) *lds_bytes = rt->lds_bytes;
+    if (clock_khz) *clock_khz = rt->clock_khz;
+    if (arch && arch_len) snprintf(arch, arch_len, "%s", rt->arch);
+    return FORGE_OK;
+}
+
+// ================================================================== streams
+
+extern "C" forge_status forge_streams_create(forge_runtime* rt, size_t n, forge_stream** out) {
+    if (!rt || (n && !out)) return fail(FORGE_EINVAL, "null argument");
+    HIP_TRY(hipEventRecord(rt->primary.event, rt->primary.stream));
+    for (size_t i = 0; i < n; i++) {
+        auto* s = new forge_stream();
+        if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess ||
+            hipEventCreateWithFlags(&s->event, hipEventDisableTiming) != hipSuccess) {
+            delete s;
+            return fail(FORGE_EHIP, "stream creation failed");
+        }
+        // CudaStream::fork: the new stream starts after the primary's work.
+        HIP_TRY(hipStreamWaitEvent(s->stream, rt->primary.event, 0));
+        rt->streams.push_back(s);
+        out[i] = s;
+    }
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_streams_fork(forge_runtime* rt, size_t n,
+                                           forge_stream* const* streams) {
+    if (!rt || (n && !streams)) return fail(FORGE_EINVAL, "null argument");
+    HIP_TRY(hipEventRecord(rt->primary.event, rt->primary.stream));
+    for (size_t i = 0; i < n; i++)
+        HIP_TRY(hipStreamWaitEvent(streams[i]->stream, rt->primary.event, 0));
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_streams_join(forge_runtime* rt, size_t n,
+                                           forge_stream* const* streams) {
+    if (!rt || (n && !streams)) return fail(FORGE_EINVAL, "null argument");
+    for (size_t i = 0; i < n; i++) {
+        HIP_TRY(hipEventRecord(streams[i]->event, streams[i]->stream));
+        HIP_TRY(hipStreamWaitEvent(rt->primary.stream, streams[i]->event, 0));
+    }
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_stream_wait(forge_runtime* rt, forge_stream* waiter,
+                                          forge_stream* signaler) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    forge_stream* w = pick(rt, waiter);
+    forge_stream* g = pick(rt, signaler);
+    if (w == g) return FORGE_OK;
+    HIP_TRY(hipEventRecord(g->event, g->stream));
+    HIP_TRY(hipStreamWaitEvent(w->stream, g->event, 0));
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_stream_destroy(forge_runtime* rt, forge_stream* s) {
+    if (!rt || !s) return fail(FORGE_EINVAL, "null argument");
+    auto it = std::find(rt->streams.begin(), rt->streams.end(), s);
+    if (it == rt->streams.end()) return fail(FORGE_EINVAL, "stream not owned by this runtime");
+    HIP_TRY(hipStreamSynchronize(s->stream));
+    if (s->ws.ptr) (void)hipFree(s->ws.ptr);
+    (void)hipEventDestroy(s->event);
+    (void)hipStreamDestroy(s->stream);
+    rt->streams.erase(it);
+    delete s;
+    return FORGE_OK;
+}
+
+// =================================================================== events
+
+struct forge_event {
+    hipEvent_t event = nullptr;
+};
+
+extern "C" forge_status forge_event_create(forge_runtime* rt, forge_event** out) {
+    if (!rt || !out) return fail(FORGE_EINVAL, "null argument");
+    auto* e = new forge_event();
+    if (hipEventCreate(&e->event) != hipSuccess) {
+        delete e;
+        return fail(FORGE_EHIP, "hipEventCreate failed");
+    }
+    *out = e;
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_event_record(forge_runtime* rt, forge_stream* s, forge_event* ev) {
+    if (!rt || !ev) return fail(FORGE_EINVAL, "null argument");
+    HIP_TRY(hipEventRecord(ev->event, pick(rt, s)->stream));
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_event_elapsed_ms(forge_runtime* rt, forge_event* start,
+                                               forge_event* end, float* ms) {
+    if (!rt || !start || !end || !ms) return fail(FORGE_EINVAL, "null argument");
+    HIP_TRY(hipEventSynchronize(end->event));
+    HIP_TRY(hipEventElapsedTime(ms, start->event, end->event));
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_event_destroy(forge_runtime* rt, forge_event* ev) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    if (!ev) return FORGE_OK;
+    (void)hipEventDestroy(ev->event);
+    delete ev;
+    return FORGE_OK;
+}
+
+// =================================================================== memory
+
+extern "C" forge_status forge_alloc(forge_runtime* rt, size_t n, forge_slice* out) {
+    if (!rt || !out) return fail(FORGE_EINVAL, "null argument");
+    out->ptr = nullptr;
+    out->len = 0;
+    if (n == 0) return FORGE_OK;
+    auto it = rt->pool.find(n);
+    if (it != rt->pool.end() && !it->second.empty()) {
+        out->ptr = it->second.back();
+        it->second.pop_back();
+        out->len = n;
+        return FORGE_OK;
+    }
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, n * sizeof(float));
+    if (e != hipSuccess)
+        return fail(FORGE_ENOMEM, "hipMalloc of %zu floats: %s", n, hipGetErrorString(e));
+    out->ptr = static_cast<float*>(p);
+    out->len = n;
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_alloc_zeroed(forge_runtime* rt, size_t n, forge_slice* out) {
+    FORGE_TRY(forge_alloc(rt, n, out));
+    return forge_fill(rt, nullptr, *out, 0.0f);
+}
+
+extern "C" forge_status forge_recycle(forge_runtime* rt, forge_slice buf) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    if (!buf.ptr || buf.len == 0) return FORGE_OK;
+    rt->pool[buf.len].push_back(buf.ptr);
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_free(forge_runtime* rt, forge_slice buf) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    if (!buf.ptr) return FORGE_OK;
+    HIP_TRY(hipStreamSynchronize(rt->primary.stream));
+    HIP_TRY(hipFree(buf.ptr));
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_reserve(forge_runtime* rt, size_t n, size_t count) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    if (n == 0) return FORGE_OK;
+    auto& v = rt->pool[n];
+    while (v.size() < count) {
+        void* p = nullptr;
+        hipError_t e = hipMalloc(&p, n * sizeof(float));
+        if (e != hipSuccess)
+            return fail(FORGE_ENOMEM, "hipMalloc of %zu floats: %s", n, hipGetErrorString(e));
+        v.push_back(static_cast<float*>(p));
+    }
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_pool_count(forge_runtime* rt, size_t n, size_t* count) {
+    if (!rt || !count) return fail(FORGE_EINVAL, "null argument");
+    auto it = rt->pool.find(n);
+    *count = it == rt->pool.end() ? 0 : it->second.size();
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_memcpy_h2d(forge_runtime* rt, forge_slice dst, const float* src,
+                                         size_t n) {
+    if (!rt || (n && !src)) return fail(FORGE_EINVAL, "null argument");
+    FORGE_TRY(need(dst, n, "memcpy_h2d dst"));
+    if (n == 0) return FORGE_OK;
+    HIP_TRY(hipMemcpyAsync(dst.ptr, src, n * sizeof(float), hipMemcpyHostToDevice,
+                           rt->primary.stream));
+    HIP_TRY(hipStreamSynchronize(rt->primary.stream));
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_memcpy_d2h(forge_runtime* rt, float* dst, forge_slice src,
+                                         size_t n) {
+    if (!rt || (n && !dst)) return fail(FORGE_EINVAL, "null argument");
+    FORGE_TRY(need(src, n, "memcpy_d2h src"));
+    if (n == 0) return FORGE_OK;
+    HIP_TRY(hipMemcpyAsync(dst, src.ptr, n * sizeof(float), hipMemcpyDeviceToHost,
+                           rt->primary.stream));
+    HIP_TRY(hipStreamSynchronize(rt->primary.stream));
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_memcpy_d2d(forge_runtime* rt, forge_stream* s, forge_slice dst,
+                                         forge_slice src, size_t n) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    FORGE_TRY(need(dst, n, "memcpy_d2d dst"));
+    FORGE_TRY(need(src, n, "memcpy_d2d src"));
+    if (n == 0) return FORGE_OK;
+    HIP_TRY(hipMemcpyAsync(dst.ptr, src.ptr, n * sizeof(float), hipMemcpyDeviceToDevice,
+                           pick(rt, s)->stream));
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_fill(forge_runtime* rt, forge_stream* s, forge_slice x, float value) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    if (!x.ptr || x.len == 0) return FORGE_OK;
+    long long n = (long long)x.len;
+    bool vec = aligned16(x.ptr);
+    unsigned g = grid_for(vec ? n / 4 + 1 : n, EW_THREADS, 4096);
+    return launch_args(rt, s, vec ? "forge_fill_v" : "forge_fill_s", dim3(g), dim3(EW_THREADS), 0,
+                       x.ptr, n, value);
+}
+
+// ================================================================== kernels
+
+namespace {
+
+struct GemmConfig {
+    const char* tag;  // e.g. "128x128x16_2x2"
+    int bm, bn, bk;
+};
+
+const GemmConfig kFast128 = {"128x128x16_2x2", 128, 128, 16};
+const GemmConfig kFast128x64 = {"128x64x16_2x2", 128, 64, 16};
+const GemmConfig kFast256 = {"256x128x16_2x2", 256, 128, 16};
+const GemmConfig kGuard64 = {"64x64x16_2x2_g", 64, 64, 16};
+
+// Picks the tile configuration: unguarded when the shape divides the tile
+// and every operand is 16-byte aligned with 4-float-multiple leading
+// dimensions, the guarded 64x64 tile otherwise.  The 256x128 tile is used
+// when it still yields at least two tiles per CU.
+const GemmConfig& choose_gemm(forge_runtime* rt, size_t M, size_t N, size_t K, bool aligned) {
+    (void)rt;
+    auto fits = [&](const GemmConfig& c) {
+        return aligned && M % c.bm == 0 && N % c.bn == 0 && K % c.bk == 0;
+    };
+    if (fits(kFast128)) return kFast128;
+    if (fits(kFast128x64)) return kFast128x64;
+    return kGuard64;
+}
+
+forge_status gemm_dispatch(forge_runtime* rt, forge_stream* s, int ta, int tb, forge_slice A,
+                           forge_slice B, forge_slice C, size_t M, size_t N, size_t K,
+                           const forge_gemm_epilogue* ep, bool plain_name) {
+    if (!fits_int(M) || !fits_int(N) || !fits_int(K))
+        return fail(FORGE_EINVAL, "gemm dimensions exceed 2^31-1");
+    FORGE_TRY(need(A, M * K, "gemm A"));
+    FORGE_TRY(need(B, K * N, "gemm B"));
+    FORGE_TRY(need(C, M * N, "gemm C"));
+    if (M == 0 || N == 0) return FORGE_OK;
+    GemmArgs a{};
+    a.A = A.ptr;
+    a.B = B.ptr;
+    a.C = C.ptr;
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.lda = ta ? (long long)M : (long long)K;
+    a.ldb = tb ? (long long)K : (long long)N;
+    a.ldc = (long long)N;
+    a.alpha = 1.0f;
+    bool aligned = aligned16(A.ptr) && aligned16(B.ptr) && aligned16(C.ptr) && a.lda % 4 == 0 &&
+                   a.ldb % 4 == 0;
+    if (ep) {
+        FORGE_TRY(need_opt(ep->bias, N, "gemm bias"));
+        FORGE_TRY(need_opt(ep->residual, M * N, "gemm residual"));
+        FORGE_TRY(need_opt(ep->aux_mul, M * N, "gemm aux_mul"));
+        FORGE_TRY(need_opt(ep->pre_out, M * N, "gemm pre_out"));
+        if (ep->activation < FORGE_ACT_IDENTITY || ep->activation > FORGE_ACT_SILU)
+            return fail(FORGE_EINVAL, "unknown activation %d", ep->activation);
+        a.alpha = ep->alpha;
+        a.bias = ep->bias.ptr;
+        a.residual = ep->residual.ptr;
+        a.aux = ep->aux_mul.ptr;
+        a.pre_out = ep->pre_out.ptr;
+        a.act = ep->activation;
+        a.update = ep->update ? 1 : 0;
+        a.update_scale = ep->update_scale;
+    }
+    const GemmConfig& cfg = choose_gemm(rt, M, N, K, aligned);
+    char name[96];
+    const char ab[2][2][3] = {{"nn", "nt"}, {"tn", "tt"}};
+    const bool epi = !(plain_name && !ta && !tb);
+    snprintf(name, sizeof name, "forge_gemm_%s_%s%s", ab[ta ? 1 : 0][tb ? 1 : 0], cfg.tag,
+             epi ? "_e" : "");
+    unsigned tiles = (unsigned)(((M + cfg.bm - 1) / cfg.bm) * ((N + cfg.bn - 1) / cfg.bn));
+    void* args[] = {&a};
+    return launch(rt, s, name, dim3(tiles), dim3(256), 0, args);
+}
+
+const char* binop_name(forge_binary_op op) {
+    switch (op) {
+    case FORGE_ADD: return "add";
+    case FORGE_SUB: return "sub";
+    case FORGE_MUL: return "mul";
+    case FORGE_DIV: return "div";
+    }
+    return nullptr;
+}
+
+const char* map_name(forge_map_op op) {
+    switch (op) {
+    case FORGE_MAP_SCALE: return "scale";
+    case FORGE_MAP_ADD: return "add";
+    case FORGE_MAP_GELU: return "gelu";
+    case FORGE_MAP_GELU_D: return "gelu_d";
+    case FORGE_MAP_RELU: return "relu";
+    case FORGE_MAP_RELU_D: return "relu_d";
+    case FORGE_MAP_SILU: return "silu";
+    case FORGE_MAP_SILU_D: return "silu_d";
+    case FORGE_MAP_EXP_SHIFT: return "exp_shift";
+    case FORGE_MAP_HALF_SQ: return "half_sq";
+    case FORGE_MAP_IDENTITY: return "identity";
+    }
+    return nullptr;
+}
+
+// Elements per lane of the register path for `cols` (0 = use the loop path).
+int row_vpt(size_t cols, bool aligned) {
+    if (!aligned || cols % 4 != 0 || cols == 0) return 0;
+    for (int v : {1, 2, 4, 8, 16})
+        if (cols <= (size_t)v * 256) return v;
+    return 0;
+}
+
+// Column sums of m [rows, cols] into out [cols] with one or two launches of
+// forge_sum_cols: chunks of at least 16 rows are summed into partial rows,
+// then the partial rows are summed.  Chunking depends only on the shape, so
+// the result is deterministic.
+size_t sum_cols_chunks(size_t rows, size_t cols) {
+    size_t gx = (cols + EW_THREADS - 1) / EW_THREADS;
+    size_t want = std::max<size_t>(1, 2048 / std::max<size_t>(1, gx));
+    size_t by_rows = (rows + 15) / 16;
+    return std::max<size_t>(1, std::min(want, by_rows));
+}
+
+// Floats of scratch sum_cols_impl needs for this shape.
+size_t sum_cols_scratch(size_t rows, size_t cols) {
+    size_t chunks = sum_cols_chunks(rows, cols);
+    return chunks > 1 ? chunks * cols : 0;
+}
+
+// scratch: sum_cols_scratch(rows, cols) floats that do not overlap m/out.
+forge_status sum_cols_impl(forge_runtime* rt, forge_stream* s, const float* m, float* out,
+                           size_t rows, size_t cols, float* scratch) {
+    if (cols == 0) return FORGE_OK;
+    int c = (int)cols;
+    unsigned gx = (unsigned)((cols + EW_THREADS - 1) / EW_THREADS);
+    size_t chunks = sum_cols_chunks(rows, cols);
+    int rpc = (int)std::max<size_t>(1, (rows + chunks - 1) / chunks);
+    chunks = rows == 0 ? 1 : (rows + rpc - 1) / rpc;
+    int r = (int)rows;
+    if (chunks == 1)
+        return launch_args(rt, s, "forge_sum_cols", dim3(gx, 1), dim3(EW_THREADS), 0, m, out, r, c,
+                           rpc);
+    FORGE_TRY(launch_args(rt, s, "forge_sum_cols", dim3(gx, (unsigned)chunks), dim3(EW_THREADS),
+                          0, m, scratch, r, c, rpc));
+    int ch = (int)chunks;
+    return launch_args(rt, s, "forge_sum_cols", dim3(gx, 1), dim3(EW_THREADS), 0,
+                       (const float*)scratch, out, ch, c, ch);
+}
+
+// Shared launcher of the six row kernels.  For the norm backward kernels
+// with dgamma/dbeta requested, the partial rows land in the stream's
+// workspace and are summed by sum_cols_impl.
+forge_status row_launch(forge_runtime* rt, forge_stream* s, const char* op, RowArgs a,
+                        float* dgamma, float* dbeta) {
+    if (a.rows == 0 || a.cols == 0) {
+        if (dgamma) FORGE_TRY(forge_fill(rt, s, forge_slice{dgamma, (size_t)a.cols}, 0.0f));
+        if (dbeta) FORGE_TRY(forge_fill(rt, s, forge_slice{dbeta, (size_t)a.cols}, 0.0f));
+        return FORGE_OK;
+    }
+    bool aligned = aligned16(a.x) && aligned16(a.y) && (!a.dy || aligned16(a.dy)) &&
+                   (!a.gamma || aligned16(a.gamma)) && (!a.beta || aligned16(a.beta));
+    int vpt = row_vpt((size_t)a.cols, aligned);
+    const bool partials = dgamma || dbeta;
+    if (partials && vpt > 8) vpt = 0;  // register path with partials: <= 8 float4
+    char name[80];
+    unsigned blocks_needed = (unsigned)((a.rows + ROW_WAVES - 1) / ROW_WAVES);
+    unsigned grid;
+    size_t shmem = 0;
+    size_t prow = 0;
+    float* ws = nullptr;
+    if (partials) {
+        // One partial row per workgroup (register path) or per wave (loop).
+        grid = std::min<unsigned>(blocks_needed, (unsigned)std::max(64, rt->cu_count));
+        prow = vpt ? grid : (size_t)grid * ROW_WAVES;
+        size_t per = prow * (size_t)a.cols;
+        FORGE_TRY(workspace(rt, s, per * 2 + sum_cols_scratch(prow, (size_t)a.cols), &ws));
+        a.pgamma = dgamma ? ws : nullptr;
+        a.pbeta = dbeta ? ws + per : nullptr;
+        if (vpt) shmem = (size_t)ROW_WAVES * (size_t)a.cols * sizeof(float);
+        if (vpt) snprintf(name, sizeof name, "forge_row_%s_v%d_p", op, vpt);
+        else snprintf(name, sizeof name, "forge_row_%s_loop", op);
+    } else {
+        grid = std::min<unsigned>(blocks_needed, 1u << 20);
+        if (vpt) snprintf(name, sizeof name, "forge_row_%s_v%d", op, vpt);
+        else snprintf(name, sizeof name, "forge_row_%s_loop", op);
+    }
+    void* args[] = {&a};
+    FORGE_TRY(launch(rt, s, name, dim3(grid), dim3(ROW_WAVES * 64), shmem, args));
+    float* chunk_scratch = ws ? ws + 2 * prow * (size_t)a.cols : nullptr;
+    if (dgamma)
+        FORGE_TRY(sum_cols_impl(rt, s, a.pgamma, dgamma, prow, (size_t)a.cols, chunk_scratch));
+    if (dbeta)
+        FORGE_TRY(sum_cols_impl(rt, s, a.pbeta, dbeta, prow, (size_t)a.cols, chunk_scratch));
+    return FORGE_OK;
+}
+
+forge_status check_rows(size_t rows, size_t cols) {
+    if (!fits_int(rows) || !fits_int(cols)) return fail(FORGE_EINVAL, "rows/cols exceed 2^31-1");
+    return FORGE_OK;
+}
+
+}  // namespace
+
+extern "C" forge_status forge_gemm_f32(forge_runtime* rt, forge_stream* s, forge_slice A,
+                                       forge_slice B, forge_slice C, size_t M, size_t N,
+                                       size_t K) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    return gemm_dispatch(rt, s, 0, 0, A, B, C, M, N, K, nullptr, true);
+}
+
+extern "C" forge_status forge_gemm_ex_f32(forge_runtime* rt, forge_stream* s, int trans_a,
+                                          int trans_b, forge_slice A, forge_slice B, forge_slice C,
+                                          size_t M, size_t N, size_t K,
+                                          const forge_gemm_epilogue* ep) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    return gemm_dispatch(rt, s, trans_a != 0, trans_b != 0, A, B, C, M, N, K, ep, false);
+}
+
+extern "C" forge_status forge_gemm_f32_tile(forge_runtime* rt, forge_stream* s,
+                                            const char* tile_tag, forge_slice A, forge_slice B,
+                                            forge_slice C, size_t M, size_t N, size_t K) {
+    if (!rt || !tile_tag) return fail(FORGE_EINVAL, "null argument");
+    unsigned bm = 0, bn = 0, bk = 0, wm = 0, wn = 0;
+    char tail[8] = {0};
+    int got = sscanf(tile_tag, "%ux%ux%u_%ux%u%7s", &bm, &bn, &bk, &wm, &wn, tail);
+    if (got < 5 || bm == 0 || bn == 0 || bk == 0 || wm == 0 || wn == 0 || wm * wn > 16)
+        return fail(FORGE_EINVAL, "bad tile tag %s", tile_tag);
+    const bool guarded = strcmp(tail, "_g") == 0;
+    if (got == 6 && !guarded) return fail(FORGE_EINVAL, "bad tile tag %s", tile_tag);
+    if (!fits_int(M) || !fits_int(N) || !fits_int(K))
+        return fail(FORGE_EINVAL, "gemm dimensions exceed 2^31-1");
+    FORGE_TRY(need(A, M * K, "gemm A"));
+    FORGE_TRY(need(B, K * N, "gemm B"));
+    FORGE_TRY(need(C, M * N, "gemm C"));
+    if (!guarded && (M % bm || N % bn || K % bk || !aligned16(A.ptr) || !aligned16(B.ptr) ||
+                     !aligned16(C.ptr) || K % 4 || N % 4))
+        return fail(FORGE_EINVAL, "shape %zux%zux%zu does not fit unguarded tile %s", M, N, K,
+                    tile_tag);
+    if (M == 0 || N == 0) return FORGE_OK;
+    GemmArgs a{};
+    a.A = A.ptr;
+    a.B = B.ptr;
+    a.C = C.ptr;
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.lda = (long long)K;
+    a.ldb = (long long)N;
+    a.ldc = (long long)N;
+    a.alpha = 1.0f;
+    char name[96];
+    snprintf(name, sizeof name, "forge_gemm_nn_%s", tile_tag);
+    unsigned tiles = (unsigned)(((M + bm - 1) / bm) * ((N + bn - 1) / bn));
+    void* args[] = {&a};
+    return launch(rt, s, name, dim3(tiles), dim3(wm * wn * 64), 0, args);
+}
+
+extern "C" forge_status forge_transpose_f32(forge_runtime* rt, forge_stream* s, forge_slice in,
+                                            forge_slice out, size_t rows, size_t cols) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    FORGE_TRY(check_rows(rows, cols));
+    FORGE_TRY(need(in, rows * cols, "transpose in"));
+    FORGE_TRY(need(out, rows * cols, "transpose out"));
+    if (rows == 0 || cols == 0) return FORGE_OK;
+    bool fast = aligned16(in.ptr) && aligned16(out.ptr) && rows % 64 == 0 && cols % 64 == 0;
+    unsigned tiles = (unsigned)(((rows + 63) / 64) * ((cols + 63) / 64));
+    int r = (int)rows, c = (int)cols;
+    return launch_args(rt, s, fast ? "forge_transpose" : "forge_transpose_g", dim3(tiles),
+                       dim3(256), 0, (const float*)in.ptr, out.ptr, r, c);
+}
+
+extern "C" forge_status forge_softmax_rows(forge_runtime* rt, forge_stream* s, forge_slice x,
+                                           size_t rows, size_t cols) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    FORGE_TRY(check_rows(rows, cols));
+    FORGE_TRY(need(x, rows * cols, "softmax x"));
+    RowArgs a{x.ptr, x.ptr, nullptr, nullptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, 0.f};
+    return row_launch(rt, s, "softmax", a, nullptr, nullptr);
+}
+
+extern "C" forge_status forge_softmax_rows_bwd(forge_runtime* rt, forge_stream* s, forge_slice p,
+                                               forge_slice g, forge_slice dx, size_t rows,
+                                               size_t cols) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    FORGE_TRY(check_rows(rows, cols));
+    FORGE_TRY(need(p, rows * cols, "softmax_bwd p"));
+    FORGE_TRY(need(g, rows * cols, "softmax_bwd g"));
+    FORGE_TRY(need(dx, rows * cols, "softmax_bwd dx"));
+    RowArgs a{p.ptr, dx.ptr, g.ptr, nullptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, 0.f};
+    return row_launch(rt, s, "softmax_bwd", a, nullptr, nullptr);
+}
+
+extern "C" forge_status forge_layer_norm_rows(forge_runtime* rt, forge_stream* s, forge_slice x,
+                                              forge_slice gamma, forge_slice beta, size_t rows,
+                                              size_t cols, float eps) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    FORGE_TRY(check_rows(rows, cols));
+    FORGE_TRY(need(x, rows * cols, "layer_norm x"));
+    FORGE_TRY(need_opt(gamma, cols, "layer_norm gamma"));
+    FORGE_TRY(need_opt(beta, cols, "layer_norm beta"));
+    RowArgs a{x.ptr, x.ptr, nullptr, gamma.ptr, beta.ptr, nullptr, nullptr, (int)rows, (int)cols, eps};
+    return row_launch(rt, s, "layer_norm", a, nullptr, nullptr);
+}
+
+extern "C" forge_status forge_layer_norm_bwd(forge_runtime* rt, forge_stream* s, forge_slice x,
+                                             forge_slice dy, forge_slice gamma, forge_slice dx,
+                                             forge_slice dgamma, forge_slice dbeta, size_t rows,
+                                             size_t cols, float eps) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    FORGE_TRY(check_rows(rows, cols));
+    FORGE_TRY(need(x, rows * cols, "layer_norm_bwd x"));
+    FORGE_TRY(need(dy, rows * cols, "layer_norm_bwd dy"));
+    FORGE_TRY(need(dx, rows * cols, "layer_norm_bwd dx"));
+    FORGE_TRY(need_opt(gamma, cols, "layer_norm_bwd gamma"));
+    FORGE_TRY(need_opt(dgamma, cols, "layer_norm_bwd dgamma"));
+    FORGE_TRY(need_opt(dbeta, cols, "layer_norm_bwd dbeta"));
+    RowArgs a{x.ptr, dx.ptr, dy.ptr, gamma.ptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, eps};
+    return row_launch(rt, s, "layer_norm_bwd", a, dgamma.ptr, dbeta.ptr);
+}
+
+extern "C" forge_status forge_rms_norm_rows(forge_runtime* rt, forge_stream* s, forge_slice x,
+                                            forge_slice gamma, size_t rows, size_t cols,
+                                            float eps) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    FORGE_TRY(check_rows(rows, cols));
+    FORGE_TRY(need(x, rows * cols, "rms_norm x"));
+    FORGE_TRY(need_opt(gamma, cols, "rms_norm gamma"));
+    RowArgs a{x.ptr, x.ptr, nullptr, gamma.ptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, eps};
+    return row_launch(rt, s, "rms_norm", a, nullptr, nullptr);
+}
+
+extern "C" forge_status forge_rms_norm_bwd(forge_runtime* rt, forge_stream* s, forge_slice x,
+                                           forge_slice dy, forge_slice gamma, forge_slice dx,
+                                           forge_slice dgamma, size_t rows, size_t cols,
+                                           float eps) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    FORGE_TRY(check_rows(rows, cols));
+    FORGE_TRY(need(x, rows * cols, "rms_norm_bwd x"));
+    FORGE_TRY(need(dy, rows * cols, "rms_norm_bwd dy"));
+    FORGE_TRY(need(dx, rows * cols, "rms_norm_bwd dx"));
+    FORGE_TRY(need_opt(gamma, cols, "rms_norm_bwd gamma"));
+    FORGE_TRY(need_opt(dgamma, cols, "rms_norm_bwd dgamma"));
+    RowArgs a{x.ptr, dx.ptr, dy.ptr, gamma.ptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, eps};
+    return row_launch(rt, s, "rms_norm_bwd", a, dgamma.ptr, nullptr);
+}
+
+extern "C" forge_status forge_binary(forge_runtime* rt, forge_stream* s, forge_slice l,
+                                     forge_slice r, forge_slice o, size_t n, forge_binary_op op) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    const char* nm = binop_name(op);
+    if (!nm) return fail(FORGE_EINVAL, "unknown binary op %d", (int)op);
+    FORGE_TRY(need(l, n, "binary l"));
+    FORGE_TRY(need(r, n, "binary r"));
+    FORGE_TRY(need(o, n, "binary o"));
+    if (n == 0) return FORGE_OK;
+    bool vec = aligned16(l.ptr) && aligned16(r.ptr) && aligned16(o.ptr);
+    char name[64];
+    snprintf(name, sizeof name, "forge_binary_%s_%s", nm, vec ? "v" : "s");
+    long long nn = (long long)n;
+    unsigned g = grid_for(vec ? nn / 4 + 1 : nn, EW_THREADS, 8192);
+    return launch_args(rt, s, name, dim3(g), dim3(EW_THREADS), 0, (const float*)l.ptr,
+                       (const float*)r.ptr, o.ptr, nn);
+}
+
+extern "C" forge_status forge_binary_assign(forge_runtime* rt, forge_stream* s, forge_slice t,
+                                            forge_slice r, size_t n, forge_binary_op op) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    const char* nm = binop_name(op);
+    if (!nm) return fail(FORGE_EINVAL, "unknown binary op %d", (int)op);
+    FORGE_TRY(need(t, n, "binary_assign t"));
+    FORGE_TRY(need(r, n, "binary_assign r"));
+    if (n == 0) return FORGE_OK;
+    bool vec = aligned16(t.ptr) && aligned16(r.ptr);
+    char name[64];
+    snprintf(name, sizeof name, "forge_binary_assign_%s_%s", nm, vec ? "v" : "s");
+    long long nn = (long long)n;
+    unsigned g = grid_for(vec ? nn / 4 + 1 : nn, EW_THREADS, 8192);
+    return launch_args(rt, s, name, dim3(g), dim3(EW_THREADS), 0, t.ptr, (const float*)r.ptr, nn);
+}
+
+extern "C" forge_status forge_binary_assign_by_rows(forge_runtime* rt, forge_stream* s,
+                                                    forge_slice m, forge_slice row, size_t rows,
+                                                    size_t cols, forge_binary_op op) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    const char* nm = binop_name(op);
+    if (!nm) return fail(FORGE_EINVAL, "unknown binary op %d", (int)op);
+    FORGE_TRY(check_rows(rows, cols));
+    FORGE_TRY(need(m, rows * cols, "by_rows m"));
+    FORGE_TRY(need(row, cols, "by_rows row"));
+    if (rows == 0 || cols == 0) return FORGE_OK;
+    bool vec = aligned16(m.ptr) && aligned16(row.ptr) && cols % 4 == 0;
+    char name[64];
+    snprintf(name, sizeof name, "forge_by_rows_%s_%s", nm, vec ? "v" : "s");
+    size_t lanes = vec ? cols / 4 : cols;
+    unsigned gx = (unsigned)((lanes + EW_THREADS - 1) / EW_THREADS);
+    // About 4096 workgroups in total, at most one row per y index.
+    unsigned gy = (unsigned)std::max<size_t>(1, std::min<size_t>(rows, std::max<size_t>(1, 4096 / gx)));
+    gy = std::min(gy, 65535u);
+    int r = (int)rows, c = (int)cols;
+    return launch_args(rt, s, name, dim3(gx, gy), dim3(EW_THREADS), 0, m.ptr,
+                       (const float*)row.ptr, r, c);
+}
+
+extern "C" forge_status forge_map(forge_runtime* rt, forge_stream* s, forge_slice x, size_t n,
+                                  forge_map_op op, float p0) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    const char* nm = map_name(op);
+    if (!nm) return fail(FORGE_EINVAL, "unknown map op %d", (int)op);
+    FORGE_TRY(need(x, n, "map x"));
+    if (n == 0) return FORGE_OK;
+    bool vec = aligned16(x.ptr);
+    char name[64];
+    snprintf(name, sizeof name, "forge_map_%s_%s", nm, vec ? "v" : "s");
+    long long nn = (long long)n;
+    unsigned g = grid_for(vec ? nn / 4 + 1 : nn, EW_THREADS, 8192);
+    return launch_args(rt, s, name, dim3(g), dim3(EW_THREADS), 0, x.ptr, nn, p0);
+}
+
+extern "C" forge_status forge_sum_rows(forge_runtime* rt, forge_stream* s, forge_slice m,
+                                       forge_slice out, size_t rows, size_t cols) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    FORGE_TRY(check_rows(rows, cols));
+    FORGE_TRY(need(m, rows * cols, "sum_rows m"));
+    FORGE_TRY(need(out, rows, "sum_rows out"));
+    if (rows == 0) return FORGE_OK;
+    bool vec = aligned16(m.ptr) && cols % 4 == 0;
+    unsigned g = grid_for((long long)rows, EW_THREADS / 64, 1u << 20);
+    int r = (int)rows, c = (int)cols;
+    return launch_args(rt, s, vec ? "forge_sum_rows_v" : "forge_sum_rows_s", dim3(g),
+                       dim3(EW_THREADS), 0, (const float*)m.ptr, out.ptr, r, c);
+}
+
+extern "C" forge_status forge_sum_cols(forge_runtime* rt, forge_stream* s, forge_slice m,
+                                       forge_slice out, size_t rows, size_t cols) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    FORGE_TRY(check_rows(rows, cols));
+    FORGE_TRY(need(m, rows * cols, "sum_cols m"));
+    FORGE_TRY(need(out, cols, "sum_cols out"));
+    float* scratch = nullptr;
+    size_t need_ws = sum_cols_scratch(rows, cols);
+    if (need_ws) FORGE_TRY(workspace(rt, s, need_ws, &scratch));
+    return sum_cols_impl(rt, s, m.ptr, out.ptr, rows, cols, scratch);
+}
+
+namespace {
+forge_status reduce_impl(forge_runtime* rt, forge_stream* s, forge_slice x, size_t n,
+                         forge_slice out, bool is_max) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    FORGE_TRY(need(x, n, "reduce x"));
+    FORGE_TRY(need(out, 1, "reduce out"));
+    const char* name = is_max ? "forge_reduce_max" : "forge_reduce_sum";
+    long long nn = (long long)n;
+    unsigned g = grid_for(nn, EW_THREADS * 4, 1024);
+    if (g == 1)
+        return launch_args(rt, s, name, dim3(1), dim3(EW_THREADS), 0, (const float*)x.ptr, nn,
+                           out.ptr);
+    float* ws;
+    FORGE_TRY(workspace(rt, s, g, &ws));
+    FORGE_TRY(launch_args(rt, s, name, dim3(g), dim3(EW_THREADS), 0, (const float*)x.ptr, nn, ws));
+    long long gn = g;
+    return launch_args(rt, s, name, dim3(1), dim3(EW_THREADS), 0, (const float*)ws, gn, out.ptr);
+}
+}  // namespace
+
+extern "C" forge_status forge_reduce_sum(forge_runtime* rt, forge_stream* s, forge_slice x,
+                                         size_t n, forge_slice out) {
+    return reduce_impl(rt, s, x, n, out, false);
+}
+
+extern "C" forge_status forge_reduce_max(forge_runtime* rt, forge_stream* s, forge_slice x,
+                                         size_t n, forge_slice out) {
+    return reduce_impl(rt, s, x, n, out, true);
+}
+
+extern "C" forge_status forge_fill_seq(forge_runtime* rt, forge_stream* s, forge_slice x, size_t n,
+                                       int ascending) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    FORGE_TRY(need(x, n, "fill_seq x"));
+    if (n == 0) return FORGE_OK;
+    long long nn = (long long)n;
+    int asc = ascending ? 1 : 0;
+    return launch_args(rt, s, "forge_fill_seq", dim3(grid_for(nn, EW_THREADS, 8192)),
+                       dim3(EW_THREADS), 0, x.ptr, nn, asc);
+}
+
+extern "C" forge_status forge_causal_mask(forge_runtime* rt, forge_stream* s, forge_slice m,
+                                          size_t rows, size_t cols) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    FORGE_TRY(check_rows(rows, cols));
+    FORGE_TRY(need(m, rows * cols, "causal_mask m"));
+    if (rows == 0 || cols == 0) return FORGE_OK;
+    unsigned gx = (unsigned)std::min<size_t>((cols + EW_THREADS - 1) / EW_THREADS, 64);
+    unsigned gy = (unsigned)std::min<size_t>(rows, 65535);
+    int r = (int)rows, c = (int)cols;
+    return launch_args(rt, s, "forge_causal_mask", dim3(gx, gy), dim3(EW_THREADS), 0, m.ptr, r, c);
+}

@@ -1,0 +1,97 @@
+"""C ABI checks that need no GPU: the library loads, exports every entry
+point include/oxforge.h declares, reports errors as status codes, and the
+code object contains every kernel instance the host dispatcher can name."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import oxforge
+from oxforge import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "oxforge.h")
+
+
+def header_functions(path):
+    text = open(path).read()
+    return sorted(set(re.findall(r"^(?:forge_status|const char \*)\s*(forge_\w+)\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = oxforge.load()
+    names = header_functions(HEADER)
+    assert len(names) >= 40
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in oxforge.h but not exported"
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+
+
+def test_status_strings_and_errors_without_device():
+    lib = oxforge.load()
+    assert lib.forge_status_string(0) == b"ok"
+    assert lib.forge_status_string(1) == b"invalid argument"
+    n = ctypes.c_int(-1)
+    assert lib.forge_device_count(ctypes.byref(n)) == 0
+    if n.value == 0:
+        h = ctypes.c_void_p()
+        st = lib.forge_runtime_create(0, None, ctypes.byref(h))
+        assert st == _lib.FORGE_ENODEV
+        assert b"device" in lib.forge_last_error()
+        assert not h.value
+    # null arguments are rejected with EINVAL, never a crash
+    assert lib.forge_device_count(None) == _lib.FORGE_EINVAL
+    assert lib.forge_sync(None, None) == _lib.FORGE_EINVAL
+    assert lib.forge_alloc(None, 4, None) == _lib.FORGE_EINVAL
+    assert lib.forge_gemm_f32(None, None, _lib.NULL_SLICE, _lib.NULL_SLICE, _lib.NULL_SLICE, 1, 1, 1) \
+        == _lib.FORGE_EINVAL
+    assert lib.forge_runtime_destroy(None) == 0
+
+
+def dispatcher_kernel_names():
+    """Every kernel name runtime.cpp can build (mirrors its naming rules)."""
+    names = []
+    for ab in ("nn", "nt", "tn", "tt"):
+        for tag in ("128x128x16_2x2", "128x64x16_2x2", "256x128x16_2x2", "64x64x16_2x2_g"):
+            names.append(f"forge_gemm_{ab}_{tag}_e")
+    for tag in ("128x128x16_2x2", "128x64x16_2x2", "64x64x16_2x2_g"):
+        names.append(f"forge_gemm_nn_{tag}")
+    for op in ("softmax", "layer_norm", "rms_norm", "softmax_bwd", "layer_norm_bwd", "rms_norm_bwd"):
+        for v in (1, 2, 4, 8, 16):
+            names.append(f"forge_row_{op}_v{v}")
+        names.append(f"forge_row_{op}_loop")
+    for op in ("layer_norm_bwd", "rms_norm_bwd"):
+        for v in (1, 2, 4, 8):
+            names.append(f"forge_row_{op}_v{v}_p")
+    for op in ("add", "sub", "mul", "div"):
+        for k in ("binary", "binary_assign", "by_rows"):
+            for s in ("v", "s"):
+                names.append(f"forge_{k}_{op}_{s}")
+    for op in ("scale", "add", "gelu", "gelu_d", "relu", "relu_d", "silu", "silu_d",
+               "exp_shift", "half_sq", "identity"):
+        names += [f"forge_map_{op}_v", f"forge_map_{op}_s"]
+    names += ["forge_fill_v", "forge_fill_s", "forge_fill_seq", "forge_causal_mask",
+              "forge_sum_cols", "forge_sum_rows_v", "forge_sum_rows_s", "forge_reduce_sum",
+              "forge_reduce_max", "forge_transpose", "forge_transpose_g"]
+    return names
+
+
+def test_code_object_contains_dispatched_kernels():
+    assert os.path.exists(_lib.KERNELS_PATH), "code object not built"
+    blob = open(_lib.KERNELS_PATH, "rb").read()
+    assert b"gfx950" in blob
+    missing = [n for n in dispatcher_kernel_names() if (n.encode() + b"\0") not in blob]
+    assert not missing, f"kernels missing from the code object: {missing}"
+
+
+def test_runtime_source_names_only_known_kernels():
+    src = open(os.path.join(ROOT, "oxide-forge_amd", "csrc", "runtime", "runtime.cpp")).read()
+    literals = set(re.findall(r'"(forge_[a-z0-9_]+)"', src))
+    known = set(dispatcher_kernel_names())
+    assert literals <= known, f"unknown kernel literals: {literals - known}"
+
+
+@pytest.mark.parametrize("fn", ["forge_alloc", "forge_softmax_rows", "forge_gemm_ex_f32"])
+def test_signatures_declared(fn):
+    assert fn in _lib.SIGNATURES

@@ -1,0 +1,412 @@
+"""GPU parity of every kernel behind the C ABI against the CPU oracle.
+
+Bars (from the task's north star):
+  - transpose, copy, broadcast, binary ops, fills: bit-exact;
+  - GEMM: max|C - C64| / max|C64| <= 1e-4 and componentwise
+    |C - C64| / (|A| |B|) <= 1e-4 against an f64-accumulated oracle, and
+    bit-exact where fp32 is exact in any summation order (small integers,
+    permutations);
+  - softmax and norms, forward and backward: <= 1e-5 absolute;
+  - maps built on tanhf/expf: <= 2e-6 absolute + relative.
+Full BASELINE sizes are covered directly (row ops, transpose) or through
+sampled rows checked against the f64 oracle (GEMM).
+"""
+import numpy as np
+import pytest
+
+import oxforge
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+TOL_ROW = 1e-5
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def gemm_errors(C, ref64, A64abs_B64abs):
+    err = np.abs(C.astype(np.float64) - ref64)
+    rel_max = float(err.max() / max(np.abs(ref64).max(), 1e-30))
+    comp = float((err / np.maximum(A64abs_B64abs, 1e-30)).max())
+    return rel_max, comp
+
+
+def op_a(A, ta):
+    return A.T if ta else A
+
+
+# ------------------------------------------------------------------- GEMM
+@pytest.mark.parametrize("M,N,K", [(256, 64, 128), (128, 128, 16), (1, 1, 1), (17, 33, 5),
+                                   (100, 257, 63), (64, 64, 64), (384, 256, 512), (130, 70, 1000)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_shapes_vs_oracle(rt, M, N, K, ta, tb):
+    say(f"gemm M={M} N={N} K={K} ta={ta} tb={tb}")
+    A = orc.uniform((K, M) if ta else (M, K), 1 + M)
+    B = orc.uniform((N, K) if tb else (K, N), 2 + N)
+    dA, dB, dC = rt.array(A), rt.array(B), rt.empty((M, N))
+    if ta or tb:
+        rt.gemm_ex(dA, dB, dC, M, N, K, trans_a=ta, trans_b=tb)
+    else:
+        rt.gemm(dA, dB, dC, M, N, K)
+    C = dC.numpy()
+    ref = orc.gemm_f64(A, B, ta, tb)
+    absprod = np.abs(op_a(A, ta)).astype(np.float64) @ np.abs(op_a(B, tb)).astype(np.float64)
+    rel_max, comp = gemm_errors(C, ref, absprod)
+    assert rel_max <= 1e-4 and comp <= 1e-4, (rel_max, comp)
+    for d in (dA, dB, dC):
+        d.recycle()
+
+
+def test_gemm_small_integers_bit_exact(rt):
+    say("gemm small integers 512x384x4096")
+    r = np.random.default_rng(0)
+    M, N, K = 512, 384, 4096
+    A = r.integers(-16, 17, (M, K)).astype(np.float32)
+    B = r.integers(-16, 17, (K, N)).astype(np.float32)
+    dA, dB, dC = rt.array(A), rt.array(B), rt.empty((M, N))
+    rt.gemm(dA, dB, dC, M, N, K)
+    exact = (A.astype(np.int64) @ B.astype(np.int64)).astype(np.float32)
+    assert np.array_equal(dC.numpy(), exact)
+
+
+def test_gemm_permutation_bit_exact(rt):
+    say("gemm permutation 256x256x256")
+    A = orc.uniform((256, 256), 5)
+    perm = np.random.default_rng(1).permutation(256)
+    P = np.zeros((256, 256), np.float32)
+    P[np.arange(256), perm] = 1.0
+    dA, dP, dC = rt.array(A), rt.array(P), rt.empty((256, 256))
+    rt.gemm(dA, dP, dC, 256, 256, 256)
+    assert np.array_equal(dC.numpy(), A @ P)
+
+
+def test_gemm_k_zero_writes_zeros(rt):
+    say("gemm K=0")
+    dA, dB, dC = rt.empty((0,)), rt.empty((0,)), rt.array(np.ones((8, 8), np.float32))
+    rt.gemm(dA, dB, dC, 8, 8, 0)
+    assert np.array_equal(dC.numpy(), np.zeros((8, 8), np.float32))
+
+
+def test_gemm_short_slice_rejected(rt):
+    dA, dB, dC = rt.empty((4, 4)), rt.empty((4, 4)), rt.empty((4, 3))
+    with pytest.raises(oxforge.ForgeError) as e:
+        rt.gemm(dA, dB, dC, 4, 4, 4)
+    assert e.value.status == 1
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 4096), (8192, 1024, 4096)])
+def test_gemm_full_size_sampled_rows(rt, M, N, K):
+    say(f"gemm full size {M}x{N}x{K}")
+    A = orc.uniform((M, K), 3)
+    B = orc.uniform((K, N), 4)
+    dA, dB, dC = rt.array(A), rt.array(B), rt.empty((M, N))
+    rt.gemm(dA, dB, dC, M, N, K)
+    C = dC.numpy()
+    rows = np.sort(np.random.default_rng(M).choice(M, 48, replace=False))
+    ref = orc.gemm_f64(np.ascontiguousarray(A[rows]), B)
+    absprod = np.abs(A[rows]).astype(np.float64) @ np.abs(B).astype(np.float64)
+    rel_max, comp = gemm_errors(C[rows], ref, absprod)
+    assert rel_max <= 1e-4 and comp <= 1e-4, (rel_max, comp)
+    # every tile was written: row sums against A @ (B @ 1) in f64
+    ones = B.astype(np.float64).sum(axis=1)
+    approx = A.astype(np.float64) @ ones
+    assert np.allclose(C.astype(np.float64).sum(axis=1), approx, rtol=1e-3, atol=1e-1)
+    for d in (dA, dB, dC):
+        d.recycle()
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1)])
+@pytest.mark.parametrize("M,N,K", [(256, 128, 64), (50, 70, 33)])
+def test_gemm_epilogue_matches_unfused_bit_exact(rt, M, N, K, ta, tb):
+    """Fused bias + residual + aux + activation + update equals the unfused
+    launch sequence of Linear::affine_on/activate_on/learn_on bit for bit."""
+    say(f"gemm epilogue M={M} N={N} K={K} ta={ta} tb={tb}")
+    A = orc.uniform((K, M) if ta else (M, K), 7)
+    B = orc.uniform((N, K) if tb else (K, N), 8)
+    bias = orc.uniform((N,), 9)
+    res = orc.uniform((M, N), 10)
+    aux = orc.uniform((M, N), 11)
+    W = orc.uniform((M, N), 12)
+    dA, dB = rt.array(A), rt.array(B)
+    dbias, dres, daux = rt.array(bias), rt.array(res), rt.array(aux)
+    for act, mop in [(oxforge.ACT_IDENTITY, None), (oxforge.ACT_GELU, oxforge.MAP_GELU),
+                     (oxforge.ACT_RELU, oxforge.MAP_RELU), (oxforge.ACT_SILU, oxforge.MAP_SILU)]:
+        # unfused: product, then by-rows bias, residual, aux, activation
+        dZ = rt.empty((M, N))
+        rt.gemm_ex(dA, dB, dZ, M, N, K, trans_a=ta, trans_b=tb)
+        rt.map(dZ, oxforge.MAP_SCALE, 0.5)
+        rt.binary_assign_by_rows(dZ, dbias, M, N, oxforge.ADD)
+        rt.binary_assign(dZ, dres, oxforge.ADD)
+        rt.binary_assign(dZ, daux, oxforge.MUL)
+        pre_ref = dZ.numpy()
+        if mop is not None:
+            rt.map(dZ, mop)
+        y_ref = dZ.numpy()
+        # fused
+        dY, dPre = rt.empty((M, N)), rt.empty((M, N))
+        rt.gemm_ex(dA, dB, dY, M, N, K, trans_a=ta, trans_b=tb, alpha=0.5, bias=dbias,
+                   residual=dres, aux_mul=daux, pre_out=dPre, activation=act)
+        assert np.array_equal(dPre.numpy(), pre_ref), act
+        assert np.array_equal(dY.numpy(), y_ref), act
+    # SGD update: W - lr * (A B), as learn_on scales then subtracts
+    lr = 1e-3
+    dW = rt.array(W)
+    rt.gemm_ex(dA, dB, dW, M, N, K, trans_a=ta, trans_b=tb, update=True, update_scale=lr)
+    dG = rt.empty((M, N))
+    rt.gemm_ex(dA, dB, dG, M, N, K, trans_a=ta, trans_b=tb)
+    rt.map(dG, oxforge.MAP_SCALE, lr)
+    dW2 = rt.array(W)
+    rt.binary_assign(dW2, dG, oxforge.SUB)
+    assert np.array_equal(dW.numpy(), dW2.numpy())
+
+
+# -------------------------------------------------------------- transpose
+@pytest.mark.parametrize("rows,cols", [(64, 64), (128, 256), (17, 33), (1, 100), (100, 1),
+                                       (65, 129), (0, 5), (8192, 4096)])
+def test_transpose_bit_exact(rt, rows, cols):
+    say(f"transpose {rows}x{cols}")
+    x = orc.uniform((rows, cols), rows + cols)
+    dx, dt = rt.array(x), rt.empty((cols, rows))
+    rt.transpose(dx, dt, rows, cols)
+    t = dt.numpy()
+    assert np.array_equal(t, x.T)
+    if rows * cols:
+        dback = rt.empty((rows, cols))
+        rt.transpose(dt, dback, cols, rows)
+        assert np.array_equal(dback.numpy(), x)
+
+
+def test_transpose_unaligned_view(rt):
+    say("transpose unaligned view")
+    x = orc.uniform((1 + 40 * 24,), 3)
+    dx = rt.array(x)
+    v = dx.view(1, (40, 24))
+    dt = rt.empty((24, 40))
+    rt.transpose(v, dt, 40, 24)
+    assert np.array_equal(dt.numpy(), x[1:].reshape(40, 24).T)
+
+
+# ---------------------------------------------------------------- row ops
+ROW_SHAPES = [(4096, 1024), (5, 1), (7, 3), (33, 63), (9, 100), (64, 256), (17, 1000),
+              (8, 1025), (16, 2048), (8, 4096), (4, 5000), (3, 9000)]
+
+
+@pytest.mark.parametrize("rows,cols", ROW_SHAPES)
+def test_softmax_fwd_bwd(rt, rows, cols):
+    say(f"softmax {rows}x{cols}")
+    x = orc.normal((rows, cols), 2)
+    g = orc.normal((rows, cols), 3)
+    dx = rt.array(x)
+    rt.softmax_rows(dx, rows, cols)
+    p = dx.numpy()
+    assert np.max(np.abs(p - orc.softmax_rows(x))) <= TOL_ROW
+    dp, dg, dd = rt.array(p), rt.array(g), rt.empty((rows, cols))
+    rt.softmax_rows_bwd(dp, dg, dd, rows, cols)
+    assert np.max(np.abs(dd.numpy() - orc.softmax_rows_backward(p, g))) <= TOL_ROW
+
+
+@pytest.mark.parametrize("rows,cols", ROW_SHAPES)
+@pytest.mark.parametrize("affine", [False, True])
+def test_layer_norm_fwd_bwd(rt, rows, cols, affine):
+    say(f"layer_norm {rows}x{cols} affine={affine}")
+    x = orc.normal((rows, cols), 2)
+    dy = orc.normal((rows, cols), 3)
+    gam = orc.normal((cols,), 4, 1.0, 0.1) if affine else None
+    bet = orc.normal((cols,), 5, 0.0, 0.1) if affine else None
+    dgam = rt.array(gam) if affine else None
+    dbet = rt.array(bet) if affine else None
+    d = rt.array(x)
+    rt.layer_norm(d, rows, cols, gamma=dgam, beta=dbet)
+    assert np.max(np.abs(d.numpy() - orc.layer_norm(x, gam, bet))) <= TOL_ROW
+    dX, dDY, dDX = rt.array(x), rt.array(dy), rt.empty((rows, cols))
+    pg, pb = rt.empty((cols,)), rt.empty((cols,))
+    rt.layer_norm_bwd(dX, dDY, dDX, rows, cols, gamma=dgam, dgamma=pg, dbeta=pb)
+    rdx, rdg, rdb = orc.layer_norm_backward(x, dy, gam, want_params=True)
+    assert np.max(np.abs(dDX.numpy() - rdx)) <= TOL_ROW
+    # column sums over `rows` terms: tolerance scales with sqrt(rows)
+    tol = TOL_ROW * max(1.0, np.sqrt(rows))
+    assert np.max(np.abs(pg.numpy() - rdg)) <= tol
+    assert np.max(np.abs(pb.numpy() - rdb)) <= tol
+
+
+@pytest.mark.parametrize("rows,cols", ROW_SHAPES)
+@pytest.mark.parametrize("affine", [False, True])
+def test_rms_norm_fwd_bwd(rt, rows, cols, affine):
+    say(f"rms_norm {rows}x{cols} affine={affine}")
+    x = orc.normal((rows, cols), 6)
+    dy = orc.normal((rows, cols), 7)
+    gam = orc.normal((cols,), 8, 1.0, 0.1) if affine else None
+    dgam = rt.array(gam) if affine else None
+    d = rt.array(x)
+    rt.rms_norm(d, rows, cols, gamma=dgam)
+    assert np.max(np.abs(d.numpy() - orc.rms_norm(x, gam))) <= TOL_ROW
+    dX, dDY, dDX, pg = rt.array(x), rt.array(dy), rt.empty((rows, cols)), rt.empty((cols,))
+    rt.rms_norm_bwd(dX, dDY, dDX, rows, cols, gamma=dgam, dgamma=pg)
+    rdx, rdg = orc.rms_norm_backward(x, dy, gam, want_params=True)
+    assert np.max(np.abs(dDX.numpy() - rdx)) <= TOL_ROW
+    assert np.max(np.abs(pg.numpy() - rdg)) <= TOL_ROW * max(1.0, np.sqrt(rows))
+
+
+def test_row_ops_reduce_to_reference_at_unit_affine(rt):
+    """gamma = 1, beta = 0 reproduces the reference (no-affine) kernels bit for bit."""
+    say("unit affine")
+    x = orc.normal((64, 1024), 9)
+    ones, zeros = rt.array(np.ones(1024, np.float32)), rt.array(np.zeros(1024, np.float32))
+    a, b = rt.array(x), rt.array(x)
+    rt.layer_norm(a, 64, 1024)
+    rt.layer_norm(b, 64, 1024, gamma=ones, beta=zeros)
+    assert np.array_equal(a.numpy(), b.numpy())
+    a, b = rt.array(x), rt.array(x)
+    rt.rms_norm(a, 64, 1024)
+    rt.rms_norm(b, 64, 1024, gamma=ones)
+    assert np.array_equal(a.numpy(), b.numpy())
+
+
+def test_row_ops_unaligned_views(rt):
+    say("row ops unaligned views")
+    x = orc.normal((1 + 12 * 40,), 10)
+    d = rt.array(x)
+    v = d.view(1, (12, 40))
+    rt.softmax_rows(v, 12, 40)
+    assert np.max(np.abs(v.numpy() - orc.softmax_rows(x[1:].reshape(12, 40)))) <= TOL_ROW
+
+
+# ------------------------------------------------------------ elementwise
+OPS = [(oxforge.ADD, np.add), (oxforge.SUB, np.subtract), (oxforge.MUL, np.multiply),
+       (oxforge.DIV, np.divide)]
+
+
+@pytest.mark.parametrize("op,fn", OPS)
+@pytest.mark.parametrize("n", [4096 * 1024, 1, 7, 1001])
+def test_binary_bit_exact(rt, op, fn, n):
+    say(f"binary op={op} n={n}")
+    a = orc.normal((n,), 1)
+    b = orc.normal((n,), 2)
+    da, db, do = rt.array(a), rt.array(b), rt.empty((n,))
+    rt.binary(da, db, do, op)
+    assert np.array_equal(do.numpy(), fn(a, b))
+    rt.binary_assign(da, db, op)
+    assert np.array_equal(da.numpy(), fn(a, b))
+
+
+def test_binary_unaligned_bit_exact(rt):
+    say("binary unaligned")
+    a = orc.normal((1001,), 1)
+    b = orc.normal((1001,), 2)
+    da, db, do = rt.array(a), rt.array(b), rt.empty((1001,))
+    rt.binary(da.view(1, (1000,)), db.view(1, (1000,)), do.view(1, (1000,)), oxforge.MUL)
+    assert np.array_equal(do.numpy()[1:], a[1:] * b[1:])
+
+
+@pytest.mark.parametrize("op,fn", OPS)
+@pytest.mark.parametrize("rows,cols", [(4096, 1024), (3, 5), (70, 33), (1, 4)])
+def test_by_rows_bit_exact(rt, op, fn, rows, cols):
+    say(f"by_rows op={op} {rows}x{cols}")
+    m = orc.normal((rows, cols), 3)
+    row = orc.normal((cols,), 4)
+    dm, dr = rt.array(m), rt.array(row)
+    rt.binary_assign_by_rows(dm, dr, rows, cols, op)
+    assert np.array_equal(dm.numpy(), fn(m, row[None, :]))
+
+
+EXACT_MAPS = [(oxforge.MAP_SCALE, 0.37), (oxforge.MAP_ADD, -1.25), (oxforge.MAP_HALF_SQ, 0.0),
+              (oxforge.MAP_RELU, 0.0), (oxforge.MAP_RELU_D, 0.0), (oxforge.MAP_IDENTITY, 0.0)]
+TRANS_MAPS = [(oxforge.MAP_GELU, 0.0), (oxforge.MAP_GELU_D, 0.0), (oxforge.MAP_SILU, 0.0),
+              (oxforge.MAP_SILU_D, 0.0), (oxforge.MAP_EXP_SHIFT, 0.75)]
+
+
+@pytest.mark.parametrize("op,p0", EXACT_MAPS + TRANS_MAPS)
+def test_maps(rt, op, p0):
+    say(f"map op={op}")
+    x = orc.normal((4096 * 1024 + 3,), 5, 0.0, 2.0)
+    d = rt.array(x)
+    rt.map(d, op, p0)
+    ref = orc.map_(x, op, p0)
+    if (op, p0) in EXACT_MAPS:
+        assert np.array_equal(d.numpy(), ref)
+    else:
+        y = d.numpy()
+        assert np.all(np.abs(y - ref) <= 2e-6 + 2e-6 * np.abs(ref))
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 1024), (3, 7), (300, 33), (1, 1), (4096, 8192)])
+def test_sum_rows_cols(rt, rows, cols):
+    say(f"sum rows/cols {rows}x{cols}")
+    m = np.random.default_rng(rows).integers(-50, 51, (rows, cols)).astype(np.float32)
+    dm, dr, dc = rt.array(m), rt.empty((rows,)), rt.empty((cols,))
+    rt.sum_rows(dm, dr, rows, cols)
+    rt.sum_cols(dm, dc, rows, cols)
+    # integer inputs: every partial sum is exact, so any order is bit-exact
+    assert np.array_equal(dr.numpy(), m.astype(np.int64).sum(axis=1).astype(np.float32))
+    assert np.array_equal(dc.numpy(), m.astype(np.int64).sum(axis=0).astype(np.float32))
+    mf = orc.normal((rows, cols), 6)
+    dm2 = rt.array(mf)
+    rt.sum_cols(dm2, dc, rows, cols)
+    rt.sum_rows(dm2, dr, rows, cols)
+    assert np.allclose(dc.numpy(), orc.sum_cols(mf), atol=1e-5 * np.sqrt(rows) + 1e-6)
+    assert np.allclose(dr.numpy(), orc.sum_rows(mf), atol=1e-5 * np.sqrt(cols) + 1e-6)
+
+
+@pytest.mark.parametrize("n", [1, 1000, 4096 * 1024, 10_000_019])
+def test_reduce_sum_max(rt, n):
+    say(f"reduce n={n}")
+    x = np.random.default_rng(n).integers(-1000, 1001, n).astype(np.float32)
+    dx, out = rt.array(x), rt.empty((1,))
+    rt.reduce_sum(dx, out)
+    assert out.numpy()[0] == float(x.astype(np.int64).sum())
+    rt.reduce_max(dx, out)
+    assert out.numpy()[0] == x.max()
+
+
+def test_fills_and_causal_mask(rt):
+    say("fills")
+    d = rt.empty((1000,))
+    rt.fill_seq(d, True)
+    assert np.array_equal(d.numpy(), orc.fill_seq(1000, True))
+    rt.fill_seq(d, False)
+    assert np.array_equal(d.numpy(), orc.fill_seq(1000, False))
+    rt.fill(d, 2.5)
+    assert np.all(d.numpy() == 2.5)
+    z = rt.zeros((77,))
+    assert np.all(z.numpy() == 0)
+    m = orc.normal((300, 257), 1)
+    dm = rt.array(m)
+    rt.causal_mask(dm, 300, 257)
+    assert np.array_equal(dm.numpy(), orc.causal_mask(m))
+
+
+# ---------------------------------------------------- runtime: pool, streams
+def test_pool_reuses_exact_sizes(rt):
+    a = rt.empty((1234,))
+    p = a.ptr
+    a.recycle()
+    assert rt.pool_count(1234) >= 1
+    b = rt.empty((1234,))
+    assert b.ptr == p
+    rt.reserve(4321, 3)
+    assert rt.pool_count(4321) == 3
+
+
+def test_streams_fork_join(rt):
+    """Three forked streams compute independent GEMMs; the joined primary
+    stream then consumes all three results (QkvProjection::project order)."""
+    say("streams fork/join")
+    streams = rt.streams_create(3)
+    A = orc.uniform((256, 512), 1)
+    Ws = [orc.uniform((512, 256), 10 + i) for i in range(3)]
+    dA = rt.array(A)
+    dWs = [rt.array(w) for w in Ws]
+    outs = [rt.empty((256, 256)) for _ in range(3)]
+    for _ in range(3):
+        rt.streams_fork(streams)
+        for s, w, o in zip(streams, dWs, outs):
+            rt.gemm(dA, w, o, 256, 256, 512, stream=s)
+        rt.streams_join(streams)
+        total = rt.empty((256, 256))
+        rt.binary(outs[0], outs[1], total, oxforge.ADD)
+        rt.binary_assign(total, outs[2], oxforge.ADD)
+        got = total.numpy()
+        ref = [orc.gemm_f64(A, w) for w in Ws]
+        assert np.max(np.abs(got - (ref[0] + ref[1] + ref[2]))) <= 1e-3
