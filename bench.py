@@ -149,6 +149,71 @@ def secondary(rt, orc, steps, warmup, extended):
     return out
 
 
+def transformer_params(orc, S, H, F, O, seed, affine):
+    p = {"WQ": orc.xavier(H, H, seed), "WK": orc.xavier(H, H, seed + 1),
+         "WV": orc.xavier(H, H, seed + 2), "POS": orc.xavier(S, H, seed + 3),
+         "W1": orc.xavier(H, F, seed + 4), "W2": orc.xavier(F, H, seed + 5),
+         "WO": orc.xavier(H, O, seed + 6)}
+    import numpy as np
+
+    for k, n in (("BQ", H), ("BK", H), ("BV", H), ("B1", F), ("B2", H), ("BO", O)):
+        p[k] = np.zeros(n, np.float32)
+    if affine:
+        p["G1"] = orc.normal((H,), seed + 20, 1.0, 0.1)
+        p["G2"] = orc.normal((H,), seed + 21, 1.0, 0.1)
+        p["BE1"] = orc.normal((H,), seed + 22, 0.0, 0.1)
+        p["BE2"] = orc.normal((H,), seed + 23, 0.0, 0.1)
+    return p
+
+
+def transformers(rt, orc, steps, warmup):
+    """C4 inference forward and C5 training step, tokens/s."""
+    from oxforge import net
+
+    out = {}
+    # C4: seq 2048, hidden 1024, FFN 4096 GELU, out 1024, RMSNorm, inference.
+    S, H, F, O = 2048, 1024, 4096, 1024
+    log("transformer C4 inference")
+    T = net.Transformer(rt, transformer_params(orc, S, H, F, O, 4, False), S, H, F, O, net.RMS,
+                        net.ENCODER_INFERENCE, qkv_streams=True)
+    X = rt.array(orc.normal((S, H), 4))
+    Y = rt.empty((S, O))
+    ms = time_launches(rt, lambda i: T.forward(X, Y), steps, warmup)
+    flops = 2.0 * S * H * H * 3 + 2.0 * S * S * H * 2 + 2.0 * S * H * F * 2 + 2.0 * S * H * O
+    out["transformer_c4_inference"] = {
+        "tokens_per_s": round(S / (ms * 1e-3), 1), "ms_per_forward": round(ms, 4),
+        "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+        "frac_mfma_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4)}
+    T.close()
+    X.recycle()
+    Y.recycle()
+    # C5: seq 4096, hidden 2048, FFN 8192 GELU, out 2048, LayerNorm, training.
+    S, H, F, O = 4096, 2048, 8192, 2048
+    log("transformer C5 training step")
+    T = net.Transformer(rt, transformer_params(orc, S, H, F, O, 5, True), S, H, F, O, net.LAYER,
+                        net.ENCODER_TRAINING)
+    X = rt.array(orc.normal((S, H), 5))
+    dY = rt.array(orc.normal((S, O), 6))
+    Y = rt.empty((S, O))
+    dX = rt.empty((S, H))
+
+    def step(i):
+        T.forward(X, Y)
+        T.backward(dY, 1e-3, dX)
+
+    ms = time_launches(rt, step, max(3, steps // 2), 2)
+    fwd = 2.0 * S * H * H * 3 + 2.0 * S * S * H * 2 + 2.0 * S * H * F * 2 + 2.0 * S * H * O
+    flops = 3 * fwd
+    out["transformer_c5_training"] = {
+        "tokens_per_s": round(S / (ms * 1e-3), 1), "ms_per_step": round(ms, 3),
+        "tflops_algorithmic": round(flops / (ms * 1e-3) / 1e12, 2),
+        "frac_mfma_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4)}
+    T.close()
+    for d in (X, dY, Y, dX):
+        d.recycle()
+    return out
+
+
 def sweep(rt, orc, steps, warmup):
     """Times every plain GEMM tile instance on the two C3 shapes."""
     import oxforge
@@ -185,16 +250,22 @@ def cpu_baseline(orc, M, N, K):
     M rows; scaled to TFLOP/s of the same workload."""
     threads = min(16, os.cpu_count() or 1)
     orc.set_threads(threads)
-    rows = 256
+    rows = 512
     A = orc.uniform((rows, K), 3)
     B = orc.uniform((K, N), 4)
+    # Repeat the 512-row block until about 10 s of CPU work has been timed.
     t0 = time.perf_counter()
-    orc.gemm(A, B)
-    dt = time.perf_counter() - t0
-    return {"value": round(2.0 * rows * N * K / dt / 1e12, 5), "unit": "TFLOP/s",
+    reps = 0
+    while True:
+        orc.gemm(A, B)
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= 10.0 or reps * rows >= 8 * M:
+            break
+    return {"value": round(2.0 * reps * rows * N * K / dt / 1e12, 5), "unit": "TFLOP/s",
             "cores": threads, "kind": "port",
-            "sample": f"{rows} of {M} rows of the {M}x{N}x{K} GEMM (oracle, f64 accumulate), "
-                      f"{dt:.2f} s"}
+            "sample": f"{reps} x {rows} rows of the {M}x{N}x{K} GEMM (oracle, f64 accumulate, "
+                      f"{threads} threads), {dt:.1f} s"}
 
 
 def main() -> int:
@@ -246,6 +317,7 @@ def main() -> int:
     }
     if not args.no_secondary:
         line["secondary"] = secondary(rt, orc, args.steps, args.warmup, args.extended)
+        line["secondary"].update(transformers(rt, orc, args.steps, args.warmup))
     if args.sweep:
         line["sweep"] = sweep(rt, orc, args.steps, args.warmup)
     if not args.no_cpu:

@@ -190,7 +190,7 @@ forge_status forge_gemm_f32(forge_runtime *rt, forge_stream *stream,
  *   Z = alpha * op(A) op(B)
  *   if bias:     Z = Z + bias[col]           (by-rows add, rows.rs:8-42)
  *   if residual: Z = Z + residual            (binary_assign, matrix.rs:38)
- *   if aux_mul:  Z = Z * aux_mul             (gradient * act'(z), linear.rs:264)
+ *   if aux_mul:  Z = Z * aux_mul, or Z * act'(aux_mul) (linear.rs:254-265)
  *   if pre_out:  pre_out = Z
  *   Y = act(Z)
  *   if update:   C = C - update_scale * Y    (SGD, linear.rs:383-384)
@@ -207,6 +207,9 @@ typedef struct forge_gemm_epilogue {
     int activation;        /* forge_activation                            */
     int update;            /* 0: C = Y; 1: C = C - update_scale * Y        */
     float update_scale;    /* learning rate for update == 1                */
+    int aux_activation;    /* 0: Z = Z * aux_mul; a forge_activation A:
+                              Z = Z * A'(aux_mul), the derivative step of
+                              Linear::backward (linear.rs:254-265)         */
 } forge_gemm_epilogue;
 
 forge_status forge_gemm_ex_f32(forge_runtime *rt, forge_stream *stream,
@@ -239,6 +242,15 @@ forge_status forge_softmax_rows(forge_runtime *rt, forge_stream *stream,
 forge_status forge_softmax_rows_bwd(forge_runtime *rt, forge_stream *stream,
                                     forge_slice p, forge_slice g,
                                     forge_slice dx, size_t rows, size_t cols);
+
+/* softmax_rows_backward followed by Matrix::scale, fused: the score
+ * gradient of attention backward (attention.rs:584-586),
+ * dx = (p * (g - sum(p * g))) * scale, two roundings as in the reference. */
+forge_status forge_softmax_rows_bwd_scaled(forge_runtime *rt,
+                                           forge_stream *stream, forge_slice p,
+                                           forge_slice g, forge_slice dx,
+                                           size_t rows, size_t cols,
+                                           float scale);
 
 /* Matrix::layer_norm (norm.rs:26-48 -> row.rs:115-177), in place.
  * gamma/beta ({NULL,0} = reference path) are the affine extension. */
@@ -283,6 +295,13 @@ forge_status forge_binary_assign_by_rows(forge_runtime *rt,
 forge_status forge_map(forge_runtime *rt, forge_stream *stream, forge_slice x,
                        size_t n, forge_map_op op, float p0);
 
+/* Linear::backward's derivative step (linear.rs:254-265: clone, map
+ * activation.derivative, multiply) in one pass: g = dy * act'(z). */
+forge_status forge_activation_backward(forge_runtime *rt, forge_stream *stream,
+                                       forge_slice dy, forge_slice z,
+                                       forge_slice g, size_t n,
+                                       forge_activation activation);
+
 /* matrix_sum_rows (rows.rs:45-88 -> row.rs:16-53): out[r] = sum_j M[r,j]. */
 forge_status forge_sum_rows(forge_runtime *rt, forge_stream *stream,
                             forge_slice m, forge_slice out, size_t rows,
@@ -303,6 +322,16 @@ forge_status forge_reduce_max(forge_runtime *rt, forge_stream *stream,
 /* slice_set_seq (elementwise.rs:23-34): i (ascending) or n - i. */
 forge_status forge_fill_seq(forge_runtime *rt, forge_stream *stream,
                             forge_slice x, size_t n, int ascending);
+/* slice_set_random (matrix.rs:283-289 -> elementwise.rs:36-43 with the
+ * hash of common.rs:3-9): x[i] = hash(seed + i) / u32::MAX.  Bit-exact. */
+forge_status forge_fill_random(forge_runtime *rt, forge_stream *stream,
+                               forge_slice x, size_t n, uint32_t seed);
+/* Vector::equals (vector.rs:117-136 -> reduction.rs:132-174): out[0] = the
+ * number of positions i < n with l[i] != r[i] (0 means equal).  Every
+ * element is compared (the reference kernel reports block 0 only). */
+forge_status forge_compare(forge_runtime *rt, forge_stream *stream,
+                           forge_slice l, forge_slice r, size_t n,
+                           forge_slice out);
 /* Matrix::causal_mask (matrix.rs:79-92 -> row.rs:5-14). */
 forge_status forge_causal_mask(forge_runtime *rt, forge_stream *stream,
                                forge_slice m, size_t rows, size_t cols);

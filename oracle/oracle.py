@@ -53,6 +53,8 @@ def lib():
             "orc_reduce_max": ([_F, c_size_t], c_float),
             "orc_fill_seq": ([_F, c_size_t, c_int], None),
             "orc_causal_mask": ([_F, c_size_t, c_size_t], None),
+            "orc_activation_backward": ([_F, _F, _F, c_size_t, c_int], None),
+            "orc_fill_random": ([_F, c_size_t, ctypes.c_uint32], None),
             "orc_fill_uniform": ([_F, c_size_t, c_uint64, c_float, c_float], None),
             "orc_fill_normal": ([_F, c_size_t, c_uint64, c_float, c_float], None),
         }
@@ -227,6 +229,19 @@ def reduce_max(x) -> float:
 def fill_seq(n, ascending=True) -> np.ndarray:
     out = np.empty(n, np.float32)
     lib().orc_fill_seq(_p(out), n, int(ascending))
+    return out
+
+
+def activation_backward(dy, z, derivative_op) -> np.ndarray:
+    dy, z = _f32(dy), _f32(z)
+    g = np.empty_like(dy)
+    lib().orc_activation_backward(_p(dy), _p(z), _p(g), dy.size, derivative_op)
+    return g
+
+
+def fill_random(n, seed) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().orc_fill_random(_p(out), n, seed)
     return out
 
 

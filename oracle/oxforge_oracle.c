@@ -408,6 +408,12 @@ void orc_map(float *x, size_t n, int op, float p0) {
     for (size_t i = 0; i < n; i++) x[i] = map_one(x[i], op, p0);
 }
 
+void orc_activation_backward(const float *dy, const float *z, float *g,
+                             size_t n, int derivative_op) {
+    /* derivative = act'(z) rounded to f32, then gradient * derivative. */
+    for (size_t i = 0; i < n; i++) g[i] = dy[i] * map_one(z[i], derivative_op, 0.f);
+}
+
 /* ------------------------------------------------------------- reductions */
 
 void orc_sum_rows(const float *m, float *out, size_t rows, size_t cols) {
@@ -459,6 +465,20 @@ void orc_causal_mask(float *m, size_t rows, size_t cols) {
     /* row.rs:5-14: M[r, c] = -inf for c > r. */
     for (size_t r = 0; r < rows; r++)
         for (size_t c = r + 1; c < cols; c++) m[r * cols + c] = -INFINITY;
+}
+
+/* common.rs:3-9: x += x << 13; x -= x >> 17; x *= x << 5 (wrapping u32). */
+static uint32_t ref_hash(uint32_t x) {
+    x += x << 13;
+    x -= x >> 17;
+    x *= x << 5;
+    return x;
+}
+
+void orc_fill_random(float *x, size_t n, uint32_t seed) {
+    /* elementwise.rs:40-41: (rand as f32) / (u32::MAX as f32). */
+    for (size_t i = 0; i < n; i++)
+        x[i] = (float)ref_hash(seed + (uint32_t)i) / (float)UINT32_MAX;
 }
 
 /* --------------------------------------------------------- synthetic data */

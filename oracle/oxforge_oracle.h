@@ -107,6 +107,14 @@ void orc_sum_cols(const float *m, float *out, size_t rows, size_t cols);
 float orc_reduce_sum(const float *x, size_t n);
 float orc_reduce_max(const float *x, size_t n);
 
+/* g = dy * act'(z): Linear::backward's derivative map and multiply
+ * (linear.rs:254-265); act is an ORC_MAP_*_D derivative op. */
+void orc_activation_backward(const float *dy, const float *z, float *g,
+                             size_t n, int derivative_op);
+
+/* slice_set_random (elementwise.rs:36-43) with the hash of common.rs:3-9. */
+void orc_fill_random(float *x, size_t n, uint32_t seed);
+
 /* Fills (elementwise.rs:23-34, row.rs:5-14). */
 void orc_fill_seq(float *x, size_t n, int ascending);
 void orc_causal_mask(float *m, size_t rows, size_t cols);

@@ -105,4 +105,13 @@ __device__ __forceinline__ float activate(int act, float x) {
     }
 }
 
+__device__ __forceinline__ float activate_derivative(int act, float x) {
+    switch (act) {
+    case ACT_GELU: return gelu_derivative(x);
+    case ACT_RELU: return relu_derivative(x);
+    case ACT_SILU: return silu_derivative(x);
+    default: return 1.0f;
+    }
+}
+
 }  // namespace forge

@@ -162,6 +162,70 @@ __device__ __forceinline__ void fill_seq_body(float* x, long long n, int ascendi
                          : (float)(unsigned long long)(n - i);
 }
 
+// slice_set_random (elementwise.rs:36-43) with the hash of common.rs:3-9:
+// x += x << 13; x -= x >> 17; x *= x << 5 (wrapping u32), value / u32::MAX.
+__device__ __forceinline__ uint32_t forge_hash(uint32_t x) {
+    x += x << 13;
+    x -= x >> 17;
+    x *= x << 5;
+    return x;
+}
+
+__device__ __forceinline__ void fill_random_body(float* x, long long n, uint32_t seed) {
+    const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    for (long long i = tid; i < n; i += stride)
+        x[i] = (float)forge_hash(seed + (uint32_t)i) / (float)4294967295u;
+}
+
+// g = dy * act'(z): Linear::backward's derivative map and multiply
+// (linear.rs:254-265) in one pass; same two roundings.
+template <bool VEC>
+__device__ __forceinline__ void act_backward_body(const float* __restrict__ dy,
+                                                  const float* __restrict__ z,
+                                                  float* __restrict__ g, long long n, int act) {
+    const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    if constexpr (VEC) {
+        const long long n4 = n / 4;
+        for (long long i = tid; i < n4; i += stride) {
+            const float4 a = reinterpret_cast<const float4*>(dy)[i];
+            const float4 b = reinterpret_cast<const float4*>(z)[i];
+            float4 c;
+            c.x = a.x * activate_derivative(act, b.x);
+            c.y = a.y * activate_derivative(act, b.y);
+            c.z = a.z * activate_derivative(act, b.z);
+            c.w = a.w * activate_derivative(act, b.w);
+            reinterpret_cast<float4*>(g)[i] = c;
+        }
+        for (long long i = n4 * 4 + tid; i < n; i += stride)
+            g[i] = dy[i] * activate_derivative(act, z[i]);
+    } else {
+        for (long long i = tid; i < n; i += stride) g[i] = dy[i] * activate_derivative(act, z[i]);
+    }
+}
+
+// Per-workgroup count of positions where l != r (compare_vectors,
+// reduction.rs:132-174, but over every element; the reference keeps only
+// block 0's verdict).  Counts are exact in f32 up to 2^24 per workgroup.
+__device__ __forceinline__ void count_neq_body(const float* __restrict__ l,
+                                               const float* __restrict__ r, long long n,
+                                               float* __restrict__ out) {
+    __shared__ float part[EW_THREADS / 64];
+    const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    float acc = 0.0f;
+    for (long long i = tid; i < n; i += stride) acc += (l[i] == r[i]) ? 0.0f : 1.0f;
+    acc = wave_sum(acc);
+    if (lane_id() == 0) part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float t = part[0];
+        for (int w = 1; w < (int)(blockDim.x >> 6); w++) t += part[w];
+        out[blockIdx.x] = t;
+    }
+}
+
 // row.rs:5-14: M[r, c] = -inf for c > r.
 __device__ __forceinline__ void causal_mask_body(float* m, int rows, int cols) {
     for (int r = blockIdx.y; r < rows; r += gridDim.y)

@@ -40,9 +40,10 @@ struct GemmArgs {
     float alpha;
     const float* bias;      // [N] or null
     const float* residual;  // [M, ldc] or null
-    const float* aux;       // [M, ldc] or null: Z *= aux
+    const float* aux;       // [M, ldc] or null: Z *= aux (or act'(aux))
     float* pre_out;         // [M, ldc] or null: stores Z before activation
     int act;
+    int aux_act;            // 0: Z *= aux; ACT_*: Z *= derivative of that act at aux
     int update;             // 0: C = act(Z); 1: C = C - update_scale * act(Z)
     float update_scale;
 };
@@ -255,7 +256,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
                     if (p.alpha != 1.0f) z = p.alpha * z;
                     if (p.bias) z = z + p.bias[col];
                     if (p.residual) z = z + p.residual[idx];
-                    if (p.aux) z = z * p.aux[idx];
+                    if (p.aux) {
+                        const float m = p.aux_act ? activate_derivative(p.aux_act, p.aux[idx])
+                                                  : p.aux[idx];
+                        z = z * m;
+                    }
                     if (p.pre_out) p.pre_out[idx] = z;
                     const float y = activate(p.act, z);
                     if (p.update) p.C[idx] = p.C[idx] - p.update_scale * y;

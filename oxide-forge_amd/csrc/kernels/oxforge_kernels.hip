@@ -113,6 +113,22 @@ FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_fill_s(float* x, long long
 FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_fill_seq(float* x, long long n, int asc) {
     fill_seq_body(x, n, asc);
 }
+FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_fill_random(float* x, long long n,
+                                                                  unsigned seed) {
+    fill_random_body(x, n, seed);
+}
+FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_act_backward_v(const float* dy, const float* z,
+                                                                     float* g, long long n, int act) {
+    act_backward_body<true>(dy, z, g, n, act);
+}
+FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_act_backward_s(const float* dy, const float* z,
+                                                                     float* g, long long n, int act) {
+    act_backward_body<false>(dy, z, g, n, act);
+}
+FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_count_neq(const float* l, const float* r,
+                                                                long long n, float* out) {
+    count_neq_body(l, r, n, out);
+}
 FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_causal_mask(float* m, int rows, int cols) {
     causal_mask_body(m, rows, cols);
 }

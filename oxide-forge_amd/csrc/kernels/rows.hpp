@@ -32,6 +32,7 @@ struct RowArgs {
     float* pbeta;        // [gridDim.x, cols] partial dbeta or null
     int rows, cols;
     float eps;
+    float scale;         // softmax backward: dx *= scale (1 = reference kernel)
 };
 
 enum RowOp {
@@ -231,6 +232,8 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                 float4 o;
                 F4_APPLY(o, v[i], v[i].x * (g[i].x - s), v[i].y * (g[i].y - s),
                          v[i].z * (g[i].z - s), v[i].w * (g[i].w - s));
+                if (a.scale != 1.0f)
+                    F4_APPLY(o, o, o.x * a.scale, o.y * a.scale, o.z * a.scale, o.w * a.scale);
                 *reinterpret_cast<float4*>(a.y + base + (i * 64 + lane) * 4) = o;
             }
         } else if constexpr (OP == ROW_RMS_NORM_BWD) {
@@ -382,7 +385,10 @@ __device__ __forceinline__ void row_kernel_loop(const RowArgs& a) {
             float s = 0.0f;
             for (int c = lane; c < cols; c += 64) s += x[c] * dy[c];
             s = wave_sum(s);
-            for (int c = lane; c < cols; c += 64) y[c] = x[c] * (dy[c] - s);
+            for (int c = lane; c < cols; c += 64) {
+                const float d = x[c] * (dy[c] - s);
+                y[c] = a.scale != 1.0f ? d * a.scale : d;
+            }
         } else if constexpr (OP == ROW_RMS_NORM_BWD) {
             float q = 0.0f, d = 0.0f;
             for (int c = lane; c < cols; c += 64) {

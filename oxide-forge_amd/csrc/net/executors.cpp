@@ -1,0 +1,801 @@
+// executors.cpp -- Linear, MLP, Attention and the single-head Post-Norm
+// transformer blocks (reference src/net/linear.rs, mlp.rs,
+// transformer/{attention,inference,encoder,decoder}.rs).
+//
+// The arithmetic order of every fused step matches the reference's separate
+// launches (each fused operation is one rounded f32 op in the same order, and
+// a+b == b+a exactly), so the fused executors compute what the reference's
+// launch sequence computes on the same GEMM products.
+#include <cmath>
+
+#include "oxforge_net.hpp"
+
+namespace oxforge {
+
+static void require(bool cond, const char* what) {
+    if (!cond) throw Error(FORGE_EINVAL, std::string("assertion failed: ") + what);
+}
+
+static forge_map_op forward_map(Activation a) {
+    switch (a) {
+    case Activation::Gelu: return FORGE_MAP_GELU;
+    case Activation::Relu: return FORGE_MAP_RELU;
+    case Activation::Silu: return FORGE_MAP_SILU;
+    default: return FORGE_MAP_IDENTITY;
+    }
+}
+
+// SGD on a parameter vector, as Linear::learn updates a bias
+// (linear.rs:385-390): scaled = clone(grad) * lr; param -= scaled.
+static void sgd_vector(CudaRuntime& rt, Vector& param, const Vector& grad, float lr) {
+    Vector scaled = rt.clone_vector(grad);
+    scaled.scale(lr, rt);
+    param.binary_assign(scaled, BinaryOp::Sub, rt);
+}
+
+// Norm backward for a training step: computes dgamma/dbeta whenever the norm
+// has parameters (to update them) or gradients are requested, applies SGD to
+// the norm's own gamma/beta, and hands the gradients to the caller.
+static Matrix norm_backward_step(Normalization& norm, const Matrix& input,
+                                 const Matrix& output_gradient, float lr, CudaRuntime& rt,
+                                 bool want, std::optional<Vector>* out_gamma,
+                                 std::optional<Vector>* out_beta) {
+    const size_t cols = input.cols();
+    std::optional<Vector> dg, db;
+    if (norm.gamma || want) dg = Vector(rt.get_uninit_buffer(cols));
+    if (norm.kind == NormType::Layer && (norm.beta || want)) db = Vector(rt.get_uninit_buffer(cols));
+    Matrix dx = norm.backward(input, output_gradient, rt, dg ? &*dg : nullptr, db ? &*db : nullptr);
+    if (norm.gamma) sgd_vector(rt, *norm.gamma, *dg, lr);
+    if (norm.beta) sgd_vector(rt, *norm.beta, *db, lr);
+    if (want) {
+        *out_gamma = std::move(dg);
+        *out_beta = std::move(db);
+    }
+    return dx;
+}
+
+// ================================================================== Linear
+
+Linear::Linear(Matrix weights, std::optional<Vector> bias, Activation activation)
+    : weights_(std::move(weights)), bias_(std::move(bias)), activation_(activation) {
+    if (bias_) require(bias_->len() == weights_.cols(), "bias.len() == weights.cols()");
+}
+
+Matrix Linear::forward_keep(const Matrix& input, const Matrix* residual, Matrix* pre_activation,
+                            CudaRuntime& rt, const CudaStream* stream) {
+    // linear.rs:116-132 -> affine_on (185-206) + activate_on (225-230).
+    require(input.cols() == weights_.rows(), "input.cols() == weights.rows()");
+    Matrix out = rt.new_uninit_matrix(input.rows(), weights_.cols());
+    rt.stream_join_primary(stream);
+    forge_gemm_epilogue ep = plain_epilogue();
+    if (bias_) ep.bias = bias_->slice();
+    if (residual) {
+        require(residual->rows() == out.rows() && residual->cols() == out.cols(),
+                "residual shape");
+        ep.residual = residual->slice();
+    }
+    if (pre_activation) {
+        require(pre_activation->rows() == out.rows() && pre_activation->cols() == out.cols(),
+                "pre-activation shape");
+        ep.pre_out = pre_activation->slice();
+    }
+    ep.activation = (int)activation_;
+    rt.gemm_ex(stream, false, false, input, weights_, out.slice(), input.rows(), weights_.cols(),
+               input.cols(), ep);
+    return out;
+}
+
+Matrix Linear::forward(const Matrix& input, const Matrix* residual, CudaRuntime& rt,
+                       const CudaStream* stream) {
+    return forward_keep(input, residual, nullptr, rt, stream);
+}
+
+Matrix Linear::affine(const Matrix& input, const Matrix* residual, CudaRuntime& rt,
+                      const CudaStream* stream) {
+    // linear.rs:157-206: product, bias by rows, residual; no activation.
+    require(input.cols() == weights_.rows(), "input.cols() == weights.rows()");
+    Matrix out = rt.new_uninit_matrix(input.rows(), weights_.cols());
+    rt.stream_join_primary(stream);
+    forge_gemm_epilogue ep = plain_epilogue();
+    if (bias_) ep.bias = bias_->slice();
+    if (residual) {
+        require(residual->rows() == out.rows() && residual->cols() == out.cols(),
+                "residual shape");
+        ep.residual = residual->slice();
+    }
+    rt.gemm_ex(stream, false, false, input, weights_, out.slice(), input.rows(), weights_.cols(),
+               input.cols(), ep);
+    return out;
+}
+
+void Linear::activate(Matrix& output, CudaRuntime& rt, const CudaStream* stream) {
+    // linear.rs:208-230.
+    if (activation_ != Activation::Identity) output.map(forward_map(activation_), 0.0f, rt, stream);
+}
+
+std::pair<Matrix, std::optional<Vector>> Linear::backward(const Matrix* pre_activation,
+                                                          const Matrix& output_gradient,
+                                                          CudaRuntime& rt,
+                                                          const CudaStream* stream) {
+    // linear.rs:232-306: gradient = dY * act'(pre); bias gradient = column
+    // sums (the reference's transpose + sum_rows).
+    Matrix gradient = rt.new_uninit_matrix(output_gradient.rows(), output_gradient.cols());
+    rt.stream_join_primary(stream);
+    if (activation_ != Activation::Identity) {
+        require(pre_activation != nullptr, "activation backward requires pre-activation");
+        require(pre_activation->rows() == output_gradient.rows() &&
+                    pre_activation->cols() == output_gradient.cols(),
+                "pre-activation shape");
+        check(forge_activation_backward(rt.raw(), stream_raw(stream), output_gradient.slice(),
+                                        pre_activation->slice(), gradient.slice(), gradient.len(),
+                                        (forge_activation)activation_),
+              "Linear::backward");
+    } else {
+        check(forge_memcpy_d2d(rt.raw(), stream_raw(stream), gradient.slice(), output_gradient.slice(),
+                               gradient.len()),
+              "Linear::backward");
+    }
+    std::optional<Vector> bias_gradient;
+    if (bias_) bias_gradient = rt.matrix_sum_cols(gradient, stream);
+    return {std::move(gradient), std::move(bias_gradient)};
+}
+
+Vector Linear::loss_rows(const Matrix& output, const Matrix& target, CudaRuntime& rt,
+                         const CudaStream* stream) {
+    // linear.rs:312-348: mean over columns of 0.5 * (o - t)^2 per row.
+    Matrix loss = rt.matrix_binary_on(stream, output, target, BinaryOp::Sub);
+    loss.map(FORGE_MAP_HALF_SQ, 0.0f, rt, stream);
+    float cols = (float)loss.cols();
+    Vector row_loss = rt.matrix_sum_rows_on(loss, stream);
+    row_loss.scale_on(1.0f / cols, rt, stream);
+    return row_loss;
+}
+
+void Linear::learn_keep(const Matrix& input, const Matrix& gradient, const Vector* bias_gradient,
+                        float learning_rate, Matrix* weight_gradient, CudaRuntime& rt,
+                        const CudaStream* stream) {
+    // linear.rs:373-415: W -= lr * (X^T G) as one TN GEMM whose epilogue
+    // scales by lr and subtracts from W; b -= lr * db.
+    require(input.rows() == gradient.rows(), "input.rows() == gradient.rows()");
+    require(input.cols() == weights_.rows() && gradient.cols() == weights_.cols(),
+            "learn shapes");
+    rt.stream_join_primary(stream);
+    forge_gemm_epilogue ep = plain_epilogue();
+    ep.update = 1;
+    ep.update_scale = learning_rate;
+    if (weight_gradient) {
+        require(weight_gradient->rows() == weights_.rows() &&
+                    weight_gradient->cols() == weights_.cols(),
+                "weight gradient shape");
+        ep.pre_out = weight_gradient->slice();
+    }
+    rt.gemm_ex(stream, true, false, input, gradient, weights_.slice(), weights_.rows(),
+               weights_.cols(), input.rows(), ep);
+    if (bias_) {
+        require(bias_gradient != nullptr, "missing bias gradient for biased Linear");
+        Vector scaled = rt.clone_vector_on(*bias_gradient, stream);
+        scaled.scale_on(learning_rate, rt, stream);
+        bias_->binary_assign_on(scaled, BinaryOp::Sub, rt, stream);
+    }
+}
+
+void Linear::learn(const Matrix& input, const Matrix& gradient, const Vector* bias_gradient,
+                   float learning_rate, CudaRuntime& rt, const CudaStream* stream) {
+    learn_keep(input, gradient, bias_gradient, learning_rate, nullptr, rt, stream);
+}
+
+Matrix Linear::input_gradient(const Matrix& gradient, CudaRuntime& rt, const CudaStream* stream) {
+    // linear.rs:417-444: G * W^T as an NT GEMM (no materialised W^T).
+    require(gradient.cols() == weights_.cols(), "gradient.cols() == weights.cols()");
+    Matrix out = rt.new_uninit_matrix(gradient.rows(), weights_.rows());
+    rt.stream_join_primary(stream);
+    rt.gemm_ex(stream, false, true, gradient, weights_, out.slice(), gradient.rows(),
+               weights_.rows(), weights_.cols(), plain_epilogue());
+    return out;
+}
+
+void Linear::input_gradient_accumulate(const Matrix& gradient, Matrix& accumulate,
+                                       CudaRuntime& rt, const CudaStream* stream) {
+    require(gradient.cols() == weights_.cols(), "gradient.cols() == weights.cols()");
+    require(accumulate.rows() == gradient.rows() && accumulate.cols() == weights_.rows(),
+            "accumulator shape");
+    rt.stream_join_primary(stream);
+    forge_gemm_epilogue ep = plain_epilogue();
+    ep.residual = accumulate.slice();
+    rt.gemm_ex(stream, false, true, gradient, weights_, accumulate.slice(), gradient.rows(),
+               weights_.rows(), weights_.cols(), ep);
+}
+
+std::pair<Matrix, std::optional<Vector>> Linear::backward_with_res(
+    const Matrix& pre_activation, const Matrix& output_gradient, const Matrix& residual_gradient,
+    CudaRuntime& rt, const CudaStream* stream) {
+    // linear.rs:446-532: (dY + dR) * act'(pre), bias gradient.
+    require(pre_activation.rows() == output_gradient.rows() &&
+                pre_activation.cols() == output_gradient.cols(),
+            "pre-activation shape");
+    require(output_gradient.rows() == residual_gradient.rows() &&
+                output_gradient.cols() == residual_gradient.cols(),
+            "residual gradient shape");
+    Matrix sum = rt.matrix_binary_on(stream, output_gradient, residual_gradient, BinaryOp::Add);
+    Matrix gradient = rt.new_uninit_matrix(sum.rows(), sum.cols());
+    if (activation_ != Activation::Identity) {
+        check(forge_activation_backward(rt.raw(), stream_raw(stream), sum.slice(), pre_activation.slice(),
+                                        gradient.slice(), gradient.len(),
+                                        (forge_activation)activation_),
+              "backward_with_res");
+    } else {
+        gradient = std::move(sum);
+    }
+    std::optional<Vector> bias_gradient;
+    if (bias_) bias_gradient = rt.matrix_sum_cols(gradient, stream);
+    return {std::move(gradient), std::move(bias_gradient)};
+}
+
+// ===================================================================== MLP
+
+MlpExecutor::MlpExecutor(std::vector<Linear> layers,
+                         std::optional<std::pair<size_t, size_t>> res_range, Loss loss)
+    : layers_(std::move(layers)), res_range_(res_range), loss_(loss) {
+    require(!layers_.empty(), "MLP must contain at least one layer");
+    if (res_range_)
+        require(res_range_->first < res_range_->second && res_range_->second <= layers_.size(),
+                "invalid residual range");
+}
+
+Matrix MlpExecutor::forward(const Matrix& input, CudaRuntime& rt) {
+    return forward_plus(input, nullptr, rt);
+}
+
+Matrix MlpExecutor::forward_plus(const Matrix& input, const Matrix* final_residual,
+                                 CudaRuntime& rt) {
+    // mlp.rs:53-85.  The residual source is kept alive instead of cloned.
+    const size_t L = layers_.size();
+    std::vector<std::optional<Matrix>> outs(L);
+    auto in_of = [&](size_t i) -> const Matrix& { return i == 0 ? input : *outs[i - 1]; };
+    for (size_t i = 0; i < L; i++) {
+        const bool consumes = res_range_ && i + 1 == res_range_->second;
+        const Matrix* residual = consumes ? &in_of(res_range_->first) : nullptr;
+        const Matrix* extra = i + 1 == L ? final_residual : nullptr;
+        Matrix out;
+        if (residual && extra) {
+            out = layers_[i].forward(in_of(i), residual, rt, nullptr);
+            out.binary_assign(*extra, BinaryOp::Add, rt);
+        } else {
+            out = layers_[i].forward(in_of(i), residual ? residual : extra, rt, nullptr);
+        }
+        outs[i] = std::move(out);
+        if (i >= 1) {
+            const size_t k = i - 1;  // outs[k] was the input of layer i
+            const bool keep = res_range_ && res_range_->first == i && i + 1 < res_range_->second;
+            if (!keep) outs[k].reset();
+        }
+        if (consumes && res_range_->first >= 1) outs[res_range_->first - 1].reset();
+    }
+    return std::move(*outs[L - 1]);
+}
+
+Matrix MlpExecutor::backward(const std::vector<Matrix>& layer_inputs,
+                             const std::vector<Matrix>& pre_activations,
+                             const Matrix& output_gradient, float learning_rate, CudaRuntime& rt,
+                             std::vector<Matrix>* weight_gradients,
+                             std::vector<std::optional<Vector>>* bias_gradients,
+                             const Matrix* input_gradient_residual) {
+    // mlp.rs:121-168, last layer first.  When the previous layer has a cached
+    // pre-activation and no residual gradient joins at this boundary, its
+    // act'(z) multiply is fused into this layer's input-gradient GEMM.
+    const size_t L = layers_.size();
+    require(layer_inputs.size() == L, "layer_inputs.len() == layers.len()");
+    if (weight_gradients) weight_gradients->resize(L);
+    if (bias_gradients) bias_gradients->resize(L);
+    auto cached_pre = [&](size_t i) -> const Matrix* {
+        return i < pre_activations.size() && pre_activations[i].len() ? &pre_activations[i]
+                                                                       : nullptr;
+    };
+    const Matrix* grad = &output_gradient;
+    std::optional<Matrix> grad_owned;
+    bool grad_preactivated = false;
+    std::optional<std::pair<size_t, Matrix>> residual_gradient;
+
+    for (size_t step = 0; step < L; step++) {
+        const size_t index = L - 1 - step;
+        Linear& layer = layers_[index];
+        std::optional<size_t> residual_index;
+        if (res_range_ && index + 1 == res_range_->second) residual_index = res_range_->first;
+
+        // Layer gradient: dY * act'(pre).
+        std::optional<Matrix> layer_grad_owned;
+        std::optional<Vector> bias_gradient;
+        const Matrix* layer_gradient = grad;
+        if (layer.needs_pre_activation() && !grad_preactivated) {
+            const Matrix* pre = cached_pre(index);
+            std::optional<Matrix> recomputed;
+            if (!pre) {
+                const Matrix* residual =
+                    residual_index ? &layer_inputs[*residual_index] : nullptr;
+                recomputed = layer.affine(layer_inputs[index], residual, rt, nullptr);
+                pre = &*recomputed;
+            }
+            auto gb = layer.backward(pre, *grad, rt, nullptr);
+            layer_grad_owned = std::move(gb.first);
+            bias_gradient = std::move(gb.second);
+            layer_gradient = &*layer_grad_owned;
+        } else if (layer.bias()) {
+            bias_gradient = rt.matrix_sum_cols(*layer_gradient);
+        }
+
+        // Input gradient G * W^T (+ act' of the previous layer, fused).
+        const bool skip_now = (residual_index && *residual_index == index) ||
+                              (residual_gradient && residual_gradient->first == index);
+        Linear* prev = index > 0 ? &layers_[index - 1] : nullptr;
+        const Matrix* prev_pre = index > 0 ? cached_pre(index - 1) : nullptr;
+        const bool fuse_prev = prev && prev->needs_pre_activation() && prev_pre && !skip_now;
+        const bool add_external = index == 0 && input_gradient_residual;
+        Matrix input_gradient = rt.new_uninit_matrix(layer_gradient->rows(), layer.weights().rows());
+        forge_gemm_epilogue ep = plain_epilogue();
+        if (fuse_prev) {
+            ep.aux_mul = prev_pre->slice();
+            ep.aux_activation = (int)prev->activation();
+        }
+        if (add_external && !skip_now) {
+            require(input_gradient_residual->rows() == input_gradient.rows() &&
+                        input_gradient_residual->cols() == input_gradient.cols(),
+                    "input gradient residual shape");
+            ep.residual = input_gradient_residual->slice();
+        }
+        rt.gemm_ex(nullptr, false, true, *layer_gradient, layer.weights(), input_gradient.slice(),
+                   layer_gradient->rows(), layer.weights().rows(), layer.weights().cols(), ep);
+
+        if (residual_index)
+            residual_gradient = std::make_pair(*residual_index, rt.clone_matrix(*layer_gradient));
+        if (residual_gradient && residual_gradient->first == index) {
+            input_gradient.binary_assign(residual_gradient->second, BinaryOp::Add, rt);
+            residual_gradient.reset();
+        }
+        if (add_external && skip_now)
+            input_gradient.binary_assign(*input_gradient_residual, BinaryOp::Add, rt);
+
+        Matrix* wg = nullptr;
+        if (weight_gradients) {
+            (*weight_gradients)[index] =
+                rt.new_uninit_matrix(layer.weights().rows(), layer.weights().cols());
+            wg = &(*weight_gradients)[index];
+        }
+        layer.learn_keep(layer_inputs[index], *layer_gradient,
+                         bias_gradient ? &*bias_gradient : nullptr, learning_rate, wg, rt,
+                         nullptr);
+        if (bias_gradients) (*bias_gradients)[index] = std::move(bias_gradient);
+
+        grad_owned = std::move(input_gradient);
+        grad = &*grad_owned;
+        grad_preactivated = fuse_prev;
+    }
+    require(!residual_gradient, "unresolved residual gradient");
+    return std::move(*grad_owned);
+}
+
+Matrix TrainingMlp::forward(Matrix input, CudaRuntime& rt) {
+    return forward_plus(std::move(input), false, rt);
+}
+
+Matrix TrainingMlp::forward_plus(Matrix input, bool add_input_to_output, CudaRuntime& rt) {
+    // mlp.rs:233-254; the pre-activation of every activated layer is kept.
+    auto& layers = executor_.layers();
+    const size_t L = layers.size();
+    const auto res = executor_.res_range();
+    layer_inputs_.clear();
+    pre_activations_.clear();
+    layer_inputs_.reserve(L);
+    pre_activations_.resize(L);
+    layer_inputs_.push_back(std::move(input));
+    for (size_t i = 0; i < L; i++) {
+        const Matrix* residual = (res && i + 1 == res->second) ? &layer_inputs_[res->first] : nullptr;
+        const Matrix* extra = (i + 1 == L && add_input_to_output) ? &layer_inputs_[0] : nullptr;
+        Matrix* pre = nullptr;
+        if (layers[i].needs_pre_activation()) {
+            pre_activations_[i] = rt.new_uninit_matrix(layer_inputs_[i].rows(), layers[i].weights().cols());
+            pre = &pre_activations_[i];
+        }
+        Matrix out;
+        if (residual && extra) {
+            out = layers[i].forward_keep(layer_inputs_[i], residual, pre, rt, nullptr);
+            out.binary_assign(*extra, BinaryOp::Add, rt);
+        } else {
+            out = layers[i].forward_keep(layer_inputs_[i], residual ? residual : extra, pre, rt,
+                                         nullptr);
+        }
+        if (i + 1 == L) return out;
+        layer_inputs_.push_back(std::move(out));
+    }
+    throw Error(FORGE_EINVAL, "MLP always contains at least one layer");
+}
+
+Matrix TrainingMlp::backward(const Matrix& output_gradient, float learning_rate, CudaRuntime& rt) {
+    return executor_.backward(layer_inputs_, pre_activations_, output_gradient, learning_rate, rt);
+}
+
+Matrix TrainingMlp::backward_grads(const Matrix& output_gradient, float learning_rate,
+                                   CudaRuntime& rt, std::vector<Matrix>* weight_gradients,
+                                   std::vector<std::optional<Vector>>* bias_gradients,
+                                   const Matrix* input_gradient_residual) {
+    return executor_.backward(layer_inputs_, pre_activations_, output_gradient, learning_rate, rt,
+                              weight_gradients, bias_gradients, input_gradient_residual);
+}
+
+// =========================================================== Normalization
+
+void Normalization::forward(Matrix& m, CudaRuntime& rt) const {
+    if (m.rows() == 0) return;
+    if (kind == NormType::Layer)
+        check(forge_layer_norm_rows(rt.raw(), nullptr, m.slice(),
+                                    gamma ? gamma->slice() : forge_slice{nullptr, 0},
+                                    beta ? beta->slice() : forge_slice{nullptr, 0}, m.rows(),
+                                    m.cols(), eps),
+              "layer_norm");
+    else
+        check(forge_rms_norm_rows(rt.raw(), nullptr, m.slice(),
+                                  gamma ? gamma->slice() : forge_slice{nullptr, 0}, m.rows(),
+                                  m.cols(), eps),
+              "rms_norm");
+}
+
+Matrix Normalization::backward(const Matrix& input, const Matrix& output_gradient,
+                               CudaRuntime& rt, Vector* dgamma, Vector* dbeta) const {
+    require(input.rows() == output_gradient.rows() && input.cols() == output_gradient.cols(),
+            "norm backward shapes");
+    Matrix out = rt.new_uninit_matrix(input.rows(), input.cols());
+    forge_slice g = gamma ? gamma->slice() : forge_slice{nullptr, 0};
+    forge_slice dg = dgamma ? dgamma->slice() : forge_slice{nullptr, 0};
+    forge_slice db = dbeta ? dbeta->slice() : forge_slice{nullptr, 0};
+    if (kind == NormType::Layer)
+        check(forge_layer_norm_bwd(rt.raw(), nullptr, input.slice(), output_gradient.slice(), g,
+                                   out.slice(), dg, db, input.rows(), input.cols(), eps),
+              "layer_norm_backward");
+    else
+        check(forge_rms_norm_bwd(rt.raw(), nullptr, input.slice(), output_gradient.slice(), g,
+                                 out.slice(), dg, input.rows(), input.cols(), eps),
+              "rms_norm_backward");
+    return out;
+}
+
+// ======================================================== QkvProjection
+
+QkvProjection::QkvProjection(Linear query, Linear key, Linear value,
+                             std::optional<std::vector<CudaStream>> streams)
+    : query_(std::move(query)), key_(std::move(key)), value_(std::move(value)),
+      streams_(std::move(streams)) {
+    if (streams_) require(streams_->size() == 3, "Q/K/V execution requires three streams");
+}
+
+QkvProjection::Projected QkvProjection::project(const Matrix& query_input,
+                                                const Matrix& key_value_input, CudaRuntime& rt) {
+    // attention.rs:65-94: three Linear::forward on three forked streams.
+    if (streams_) rt.fork_streams(*streams_);
+    else streams_ = rt.create_extra_streams(3);
+    const auto& s = *streams_;
+    Projected p;
+    p.query = query_.forward(query_input, nullptr, rt, &s[0]);
+    p.key = key_.forward(key_value_input, nullptr, rt, &s[1]);
+    p.value = value_.forward(key_value_input, nullptr, rt, &s[2]);
+    return p;
+}
+
+void QkvProjection::wait_for_query_key(CudaRuntime& rt) {
+    rt.join_streams({(*streams_)[0], (*streams_)[1]});
+}
+
+void QkvProjection::wait_for_value(CudaRuntime& rt) { rt.join_streams({(*streams_)[2]}); }
+
+// ============================================================== Attention
+
+Attention::Attention(Linear query, Linear key, Linear value,
+                     std::optional<std::vector<CudaStream>> streams, Normalization norm)
+    : qkv_(std::move(query), std::move(key), std::move(value), std::move(streams)),
+      norm_(std::move(norm)) {}
+
+void Attention::normalize(Matrix& m, CudaRuntime& rt, const Normalization* norm) const {
+    (norm ? *norm : norm_).forward(m, rt);
+}
+
+static float score_scale(size_t query_cols) {
+    // attention.rs:372,398: 1.0 / (query.cols as f32).sqrt()
+    return 1.0f / std::sqrt((float)query_cols);
+}
+
+Matrix Attention::attention_value(QkvProjection::Projected projected, const Matrix& residual,
+                                  bool mask, CudaRuntime& rt) {
+    // attention.rs:618-669: S = Q K^T / sqrt(d) as one NT GEMM with the
+    // scale in its epilogue; (mask); softmax; A = P V with the residual add
+    // of finish_forward (attention.rs:525-535) fused.
+    qkv_.wait_for_query_key(rt);
+    const Matrix& q = projected.query;
+    const Matrix& k = projected.key;
+    require(q.cols() == k.cols(), "query/key widths");
+    Matrix scores = rt.new_uninit_matrix(q.rows(), k.rows());
+    forge_gemm_epilogue ep = plain_epilogue();
+    ep.alpha = score_scale(q.cols());
+    rt.gemm_ex(nullptr, false, true, q, k, scores.slice(), q.rows(), k.rows(), q.cols(), ep);
+    if (mask) scores.causal_mask(rt);
+    scores.softmax_rows(rt);
+    qkv_.wait_for_value(rt);
+    const Matrix& v = projected.value;
+    require(v.rows() == k.rows(), "value rows == key rows");
+    require(residual.rows() == q.rows() && residual.cols() == v.cols(), "residual shape");
+    Matrix out = rt.new_uninit_matrix(q.rows(), v.cols());
+    forge_gemm_epilogue ep2 = plain_epilogue();
+    ep2.residual = residual.slice();
+    rt.gemm_ex(nullptr, false, false, scores, v, out.slice(), q.rows(), v.cols(), v.rows(), ep2);
+    return out;
+}
+
+Matrix Attention::forward(const Matrix& query_input, const Matrix& key_value_input,
+                          CudaRuntime& rt) {
+    // attention.rs:503-512.
+    Matrix out = attention_value(qkv_.project(query_input, key_value_input, rt), query_input,
+                                 false, rt);
+    normalize(out, rt);
+    return out;
+}
+
+Matrix Attention::forward_mask(const Matrix& query_input, const Matrix& key_value_input,
+                               CudaRuntime& rt) {
+    // attention.rs:514-523.
+    Matrix out = attention_value(qkv_.project(query_input, key_value_input, rt), query_input,
+                                 true, rt);
+    normalize(out, rt);
+    return out;
+}
+
+Matrix Attention::forward_self_training(Matrix input, CudaRuntime& rt) {
+    // attention.rs:540-563: keeps input, Q, K, V, P and the pre-norm sum.
+    QkvProjection::Projected p = qkv_.project(input, input, rt);
+    qkv_.wait_for_query_key(rt);
+    Matrix probabilities = rt.new_uninit_matrix(p.query.rows(), p.key.rows());
+    forge_gemm_epilogue ep = plain_epilogue();
+    ep.alpha = score_scale(p.query.cols());
+    rt.gemm_ex(nullptr, false, true, p.query, p.key, probabilities.slice(), p.query.rows(),
+               p.key.rows(), p.query.cols(), ep);
+    probabilities.softmax_rows(rt);
+    qkv_.wait_for_value(rt);
+    Matrix pre_norm = rt.new_uninit_matrix(p.query.rows(), p.value.cols());
+    forge_gemm_epilogue ep2 = plain_epilogue();
+    ep2.residual = input.slice();
+    rt.gemm_ex(nullptr, false, false, probabilities, p.value, pre_norm.slice(), p.query.rows(),
+               p.value.cols(), p.value.rows(), ep2);
+    Matrix output = rt.clone_matrix(pre_norm);
+    normalize(output, rt);
+    cache_ = Cache{std::move(input), std::move(p.query), std::move(p.key), std::move(p.value),
+                   std::move(probabilities), std::move(pre_norm)};
+    return output;
+}
+
+Matrix Attention::backward_self(const Matrix& output_gradient, float learning_rate,
+                                CudaRuntime& rt, TransformerGrads* grads) {
+    // attention.rs:565-603 with the QKV part of attention.rs:386-427.
+    require(cache_.has_value(), "attention forward must run before backward");
+    Cache& c = *cache_;
+    const size_t S = c.query.rows(), Sk = c.key.rows(), H = c.value.cols();
+    if (grads && grads->weights.size() < 3) {
+        grads->weights.resize(3);
+        grads->biases.resize(3);
+    }
+    Matrix residual_gradient =
+        norm_backward_step(norm_, c.pre_norm, output_gradient, learning_rate, rt, grads != nullptr,
+                           grads ? &grads->norm1_gamma : nullptr,
+                           grads ? &grads->norm1_beta : nullptr);
+
+    // dP = R V^T (NT), dV = P^T R (TN).
+    Matrix probabilities_gradient = rt.new_uninit_matrix(S, Sk);
+    rt.gemm_ex(nullptr, false, true, residual_gradient, c.value, probabilities_gradient.slice(),
+               S, Sk, H, plain_epilogue());
+    Matrix value_gradient = rt.new_uninit_matrix(Sk, H);
+    rt.gemm_ex(nullptr, true, false, c.probabilities, residual_gradient, value_gradient.slice(),
+               Sk, H, S, plain_epilogue());
+    // dS = softmax_bwd(P, dP) / sqrt(d), fused.
+    Matrix score_gradient = rt.new_uninit_matrix(S, Sk);
+    check(forge_softmax_rows_bwd_scaled(rt.raw(), nullptr, c.probabilities.slice(),
+                                        probabilities_gradient.slice(), score_gradient.slice(),
+                                        S, Sk, score_scale(c.query.cols())),
+          "softmax_rows_backward");
+    probabilities_gradient = Matrix();
+    // dQ = dS K (NN), dK = dS^T Q (TN).
+    const size_t D = c.query.cols();
+    Matrix query_gradient = rt.new_uninit_matrix(S, D);
+    rt.gemm_ex(nullptr, false, false, score_gradient, c.key, query_gradient.slice(), S, D, Sk,
+               plain_epilogue());
+    Matrix key_gradient = rt.new_uninit_matrix(Sk, D);
+    rt.gemm_ex(nullptr, true, false, score_gradient, c.query, key_gradient.slice(), Sk, D, S,
+               plain_epilogue());
+    score_gradient = Matrix();
+
+    // QkvProjection::backward_self: per projection dX accumulates and W, b
+    // are updated (dW, db kept when grads are requested).
+    std::optional<Matrix> projection_gradient;
+    Linear* linears[3] = {&qkv_.query(), &qkv_.key(), &qkv_.value()};
+    const Matrix* projected[3] = {&query_gradient, &key_gradient, &value_gradient};
+    for (int i = 0; i < 3; i++) {
+        Linear& lin = *linears[i];
+        std::optional<Matrix> g_owned;
+        std::optional<Vector> db;
+        const Matrix* g = projected[i];
+        if (lin.needs_pre_activation()) {
+            Matrix pre = lin.affine(c.input, nullptr, rt, nullptr);
+            auto gb = lin.backward(&pre, *projected[i], rt, nullptr);
+            g_owned = std::move(gb.first);
+            db = std::move(gb.second);
+            g = &*g_owned;
+        } else if (lin.bias()) {
+            db = rt.matrix_sum_cols(*g);
+        }
+        if (!projection_gradient) projection_gradient = lin.input_gradient(*g, rt, nullptr);
+        else lin.input_gradient_accumulate(*g, *projection_gradient, rt, nullptr);
+        Matrix* wg = nullptr;
+        if (grads) {
+            grads->weights[i] = rt.new_uninit_matrix(lin.weights().rows(), lin.weights().cols());
+            wg = &grads->weights[i];
+        }
+        lin.learn_keep(c.input, *g, db ? &*db : nullptr, learning_rate, wg, rt, nullptr);
+        if (grads) grads->biases[i] = std::move(db);
+    }
+    residual_gradient.binary_assign(*projection_gradient, BinaryOp::Add, rt);
+    return residual_gradient;
+}
+
+// ========================================================= InferenceBlock
+
+static Normalization default_norm(NormType kind) {
+    Normalization n;
+    n.kind = kind;
+    return n;
+}
+
+InferenceBlock::InferenceBlock(Linear query, Linear key, Linear value, Matrix position,
+                               InferenceMLP fcs, Linear output,
+                               std::optional<std::vector<CudaStream>> qkv_streams,
+                               NormType norm_type, std::optional<Normalization> norm2)
+    : attention_(std::move(query), std::move(key), std::move(value), std::move(qkv_streams),
+                 default_norm(norm_type)),
+      position_(std::move(position)), fcs_(std::move(fcs)), output_(std::move(output)),
+      norm2_(norm2 ? std::move(*norm2) : default_norm(norm_type)) {}
+
+Matrix InferenceBlock::forward(const Matrix& input, CudaRuntime& rt) {
+    // inference.rs:76-80.
+    Matrix positioned = rt.matrix_add(input, position_);
+    Matrix x = attention_.forward(positioned, positioned, rt);
+    return finish_forward(std::move(positioned), std::move(x), rt);
+}
+
+Matrix InferenceBlock::forward_mask(const Matrix& input, CudaRuntime& rt) {
+    // inference.rs:82-88.
+    Matrix positioned = rt.matrix_add(input, position_);
+    Matrix x = attention_.forward_mask(positioned, positioned, rt);
+    return finish_forward(std::move(positioned), std::move(x), rt);
+}
+
+Matrix InferenceBlock::finish_forward(Matrix positioned, Matrix x, CudaRuntime& rt) {
+    // inference.rs:90-108: norm(x + ffn(x)) then the output projection; the
+    // x + ffn add is fused into the last FFN layer's epilogue.
+    positioned = Matrix();
+    Matrix out = fcs_.executor().forward_plus(x, &x, rt);
+    x = Matrix();
+    norm2_.forward(out, rt);
+    return output_.forward(out, nullptr, rt, nullptr);
+}
+
+namespace encoder {
+
+InferenceTransformer::InferenceTransformer(Linear q, Linear k, Linear v, Matrix position,
+                                           InferenceMLP fcs, Linear output,
+                                           std::optional<std::vector<CudaStream>> qkv_streams,
+                                           NormType norm_type,
+                                           std::optional<Normalization> norm1,
+                                           std::optional<Normalization> norm2)
+    : block_(std::move(q), std::move(k), std::move(v), std::move(position), std::move(fcs),
+             std::move(output), std::move(qkv_streams), norm_type, std::move(norm2)) {
+    if (norm1) block_.attention().normalization() = std::move(*norm1);
+}
+
+TrainingTransformer::TrainingTransformer(Linear q, Linear k, Linear v, Matrix position,
+                                         TrainingMlp fcs, Linear output, NormType norm_type,
+                                         std::optional<Normalization> norm1,
+                                         std::optional<Normalization> norm2)
+    : attention_(std::move(q), std::move(k), std::move(v), std::nullopt,
+                 norm1 ? std::move(*norm1) : default_norm(norm_type)),
+      position_(std::move(position)), fcs_(std::move(fcs)), output_(std::move(output)),
+      norm2_(norm2 ? std::move(*norm2) : default_norm(norm_type)) {}
+
+Matrix TrainingTransformer::forward(const Matrix& input, CudaRuntime& rt) {
+    // encoder.rs:114-131.
+    Matrix positioned = rt.matrix_add(input, position_);
+    Matrix first_output = attention_.forward_self_training(std::move(positioned), rt);
+    // second_pre_norm = first_output + ffn(first_output), fused.
+    Matrix second_pre_norm = fcs_.forward_plus(std::move(first_output), true, rt);
+    Matrix encoded = rt.clone_matrix(second_pre_norm);
+    norm2_.forward(encoded, rt);
+    Matrix output = output_.forward(encoded, nullptr, rt, nullptr);
+    cache_ = Cache{std::move(second_pre_norm), std::move(encoded)};
+    return output;
+}
+
+Matrix TrainingTransformer::backward(const Matrix& output_gradient, float learning_rate,
+                                     CudaRuntime& rt) {
+    return backward_impl(output_gradient, learning_rate, rt, nullptr);
+}
+
+Matrix TrainingTransformer::backward_grads(const Matrix& output_gradient, float learning_rate,
+                                           CudaRuntime& rt, TransformerGrads& grads) {
+    return backward_impl(output_gradient, learning_rate, rt, &grads);
+}
+
+Matrix TrainingTransformer::backward_impl(const Matrix& output_gradient, float learning_rate,
+                                          CudaRuntime& rt, TransformerGrads* grads) {
+    // encoder.rs:133-186.
+    require(cache_.has_value(), "forward must run before backward");
+    Cache& c = *cache_;
+    const size_t n_ffn = fcs_.executor().len();
+    if (grads) {
+        grads->weights.clear();
+        grads->biases.clear();
+        grads->weights.resize(3 + n_ffn + 1);
+        grads->biases.resize(3 + n_ffn + 1);
+    }
+
+    // Output projection.
+    std::optional<Matrix> g_owned;
+    std::optional<Vector> db_o;
+    const Matrix* g_o = &output_gradient;
+    if (output_.needs_pre_activation()) {
+        Matrix pre = output_.affine(c.encoded, nullptr, rt, nullptr);
+        auto gb = output_.backward(&pre, output_gradient, rt, nullptr);
+        g_owned = std::move(gb.first);
+        db_o = std::move(gb.second);
+        g_o = &*g_owned;
+    } else if (output_.bias()) {
+        db_o = rt.matrix_sum_cols(output_gradient);
+    }
+    Matrix encoded_gradient = output_.input_gradient(*g_o, rt, nullptr);
+    Matrix* wg_o = nullptr;
+    if (grads) {
+        grads->weights[3 + n_ffn] =
+            rt.new_uninit_matrix(output_.weights().rows(), output_.weights().cols());
+        wg_o = &grads->weights[3 + n_ffn];
+    }
+    output_.learn_keep(c.encoded, *g_o, db_o ? &*db_o : nullptr, learning_rate, wg_o, rt,
+                       nullptr);
+    if (grads) grads->biases[3 + n_ffn] = std::move(db_o);
+
+    // Second norm (its gamma/beta, when present, take the SGD step too).
+    Matrix second_gradient = norm_backward_step(
+        norm2_, c.second_pre_norm, encoded_gradient, learning_rate, rt, grads != nullptr,
+        grads ? &grads->norm2_gamma : nullptr, grads ? &grads->norm2_beta : nullptr);
+    encoded_gradient = Matrix();
+
+    // FFN; the residual gradient (second_gradient + ffn input gradient) is
+    // fused into its first layer's input-gradient GEMM.
+    std::vector<Matrix> ffn_w;
+    std::vector<std::optional<Vector>> ffn_b;
+    Matrix first_output_gradient =
+        fcs_.backward_grads(second_gradient, learning_rate, rt, grads ? &ffn_w : nullptr,
+                            grads ? &ffn_b : nullptr, &second_gradient);
+    if (grads) {
+        for (size_t i = 0; i < n_ffn; i++) {
+            grads->weights[3 + i] = std::move(ffn_w[i]);
+            grads->biases[3 + i] = std::move(ffn_b[i]);
+        }
+    }
+    second_gradient = Matrix();
+
+    // Attention (fills grads->weights[0..3) and the first norm).
+    Matrix positioned_gradient =
+        attention_.backward_self(first_output_gradient, learning_rate, rt, grads);
+
+    // Position matrix: P -= lr * dXp (encoder.rs:180-184).
+    Matrix input_gradient = rt.clone_matrix(positioned_gradient);
+    if (grads) grads->position = rt.clone_matrix(positioned_gradient);
+    positioned_gradient.scale(learning_rate, rt);
+    position_.binary_assign(positioned_gradient, BinaryOp::Sub, rt);
+    if (grads) grads->input = rt.clone_matrix(input_gradient);
+    return input_gradient;
+}
+
+}  // namespace encoder
+}  // namespace oxforge

@@ -60,6 +60,7 @@ struct GemmArgs {
     const float* aux;
     float* pre_out;
     int act;
+    int aux_act;
     int update;
     float update_scale;
 };
@@ -75,6 +76,7 @@ struct RowArgs {
     float* pbeta;
     int rows, cols;
     float eps;
+    float scale;
 };
 
 constexpr int ROW_WAVES = 4;   // rows.hpp ROW_WAVES
@@ -226,6 +228,12 @@ extern "C" const char* forge_status_string(forge_status s) {
 }
 
 extern "C" const char* forge_last_error(void) { return g_last_error.c_str(); }
+
+// Lets the executor entry points (net_capi.cpp) report exceptions through
+// forge_last_error(); not part of the public ABI.
+extern "C" void forge_internal_set_error(const char* message) {
+    g_last_error = message ? message : "";
+}
 
 extern "C" forge_status forge_runtime_create(int device, const char* module_path,
                                              forge_runtime** out) {
@@ -574,6 +582,9 @@ forge_status gemm_dispatch(forge_runtime* rt, forge_stream* s, int ta, int tb, f
         a.aux = ep->aux_mul.ptr;
         a.pre_out = ep->pre_out.ptr;
         a.act = ep->activation;
+        if (ep->aux_activation < FORGE_ACT_IDENTITY || ep->aux_activation > FORGE_ACT_SILU)
+            return fail(FORGE_EINVAL, "unknown aux activation %d", ep->aux_activation);
+        a.aux_act = ep->aux_activation;
         a.update = ep->update ? 1 : 0;
         a.update_scale = ep->update_scale;
     }
@@ -787,7 +798,7 @@ extern "C" forge_status forge_softmax_rows(forge_runtime* rt, forge_stream* s, f
     if (!rt) return fail(FORGE_EINVAL, "runtime is null");
     FORGE_TRY(check_rows(rows, cols));
     FORGE_TRY(need(x, rows * cols, "softmax x"));
-    RowArgs a{x.ptr, x.ptr, nullptr, nullptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, 0.f};
+    RowArgs a{x.ptr, x.ptr, nullptr, nullptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, 0.f, 1.0f};
     return row_launch(rt, s, "softmax", a, nullptr, nullptr);
 }
 
@@ -799,7 +810,7 @@ extern "C" forge_status forge_softmax_rows_bwd(forge_runtime* rt, forge_stream* 
     FORGE_TRY(need(p, rows * cols, "softmax_bwd p"));
     FORGE_TRY(need(g, rows * cols, "softmax_bwd g"));
     FORGE_TRY(need(dx, rows * cols, "softmax_bwd dx"));
-    RowArgs a{p.ptr, dx.ptr, g.ptr, nullptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, 0.f};
+    RowArgs a{p.ptr, dx.ptr, g.ptr, nullptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, 0.f, 1.0f};
     return row_launch(rt, s, "softmax_bwd", a, nullptr, nullptr);
 }
 
@@ -811,7 +822,7 @@ extern "C" forge_status forge_layer_norm_rows(forge_runtime* rt, forge_stream* s
     FORGE_TRY(need(x, rows * cols, "layer_norm x"));
     FORGE_TRY(need_opt(gamma, cols, "layer_norm gamma"));
     FORGE_TRY(need_opt(beta, cols, "layer_norm beta"));
-    RowArgs a{x.ptr, x.ptr, nullptr, gamma.ptr, beta.ptr, nullptr, nullptr, (int)rows, (int)cols, eps};
+    RowArgs a{x.ptr, x.ptr, nullptr, gamma.ptr, beta.ptr, nullptr, nullptr, (int)rows, (int)cols, eps, 1.0f};
     return row_launch(rt, s, "layer_norm", a, nullptr, nullptr);
 }
 
@@ -827,7 +838,7 @@ extern "C" forge_status forge_layer_norm_bwd(forge_runtime* rt, forge_stream* s,
     FORGE_TRY(need_opt(gamma, cols, "layer_norm_bwd gamma"));
     FORGE_TRY(need_opt(dgamma, cols, "layer_norm_bwd dgamma"));
     FORGE_TRY(need_opt(dbeta, cols, "layer_norm_bwd dbeta"));
-    RowArgs a{x.ptr, dx.ptr, dy.ptr, gamma.ptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, eps};
+    RowArgs a{x.ptr, dx.ptr, dy.ptr, gamma.ptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, eps, 1.0f};
     return row_launch(rt, s, "layer_norm_bwd", a, dgamma.ptr, dbeta.ptr);
 }
 
@@ -838,7 +849,7 @@ extern "C" forge_status forge_rms_norm_rows(forge_runtime* rt, forge_stream* s, 
     FORGE_TRY(check_rows(rows, cols));
     FORGE_TRY(need(x, rows * cols, "rms_norm x"));
     FORGE_TRY(need_opt(gamma, cols, "rms_norm gamma"));
-    RowArgs a{x.ptr, x.ptr, nullptr, gamma.ptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, eps};
+    RowArgs a{x.ptr, x.ptr, nullptr, gamma.ptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, eps, 1.0f};
     return row_launch(rt, s, "rms_norm", a, nullptr, nullptr);
 }
 
@@ -853,7 +864,7 @@ extern "C" forge_status forge_rms_norm_bwd(forge_runtime* rt, forge_stream* s, f
     FORGE_TRY(need(dx, rows * cols, "rms_norm_bwd dx"));
     FORGE_TRY(need_opt(gamma, cols, "rms_norm_bwd gamma"));
     FORGE_TRY(need_opt(dgamma, cols, "rms_norm_bwd dgamma"));
-    RowArgs a{x.ptr, dx.ptr, dy.ptr, gamma.ptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, eps};
+    RowArgs a{x.ptr, dx.ptr, dy.ptr, gamma.ptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, eps, 1.0f};
     return row_launch(rt, s, "rms_norm_bwd", a, dgamma.ptr, nullptr);
 }
 
@@ -983,6 +994,70 @@ extern "C" forge_status forge_reduce_sum(forge_runtime* rt, forge_stream* s, for
 extern "C" forge_status forge_reduce_max(forge_runtime* rt, forge_stream* s, forge_slice x,
                                          size_t n, forge_slice out) {
     return reduce_impl(rt, s, x, n, out, true);
+}
+
+extern "C" forge_status forge_softmax_rows_bwd_scaled(forge_runtime* rt, forge_stream* s,
+                                                      forge_slice p, forge_slice g,
+                                                      forge_slice dx, size_t rows, size_t cols,
+                                                      float scale) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    FORGE_TRY(check_rows(rows, cols));
+    FORGE_TRY(need(p, rows * cols, "softmax_bwd p"));
+    FORGE_TRY(need(g, rows * cols, "softmax_bwd g"));
+    FORGE_TRY(need(dx, rows * cols, "softmax_bwd dx"));
+    RowArgs a{p.ptr, dx.ptr, g.ptr, nullptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, 0.f,
+              scale};
+    return row_launch(rt, s, "softmax_bwd", a, nullptr, nullptr);
+}
+
+extern "C" forge_status forge_activation_backward(forge_runtime* rt, forge_stream* s,
+                                                  forge_slice dy, forge_slice z, forge_slice g,
+                                                  size_t n, forge_activation act) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    if (act < FORGE_ACT_IDENTITY || act > FORGE_ACT_SILU)
+        return fail(FORGE_EINVAL, "unknown activation %d", (int)act);
+    FORGE_TRY(need(dy, n, "activation_backward dy"));
+    FORGE_TRY(need(z, n, "activation_backward z"));
+    FORGE_TRY(need(g, n, "activation_backward g"));
+    if (n == 0) return FORGE_OK;
+    bool vec = aligned16(dy.ptr) && aligned16(z.ptr) && aligned16(g.ptr);
+    long long nn = (long long)n;
+    int a = (int)act;
+    unsigned grid = grid_for(vec ? nn / 4 + 1 : nn, EW_THREADS, 8192);
+    return launch_args(rt, s, vec ? "forge_act_backward_v" : "forge_act_backward_s", dim3(grid),
+                       dim3(EW_THREADS), 0, (const float*)dy.ptr, (const float*)z.ptr, g.ptr, nn,
+                       a);
+}
+
+extern "C" forge_status forge_fill_random(forge_runtime* rt, forge_stream* s, forge_slice x,
+                                          size_t n, uint32_t seed) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    FORGE_TRY(need(x, n, "fill_random x"));
+    if (n == 0) return FORGE_OK;
+    long long nn = (long long)n;
+    unsigned sd = seed;
+    return launch_args(rt, s, "forge_fill_random", dim3(grid_for(nn, EW_THREADS, 8192)),
+                       dim3(EW_THREADS), 0, x.ptr, nn, sd);
+}
+
+extern "C" forge_status forge_compare(forge_runtime* rt, forge_stream* s, forge_slice l,
+                                      forge_slice r, size_t n, forge_slice out) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    FORGE_TRY(need(l, n, "compare l"));
+    FORGE_TRY(need(r, n, "compare r"));
+    FORGE_TRY(need(out, 1, "compare out"));
+    long long nn = (long long)n;
+    unsigned g = grid_for(nn, EW_THREADS * 4, 1024);
+    if (g == 1)
+        return launch_args(rt, s, "forge_count_neq", dim3(1), dim3(EW_THREADS), 0,
+                           (const float*)l.ptr, (const float*)r.ptr, nn, out.ptr);
+    float* ws;
+    FORGE_TRY(workspace(rt, s, g, &ws));
+    FORGE_TRY(launch_args(rt, s, "forge_count_neq", dim3(g), dim3(EW_THREADS), 0,
+                          (const float*)l.ptr, (const float*)r.ptr, nn, ws));
+    long long gn = g;
+    return launch_args(rt, s, "forge_reduce_sum", dim3(1), dim3(EW_THREADS), 0, (const float*)ws,
+                       gn, out.ptr);
 }
 
 extern "C" forge_status forge_fill_seq(forge_runtime* rt, forge_stream* s, forge_slice x, size_t n,

@@ -195,9 +195,9 @@ class Runtime:
 
     def gemm_ex(self, A, B, C, M, N, K, trans_a=False, trans_b=False, alpha=1.0, bias=None,
                 residual=None, aux_mul=None, pre_out=None, activation=ACT_IDENTITY,
-                update=False, update_scale=0.0, stream=None) -> None:
+                update=False, update_scale=0.0, aux_activation=0, stream=None) -> None:
         ep = GemmEpilogue(alpha, _sl(bias), _sl(residual), _sl(aux_mul), _sl(pre_out),
-                          activation, 1 if update else 0, update_scale)
+                          activation, 1 if update else 0, update_scale, aux_activation)
         call("forge_gemm_ex_f32", self.handle, stream, int(trans_a), int(trans_b), A.slice,
              B.slice, C.slice, M, N, K, byref(ep))
 
@@ -263,3 +263,18 @@ class Runtime:
 
     def causal_mask(self, m, rows, cols, stream=None) -> None:
         call("forge_causal_mask", self.handle, stream, m.slice, rows, cols)
+
+    def softmax_rows_bwd_scaled(self, p, g, dx, rows, cols, scale, stream=None) -> None:
+        call("forge_softmax_rows_bwd_scaled", self.handle, stream, p.slice, g.slice, dx.slice,
+             rows, cols, scale)
+
+    def activation_backward(self, dy, z, g, activation, n=None, stream=None) -> None:
+        call("forge_activation_backward", self.handle, stream, dy.slice, z.slice, g.slice,
+             g.size if n is None else n, activation)
+
+    def fill_random(self, x, seed, n=None, stream=None) -> None:
+        call("forge_fill_random", self.handle, stream, x.slice, x.size if n is None else n, seed)
+
+    def compare(self, l, r, out, n=None, stream=None) -> None:
+        call("forge_compare", self.handle, stream, l.slice, r.slice, l.size if n is None else n,
+             out.slice)

@@ -62,6 +62,7 @@ class GemmEpilogue(ctypes.Structure):
         ("activation", c_int),
         ("update", c_int),
         ("update_scale", c_float),
+        ("aux_activation", c_int),
     ]
 
 
@@ -120,6 +121,10 @@ SIGNATURES = {
     "forge_reduce_max": [RT, ST, Slice, c_size_t, Slice],
     "forge_fill_seq": [RT, ST, Slice, c_size_t, c_int],
     "forge_causal_mask": [RT, ST, Slice, c_size_t, c_size_t],
+    "forge_softmax_rows_bwd_scaled": [RT, ST, Slice, Slice, Slice, c_size_t, c_size_t, c_float],
+    "forge_activation_backward": [RT, ST, Slice, Slice, Slice, c_size_t, c_int],
+    "forge_fill_random": [RT, ST, Slice, c_size_t, ctypes.c_uint32],
+    "forge_compare": [RT, ST, Slice, Slice, c_size_t, Slice],
 }
 
 _RESTYPES = {"forge_status_string": c_char_p, "forge_last_error": c_char_p}

@@ -28,6 +28,17 @@ def test_library_exports_every_declared_symbol():
         assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
 
 
+def test_executor_entry_points_exported():
+    from oxforge import net
+
+    lib = oxforge.load()
+    names = header_functions(os.path.join(ROOT, "include", "oxforge_net.h"))
+    assert len(names) >= 15
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in oxforge_net.h but not exported"
+        assert n in net.SIGNATURES, f"{n} has no ctypes signature"
+
+
 def test_status_strings_and_errors_without_device():
     lib = oxforge.load()
     assert lib.forge_status_string(0) == b"ok"
@@ -71,6 +82,8 @@ def dispatcher_kernel_names():
     for op in ("scale", "add", "gelu", "gelu_d", "relu", "relu_d", "silu", "silu_d",
                "exp_shift", "half_sq", "identity"):
         names += [f"forge_map_{op}_v", f"forge_map_{op}_s"]
+    names += ["forge_fill_random", "forge_act_backward_v", "forge_act_backward_s",
+              "forge_count_neq"]
     names += ["forge_fill_v", "forge_fill_s", "forge_fill_seq", "forge_causal_mask",
               "forge_sum_cols", "forge_sum_rows_v", "forge_sum_rows_s", "forge_reduce_sum",
               "forge_reduce_max", "forge_transpose", "forge_transpose_g"]

@@ -1,0 +1,201 @@
+"""GPU parity of the executors (Linear, MLP, transformer inference and
+training step) against the f64 executor oracle (oracle/executors.py).
+
+Bar: max|GPU - oracle| / max|oracle| <= 1e-4 for every output, input
+gradient and parameter gradient (the north star's GEMM/attention bound,
+applied to the whole composition); the SGD update is checked bit-exactly as
+W_new == fl(W - fl(lr * dW)) from the returned f32 gradient.
+"""
+import numpy as np
+import pytest
+
+import oxforge
+from oracle import executors as ex
+from oracle import oracle as orc
+from oxforge import net
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def rel(a, b):
+    b = np.asarray(b, np.float64)
+    return float(np.max(np.abs(np.asarray(a, np.float64) - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def make_params(S, H, F, O, seed, bias=True, affine=True, norm=net.LAYER):
+    p = {"WQ": orc.xavier(H, H, seed), "WK": orc.xavier(H, H, seed + 1),
+         "WV": orc.xavier(H, H, seed + 2), "POS": orc.xavier(S, H, seed + 3),
+         "W1": orc.xavier(H, F, seed + 4), "W2": orc.xavier(F, H, seed + 5),
+         "WO": orc.xavier(H, O, seed + 6)}
+    for i, (k, n) in enumerate((("BQ", H), ("BK", H), ("BV", H), ("B1", F), ("B2", H), ("BO", O))):
+        p[k] = orc.normal((n,), seed + 10 + i, 0.0, 0.1) if bias else None
+    p["G1"] = orc.normal((H,), seed + 20, 1.0, 0.1) if affine else None
+    p["G2"] = orc.normal((H,), seed + 21, 1.0, 0.1) if affine else None
+    p["BE1"] = orc.normal((H,), seed + 22, 0.0, 0.1) if affine and norm == net.LAYER else None
+    p["BE2"] = orc.normal((H,), seed + 23, 0.0, 0.1) if affine and norm == net.LAYER else None
+    return p
+
+
+# ------------------------------------------------------------------ Linear
+def test_linear_c1_identity_no_bias(rt):
+    """X [256,128] x W [128,64], identity, no bias."""
+    say("linear C1")
+    X = orc.uniform((256, 128), 1)
+    W = orc.uniform((128, 64), 2)
+    lin = net.Linear(rt, W)
+    Y = lin.forward(rt.array(X)).numpy()
+    ref, _ = ex.linear_forward(X, W)
+    assert rel(Y, ref) <= TOL
+
+
+@pytest.mark.parametrize("act", [0, 1, 2, 3])
+def test_linear_forward_backward_learn(rt, act):
+    say(f"linear act={act}")
+    M, I, O = 96, 80, 48
+    X, W = orc.uniform((M, I), 3), orc.uniform((I, O), 4)
+    b, R = orc.uniform((O,), 5), orc.uniform((M, O), 6)
+    dY = orc.normal((M, O), 7)
+    lin = net.Linear(rt, W, b, act)
+    dX_, dR = rt.array(X), rt.array(R)
+    pre = rt.empty((M, O))
+    Y = lin.forward(dX_, dR, pre_out=pre).numpy()
+    refY, refZ = ex.linear_forward(X, W, b, R, act)
+    assert rel(Y, refY) <= TOL and rel(pre.numpy(), refZ) <= TOL
+    G, db = rt.empty((M, O)), rt.empty((O,))
+    lin.backward(pre, rt.array(dY), G, db)
+    refG, refdb = ex.linear_backward(pre.numpy(), dY, act, True)
+    assert rel(G.numpy(), refG) <= TOL and rel(db.numpy(), refdb) <= TOL
+    dXg = rt.empty((M, I))
+    lin.input_gradient(G, dXg)
+    assert rel(dXg.numpy(), G.numpy().astype(np.float64) @ W.T.astype(np.float64)) <= TOL
+    lr = 1e-2
+    lin.learn(dX_, G, db, lr)
+    dW = X.T.astype(np.float64) @ G.numpy().astype(np.float64)
+    assert rel(lin.param(0), W - lr * dW) <= TOL
+    assert np.array_equal(lin.param(1), b - np.float32(lr) * db.numpy())
+
+
+def test_loss_rows(rt):
+    O, T = orc.normal((37, 21), 1), orc.normal((37, 21), 2)
+    out = rt.empty((37,))
+    net.loss_rows(rt, rt.array(O), rt.array(T), out)
+    assert rel(out.numpy(), ex.loss_rows(O, T)) <= 1e-5
+
+
+# --------------------------------------------------------------------- MLP
+@pytest.mark.parametrize("res_range", [None, (0, 2), (1, 3), (0, 3)])
+def test_mlp_training(rt, res_range):
+    say(f"mlp res_range={res_range}")
+    dims = {None: [64, 96, 80, 48], (0, 2): [64, 96, 64, 48], (1, 3): [64, 96, 80, 96],
+            (0, 3): [64, 96, 80, 64]}[res_range]
+    acts = [1, 3, 0]
+    layers = [(orc.xavier(dims[i], dims[i + 1], 10 + i), orc.normal((dims[i + 1],), 20 + i, 0, 0.1),
+               acts[i]) for i in range(3)]
+    X, dY = orc.normal((50, dims[0]), 1), orc.normal((50, dims[-1]), 2)
+    m = net.Mlp(rt, layers, res_range, training=True)
+    Y = m.forward(rt.array(X)).numpy()
+    ref, ins, pres = ex.mlp_forward(layers, X, res_range)
+    assert rel(Y, ref) <= TOL
+    lr = 1e-2
+    dX = m.backward(rt.array(dY), lr).numpy()
+    rdX, dWs, dbs = ex.mlp_backward(layers, ins, pres, dY, res_range)
+    assert rel(dX, rdX) <= TOL
+    for i, (W, b, _) in enumerate(layers):
+        assert rel(m.param(i, 0), W - lr * dWs[i]) <= TOL
+        assert rel(m.param(i, 1), b - lr * dbs[i]) <= TOL
+
+
+# ------------------------------------------------------------- transformer
+INFER_CASES = [
+    ("encoder rms small", 64, 64, 256, 64, net.RMS, net.ENCODER_INFERENCE, True),
+    ("encoder layer small", 96, 128, 256, 80, net.LAYER, net.ENCODER_INFERENCE, False),
+    ("decoder layer small", 64, 64, 128, 32, net.LAYER, net.DECODER_INFERENCE, True),
+    ("C4 full: S=2048 H=1024 F=4096 O=1024 RMS", 2048, 1024, 4096, 1024, net.RMS,
+     net.ENCODER_INFERENCE, True),
+]
+
+
+@pytest.mark.parametrize("name,S,H,F,O,norm,kind,streams", INFER_CASES)
+def test_transformer_inference(rt, name, S, H, F, O, norm, kind, streams):
+    say(f"inference {name}")
+    full = S == 2048
+    p = make_params(S, H, F, O, 40, bias=not full, affine=not full, norm=norm)
+    if full:  # biases zero, reference (parameterless) norm
+        for k in ("BQ", "BK", "BV", "B1", "B2", "BO"):
+            n = {"B1": F, "BO": O}.get(k, H)
+            p[k] = np.zeros(n, np.float32)
+    X = orc.normal((S, H), 4)
+    T = net.Transformer(rt, p, S, H, F, O, norm, kind, streams)
+    Y1 = T.forward(rt.array(X)).numpy()
+    Y2 = T.forward(rt.array(X)).numpy()
+    assert np.array_equal(Y1, Y2), "forward is not deterministic"
+    ref, _ = ex.transformer_forward(p, X, norm, causal=(kind == net.DECODER_INFERENCE))
+    err = rel(Y1, ref)
+    print(f"  rel err {err:.3e}")
+    assert err <= TOL
+
+
+TRAIN_CASES = [
+    ("layer small", 64, 64, 256, 64, net.LAYER, True, True),
+    ("rms small no-bias", 48, 32, 96, 40, net.RMS, False, True),
+    ("layer medium", 512, 256, 1024, 256, net.LAYER, True, True),
+    ("layer reference norm", 64, 64, 128, 64, net.LAYER, True, False),
+]
+
+
+@pytest.mark.parametrize("name,S,H,F,O,norm,bias,affine", TRAIN_CASES)
+def test_transformer_training_step(rt, name, S, H, F, O, norm, bias, affine):
+    say(f"training {name}")
+    p = make_params(S, H, F, O, 50, bias=bias, affine=affine, norm=norm)
+    X = orc.normal((S, H), 5)
+    dY = orc.normal((S, O), 6)
+    lr = np.float32(1e-3)
+    T = net.Transformer(rt, p, S, H, F, O, norm, net.ENCODER_TRAINING)
+    Y = T.forward(rt.array(X)).numpy()
+    ref, cache = ex.transformer_forward(p, X, norm)
+    assert rel(Y, ref) <= TOL
+    dXd = rt.empty((S, H))
+    grads = T.backward(rt.array(dY), float(lr), dXd, want_grads=True)
+    rdX, rg = ex.transformer_backward(p, cache, dY, norm)
+    errs = {"dX": rel(dXd.numpy(), rdX)}
+    for k in net.TP_SLOTS:
+        if rg.get(k) is None or p.get(k) is None:
+            continue
+        g = grads[k].numpy()
+        errs[k] = rel(g, rg[k])
+        # SGD identity on the updated parameter, from the returned gradient.
+        new = T.param(k)
+        assert np.array_equal(new, p[k] - lr * g), f"SGD update of {k}"
+    print("  " + " ".join(f"{k}={v:.1e}" for k, v in errs.items()))
+    bad = {k: v for k, v in errs.items() if v > TOL}
+    assert not bad, bad
+
+
+def test_transformer_training_c5_full_size(rt):
+    """BASELINE config 5 at full size (S=4096, H=2048, F=8192, O=2048,
+    LayerNorm): one step against the f64 oracle."""
+    S, H, F, O = 4096, 2048, 8192, 2048
+    say("training C5 full size")
+    p = make_params(S, H, F, O, 60, bias=True, affine=True, norm=net.LAYER)
+    for k in ("BQ", "BK", "BV", "B1", "B2", "BO"):
+        p[k] = np.zeros_like(p[k])
+    X = orc.normal((S, H), 7)
+    dY = orc.normal((S, O), 8)
+    T = net.Transformer(rt, p, S, H, F, O, net.LAYER, net.ENCODER_TRAINING)
+    Y = T.forward(rt.array(X)).numpy()
+    dXd = rt.empty((S, H))
+    grads = T.backward(rt.array(dY), 1e-3, dXd, want_grads=True)
+    ref, cache = ex.transformer_forward(p, X, net.LAYER)
+    errs = {"Y": rel(Y, ref)}
+    rdX, rg = ex.transformer_backward(p, cache, dY, net.LAYER)
+    errs["dX"] = rel(dXd.numpy(), rdX)
+    for k in ("WQ", "WK", "WV", "W1", "W2", "WO", "G1", "BE1", "G2", "BE2", "B1", "BO"):
+        errs[k] = rel(grads[k].numpy(), rg[k])
+    print("  " + " ".join(f"{k}={v:.1e}" for k, v in errs.items()))
+    bad = {k: v for k, v in errs.items() if v > TOL}
+    assert not bad, bad

@@ -410,3 +410,72 @@ def test_streams_fork_join(rt):
         got = total.numpy()
         ref = [orc.gemm_f64(A, w) for w in Ws]
         assert np.max(np.abs(got - (ref[0] + ref[1] + ref[2]))) <= 1e-3
+
+
+# ------------------------------------------------ executor support kernels
+def test_fill_random_bit_exact(rt):
+    say("fill_random")
+    d = rt.empty((100_003,))
+    rt.fill_random(d, 0xC0FFEE)
+    assert np.array_equal(d.numpy(), orc.fill_random(100_003, 0xC0FFEE))
+
+
+@pytest.mark.parametrize("act,dop", [(1, orc.MAP_GELU_D), (2, orc.MAP_RELU_D), (3, orc.MAP_SILU_D),
+                                     (0, orc.MAP_IDENTITY)])
+def test_activation_backward(rt, act, dop):
+    say(f"activation_backward act={act}")
+    dy = orc.normal((1001,), 1)
+    z = orc.normal((1001,), 2, 0.0, 2.0)
+    g = rt.empty((1001,))
+    rt.activation_backward(rt.array(dy), rt.array(z), g, act)
+    if act == 0:
+        assert np.array_equal(g.numpy(), dy)
+    else:
+        ref = orc.activation_backward(dy, z, dop)
+        assert np.all(np.abs(g.numpy() - ref) <= 2e-6 + 2e-6 * np.abs(ref))
+
+
+def test_compare_counts_every_mismatch(rt):
+    say("compare")
+    a = orc.normal((300_000,), 1)
+    b = a.copy()
+    b[[0, 1023, 1024, 299_999]] += 1.0
+    out = rt.empty((1,))
+    rt.compare(rt.array(a), rt.array(b), out)
+    assert out.numpy()[0] == 4.0
+    rt.compare(rt.array(a), rt.array(a), out)
+    assert out.numpy()[0] == 0.0
+
+
+def test_softmax_bwd_scaled_equals_bwd_then_scale(rt):
+    say("softmax_bwd_scaled")
+    p = orc.softmax_rows(orc.normal((64, 300), 1))
+    g = orc.normal((64, 300), 2)
+    s = np.float32(1.0 / np.sqrt(np.float32(1024)))
+    dp, dg = rt.array(p), rt.array(g)
+    a, b = rt.empty((64, 300)), rt.empty((64, 300))
+    rt.softmax_rows_bwd_scaled(dp, dg, a, 64, 300, float(s))
+    rt.softmax_rows_bwd(dp, dg, b, 64, 300)
+    rt.map(b, oxforge.MAP_SCALE, float(s))
+    assert np.array_equal(a.numpy(), b.numpy())
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 128, 192), (70, 50, 33)])
+def test_transposed_operands_bit_identical_to_materialised_transpose(rt, M, N, K):
+    """NT/TN GEMMs read A^T/B^T in place; the products equal the reference's
+    transpose-then-GEMM sequence bit for bit."""
+    say(f"nt/tn vs transpose {M}x{N}x{K}")
+    At = orc.uniform((K, M), 1)
+    Bt = orc.uniform((N, K), 2)
+    B = orc.uniform((K, N), 3)
+    dAt, dBt, dB = rt.array(At), rt.array(Bt), rt.array(B)
+    dA, dBn = rt.empty((M, K)), rt.empty((K, N))
+    rt.transpose(dAt, dA, K, M)
+    rt.transpose(dBt, dBn, N, K)
+    c1, c2 = rt.empty((M, N)), rt.empty((M, N))
+    rt.gemm_ex(dAt, dB, c1, M, N, K, trans_a=True)
+    rt.gemm_ex(dA, dB, c2, M, N, K)
+    assert np.array_equal(c1.numpy(), c2.numpy())
+    rt.gemm_ex(dA, dBt, c1, M, N, K, trans_b=True)
+    rt.gemm_ex(dA, dBn, c2, M, N, K)
+    assert np.array_equal(c1.numpy(), c2.numpy())

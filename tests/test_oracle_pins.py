@@ -261,3 +261,24 @@ def test_synthetic_generators_are_deterministic():
     assert a.min() >= -1 and a.max() < 1 and abs(a.mean()) < 0.1
     n = orc.normal((20000,), 6)
     assert abs(n.mean()) < 0.03 and abs(n.std() - 1) < 0.03
+
+
+def test_fill_random_hash_restated_independently():
+    # common.rs:3-9 in wrapping u32 arithmetic, restated with numpy uint64
+    # masks; elementwise.rs:40-41 divides by u32::MAX as f32.
+    seed = 0xC0FFEE
+    i = np.arange(5000, dtype=np.uint64)
+    x = (seed + i) & 0xFFFFFFFF
+    x = (x + (x << 13)) & 0xFFFFFFFF
+    x = (x - (x >> 17)) & 0xFFFFFFFF
+    x = (x * ((x << 5) & 0xFFFFFFFF)) & 0xFFFFFFFF
+    ref = x.astype(np.float32) / np.float32(4294967295.0)
+    assert np.array_equal(orc.fill_random(5000, seed), ref)
+
+
+def test_activation_backward_is_dy_times_derivative():
+    r = rng(11)
+    dy = r.normal(0, 1, 500).astype(np.float32)
+    z = r.normal(0, 2, 500).astype(np.float32)
+    for op in (orc.MAP_GELU_D, orc.MAP_RELU_D, orc.MAP_SILU_D):
+        assert np.array_equal(orc.activation_backward(dy, z, op), dy * orc.map_(z, op))
