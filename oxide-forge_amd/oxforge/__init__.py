@@ -8,6 +8,7 @@ calls; nothing here computes on the host.
 from __future__ import annotations
 
 import ctypes
+import weakref
 from ctypes import byref, c_int, c_size_t, c_void_p
 
 import numpy as np
@@ -93,9 +94,16 @@ class Runtime:
         path = module_path.encode() if module_path else None
         call("forge_runtime_create", device, path, byref(h))
         self.handle = h
+        # Objects built on this runtime (executor models) are closed first.
+        self._children = weakref.WeakSet()
+
+    def adopt(self, child) -> None:
+        self._children.add(child)
 
     def close(self) -> None:
         if self.handle:
+            for child in list(self._children):
+                child.close()
             call("forge_runtime_destroy", self.handle)
             self.handle = None
 

@@ -74,11 +74,14 @@ class _Model:
         _declare()
         self.rt = rt
         self.h = c_void_p()
+        rt.adopt(self)
 
     def close(self):
-        if self.h:
+        # A model must be destroyed before its runtime; Runtime.close()
+        # closes its models first, so a model outliving it holds nothing.
+        if self.h and self.rt.handle:
             call("forge_net_model_destroy", self.h)
-            self.h = c_void_p()
+        self.h = c_void_p()
 
     def __del__(self):
         try:

@@ -167,7 +167,14 @@ def test_transformer_training_step(rt, name, S, H, F, O, norm, bias, affine):
         if rg.get(k) is None or p.get(k) is None:
             continue
         g = grads[k].numpy()
-        errs[k] = rel(g, rg[k])
+        if k == "BK":
+            # d(BK) = column sums of dK = sum_i Q_i * sum_j dS_ij = 0 exactly
+            # (softmax is invariant to the per-row shift a key bias adds), so
+            # only rounding noise remains: bound it against the value bias
+            # gradient's scale instead of a relative error to zero.
+            errs[k] = float(np.max(np.abs(g)) / np.max(np.abs(rg["BV"])))
+        else:
+            errs[k] = rel(g, rg[k])
         # SGD identity on the updated parameter, from the returned gradient.
         new = T.param(k)
         assert np.array_equal(new, p[k] - lr * g), f"SGD update of {k}"
