@@ -37,10 +37,24 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+SPIN_UP_S = 0.3
+
+
 def time_launches(rt, fn, steps: int, warmup: int, stream=None) -> float:
-    """Average milliseconds of fn(i) over `steps` launches (events on stream)."""
-    for i in range(warmup):
+    """Average milliseconds of fn(i) over `steps` launches (events on stream).
+
+    Warmup runs at least `warmup` launches and at least SPIN_UP_S seconds of
+    the same work: the MI355X raises its clocks over the first tens of
+    milliseconds of sustained load (a GEMM dispatch drops from 1.31 ms to
+    1.03 ms over its first ~25 launches), and the timed steps should see
+    the steady state."""
+    t0 = time.perf_counter()
+    i = 0
+    while i < warmup or time.perf_counter() - t0 < SPIN_UP_S:
         fn(i)
+        i += 1
+        if i % 8 == 0:
+            rt.sync(stream)
     rt.sync(stream)
     e0, e1 = rt.event(), rt.event()
     rt.record(e0, stream)
@@ -88,8 +102,6 @@ def rotating(rt, orc, shape, sets, seed):
 
 
 def secondary(rt, orc, steps, warmup, extended):
-    import oxforge
-
     out = {}
     log("gemm 8192x1024x4096")
     t, ms = gemm_tflops(rt, orc, 8192, 1024, 4096, steps, warmup)
@@ -106,7 +118,16 @@ def secondary(rt, orc, steps, warmup, extended):
     for b in xs + ys:
         b.recycle()
 
-    # C2: X [4096, 1024]; 32 rotating sets = 512 MiB per operand.
+    out.update(secondary_rows(rt, orc, steps, warmup, extended))
+    return out
+
+
+def secondary_rows(rt, orc, steps, warmup, extended=True):
+    """C2 row / elementwise kernels on X [4096, 1024], 32 rotating buffer
+    sets (512 MiB per operand) so the MALL cannot serve them."""
+    import oxforge
+
+    out = {}
     rows, cols, sets = 4096, 1024, 32
     X = 4 * rows * cols
     log("row ops 4096x1024")
@@ -221,12 +242,20 @@ def sweep(rt, orc, steps, warmup):
 
     lib = oxforge.load()
     res = {}
-    for (M, N, K) in [(4096, 4096, 4096), (8192, 1024, 4096)]:
+    shapes = [(4096, 4096, 4096), (8192, 1024, 4096),
+              # C4 GEMMs: QKV/out, QK^T, AV, FFN1, FFN2
+              (2048, 1024, 1024), (2048, 2048, 1024), (2048, 1024, 2048), (2048, 4096, 1024),
+              (2048, 1024, 4096),
+              # C5 GEMMs
+              (4096, 2048, 2048), (4096, 4096, 2048), (4096, 2048, 4096), (4096, 8192, 2048),
+              (4096, 2048, 8192), (2048, 2048, 4096), (2048, 8192, 4096)]
+    for (M, N, K) in shapes:
         A = orc.uniform((M, K), 3)
         B = orc.uniform((K, N), 4)
         dA, dB, dC = rt.array(A), rt.array(B), rt.empty((M, N))
         for tag in ["128x128x16_2x2", "128x128x32_2x2", "128x64x16_2x2", "256x128x16_2x2",
-                    "128x256x16_2x2", "256x128x16_4x2"]:
+                    "128x256x16_2x2", "256x128x16_4x2", "128x256x16_2x4", "256x256x16_4x4",
+                    "256x128x32_4x2", "128x128x16_4x2", "128x64x16_2x1", "64x64x16_1x1"]:
             key = f"{M}x{N}x{K}:{tag}"
 
             def fn(i, tag=tag.encode()):
@@ -243,6 +272,58 @@ def sweep(rt, orc, steps, warmup):
         for d in (dA, dB, dC):
             d.recycle()
     return res
+
+
+def profile_workload(rt, orc, name, steps, warmup):
+    """Runs one workload `steps` times (for rocprofv3 runs) and returns its
+    average time.  copy: an identity map over 256 MiB (reads and writes
+    exactly 256 MiB per launch), the calibration kernel for FETCH_SIZE and
+    WRITE_SIZE."""
+    import oxforge
+    from oxforge import net
+
+    if name in ("gemm4096", "gemm8192x1024"):
+        M, N, K = (4096, 4096, 4096) if name == "gemm4096" else (8192, 1024, 4096)
+        t, ms = gemm_tflops(rt, orc, M, N, K, steps, warmup)
+        return {"workload": name, "ms": round(ms, 5), "tflops": round(t, 3)}
+    if name == "copy":
+        # x = x * 1.0 with the scale a kernel argument: one read and one
+        # write per element that the compiler cannot elide.
+        n = 64 * 1024 * 1024
+        x = rt.empty((n,))
+        rt.fill(x, 1.0)
+        ms = time_launches(rt, lambda i: rt.map(x, oxforge.MAP_SCALE, 1.0), steps, warmup)
+        return {"workload": name, "ms": round(ms, 5), "bytes_per_launch": 2 * 4 * n,
+                "gbs": round(2 * 4 * n / (ms * 1e-3) / 1e9, 1)}
+    if name == "transpose":
+        R, C = 8192, 4096
+        x, y = rt.array(orc.uniform((R, C), 21)), rt.empty((C, R))
+        ms = time_launches(rt, lambda i: rt.transpose(x, y, R, C), steps, warmup)
+        return {"workload": name, "ms": round(ms, 5)}
+    if name in ("c4", "c5"):
+        if name == "c4":
+            S, H, F, O = 2048, 1024, 4096, 1024
+            T = net.Transformer(rt, transformer_params(orc, S, H, F, O, 4, False), S, H, F, O,
+                                net.RMS, net.ENCODER_INFERENCE, qkv_streams=True)
+            X, Y = rt.array(orc.normal((S, H), 4)), rt.empty((S, O))
+            ms = time_launches(rt, lambda i: T.forward(X, Y), steps, warmup)
+        else:
+            S, H, F, O = 4096, 2048, 8192, 2048
+            T = net.Transformer(rt, transformer_params(orc, S, H, F, O, 5, True), S, H, F, O,
+                                net.LAYER, net.ENCODER_TRAINING)
+            X, dY = rt.array(orc.normal((S, H), 5)), rt.array(orc.normal((S, O), 6))
+            Y, dX = rt.empty((S, O)), rt.empty((S, H))
+
+            def step(i):
+                T.forward(X, Y)
+                T.backward(dY, 1e-3, dX)
+
+            ms = time_launches(rt, step, steps, warmup)
+        T.close()
+        return {"workload": name, "ms": round(ms, 4)}
+    if name == "rows":
+        return {"workload": name, "results": secondary_rows(rt, orc, steps, warmup)}
+    raise SystemExit(f"unknown profile workload {name}")
 
 
 def cpu_baseline(orc, M, N, K):
@@ -277,6 +358,9 @@ def main() -> int:
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--extended", action="store_true")
     ap.add_argument("--sweep", action="store_true")
+    ap.add_argument("--profile", default=None,
+                    help="run only one workload (gemm4096, gemm8192x1024, copy, transpose, rows, "
+                         "c4, c5) for rocprofv3")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -291,10 +375,15 @@ def main() -> int:
     rt = oxforge.Runtime(0)
     props = rt.props()
     log(f"device {props}")
+    if args.profile:
+        res = profile_workload(rt, orc, args.profile, args.steps, args.warmup)
+        rt.close()
+        print(json.dumps(res), flush=True)
+        return 0
     M = N = K = 4096
     log("gemm 4096^3")
     tflops, ms = gemm_tflops(rt, orc, M, N, K, args.steps, args.warmup)
-    kernel = "forge_gemm_nn_128x128x16_2x2"
+    kernel = "forge_gemm_nn_256x128x16_4x2"
     traffic = load_traffic(kernel)
     line = {
         "metric": METRIC,

@@ -244,7 +244,7 @@ forge_status forge_softmax_rows_bwd(forge_runtime *rt, forge_stream *stream,
                                     forge_slice dx, size_t rows, size_t cols);
 
 /* softmax_rows_backward followed by Matrix::scale, fused: the score
- * gradient of attention backward (attention.rs:584-586),
+ * gradient of attention backward (attention.rs:302-304),
  * dx = (p * (g - sum(p * g))) * scale, two roundings as in the reference. */
 forge_status forge_softmax_rows_bwd_scaled(forge_runtime *rt,
                                            forge_stream *stream, forge_slice p,

@@ -20,7 +20,7 @@
 //   - Linear::forward is one GEMM with bias, residual and activation fused
 //     into its epilogue (linear.rs:185-230 launches up to four kernels);
 //   - transposed operands are read in place by NT/TN GEMMs instead of being
-//     materialised (linear.rs:381-443, attention.rs:579-590, 648-680);
+//     materialised (linear.rs:381-443, attention.rs:297-308, 366-398);
 //   - Linear::learn fuses the lr scale and the subtraction into the dW GEMM;
 //   - TrainingMlp keeps each layer's pre-activation from the forward pass
 //     instead of recomputing it with an extra GEMM (mlp.rs:136-139).

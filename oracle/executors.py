@@ -162,7 +162,7 @@ def transformer_backward(p, cache, dY, norm_kind, ffn_act=GELU):
     g["W1"] = c["out1"].T @ G1
     g["B1"] = G1.sum(axis=0) if p.get("B1") is not None else None
     d_out1 = d_pre2 + G1 @ f64(p["W1"]).T
-    # Attention (attention.rs:565-603, 386-427).
+    # Attention (attention.rs:283-321 and 104-144).
     R, g["G1"], g["BE1"] = norm_backward(c["pre1"], d_out1, norm_kind, p.get("G1"))
     dP = R @ c["V"].T
     dV = c["P"].T @ R

@@ -236,20 +236,73 @@ __device__ __forceinline__ void causal_mask_body(float* m, int rows, int cols) {
 
 // ------------------------------------------------------------ reductions
 
-// Column sums of a [rows, cols] matrix over the row range of chunk
-// blockIdx.y, written to out[blockIdx.y * cols + c].  One thread per column
-// sums its chunk in row order (coalesced across the wave, deterministic);
-// the host reduces the chunk rows with a second launch of the same kernel.
+// Column sums, first pass: chunk blockIdx.y of rows_per_chunk rows, 4 waves
+// taking every 4th row of the chunk.  VEC: a lane owns 4 consecutive columns
+// (one float4 load per row, 1 KiB per wave-row) so a workgroup covers 256
+// columns; scalar: a lane owns one column, 64 per workgroup.  The 4 wave
+// partials are added in LDS in wave order and written to
+// out[blockIdx.y * cols + c].  Summation order depends only on the shape.
+constexpr int SUMCOL_WAVES = 4;
+
+template <bool VEC>
 __device__ __forceinline__ void sum_cols_body(const float* __restrict__ m,
                                               float* __restrict__ out, int rows,
                                               int cols, int rows_per_chunk) {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= cols) return;
+    __shared__ float4 part[SUMCOL_WAVES][64];
+    const int lane = lane_id(), wave = threadIdx.x >> 6;
     const int r0 = blockIdx.y * rows_per_chunk;
     const int r1 = min(rows, r0 + rows_per_chunk);
-    float s = 0.0f;
-    for (int r = r0; r < r1; r++) s += m[(long long)r * cols + c];
-    out[(long long)blockIdx.y * cols + c] = s;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    const int c = VEC ? (blockIdx.x * 64 + lane) * 4 : blockIdx.x * 64 + lane;
+    if (c < cols) {
+        int r = r0 + wave;
+#pragma unroll 4
+        for (; r < r1; r += SUMCOL_WAVES) {
+            const float* p = m + (long long)r * cols + c;
+            if constexpr (VEC) {
+                const float4 v = *reinterpret_cast<const float4*>(p);
+                acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+            } else {
+                acc.x += *p;
+            }
+        }
+    }
+    part[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0 && c < cols) {
+        float4 t = part[0][lane];
+        for (int w = 1; w < SUMCOL_WAVES; w++) {
+            const float4 u = part[w][lane];
+            t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+        }
+        float* o = out + (long long)blockIdx.y * cols + c;
+        if constexpr (VEC) *reinterpret_cast<float4*>(o) = t;
+        else *o = t.x;
+    }
+}
+
+// Column sums, final pass over a short matrix (the first pass's partial
+// rows, or any matrix of few rows): 16 waves per workgroup each take every
+// 16th row of 64 columns, then add in LDS in wave order.
+constexpr int SUMCOL_FINAL_WAVES = 16;
+
+__device__ __forceinline__ void sum_cols_final_body(const float* __restrict__ m,
+                                                    float* __restrict__ out, int rows, int cols) {
+    __shared__ float part[SUMCOL_FINAL_WAVES][64];
+    const int lane = lane_id(), wave = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + lane;
+    float acc = 0.0f;
+    if (c < cols) {
+#pragma unroll 4
+        for (int r = wave; r < rows; r += SUMCOL_FINAL_WAVES) acc += m[(long long)r * cols + c];
+    }
+    part[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0 && c < cols) {
+        float t = part[0][lane];
+        for (int w = 1; w < SUMCOL_FINAL_WAVES; w++) t += part[w][lane];
+        out[c] = t;
+    }
 }
 
 // Row sums: one wave per row (row.rs:16-53).

@@ -19,10 +19,12 @@ using namespace forge;
         gemm_body<BM, BN, BK, WMW, WNW, TA, TB, GUARD, EPI>(p);              \
     }
 
+// Epilogue instances: the three unguarded tiles the dispatcher chooses from
+// (by tile count, see runtime.cpp choose_gemm) and the guarded fallback.
 #define GEMM_FAMILY(AB, TA, TB)                                                   \
-    GEMM_KERNEL(forge_gemm_##AB##_128x128x16_2x2_e, 128, 128, 16, 2, 2, TA, TB, false, true) \
+    GEMM_KERNEL(forge_gemm_##AB##_256x128x16_4x2_e, 256, 128, 16, 4, 2, TA, TB, false, true) \
+    GEMM_KERNEL(forge_gemm_##AB##_128x128x16_4x2_e, 128, 128, 16, 4, 2, TA, TB, false, true) \
     GEMM_KERNEL(forge_gemm_##AB##_128x64x16_2x2_e, 128, 64, 16, 2, 2, TA, TB, false, true)   \
-    GEMM_KERNEL(forge_gemm_##AB##_256x128x16_2x2_e, 256, 128, 16, 2, 2, TA, TB, false, true) \
     GEMM_KERNEL(forge_gemm_##AB##_64x64x16_2x2_g_e, 64, 64, 16, 2, 2, TA, TB, true, true)
 
 GEMM_FAMILY(nn, false, false)
@@ -30,14 +32,20 @@ GEMM_FAMILY(nt, false, true)
 GEMM_FAMILY(tn, true, false)
 GEMM_FAMILY(tt, true, true)
 
-// Plain C = A * B instances (forge_gemm_f32) and the tile-shape candidates
-// measured by the bench sweep.
+// Plain C = A * B instances (forge_gemm_f32 uses the first three and the
+// guarded one) and the other tile-shape candidates of the bench sweep.
 GEMM_KERNEL(forge_gemm_nn_128x128x16_2x2, 128, 128, 16, 2, 2, false, false, false, false)
 GEMM_KERNEL(forge_gemm_nn_128x128x32_2x2, 128, 128, 32, 2, 2, false, false, false, false)
 GEMM_KERNEL(forge_gemm_nn_128x64x16_2x2, 128, 64, 16, 2, 2, false, false, false, false)
 GEMM_KERNEL(forge_gemm_nn_256x128x16_2x2, 256, 128, 16, 2, 2, false, false, false, false)
 GEMM_KERNEL(forge_gemm_nn_128x256x16_2x2, 128, 256, 16, 2, 2, false, false, false, false)
 GEMM_KERNEL(forge_gemm_nn_256x128x16_4x2, 256, 128, 16, 4, 2, false, false, false, false)
+GEMM_KERNEL(forge_gemm_nn_128x256x16_2x4, 128, 256, 16, 2, 4, false, false, false, false)
+GEMM_KERNEL(forge_gemm_nn_256x256x16_4x4, 256, 256, 16, 4, 4, false, false, false, false)
+GEMM_KERNEL(forge_gemm_nn_256x128x32_4x2, 256, 128, 32, 4, 2, false, false, false, false)
+GEMM_KERNEL(forge_gemm_nn_128x128x16_4x2, 128, 128, 16, 4, 2, false, false, false, false)
+GEMM_KERNEL(forge_gemm_nn_128x64x16_2x1, 128, 64, 16, 2, 1, false, false, false, false)
+GEMM_KERNEL(forge_gemm_nn_64x64x16_1x1, 64, 64, 16, 1, 1, false, false, false, false)
 GEMM_KERNEL(forge_gemm_nn_64x64x16_2x2_g, 64, 64, 16, 2, 2, false, false, true, false)
 
 // ------------------------------------------------------------------- rows
@@ -132,9 +140,20 @@ FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_count_neq(const float* l, 
 FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_causal_mask(float* m, int rows, int cols) {
     causal_mask_body(m, rows, cols);
 }
-FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_sum_cols(const float* m, float* out, int rows,
-                                                               int cols, int rows_per_chunk) {
-    sum_cols_body(m, out, rows, cols, rows_per_chunk);
+FORGE_KERNEL void __launch_bounds__(SUMCOL_WAVES * 64) forge_sum_cols_v(const float* m, float* out,
+                                                                       int rows, int cols,
+                                                                       int rows_per_chunk) {
+    sum_cols_body<true>(m, out, rows, cols, rows_per_chunk);
+}
+FORGE_KERNEL void __launch_bounds__(SUMCOL_WAVES * 64) forge_sum_cols_s(const float* m, float* out,
+                                                                       int rows, int cols,
+                                                                       int rows_per_chunk) {
+    sum_cols_body<false>(m, out, rows, cols, rows_per_chunk);
+}
+FORGE_KERNEL void __launch_bounds__(SUMCOL_FINAL_WAVES * 64) forge_sum_cols_final(const float* m,
+                                                                                 float* out,
+                                                                                 int rows, int cols) {
+    sum_cols_final_body(m, out, rows, cols);
 }
 FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_sum_rows_v(const float* m, float* out, int rows,
                                                                  int cols) {

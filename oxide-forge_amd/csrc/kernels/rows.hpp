@@ -52,8 +52,29 @@ __device__ __forceinline__ float max4(float4 a) {
 #define F4_APPLY(dst, a, EXPR_X, EXPR_Y, EXPR_Z, EXPR_W) \
     do { dst.x = (EXPR_X); dst.y = (EXPR_Y); dst.z = (EXPR_Z); dst.w = (EXPR_W); } while (0)
 
+// Loads row `row` into the register arrays of the register path (fill
+// values past cols: -FLT_MAX for softmax, 0 otherwise).
+template <int OP, int VPT, bool BWD>
+__device__ __forceinline__ void row_load(const RowArgs& a, int row, int lane, float4* v,
+                                         float4* g) {
+    const long long base = (long long)row * a.cols;
+    const float fill = (OP == ROW_SOFTMAX) ? -FLT_MAX : 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; i++) {
+        const int c = (i * 64 + lane) * 4;
+        const bool ok = c < a.cols;
+        v[i] = ok ? *reinterpret_cast<const float4*>(a.x + base + c)
+                  : make_float4(fill, fill, fill, fill);
+        if constexpr (BWD)
+            g[i] = ok ? *reinterpret_cast<const float4*>(a.dy + base + c)
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
 // Register path.  VPT float4 per lane; lane l holds columns
-// 4*(64*i + l) .. +3 for i < VPT.
+// 4*(64*i + l) .. +3 for i < VPT.  The partial-producing backward kernels
+// walk several rows per wave, so they prefetch the next row's registers
+// before reducing the current one.
 template <int OP, int VPT, bool PARTIALS>
 __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
     const int lane = lane_id();
@@ -73,21 +94,26 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
         }
     }
 
-    for (int row = blockIdx.x * ROW_WAVES + wave; row < a.rows;
-         row += gridDim.x * ROW_WAVES) {
+    constexpr bool PREFETCH = PARTIALS;
+    const int stride = gridDim.x * ROW_WAVES;
+    int row = blockIdx.x * ROW_WAVES + wave;
+    float4 nv[PREFETCH ? VPT : 1], ng[(PREFETCH && BWD) ? VPT : 1];
+    if (PREFETCH && row < a.rows) row_load<OP, VPT, BWD>(a, row, lane, nv, ng);
+    for (; row < a.rows; row += stride) {
         const long long base = (long long)row * cols;
         float4 v[VPT], g[BWD ? VPT : 1];
         bool ok[VPT];
 #pragma unroll
-        for (int i = 0; i < VPT; i++) {
-            const int c = (i * 64 + lane) * 4;
-            ok[i] = c < cols;
-            const float fill = (OP == ROW_SOFTMAX) ? -FLT_MAX : 0.0f;
-            v[i] = ok[i] ? *reinterpret_cast<const float4*>(a.x + base + c)
-                         : make_float4(fill, fill, fill, fill);
-            if constexpr (BWD)
-                g[i] = ok[i] ? *reinterpret_cast<const float4*>(a.dy + base + c)
-                             : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int i = 0; i < VPT; i++) ok[i] = (i * 64 + lane) * 4 < cols;
+        if constexpr (PREFETCH) {
+#pragma unroll
+            for (int i = 0; i < VPT; i++) {
+                v[i] = nv[i];
+                if constexpr (BWD) g[i] = ng[i];
+            }
+            if (row + stride < a.rows) row_load<OP, VPT, BWD>(a, row + stride, lane, nv, ng);
+        } else {
+            row_load<OP, VPT, BWD>(a, row, lane, v, g);
         }
 
         if constexpr (OP == ROW_SOFTMAX) {

@@ -503,9 +503,9 @@ static float score_scale(size_t query_cols) {
 
 Matrix Attention::attention_value(QkvProjection::Projected projected, const Matrix& residual,
                                   bool mask, CudaRuntime& rt) {
-    // attention.rs:618-669: S = Q K^T / sqrt(d) as one NT GEMM with the
+    // attention.rs:336-387: S = Q K^T / sqrt(d) as one NT GEMM with the
     // scale in its epilogue; (mask); softmax; A = P V with the residual add
-    // of finish_forward (attention.rs:525-535) fused.
+    // of finish_forward (attention.rs:243-253) fused.
     qkv_.wait_for_query_key(rt);
     const Matrix& q = projected.query;
     const Matrix& k = projected.key;
@@ -529,7 +529,7 @@ Matrix Attention::attention_value(QkvProjection::Projected projected, const Matr
 
 Matrix Attention::forward(const Matrix& query_input, const Matrix& key_value_input,
                           CudaRuntime& rt) {
-    // attention.rs:503-512.
+    // attention.rs:221-230.
     Matrix out = attention_value(qkv_.project(query_input, key_value_input, rt), query_input,
                                  false, rt);
     normalize(out, rt);
@@ -538,7 +538,7 @@ Matrix Attention::forward(const Matrix& query_input, const Matrix& key_value_inp
 
 Matrix Attention::forward_mask(const Matrix& query_input, const Matrix& key_value_input,
                                CudaRuntime& rt) {
-    // attention.rs:514-523.
+    // attention.rs:232-241.
     Matrix out = attention_value(qkv_.project(query_input, key_value_input, rt), query_input,
                                  true, rt);
     normalize(out, rt);
@@ -546,7 +546,7 @@ Matrix Attention::forward_mask(const Matrix& query_input, const Matrix& key_valu
 }
 
 Matrix Attention::forward_self_training(Matrix input, CudaRuntime& rt) {
-    // attention.rs:540-563: keeps input, Q, K, V, P and the pre-norm sum.
+    // attention.rs:258-281: keeps input, Q, K, V, P and the pre-norm sum.
     QkvProjection::Projected p = qkv_.project(input, input, rt);
     qkv_.wait_for_query_key(rt);
     Matrix probabilities = rt.new_uninit_matrix(p.query.rows(), p.key.rows());
@@ -570,7 +570,7 @@ Matrix Attention::forward_self_training(Matrix input, CudaRuntime& rt) {
 
 Matrix Attention::backward_self(const Matrix& output_gradient, float learning_rate,
                                 CudaRuntime& rt, TransformerGrads* grads) {
-    // attention.rs:565-603 with the QKV part of attention.rs:386-427.
+    // attention.rs:283-321 with the QKV part of attention.rs:104-144.
     require(cache_.has_value(), "attention forward must run before backward");
     Cache& c = *cache_;
     const size_t S = c.query.rows(), Sk = c.key.rows(), H = c.value.cols();

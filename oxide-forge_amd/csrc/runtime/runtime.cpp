@@ -524,26 +524,29 @@ extern "C" forge_status forge_fill(forge_runtime* rt, forge_stream* s, forge_sli
 namespace {
 
 struct GemmConfig {
-    const char* tag;  // e.g. "128x128x16_2x2"
-    int bm, bn, bk;
+    const char* tag;  // e.g. "256x128x16_4x2"
+    int bm, bn, bk, threads;
 };
 
-const GemmConfig kFast128 = {"128x128x16_2x2", 128, 128, 16};
-const GemmConfig kFast128x64 = {"128x64x16_2x2", 128, 64, 16};
-const GemmConfig kFast256 = {"256x128x16_2x2", 256, 128, 16};
-const GemmConfig kGuard64 = {"64x64x16_2x2_g", 64, 64, 16};
+const GemmConfig kTile256x128 = {"256x128x16_4x2", 256, 128, 16, 512};
+const GemmConfig kTile128x128 = {"128x128x16_4x2", 128, 128, 16, 512};
+const GemmConfig kTile128x64 = {"128x64x16_2x2", 128, 64, 16, 256};
+const GemmConfig kGuard64 = {"64x64x16_2x2_g", 64, 64, 16, 256};
 
-// Picks the tile configuration: unguarded when the shape divides the tile
-// and every operand is 16-byte aligned with 4-float-multiple leading
-// dimensions, the guarded 64x64 tile otherwise.  The 256x128 tile is used
-// when it still yields at least two tiles per CU.
+// Tile choice, measured on MI355X over the C3/C4/C5 GEMM shapes: the
+// 256x128 tile (8 waves of 64x64) is fastest whenever it still gives at
+// least one tile per CU; otherwise 128x128 (8 waves of 32x64) if that fills
+// the CUs, otherwise 128x64 (the most tiles).  Unaligned shapes, or shapes
+// the tiles do not divide, take the bounds-guarded 64x64 tile.
 const GemmConfig& choose_gemm(forge_runtime* rt, size_t M, size_t N, size_t K, bool aligned) {
-    (void)rt;
     auto fits = [&](const GemmConfig& c) {
         return aligned && M % c.bm == 0 && N % c.bn == 0 && K % c.bk == 0;
     };
-    if (fits(kFast128)) return kFast128;
-    if (fits(kFast128x64)) return kFast128x64;
+    auto tiles = [&](const GemmConfig& c) { return (M / c.bm) * (N / c.bn); };
+    const size_t cus = rt->cu_count > 0 ? (size_t)rt->cu_count : 256;
+    if (fits(kTile256x128) && tiles(kTile256x128) >= cus) return kTile256x128;
+    if (fits(kTile128x128) && tiles(kTile128x128) >= cus) return kTile128x128;
+    if (fits(kTile128x64)) return kTile128x64;
     return kGuard64;
 }
 
@@ -596,7 +599,7 @@ forge_status gemm_dispatch(forge_runtime* rt, forge_stream* s, int ta, int tb, f
              epi ? "_e" : "");
     unsigned tiles = (unsigned)(((M + cfg.bm - 1) / cfg.bm) * ((N + cfg.bn - 1) / cfg.bn));
     void* args[] = {&a};
-    return launch(rt, s, name, dim3(tiles), dim3(256), 0, args);
+    return launch(rt, s, name, dim3(tiles), dim3(cfg.threads), 0, args);
 }
 
 const char* binop_name(forge_binary_op op) {
@@ -634,21 +637,31 @@ int row_vpt(size_t cols, bool aligned) {
     return 0;
 }
 
-// Column sums of m [rows, cols] into out [cols] with one or two launches of
-// forge_sum_cols: chunks of at least 16 rows are summed into partial rows,
-// then the partial rows are summed.  Chunking depends only on the shape, so
-// the result is deterministic.
-size_t sum_cols_chunks(size_t rows, size_t cols) {
-    size_t gx = (cols + EW_THREADS - 1) / EW_THREADS;
+// Column sums of m [rows, cols] into out [cols].  Matrices of at most 256
+// rows take one launch of forge_sum_cols_final; taller ones first reduce
+// chunks of rows into partial rows (forge_sum_cols_v/_s, about 2048
+// workgroups, >= 16 rows per chunk), then sum the partial rows with
+// forge_sum_cols_final.  The chunking depends only on the shape, so the
+// result is deterministic.
+constexpr int SUMCOL_FINAL_MAX_ROWS = 256;
+
+size_t sum_cols_chunks(size_t rows, size_t cols, bool vec) {
+    if (rows <= (size_t)SUMCOL_FINAL_MAX_ROWS) return 1;
+    size_t per_block = vec ? 256 : 64;
+    size_t gx = (cols + per_block - 1) / per_block;
     size_t want = std::max<size_t>(1, 2048 / std::max<size_t>(1, gx));
     size_t by_rows = (rows + 15) / 16;
-    return std::max<size_t>(1, std::min(want, by_rows));
+    return std::max<size_t>(2, std::min(want, std::min(by_rows, (size_t)SUMCOL_FINAL_MAX_ROWS)));
 }
+
+bool sum_cols_vec(const float* m, size_t cols) { return aligned16(m) && cols % 4 == 0; }
 
 // Floats of scratch sum_cols_impl needs for this shape.
 size_t sum_cols_scratch(size_t rows, size_t cols) {
-    size_t chunks = sum_cols_chunks(rows, cols);
-    return chunks > 1 ? chunks * cols : 0;
+    size_t chunks = sum_cols_chunks(rows, cols, true);
+    size_t chunks_s = sum_cols_chunks(rows, cols, false);
+    size_t c = std::max(chunks, chunks_s);
+    return c > 1 ? c * cols : 0;
 }
 
 // scratch: sum_cols_scratch(rows, cols) floats that do not overlap m/out.
@@ -656,19 +669,33 @@ forge_status sum_cols_impl(forge_runtime* rt, forge_stream* s, const float* m, f
                            size_t rows, size_t cols, float* scratch) {
     if (cols == 0) return FORGE_OK;
     int c = (int)cols;
-    unsigned gx = (unsigned)((cols + EW_THREADS - 1) / EW_THREADS);
-    size_t chunks = sum_cols_chunks(rows, cols);
-    int rpc = (int)std::max<size_t>(1, (rows + chunks - 1) / chunks);
-    chunks = rows == 0 ? 1 : (rows + rpc - 1) / rpc;
+    unsigned gfinal = (unsigned)((cols + 63) / 64);
+    const bool vec = sum_cols_vec(m, cols);
+    size_t chunks = sum_cols_chunks(rows, cols, vec);
+    if (chunks == 1) {
+        int r = (int)rows;
+        return launch_args(rt, s, "forge_sum_cols_final", dim3(gfinal), dim3(1024), 0, m, out, r, c);
+    }
+    int rpc = (int)((rows + chunks - 1) / chunks);
+    chunks = (rows + rpc - 1) / rpc;
     int r = (int)rows;
-    if (chunks == 1)
-        return launch_args(rt, s, "forge_sum_cols", dim3(gx, 1), dim3(EW_THREADS), 0, m, out, r, c,
-                           rpc);
-    FORGE_TRY(launch_args(rt, s, "forge_sum_cols", dim3(gx, (unsigned)chunks), dim3(EW_THREADS),
-                          0, m, scratch, r, c, rpc));
+    unsigned gx = (unsigned)((cols + (vec ? 255 : 63)) / (vec ? 256 : 64));
+    FORGE_TRY(launch_args(rt, s, vec ? "forge_sum_cols_v" : "forge_sum_cols_s",
+                          dim3(gx, (unsigned)chunks), dim3(256), 0, m, scratch, r, c, rpc));
     int ch = (int)chunks;
-    return launch_args(rt, s, "forge_sum_cols", dim3(gx, 1), dim3(EW_THREADS), 0,
-                       (const float*)scratch, out, ch, c, ch);
+    return launch_args(rt, s, "forge_sum_cols_final", dim3(gfinal), dim3(1024), 0,
+                       (const float*)scratch, out, ch, c);
+}
+
+// Workgroups of the dgamma/dbeta partial pass of the norm backward kernels:
+// $OXFORGE_NORM_BWD_BLOCKS when set (a tuning knob), else the CU count.
+unsigned norm_bwd_blocks(forge_runtime* rt) {
+    static const long env = [] {
+        const char* v = getenv("OXFORGE_NORM_BWD_BLOCKS");
+        return v ? strtol(v, nullptr, 10) : 0L;
+    }();
+    if (env > 0) return (unsigned)env;
+    return (unsigned)std::max(64, rt->cu_count);
 }
 
 // Shared launcher of the six row kernels.  For the norm backward kernels
@@ -694,7 +721,7 @@ forge_status row_launch(forge_runtime* rt, forge_stream* s, const char* op, RowA
     float* ws = nullptr;
     if (partials) {
         // One partial row per workgroup (register path) or per wave (loop).
-        grid = std::min<unsigned>(blocks_needed, (unsigned)std::max(64, rt->cu_count));
+        grid = std::min<unsigned>(blocks_needed, norm_bwd_blocks(rt));
         prow = vpt ? grid : (size_t)grid * ROW_WAVES;
         size_t per = prow * (size_t)a.cols;
         FORGE_TRY(workspace(rt, s, per * 2 + sum_cols_scratch(prow, (size_t)a.cols), &ws));

@@ -64,9 +64,9 @@ def dispatcher_kernel_names():
     """Every kernel name runtime.cpp can build (mirrors its naming rules)."""
     names = []
     for ab in ("nn", "nt", "tn", "tt"):
-        for tag in ("128x128x16_2x2", "128x64x16_2x2", "256x128x16_2x2", "64x64x16_2x2_g"):
+        for tag in ("256x128x16_4x2", "128x128x16_4x2", "128x64x16_2x2", "64x64x16_2x2_g"):
             names.append(f"forge_gemm_{ab}_{tag}_e")
-    for tag in ("128x128x16_2x2", "128x64x16_2x2", "64x64x16_2x2_g"):
+    for tag in ("256x128x16_4x2", "128x128x16_4x2", "128x64x16_2x2", "64x64x16_2x2_g"):
         names.append(f"forge_gemm_nn_{tag}")
     for op in ("softmax", "layer_norm", "rms_norm", "softmax_bwd", "layer_norm_bwd", "rms_norm_bwd"):
         for v in (1, 2, 4, 8, 16):
@@ -85,7 +85,7 @@ def dispatcher_kernel_names():
     names += ["forge_fill_random", "forge_act_backward_v", "forge_act_backward_s",
               "forge_count_neq"]
     names += ["forge_fill_v", "forge_fill_s", "forge_fill_seq", "forge_causal_mask",
-              "forge_sum_cols", "forge_sum_rows_v", "forge_sum_rows_s", "forge_reduce_sum",
+              "forge_sum_cols_v", "forge_sum_cols_s", "forge_sum_cols_final", "forge_sum_rows_v", "forge_sum_rows_s", "forge_reduce_sum",
               "forge_reduce_max", "forge_transpose", "forge_transpose_g"]
     return names
 
