@@ -69,14 +69,18 @@ def time_launches(rt, fn, steps: int, warmup: int, stream=None) -> float:
 
 
 def load_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
-    summary (profiles/traffic.json), scaled by the copy-kernel calibration
-    factor recorded there; None if it has not been measured."""
+    """HBM-side bytes per launch of `kernel` from the committed rocprofv3
+    --pmc summary (profiles/traffic.json): FETCH_SIZE and WRITE_SIZE (KiB per
+    dispatch), each scaled by the factor a copy kernel of known size gives
+    that counter.  None if the kernel has not been measured."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
-        data = json.load(open(path))
+        with open(path) as f:
+            data = json.load(f)
         k = data["kernels"][kernel]
-        return int(round((k["fetch_kib"] + k["write_kib"]) * 1024 * data.get("copy_factor", 1.0)))
+        fetch = k["fetch_kib"] * 1024 * data["fetch_factor"]
+        write = k["write_kib"] * 1024 * data["write_factor"]
+        return int(round(fetch + write))
     except (OSError, KeyError, ValueError):
         return None
 
