@@ -11,6 +11,10 @@
 
 namespace forge {
 
+// Every kernel here is launched with exactly EW_THREADS threads per
+// workgroup, and the bodies use the constant rather than blockDim.x: on
+// gfx950 blockDim.x is read from the dispatch packet by a vector memory load
+// that every wave waits for before it can form its first address.
 constexpr int EW_THREADS = 256;
 
 // ---------------------------------------------------------------- binary
@@ -19,13 +23,13 @@ template <int OP, bool VEC>
 __device__ __forceinline__ void binary_body(const float* __restrict__ l,
                                             const float* __restrict__ r,
                                             float* __restrict__ o, long long n) {
-    const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long long stride = (long long)gridDim.x * blockDim.x;
+    const long long tid = (long long)blockIdx.x * EW_THREADS + threadIdx.x;
+    const long long stride = (long long)gridDim.x * EW_THREADS;
     if constexpr (VEC) {
         const long long n4 = n / 4;
         for (long long i = tid; i < n4; i += stride) {
-            const float4 a = reinterpret_cast<const float4*>(l)[i];
-            const float4 b = reinterpret_cast<const float4*>(r)[i];
+            const float4 a = load_stream(l + 4 * i);
+            const float4 b = load_stream(r + 4 * i);
             float4 c;
             c.x = apply_binary<OP>(a.x, b.x);
             c.y = apply_binary<OP>(a.y, b.y);
@@ -44,13 +48,13 @@ __device__ __forceinline__ void binary_body(const float* __restrict__ l,
 template <int OP, bool VEC>
 __device__ __forceinline__ void binary_assign_body(float* t, const float* r,
                                                    long long n) {
-    const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long long stride = (long long)gridDim.x * blockDim.x;
+    const long long tid = (long long)blockIdx.x * EW_THREADS + threadIdx.x;
+    const long long stride = (long long)gridDim.x * EW_THREADS;
     if constexpr (VEC) {
         const long long n4 = n / 4;
         for (long long i = tid; i < n4; i += stride) {
-            float4 a = reinterpret_cast<float4*>(t)[i];
-            const float4 b = reinterpret_cast<const float4*>(r)[i];
+            float4 a = load_stream(t + 4 * i);
+            const float4 b = load_stream(r + 4 * i);
             a.x = apply_binary<OP>(a.x, b.x);
             a.y = apply_binary<OP>(a.y, b.y);
             a.z = apply_binary<OP>(a.z, b.z);
@@ -71,12 +75,12 @@ template <int OP, bool VEC>
 __device__ __forceinline__ void by_rows_body(float* m, const float* __restrict__ row,
                                              int rows, int cols) {
     if constexpr (VEC) {
-        const int c4 = blockIdx.x * blockDim.x + threadIdx.x;
+        const int c4 = blockIdx.x * EW_THREADS + threadIdx.x;
         if (c4 * 4 >= cols) return;
         const float4 b = reinterpret_cast<const float4*>(row)[c4];
         for (int r = blockIdx.y; r < rows; r += gridDim.y) {
             float4* p = reinterpret_cast<float4*>(m + (long long)r * cols) + c4;
-            float4 a = *p;
+            float4 a = load_stream(m + (long long)r * cols + 4 * c4);
             a.x = apply_binary<OP>(a.x, b.x);
             a.y = apply_binary<OP>(a.y, b.y);
             a.z = apply_binary<OP>(a.z, b.z);
@@ -84,7 +88,7 @@ __device__ __forceinline__ void by_rows_body(float* m, const float* __restrict__
             *p = a;
         }
     } else {
-        const int c = blockIdx.x * blockDim.x + threadIdx.x;
+        const int c = blockIdx.x * EW_THREADS + threadIdx.x;
         if (c >= cols) return;
         const float b = row[c];
         for (int r = blockIdx.y; r < rows; r += gridDim.y) {
@@ -119,12 +123,12 @@ __device__ __forceinline__ float map_one(float x, float p0) {
 
 template <int OP, bool VEC>
 __device__ __forceinline__ void map_body(float* x, long long n, float p0) {
-    const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long long stride = (long long)gridDim.x * blockDim.x;
+    const long long tid = (long long)blockIdx.x * EW_THREADS + threadIdx.x;
+    const long long stride = (long long)gridDim.x * EW_THREADS;
     if constexpr (VEC) {
         const long long n4 = n / 4;
         for (long long i = tid; i < n4; i += stride) {
-            float4 a = reinterpret_cast<float4*>(x)[i];
+            float4 a = load_stream(x + 4 * i);
             a.x = map_one<OP>(a.x, p0);
             a.y = map_one<OP>(a.y, p0);
             a.z = map_one<OP>(a.z, p0);
@@ -141,8 +145,8 @@ __device__ __forceinline__ void map_body(float* x, long long n, float p0) {
 
 template <bool VEC>
 __device__ __forceinline__ void fill_body(float* x, long long n, float v) {
-    const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long long stride = (long long)gridDim.x * blockDim.x;
+    const long long tid = (long long)blockIdx.x * EW_THREADS + threadIdx.x;
+    const long long stride = (long long)gridDim.x * EW_THREADS;
     if constexpr (VEC) {
         const long long n4 = n / 4;
         const float4 f = make_float4(v, v, v, v);
@@ -155,8 +159,8 @@ __device__ __forceinline__ void fill_body(float* x, long long n, float v) {
 
 // elementwise.rs:23-34: index as f32 (ascending) or (len - index) as f32.
 __device__ __forceinline__ void fill_seq_body(float* x, long long n, int ascending) {
-    const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long long stride = (long long)gridDim.x * blockDim.x;
+    const long long tid = (long long)blockIdx.x * EW_THREADS + threadIdx.x;
+    const long long stride = (long long)gridDim.x * EW_THREADS;
     for (long long i = tid; i < n; i += stride)
         x[i] = ascending ? (float)(unsigned long long)i
                          : (float)(unsigned long long)(n - i);
@@ -172,8 +176,8 @@ __device__ __forceinline__ uint32_t forge_hash(uint32_t x) {
 }
 
 __device__ __forceinline__ void fill_random_body(float* x, long long n, uint32_t seed) {
-    const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long long stride = (long long)gridDim.x * blockDim.x;
+    const long long tid = (long long)blockIdx.x * EW_THREADS + threadIdx.x;
+    const long long stride = (long long)gridDim.x * EW_THREADS;
     for (long long i = tid; i < n; i += stride)
         x[i] = (float)forge_hash(seed + (uint32_t)i) / (float)4294967295u;
 }
@@ -184,13 +188,13 @@ template <bool VEC>
 __device__ __forceinline__ void act_backward_body(const float* __restrict__ dy,
                                                   const float* __restrict__ z,
                                                   float* __restrict__ g, long long n, int act) {
-    const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long long stride = (long long)gridDim.x * blockDim.x;
+    const long long tid = (long long)blockIdx.x * EW_THREADS + threadIdx.x;
+    const long long stride = (long long)gridDim.x * EW_THREADS;
     if constexpr (VEC) {
         const long long n4 = n / 4;
         for (long long i = tid; i < n4; i += stride) {
-            const float4 a = reinterpret_cast<const float4*>(dy)[i];
-            const float4 b = reinterpret_cast<const float4*>(z)[i];
+            const float4 a = load_stream(dy + 4 * i);
+            const float4 b = load_stream(z + 4 * i);
             float4 c;
             c.x = a.x * activate_derivative(act, b.x);
             c.y = a.y * activate_derivative(act, b.y);
@@ -212,8 +216,8 @@ __device__ __forceinline__ void count_neq_body(const float* __restrict__ l,
                                                const float* __restrict__ r, long long n,
                                                float* __restrict__ out) {
     __shared__ float part[EW_THREADS / 64];
-    const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long long stride = (long long)gridDim.x * blockDim.x;
+    const long long tid = (long long)blockIdx.x * EW_THREADS + threadIdx.x;
+    const long long stride = (long long)gridDim.x * EW_THREADS;
     float acc = 0.0f;
     for (long long i = tid; i < n; i += stride) acc += (l[i] == r[i]) ? 0.0f : 1.0f;
     acc = wave_sum(acc);
@@ -221,7 +225,7 @@ __device__ __forceinline__ void count_neq_body(const float* __restrict__ l,
     __syncthreads();
     if (threadIdx.x == 0) {
         float t = part[0];
-        for (int w = 1; w < (int)(blockDim.x >> 6); w++) t += part[w];
+        for (int w = 1; w < (EW_THREADS >> 6); w++) t += part[w];
         out[blockIdx.x] = t;
     }
 }
@@ -229,8 +233,8 @@ __device__ __forceinline__ void count_neq_body(const float* __restrict__ l,
 // row.rs:5-14: M[r, c] = -inf for c > r.
 __device__ __forceinline__ void causal_mask_body(float* m, int rows, int cols) {
     for (int r = blockIdx.y; r < rows; r += gridDim.y)
-        for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < cols;
-             c += gridDim.x * blockDim.x)
+        for (int c = blockIdx.x * EW_THREADS + threadIdx.x; c < cols;
+             c += gridDim.x * EW_THREADS)
             if (c > r) m[(long long)r * cols + c] = -INFINITY;
 }
 
@@ -293,7 +297,7 @@ __device__ __forceinline__ void sum_cols_final_body(const float* __restrict__ m,
     const int c = blockIdx.x * 64 + lane;
     float acc = 0.0f;
     if (c < cols) {
-#pragma unroll 4
+#pragma unroll 8
         for (int r = wave; r < rows; r += SUMCOL_FINAL_WAVES) acc += m[(long long)r * cols + c];
     }
     part[wave][lane] = acc;
@@ -312,7 +316,7 @@ __device__ __forceinline__ void sum_rows_body(const float* __restrict__ m,
                                               int cols) {
     const int lane = lane_id();
     const int wave = threadIdx.x >> 6;
-    const int waves = blockDim.x >> 6;
+    constexpr int waves = EW_THREADS >> 6;
     for (int r = blockIdx.x * waves + wave; r < rows; r += gridDim.x * waves) {
         const float* p = m + (long long)r * cols;
         float s = 0.0f;
@@ -336,8 +340,8 @@ template <bool IS_MAX>
 __device__ __forceinline__ void reduce_body(const float* __restrict__ x, long long n,
                                             float* __restrict__ out) {
     __shared__ float part[EW_THREADS / 64];
-    const long long tid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long long stride = (long long)gridDim.x * blockDim.x;
+    const long long tid = (long long)blockIdx.x * EW_THREADS + threadIdx.x;
+    const long long stride = (long long)gridDim.x * EW_THREADS;
     float acc = IS_MAX ? -FLT_MAX : 0.0f;
     for (long long i = tid; i < n; i += stride)
         acc = IS_MAX ? fmaxf(acc, x[i]) : acc + x[i];
@@ -347,7 +351,7 @@ __device__ __forceinline__ void reduce_body(const float* __restrict__ x, long lo
     __syncthreads();
     if (threadIdx.x == 0) {
         float t = part[0];
-        for (int w = 1; w < (int)(blockDim.x >> 6); w++)
+        for (int w = 1; w < (EW_THREADS >> 6); w++)
             t = IS_MAX ? fmaxf(t, part[w]) : t + part[w];
         out[blockIdx.x] = t;
     }

@@ -73,8 +73,7 @@ __device__ __forceinline__ void gemm_tile_coords(int num_m, int num_n,
 // Loads a ROWS x COLS tile (COLS contiguous in global memory) into registers,
 // COLS/4 four-float vectors per row, dealt over NT threads.  GUARD zero-fills
 // outside [vr, vc) and uses scalar loads (no alignment assumption).  The
-// staging registers are a native 4-float vector so they stay in VGPRs.
-typedef float f4 __attribute__((ext_vector_type(4)));
+// staging registers are the native 4-float vector f4 so they stay in VGPRs.
 
 template <int ROWS, int COLS, int NT>
 struct TileShape {

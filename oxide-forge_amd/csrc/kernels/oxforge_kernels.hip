@@ -58,12 +58,20 @@ GEMM_KERNEL(forge_gemm_nn_64x64x16_2x2_g, 64, 64, 16, 2, 2, false, false, true, 
     ROW_KERNEL(forge_row_##OPNAME##_v8, OP, 8, false)             \
     ROW_KERNEL(forge_row_##OPNAME##_v16, OP, 16, false)           \
     FORGE_KERNEL void __launch_bounds__(256) forge_row_##OPNAME##_loop(RowArgs a) { row_kernel_loop<OP>(a); }
-// Norm backward instances that also emit per-workgroup dgamma/dbeta partials.
+// Norm backward instances that also emit per-workgroup dgamma/dbeta
+// partials: 16 waves per workgroup (8 for the 8-float4 rows, whose
+// registers allow two waves per SIMD), so one partial row covers many rows
+// without each wave walking several rows.  The runtime launches them with
+// row_partial_waves(vpt) * 64 threads.
+#define ROW_PARTIAL_KERNEL(NAME, OP, VPT, WAVES)                                  \
+    FORGE_KERNEL void __launch_bounds__(WAVES * 64) NAME(RowArgs a) {             \
+        row_kernel_reg<OP, VPT, true, WAVES>(a);                                  \
+    }
 #define ROW_PARTIAL_KERNELS(OPNAME, OP)                           \
-    ROW_KERNEL(forge_row_##OPNAME##_v1_p, OP, 1, true)            \
-    ROW_KERNEL(forge_row_##OPNAME##_v2_p, OP, 2, true)            \
-    ROW_KERNEL(forge_row_##OPNAME##_v4_p, OP, 4, true)            \
-    ROW_KERNEL(forge_row_##OPNAME##_v8_p, OP, 8, true)
+    ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v1_p, OP, 1, 16)      \
+    ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v2_p, OP, 2, 16)      \
+    ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v4_p, OP, 4, 16)      \
+    ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v8_p, OP, 8, 8)
 
 ROW_KERNELS(softmax, ROW_SOFTMAX)
 ROW_KERNELS(layer_norm, ROW_LAYER_NORM)
@@ -154,6 +162,13 @@ FORGE_KERNEL void __launch_bounds__(SUMCOL_FINAL_WAVES * 64) forge_sum_cols_fina
                                                                                  float* out,
                                                                                  int rows, int cols) {
     sum_cols_final_body(m, out, rows, cols);
+}
+// Two independent column sums in one launch (blockIdx.y selects the pair):
+// dgamma and dbeta of the LayerNorm backward.
+FORGE_KERNEL void __launch_bounds__(SUMCOL_FINAL_WAVES * 64) forge_sum_cols_final2(
+    const float* m0, float* out0, const float* m1, float* out1, int rows, int cols) {
+    if (blockIdx.y == 0) sum_cols_final_body(m0, out0, rows, cols);
+    else sum_cols_final_body(m1, out1, rows, cols);
 }
 FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_sum_rows_v(const float* m, float* out, int rows,
                                                                  int cols) {

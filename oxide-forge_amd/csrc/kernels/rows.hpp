@@ -45,6 +45,17 @@ enum RowOp {
 };
 
 __device__ __forceinline__ float sum4(float4 a) { return (a.x + a.y) + (a.z + a.w); }
+
+// exp(x - m) of the softmax as 2^((x - m) * log2 e) on v_exp_f32, with the
+// row normalised by one reciprocal and a multiply per element.  Softmax is
+// VALU-bound otherwise on gfx950 (a wave64 VALU instruction takes 4 cycles
+// and the IEEE expf and divide cost about 25 of them per element).  The
+// error against exact arithmetic is below 2e-6 relative for |x - m| < 30 and
+// the result is at most 1e-13 below that range; masked -inf entries give 0.
+__device__ __forceinline__ float softmax_exp(float x, float m) {
+    constexpr float LOG2E = 1.44269504088896341f;
+    return __builtin_amdgcn_exp2f((x - m) * LOG2E);
+}
 __device__ __forceinline__ float max4(float4 a) {
     return fmaxf(fmaxf(a.x, a.y), fmaxf(a.z, a.w));
 }
@@ -53,7 +64,8 @@ __device__ __forceinline__ float max4(float4 a) {
     do { dst.x = (EXPR_X); dst.y = (EXPR_Y); dst.z = (EXPR_Z); dst.w = (EXPR_W); } while (0)
 
 // Loads row `row` into the register arrays of the register path (fill
-// values past cols: -FLT_MAX for softmax, 0 otherwise).
+// values past cols: -FLT_MAX for softmax, 0 otherwise).  Streaming loads:
+// the forward kernels overwrite the row in place.
 template <int OP, int VPT, bool BWD>
 __device__ __forceinline__ void row_load(const RowArgs& a, int row, int lane, float4* v,
                                          float4* g) {
@@ -63,25 +75,52 @@ __device__ __forceinline__ void row_load(const RowArgs& a, int row, int lane, fl
     for (int i = 0; i < VPT; i++) {
         const int c = (i * 64 + lane) * 4;
         const bool ok = c < a.cols;
-        v[i] = ok ? *reinterpret_cast<const float4*>(a.x + base + c)
-                  : make_float4(fill, fill, fill, fill);
+        v[i] = ok ? load_stream(a.x + base + c) : make_float4(fill, fill, fill, fill);
         if constexpr (BWD)
-            g[i] = ok ? *reinterpret_cast<const float4*>(a.dy + base + c)
-                      : make_float4(0.f, 0.f, 0.f, 0.f);
+            g[i] = ok ? load_stream(a.dy + base + c) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 }
 
 // Register path.  VPT float4 per lane; lane l holds columns
-// 4*(64*i + l) .. +3 for i < VPT.  The partial-producing backward kernels
+// 4*(64*i + l) .. +3 for i < VPT.  WAVES wavefronts per workgroup, rows
+// grid-stride.  The partial-producing backward kernels with at most 8 waves
 // walk several rows per wave, so they prefetch the next row's registers
 // before reducing the current one.
-template <int OP, int VPT, bool PARTIALS>
+template <int OP, int VPT, bool PARTIALS, int WAVES = ROW_WAVES>
 __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
     const int lane = lane_id();
     const int wave = threadIdx.x >> 6;
     const int cols = a.cols;
     const float n = (float)cols;
     constexpr bool BWD = OP >= ROW_SOFTMAX_BWD;
+    constexpr bool USES_GAMMA = OP == ROW_LAYER_NORM || OP == ROW_RMS_NORM ||
+                                OP == ROW_LAYER_NORM_BWD || OP == ROW_RMS_NORM_BWD;
+    constexpr bool USES_BETA = OP == ROW_LAYER_NORM;
+    // gamma/beta are the same for every row: load them once, before the first
+    // row's reductions, so their latency is not exposed per row.
+    constexpr bool PRELOAD = USES_GAMMA && VPT <= 8;
+    float4 gm[PRELOAD ? VPT : 1], bt[(PRELOAD && USES_BETA) ? VPT : 1];
+    if constexpr (PRELOAD) {
+#pragma unroll
+        for (int i = 0; i < VPT; i++) {
+            const int c = (i * 64 + lane) * 4;
+            const bool in = c < cols;
+            gm[i] = (a.gamma && in) ? *reinterpret_cast<const float4*>(a.gamma + c)
+                                    : make_float4(1.f, 1.f, 1.f, 1.f);
+            if constexpr (USES_BETA)
+                bt[i] = (a.beta && in) ? *reinterpret_cast<const float4*>(a.beta + c)
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    // gamma / beta of float4 column group i (preloaded, or read per use).
+    auto gamma4 = [&](int i) -> float4 {
+        if constexpr (PRELOAD) return gm[i];
+        else return *reinterpret_cast<const float4*>(a.gamma + (i * 64 + lane) * 4);
+    };
+    auto beta4 = [&](int i) -> float4 {
+        if constexpr (PRELOAD && USES_BETA) return bt[i];
+        else return *reinterpret_cast<const float4*>(a.beta + (i * 64 + lane) * 4);
+    };
     static_assert(!PARTIALS || OP == ROW_LAYER_NORM_BWD || OP == ROW_RMS_NORM_BWD,
                   "only the norm backward kernels produce column partials");
 
@@ -94,9 +133,12 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
         }
     }
 
-    constexpr bool PREFETCH = PARTIALS;
-    const int stride = gridDim.x * ROW_WAVES;
-    int row = blockIdx.x * ROW_WAVES + wave;
+    // Prefetch the next row when a wave walks several rows; the 16-wave
+    // instances (one row per wave at the usual shapes) would exceed the 128
+    // VGPRs a 1024-thread workgroup allows.
+    constexpr bool PREFETCH = PARTIALS && WAVES <= 8;
+    const int stride = gridDim.x * WAVES;
+    int row = blockIdx.x * WAVES + wave;
     float4 nv[PREFETCH ? VPT : 1], ng[(PREFETCH && BWD) ? VPT : 1];
     if (PREFETCH && row < a.rows) row_load<OP, VPT, BWD>(a, row, lane, nv, ng);
     for (; row < a.rows; row += stride) {
@@ -117,7 +159,7 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
         }
 
         if constexpr (OP == ROW_SOFTMAX) {
-            // row.rs:64-112: max, exp(x - max), sum, divide.
+            // row.rs:64-112: max, exp(x - max), sum, normalise.
             float m = -FLT_MAX;
 #pragma unroll
             for (int i = 0; i < VPT; i++) m = fmaxf(m, max4(v[i]));
@@ -126,17 +168,17 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
 #pragma unroll
             for (int i = 0; i < VPT; i++) {
                 if (ok[i]) {
-                    F4_APPLY(v[i], v[i], expf(v[i].x - m), expf(v[i].y - m),
-                             expf(v[i].z - m), expf(v[i].w - m));
+                    F4_APPLY(v[i], v[i], softmax_exp(v[i].x, m), softmax_exp(v[i].y, m),
+                             softmax_exp(v[i].z, m), softmax_exp(v[i].w, m));
                     s += sum4(v[i]);
                 }
             }
-            s = wave_sum(s);
+            const float inv = 1.0f / wave_sum(s);
 #pragma unroll
             for (int i = 0; i < VPT; i++) {
                 if (ok[i]) {
                     float4 o;
-                    F4_APPLY(o, v[i], v[i].x / s, v[i].y / s, v[i].z / s, v[i].w / s);
+                    F4_APPLY(o, v[i], v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv);
                     *reinterpret_cast<float4*>(a.y + base + (i * 64 + lane) * 4) = o;
                 }
             }
@@ -167,12 +209,12 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                     F4_APPLY(o, v[i], v[i].x * rstd, v[i].y * rstd, v[i].z * rstd,
                              v[i].w * rstd);
                     if (a.gamma) {
-                        const float4 gm = *reinterpret_cast<const float4*>(a.gamma + c);
-                        F4_APPLY(o, o, o.x * gm.x, o.y * gm.y, o.z * gm.z, o.w * gm.w);
+                        const float4 g4 = gamma4(i);
+                        F4_APPLY(o, o, o.x * g4.x, o.y * g4.y, o.z * g4.z, o.w * g4.w);
                     }
                     if (a.beta) {
-                        const float4 bt = *reinterpret_cast<const float4*>(a.beta + c);
-                        F4_APPLY(o, o, o.x + bt.x, o.y + bt.y, o.z + bt.z, o.w + bt.w);
+                        const float4 b4 = beta4(i);
+                        F4_APPLY(o, o, o.x + b4.x, o.y + b4.y, o.z + b4.z, o.w + b4.w);
                     }
                     *reinterpret_cast<float4*>(a.y + base + c) = o;
                 }
@@ -188,7 +230,7 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                     const int c = (i * 64 + lane) * 4;
                     float4 gg = g[i];
                     if (a.gamma) {
-                        const float4 gm = *reinterpret_cast<const float4*>(a.gamma + c);
+                        const float4 gm = gamma4(i);
                         F4_APPLY(gg, g[i], g[i].x * gm.x, g[i].y * gm.y, g[i].z * gm.z,
                                  g[i].w * gm.w);
                     }
@@ -205,7 +247,7 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                     const int c = (i * 64 + lane) * 4;
                     float4 gg = g[i];
                     if (a.gamma) {
-                        const float4 gm = *reinterpret_cast<const float4*>(a.gamma + c);
+                        const float4 gm = gamma4(i);
                         F4_APPLY(gg, g[i], g[i].x * gm.x, g[i].y * gm.y, g[i].z * gm.z,
                                  g[i].w * gm.w);
                     }
@@ -240,7 +282,7 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                 float4 o;
                 F4_APPLY(o, v[i], v[i].x / rms, v[i].y / rms, v[i].z / rms, v[i].w / rms);
                 if (a.gamma) {
-                    const float4 gm = *reinterpret_cast<const float4*>(a.gamma + c);
+                    const float4 gm = gamma4(i);
                     F4_APPLY(o, o, o.x * gm.x, o.y * gm.y, o.z * gm.z, o.w * gm.w);
                 }
                 *reinterpret_cast<float4*>(a.y + base + c) = o;
@@ -271,7 +313,7 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                 const int c = (i * 64 + lane) * 4;
                 float4 gg = g[i];
                 if (a.gamma && ok[i]) {
-                    const float4 gm = *reinterpret_cast<const float4*>(a.gamma + c);
+                    const float4 gm = gamma4(i);
                     F4_APPLY(gg, g[i], g[i].x * gm.x, g[i].y * gm.y, g[i].z * gm.z,
                              g[i].w * gm.w);
                 }
@@ -289,7 +331,7 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                 const int c = (i * 64 + lane) * 4;
                 float4 gg = g[i];
                 if (a.gamma) {
-                    const float4 gm = *reinterpret_cast<const float4*>(a.gamma + c);
+                    const float4 gm = gamma4(i);
                     F4_APPLY(gg, g[i], g[i].x * gm.x, g[i].y * gm.y, g[i].z * gm.z,
                              g[i].w * gm.w);
                 }
@@ -306,10 +348,10 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
     }
 
     if constexpr (PARTIALS) {
-        // Combine the ROW_WAVES waves of this workgroup in LDS, then write one
-        // partial row per workgroup.
+        // Combine the WAVES waves of this workgroup in LDS (in wave order), then
+        // write one partial row per workgroup.
         if (!a.pgamma && !a.pbeta) return;
-        extern __shared__ float4 red[];  // [ROW_WAVES][cols/4]
+        extern __shared__ float4 red[];  // [WAVES][cols/4]
         const int c4n = cols / 4;
         for (int pass = 0; pass < 2; pass++) {
             float* dst = pass == 0 ? a.pgamma : a.pbeta;
@@ -320,9 +362,9 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                 if (c4 < c4n) red[wave * c4n + c4] = pass == 0 ? pg[i] : pb[i];
             }
             __syncthreads();
-            for (int c4 = threadIdx.x; c4 < c4n; c4 += blockDim.x) {
+            for (int c4 = threadIdx.x; c4 < c4n; c4 += WAVES * 64) {
                 float4 t = red[c4];
-                for (int w = 1; w < ROW_WAVES; w++) {
+                for (int w = 1; w < WAVES; w++) {
                     const float4 u = red[w * c4n + c4];
                     t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
                 }
@@ -360,9 +402,9 @@ __device__ __forceinline__ void row_kernel_loop(const RowArgs& a) {
             for (int c = lane; c < cols; c += 64) m = fmaxf(m, x[c]);
             m = wave_max(m);
             float s = 0.0f;
-            for (int c = lane; c < cols; c += 64) s += expf(x[c] - m);
-            s = wave_sum(s);
-            for (int c = lane; c < cols; c += 64) y[c] = expf(x[c] - m) / s;
+            for (int c = lane; c < cols; c += 64) s += softmax_exp(x[c], m);
+            const float inv = 1.0f / wave_sum(s);
+            for (int c = lane; c < cols; c += 64) y[c] = softmax_exp(x[c], m) * inv;
         } else if constexpr (OP == ROW_LAYER_NORM || OP == ROW_LAYER_NORM_BWD) {
             float s = 0.0f;
             for (int c = lane; c < cols; c += 64) s += x[c];

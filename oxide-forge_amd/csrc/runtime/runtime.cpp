@@ -687,6 +687,10 @@ forge_status sum_cols_impl(forge_runtime* rt, forge_stream* s, const float* m, f
                        (const float*)scratch, out, ch, c);
 }
 
+// Waves per workgroup of the partial-producing register kernels
+// (forge_row_*_v<vpt>_p, instantiated with these counts).
+int row_partial_waves(int vpt) { return vpt <= 4 ? 16 : 8; }
+
 // Workgroups of the dgamma/dbeta partial pass of the norm backward kernels:
 // $OXFORGE_NORM_BWD_BLOCKS when set (a tuning knob), else the CU count.
 unsigned norm_bwd_blocks(forge_runtime* rt) {
@@ -714,7 +718,11 @@ forge_status row_launch(forge_runtime* rt, forge_stream* s, const char* op, RowA
     const bool partials = dgamma || dbeta;
     if (partials && vpt > 8) vpt = 0;  // register path with partials: <= 8 float4
     char name[80];
-    unsigned blocks_needed = (unsigned)((a.rows + ROW_WAVES - 1) / ROW_WAVES);
+    // Waves per workgroup: the register partial kernels use more waves so
+    // one partial row (LDS-combined) covers more rows; everything else uses
+    // ROW_WAVES.
+    const int waves = (partials && vpt) ? row_partial_waves(vpt) : ROW_WAVES;
+    unsigned blocks_needed = (unsigned)((a.rows + waves - 1) / waves);
     unsigned grid;
     size_t shmem = 0;
     size_t prow = 0;
@@ -727,7 +735,7 @@ forge_status row_launch(forge_runtime* rt, forge_stream* s, const char* op, RowA
         FORGE_TRY(workspace(rt, s, per * 2 + sum_cols_scratch(prow, (size_t)a.cols), &ws));
         a.pgamma = dgamma ? ws : nullptr;
         a.pbeta = dbeta ? ws + per : nullptr;
-        if (vpt) shmem = (size_t)ROW_WAVES * (size_t)a.cols * sizeof(float);
+        if (vpt) shmem = (size_t)waves * (size_t)a.cols * sizeof(float);
         if (vpt) snprintf(name, sizeof name, "forge_row_%s_v%d_p", op, vpt);
         else snprintf(name, sizeof name, "forge_row_%s_loop", op);
     } else {
@@ -735,9 +743,19 @@ forge_status row_launch(forge_runtime* rt, forge_stream* s, const char* op, RowA
         if (vpt) snprintf(name, sizeof name, "forge_row_%s_v%d", op, vpt);
         else snprintf(name, sizeof name, "forge_row_%s_loop", op);
     }
+    if (shmem > rt->lds_bytes)
+        return fail(FORGE_EINVAL, "row kernel needs %zu B of LDS, the device has %zu", shmem,
+                    rt->lds_bytes);
     void* args[] = {&a};
-    FORGE_TRY(launch(rt, s, name, dim3(grid), dim3(ROW_WAVES * 64), shmem, args));
+    FORGE_TRY(launch(rt, s, name, dim3(grid), dim3(waves * 64), shmem, args));
     float* chunk_scratch = ws ? ws + 2 * prow * (size_t)a.cols : nullptr;
+    if (dgamma && dbeta && sum_cols_chunks(prow, (size_t)a.cols, true) == 1) {
+        // Both column sums fit one final pass: one launch for the pair.
+        int r = (int)prow, c = a.cols;
+        unsigned gfinal = (unsigned)((a.cols + 63) / 64);
+        return launch_args(rt, s, "forge_sum_cols_final2", dim3(gfinal, 2), dim3(1024), 0,
+                           (const float*)a.pgamma, dgamma, (const float*)a.pbeta, dbeta, r, c);
+    }
     if (dgamma)
         FORGE_TRY(sum_cols_impl(rt, s, a.pgamma, dgamma, prow, (size_t)a.cols, chunk_scratch));
     if (dbeta)
