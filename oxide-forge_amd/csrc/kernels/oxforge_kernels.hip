@@ -59,19 +59,19 @@ GEMM_KERNEL(forge_gemm_nn_64x64x16_2x2_g, 64, 64, 16, 2, 2, false, false, true, 
     ROW_KERNEL(forge_row_##OPNAME##_v16, OP, 16, false)           \
     FORGE_KERNEL void __launch_bounds__(256) forge_row_##OPNAME##_loop(RowArgs a) { row_kernel_loop<OP>(a); }
 // Norm backward instances that also emit per-workgroup dgamma/dbeta
-// partials: 16 waves per workgroup (8 for the 8-float4 rows, whose
-// registers allow two waves per SIMD), so one partial row covers many rows
-// without each wave walking several rows.  The runtime launches them with
-// row_partial_waves(vpt) * 64 threads.
-#define ROW_PARTIAL_KERNEL(NAME, OP, VPT, WAVES)                                  \
-    FORGE_KERNEL void __launch_bounds__(WAVES * 64) NAME(RowArgs a) {             \
-        row_kernel_reg<OP, VPT, true, WAVES>(a);                                  \
+// partials: 8 waves per workgroup, each walking its rows with the next row
+// prefetched (measured on MI355X at [4096,1024]: 8 waves x 256 workgroups,
+// two rows per wave, beats 16 waves or one row per wave by 1.5-3 us).  The
+// runtime launches them with ROW_PARTIAL_WAVES * 64 threads.
+#define ROW_PARTIAL_KERNEL(NAME, OP, VPT)                                               \
+    FORGE_KERNEL void __launch_bounds__(ROW_PARTIAL_WAVES * 64) NAME(RowArgs a) {       \
+        row_kernel_reg<OP, VPT, true, ROW_PARTIAL_WAVES>(a);                            \
     }
 #define ROW_PARTIAL_KERNELS(OPNAME, OP)                           \
-    ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v1_p, OP, 1, 16)      \
-    ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v2_p, OP, 2, 16)      \
-    ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v4_p, OP, 4, 16)      \
-    ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v8_p, OP, 8, 8)
+    ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v1_p, OP, 1)          \
+    ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v2_p, OP, 2)          \
+    ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v4_p, OP, 4)          \
+    ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v8_p, OP, 8)
 
 ROW_KERNELS(softmax, ROW_SOFTMAX)
 ROW_KERNELS(layer_norm, ROW_LAYER_NORM)

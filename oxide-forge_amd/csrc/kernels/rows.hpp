@@ -20,7 +20,8 @@
 
 namespace forge {
 
-constexpr int ROW_WAVES = 4;  // wavefronts (rows in flight) per workgroup
+constexpr int ROW_WAVES = 4;          // wavefronts (rows in flight) per workgroup
+constexpr int ROW_PARTIAL_WAVES = 8;  // the same for the dgamma/dbeta partial kernels
 
 struct RowArgs {
     const float* x;      // input (forward: in/out when y == x)
@@ -133,9 +134,9 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
         }
     }
 
-    // Prefetch the next row when a wave walks several rows; the 16-wave
-    // instances (one row per wave at the usual shapes) would exceed the 128
-    // VGPRs a 1024-thread workgroup allows.
+    // Prefetch the next row when a wave walks several rows (the partial
+    // kernels, whose grid is capped at one workgroup per CU).  Wider
+    // workgroups would not leave the registers for it.
     constexpr bool PREFETCH = PARTIALS && WAVES <= 8;
     const int stride = gridDim.x * WAVES;
     int row = blockIdx.x * WAVES + wave;

@@ -80,6 +80,7 @@ struct RowArgs {
 };
 
 constexpr int ROW_WAVES = 4;   // rows.hpp ROW_WAVES
+constexpr int ROW_PARTIAL_WAVES = 8;  // rows.hpp ROW_PARTIAL_WAVES
 constexpr int EW_THREADS = 256;  // elementwise.hpp EW_THREADS
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -637,13 +638,14 @@ int row_vpt(size_t cols, bool aligned) {
     return 0;
 }
 
-// Column sums of m [rows, cols] into out [cols].  Matrices of at most 256
-// rows take one launch of forge_sum_cols_final; taller ones first reduce
+// Column sums of m [rows, cols] into out [cols].  Matrices of at most 512
+// rows take one launch of forge_sum_cols_final (about 3 us on MI355X up to
+// that height, latency-bound); taller ones first reduce
 // chunks of rows into partial rows (forge_sum_cols_v/_s, about 2048
 // workgroups, >= 16 rows per chunk), then sum the partial rows with
 // forge_sum_cols_final.  The chunking depends only on the shape, so the
 // result is deterministic.
-constexpr int SUMCOL_FINAL_MAX_ROWS = 256;
+constexpr int SUMCOL_FINAL_MAX_ROWS = 512;
 
 size_t sum_cols_chunks(size_t rows, size_t cols, bool vec) {
     if (rows <= (size_t)SUMCOL_FINAL_MAX_ROWS) return 1;
@@ -687,9 +689,6 @@ forge_status sum_cols_impl(forge_runtime* rt, forge_stream* s, const float* m, f
                        (const float*)scratch, out, ch, c);
 }
 
-// Waves per workgroup of the partial-producing register kernels
-// (forge_row_*_v<vpt>_p, instantiated with these counts).
-int row_partial_waves(int vpt) { return vpt <= 4 ? 16 : 8; }
 
 // Workgroups of the dgamma/dbeta partial pass of the norm backward kernels:
 // $OXFORGE_NORM_BWD_BLOCKS when set (a tuning knob), else the CU count.
@@ -718,10 +717,9 @@ forge_status row_launch(forge_runtime* rt, forge_stream* s, const char* op, RowA
     const bool partials = dgamma || dbeta;
     if (partials && vpt > 8) vpt = 0;  // register path with partials: <= 8 float4
     char name[80];
-    // Waves per workgroup: the register partial kernels use more waves so
-    // one partial row (LDS-combined) covers more rows; everything else uses
-    // ROW_WAVES.
-    const int waves = (partials && vpt) ? row_partial_waves(vpt) : ROW_WAVES;
+    // Waves per workgroup: the register partial kernels use ROW_PARTIAL_WAVES
+    // (one LDS-combined partial row per workgroup); everything else ROW_WAVES.
+    const int waves = (partials && vpt) ? ROW_PARTIAL_WAVES : ROW_WAVES;
     unsigned blocks_needed = (unsigned)((a.rows + waves - 1) / waves);
     unsigned grid;
     size_t shmem = 0;

@@ -331,7 +331,10 @@ def test_maps(rt, op, p0):
         assert np.all(np.abs(y - ref) <= 2e-6 + 2e-6 * np.abs(ref))
 
 
-@pytest.mark.parametrize("rows,cols", [(4096, 1024), (3, 7), (300, 33), (1, 1), (4096, 8192)])
+# Column sums take one pass up to 512 rows and two passes above: (512, 64)
+# and (513, 64) sit on either side, (600, 33) is the unaligned two-pass path.
+@pytest.mark.parametrize("rows,cols", [(4096, 1024), (3, 7), (300, 33), (600, 33), (512, 64),
+                                       (513, 64), (1, 1), (4096, 8192)])
 def test_sum_rows_cols(rt, rows, cols):
     say(f"sum rows/cols {rows}x{cols}")
     m = np.random.default_rng(rows).integers(-50, 51, (rows, cols)).astype(np.float32)
