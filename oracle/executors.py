@@ -5,7 +5,9 @@ TEST INFRASTRUCTURE ONLY: the parity checker for the HIP executors (the
 product never imports this).  Everything is evaluated in float64 from f32
 inputs, i.e. the exact mathematics of the reference's algorithm; pinned by
 central finite differences and closed-form special cases in
-tests/test_oracle_executors.py.  Reference files are under src/net/.
+tests/test_oracle_executors.py, and to 1e-11 by the PyTorch float64
+autograd known answers of tests/golden/ (tests/test_golden.py).  Reference
+files are under src/net/.
 """
 from __future__ import annotations
 

@@ -24,8 +24,10 @@
  *     transpose + sum_rows (linear.rs:267-272).
  *
  * Parity pinning of each function is described in the tests that exercise it
- * (tests/test_oracle_pins.py); there is no reference golden data (the
- * reference ships no tests) and the reference cannot be built here.
+ * (tests/test_oracle_pins.py: closed forms, invariants, finite differences,
+ * library routines; tests/test_golden.py: known answers from PyTorch float64
+ * autograd in tests/golden/).  The reference ships no test data and cannot be
+ * built here.
  */
 #ifndef OXFORGE_ORACLE_H
 #define OXFORGE_ORACLE_H
