@@ -11,7 +11,10 @@ rotating over >= 512 MiB of buffers so the 256 MiB MALL cannot serve them),
 and the transformer executors when built.
 
 The CPU baseline is the oracle (oracle/oxforge_oracle.c, f64-accumulate
-GEMM) on a bounded sample of the same workload, multithreaded on the host.
+GEMM) on a bounded sample of the same workload, multithreaded on the host;
+with the secondary figures, the transformer layer's host tokens/s (one C4
+forward and one C5 training step of oracle/executors.py in numpy float64)
+is reported beside the GPU's.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
        [--no-secondary] [--sweep]
@@ -239,6 +242,41 @@ def transformers(rt, orc, steps, warmup):
     return out
 
 
+def cpu_transformer_baseline(orc):
+    """The transformer layer on the host: oracle/executors.py (numpy float64
+    over the host BLAS, at most 16 threads), one full C4 forward and one full
+    C5 training step (forward + backward) on the same synthetic inputs as
+    the GPU runs.  A reported baseline, not the optimisation target."""
+    from threadpoolctl import threadpool_info, threadpool_limits
+
+    from oracle import executors as ex
+
+    threads = min(16, os.cpu_count() or 1)
+    out = {}
+    with threadpool_limits(limits=threads, user_api="blas"):
+        used = max([i["num_threads"] for i in threadpool_info() if i["user_api"] == "blas"],
+                   default=1)
+        S, H, F, O = 2048, 1024, 4096, 1024
+        p = transformer_params(orc, S, H, F, O, 4, False)
+        X = orc.normal((S, H), 4)
+        t0 = time.perf_counter()
+        ex.transformer_forward(p, X, ex.RMS)
+        c4 = time.perf_counter() - t0
+        S, H, F, O = 4096, 2048, 8192, 2048
+        p = transformer_params(orc, S, H, F, O, 5, True)
+        X, dY = orc.normal((S, H), 5), orc.normal((S, O), 6)
+        t0 = time.perf_counter()
+        _, cache = ex.transformer_forward(p, X, ex.LAYER)
+        ex.transformer_backward(p, cache, dY, ex.LAYER)
+        c5 = time.perf_counter() - t0
+    out["c4_inference_tokens_per_s"] = round(2048 / c4, 1)
+    out["c5_training_tokens_per_s"] = round(4096 / c5, 1)
+    out.update({"cores": used, "kind": "port",
+                "sample": f"one C4 forward ({c4:.1f} s) and one C5 training step ({c5:.1f} s) "
+                          f"of oracle/executors.py (numpy float64, {used} BLAS threads)"})
+    return out
+
+
 def sweep(rt, orc, steps, warmup):
     """Times every plain GEMM tile instance on the two C3 shapes."""
     import oxforge
@@ -416,6 +454,9 @@ def main() -> int:
     if not args.no_cpu:
         log("cpu baseline")
         line["cpu_baseline"] = cpu_baseline(orc, M, N, K)
+        if "secondary" in line:
+            log("cpu baseline: transformer layer")
+            line["secondary"]["cpu_baseline_transformer"] = cpu_transformer_baseline(orc)
     rt.close()
     print(json.dumps(line), flush=True)
     return 0
