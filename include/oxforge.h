@@ -258,6 +258,14 @@ forge_status forge_layer_norm_rows(forge_runtime *rt, forge_stream *stream,
                                    forge_slice x, forge_slice gamma,
                                    forge_slice beta, size_t rows, size_t cols,
                                    float eps);
+/* Matrix::layer_norm with the result written to y (y == x is the in-place
+ * call; otherwise y must not overlap x).  Lets a caller that keeps the
+ * pre-norm matrix skip the clone the reference makes first
+ * (attention.rs:258-281, encoder.rs:114-131). */
+forge_status forge_layer_norm_rows_out(forge_runtime *rt, forge_stream *stream,
+                                       forge_slice x, forge_slice y,
+                                       forge_slice gamma, forge_slice beta,
+                                       size_t rows, size_t cols, float eps);
 /* layer_norm_backward (norm.rs:103-127 -> row.rs:239-347).  dgamma/dbeta
  * ({NULL,0} to skip) receive column sums over all rows. */
 forge_status forge_layer_norm_bwd(forge_runtime *rt, forge_stream *stream,
@@ -269,6 +277,10 @@ forge_status forge_layer_norm_bwd(forge_runtime *rt, forge_stream *stream,
 forge_status forge_rms_norm_rows(forge_runtime *rt, forge_stream *stream,
                                  forge_slice x, forge_slice gamma, size_t rows,
                                  size_t cols, float eps);
+/* Matrix::rms_norm with the result written to y (as forge_layer_norm_rows_out). */
+forge_status forge_rms_norm_rows_out(forge_runtime *rt, forge_stream *stream,
+                                     forge_slice x, forge_slice y, forge_slice gamma,
+                                     size_t rows, size_t cols, float eps);
 /* rms_norm_backward (norm.rs:129-158 -> row.rs:398-468). */
 forge_status forge_rms_norm_bwd(forge_runtime *rt, forge_stream *stream,
                                 forge_slice x, forge_slice dy,
@@ -294,6 +306,13 @@ forge_status forge_binary_assign_by_rows(forge_runtime *rt,
 /* for_each (span.rs:261-279 -> elementwise.rs:70-79): x = f(x). */
 forge_status forge_map(forge_runtime *rt, forge_stream *stream, forge_slice x,
                        size_t n, forge_map_op op, float p0);
+
+/* The SGD step of a bias or norm parameter (linear.rs:385-390: clone the
+ * gradient, scale it by lr, subtract) in one pass: param = param - lr * grad,
+ * the same two roundings.  Bit-exact. */
+forge_status forge_sgd_update(forge_runtime *rt, forge_stream *stream,
+                              forge_slice param, forge_slice grad, size_t n,
+                              float lr);
 
 /* Linear::backward's derivative step (linear.rs:254-265: clone, map
  * activation.derivative, multiply) in one pass: g = dy * act'(z). */

@@ -314,6 +314,10 @@ public:
     // forward that also stores the pre-activation (nullptr to skip).
     Matrix forward_keep(const Matrix& input, const Matrix* residual, Matrix* pre_activation,
                         CudaRuntime& rt, const CudaStream* stream);
+    // forward into a caller-owned output (Linear::forward_on, linear.rs:145-155).
+    void forward_into(const Matrix& input, const Matrix* residual, Matrix& output,
+                      CudaRuntime& rt, const CudaStream* stream,
+                      Matrix* pre_activation = nullptr);
     // learn that also stores dW (and db) when given, for explicit gradients.
     void learn_keep(const Matrix& input, const Matrix& gradient, const Vector* bias_gradient,
                     float learning_rate, Matrix* weight_gradient, CudaRuntime& rt,
@@ -417,6 +421,8 @@ struct Normalization {
     std::optional<Vector> beta;   // LayerNorm only
     float eps = 1e-5f;            // norm.rs:45,66,123,153
     void forward(Matrix& m, CudaRuntime& rt) const;
+    // The same normalisation written to dst (dst == src is the in-place call).
+    void forward_into(const Matrix& src, Matrix& dst, CudaRuntime& rt) const;
     Matrix backward(const Matrix& input, const Matrix& output_gradient, CudaRuntime& rt,
                     Vector* dgamma = nullptr, Vector* dbeta = nullptr) const;
 };
@@ -486,6 +492,8 @@ public:
                    NormType norm_type, std::optional<Normalization> norm2 = std::nullopt);
     Matrix forward(const Matrix& input, CudaRuntime& rt);
     Matrix forward_mask(const Matrix& input, CudaRuntime& rt);
+    // The same, with the output projection written into `output`.
+    void forward_into(const Matrix& input, Matrix& output, CudaRuntime& rt, bool mask = false);
     Attention& attention() { return attention_; }
     Normalization& norm2() { return norm2_; }
     Matrix& position() { return position_; }
@@ -493,7 +501,7 @@ public:
     Linear& output() { return output_; }
 
 private:
-    Matrix finish_forward(Matrix positioned, Matrix x, CudaRuntime& rt);
+    Matrix finish_forward(Matrix positioned, Matrix x, CudaRuntime& rt, Matrix* target);
     Attention attention_;
     Matrix position_;
     InferenceMLP fcs_;
@@ -510,6 +518,9 @@ public:
                          NormType norm_type, std::optional<Normalization> norm1 = std::nullopt,
                          std::optional<Normalization> norm2 = std::nullopt);
     Matrix forward(const Matrix& input, CudaRuntime& rt) { return block_.forward(input, rt); }
+    void forward_into(const Matrix& input, Matrix& output, CudaRuntime& rt) {
+        block_.forward_into(input, output, rt, false);
+    }
     InferenceBlock& block() { return block_; }
 
 private:
@@ -524,6 +535,8 @@ public:
                         std::optional<Normalization> norm1 = std::nullopt,
                         std::optional<Normalization> norm2 = std::nullopt);
     Matrix forward(const Matrix& input, CudaRuntime& rt);
+    // The same, with the output projection written into `output`.
+    void forward_into(const Matrix& input, Matrix& output, CudaRuntime& rt);
     // Gradients, then SGD with learning_rate (reference semantics).
     Matrix backward(const Matrix& output_gradient, float learning_rate, CudaRuntime& rt);
     // Same update, and every gradient exposed in `grads`.
@@ -560,6 +573,9 @@ public:
         : block_(std::move(q), std::move(k), std::move(v), std::move(position), std::move(fcs),
                  std::move(output), std::move(qkv_streams), norm_type) {}
     Matrix forward(const Matrix& input, CudaRuntime& rt) { return block_.forward_mask(input, rt); }
+    void forward_into(const Matrix& input, Matrix& output, CudaRuntime& rt) {
+        block_.forward_into(input, output, rt, true);
+    }
     InferenceBlock& block() { return block_; }
 
 private:

@@ -182,6 +182,31 @@ __device__ __forceinline__ void fill_random_body(float* x, long long n, uint32_t
         x[i] = (float)forge_hash(seed + (uint32_t)i) / (float)4294967295u;
 }
 
+// p = p - lr * g: Linear::learn's bias update (linear.rs:385-390: clone the
+// gradient, scale it by the learning rate, subtract) in one pass with the
+// same two roundings.
+template <bool VEC>
+__device__ __forceinline__ void sgd_body(float* p, const float* __restrict__ g, long long n,
+                                         float lr) {
+    const long long tid = (long long)blockIdx.x * EW_THREADS + threadIdx.x;
+    const long long stride = (long long)gridDim.x * EW_THREADS;
+    if constexpr (VEC) {
+        const long long n4 = n / 4;
+        for (long long i = tid; i < n4; i += stride) {
+            float4 a = load_stream(p + 4 * i);
+            const float4 b = load_stream(g + 4 * i);
+            a.x = a.x - lr * b.x;
+            a.y = a.y - lr * b.y;
+            a.z = a.z - lr * b.z;
+            a.w = a.w - lr * b.w;
+            reinterpret_cast<float4*>(p)[i] = a;
+        }
+        for (long long i = n4 * 4 + tid; i < n; i += stride) p[i] = p[i] - lr * g[i];
+    } else {
+        for (long long i = tid; i < n; i += stride) p[i] = p[i] - lr * g[i];
+    }
+}
+
 // g = dy * act'(z): Linear::backward's derivative map and multiply
 // (linear.rs:254-265) in one pass; same two roundings.
 template <bool VEC>

@@ -141,6 +141,14 @@ FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_act_backward_s(const float
                                                                      float* g, long long n, int act) {
     act_backward_body<false>(dy, z, g, n, act);
 }
+FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_sgd_v(float* p, const float* g, long long n,
+                                                            float lr) {
+    sgd_body<true>(p, g, n, lr);
+}
+FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_sgd_s(float* p, const float* g, long long n,
+                                                            float lr) {
+    sgd_body<false>(p, g, n, lr);
+}
 FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_count_neq(const float* l, const float* r,
                                                                 long long n, float* out) {
     count_neq_body(l, r, n, out);

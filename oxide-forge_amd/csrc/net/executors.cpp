@@ -26,11 +26,14 @@ static forge_map_op forward_map(Activation a) {
 }
 
 // SGD on a parameter vector, as Linear::learn updates a bias
-// (linear.rs:385-390): scaled = clone(grad) * lr; param -= scaled.
-static void sgd_vector(CudaRuntime& rt, Vector& param, const Vector& grad, float lr) {
-    Vector scaled = rt.clone_vector(grad);
-    scaled.scale(lr, rt);
-    param.binary_assign(scaled, BinaryOp::Sub, rt);
+// (linear.rs:385-390): scaled = clone(grad) * lr; param -= scaled, as one
+// kernel with the same two roundings.
+static void sgd_vector(CudaRuntime& rt, Vector& param, const Vector& grad, float lr,
+                       const CudaStream* stream = nullptr) {
+    require(param.len() == grad.len(), "parameter and gradient lengths");
+    check(forge_sgd_update(rt.raw(), stream_raw(stream), param.slice(), grad.slice(), param.len(),
+                           lr),
+          "sgd_update");
 }
 
 // Norm backward for a training step: computes dgamma/dbeta whenever the norm
@@ -66,6 +69,14 @@ Matrix Linear::forward_keep(const Matrix& input, const Matrix* residual, Matrix*
     // linear.rs:116-132 -> affine_on (185-206) + activate_on (225-230).
     require(input.cols() == weights_.rows(), "input.cols() == weights.rows()");
     Matrix out = rt.new_uninit_matrix(input.rows(), weights_.cols());
+    forward_into(input, residual, out, rt, stream, pre_activation);
+    return out;
+}
+
+void Linear::forward_into(const Matrix& input, const Matrix* residual, Matrix& out,
+                          CudaRuntime& rt, const CudaStream* stream, Matrix* pre_activation) {
+    require(input.cols() == weights_.rows(), "input.cols() == weights.rows()");
+    require(out.rows() == input.rows() && out.cols() == weights_.cols(), "output shape");
     rt.stream_join_primary(stream);
     forge_gemm_epilogue ep = plain_epilogue();
     if (bias_) ep.bias = bias_->slice();
@@ -82,7 +93,6 @@ Matrix Linear::forward_keep(const Matrix& input, const Matrix* residual, Matrix*
     ep.activation = (int)activation_;
     rt.gemm_ex(stream, false, false, input, weights_, out.slice(), input.rows(), weights_.cols(),
                input.cols(), ep);
-    return out;
 }
 
 Matrix Linear::forward(const Matrix& input, const Matrix* residual, CudaRuntime& rt,
@@ -173,9 +183,7 @@ void Linear::learn_keep(const Matrix& input, const Matrix& gradient, const Vecto
                weights_.cols(), input.rows(), ep);
     if (bias_) {
         require(bias_gradient != nullptr, "missing bias gradient for biased Linear");
-        Vector scaled = rt.clone_vector_on(*bias_gradient, stream);
-        scaled.scale_on(learning_rate, rt, stream);
-        bias_->binary_assign_on(scaled, BinaryOp::Sub, rt, stream);
+        sgd_vector(rt, *bias_, *bias_gradient, learning_rate, stream);
     }
 }
 
@@ -423,18 +431,21 @@ Matrix TrainingMlp::backward_grads(const Matrix& output_gradient, float learning
 
 // =========================================================== Normalization
 
-void Normalization::forward(Matrix& m, CudaRuntime& rt) const {
-    if (m.rows() == 0) return;
+void Normalization::forward(Matrix& m, CudaRuntime& rt) const { forward_into(m, m, rt); }
+
+void Normalization::forward_into(const Matrix& src, Matrix& dst, CudaRuntime& rt) const {
+    require(src.rows() == dst.rows() && src.cols() == dst.cols(), "norm output shape");
+    if (src.rows() == 0) return;
     if (kind == NormType::Layer)
-        check(forge_layer_norm_rows(rt.raw(), nullptr, m.slice(),
-                                    gamma ? gamma->slice() : forge_slice{nullptr, 0},
-                                    beta ? beta->slice() : forge_slice{nullptr, 0}, m.rows(),
-                                    m.cols(), eps),
+        check(forge_layer_norm_rows_out(rt.raw(), nullptr, src.slice(), dst.slice(),
+                                        gamma ? gamma->slice() : forge_slice{nullptr, 0},
+                                        beta ? beta->slice() : forge_slice{nullptr, 0},
+                                        src.rows(), src.cols(), eps),
               "layer_norm");
     else
-        check(forge_rms_norm_rows(rt.raw(), nullptr, m.slice(),
-                                  gamma ? gamma->slice() : forge_slice{nullptr, 0}, m.rows(),
-                                  m.cols(), eps),
+        check(forge_rms_norm_rows_out(rt.raw(), nullptr, src.slice(), dst.slice(),
+                                      gamma ? gamma->slice() : forge_slice{nullptr, 0},
+                                      src.rows(), src.cols(), eps),
               "rms_norm");
 }
 
@@ -561,8 +572,10 @@ Matrix Attention::forward_self_training(Matrix input, CudaRuntime& rt) {
     ep2.residual = input.slice();
     rt.gemm_ex(nullptr, false, false, probabilities, p.value, pre_norm.slice(), p.query.rows(),
                p.value.cols(), p.value.rows(), ep2);
-    Matrix output = rt.clone_matrix(pre_norm);
-    normalize(output, rt);
+    // The pre-norm matrix is cached for backward, so the norm writes a new
+    // matrix instead of cloning and normalising in place.
+    Matrix output = rt.new_uninit_matrix(pre_norm.rows(), pre_norm.cols());
+    norm_.forward_into(pre_norm, output, rt);
     cache_ = Cache{std::move(input), std::move(p.query), std::move(p.key), std::move(p.value),
                    std::move(probabilities), std::move(pre_norm)};
     return output;
@@ -661,23 +674,37 @@ Matrix InferenceBlock::forward(const Matrix& input, CudaRuntime& rt) {
     // inference.rs:76-80.
     Matrix positioned = rt.matrix_add(input, position_);
     Matrix x = attention_.forward(positioned, positioned, rt);
-    return finish_forward(std::move(positioned), std::move(x), rt);
+    return finish_forward(std::move(positioned), std::move(x), rt, nullptr);
 }
 
 Matrix InferenceBlock::forward_mask(const Matrix& input, CudaRuntime& rt) {
     // inference.rs:82-88.
     Matrix positioned = rt.matrix_add(input, position_);
     Matrix x = attention_.forward_mask(positioned, positioned, rt);
-    return finish_forward(std::move(positioned), std::move(x), rt);
+    return finish_forward(std::move(positioned), std::move(x), rt, nullptr);
 }
 
-Matrix InferenceBlock::finish_forward(Matrix positioned, Matrix x, CudaRuntime& rt) {
+void InferenceBlock::forward_into(const Matrix& input, Matrix& output, CudaRuntime& rt,
+                                  bool mask) {
+    Matrix positioned = rt.matrix_add(input, position_);
+    Matrix x = mask ? attention_.forward_mask(positioned, positioned, rt)
+                    : attention_.forward(positioned, positioned, rt);
+    finish_forward(std::move(positioned), std::move(x), rt, &output);
+}
+
+Matrix InferenceBlock::finish_forward(Matrix positioned, Matrix x, CudaRuntime& rt,
+                                      Matrix* target) {
     // inference.rs:90-108: norm(x + ffn(x)) then the output projection; the
-    // x + ffn add is fused into the last FFN layer's epilogue.
+    // x + ffn add is fused into the last FFN layer's epilogue.  With a
+    // target, the projection writes there and an empty Matrix is returned.
     positioned = Matrix();
     Matrix out = fcs_.executor().forward_plus(x, &x, rt);
     x = Matrix();
     norm2_.forward(out, rt);
+    if (target) {
+        output_.forward_into(out, nullptr, *target, rt, nullptr);
+        return Matrix();
+    }
     return output_.forward(out, nullptr, rt, nullptr);
 }
 
@@ -704,16 +731,21 @@ TrainingTransformer::TrainingTransformer(Linear q, Linear k, Linear v, Matrix po
       norm2_(norm2 ? std::move(*norm2) : default_norm(norm_type)) {}
 
 Matrix TrainingTransformer::forward(const Matrix& input, CudaRuntime& rt) {
+    Matrix output = rt.new_uninit_matrix(input.rows(), output_.weights().cols());
+    forward_into(input, output, rt);
+    return output;
+}
+
+void TrainingTransformer::forward_into(const Matrix& input, Matrix& output, CudaRuntime& rt) {
     // encoder.rs:114-131.
     Matrix positioned = rt.matrix_add(input, position_);
     Matrix first_output = attention_.forward_self_training(std::move(positioned), rt);
     // second_pre_norm = first_output + ffn(first_output), fused.
     Matrix second_pre_norm = fcs_.forward_plus(std::move(first_output), true, rt);
-    Matrix encoded = rt.clone_matrix(second_pre_norm);
-    norm2_.forward(encoded, rt);
-    Matrix output = output_.forward(encoded, nullptr, rt, nullptr);
+    Matrix encoded = rt.new_uninit_matrix(second_pre_norm.rows(), second_pre_norm.cols());
+    norm2_.forward_into(second_pre_norm, encoded, rt);
+    output_.forward_into(encoded, nullptr, output, rt, nullptr);
     cache_ = Cache{std::move(second_pre_norm), std::move(encoded)};
-    return output;
 }
 
 Matrix TrainingTransformer::backward(const Matrix& output_gradient, float learning_rate,

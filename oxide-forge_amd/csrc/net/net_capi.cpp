@@ -382,12 +382,13 @@ extern "C" forge_status forge_net_transformer_forward(forge_net_model* m, forge_
         const forge_transformer_desc& d = m->desc;
         need(input, d.seq * d.hidden, "transformer input");
         need(output, d.seq * d.out, "transformer output");
-        // The input is read in place: a non-owning Matrix view.
+        // Input and output are caller buffers: non-owning Matrix views, and
+        // the output projection writes straight into the caller's buffer.
         Matrix X(DeviceBuffer(nullptr, forge_slice{input.ptr, d.seq * d.hidden}), d.seq, d.hidden);
-        Matrix Y = m->enc_train ? m->enc_train->forward(X, rt)
-                   : m->enc_inf ? m->enc_inf->forward(X, rt)
-                                : m->dec_inf->forward(X, rt);
-        check(forge_memcpy_d2d(rt.raw(), nullptr, output, Y.slice(), Y.len()), "forward output");
+        Matrix Y(DeviceBuffer(nullptr, forge_slice{output.ptr, d.seq * d.out}), d.seq, d.out);
+        if (m->enc_train) m->enc_train->forward_into(X, Y, rt);
+        else if (m->enc_inf) m->enc_inf->forward_into(X, Y, rt);
+        else m->dec_inf->forward_into(X, Y, rt);
     });
 }
 

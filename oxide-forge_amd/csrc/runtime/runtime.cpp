@@ -857,16 +857,34 @@ extern "C" forge_status forge_softmax_rows_bwd(forge_runtime* rt, forge_stream* 
     return row_launch(rt, s, "softmax_bwd", a, nullptr, nullptr);
 }
 
-extern "C" forge_status forge_layer_norm_rows(forge_runtime* rt, forge_stream* s, forge_slice x,
-                                              forge_slice gamma, forge_slice beta, size_t rows,
-                                              size_t cols, float eps) {
+// y == x (in place) or y disjoint from x; partial overlap is rejected.
+static forge_status check_out_of_place(forge_slice x, forge_slice y, size_t n, const char* what) {
+    if (x.ptr == y.ptr) return FORGE_OK;
+    const float *xb = x.ptr, *yb = y.ptr;
+    if (yb < xb + n && xb < yb + n)
+        return fail(FORGE_EINVAL, "%s: output overlaps the input without being it", what);
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_layer_norm_rows_out(forge_runtime* rt, forge_stream* s,
+                                                  forge_slice x, forge_slice y, forge_slice gamma,
+                                                  forge_slice beta, size_t rows, size_t cols,
+                                                  float eps) {
     if (!rt) return fail(FORGE_EINVAL, "runtime is null");
     FORGE_TRY(check_rows(rows, cols));
     FORGE_TRY(need(x, rows * cols, "layer_norm x"));
+    FORGE_TRY(need(y, rows * cols, "layer_norm y"));
+    FORGE_TRY(check_out_of_place(x, y, rows * cols, "layer_norm"));
     FORGE_TRY(need_opt(gamma, cols, "layer_norm gamma"));
     FORGE_TRY(need_opt(beta, cols, "layer_norm beta"));
-    RowArgs a{x.ptr, x.ptr, nullptr, gamma.ptr, beta.ptr, nullptr, nullptr, (int)rows, (int)cols, eps, 1.0f};
+    RowArgs a{x.ptr, y.ptr, nullptr, gamma.ptr, beta.ptr, nullptr, nullptr, (int)rows, (int)cols, eps, 1.0f};
     return row_launch(rt, s, "layer_norm", a, nullptr, nullptr);
+}
+
+extern "C" forge_status forge_layer_norm_rows(forge_runtime* rt, forge_stream* s, forge_slice x,
+                                              forge_slice gamma, forge_slice beta, size_t rows,
+                                              size_t cols, float eps) {
+    return forge_layer_norm_rows_out(rt, s, x, x, gamma, beta, rows, cols, eps);
 }
 
 extern "C" forge_status forge_layer_norm_bwd(forge_runtime* rt, forge_stream* s, forge_slice x,
@@ -885,15 +903,23 @@ extern "C" forge_status forge_layer_norm_bwd(forge_runtime* rt, forge_stream* s,
     return row_launch(rt, s, "layer_norm_bwd", a, dgamma.ptr, dbeta.ptr);
 }
 
-extern "C" forge_status forge_rms_norm_rows(forge_runtime* rt, forge_stream* s, forge_slice x,
-                                            forge_slice gamma, size_t rows, size_t cols,
-                                            float eps) {
+extern "C" forge_status forge_rms_norm_rows_out(forge_runtime* rt, forge_stream* s,
+                                                forge_slice x, forge_slice y, forge_slice gamma,
+                                                size_t rows, size_t cols, float eps) {
     if (!rt) return fail(FORGE_EINVAL, "runtime is null");
     FORGE_TRY(check_rows(rows, cols));
     FORGE_TRY(need(x, rows * cols, "rms_norm x"));
+    FORGE_TRY(need(y, rows * cols, "rms_norm y"));
+    FORGE_TRY(check_out_of_place(x, y, rows * cols, "rms_norm"));
     FORGE_TRY(need_opt(gamma, cols, "rms_norm gamma"));
-    RowArgs a{x.ptr, x.ptr, nullptr, gamma.ptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, eps, 1.0f};
+    RowArgs a{x.ptr, y.ptr, nullptr, gamma.ptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, eps, 1.0f};
     return row_launch(rt, s, "rms_norm", a, nullptr, nullptr);
+}
+
+extern "C" forge_status forge_rms_norm_rows(forge_runtime* rt, forge_stream* s, forge_slice x,
+                                            forge_slice gamma, size_t rows, size_t cols,
+                                            float eps) {
+    return forge_rms_norm_rows_out(rt, s, x, x, gamma, rows, cols, eps);
 }
 
 extern "C" forge_status forge_rms_norm_bwd(forge_runtime* rt, forge_stream* s, forge_slice x,
@@ -943,6 +969,19 @@ extern "C" forge_status forge_binary_assign(forge_runtime* rt, forge_stream* s, 
     long long nn = (long long)n;
     unsigned g = grid_for(vec ? nn / 4 + 1 : nn, EW_THREADS, 8192);
     return launch_args(rt, s, name, dim3(g), dim3(EW_THREADS), 0, t.ptr, (const float*)r.ptr, nn);
+}
+
+extern "C" forge_status forge_sgd_update(forge_runtime* rt, forge_stream* s, forge_slice param,
+                                         forge_slice grad, size_t n, float lr) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    FORGE_TRY(need(param, n, "sgd_update param"));
+    FORGE_TRY(need(grad, n, "sgd_update grad"));
+    if (n == 0) return FORGE_OK;
+    bool vec = aligned16(param.ptr) && aligned16(grad.ptr);
+    long long nn = (long long)n;
+    unsigned g = grid_for(vec ? nn / 4 + 1 : nn, EW_THREADS, 8192);
+    return launch_args(rt, s, vec ? "forge_sgd_v" : "forge_sgd_s", dim3(g), dim3(EW_THREADS), 0,
+                       param.ptr, (const float*)grad.ptr, nn, lr);
 }
 
 extern "C" forge_status forge_binary_assign_by_rows(forge_runtime* rt, forge_stream* s,

@@ -223,6 +223,11 @@ class Runtime:
         call("forge_layer_norm_rows", self.handle, stream, x.slice, _sl(gamma), _sl(beta), rows,
              cols, eps)
 
+    def layer_norm_out(self, x, y, rows, cols, gamma=None, beta=None, eps=1e-5,
+                       stream=None) -> None:
+        call("forge_layer_norm_rows_out", self.handle, stream, x.slice, y.slice, _sl(gamma),
+             _sl(beta), rows, cols, eps)
+
     def layer_norm_bwd(self, x, dy, dx, rows, cols, gamma=None, dgamma=None, dbeta=None,
                        eps=1e-5, stream=None) -> None:
         call("forge_layer_norm_bwd", self.handle, stream, x.slice, dy.slice, _sl(gamma),
@@ -230,6 +235,10 @@ class Runtime:
 
     def rms_norm(self, x, rows, cols, gamma=None, eps=1e-5, stream=None) -> None:
         call("forge_rms_norm_rows", self.handle, stream, x.slice, _sl(gamma), rows, cols, eps)
+
+    def rms_norm_out(self, x, y, rows, cols, gamma=None, eps=1e-5, stream=None) -> None:
+        call("forge_rms_norm_rows_out", self.handle, stream, x.slice, y.slice, _sl(gamma), rows,
+             cols, eps)
 
     def rms_norm_bwd(self, x, dy, dx, rows, cols, gamma=None, dgamma=None, eps=1e-5,
                      stream=None) -> None:
@@ -279,6 +288,10 @@ class Runtime:
     def activation_backward(self, dy, z, g, activation, n=None, stream=None) -> None:
         call("forge_activation_backward", self.handle, stream, dy.slice, z.slice, g.slice,
              g.size if n is None else n, activation)
+
+    def sgd_update(self, param, grad, lr, n=None, stream=None) -> None:
+        call("forge_sgd_update", self.handle, stream, param.slice, grad.slice,
+             param.size if n is None else n, lr)
 
     def fill_random(self, x, seed, n=None, stream=None) -> None:
         call("forge_fill_random", self.handle, stream, x.slice, x.size if n is None else n, seed)

@@ -106,9 +106,12 @@ SIGNATURES = {
     "forge_softmax_rows": [RT, ST, Slice, c_size_t, c_size_t],
     "forge_softmax_rows_bwd": [RT, ST, Slice, Slice, Slice, c_size_t, c_size_t],
     "forge_layer_norm_rows": [RT, ST, Slice, Slice, Slice, c_size_t, c_size_t, c_float],
+    "forge_layer_norm_rows_out": [RT, ST, Slice, Slice, Slice, Slice, c_size_t, c_size_t,
+                                  c_float],
     "forge_layer_norm_bwd": [RT, ST, Slice, Slice, Slice, Slice, Slice, Slice, c_size_t,
                              c_size_t, c_float],
     "forge_rms_norm_rows": [RT, ST, Slice, Slice, c_size_t, c_size_t, c_float],
+    "forge_rms_norm_rows_out": [RT, ST, Slice, Slice, Slice, c_size_t, c_size_t, c_float],
     "forge_rms_norm_bwd": [RT, ST, Slice, Slice, Slice, Slice, Slice, c_size_t, c_size_t,
                            c_float],
     "forge_binary": [RT, ST, Slice, Slice, Slice, c_size_t, c_int],
@@ -123,6 +126,7 @@ SIGNATURES = {
     "forge_causal_mask": [RT, ST, Slice, c_size_t, c_size_t],
     "forge_softmax_rows_bwd_scaled": [RT, ST, Slice, Slice, Slice, c_size_t, c_size_t, c_float],
     "forge_activation_backward": [RT, ST, Slice, Slice, Slice, c_size_t, c_int],
+    "forge_sgd_update": [RT, ST, Slice, Slice, c_size_t, c_float],
     "forge_fill_random": [RT, ST, Slice, c_size_t, ctypes.c_uint32],
     "forge_compare": [RT, ST, Slice, Slice, c_size_t, Slice],
 }

@@ -463,6 +463,41 @@ def test_softmax_bwd_scaled_equals_bwd_then_scale(rt):
     assert np.array_equal(a.numpy(), b.numpy())
 
 
+@pytest.mark.parametrize("n", [1, 7, 1024, 100_003])
+def test_sgd_update_bit_exact(rt, n):
+    """param - lr * grad with two roundings, as the reference's clone / scale /
+    subtract sequence (linear.rs:385-390)."""
+    say(f"sgd_update n={n}")
+    p, g = orc.normal((n,), 1), orc.normal((n,), 2)
+    lr = np.float32(3e-3)
+    dp = rt.array(p)
+    rt.sgd_update(dp, rt.array(g), float(lr))
+    assert np.array_equal(dp.numpy(), p - lr * g)
+    # Unaligned views take the scalar kernel.
+    dp2 = rt.array(np.concatenate([[0.0], p]).astype(np.float32)).view(1, (n,))
+    dg2 = rt.array(np.concatenate([[0.0], g]).astype(np.float32)).view(1, (n,))
+    rt.sgd_update(dp2, dg2, float(lr))
+    assert np.array_equal(dp2.numpy(), p - lr * g)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 1024), (33, 70)])
+def test_norm_out_of_place_equals_in_place(rt, rows, cols):
+    say(f"norm out-of-place {rows}x{cols}")
+    x = orc.normal((rows, cols), 3)
+    gm, bt = orc.normal((cols,), 4, 1.0, 0.1), orc.normal((cols,), 5, 0.0, 0.1)
+    dgm, dbt = rt.array(gm), rt.array(bt)
+    for name, args in (("layer", (dgm, dbt)), ("rms", (dgm,))):
+        src, inplace, out = rt.array(x), rt.array(x), rt.empty((rows, cols))
+        getattr(rt, f"{name}_norm")(inplace, rows, cols, *args)
+        getattr(rt, f"{name}_norm_out")(src, out, rows, cols, *args)
+        assert np.array_equal(out.numpy(), inplace.numpy()), name
+        assert np.array_equal(src.numpy(), x), f"{name}: input modified"
+    # Partial overlap of input and output is rejected.
+    big = rt.array(np.zeros((rows + 1) * cols, np.float32))
+    with pytest.raises(oxforge.ForgeError):
+        rt.layer_norm_out(big.view(0, (rows, cols)), big.view(cols, (rows, cols)), rows, cols)
+
+
 @pytest.mark.parametrize("M,N,K", [(256, 128, 192), (70, 50, 33)])
 def test_transposed_operands_bit_identical_to_materialised_transpose(rt, M, N, K):
     """NT/TN GEMMs read A^T/B^T in place; the products equal the reference's
