@@ -311,6 +311,18 @@ def sweep(rt, orc, steps, warmup):
                 continue
             res[key] = round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 2)
             log(f"sweep {key}: {res[key]}")
+        # Split-K candidates for the shapes with few output tiles.
+        for tag in ["256x128x16_4x2", "128x128x16_4x2", "128x64x16_2x2"]:
+            for splits in (2, 4):
+                key = f"{M}x{N}x{K}:{tag}:split{splits}"
+                try:
+                    ms = time_launches(rt, lambda i, t=tag, sp=splits: rt.gemm_split(
+                        t, sp, dA, dB, dC, M, N, K), steps, warmup)
+                except oxforge.ForgeError as e:
+                    res[key] = f"error: {e}"
+                    continue
+                res[key] = round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 2)
+                log(f"sweep {key}: {res[key]}")
         for d in (dA, dB, dC):
             d.recycle()
     return res

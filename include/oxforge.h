@@ -177,7 +177,10 @@ forge_status forge_fill(forge_runtime *rt, forge_stream *stream,
 /* matrix_multiply / matrix_multiply_into_on (matrix.rs:113-176, kernel
  * gemm.rs:202-373): C[M,N] = A[M,K] * B[K,N], row-major, C overwritten.
  * True fp32 (v_mfma_f32_32x32x2_f32), not the reference's TF32.  Any
- * M, N, K >= 0 (the reference asserts multiples of 16). */
+ * M, N, K >= 0 (the reference asserts multiples of 16).  Outputs with too
+ * few tiles to fill the device and K >= 2048 are computed as K slices summed
+ * in slice order (deterministic; the choice depends only on the shape and
+ * alignment, the same for this call and forge_gemm_ex_f32). */
 forge_status forge_gemm_f32(forge_runtime *rt, forge_stream *stream,
                             forge_slice A, forge_slice B, forge_slice C,
                             size_t M, size_t N, size_t K);
@@ -227,6 +230,33 @@ forge_status forge_gemm_f32_tile(forge_runtime *rt, forge_stream *stream,
                                  const char *tile_tag, forge_slice A,
                                  forge_slice B, forge_slice C, size_t M,
                                  size_t N, size_t K);
+
+/* Tuning entry point (no reference counterpart): forge_gemm_f32 computed as
+ * `splits` K slices (one batched launch) plus a reduction in slice order,
+ * with tile "256x128x16_4x2", "128x128x16_4x2" or "128x64x16_2x2".  Requires
+ * M % BM == N % BN == K % (splits * BK) == 0, 16-byte aligned operands and
+ * 1 <= splits <= 8.  Used by the benchmark's sweep. */
+forge_status forge_gemm_f32_split(forge_runtime *rt, forge_stream *stream,
+                                  const char *tile_tag, int splits, forge_slice A,
+                                  forge_slice B, forge_slice C, size_t M, size_t N,
+                                  size_t K);
+
+/* One product of a batch: operands and its own fused epilogue. */
+typedef struct forge_gemm_problem {
+    forge_slice A, B, C;
+    forge_gemm_epilogue epilogue;
+} forge_gemm_problem;
+
+/* `count` products of the same shape and transposes in one launch, each as
+ * forge_gemm_ex_f32 would compute it (bit-identical; shapes that call splits
+ * in K run one product at a time).  Replaces the three
+ * forked streams of the Q/K/V projections (attention.rs:65-94) and of their
+ * weight updates (attention.rs:104-144): one launch fills the device without
+ * the cross-queue event latency of a fork and join. */
+forge_status forge_gemm_batch_f32(forge_runtime *rt, forge_stream *stream,
+                                  int trans_a, int trans_b, size_t M, size_t N,
+                                  size_t K, size_t count,
+                                  const forge_gemm_problem *problems);
 
 /* matrix_transpose (convert.rs:17-63 -> layout.rs:8-55):
  * out[c,r] = in[r,c]; in is [rows,cols]. Bit-exact. */

@@ -318,6 +318,8 @@ public:
     void forward_into(const Matrix& input, const Matrix* residual, Matrix& output,
                       CudaRuntime& rt, const CudaStream* stream,
                       Matrix* pre_activation = nullptr);
+    // The GEMM of forward_into as a batch entry (bias and activation fused).
+    forge_gemm_problem forward_problem(const Matrix& input, Matrix& output) const;
     // learn that also stores dW (and db) when given, for explicit gradients.
     void learn_keep(const Matrix& input, const Matrix& gradient, const Vector* bias_gradient,
                     float learning_rate, Matrix* weight_gradient, CudaRuntime& rt,
@@ -428,6 +430,10 @@ struct Normalization {
 };
 
 // QkvProjection (attention.rs:15-145).
+// QkvProjection (attention.rs:15-144).  The reference runs the three
+// projections on three forked streams; here they are one batched GEMM launch
+// on the primary stream (same results, no cross-queue fork and joins), and
+// `streams` is accepted for interface compatibility only.
 class QkvProjection {
 public:
     QkvProjection(Linear query, Linear key, Linear value,

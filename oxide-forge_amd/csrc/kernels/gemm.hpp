@@ -51,16 +51,21 @@ struct GemmArgs {
 constexpr int GEMM_GROUP_M = 8;
 constexpr int LDS_PAD = 4;
 
-// Maps the hardware workgroup id to a (tile_m, tile_n) pair; see the file
-// comment.  Correctness does not depend on the dispatch order.
-__device__ __forceinline__ void gemm_tile_coords(int num_m, int num_n,
-                                                 int& tm, int& tn) {
-    const int nwg = num_m * num_n;
-    const int b = blockIdx.x;
+// Maps hardware workgroup id b of nwg to a logical tile index so that each
+// XCD (workgroups are dealt round-robin over the 8 XCDs) receives a
+// contiguous range of logical tiles.
+__device__ __forceinline__ int xcd_logical(int b, int nwg) {
     const int per_xcd = nwg / 8, rem = nwg % 8;
     const int xcd = b % 8, local = b / 8;
-    const int logical = xcd < rem ? xcd * (per_xcd + 1) + local
-                                  : rem * (per_xcd + 1) + (xcd - rem) * per_xcd + local;
+    return xcd < rem ? xcd * (per_xcd + 1) + local
+                     : rem * (per_xcd + 1) + (xcd - rem) * per_xcd + local;
+}
+
+// Maps a logical tile index to (tile_m, tile_n), walking GEMM_GROUP_M-row
+// bands so consecutive tiles share A and B slabs.  Correctness does not
+// depend on the order.
+__device__ __forceinline__ void gemm_tile_coords(int logical, int num_m, int num_n,
+                                                 int& tm, int& tn) {
     const int in_group = GEMM_GROUP_M * num_n;
     const int group = logical / in_group;
     const int first_m = group * GEMM_GROUP_M;
@@ -70,10 +75,39 @@ __device__ __forceinline__ void gemm_tile_coords(int num_m, int num_n,
     tn = r / gsize;
 }
 
+// A batch of GEMMs with the same M and N (and tile instance) in one launch:
+// logical tile t belongs to problem t / tiles.  Used for the Q/K/V
+// projections and for the K slices of a split-K product.
+constexpr int GEMM_BATCH_MAX = 8;
+struct GemmBatchArgs {
+    GemmArgs p[GEMM_BATCH_MAX];
+    int count;  // problems
+    int tiles;  // tiles per problem
+};
+
 // Loads a ROWS x COLS tile (COLS contiguous in global memory) into registers,
 // COLS/4 four-float vectors per row, dealt over NT threads.  GUARD zero-fills
 // outside [vr, vc) and uses scalar loads (no alignment assumption).  The
 // staging registers are the native 4-float vector f4 so they stay in VGPRs.
+
+// The fused epilogue on one element z of the product at (row, col), idx =
+// row * ldc + col: alpha, bias, residual, aux multiply (or act'(aux)),
+// pre-activation store, activation, then store or SGD update.  Each step is
+// one rounded f32 operation in the reference's launch order.
+__device__ __forceinline__ void gemm_epilogue_store(const GemmArgs& p, long long idx, int col,
+                                                    float z) {
+    if (p.alpha != 1.0f) z = p.alpha * z;
+    if (p.bias) z = z + p.bias[col];
+    if (p.residual) z = z + p.residual[idx];
+    if (p.aux) {
+        const float m = p.aux_act ? activate_derivative(p.aux_act, p.aux[idx]) : p.aux[idx];
+        z = z * m;
+    }
+    if (p.pre_out) p.pre_out[idx] = z;
+    const float y = activate(p.act, z);
+    if (p.update) p.C[idx] = p.C[idx] - p.update_scale * y;
+    else p.C[idx] = y;
+}
 
 template <int ROWS, int COLS, int NT>
 struct TileShape {
@@ -143,7 +177,7 @@ __device__ __forceinline__ void load_frag(const float* __restrict__ s, int row,
 
 template <int BM, int BN, int BK, int WARPS_M, int WARPS_N, bool TA, bool TB,
           bool GUARD, bool EPI>
-__device__ __forceinline__ void gemm_body(const GemmArgs& p) {
+__device__ __forceinline__ void gemm_body(const GemmArgs& p, int logical) {
     constexpr int NT = WARPS_M * WARPS_N * 64;
     constexpr int WM = BM / WARPS_M, WN = BN / WARPS_N;
     constexpr int FM = WM / 32, FN = WN / 32;
@@ -160,7 +194,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
 
     const int num_m = (p.M + BM - 1) / BM, num_n = (p.N + BN - 1) / BN;
     int tm, tn;
-    gemm_tile_coords(num_m, num_n, tm, tn);
+    gemm_tile_coords(logical, num_m, num_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
 
     const int lane = threadIdx.x & 63;
@@ -240,35 +274,123 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p) {
 
     // Epilogue.  Accumulator register r of a 32x32 block holds
     // row 8*(r/4) + 4*(lane/32) + r%4, column lane%32.
+    const int row_base = m0 + wm * WM + 4 * half;
+    const int col_base = n0 + wn * WN + l32;
 #pragma unroll
     for (int i = 0; i < FM; i++) {
 #pragma unroll
         for (int j = 0; j < FN; j++) {
-            const int col = n0 + wn * WN + j * 32 + l32;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                if (GUARD && (row >= p.M || col >= p.N)) continue;
-                const long long idx = (long long)row * p.ldc + col;
-                float z = acc[i][j][r];
-                if constexpr (EPI) {
-                    if (p.alpha != 1.0f) z = p.alpha * z;
-                    if (p.bias) z = z + p.bias[col];
-                    if (p.residual) z = z + p.residual[idx];
-                    if (p.aux) {
-                        const float m = p.aux_act ? activate_derivative(p.aux_act, p.aux[idx])
-                                                  : p.aux[idx];
-                        z = z * m;
-                    }
-                    if (p.pre_out) p.pre_out[idx] = z;
-                    const float y = activate(p.act, z);
-                    if (p.update) p.C[idx] = p.C[idx] - p.update_scale * y;
-                    else p.C[idx] = y;
-                } else {
-                    p.C[idx] = z;
+            v16f& a = acc[i][j];
+            const int col = col_base + j * 32;
+            // Visits the 16 accumulators of block (i, j) as (r, row, EL(ptr)),
+            // EL(ptr) being the element (row, col) of an [M, ldc] operand.
+            // Guarded tiles skip elements outside the matrix and address with
+            // 64-bit indices; unguarded tiles (matrices below 2^30 elements,
+            // checked by the host) use a 32-bit byte offset from the
+            // operand's base, so each address takes one VGPR instead of two.
+#define FORGE_EPI_EACH(BODY)                                                     \
+    _Pragma("unroll") for (int r = 0; r < 16; r++) {                             \
+        const int row = row_base + i * 32 + 8 * (r >> 2) + (r & 3);              \
+        if (GUARD && (row >= p.M || col >= p.N)) continue;                       \
+        const long long idx = (long long)row * p.ldc + col;                      \
+        const unsigned boff = ((unsigned)row * (unsigned)p.ldc + (unsigned)col) * 4u; \
+        (void)idx; (void)boff;                                                   \
+        BODY;                                                                    \
+    }
+#define EL(ptr) (*(GUARD ? (ptr) + idx                                           \
+                         : reinterpret_cast<float*>(reinterpret_cast<char*>(     \
+                               const_cast<float*>(ptr)) + boff)))
+            // The same, one element at a time: the scheduler may not
+            // interleave the (long) activation code of several elements,
+            // which would need registers for all of them at once.
+#define FORGE_EPI_EACH_SEQ(BODY) FORGE_EPI_EACH(BODY; __builtin_amdgcn_sched_barrier(0))
+            if constexpr (EPI) {
+                // Block by block, the fused steps run as separate passes over
+                // the block's accumulators, each under one uniform branch:
+                // the optional steps neither multiply the unrolled code nor
+                // keep more than one block's operands live.  Per element the
+                // order (alpha, bias, residual, aux, pre_out, activation, store
+                // or update) is that of gemm_epilogue_store.
+                if (p.alpha != 1.0f) FORGE_EPI_EACH(a[r] = p.alpha * a[r]);
+                if (p.bias && (!GUARD || col < p.N)) {
+                    const float b = p.bias[col];
+                    FORGE_EPI_EACH(a[r] = a[r] + b);
                 }
+                if (p.residual) FORGE_EPI_EACH(a[r] = a[r] + EL(p.residual));
+                if (p.aux) {
+                    switch (p.aux_act) {
+                    case ACT_GELU: FORGE_EPI_EACH_SEQ(a[r] = a[r] * gelu_derivative(EL(p.aux))); break;
+                    case ACT_RELU: FORGE_EPI_EACH_SEQ(a[r] = a[r] * relu_derivative(EL(p.aux))); break;
+                    case ACT_SILU: FORGE_EPI_EACH_SEQ(a[r] = a[r] * silu_derivative(EL(p.aux))); break;
+                    default: FORGE_EPI_EACH(a[r] = a[r] * EL(p.aux)); break;
+                    }
+                }
+                if (p.pre_out) FORGE_EPI_EACH(EL(p.pre_out) = a[r]);
+                switch (p.act) {
+                case ACT_GELU: FORGE_EPI_EACH_SEQ(a[r] = gelu(a[r])); break;
+                case ACT_RELU: FORGE_EPI_EACH_SEQ(a[r] = relu(a[r])); break;
+                case ACT_SILU: FORGE_EPI_EACH_SEQ(a[r] = silu(a[r])); break;
+                default: break;
+                }
+                if (p.update) {
+                    FORGE_EPI_EACH(EL(p.C) = EL(p.C) - p.update_scale * a[r]);
+                } else {
+                    FORGE_EPI_EACH(EL(p.C) = a[r]);
+                }
+            } else {
+                FORGE_EPI_EACH(EL(p.C) = a[r]);
             }
+#undef EL
+#undef FORGE_EPI_EACH_SEQ
+#undef FORGE_EPI_EACH
         }
+    }
+}
+
+// One GEMM per launch: grid = tiles.
+template <int BM, int BN, int BK, int WARPS_M, int WARPS_N, bool TA, bool TB,
+          bool GUARD, bool EPI>
+__device__ __forceinline__ void gemm_single(const GemmArgs& p) {
+    gemm_body<BM, BN, BK, WARPS_M, WARPS_N, TA, TB, GUARD, EPI>(
+        p, xcd_logical(blockIdx.x, gridDim.x));
+}
+
+// A batch of GEMMs per launch: grid = count * tiles.
+template <int BM, int BN, int BK, int WARPS_M, int WARPS_N, bool TA, bool TB>
+__device__ __forceinline__ void gemm_batch(const GemmBatchArgs& b) {
+    const int logical = xcd_logical(blockIdx.x, gridDim.x);
+    const int z = logical / b.tiles;
+    gemm_body<BM, BN, BK, WARPS_M, WARPS_N, TA, TB, false, true>(b.p[z], logical - z * b.tiles);
+}
+
+// Sum of the split-K partial products P[s] ([splits][M][N], row pitch N) in
+// split order, then the GEMM epilogue of p into p.C (row pitch p.ldc).  The
+// order of the sum depends only on the shape, so results are deterministic.
+constexpr int SPLITK_THREADS = 256;  // launch size of the reduce kernels
+template <bool VEC>
+__device__ __forceinline__ void splitk_reduce_body(const float* __restrict__ P, int splits,
+                                                   const GemmArgs& p) {
+    const long long MN = (long long)p.M * p.N;
+    constexpr int W = VEC ? 4 : 1;  // VEC requires N % 4 == 0 and a 16-byte aligned P
+    const long long stride = (long long)gridDim.x * SPLITK_THREADS * W;
+    for (long long e = ((long long)blockIdx.x * SPLITK_THREADS + threadIdx.x) * W; e < MN;
+         e += stride) {
+        const int row = (int)(e / p.N), col0 = (int)(e % p.N);
+        float z[W];
+        if constexpr (VEC) {
+            const float4 v = load_stream(P + e);
+            z[0] = v.x; z[1] = v.y; z[2] = v.z; z[3] = v.w;
+            for (int s = 1; s < splits; s++) {
+                const float4 u = load_stream(P + s * MN + e);
+                z[0] += u.x; z[1] += u.y; z[2] += u.z; z[3] += u.w;
+            }
+        } else {
+            z[0] = P[e];
+            for (int s = 1; s < splits; s++) z[0] += P[s * MN + e];
+        }
+#pragma unroll
+        for (int w = 0; w < W; w++)
+            gemm_epilogue_store(p, (long long)row * p.ldc + col0 + w, col0 + w, z[w]);
     }
 }
 

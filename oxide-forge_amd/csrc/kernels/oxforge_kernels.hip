@@ -16,7 +16,7 @@ using namespace forge;
 //   _g: bounds-guarded (any shape, any alignment); _e: fused epilogue.
 #define GEMM_KERNEL(NAME, BM, BN, BK, WMW, WNW, TA, TB, GUARD, EPI)          \
     FORGE_KERNEL void __launch_bounds__(WMW * WNW * 64) NAME(GemmArgs p) {   \
-        gemm_body<BM, BN, BK, WMW, WNW, TA, TB, GUARD, EPI>(p);              \
+        gemm_single<BM, BN, BK, WMW, WNW, TA, TB, GUARD, EPI>(p);            \
     }
 
 // Epilogue instances: the three unguarded tiles the dispatcher chooses from
@@ -31,6 +31,33 @@ GEMM_FAMILY(nn, false, false)
 GEMM_FAMILY(nt, false, true)
 GEMM_FAMILY(tn, true, false)
 GEMM_FAMILY(tt, true, true)
+
+// Batched instances (forge_gemm_batch_<ab>_<tile>): several same-shape
+// products per launch, each with its own operands and epilogue.  They serve
+// the Q/K/V projections and the K slices of split-K products.
+#define GEMM_BATCH_KERNEL(NAME, BM, BN, BK, WMW, WNW, TA, TB)                          \
+    FORGE_KERNEL void __launch_bounds__(WMW * WNW * 64) NAME(GemmBatchArgs b) {      \
+        gemm_batch<BM, BN, BK, WMW, WNW, TA, TB>(b);                                 \
+    }
+#define GEMM_BATCH_FAMILY(AB, TA, TB)                                                             \
+    GEMM_BATCH_KERNEL(forge_gemm_batch_##AB##_256x128x16_4x2, 256, 128, 16, 4, 2, TA, TB)      \
+    GEMM_BATCH_KERNEL(forge_gemm_batch_##AB##_128x128x16_4x2, 128, 128, 16, 4, 2, TA, TB)      \
+    GEMM_BATCH_KERNEL(forge_gemm_batch_##AB##_128x64x16_2x2, 128, 64, 16, 2, 2, TA, TB)
+GEMM_BATCH_FAMILY(nn, false, false)
+GEMM_BATCH_FAMILY(nt, false, true)
+GEMM_BATCH_FAMILY(tn, true, false)
+
+// Split-K: sum of the partial products in split order, then the epilogue.
+FORGE_KERNEL void __launch_bounds__(SPLITK_THREADS) forge_gemm_splitk_reduce_v(const float* P,
+                                                                            int splits,
+                                                                            GemmArgs p) {
+    splitk_reduce_body<true>(P, splits, p);
+}
+FORGE_KERNEL void __launch_bounds__(SPLITK_THREADS) forge_gemm_splitk_reduce_s(const float* P,
+                                                                            int splits,
+                                                                            GemmArgs p) {
+    splitk_reduce_body<false>(P, splits, p);
+}
 
 // Plain C = A * B instances (forge_gemm_f32 uses the first three and the
 // guarded one) and the other tile-shape candidates of the bench sweep.

@@ -95,6 +95,19 @@ void Linear::forward_into(const Matrix& input, const Matrix* residual, Matrix& o
                input.cols(), ep);
 }
 
+forge_gemm_problem Linear::forward_problem(const Matrix& input, Matrix& out) const {
+    require(input.cols() == weights_.rows(), "input.cols() == weights.rows()");
+    require(out.rows() == input.rows() && out.cols() == weights_.cols(), "output shape");
+    forge_gemm_problem pr{};
+    pr.A = input.slice();
+    pr.B = weights_.slice();
+    pr.C = out.slice();
+    pr.epilogue = plain_epilogue();
+    if (bias_) pr.epilogue.bias = bias_->slice();
+    pr.epilogue.activation = (int)activation_;
+    return pr;
+}
+
 Matrix Linear::forward(const Matrix& input, const Matrix* residual, CudaRuntime& rt,
                        const CudaStream* stream) {
     return forward_keep(input, residual, nullptr, rt, stream);
@@ -479,22 +492,35 @@ QkvProjection::QkvProjection(Linear query, Linear key, Linear value,
 
 QkvProjection::Projected QkvProjection::project(const Matrix& query_input,
                                                 const Matrix& key_value_input, CudaRuntime& rt) {
-    // attention.rs:65-94: three Linear::forward on three forked streams.
-    if (streams_) rt.fork_streams(*streams_);
-    else streams_ = rt.create_extra_streams(3);
-    const auto& s = *streams_;
+    // attention.rs:65-94: three Linear::forward, here as one batched launch
+    // on the primary stream when the three products share a shape.
     Projected p;
-    p.query = query_.forward(query_input, nullptr, rt, &s[0]);
-    p.key = key_.forward(key_value_input, nullptr, rt, &s[1]);
-    p.value = value_.forward(key_value_input, nullptr, rt, &s[2]);
+    Linear* lins[3] = {&query_, &key_, &value_};
+    const Matrix* ins[3] = {&query_input, &key_value_input, &key_value_input};
+    Matrix* outs[3] = {&p.query, &p.key, &p.value};
+    bool same = true;
+    for (int z = 0; z < 3; z++) {
+        require(ins[z]->cols() == lins[z]->weights().rows(), "input.cols() == weights.rows()");
+        *outs[z] = rt.new_uninit_matrix(ins[z]->rows(), lins[z]->weights().cols());
+        same = same && ins[z]->rows() == ins[0]->rows() && ins[z]->cols() == ins[0]->cols() &&
+               outs[z]->cols() == outs[0]->cols();
+    }
+    if (same) {
+        forge_gemm_problem probs[3];
+        for (int z = 0; z < 3; z++) probs[z] = lins[z]->forward_problem(*ins[z], *outs[z]);
+        check(forge_gemm_batch_f32(rt.raw(), nullptr, 0, 0, ins[0]->rows(), outs[0]->cols(),
+                                   ins[0]->cols(), 3, probs),
+              "qkv projection");
+    } else {
+        for (int z = 0; z < 3; z++) lins[z]->forward_into(*ins[z], nullptr, *outs[z], rt, nullptr);
+    }
     return p;
 }
 
-void QkvProjection::wait_for_query_key(CudaRuntime& rt) {
-    rt.join_streams({(*streams_)[0], (*streams_)[1]});
-}
+// The projections ran on the primary stream: nothing to join.
+void QkvProjection::wait_for_query_key(CudaRuntime&) {}
 
-void QkvProjection::wait_for_value(CudaRuntime& rt) { rt.join_streams({(*streams_)[2]}); }
+void QkvProjection::wait_for_value(CudaRuntime&) {}
 
 // ============================================================== Attention
 

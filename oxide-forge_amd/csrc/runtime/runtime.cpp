@@ -65,6 +65,14 @@ struct GemmArgs {
     float update_scale;
 };
 
+// Must match forge::GemmBatchArgs in csrc/kernels/gemm.hpp.
+constexpr int GEMM_BATCH_MAX = 8;
+struct GemmBatchArgs {
+    GemmArgs p[GEMM_BATCH_MAX];
+    int count;
+    int tiles;
+};
+
 // Must match forge::RowArgs in csrc/kernels/rows.hpp.
 struct RowArgs {
     const float* x;
@@ -534,16 +542,23 @@ const GemmConfig kTile128x128 = {"128x128x16_4x2", 128, 128, 16, 512};
 const GemmConfig kTile128x64 = {"128x64x16_2x2", 128, 64, 16, 256};
 const GemmConfig kGuard64 = {"64x64x16_2x2_g", 64, 64, 16, 256};
 
+// Unguarded tiles address the epilogue with 32-bit byte offsets, so their C
+// (and residual / aux / pre-activation) must hold fewer than 2^30 elements.
+constexpr size_t GEMM_OFF32_MAX = size_t(1) << 30;
+
 // Tile choice, measured on MI355X over the C3/C4/C5 GEMM shapes: the
 // 256x128 tile (8 waves of 64x64) is fastest whenever it still gives at
 // least one tile per CU; otherwise 128x128 (8 waves of 32x64) if that fills
-// the CUs, otherwise 128x64 (the most tiles).  Unaligned shapes, or shapes
-// the tiles do not divide, take the bounds-guarded 64x64 tile.
-const GemmConfig& choose_gemm(forge_runtime* rt, size_t M, size_t N, size_t K, bool aligned) {
+// the CUs, otherwise 128x64 (the most tiles).  Unaligned shapes, shapes the
+// tiles do not divide and matrices of 2^30 or more elements take the
+// bounds-guarded 64x64 tile.  `count` same-shape products share the launch.
+const GemmConfig& choose_gemm(forge_runtime* rt, size_t M, size_t N, size_t K, bool aligned,
+                              size_t count = 1) {
     auto fits = [&](const GemmConfig& c) {
-        return aligned && M % c.bm == 0 && N % c.bn == 0 && K % c.bk == 0;
+        return aligned && M % c.bm == 0 && N % c.bn == 0 && K % c.bk == 0 &&
+               M * N < GEMM_OFF32_MAX;
     };
-    auto tiles = [&](const GemmConfig& c) { return (M / c.bm) * (N / c.bn); };
+    auto tiles = [&](const GemmConfig& c) { return count * (M / c.bm) * (N / c.bn); };
     const size_t cus = rt->cu_count > 0 ? (size_t)rt->cu_count : 256;
     if (fits(kTile256x128) && tiles(kTile256x128) >= cus) return kTile256x128;
     if (fits(kTile128x128) && tiles(kTile128x128) >= cus) return kTile128x128;
@@ -551,15 +566,59 @@ const GemmConfig& choose_gemm(forge_runtime* rt, size_t M, size_t N, size_t K, b
     return kGuard64;
 }
 
-forge_status gemm_dispatch(forge_runtime* rt, forge_stream* s, int ta, int tb, forge_slice A,
-                           forge_slice B, forge_slice C, size_t M, size_t N, size_t K,
-                           const forge_gemm_epilogue* ep, bool plain_name) {
+// Split-K plan for one product, measured on MI355X (bench.py --sweep) over
+// the C3/C4/C5 shapes.  A split pays off when the output has too few tiles
+// to give every CU two waves' worth of work and K is long:
+//   - 256x128 tiles already fill the CUs: split in two only for K >= 8192
+//     (4096x2048x8192: 133.7 vs 131.6 TFLOP/s);
+//   - otherwise, for K >= 2048, four K slices of 256x128 tiles when that
+//     fills the CUs with slices of >= 1024 (2048x2048x4096: 125.0 vs 118.9),
+//     else four slices of 128x128 tiles (2048x1024x2048: 105.7 vs 98.4;
+//     2048x1024x4096: 117.3 vs 100.5);
+//   - no split for K < 2048 (2048x1024x1024: 93.2 unsplit, 85.6 split).
+// Returns the split count and sets *cfg to the tile to use.
+int choose_splits(forge_runtime* rt, size_t M, size_t N, size_t K, bool aligned,
+                  const GemmConfig** cfg) {
+    const size_t cus = rt->cu_count > 0 ? (size_t)rt->cu_count : 256;
+    auto fits = [&](const GemmConfig& c, size_t splits) {
+        return aligned && M % c.bm == 0 && N % c.bn == 0 && K % (splits * c.bk) == 0 &&
+               M * N < GEMM_OFF32_MAX;
+    };
+    auto tiles = [&](const GemmConfig& c) { return (M / c.bm) * (N / c.bn); };
+    if (fits(kTile256x128, 1) && tiles(kTile256x128) >= cus) {
+        if (K >= 8192 && fits(kTile256x128, 2)) {
+            *cfg = &kTile256x128;
+            return 2;
+        }
+        return 1;
+    }
+    if (K < 2048) return 1;
+    if (fits(kTile256x128, 4) && tiles(kTile256x128) * 4 >= cus && K / 4 >= 1024) {
+        *cfg = &kTile256x128;
+        return 4;
+    }
+    if (fits(kTile128x128, 4) && K / 4 >= 512) {
+        *cfg = &kTile128x128;
+        return 4;
+    }
+    return 1;
+}
+
+const char* gemm_ab(int ta, int tb) {
+    static const char ab[2][2][3] = {{"nn", "nt"}, {"tn", "tt"}};
+    return ab[ta ? 1 : 0][tb ? 1 : 0];
+}
+
+// Validates one product and fills its kernel arguments; *aligned reports
+// whether the unguarded tiles may read the operands.
+forge_status gemm_args(int ta, int tb, forge_slice A, forge_slice B, forge_slice C, size_t M,
+                       size_t N, size_t K, const forge_gemm_epilogue* ep, GemmArgs* out,
+                       bool* aligned) {
     if (!fits_int(M) || !fits_int(N) || !fits_int(K))
         return fail(FORGE_EINVAL, "gemm dimensions exceed 2^31-1");
     FORGE_TRY(need(A, M * K, "gemm A"));
     FORGE_TRY(need(B, K * N, "gemm B"));
     FORGE_TRY(need(C, M * N, "gemm C"));
-    if (M == 0 || N == 0) return FORGE_OK;
     GemmArgs a{};
     a.A = A.ptr;
     a.B = B.ptr;
@@ -571,8 +630,8 @@ forge_status gemm_dispatch(forge_runtime* rt, forge_stream* s, int ta, int tb, f
     a.ldb = tb ? (long long)K : (long long)N;
     a.ldc = (long long)N;
     a.alpha = 1.0f;
-    bool aligned = aligned16(A.ptr) && aligned16(B.ptr) && aligned16(C.ptr) && a.lda % 4 == 0 &&
-                   a.ldb % 4 == 0;
+    bool al = aligned16(A.ptr) && aligned16(B.ptr) && aligned16(C.ptr) && a.lda % 4 == 0 &&
+              a.ldb % 4 == 0;
     if (ep) {
         FORGE_TRY(need_opt(ep->bias, N, "gemm bias"));
         FORGE_TRY(need_opt(ep->residual, M * N, "gemm residual"));
@@ -580,23 +639,81 @@ forge_status gemm_dispatch(forge_runtime* rt, forge_stream* s, int ta, int tb, f
         FORGE_TRY(need_opt(ep->pre_out, M * N, "gemm pre_out"));
         if (ep->activation < FORGE_ACT_IDENTITY || ep->activation > FORGE_ACT_SILU)
             return fail(FORGE_EINVAL, "unknown activation %d", ep->activation);
+        if (ep->aux_activation < FORGE_ACT_IDENTITY || ep->aux_activation > FORGE_ACT_SILU)
+            return fail(FORGE_EINVAL, "unknown aux activation %d", ep->aux_activation);
         a.alpha = ep->alpha;
         a.bias = ep->bias.ptr;
         a.residual = ep->residual.ptr;
         a.aux = ep->aux_mul.ptr;
         a.pre_out = ep->pre_out.ptr;
         a.act = ep->activation;
-        if (ep->aux_activation < FORGE_ACT_IDENTITY || ep->aux_activation > FORGE_ACT_SILU)
-            return fail(FORGE_EINVAL, "unknown aux activation %d", ep->aux_activation);
         a.aux_act = ep->aux_activation;
         a.update = ep->update ? 1 : 0;
         a.update_scale = ep->update_scale;
     }
+    *out = a;
+    *aligned = al;
+    return FORGE_OK;
+}
+
+// Split-K: `splits` K slices of the product as one batched launch writing
+// raw partial products to the stream's workspace, then one kernel summing
+// them in slice order and applying a's epilogue.  Requires an unguarded
+// tile and K % (splits * bk) == 0.
+forge_status gemm_split_launch(forge_runtime* rt, forge_stream* s, int ta, int tb,
+                               const GemmArgs& a, const GemmConfig& cfg, int splits) {
+    const size_t mn = (size_t)a.M * (size_t)a.N;
+    float* ws = nullptr;
+    FORGE_TRY(workspace(rt, s, (size_t)splits * mn, &ws));
+    const int ks = a.K / splits;
+    GemmBatchArgs b{};
+    b.count = splits;
+    b.tiles = (a.M / cfg.bm) * (a.N / cfg.bn);
+    for (int z = 0; z < splits; z++) {
+        GemmArgs q{};
+        const long long k0 = (long long)z * ks;
+        q.A = ta ? a.A + k0 * a.lda : a.A + k0;
+        q.B = tb ? a.B + k0 : a.B + k0 * a.ldb;
+        q.C = ws + (size_t)z * mn;
+        q.M = a.M;
+        q.N = a.N;
+        q.K = ks;
+        q.lda = a.lda;
+        q.ldb = a.ldb;
+        q.ldc = a.N;
+        q.alpha = 1.0f;
+        b.p[z] = q;
+    }
+    char name[96];
+    snprintf(name, sizeof name, "forge_gemm_batch_%s_%s", gemm_ab(ta, tb), cfg.tag);
+    void* args[] = {&b};
+    FORGE_TRY(launch(rt, s, name, dim3((unsigned)(b.tiles * splits)), dim3(cfg.threads), 0,
+                     args));
+    const bool vec = a.N % 4 == 0;
+    const size_t items = vec ? mn / 4 : mn;
+    const unsigned grid = (unsigned)std::min<size_t>((items + 255) / 256, 8192);
+    const float* P = ws;
+    int sp = splits;
+    GemmArgs e = a;
+    void* rargs[] = {&P, &sp, &e};
+    return launch(rt, s, vec ? "forge_gemm_splitk_reduce_v" : "forge_gemm_splitk_reduce_s",
+                  dim3(grid), dim3(256), 0, rargs);
+}
+
+forge_status gemm_dispatch(forge_runtime* rt, forge_stream* s, int ta, int tb, forge_slice A,
+                           forge_slice B, forge_slice C, size_t M, size_t N, size_t K,
+                           const forge_gemm_epilogue* ep, bool plain_name) {
+    GemmArgs a{};
+    bool aligned = false;
+    FORGE_TRY(gemm_args(ta, tb, A, B, C, M, N, K, ep, &a, &aligned));
+    if (M == 0 || N == 0) return FORGE_OK;
+    const GemmConfig* split_cfg = nullptr;
+    const int splits = choose_splits(rt, M, N, K, aligned, &split_cfg);
+    if (splits > 1) return gemm_split_launch(rt, s, ta, tb, a, *split_cfg, splits);
     const GemmConfig& cfg = choose_gemm(rt, M, N, K, aligned);
     char name[96];
-    const char ab[2][2][3] = {{"nn", "nt"}, {"tn", "tt"}};
     const bool epi = !(plain_name && !ta && !tb);
-    snprintf(name, sizeof name, "forge_gemm_%s_%s%s", ab[ta ? 1 : 0][tb ? 1 : 0], cfg.tag,
+    snprintf(name, sizeof name, "forge_gemm_%s_%s%s", gemm_ab(ta, tb), cfg.tag,
              epi ? "_e" : "");
     unsigned tiles = (unsigned)(((M + cfg.bm - 1) / cfg.bm) * ((N + cfg.bn - 1) / cfg.bn));
     void* args[] = {&a};
@@ -800,7 +917,7 @@ extern "C" forge_status forge_gemm_f32_tile(forge_runtime* rt, forge_stream* s,
     FORGE_TRY(need(B, K * N, "gemm B"));
     FORGE_TRY(need(C, M * N, "gemm C"));
     if (!guarded && (M % bm || N % bn || K % bk || !aligned16(A.ptr) || !aligned16(B.ptr) ||
-                     !aligned16(C.ptr) || K % 4 || N % 4))
+                     !aligned16(C.ptr) || K % 4 || N % 4 || M * N >= GEMM_OFF32_MAX))
         return fail(FORGE_EINVAL, "shape %zux%zux%zu does not fit unguarded tile %s", M, N, K,
                     tile_tag);
     if (M == 0 || N == 0) return FORGE_OK;
@@ -820,6 +937,70 @@ extern "C" forge_status forge_gemm_f32_tile(forge_runtime* rt, forge_stream* s,
     unsigned tiles = (unsigned)(((M + bm - 1) / bm) * ((N + bn - 1) / bn));
     void* args[] = {&a};
     return launch(rt, s, name, dim3(tiles), dim3(wm * wn * 64), 0, args);
+}
+
+extern "C" forge_status forge_gemm_f32_split(forge_runtime* rt, forge_stream* s,
+                                             const char* tile_tag, int splits, forge_slice A,
+                                             forge_slice B, forge_slice C, size_t M, size_t N,
+                                             size_t K) {
+    if (!rt || !tile_tag) return fail(FORGE_EINVAL, "null argument");
+    const GemmConfig* cfg = nullptr;
+    for (const GemmConfig* c : {&kTile256x128, &kTile128x128, &kTile128x64})
+        if (strcmp(c->tag, tile_tag) == 0) cfg = c;
+    if (!cfg) return fail(FORGE_EINVAL, "tile %s has no batched instance", tile_tag);
+    if (splits < 1 || splits > GEMM_BATCH_MAX)
+        return fail(FORGE_EINVAL, "splits must be in [1, %d]", GEMM_BATCH_MAX);
+    GemmArgs a{};
+    bool aligned = false;
+    FORGE_TRY(gemm_args(0, 0, A, B, C, M, N, K, nullptr, &a, &aligned));
+    if (!aligned || M % cfg->bm || N % cfg->bn || K % ((size_t)splits * cfg->bk) ||
+        M * N >= GEMM_OFF32_MAX)
+        return fail(FORGE_EINVAL, "shape %zux%zux%zu does not fit tile %s with %d splits", M, N,
+                    K, tile_tag, splits);
+    if (M == 0 || N == 0) return FORGE_OK;
+    return gemm_split_launch(rt, s, 0, 0, a, *cfg, splits);
+}
+
+extern "C" forge_status forge_gemm_batch_f32(forge_runtime* rt, forge_stream* s, int trans_a,
+                                             int trans_b, size_t M, size_t N, size_t K,
+                                             size_t count, const forge_gemm_problem* problems) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    if (count > 0 && !problems) return fail(FORGE_EINVAL, "problems is null");
+    if (trans_a && trans_b) {
+        // No batched TT instance: one launch per product.
+        for (size_t z = 0; z < count; z++)
+            FORGE_TRY(gemm_dispatch(rt, s, 1, 1, problems[z].A, problems[z].B, problems[z].C, M,
+                                    N, K, &problems[z].epilogue, false));
+        return FORGE_OK;
+    }
+    GemmBatchArgs b{};
+    bool all_aligned = true;
+    for (size_t z = 0; z < count; z++) {
+        GemmArgs a{};
+        bool aligned = false;
+        FORGE_TRY(gemm_args(trans_a, trans_b, problems[z].A, problems[z].B, problems[z].C, M, N,
+                            K, &problems[z].epilogue, &a, &aligned));
+        all_aligned = all_aligned && aligned;
+        if (z < (size_t)GEMM_BATCH_MAX) b.p[z] = a;
+    }
+    if (count == 0 || M == 0 || N == 0) return FORGE_OK;
+    const GemmConfig& cfg = choose_gemm(rt, M, N, K, all_aligned, count);
+    const GemmConfig* split_cfg = nullptr;
+    // Shapes the single-product path splits in K are dispatched one by one,
+    // so every product equals its forge_gemm_ex_f32 result bit for bit.
+    const bool split = choose_splits(rt, M, N, K, all_aligned, &split_cfg) > 1;
+    if (count > (size_t)GEMM_BATCH_MAX || cfg.bm == kGuard64.bm || split) {
+        for (size_t z = 0; z < count; z++)
+            FORGE_TRY(gemm_dispatch(rt, s, trans_a, trans_b, problems[z].A, problems[z].B,
+                                    problems[z].C, M, N, K, &problems[z].epilogue, false));
+        return FORGE_OK;
+    }
+    b.count = (int)count;
+    b.tiles = (int)((M / cfg.bm) * (N / cfg.bn));
+    char name[96];
+    snprintf(name, sizeof name, "forge_gemm_batch_%s_%s", gemm_ab(trans_a, trans_b), cfg.tag);
+    void* args[] = {&b};
+    return launch(rt, s, name, dim3((unsigned)(b.tiles * count)), dim3(cfg.threads), 0, args);
 }
 
 extern "C" forge_status forge_transpose_f32(forge_runtime* rt, forge_stream* s, forge_slice in,

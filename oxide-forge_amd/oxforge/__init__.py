@@ -85,6 +85,12 @@ def _sl(a) -> Slice:
     return a.slice
 
 
+def _epilogue(alpha=1.0, bias=None, residual=None, aux_mul=None, pre_out=None,
+              activation=ACT_IDENTITY, update=False, update_scale=0.0, aux_activation=0):
+    return GemmEpilogue(alpha, _sl(bias), _sl(residual), _sl(aux_mul), _sl(pre_out), activation,
+                        1 if update else 0, update_scale, aux_activation)
+
+
 class Runtime:
     """forge_runtime: CudaRuntime (runtime.rs:34-45) behind the C ABI."""
 
@@ -204,10 +210,22 @@ class Runtime:
     def gemm_ex(self, A, B, C, M, N, K, trans_a=False, trans_b=False, alpha=1.0, bias=None,
                 residual=None, aux_mul=None, pre_out=None, activation=ACT_IDENTITY,
                 update=False, update_scale=0.0, aux_activation=0, stream=None) -> None:
-        ep = GemmEpilogue(alpha, _sl(bias), _sl(residual), _sl(aux_mul), _sl(pre_out),
-                          activation, 1 if update else 0, update_scale, aux_activation)
+        ep = _epilogue(alpha, bias, residual, aux_mul, pre_out, activation, update,
+                       update_scale, aux_activation)
         call("forge_gemm_ex_f32", self.handle, stream, int(trans_a), int(trans_b), A.slice,
              B.slice, C.slice, M, N, K, byref(ep))
+
+    def gemm_batch(self, problems, M, N, K, trans_a=False, trans_b=False, stream=None) -> None:
+        """problems: [(A, B, C, dict of gemm_ex epilogue keywords), ...]."""
+        arr = (_lib.GemmProblem * max(1, len(problems)))()
+        for z, (A, B, C, ep) in enumerate(problems):
+            arr[z] = _lib.GemmProblem(A.slice, B.slice, C.slice, _epilogue(**ep))
+        call("forge_gemm_batch_f32", self.handle, stream, int(trans_a), int(trans_b), M, N, K,
+             len(problems), arr)
+
+    def gemm_split(self, tile, splits, A, B, C, M, N, K, stream=None) -> None:
+        call("forge_gemm_f32_split", self.handle, stream, tile.encode(), splits, A.slice,
+             B.slice, C.slice, M, N, K)
 
     def transpose(self, x, out, rows, cols, stream=None) -> None:
         call("forge_transpose_f32", self.handle, stream, x.slice, out.slice, rows, cols)

@@ -66,6 +66,12 @@ class GemmEpilogue(ctypes.Structure):
     ]
 
 
+class GemmProblem(ctypes.Structure):
+    """forge_gemm_problem."""
+
+    _fields_ = [("A", Slice), ("B", Slice), ("C", Slice), ("epilogue", GemmEpilogue)]
+
+
 RT = c_void_p  # forge_runtime*
 ST = c_void_p  # forge_stream*
 
@@ -102,6 +108,10 @@ SIGNATURES = {
                           c_size_t, POINTER(GemmEpilogue)],
     "forge_gemm_f32_tile": [RT, ST, c_char_p, Slice, Slice, Slice, c_size_t, c_size_t,
                             c_size_t],
+    "forge_gemm_f32_split": [RT, ST, c_char_p, c_int, Slice, Slice, Slice, c_size_t, c_size_t,
+                             c_size_t],
+    "forge_gemm_batch_f32": [RT, ST, c_int, c_int, c_size_t, c_size_t, c_size_t, c_size_t,
+                             POINTER(GemmProblem)],
     "forge_transpose_f32": [RT, ST, Slice, Slice, c_size_t, c_size_t],
     "forge_softmax_rows": [RT, ST, Slice, c_size_t, c_size_t],
     "forge_softmax_rows_bwd": [RT, ST, Slice, Slice, Slice, c_size_t, c_size_t],

@@ -68,6 +68,10 @@ def dispatcher_kernel_names():
             names.append(f"forge_gemm_{ab}_{tag}_e")
     for tag in ("256x128x16_4x2", "128x128x16_4x2", "128x64x16_2x2", "64x64x16_2x2_g"):
         names.append(f"forge_gemm_nn_{tag}")
+    for ab in ("nn", "nt", "tn"):
+        for tag in ("256x128x16_4x2", "128x128x16_4x2", "128x64x16_2x2"):
+            names.append(f"forge_gemm_batch_{ab}_{tag}")
+    names += ["forge_gemm_splitk_reduce_v", "forge_gemm_splitk_reduce_s"]
     for op in ("softmax", "layer_norm", "rms_norm", "softmax_bwd", "layer_norm_bwd", "rms_norm_bwd"):
         for v in (1, 2, 4, 8, 16):
             names.append(f"forge_row_{op}_v{v}")

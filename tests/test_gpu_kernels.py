@@ -463,6 +463,67 @@ def test_softmax_bwd_scaled_equals_bwd_then_scale(rt):
     assert np.array_equal(a.numpy(), b.numpy())
 
 
+@pytest.mark.parametrize("tile,splits,M,N,K", [("256x128x16_4x2", 2, 256, 128, 512),
+                                               ("128x128x16_4x2", 4, 256, 256, 1024),
+                                               ("128x64x16_2x2", 3, 128, 128, 96),
+                                               ("128x128x16_4x2", 8, 128, 128, 128),
+                                               ("128x64x16_2x2", 1, 128, 64, 64)])
+def test_gemm_split_k_vs_oracle(rt, tile, splits, M, N, K):
+    """K slices summed in slice order: the same bar as any GEMM; one slice is
+    the plain product bit for bit."""
+    say(f"gemm split-K {tile} splits={splits} {M}x{N}x{K}")
+    A, B = orc.uniform((M, K), 5), orc.uniform((K, N), 6)
+    dA, dB, dC = rt.array(A), rt.array(B), rt.empty((M, N))
+    rt.gemm_split(tile, splits, dA, dB, dC, M, N, K)
+    C = dC.numpy()
+    ref = orc.gemm_f64(A, B)
+    absprod = np.abs(A).astype(np.float64) @ np.abs(B).astype(np.float64)
+    rel_max, comp = gemm_errors(C, ref, absprod)
+    assert rel_max <= 1e-4 and comp <= 1e-4, (rel_max, comp)
+    if splits == 1:
+        plain = rt.empty((M, N))
+        rt.gemm(dA, dB, plain, M, N, K)
+        assert np.array_equal(C, plain.numpy())
+    with pytest.raises(oxforge.ForgeError):
+        rt.gemm_split(tile, splits, dA, dB, dC, M, N, K + 16 * splits + 8)
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 128, 192), (70, 50, 33)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_batch_bit_identical_to_single(rt, M, N, K, ta, tb):
+    """Three products with different fused epilogues in one launch equal
+    three forge_gemm_ex_f32 calls bit for bit."""
+    say(f"gemm batch {M}x{N}x{K} ta={ta} tb={tb}")
+    rng = np.random.default_rng(M + 2 * ta + tb)
+
+    def mat(*shape):
+        return rng.uniform(-1, 1, shape).astype(np.float32)
+
+    As = [rt.array(mat(*((K, M) if ta else (M, K)))) for _ in range(3)]
+    Bs = [rt.array(mat(*((N, K) if tb else (K, N)))) for _ in range(3)]
+    bias, res, c0 = rt.array(mat(N)), rt.array(mat(M, N)), mat(M, N)
+    eps = [dict(bias=None, activation=oxforge.ACT_GELU),
+           dict(alpha=0.125, residual=res),
+           dict(update=True, update_scale=0.01)]
+    eps[0]["bias"] = bias
+    outs = {}
+    for mode in ("batch", "single"):
+        Cs = [rt.array(c0) for _ in range(3)]
+        pres = [rt.empty((M, N)) for _ in range(3)]
+        problems = []
+        for z in range(3):
+            ep = dict(eps[z], pre_out=pres[z])
+            problems.append((As[z], Bs[z], Cs[z], ep))
+        if mode == "batch":
+            rt.gemm_batch(problems, M, N, K, trans_a=bool(ta), trans_b=bool(tb))
+        else:
+            for A, B, C, ep in problems:
+                rt.gemm_ex(A, B, C, M, N, K, trans_a=bool(ta), trans_b=bool(tb), **ep)
+        outs[mode] = [c.numpy() for c in Cs] + [p.numpy() for p in pres]
+    for a, b in zip(outs["batch"], outs["single"]):
+        assert np.array_equal(a, b)
+
+
 @pytest.mark.parametrize("n", [1, 7, 1024, 100_003])
 def test_sgd_update_bit_exact(rt, n):
     """param - lr * grad with two roundings, as the reference's clone / scale /
