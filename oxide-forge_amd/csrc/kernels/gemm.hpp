@@ -378,11 +378,18 @@ __device__ __forceinline__ void splitk_reduce_body(const float* __restrict__ P, 
         const int row = (int)(e / p.N), col0 = (int)(e % p.N);
         float z[W];
         if constexpr (VEC) {
-            const float4 v = load_stream(P + e);
-            z[0] = v.x; z[1] = v.y; z[2] = v.z; z[3] = v.w;
-            for (int s = 1; s < splits; s++) {
-                const float4 u = load_stream(P + s * MN + e);
-                z[0] += u.x; z[1] += u.y; z[2] += u.z; z[3] += u.w;
+            // All slices are loaded before the sum (up to 8 in flight), then
+            // added in slice order.
+            float4 u[GEMM_BATCH_MAX];
+#pragma unroll
+            for (int s = 0; s < GEMM_BATCH_MAX; s++)
+                if (s < splits) u[s] = load_stream(P + s * MN + e);
+            z[0] = u[0].x; z[1] = u[0].y; z[2] = u[0].z; z[3] = u[0].w;
+#pragma unroll
+            for (int s = 1; s < GEMM_BATCH_MAX; s++) {
+                if (s < splits) {
+                    z[0] += u[s].x; z[1] += u[s].y; z[2] += u[s].z; z[3] += u[s].w;
+                }
             }
         } else {
             z[0] = P[e];

@@ -546,24 +546,38 @@ const GemmConfig kGuard64 = {"64x64x16_2x2_g", 64, 64, 16, 256};
 // (and residual / aux / pre-activation) must hold fewer than 2^30 elements.
 constexpr size_t GEMM_OFF32_MAX = size_t(1) << 30;
 
-// Tile choice, measured on MI355X over the C3/C4/C5 GEMM shapes: the
-// 256x128 tile (8 waves of 64x64) is fastest whenever it still gives at
-// least one tile per CU; otherwise 128x128 (8 waves of 32x64) if that fills
-// the CUs, otherwise 128x64 (the most tiles).  Unaligned shapes, shapes the
-// tiles do not divide and matrices of 2^30 or more elements take the
+// Tile choice.  Each unguarded tile has a measured full-device efficiency
+// (4096^3 on MI355X: 256x128 136.5, 128x128 133.3, 128x64 128.5 TFLOP/s),
+// scaled by how evenly its tiles spread over the CUs: t tiles occupy
+// ceil(t / CUs) rounds, so the balance is t / (CUs * ceil(t / CUs)).  The
+// best score wins (ties to the larger tile): 4096^3 -> 256x128, 2048x2048 ->
+// 128x128, 2048x1024 -> 128x64, and three 2048x1024 products in one batch
+// -> 128x64 (768 tiles, three per CU).  Unaligned shapes, shapes the tiles
+// do not divide and matrices of 2^30 or more elements take the
 // bounds-guarded 64x64 tile.  `count` same-shape products share the launch.
 const GemmConfig& choose_gemm(forge_runtime* rt, size_t M, size_t N, size_t K, bool aligned,
                               size_t count = 1) {
-    auto fits = [&](const GemmConfig& c) {
-        return aligned && M % c.bm == 0 && N % c.bn == 0 && K % c.bk == 0 &&
-               M * N < GEMM_OFF32_MAX;
-    };
-    auto tiles = [&](const GemmConfig& c) { return count * (M / c.bm) * (N / c.bn); };
     const size_t cus = rt->cu_count > 0 ? (size_t)rt->cu_count : 256;
-    if (fits(kTile256x128) && tiles(kTile256x128) >= cus) return kTile256x128;
-    if (fits(kTile128x128) && tiles(kTile128x128) >= cus) return kTile128x128;
-    if (fits(kTile128x64)) return kTile128x64;
-    return kGuard64;
+    struct Candidate {
+        const GemmConfig* cfg;
+        double efficiency;
+    };
+    const Candidate candidates[] = {
+        {&kTile256x128, 1.0}, {&kTile128x128, 0.977}, {&kTile128x64, 0.941}};
+    const GemmConfig* best = &kGuard64;
+    double best_score = 0.0;
+    for (const Candidate& c : candidates) {
+        const GemmConfig& g = *c.cfg;
+        if (!aligned || M % g.bm || N % g.bn || K % g.bk || M * N >= GEMM_OFF32_MAX) continue;
+        const size_t t = count * (M / g.bm) * (N / g.bn);
+        const size_t rounds = (t + cus - 1) / cus;
+        const double score = c.efficiency * (double)t / (double)(cus * rounds);
+        if (score > best_score + 1e-9) {
+            best = c.cfg;
+            best_score = score;
+        }
+    }
+    return *best;
 }
 
 // Split-K plan for one product, measured on MI355X (bench.py --sweep) over
