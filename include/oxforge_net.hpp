@@ -459,8 +459,7 @@ struct TransformerGrads {
     std::vector<Matrix> weights;
     std::vector<std::optional<Vector>> biases;
     std::optional<Vector> norm1_gamma, norm1_beta, norm2_gamma, norm2_beta;
-    Matrix position;
-    Matrix input;
+    Matrix position;  // also the input gradient (input and position enter as X + P)
 };
 
 // Attention (attention.rs:177-401).

@@ -846,13 +846,17 @@ Matrix TrainingTransformer::backward_impl(const Matrix& output_gradient, float l
     Matrix positioned_gradient =
         attention_.backward_self(first_output_gradient, learning_rate, rt, grads);
 
-    // Position matrix: P -= lr * dXp (encoder.rs:180-184).
-    Matrix input_gradient = rt.clone_matrix(positioned_gradient);
+    // Position matrix: P -= lr * dXp (encoder.rs:180-184: clone, scale,
+    // subtract) as one fused update.  dXp is not scaled in place, so it is
+    // returned as the input gradient without the reference's clone.
+    require(position_.rows() == positioned_gradient.rows() &&
+                position_.cols() == positioned_gradient.cols(),
+            "position gradient shape");
+    check(forge_sgd_update(rt.raw(), nullptr, position_.slice(), positioned_gradient.slice(),
+                           position_.len(), learning_rate),
+          "position update");
     if (grads) grads->position = rt.clone_matrix(positioned_gradient);
-    positioned_gradient.scale(learning_rate, rt);
-    position_.binary_assign(positioned_gradient, BinaryOp::Sub, rt);
-    if (grads) grads->input = rt.clone_matrix(input_gradient);
-    return input_gradient;
+    return positioned_gradient;
 }
 
 }  // namespace encoder
