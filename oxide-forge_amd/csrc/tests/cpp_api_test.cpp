@@ -1,0 +1,445 @@
+// cpp_api_test.cpp -- exercises the C++ drop-in API of include/oxforge_net.hpp
+// (CudaRuntime / Matrix / Vector / streams / pool / conversions / Linear /
+// MLP) on a GPU against host arithmetic written out here.  Built in-tree by
+// the Makefile as lib/oxforge_cpp_api_test; run by tests/test_gpu_cpp_api.py.
+// Exit status 0 when every check passes; one line per check group.
+//
+// Bars: bit-exact for copies, fills, transposes, conversions, single
+// rounded elementwise ops and integer-valued sums; 1e-4 relative-to-max for
+// the GEMM; 1e-5 absolute for softmax and the norms.
+#include "oxforge_net.hpp"
+
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <string>
+#include <vector>
+
+using namespace oxforge;
+
+static int g_failures = 0;
+
+#define CHECK(cond, what)                                                   \
+    do {                                                                    \
+        if (!(cond)) {                                                      \
+            std::printf("FAIL %s (%s:%d)\n", what, __FILE__, __LINE__);     \
+            g_failures++;                                                   \
+        }                                                                   \
+    } while (0)
+
+static std::vector<float> iota(size_t n, float scale = 1.0f, float offset = 0.0f) {
+    std::vector<float> v(n);
+    for (size_t i = 0; i < n; i++) v[i] = offset + scale * (float)((i * 7919u) % 97u);
+    return v;
+}
+
+static std::vector<float> uniform(size_t n, uint64_t seed) {
+    std::vector<float> v(n);
+    uint64_t x = seed * 0x9E3779B97F4A7C15ull + 1;
+    for (size_t i = 0; i < n; i++) {
+        x ^= x >> 12;
+        x ^= x << 25;
+        x ^= x >> 27;
+        v[i] = (float)((double)((x * 0x2545F4914F6CDD1Dull) >> 40) / (double)(1ull << 24)) * 2.0f - 1.0f;
+    }
+    return v;
+}
+
+static double max_abs(const std::vector<double>& v) {
+    double m = 0;
+    for (double x : v) m = std::fmax(m, std::fabs(x));
+    return m;
+}
+
+static void group(const char* name, int before) {
+    std::printf("%s %s\n", g_failures == before ? "PASS" : "FAIL", name);
+}
+
+int main() {
+    int dev = 0;
+    if (forge_device_count(&dev) != FORGE_OK || dev == 0) {
+        std::printf("no GPU\n");
+        return 2;
+    }
+    auto rt = CudaRuntime::create();
+    CudaRuntime& R = *rt;
+
+    // ---------------------------------------------------- host round trip
+    {
+        int f = g_failures;
+        auto h = uniform(37 * 19, 1);
+        Matrix m = R.matrix_from_host(h, 37, 19);
+        CHECK(m.rows() == 37 && m.cols() == 19 && m.len() == h.size(), "matrix shape");
+        CHECK(m.to_host(R) == h, "matrix round trip");
+        Vector v = R.vector_from_host(h);
+        CHECK(v.len() == h.size() && v.to_host(R) == h, "vector round trip");
+        group("round_trip", f);
+    }
+
+    // ----------------------------------------------------------- init types
+    {
+        int f = g_failures;
+        Vector seq = R.new_vector(InitType::Sequence, 1000);
+        Vector rev = R.new_vector(InitType::Reserve, 1000);
+        Vector zero = R.new_vector(InitType::Zero, 1000);
+        Vector rnd = R.new_vector(InitType::Random, 1000);
+        auto s = seq.to_host(R), r = rev.to_host(R), z = zero.to_host(R), q = rnd.to_host(R);
+        bool ok_s = true, ok_r = true, ok_z = true, ok_q = true;
+        for (size_t i = 0; i < 1000; i++) {
+            ok_s = ok_s && s[i] == (float)i;             // elementwise.rs:23-34 ascending
+            ok_r = ok_r && r[i] == (float)(1000 - i);    // descending: len - index
+            ok_z = ok_z && z[i] == 0.0f;
+            ok_q = ok_q && q[i] >= 0.0f && q[i] <= 1.0f;  // hash / u32::MAX
+        }
+        CHECK(ok_s, "InitType::Sequence");
+        CHECK(ok_r, "InitType::Reserve");
+        CHECK(ok_z, "InitType::Zero");
+        CHECK(ok_q, "InitType::Random range");
+        Matrix ms = R.new_matrix(InitType::Sequence, 4, 5);
+        auto mh = ms.to_host(R);
+        CHECK(ms.rows() == 4 && ms.cols() == 5 && mh[19] == 19.0f, "new_matrix Sequence");
+        group("init_types", f);
+    }
+
+    // ------------------------------------------------------------------ GEMM
+    {
+        int f = g_failures;
+        const size_t M = 70, K = 45, N = 33;
+        auto a = uniform(M * K, 2), b = uniform(K * N, 3);
+        Matrix A = R.matrix_from_host(a, M, K), B = R.matrix_from_host(b, K, N);
+        Matrix C = R.matrix_multiply(A, B);
+        auto c = C.to_host(R);
+        std::vector<double> ref(M * N, 0.0), err(M * N);
+        for (size_t i = 0; i < M; i++)
+            for (size_t k = 0; k < K; k++)
+                for (size_t j = 0; j < N; j++) ref[i * N + j] += (double)a[i * K + k] * b[k * N + j];
+        for (size_t i = 0; i < M * N; i++) err[i] = c[i] - ref[i];
+        CHECK(C.rows() == M && C.cols() == N, "matrix_multiply shape");
+        CHECK(max_abs(err) <= 1e-4 * max_abs(ref), "matrix_multiply vs f64");
+        // On an extra stream, forked from and joined to the primary.
+        auto streams = R.create_extra_streams(1);
+        Matrix C2 = R.matrix_multiply_on(&streams[0], A, B);
+        R.join_streams(streams);
+        CHECK(C2.to_host(R) == c, "matrix_multiply_on a forked stream");
+        group("gemm", f);
+    }
+
+    // ------------------------------------------------ elementwise, bit-exact
+    {
+        int f = g_failures;
+        const size_t rows = 13, cols = 21, n = rows * cols;
+        auto x = uniform(n, 4), y = uniform(n, 5);
+        for (auto& v : y) v = v == 0.0f ? 0.5f : v;
+        Matrix X = R.matrix_from_host(x, rows, cols), Y = R.matrix_from_host(y, rows, cols);
+        const BinaryOp ops[4] = {BinaryOp::Add, BinaryOp::Sub, BinaryOp::Mul, BinaryOp::Div};
+        for (BinaryOp op : ops) {
+            auto got = R.matrix_binary(X, Y, op).to_host(R);
+            bool ok = true;
+            for (size_t i = 0; i < n; i++) {
+                float want = op == BinaryOp::Add ? x[i] + y[i]
+                             : op == BinaryOp::Sub ? x[i] - y[i]
+                             : op == BinaryOp::Mul ? x[i] * y[i]
+                                                   : x[i] / y[i];
+                ok = ok && got[i] == want;
+            }
+            CHECK(ok, "matrix_binary");
+        }
+        Matrix S = R.clone_matrix(X);
+        S.scale(0.37f, R);
+        S.add_scalar(-1.5f, R);
+        auto sh = S.to_host(R);
+        bool ok = true;
+        for (size_t i = 0; i < n; i++) ok = ok && sh[i] == x[i] * 0.37f + -1.5f;
+        CHECK(ok, "scale + add_scalar");
+        CHECK(X.to_host(R) == x, "clone_matrix leaves the source");
+        Matrix T = R.clone_matrix(X);
+        T.binary_assign(Y, BinaryOp::Mul, R);
+        auto th = T.to_host(R);
+        ok = true;
+        for (size_t i = 0; i < n; i++) ok = ok && th[i] == x[i] * y[i];
+        CHECK(ok, "binary_assign");
+        auto rv = uniform(cols, 6);
+        Vector row = R.vector_from_host(rv);
+        Matrix Bc = R.clone_matrix(X);
+        Bc.binary_assign_by_rows(row, BinaryOp::Sub, R);
+        auto bh = Bc.to_host(R);
+        ok = true;
+        for (size_t i = 0; i < n; i++) ok = ok && bh[i] == x[i] - rv[i % cols];
+        CHECK(ok, "binary_assign_by_rows");
+        group("elementwise", f);
+    }
+
+    // --------------------------------------------------- rows: softmax, norms
+    {
+        int f = g_failures;
+        const size_t rows = 9, cols = 37;
+        auto x = uniform(rows * cols, 7), g = uniform(rows * cols, 8);
+        for (auto& v : x) v *= 3.0f;
+        std::vector<double> sm(rows * cols), ln(rows * cols), rms(rows * cols);
+        for (size_t r = 0; r < rows; r++) {
+            const float* xr = &x[r * cols];
+            double m = -1e300, s = 0, mean = 0, var = 0, q = 0;
+            for (size_t c = 0; c < cols; c++) m = std::fmax(m, xr[c]);
+            for (size_t c = 0; c < cols; c++) s += std::exp(xr[c] - m);
+            for (size_t c = 0; c < cols; c++) mean += xr[c];
+            mean /= cols;
+            for (size_t c = 0; c < cols; c++) var += (xr[c] - mean) * (xr[c] - mean);
+            var /= cols;
+            for (size_t c = 0; c < cols; c++) q += (double)xr[c] * xr[c];
+            for (size_t c = 0; c < cols; c++) {
+                sm[r * cols + c] = std::exp(xr[c] - m) / s;
+                ln[r * cols + c] = (xr[c] - mean) / std::sqrt(var + 1e-5);
+                rms[r * cols + c] = xr[c] / std::sqrt(q / cols + 1e-5);
+            }
+        }
+        auto close = [&](const std::vector<float>& a, const std::vector<double>& b) {
+            double e = 0;
+            for (size_t i = 0; i < a.size(); i++) e = std::fmax(e, std::fabs(a[i] - b[i]));
+            return e <= 1e-5;
+        };
+        Matrix P = R.matrix_from_host(x, rows, cols);
+        P.softmax_rows(R);
+        CHECK(close(P.to_host(R), sm), "softmax_rows");
+        Matrix L = R.matrix_from_host(x, rows, cols);
+        L.layer_norm(R);
+        CHECK(close(L.to_host(R), ln), "layer_norm");
+        Matrix Q = R.matrix_from_host(x, rows, cols);
+        Q.rms_norm(R);
+        CHECK(close(Q.to_host(R), rms), "rms_norm");
+        // Backward: softmax dx = p (g - sum p g); LN / RMS vs host f64.
+        Matrix G = R.matrix_from_host(g, rows, cols);
+        auto dsm = R.softmax_rows_backward(P, G).to_host(R);
+        auto ph = P.to_host(R);
+        std::vector<double> dref(rows * cols);
+        for (size_t r = 0; r < rows; r++) {
+            double s = 0;
+            for (size_t c = 0; c < cols; c++) s += (double)ph[r * cols + c] * g[r * cols + c];
+            for (size_t c = 0; c < cols; c++)
+                dref[r * cols + c] = ph[r * cols + c] * (g[r * cols + c] - s);
+        }
+        CHECK(close(dsm, dref), "softmax_rows_backward");
+        Matrix Xm = R.matrix_from_host(x, rows, cols);
+        auto dln = R.layer_norm_backward(Xm, G).to_host(R);
+        for (size_t r = 0; r < rows; r++) {
+            const float* xr = &x[r * cols];
+            const float* gr = &g[r * cols];
+            double mean = 0, var = 0, A = 0, Bs = 0;
+            for (size_t c = 0; c < cols; c++) mean += xr[c];
+            mean /= cols;
+            for (size_t c = 0; c < cols; c++) var += (xr[c] - mean) * (xr[c] - mean);
+            var /= cols;
+            const double rs = 1.0 / std::sqrt(var + 1e-5);
+            for (size_t c = 0; c < cols; c++) {
+                A += gr[c];
+                Bs += gr[c] * (xr[c] - mean) * rs;
+            }
+            for (size_t c = 0; c < cols; c++)
+                dref[r * cols + c] = rs / cols * (cols * gr[c] - A - (xr[c] - mean) * rs * Bs);
+        }
+        CHECK(close(dln, dref), "layer_norm_backward");
+        auto drms = R.rms_norm_backward(Xm, G).to_host(R);
+        for (size_t r = 0; r < rows; r++) {
+            const float* xr = &x[r * cols];
+            const float* gr = &g[r * cols];
+            double q = 0, d = 0;
+            for (size_t c = 0; c < cols; c++) {
+                q += (double)xr[c] * xr[c];
+                d += (double)xr[c] * gr[c];
+            }
+            const double inv = 1.0 / std::sqrt(q / cols + 1e-5);
+            for (size_t c = 0; c < cols; c++)
+                dref[r * cols + c] = gr[c] * inv - xr[c] * (d / cols * inv * inv * inv);
+        }
+        CHECK(close(drms, dref), "rms_norm_backward");
+        // Causal mask then softmax: masked entries are exactly zero and each
+        // row sums to one over its unmasked prefix.
+        std::vector<float> sq(x.begin(), x.begin() + rows * rows);
+        Matrix Cm = R.matrix_from_host(sq, rows, rows);
+        Cm.causal_mask(R);
+        Cm.softmax_rows(R);
+        auto ch = Cm.to_host(R);
+        bool ok_mask = true;
+        for (size_t r = 0; r < rows; r++) {
+            double s = 0;
+            for (size_t c = 0; c < rows; c++) {
+                if (c > r) ok_mask = ok_mask && ch[r * rows + c] == 0.0f;
+                s += ch[r * rows + c];
+            }
+            ok_mask = ok_mask && std::fabs(s - 1.0) <= 1e-5;
+        }
+        CHECK(ok_mask, "causal_mask + softmax_rows");
+        group("rows", f);
+    }
+
+    // ----------------------------------------------- sums and transposes
+    {
+        int f = g_failures;
+        const size_t rows = 300, cols = 33;
+        auto x = iota(rows * cols, 1.0f, -40.0f);
+        Matrix X = R.matrix_from_host(x, rows, cols);
+        auto sr = R.matrix_sum_rows(X).to_host(R);
+        auto sc = R.matrix_sum_cols(X).to_host(R);
+        bool ok_r = true, ok_c = true;
+        for (size_t r = 0; r < rows; r++) {
+            double s = 0;
+            for (size_t c = 0; c < cols; c++) s += x[r * cols + c];
+            ok_r = ok_r && sr[r] == (float)s;
+        }
+        for (size_t c = 0; c < cols; c++) {
+            double s = 0;
+            for (size_t r = 0; r < rows; r++) s += x[r * cols + c];
+            ok_c = ok_c && sc[c] == (float)s;
+        }
+        CHECK(ok_r, "matrix_sum_rows (integer data, exact)");
+        CHECK(ok_c, "matrix_sum_cols (integer data, exact)");
+        auto t = R.matrix_transpose(X);
+        auto th = t.to_host(R);
+        bool ok_t = t.rows() == cols && t.cols() == rows;
+        for (size_t r = 0; r < rows && ok_t; r++)
+            for (size_t c = 0; c < cols; c++) ok_t = ok_t && th[c * rows + r] == x[r * cols + c];
+        CHECK(ok_t, "matrix_transpose");
+        group("sums_transpose", f);
+    }
+
+    // ---------------------------------------------------- vector operations
+    {
+        int f = g_failures;
+        const size_t n = 5000;
+        auto a = iota(n, 1.0f, -48.0f), b = iota(n, 0.5f, 1.0f);
+        Vector A = R.vector_from_host(a), B = R.vector_from_host(b);
+        double s = 0, m = -1e300, d = 0;
+        for (size_t i = 0; i < n; i++) {
+            s += a[i];
+            m = std::fmax(m, a[i]);
+            d += (double)a[i] * b[i];
+        }
+        CHECK(A.sum(R) == (float)s, "Vector::sum (integer data, exact)");
+        CHECK(A.max(R) == (float)m, "Vector::max");
+        CHECK(std::fabs(A.dot(B, R) - d) <= 1e-6 * std::fabs(d) + 1e-3, "Vector::dot");
+        Vector C = R.clone_vector(A);
+        CHECK(A.equals(C, R), "Vector::equals (same)");
+        C.add_scalar(1.0f, R);
+        CHECK(!A.equals(C, R), "Vector::equals (different)");
+        auto sum_v = R.vector_add(A, B).to_host(R);
+        bool ok = true;
+        for (size_t i = 0; i < n; i++) ok = ok && sum_v[i] == a[i] + b[i];
+        CHECK(ok, "vector_add");
+        auto sm_in = uniform(200, 9);
+        Vector V = R.vector_from_host(sm_in);
+        V.softmax(R);
+        auto vh = V.to_host(R);
+        double mx = -1e300, z = 0, e = 0;
+        for (float v : sm_in) mx = std::fmax(mx, v);
+        for (float v : sm_in) z += std::exp(v - mx);
+        for (size_t i = 0; i < 200; i++) e = std::fmax(e, std::fabs(vh[i] - std::exp(sm_in[i] - mx) / z));
+        CHECK(e <= 1e-5, "Vector::softmax");
+        group("vectors", f);
+    }
+
+    // ------------------------------------------------------- conversions
+    {
+        int f = g_failures;
+        std::vector<Vector> vs;
+        for (int i = 0; i < 3; i++) vs.push_back(R.vector_from_host(iota(8, 1.0f, (float)(10 * i))));
+        Matrix Z = R.vector_zip(vs);
+        auto zh = Z.to_host(R);
+        bool ok = Z.rows() == 3 && Z.cols() == 8;
+        for (int i = 0; i < 3 && ok; i++) {
+            auto want = iota(8, 1.0f, (float)(10 * i));
+            for (int j = 0; j < 8; j++) ok = ok && zh[i * 8 + j] == want[j];
+        }
+        CHECK(ok, "vector_zip");
+        auto parts = R.matrix_split(Z);
+        ok = parts.size() == 3;
+        for (size_t i = 0; i < parts.size() && ok; i++) ok = parts[i].to_host(R) == iota(8, 1.0f, (float)(10 * i));
+        CHECK(ok, "matrix_split");
+        Matrix Bc = R.broadcast(vs[1], 4);
+        auto bh = Bc.to_host(R);
+        ok = Bc.rows() == 4 && Bc.cols() == 8;
+        for (int r = 0; r < 4 && ok; r++)
+            for (int j = 0; j < 8; j++) ok = ok && bh[r * 8 + j] == iota(8, 1.0f, 10.0f)[j];
+        CHECK(ok, "broadcast");
+        Vector first = R.extract_vector(R.clone_matrix(Z));
+        CHECK(first.to_host(R) == iota(8, 1.0f, 0.0f), "extract_vector (first row)");
+        // matrix_slice: [4, 6] into 2x3 tiles, row-major over tiles.
+        auto src = iota(24, 1.0f, 0.0f);
+        for (int i = 0; i < 24; i++) src[i] = (float)i;
+        Matrix S = R.matrix_from_host(src, 4, 6);
+        auto tiles = R.matrix_slice(S, 3, 2);
+        ok = tiles.size() == 4;
+        for (size_t t = 0; t < tiles.size() && ok; t++) {
+            auto th = tiles[t].to_host(R);
+            const size_t tr = t / 2, tc = t % 2;
+            for (size_t r = 0; r < 2; r++)
+                for (size_t c = 0; c < 3; c++)
+                    ok = ok && th[r * 3 + c] == src[(tr * 2 + r) * 6 + tc * 3 + c];
+        }
+        CHECK(ok, "matrix_slice");
+        Vector flat = R.matrix_into_vector(R.clone_matrix(S));
+        CHECK(flat.len() == 24 && flat.to_host(R) == src, "matrix_into_vector");
+        Matrix col = R.vector_into_matrix(std::move(flat));
+        CHECK(col.rows() == 24 && col.cols() == 1 && col.to_host(R) == src, "vector_into_matrix");
+        group("conversions", f);
+    }
+
+    // ------------------------------------------------------- buffer pool
+    {
+        int f = g_failures;
+        const size_t n = 12345;
+        R.reserve_buffers(n, 2);
+        DeviceBuffer a = R.get_uninit_buffer(n);
+        float* p = a.ptr();
+        R.recycle_buffer(std::move(a));
+        DeviceBuffer b = R.get_uninit_buffer(n);
+        CHECK(b.ptr() == p, "recycled buffer is reused");
+        DeviceBuffer z = R.get_zerod_buffer(n);
+        Vector zv(std::move(z));
+        bool ok = true;
+        for (float v : zv.to_host(R)) ok = ok && v == 0.0f;
+        CHECK(ok, "get_zerod_buffer");
+        Vector u = R.vector_from_host(iota(5, 1.0f, 1.0f)), w = R.vector_from_host(iota(3, 1.0f, 100.0f));
+        DeviceBuffer cat = R.concat_buffers({&u.buffer(), &w.buffer()});
+        Vector cv(std::move(cat));
+        auto ch = cv.to_host(R);
+        auto want = iota(5, 1.0f, 1.0f);
+        auto w2 = iota(3, 1.0f, 100.0f);
+        want.insert(want.end(), w2.begin(), w2.end());
+        CHECK(ch == want, "concat_buffers");
+        group("pool", f);
+    }
+
+    // ------------------------------------------------------ Linear and MLP
+    {
+        int f = g_failures;
+        const size_t B = 17, I = 24, O = 12;
+        auto x = uniform(B * I, 10), wv = uniform(I * O, 11), bv = uniform(O, 12);
+        Linear lin(R.matrix_from_host(wv, I, O), R.vector_from_host(bv), Activation::Relu);
+        Matrix X = R.matrix_from_host(x, B, I);
+        auto y = lin.forward(X, nullptr, R, nullptr).to_host(R);
+        std::vector<double> ref(B * O), err(B * O);
+        for (size_t i = 0; i < B; i++)
+            for (size_t j = 0; j < O; j++) {
+                double z = bv[j];
+                for (size_t k = 0; k < I; k++) z += (double)x[i * I + k] * wv[k * O + j];
+                ref[i * O + j] = z > 0 ? z : 0;
+            }
+        for (size_t i = 0; i < B * O; i++) err[i] = y[i] - ref[i];
+        CHECK(max_abs(err) <= 1e-4 * max_abs(ref), "Linear::forward (ReLU, bias)");
+        std::vector<Linear> layers;
+        layers.emplace_back(R.matrix_from_host(wv, I, O), std::nullopt, Activation::Identity);
+        InferenceMLP mlp(std::move(layers), std::nullopt);
+        auto y2 = mlp.forward(X, R).to_host(R);
+        for (size_t i = 0; i < B; i++)
+            for (size_t j = 0; j < O; j++) {
+                double z = 0;
+                for (size_t k = 0; k < I; k++) z += (double)x[i * I + k] * wv[k * O + j];
+                err[i * O + j] = y2[i * O + j] - z;
+            }
+        CHECK(max_abs(err) <= 1e-4 * 10.0, "InferenceMLP::forward");
+        group("executors", f);
+    }
+
+    R.sync();
+    std::printf("%s: %d failed check(s)\n", g_failures ? "FAILED" : "OK", g_failures);
+    return g_failures ? 1 : 0;
+}
