@@ -118,10 +118,12 @@ def test_gemm_full_size_sampled_rows(rt, M, N, K):
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1)])
-@pytest.mark.parametrize("M,N,K", [(256, 128, 64), (50, 70, 33)])
+@pytest.mark.parametrize("M,N,K", [(256, 128, 64), (50, 70, 33), (256, 128, 2048)])
 def test_gemm_epilogue_matches_unfused_bit_exact(rt, M, N, K, ta, tb):
     """Fused bias + residual + aux + activation + update equals the unfused
-    launch sequence of Linear::affine_on/activate_on/learn_on bit for bit."""
+    launch sequence of Linear::affine_on/activate_on/learn_on bit for bit.
+    256x128x2048 is computed as four K slices, so the split-K reduction's
+    epilogue is covered too."""
     say(f"gemm epilogue M={M} N={N} K={K} ta={ta} tb={tb}")
     A = orc.uniform((K, M) if ta else (M, K), 7)
     B = orc.uniform((N, K) if tb else (K, N), 8)
@@ -150,6 +152,18 @@ def test_gemm_epilogue_matches_unfused_bit_exact(rt, M, N, K, ta, tb):
                    residual=dres, aux_mul=daux, pre_out=dPre, activation=act)
         assert np.array_equal(dPre.numpy(), pre_ref), act
         assert np.array_equal(dY.numpy(), y_ref), act
+    # Z * act'(aux): the derivative step of Linear::backward fused.
+    for act, dop in [(oxforge.ACT_GELU, oxforge.MAP_GELU_D), (oxforge.ACT_RELU, oxforge.MAP_RELU_D),
+                     (oxforge.ACT_SILU, oxforge.MAP_SILU_D)]:
+        dZ = rt.empty((M, N))
+        rt.gemm_ex(dA, dB, dZ, M, N, K, trans_a=ta, trans_b=tb)
+        dD = rt.array(aux)
+        rt.map(dD, dop)
+        rt.binary_assign(dZ, dD, oxforge.MUL)
+        dY = rt.empty((M, N))
+        rt.gemm_ex(dA, dB, dY, M, N, K, trans_a=ta, trans_b=tb, aux_mul=daux,
+                   aux_activation=act)
+        assert np.array_equal(dY.numpy(), dZ.numpy()), act
     # SGD update: W - lr * (A B), as learn_on scales then subtracts
     lr = 1e-3
     dW = rt.array(W)
