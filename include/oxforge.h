@@ -38,7 +38,8 @@ typedef enum forge_status {
     FORGE_ENOMEM = 2,    /* device or host allocation failed             */
     FORGE_EHIP = 3,      /* a HIP runtime call failed                    */
     FORGE_ENOMODULE = 4, /* code object missing or a kernel not found    */
-    FORGE_ENODEV = 5     /* no HIP device / requested device absent      */
+    FORGE_ENODEV = 5,    /* no HIP device / requested device absent      */
+    FORGE_EIO = 6        /* a file could not be opened, read or written  */
 } forge_status;
 
 typedef struct forge_runtime forge_runtime;

@@ -120,6 +120,45 @@ forge_status forge_net_transformer_backward(forge_net_model *m, forge_slice dy,
 forge_status forge_net_transformer_param(forge_net_model *m, int slot,
                                          forge_slice *out);
 
+/* ------------------------------------------------------------ checkpoint */
+
+/* Checkpoint format version 1 (include/oxforge_checkpoint.hpp): <path>.toml
+ * metadata plus <path>.bin of little-endian f32 parameters.  A path without
+ * an extension gets ".toml"; another extension than ".toml" is FORGE_EINVAL
+ * (io.rs:20-29).  Invalid files are FORGE_EINVAL, unreadable or unwritable
+ * ones FORGE_EIO, each with a message in forge_last_error(). */
+enum forge_checkpoint_kind {
+    FORGE_CK_LINEAR = 0,               /* load_linear (model.rs:73-76)        */
+    FORGE_CK_MLP_INFERENCE = 1,        /* load_inference_mlp (model.rs:108)   */
+    FORGE_CK_MLP_TRAINING = 2,         /* load_training_mlp (model.rs:129)    */
+    FORGE_CK_ENCODER_INFERENCE = 3,    /* load_transformer (model.rs:150)     */
+    FORGE_CK_ENCODER_TRAINING = 4,     /* load_training_transformer (:186)    */
+    FORGE_CK_DECODER_INFERENCE = 5     /* extension: same transformer layout  */
+};
+
+/* dump_linear / dump_inference_mlp / dump_training_mlp / dump_transformer /
+ * dump_training_transformer (model.rs:53-207), chosen by the handle's model. */
+forge_status forge_net_checkpoint_save(forge_net_model *m, const char *path);
+/* load_* (model.rs:73-207) into a new handle of the given kind.  A
+ * transformer loads into a handle only with a two-layer feed-forward network
+ * and query/key width equal to the embedding (the parameter slots above);
+ * other shapes are FORGE_EINVAL here (the C++ API loads them all). */
+forge_status forge_net_checkpoint_load(forge_runtime *rt, const char *path,
+                                       int kind, forge_net_model **out_model);
+/* Validates metadata and data-file size without a device; copies the model
+ * type ("linear", "mlp" or "transformer", NUL-terminated) into model_type
+ * (capacity cap >= 12) and the parameter byte count into *data_bytes. */
+forge_status forge_checkpoint_inspect(const char *path, char *model_type,
+                                      size_t cap, uint64_t *data_bytes);
+/* The widths of a handle's model, for callers holding a loaded handle:
+ * Linear {in, out}; MLP {in, width of each layer}; transformer {seq, hidden,
+ * ffn, out}.  *count receives the number of widths (at most cap written). */
+forge_status forge_net_model_dims(forge_net_model *m, size_t *dims, size_t cap,
+                                  size_t *count);
+/* The descriptor of a transformer handle (as created or as loaded). */
+forge_status forge_net_transformer_describe(forge_net_model *m,
+                                            forge_transformer_desc *out);
+
 #ifdef __cplusplus
 }
 #endif

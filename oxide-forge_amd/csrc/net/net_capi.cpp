@@ -1,9 +1,11 @@
 // net_capi.cpp -- C entry points of include/oxforge_net.h over the C++
 // executors.  Exceptions become status codes; parameters are copied into
 // model-owned device buffers at creation.
+#include <cstring>
 #include <new>
 
 #include "oxforge_net.h"
+#include "oxforge_checkpoint.hpp"
 #include "oxforge_net.hpp"
 
 extern "C" void forge_internal_set_error(const char* message);
@@ -455,4 +457,115 @@ extern "C" forge_status forge_net_transformer_param(forge_net_model* m, int slot
         default: throw Error(FORGE_EINVAL, "unknown parameter slot");
         }
     });
+}
+
+// ============================================================== checkpoint
+
+extern "C" forge_status forge_net_checkpoint_save(forge_net_model* m, const char* path) {
+    if (!m || !path) return FORGE_EINVAL;
+    return guard([&] {
+        CudaRuntime& rt = *m->rt;
+        if (m->linear) checkpoint::dump_linear(*m->linear, path, rt);
+        else if (m->imlp) checkpoint::dump_inference_mlp(*m->imlp, path, rt);
+        else if (m->tmlp) checkpoint::dump_training_mlp(*m->tmlp, path, rt);
+        else if (m->enc_inf) checkpoint::dump_transformer(*m->enc_inf, path, rt);
+        else if (m->enc_train) checkpoint::dump_training_transformer(*m->enc_train, path, rt);
+        else if (m->dec_inf) checkpoint::dump_decoder_transformer(*m->dec_inf, path, rt);
+        else throw Error(FORGE_EINVAL, "empty model handle");
+    });
+}
+
+extern "C" forge_status forge_net_checkpoint_load(forge_runtime* rt, const char* path, int kind,
+                                                  forge_net_model** out_model) {
+    if (!rt || !path || !out_model) return FORGE_EINVAL;
+    *out_model = nullptr;
+    return guard([&] {
+        std::unique_ptr<forge_net_model> m(new_model(rt));
+        CudaRuntime& r = *m->rt;
+        switch (kind) {
+        case FORGE_CK_LINEAR: m->linear.reset(new Linear(checkpoint::load_linear(path, r))); break;
+        case FORGE_CK_MLP_INFERENCE:
+            m->imlp.reset(new InferenceMLP(checkpoint::load_inference_mlp(path, r)));
+            break;
+        case FORGE_CK_MLP_TRAINING:
+            m->tmlp.reset(new TrainingMlp(checkpoint::load_training_mlp(path, r)));
+            break;
+        case FORGE_CK_ENCODER_INFERENCE:
+        case FORGE_CK_ENCODER_TRAINING:
+        case FORGE_CK_DECODER_INFERENCE: {
+            const checkpoint::TransformerMetadata t = checkpoint::read_transformer_metadata(path);
+            const size_t hidden = t.position.cols;
+            require(t.feed_forward.layers.size() == 2,
+                    "a transformer handle needs a two-layer feed-forward network");
+            require(t.query.output_neurons == hidden,
+                    "a transformer handle needs query/key width equal to the embedding");
+            m->desc.seq = t.position.rows;
+            m->desc.hidden = hidden;
+            m->desc.ffn = t.feed_forward.layers[0].output_neurons;
+            m->desc.out = t.output.output_neurons;
+            m->desc.norm_type = t.normalization == NormType::Rms ? 0 : 1;
+            m->desc.qkv_streams = 0;
+            m->desc.ffn_activation = (int)t.feed_forward.layers[0].activation;
+            if (kind == FORGE_CK_ENCODER_INFERENCE) {
+                m->desc.kind = FORGE_TK_ENCODER_INFERENCE;
+                m->enc_inf.reset(
+                    new encoder::InferenceTransformer(checkpoint::load_transformer(path, r)));
+            } else if (kind == FORGE_CK_ENCODER_TRAINING) {
+                m->desc.kind = FORGE_TK_ENCODER_TRAINING;
+                m->enc_train.reset(new encoder::TrainingTransformer(
+                    checkpoint::load_training_transformer(path, r)));
+            } else {
+                m->desc.kind = FORGE_TK_DECODER_INFERENCE;
+                m->dec_inf.reset(new decoder::InferenceTransformer(
+                    checkpoint::load_decoder_transformer(path, r)));
+            }
+            break;
+        }
+        default: throw Error(FORGE_EINVAL, "unknown checkpoint kind");
+        }
+        r.sync();
+        *out_model = m.release();
+    });
+}
+
+extern "C" forge_status forge_checkpoint_inspect(const char* path, char* model_type, size_t cap,
+                                                 uint64_t* data_bytes) {
+    if (!path) return FORGE_EINVAL;
+    return guard([&] {
+        uint64_t bytes = 0;
+        const std::string type = checkpoint::inspect(path, &bytes);
+        if (model_type) {
+            require(cap > type.size(), "model_type buffer too small");
+            std::memcpy(model_type, type.c_str(), type.size() + 1);
+        }
+        if (data_bytes) *data_bytes = bytes;
+    });
+}
+
+extern "C" forge_status forge_net_model_dims(forge_net_model* m, size_t* dims, size_t cap,
+                                             size_t* count) {
+    if (!m || !count || (cap && !dims)) return FORGE_EINVAL;
+    return guard([&] {
+        std::vector<size_t> d;
+        if (m->linear) {
+            d = {m->linear->weights().rows(), m->linear->weights().cols()};
+        } else if (m->imlp || m->tmlp) {
+            MlpExecutor& ex = mlp_exec(m);
+            d.push_back(ex.layers().front().weights().rows());
+            for (const Linear& l : ex.layers()) d.push_back(l.weights().cols());
+        } else if (m->enc_inf || m->enc_train || m->dec_inf) {
+            d = {m->desc.seq, m->desc.hidden, m->desc.ffn, m->desc.out};
+        } else {
+            throw Error(FORGE_EINVAL, "empty model handle");
+        }
+        *count = d.size();
+        for (size_t i = 0; i < d.size() && i < cap; i++) dims[i] = d[i];
+    });
+}
+
+extern "C" forge_status forge_net_transformer_describe(forge_net_model* m,
+                                                       forge_transformer_desc* out) {
+    if (!m || !out || (!m->enc_inf && !m->enc_train && !m->dec_inf)) return FORGE_EINVAL;
+    *out = m->desc;
+    return FORGE_OK;
 }

@@ -232,6 +232,7 @@ extern "C" const char* forge_status_string(forge_status s) {
     case FORGE_EHIP: return "HIP runtime error";
     case FORGE_ENOMODULE: return "code object or kernel missing";
     case FORGE_ENODEV: return "no HIP device";
+    case FORGE_EIO: return "file I/O failed";
     }
     return "unknown status";
 }

@@ -7,7 +7,10 @@
 // Bars: bit-exact for copies, fills, transposes, conversions, single
 // rounded elementwise ops and integer-valued sums; 1e-4 relative-to-max for
 // the GEMM; 1e-5 absolute for softmax and the norms.
+#include "oxforge_checkpoint.hpp"
 #include "oxforge_net.hpp"
+
+#include <unistd.h>
 
 #include <cmath>
 #include <cstdio>
@@ -437,6 +440,79 @@ int main() {
             }
         CHECK(max_abs(err) <= 1e-4 * 10.0, "InferenceMLP::forward");
         group("executors", f);
+    }
+
+    // ---------------------------------------------------------- checkpoint
+    // Shapes only the C++ API can hold: a three-layer feed-forward network
+    // with a residual, query/key narrower than the embedding.
+    {
+        int f = g_failures;
+        const char* tmp = std::getenv("TMPDIR");
+        const std::string base = std::string(tmp && *tmp ? tmp : "/tmp") + "/oxforge_ckpt_" +
+                                 std::to_string((long)getpid());
+        const size_t S = 24, H = 32, QK = 16, F = 48, O = 8;
+        auto lin = [&](size_t in, size_t out, uint64_t seed, bool bias, Activation a) {
+            auto w = uniform(in * out, seed);
+            for (auto& v : w) v *= 0.3f;
+            std::optional<Vector> b;
+            if (bias) b = R.vector_from_host(uniform(out, seed + 100));
+            return Linear(R.matrix_from_host(w, in, out), std::move(b), a);
+        };
+        auto layers = [&]() {
+            std::vector<Linear> l;
+            l.push_back(lin(H, F, 31, true, Activation::Gelu));
+            l.push_back(lin(F, F, 32, false, Activation::Silu));
+            l.push_back(lin(F, H, 33, true, Activation::Identity));
+            return l;
+        };
+        auto norm = [&](uint64_t seed) {
+            Normalization n;
+            n.kind = NormType::Layer;
+            auto g = uniform(H, seed);
+            for (auto& v : g) v = 1.0f + 0.1f * v;
+            n.gamma = R.vector_from_host(g);
+            n.beta = R.vector_from_host(uniform(H, seed + 1));
+            return n;
+        };
+        encoder::InferenceTransformer t(
+            lin(H, QK, 21, true, Activation::Identity), lin(H, QK, 22, true, Activation::Identity),
+            lin(H, H, 23, false, Activation::Identity), R.matrix_from_host(uniform(S * H, 24), S, H),
+            InferenceMLP(layers(), std::make_pair((size_t)0, (size_t)3)),
+            lin(H, O, 25, true, Activation::Identity), std::nullopt, NormType::Layer, norm(40),
+            norm(50));
+        Matrix X = R.matrix_from_host(uniform(S * H, 26), S, H);
+        auto want = t.forward(X, R).to_host(R);
+        checkpoint::dump_transformer(t, base, R);
+        const checkpoint::TransformerMetadata md = checkpoint::read_transformer_metadata(base);
+        CHECK(md.feed_forward.layers.size() == 3 && md.feed_forward.residual &&
+                  md.feed_forward.residual->end == 3 && md.query.output_neurons == QK &&
+                  md.norm2_beta && md.feed_forward.layers[1].activation == Activation::Silu,
+              "transformer metadata");
+        uint64_t bytes = 0;
+        CHECK(checkpoint::inspect(base + ".toml", &bytes) == "transformer" &&
+                  bytes == md.norm2_beta->byte_end,
+              "inspect");
+        encoder::InferenceTransformer back = checkpoint::load_transformer(base, R);
+        CHECK(back.forward(X, R).to_host(R) == want, "load_transformer forward bit-identical");
+        encoder::TrainingTransformer train = checkpoint::load_training_transformer(base, R);
+        CHECK(train.forward(X, R).to_host(R) == want, "load_training_transformer forward");
+        bool refused = false;
+        try {
+            checkpoint::load_linear(base, R);
+        } catch (const Error& e) {
+            refused = e.status() == FORGE_EINVAL;
+        }
+        CHECK(refused, "model type mismatch refused");
+        Linear l = lin(H, O, 60, true, Activation::Relu);
+        checkpoint::dump_linear(l, base + "_lin.toml", R);
+        Linear l2 = checkpoint::load_linear(base + "_lin", R);
+        CHECK(l2.weights().to_host(R) == l.weights().to_host(R) &&
+                  l2.bias()->to_host(R) == l.bias()->to_host(R) &&
+                  l2.activation() == Activation::Relu,
+              "Linear round trip");
+        for (const char* suffix : {".toml", ".bin", "_lin.toml", "_lin.bin"})
+            std::remove((base + suffix).c_str());
+        group("checkpoint", f);
     }
 
     R.sync();

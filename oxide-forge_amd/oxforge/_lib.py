@@ -22,6 +22,7 @@ FORGE_ENOMEM = 2
 FORGE_EHIP = 3
 FORGE_ENOMODULE = 4
 FORGE_ENODEV = 5
+FORGE_EIO = 6
 
 # forge_binary_op (BinaryOp, cuda.rs:3-10)
 ADD, SUB, MUL, DIV = 0, 1, 2, 3

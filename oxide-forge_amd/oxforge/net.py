@@ -2,7 +2,8 @@
 from __future__ import annotations
 
 import ctypes
-from ctypes import POINTER, byref, c_float, c_int, c_long, c_size_t, c_void_p
+import os
+from ctypes import POINTER, byref, c_char_p, c_float, c_int, c_long, c_size_t, c_uint64, c_void_p
 
 import numpy as np
 
@@ -13,6 +14,9 @@ TP_SLOTS = ["WQ", "BQ", "WK", "BK", "WV", "BV", "POS", "W1", "B1", "W2", "B2", "
             "G1", "BE1", "G2", "BE2"]
 ENCODER_INFERENCE, ENCODER_TRAINING, DECODER_INFERENCE = 0, 1, 2
 RMS, LAYER = 0, 1
+# forge_checkpoint_kind
+(CK_LINEAR, CK_MLP_INFERENCE, CK_MLP_TRAINING, CK_ENCODER_INFERENCE, CK_ENCODER_TRAINING,
+ CK_DECODER_INFERENCE) = range(6)
 
 
 class TransformerDesc(ctypes.Structure):
@@ -41,6 +45,11 @@ SIGNATURES = {
     "forge_net_transformer_forward": [c_void_p, Slice, Slice],
     "forge_net_transformer_backward": [c_void_p, Slice, c_float, Slice, POINTER(Slice)],
     "forge_net_transformer_param": [c_void_p, c_int, POINTER(Slice)],
+    "forge_net_checkpoint_save": [c_void_p, c_char_p],
+    "forge_net_checkpoint_load": [c_void_p, c_char_p, c_int, POINTER(c_void_p)],
+    "forge_checkpoint_inspect": [c_char_p, c_char_p, c_size_t, POINTER(c_uint64)],
+    "forge_net_model_dims": [c_void_p, POINTER(c_size_t), c_size_t, POINTER(c_size_t)],
+    "forge_net_transformer_describe": [c_void_p, POINTER(TransformerDesc)],
 }
 
 _declared = False
@@ -89,6 +98,20 @@ class _Model:
         except Exception:
             pass
 
+    def save(self, path):
+        """dump_* (model.rs:53-207): writes <path>.toml and <path>.bin."""
+        call("forge_net_checkpoint_save", self.h, os.fsencode(path))
+
+    def _dims(self):
+        cap = 64
+        dims = (c_size_t * cap)()
+        n = c_size_t()
+        call("forge_net_model_dims", self.h, dims, cap, byref(n))
+        if n.value > cap:
+            dims = (c_size_t * n.value)()
+            call("forge_net_model_dims", self.h, dims, n.value, byref(n))
+        return [int(d) for d in dims[:n.value]]
+
 
 class Linear(_Model):
     """Linear (linear.rs:72-532) on device; weights [in, out]."""
@@ -103,6 +126,9 @@ class Linear(_Model):
         dW.recycle()
         if db is not None:
             db.recycle()
+
+    def _describe(self):
+        self.n_in, self.n_out = self._dims()
 
     def forward(self, X, R=None, pre_out=None, Y=None):
         rows = X.shape[0]
@@ -154,6 +180,9 @@ class Mlp(_Model):
             if b is not None:
                 b.recycle()
 
+    def _describe(self):
+        self.dims = self._dims()
+
     def forward(self, X):
         Y = self.rt.empty((X.shape[0], self.dims[-1]))
         call("forge_net_mlp_forward", self.h, X.slice, X.shape[0], Y.slice)
@@ -179,16 +208,25 @@ class Transformer(_Model):
         super().__init__(rt)
         self.desc = TransformerDesc(seq, hidden, ffn, out, norm_type, kind, int(qkv_streams),
                                     ffn_activation)
-        self.shapes = {"WQ": (hidden, hidden), "BQ": (hidden,), "WK": (hidden, hidden),
-                       "BK": (hidden,), "WV": (hidden, hidden), "BV": (hidden,),
-                       "POS": (seq, hidden), "W1": (hidden, ffn), "B1": (ffn,),
-                       "W2": (ffn, hidden), "B2": (hidden,), "WO": (hidden, out), "BO": (out,),
-                       "G1": (hidden,), "BE1": (hidden,), "G2": (hidden,), "BE2": (hidden,)}
+        self._set_shapes()
         dev = {k: rt.array(v) for k, v in params.items() if v is not None}
         slots = (Slice * len(TP_SLOTS))(*[_sl(dev.get(k)) for k in TP_SLOTS])
         call("forge_net_transformer_create", rt.handle, byref(self.desc), slots, byref(self.h))
         for d in dev.values():
             d.recycle()
+
+    def _set_shapes(self):
+        seq, hidden, ffn, out = self.desc.seq, self.desc.hidden, self.desc.ffn, self.desc.out
+        self.shapes = {"WQ": (hidden, hidden), "BQ": (hidden,), "WK": (hidden, hidden),
+                       "BK": (hidden,), "WV": (hidden, hidden), "BV": (hidden,),
+                       "POS": (seq, hidden), "W1": (hidden, ffn), "B1": (ffn,),
+                       "W2": (ffn, hidden), "B2": (hidden,), "WO": (hidden, out), "BO": (out,),
+                       "G1": (hidden,), "BE1": (hidden,), "G2": (hidden,), "BE2": (hidden,)}
+
+    def _describe(self):
+        self.desc = TransformerDesc()
+        call("forge_net_transformer_describe", self.h, byref(self.desc))
+        self._set_shapes()
 
     def forward(self, X, Y=None):
         Y = Y or self.rt.empty((self.desc.seq, self.desc.out))
@@ -208,3 +246,32 @@ class Transformer(_Model):
         sl = Slice()
         call("forge_net_transformer_param", self.h, TP_SLOTS.index(name), byref(sl))
         return _read(self.rt, sl, self.shapes[name]) if sl.ptr else None
+
+
+_KIND_CLASS = {CK_LINEAR: Linear, CK_MLP_INFERENCE: Mlp, CK_MLP_TRAINING: Mlp,
+               CK_ENCODER_INFERENCE: Transformer, CK_ENCODER_TRAINING: Transformer,
+               CK_DECODER_INFERENCE: Transformer}
+
+
+def load(rt, path, kind):
+    """load_* (model.rs:73-207): a new model of `kind` (a CK_* constant) from
+    <path>.toml and its data file."""
+    _declare()
+    if kind not in _KIND_CLASS:
+        raise ValueError(f"unknown checkpoint kind {kind}")
+    h = c_void_p()
+    call("forge_net_checkpoint_load", rt.handle, os.fsencode(path), kind, byref(h))
+    model = _KIND_CLASS[kind].__new__(_KIND_CLASS[kind])
+    _Model.__init__(model, rt)
+    model.h = h
+    model._describe()
+    return model
+
+
+def inspect(path):
+    """Validates a checkpoint without a device: (model_type, data_bytes)."""
+    _declare()
+    buf = ctypes.create_string_buffer(16)
+    n = c_uint64()
+    call("forge_checkpoint_inspect", os.fsencode(path), buf, len(buf), byref(n))
+    return buf.value.decode(), int(n.value)
