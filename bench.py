@@ -282,7 +282,8 @@ def cpu_transformer_baseline(orc):
 
 
 def sweep(rt, orc, steps, warmup):
-    """Times every plain GEMM tile instance on the two C3 shapes."""
+    """Times every plain GEMM tile instance and the split-K candidates on the
+    C3, C4 and C5 GEMM shapes."""
     import oxforge
     from oxforge import _lib
 
@@ -299,9 +300,8 @@ def sweep(rt, orc, steps, warmup):
         A = orc.uniform((M, K), 3)
         B = orc.uniform((K, N), 4)
         dA, dB, dC = rt.array(A), rt.array(B), rt.empty((M, N))
-        for tag in ["128x128x16_2x2", "128x128x32_2x2", "128x64x16_2x2", "256x128x16_2x2",
-                    "128x256x16_2x2", "256x128x16_4x2", "128x256x16_2x4", "256x256x16_4x4",
-                    "256x128x32_4x2", "128x128x16_4x2", "128x64x16_2x1", "64x64x16_1x1"]:
+        for tag in ["128x256x32_x", "256x128x32_x", "128x128x32_x", "128x128x64_x",
+                    "128x64x32_x", "64x128x32_x", "64x64x32_x"]:
             key = f"{M}x{N}x{K}:{tag}"
 
             def fn(i, tag=tag.encode()):
@@ -316,7 +316,7 @@ def sweep(rt, orc, steps, warmup):
             res[key] = round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 2)
             log(f"sweep {key}: {res[key]}")
         # Split-K candidates for the shapes with few output tiles.
-        for tag in ["256x128x16_4x2", "128x128x16_4x2", "128x64x16_2x2"]:
+        for tag in ["128x128x32_x", "128x64x32_x", "64x128x32_x", "64x64x32_x"]:
             for splits in (2, 4):
                 key = f"{M}x{N}x{K}:{tag}:split{splits}"
                 try:
@@ -441,7 +441,7 @@ def main() -> int:
     M = N = K = 4096
     log("gemm 4096^3")
     tflops, ms = gemm_tflops(rt, orc, M, N, K, args.steps, args.warmup)
-    kernel = "forge_gemm_nn_256x128x16_4x2"
+    kernel = "forge_gemm_nn_128x256x32_x"
     traffic = load_traffic(kernel)
     line = {
         "metric": METRIC,

@@ -177,11 +177,12 @@ forge_status forge_fill(forge_runtime *rt, forge_stream *stream,
 
 /* matrix_multiply / matrix_multiply_into_on (matrix.rs:113-176, kernel
  * gemm.rs:202-373): C[M,N] = A[M,K] * B[K,N], row-major, C overwritten.
- * True fp32 (v_mfma_f32_32x32x2_f32), not the reference's TF32.  Any
- * M, N, K >= 0 (the reference asserts multiples of 16).  Outputs with too
- * few tiles to fill the device and K >= 2048 are computed as K slices summed
- * in slice order (deterministic; the choice depends only on the shape and
- * alignment, the same for this call and forge_gemm_ex_f32). */
+ * True fp32 (v_mfma_f32_16x16x4_f32; v_mfma_f32_32x32x2_f32 in the guarded
+ * fallback), not the reference's TF32.  Any M, N, K >= 0 (the reference
+ * asserts multiples of 16).  Outputs whose tiles leave three quarters of the
+ * CUs idle, with K >= 2048, are computed as K slices summed in slice order
+ * (deterministic; the choice depends only on the shape and alignment, the
+ * same for this call and forge_gemm_ex_f32). */
 forge_status forge_gemm_f32(forge_runtime *rt, forge_stream *stream,
                             forge_slice A, forge_slice B, forge_slice C,
                             size_t M, size_t N, size_t K);
@@ -223,10 +224,12 @@ forge_status forge_gemm_ex_f32(forge_runtime *rt, forge_stream *stream,
                                const forge_gemm_epilogue *epilogue);
 
 /* Tuning entry point (no reference counterpart): forge_gemm_f32 with an
- * explicit plain tile instance, tile_tag "<BM>x<BN>x<BK>_<WM>x<WN>" (for
- * example "128x128x16_2x2").  Unguarded tiles require M % BM == N % BN ==
- * K % BK == 0 and 16-byte aligned operands; anything else is FORGE_EINVAL.
- * Used by the benchmark's tile sweep. */
+ * explicit plain tile instance: "<BM>x<BN>x<BK>_x" for the unguarded
+ * four-wave tiles (128x256x32, 256x128x32, 128x128x32, 128x128x64,
+ * 128x64x32, 64x128x32, 64x64x32) or "64x64x16_2x2_g" for the guarded one.
+ * Unguarded tiles require M % BM == N % BN == K % BK == 0 and 16-byte
+ * aligned operands; anything else is FORGE_EINVAL.  Used by the benchmark's
+ * tile sweep. */
 forge_status forge_gemm_f32_tile(forge_runtime *rt, forge_stream *stream,
                                  const char *tile_tag, forge_slice A,
                                  forge_slice B, forge_slice C, size_t M,
@@ -234,13 +237,24 @@ forge_status forge_gemm_f32_tile(forge_runtime *rt, forge_stream *stream,
 
 /* Tuning entry point (no reference counterpart): forge_gemm_f32 computed as
  * `splits` K slices (one batched launch) plus a reduction in slice order,
- * with tile "256x128x16_4x2", "128x128x16_4x2" or "128x64x16_2x2".  Requires
- * M % BM == N % BN == K % (splits * BK) == 0, 16-byte aligned operands and
- * 1 <= splits <= 8.  Used by the benchmark's sweep. */
+ * with tile "128x128x32_x", "128x64x32_x", "64x128x32_x" or "64x64x32_x".
+ * Requires M % BM == N % BN == K % (splits * BK) == 0, 16-byte aligned
+ * operands and 1 <= splits <= 8.  Used by the benchmark's sweep. */
 forge_status forge_gemm_f32_split(forge_runtime *rt, forge_stream *stream,
                                   const char *tile_tag, int splits, forge_slice A,
                                   forge_slice B, forge_slice C, size_t M, size_t N,
                                   size_t K);
+
+/* Testing entry point (no reference counterpart): forge_gemm_ex_f32 through
+ * the fused-epilogue instance of one named tile ("128x128x32_x",
+ * "128x64x32_x", "64x128x32_x", "64x64x32_x" or "64x64x16_2x2_g"), so every
+ * instance the dispatcher can pick is testable at small shapes.  The same
+ * shape and alignment rules as forge_gemm_f32_tile. */
+forge_status forge_gemm_ex_f32_tile(forge_runtime *rt, forge_stream *stream,
+                                    const char *tile_tag, int trans_a, int trans_b,
+                                    forge_slice A, forge_slice B, forge_slice C,
+                                    size_t M, size_t N, size_t K,
+                                    const forge_gemm_epilogue *epilogue);
 
 /* One product of a batch: operands and its own fused epilogue. */
 typedef struct forge_gemm_problem {

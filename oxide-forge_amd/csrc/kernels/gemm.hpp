@@ -1,4 +1,7 @@
-// gemm.hpp -- fp32 GEMM on CDNA4 matrix cores.
+// gemm.hpp -- fp32 GEMM on CDNA4 matrix cores: the shared GEMM argument
+// structs, tile ordering and split-K reduction, and the bounds-guarded
+// kernel body that serves shapes or alignments the unguarded four-wave tiles
+// (gemm_x.hpp) cannot take.
 //
 // Replaces matrix_multiply_device (reference gemm.rs:202-373, TF32 mma.sync)
 // with true fp32 v_mfma_f32_32x32x2_f32.  Semantics follow the strict-fp32

@@ -1,0 +1,438 @@
+// gemm_x.hpp -- fp32 GEMM on CDNA4 matrix cores, four-wave layout with
+// v_mfma_f32_16x16x4_f32 and 128-bit LDS operand reads.
+//
+// Same contract as gemm_body (gemm.hpp): C = A * B row-major, f32 accumulate,
+// the same fused epilogue; unguarded (M % BM == N % BN == K % BK == 0,
+// 16-byte aligned operands).
+//
+// Structure
+//   - A workgroup of four waves (2 x 2) computes a BM x BN tile; each wave
+//     owns a (BM/2) x (BN/2) sub-tile of FM x FN blocks of 16 x 16, whose
+//     accumulators (four floats per lane per block) stay in registers.
+//   - One MFMA sums four k values, lane group kq = lane / 16 supplying one.
+//     Inside a 16-wide k chunk, sub-step s (0..3) gives lane group kq the
+//     value k = 4 kq + s.  A lane's operands for a whole chunk are therefore
+//     one 128-bit LDS read per block for an operand that is k-contiguous in
+//     LDS (A, or B^T), and one 128-bit read per sub-step for an operand that
+//     is m/n-contiguous (B, or A^T).  For the latter the four floats of a
+//     read belong to four different blocks: block 4g + e holds rows (or
+//     columns) base + 64 g + 4 i + e for MFMA index i.  The epilogue undoes
+//     this mapping, and the four columns of a lane become one 128-bit store.
+//   - K advances in BK slabs through two LDS buffers.  The next slab is
+//     loaded from global memory into registers while the current one is
+//     multiplied, then written to the other buffer: one barrier per slab.
+//     Operand reads for chunk c + 1 are issued before the MFMAs of chunk c.
+//   - LDS keeps the global orientation of each slab with a 4-float row pad:
+//     k-contiguous rows then start 4 banks apart, so sixteen lanes reading
+//     sixteen rows hit distinct banks; m/n-contiguous reads are contiguous.
+#pragma once
+#include "gemm.hpp"
+
+namespace forge {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+template <int F>
+struct XVec {
+    // Floats per 128/64/32-bit operand read of an m/n-contiguous operand.
+    static constexpr int W = F >= 4 ? 4 : F;
+    static_assert(F % W == 0, "block count must be a multiple of the read width");
+};
+
+// Row (or column) of MFMA index i of block b in a wave sub-tile starting at
+// base: k-contiguous operands keep blocks contiguous, m/n-contiguous ones
+// interleave them W at a time.
+template <bool KC, int F>
+__device__ __forceinline__ int x_index(int base, int b, int i) {
+    if constexpr (KC) {
+        return base + 16 * b + i;
+    } else {
+        constexpr int W = XVec<F>::W;
+        return base + 16 * W * (b / W) + W * i + (b % W);
+    }
+}
+
+// Direct global -> LDS slab loads (global_load_lds_dwordx4): each wave
+// instruction fills 1 KiB of LDS, 16 bytes per lane in lane order, from one
+// 16-byte piece of the global tile per lane.  A slab is ROWS x COLS floats
+// of the global orientation (COLS contiguous); piece q of the LDS slab holds
+// row q / P, piece (q % P) ^ swz(row) of that row, P = COLS / 4.  For the
+// k-contiguous operand the swizzle makes the 128-bit reads of sixteen
+// consecutive rows free of bank conflicts.  The XOR masks were chosen by
+// measurement (SQ_LDS_BANK_CONFLICT on gfx950, every read pattern of the
+// kernel): row & 7 for 8 pieces per row and row & 15 for 16 are
+// conflict-free, while (row & 7) ^ ((row >> 3) & 1), row & 7 with 16 pieces
+// and unswizzled rows cost two to four times the read cycles.  The
+// m/n-contiguous operand is read contiguously and stored unswizzled.
+template <int P, bool SWZ>
+__device__ __forceinline__ int x_swz(int row) {
+    if constexpr (!SWZ) return 0;
+    else if constexpr (P == 8) return row & 7;
+    else if constexpr (P == 16) return row & 15;
+    else static_assert(P == 8 || P == 16, "k-contiguous slabs are 32 or 64 wide");
+    return 0;
+}
+
+template <int ROWS, int COLS, bool SWZ>
+struct XSlab {
+    static constexpr int P = COLS / 4;
+    static constexpr int INSTR = ROWS * P / 64;  // wave instructions per slab
+    static constexpr int PER_WAVE = INSTR / 4;
+    static_assert(INSTR % 4 == 0, "slab must split evenly over four waves");
+};
+
+template <int ROWS, int COLS, bool SWZ>
+__device__ __forceinline__ void x_dma_slab(float* lds, const float* __restrict__ g, long long ld,
+                                           int wave, int lane) {
+    using S = XSlab<ROWS, COLS, SWZ>;
+#pragma unroll
+    for (int i = 0; i < S::PER_WAVE; i++) {
+        const int inst = wave * S::PER_WAVE + i;
+        const int q = inst * 64 + lane;
+        const int row = q / S::P;
+        const int piece = (q % S::P) ^ x_swz<S::P, SWZ>(row);
+        __builtin_amdgcn_global_load_lds(
+            (const void*)(g + (long long)row * ld + 4 * piece),
+            (void __attribute__((address_space(3)))*)(lds + inst * 256), 16, 0, 0);
+    }
+}
+
+// Operand fragments of one 16-wide k chunk from a slab laid out by
+// x_dma_slab: frag[b * 4 + s] is block b's value at sub-step s.
+template <bool KC, int ROWS, int BK, int F>
+__device__ __forceinline__ void x_load_frag_dma(const float* __restrict__ s, int base, int chunk,
+                                                int l16, int kq, float (&frag)[F * 4]) {
+    if constexpr (KC) {
+        constexpr int P = BK / 4;
+#pragma unroll
+        for (int b = 0; b < F; b++) {
+            const int row = base + 16 * b + l16;
+            const int piece = (chunk * 4 + kq) ^ x_swz<P, true>(row);
+            const f4 v = *reinterpret_cast<const f4*>(s + row * BK + 4 * piece);
+            frag[b * 4 + 0] = v.x;
+            frag[b * 4 + 1] = v.y;
+            frag[b * 4 + 2] = v.z;
+            frag[b * 4 + 3] = v.w;
+        }
+    } else {
+        constexpr int W = XVec<F>::W;
+#pragma unroll
+        for (int st = 0; st < 4; st++) {
+            const float* row = s + (chunk * 16 + 4 * kq + st) * ROWS + base;
+#pragma unroll
+            for (int g = 0; g < F / W; g++) {
+                const float* q = row + 16 * W * g + W * l16;
+                if constexpr (W == 4) {
+                    const f4 v = *reinterpret_cast<const f4*>(q);
+                    frag[(4 * g + 0) * 4 + st] = v.x;
+                    frag[(4 * g + 1) * 4 + st] = v.y;
+                    frag[(4 * g + 2) * 4 + st] = v.z;
+                    frag[(4 * g + 3) * 4 + st] = v.w;
+                } else if constexpr (W == 2) {
+                    const float2 v = *reinterpret_cast<const float2*>(q);
+                    frag[(2 * g + 0) * 4 + st] = v.x;
+                    frag[(2 * g + 1) * 4 + st] = v.y;
+                } else {
+                    frag[g * 4 + st] = q[0];
+                }
+            }
+        }
+    }
+}
+
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void x_wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Workgroup barrier after waiting for this wave's slab loads down to N
+// outstanding.  __syncthreads() would also wait for the loads of the slab
+// after (its release fence waits for every outstanding load into LDS); the
+// explicit count keeps that slab in flight.  The empty asm statements stop
+// the compiler from moving memory accesses across the barrier.
+template <int N>
+__device__ __forceinline__ void x_barrier() {
+    x_wait_vmcnt<N>();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// The same after this wave's slab loads and LDS reads have all completed.
+__device__ __forceinline__ void x_barrier_all() {
+    __builtin_amdgcn_s_waitcnt((0x7 << 4));  // vmcnt(0) lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// LDS read instructions per chunk for one operand (x_load_frag_dma).
+template <bool KC, int F>
+struct XReads {
+    static constexpr int N = KC ? F : 4 * (F / XVec<F>::W);
+};
+
+template <int BM, int BN, int BK, bool TA, bool TB, bool EPI>
+__device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
+    constexpr int NT = 256;
+    constexpr int TM = BM / 2, TN = BN / 2;
+    constexpr int FM = TM / 16, FN = TN / 16;
+    constexpr int CH = BK / 16;
+    static_assert(TM % 16 == 0 && TN % 16 == 0 && BK % 16 == 0, "tile shape");
+    constexpr bool A_KC = !TA, B_KC = TB;
+
+    constexpr int A_ROWS = TA ? BK : BM, A_COLS = TA ? BM : BK;
+    constexpr int B_ROWS = TB ? BN : BK, B_COLS = TB ? BK : BN;
+    constexpr int A_ELEMS = A_ROWS * A_COLS;
+    constexpr int B_ELEMS = B_ROWS * B_COLS;
+    constexpr int STAGE = A_ELEMS + B_ELEMS;
+    using SA = XSlab<A_ROWS, A_COLS, A_KC>;
+    using SB = XSlab<B_ROWS, B_COLS, B_KC>;
+    constexpr int DMA_PER_STAGE = SA::PER_WAVE + SB::PER_WAVE;
+    static_assert(CH % 2 == 0, "slabs hold an even number of 16-wide chunks");
+    // The two slab stages, reused by the epilogue for each wave's TM x TN
+    // sub-tile of C (row pitch CP).
+    constexpr int CP = TN + 4;
+    constexpr int SMEM = 2 * STAGE > 4 * TM * CP ? 2 * STAGE : 4 * TM * CP;
+    __shared__ __attribute__((aligned(1024))) float smem[SMEM];
+
+    const int num_m = p.M / BM, num_n = p.N / BN;
+    int tm, tn;
+    gemm_tile_coords(logical, num_m, num_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int l16 = lane & 15, kq = lane >> 4;
+
+    const float* a_base = TA ? p.A + m0 : p.A + (long long)m0 * p.lda;
+    const float* b_base = TB ? p.B + (long long)n0 * p.ldb : p.B + n0;
+    const long long a_kstride = TA ? (long long)BK * p.lda : BK;
+    const long long b_kstride = TB ? BK : (long long)BK * p.ldb;
+
+    v4f acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Fragment origins inside a slab: the wave's first row (KC) or column
+    // offset (MC) of its sub-tile.
+    const int a_off = wm * TM, b_off = wn * TN;
+    float fa[2][FM * 4], fb[2][FN * 4];
+
+    const int KT = p.K / BK;
+    auto issue = [&](int k_slab, int stage) {
+        float* d = smem + stage * STAGE;
+        x_dma_slab<A_ROWS, A_COLS, A_KC>(d, a_base + k_slab * a_kstride, p.lda, wave, lane);
+        x_dma_slab<B_ROWS, B_COLS, B_KC>(d + A_ELEMS, b_base + k_slab * b_kstride, p.ldb, wave,
+                                         lane);
+    };
+    auto frags = [&](const float* st, int chunk, int slot) {
+        x_load_frag_dma<A_KC, A_KC ? BK : BM, BK, FM>(st, a_off, chunk, l16, kq, fa[slot]);
+        x_load_frag_dma<B_KC, B_KC ? BK : BN, BK, FN>(st + A_ELEMS, b_off, chunk, l16, kq,
+                                                      fb[slot]);
+    };
+    auto mfmas = [&](int slot, int st0, int st1) {
+#pragma unroll
+        for (int st = st0; st < st1; st++)
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                        fa[slot][i * 4 + st], fb[slot][j * 4 + st], acc[i][j], 0, 0, 0);
+    };
+    // Instruction counts that the schedule below interleaves.
+    constexpr int NMFMA = 4 * FM * FN;  // per chunk
+    constexpr int NREAD = XReads<A_KC, FM>::N + XReads<B_KC, FN>::N;  // LDS reads per chunk
+    constexpr int NDMA = DMA_PER_STAGE;  // slab loads per stage
+    constexpr int MF_PER_READ = NMFMA / 2 / NREAD > 0 ? NMFMA / 2 / NREAD : 1;
+
+    // Prologue: slabs 0 and 1 in flight, slab 0 waited for (K = 0 reads
+    // nothing and stores zeros).
+    if (KT > 0) {
+        issue(0, 0);
+        if (KT > 1) {
+            issue(1, 1);
+            x_barrier<DMA_PER_STAGE>();
+        } else {
+            x_barrier<0>();
+        }
+        frags(smem, 0, 0);
+    }
+
+    // Slab kt lives in stage kt % 2.  Its last chunk is split: after the
+    // first half of its MFMAs every wave has finished reading the stage
+    // (the operands are in registers), so after one barrier the next slab's
+    // first operands are read and the slab after next is loaded into this
+    // stage while the second half of the MFMAs runs.  Every path through
+    // the loop body is the same instruction stream (no branches), which
+    // keeps the accumulators in place; the load issued in the last
+    // iteration repeats slab KT - 1 into the stage that is no longer read.
+    constexpr int LAST = (CH - 1) & 1;
+    auto early_chunks = [&](const float* sa) {
+#pragma unroll
+        for (int c = 0; c + 1 < CH; c++) {
+            frags(sa, c + 1, (c + 1) & 1);
+            mfmas(c & 1, 0, 4);
+#pragma unroll
+            for (int r = 0; r < NREAD; r++) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+                __builtin_amdgcn_sched_group_barrier(0x008, MF_PER_READ, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, NMFMA - NREAD * MF_PER_READ, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    for (int kt = 0; kt + 1 < KT; kt++) {
+        early_chunks(smem + (kt & 1) * STAGE);
+        mfmas(LAST, 0, 2);
+        __builtin_amdgcn_sched_barrier(0);
+        // Slab kt + 1 was loaded one stage ago and is the only load in
+        // flight; after the barrier no wave has an LDS read of slab kt
+        // outstanding.
+        x_barrier_all();
+        frags(smem + ((kt + 1) & 1) * STAGE, 0, 0);
+        issue(min(kt + 2, KT - 1), kt & 1);
+        mfmas(LAST, 2, 4);
+#pragma unroll
+        for (int r = 0; r < NREAD; r++) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < NDMA; r++) {
+            __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);  // one slab load
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (KT > 0) {
+        early_chunks(smem + ((KT - 1) & 1) * STAGE);
+        mfmas(LAST, 0, 4);
+    }
+    // No slab load may still be writing LDS when the workgroup ends.
+    x_wait_vmcnt<0>();
+
+    // Epilogue through LDS.  Each wave writes its accumulators as a plain
+    // TM x TN sub-tile into its own LDS region (accumulator r of a 16x16
+    // block is MFMA row 4 kq + r, column l16), then streams the sub-tile
+    // back row by row: four consecutive columns per lane, so operands and
+    // results move as 128-bit accesses and the fused steps are one compact
+    // loop instead of code unrolled over every accumulator.
+    __syncthreads();  // every wave is done with the slab stages
+    float* cw = smem + wave * (TM * CP);
+    if constexpr (!B_KC && XVec<FN>::W == 4) {
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int rr = x_index<A_KC, FM>(0, i, 4 * kq + r);
+#pragma unroll
+                for (int g = 0; g < FN / 4; g++) {
+                    const f4 v = {acc[i][4 * g + 0][r], acc[i][4 * g + 1][r],
+                                  acc[i][4 * g + 2][r], acc[i][4 * g + 3][r]};
+                    *reinterpret_cast<f4*>(cw + rr * CP + 64 * g + 4 * l16) = v;
+                }
+            }
+    } else {
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int rr = x_index<A_KC, FM>(0, i, 4 * kq + r);
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+                    cw[rr * CP + x_index<B_KC, FN>(0, j, l16)] = acc[i][j][r];
+            }
+    }
+    const int row0 = m0 + a_off, col0 = n0 + b_off;
+    constexpr int F4_ROW = TN / 4;
+    constexpr int ITER = TM * F4_ROW / 64;  // 128-bit groups per lane
+    constexpr int NB = ITER < 4 ? ITER : 4;  // groups whose operands load together
+    static_assert(ITER % NB == 0, "epilogue batches");
+    const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 1
+    for (int b0 = 0; b0 < ITER; b0 += NB) {
+        // Loads of a batch first, so NB global reads per operand are in
+        // flight together.
+        f4 z[NB], res[NB], mul[NB], old[NB];
+        long long idx[NB];
+        int col[NB];
+#pragma unroll
+        for (int u = 0; u < NB; u++) {
+            const int q = lane + 64 * (b0 + u);
+            const int rr = q / F4_ROW, c4 = q % F4_ROW;
+            z[u] = *reinterpret_cast<const f4*>(cw + rr * CP + 4 * c4);
+            col[u] = col0 + 4 * c4;
+            idx[u] = (long long)(row0 + rr) * p.ldc + col[u];
+            res[u] = mul[u] = old[u] = zero;
+            if constexpr (EPI) {
+                if (p.residual) res[u] = *reinterpret_cast<const f4*>(p.residual + idx[u]);
+                if (p.aux) mul[u] = *reinterpret_cast<const f4*>(p.aux + idx[u]);
+                if (p.update) old[u] = *reinterpret_cast<const f4*>(p.C + idx[u]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < NB; u++) {
+            float y[4] = {z[u].x, z[u].y, z[u].z, z[u].w};
+            if constexpr (EPI) {
+                // Per element: alpha, bias, residual, aux (or act'(aux)),
+                // pre-activation store, activation, store or SGD update --
+                // the order of gemm_epilogue_store, each one rounded f32
+                // operation.
+                if (p.alpha != 1.0f)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) y[e] = p.alpha * y[e];
+                if (p.bias) {
+                    const f4 v = *reinterpret_cast<const f4*>(p.bias + col[u]);
+                    y[0] = y[0] + v.x; y[1] = y[1] + v.y; y[2] = y[2] + v.z; y[3] = y[3] + v.w;
+                }
+                if (p.residual) {
+                    y[0] = y[0] + res[u].x; y[1] = y[1] + res[u].y;
+                    y[2] = y[2] + res[u].z; y[3] = y[3] + res[u].w;
+                }
+                if (p.aux) {
+                    const float m[4] = {mul[u].x, mul[u].y, mul[u].z, mul[u].w};
+                    if (p.aux_act) {
+#pragma unroll
+                        for (int e = 0; e < 4; e++) y[e] = y[e] * activate_derivative(p.aux_act, m[e]);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; e++) y[e] = y[e] * m[e];
+                    }
+                }
+                if (p.pre_out)
+                    *reinterpret_cast<f4*>(p.pre_out + idx[u]) = f4{y[0], y[1], y[2], y[3]};
+                if (p.act != ACT_IDENTITY)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) y[e] = activate(p.act, y[e]);
+                if (p.update) {
+                    y[0] = old[u].x - p.update_scale * y[0];
+                    y[1] = old[u].y - p.update_scale * y[1];
+                    y[2] = old[u].z - p.update_scale * y[2];
+                    y[3] = old[u].w - p.update_scale * y[3];
+                }
+            }
+            *reinterpret_cast<f4*>(p.C + idx[u]) = f4{y[0], y[1], y[2], y[3]};
+        }
+    }
+}
+
+template <int BM, int BN, int BK, bool TA, bool TB, bool EPI>
+__device__ __forceinline__ void gemm_single_x(const GemmArgs& p) {
+    gemm_body_x<BM, BN, BK, TA, TB, EPI>(p, xcd_logical(blockIdx.x, gridDim.x));
+}
+
+template <int BM, int BN, int BK, bool TA, bool TB>
+__device__ __forceinline__ void gemm_batch_x(const GemmBatchArgs& b) {
+    const int logical = xcd_logical(blockIdx.x, gridDim.x);
+    const int z = logical / b.tiles;
+    gemm_body_x<BM, BN, BK, TA, TB, true>(b.p[z], logical - z * b.tiles);
+}
+
+}  // namespace forge

@@ -6,25 +6,33 @@
 #include "common.hpp"
 #include "elementwise.hpp"
 #include "gemm.hpp"
+#include "gemm_x.hpp"
 #include "rows.hpp"
 
 using namespace forge;
 
 // ------------------------------------------------------------------- GEMM
-// forge_gemm_<ab>_<BM>x<BN>x<BK>_<WARPS_M>x<WARPS_N>[_g][_e]
+// forge_gemm_<ab>_<tile>[_e]
 //   ab: n/t for A then B (t = operand stored transposed)
-//   _g: bounds-guarded (any shape, any alignment); _e: fused epilogue.
+//   tile <BM>x<BN>x<BK>_x: the unguarded four-wave kernel (gemm_x.hpp);
+//   tile 64x64x16_2x2_g: the bounds-guarded kernel for any shape and
+//   alignment (gemm.hpp); _e: fused epilogue.
+#define GEMM_X_KERNEL(NAME, BM, BN, BK, TA, TB, EPI)                          \
+    FORGE_KERNEL void __launch_bounds__(256) NAME(GemmArgs p) {               \
+        gemm_single_x<BM, BN, BK, TA, TB, EPI>(p);                             \
+    }
 #define GEMM_KERNEL(NAME, BM, BN, BK, WMW, WNW, TA, TB, GUARD, EPI)          \
     FORGE_KERNEL void __launch_bounds__(WMW * WNW * 64) NAME(GemmArgs p) {   \
         gemm_single<BM, BN, BK, WMW, WNW, TA, TB, GUARD, EPI>(p);            \
     }
 
-// Epilogue instances: the three unguarded tiles the dispatcher chooses from
-// (by tile count, see runtime.cpp choose_gemm) and the guarded fallback.
-#define GEMM_FAMILY(AB, TA, TB)                                                   \
-    GEMM_KERNEL(forge_gemm_##AB##_256x128x16_4x2_e, 256, 128, 16, 4, 2, TA, TB, false, true) \
-    GEMM_KERNEL(forge_gemm_##AB##_128x128x16_4x2_e, 128, 128, 16, 4, 2, TA, TB, false, true) \
-    GEMM_KERNEL(forge_gemm_##AB##_128x64x16_2x2_e, 128, 64, 16, 2, 2, TA, TB, false, true)   \
+// Epilogue instances: the unguarded tiles the dispatcher chooses from (by
+// shape, see runtime.cpp choose_gemm) and the guarded fallback.
+#define GEMM_FAMILY(AB, TA, TB)                                                      \
+    GEMM_X_KERNEL(forge_gemm_##AB##_128x128x32_x_e, 128, 128, 32, TA, TB, true)      \
+    GEMM_X_KERNEL(forge_gemm_##AB##_128x64x32_x_e, 128, 64, 32, TA, TB, true)        \
+    GEMM_X_KERNEL(forge_gemm_##AB##_64x128x32_x_e, 64, 128, 32, TA, TB, true)        \
+    GEMM_X_KERNEL(forge_gemm_##AB##_64x64x32_x_e, 64, 64, 32, TA, TB, true)          \
     GEMM_KERNEL(forge_gemm_##AB##_64x64x16_2x2_g_e, 64, 64, 16, 2, 2, TA, TB, true, true)
 
 GEMM_FAMILY(nn, false, false)
@@ -35,14 +43,15 @@ GEMM_FAMILY(tt, true, true)
 // Batched instances (forge_gemm_batch_<ab>_<tile>): several same-shape
 // products per launch, each with its own operands and epilogue.  They serve
 // the Q/K/V projections and the K slices of split-K products.
-#define GEMM_BATCH_KERNEL(NAME, BM, BN, BK, WMW, WNW, TA, TB)                          \
-    FORGE_KERNEL void __launch_bounds__(WMW * WNW * 64) NAME(GemmBatchArgs b) {      \
-        gemm_batch<BM, BN, BK, WMW, WNW, TA, TB>(b);                                 \
+#define GEMM_BATCH_KERNEL(NAME, BM, BN, BK, TA, TB)                                    \
+    FORGE_KERNEL void __launch_bounds__(256) NAME(GemmBatchArgs b) {                 \
+        gemm_batch_x<BM, BN, BK, TA, TB>(b);                                         \
     }
-#define GEMM_BATCH_FAMILY(AB, TA, TB)                                                             \
-    GEMM_BATCH_KERNEL(forge_gemm_batch_##AB##_256x128x16_4x2, 256, 128, 16, 4, 2, TA, TB)      \
-    GEMM_BATCH_KERNEL(forge_gemm_batch_##AB##_128x128x16_4x2, 128, 128, 16, 4, 2, TA, TB)      \
-    GEMM_BATCH_KERNEL(forge_gemm_batch_##AB##_128x64x16_2x2, 128, 64, 16, 2, 2, TA, TB)
+#define GEMM_BATCH_FAMILY(AB, TA, TB)                                                   \
+    GEMM_BATCH_KERNEL(forge_gemm_batch_##AB##_128x128x32_x, 128, 128, 32, TA, TB)      \
+    GEMM_BATCH_KERNEL(forge_gemm_batch_##AB##_128x64x32_x, 128, 64, 32, TA, TB)        \
+    GEMM_BATCH_KERNEL(forge_gemm_batch_##AB##_64x128x32_x, 64, 128, 32, TA, TB)        \
+    GEMM_BATCH_KERNEL(forge_gemm_batch_##AB##_64x64x32_x, 64, 64, 32, TA, TB)
 GEMM_BATCH_FAMILY(nn, false, false)
 GEMM_BATCH_FAMILY(nt, false, true)
 GEMM_BATCH_FAMILY(tn, true, false)
@@ -59,20 +68,15 @@ FORGE_KERNEL void __launch_bounds__(SPLITK_THREADS) forge_gemm_splitk_reduce_s(c
     splitk_reduce_body<false>(P, splits, p);
 }
 
-// Plain C = A * B instances (forge_gemm_f32 uses the first three and the
-// guarded one) and the other tile-shape candidates of the bench sweep.
-GEMM_KERNEL(forge_gemm_nn_128x128x16_2x2, 128, 128, 16, 2, 2, false, false, false, false)
-GEMM_KERNEL(forge_gemm_nn_128x128x32_2x2, 128, 128, 32, 2, 2, false, false, false, false)
-GEMM_KERNEL(forge_gemm_nn_128x64x16_2x2, 128, 64, 16, 2, 2, false, false, false, false)
-GEMM_KERNEL(forge_gemm_nn_256x128x16_2x2, 256, 128, 16, 2, 2, false, false, false, false)
-GEMM_KERNEL(forge_gemm_nn_128x256x16_2x2, 128, 256, 16, 2, 2, false, false, false, false)
-GEMM_KERNEL(forge_gemm_nn_256x128x16_4x2, 256, 128, 16, 4, 2, false, false, false, false)
-GEMM_KERNEL(forge_gemm_nn_128x256x16_2x4, 128, 256, 16, 2, 4, false, false, false, false)
-GEMM_KERNEL(forge_gemm_nn_256x256x16_4x4, 256, 256, 16, 4, 4, false, false, false, false)
-GEMM_KERNEL(forge_gemm_nn_256x128x32_4x2, 256, 128, 32, 4, 2, false, false, false, false)
-GEMM_KERNEL(forge_gemm_nn_128x128x16_4x2, 128, 128, 16, 4, 2, false, false, false, false)
-GEMM_KERNEL(forge_gemm_nn_128x64x16_2x1, 128, 64, 16, 2, 1, false, false, false, false)
-GEMM_KERNEL(forge_gemm_nn_64x64x16_1x1, 64, 64, 16, 1, 1, false, false, false, false)
+// Plain C = A * B instances: forge_gemm_f32 (the headline GEMM) and the
+// tile candidates of the bench sweep.
+GEMM_X_KERNEL(forge_gemm_nn_128x256x32_x, 128, 256, 32, false, false, false)
+GEMM_X_KERNEL(forge_gemm_nn_256x128x32_x, 256, 128, 32, false, false, false)
+GEMM_X_KERNEL(forge_gemm_nn_128x128x32_x, 128, 128, 32, false, false, false)
+GEMM_X_KERNEL(forge_gemm_nn_128x128x64_x, 128, 128, 64, false, false, false)
+GEMM_X_KERNEL(forge_gemm_nn_128x64x32_x, 128, 64, 32, false, false, false)
+GEMM_X_KERNEL(forge_gemm_nn_64x128x32_x, 64, 128, 32, false, false, false)
+GEMM_X_KERNEL(forge_gemm_nn_64x64x32_x, 64, 64, 32, false, false, false)
 GEMM_KERNEL(forge_gemm_nn_64x64x16_2x2_g, 64, 64, 16, 2, 2, false, false, true, false)
 
 // ------------------------------------------------------------------- rows

@@ -534,89 +534,85 @@ extern "C" forge_status forge_fill(forge_runtime* rt, forge_stream* s, forge_sli
 namespace {
 
 struct GemmConfig {
-    const char* tag;  // e.g. "256x128x16_4x2"
+    const char* tag;  // e.g. "128x256x32_x"
     int bm, bn, bk, threads;
 };
 
-const GemmConfig kTile256x128 = {"256x128x16_4x2", 256, 128, 16, 512};
-const GemmConfig kTile128x128 = {"128x128x16_4x2", 128, 128, 16, 512};
-const GemmConfig kTile128x64 = {"128x64x16_2x2", 128, 64, 16, 256};
+const GemmConfig kTile128x256 = {"128x256x32_x", 128, 256, 32, 256};
+const GemmConfig kTile128x128 = {"128x128x32_x", 128, 128, 32, 256};
+const GemmConfig kTile128x64 = {"128x64x32_x", 128, 64, 32, 256};
+const GemmConfig kTile64x128 = {"64x128x32_x", 64, 128, 32, 256};
+const GemmConfig kTile64x64 = {"64x64x32_x", 64, 64, 32, 256};
 const GemmConfig kGuard64 = {"64x64x16_2x2_g", 64, 64, 16, 256};
 
-// Unguarded tiles address the epilogue with 32-bit byte offsets, so their C
-// (and residual / aux / pre-activation) must hold fewer than 2^30 elements.
-constexpr size_t GEMM_OFF32_MAX = size_t(1) << 30;
+// Unguarded tiles, largest first, and their measured full-device
+// efficiency relative to 128x256 (4096^3 on MI355X: 140.6, 138.5, 134.7,
+// 133.8 and 121 TFLOP/s).  All but 128x256 have fused-epilogue and batched
+// instances; 128x256 has a plain one.
+const GemmConfig* const kUnguarded[] = {&kTile128x256, &kTile128x128, &kTile128x64,
+                                        &kTile64x128, &kTile64x64};
+const double kTileEfficiency[] = {1.0, 0.985, 0.958, 0.951, 0.86};
 
-// Tile choice.  Each unguarded tile has a measured full-device efficiency
-// (4096^3 on MI355X: 256x128 136.5, 128x128 133.3, 128x64 128.5 TFLOP/s),
-// scaled by how evenly its tiles spread over the CUs: t tiles occupy
-// ceil(t / CUs) rounds, so the balance is t / (CUs * ceil(t / CUs)).  The
-// best score wins (ties to the larger tile): 4096^3 -> 256x128, 2048x2048 ->
-// 128x128, 2048x1024 -> 128x64, and three 2048x1024 products in one batch
-// -> 128x64 (768 tiles, three per CU).  Unaligned shapes, shapes the tiles
-// do not divide and matrices of 2^30 or more elements take the
-// bounds-guarded 64x64 tile.  `count` same-shape products share the launch.
+// Tile choice: the best efficiency x balance, where t tiles occupy
+// ceil(t / CUs) rounds and the balance is t / (CUs * ceil(t / CUs)); ties go
+// to the larger tile.  128x256 (one workgroup per CU) serves plain products
+// only: with a fused epilogue, 128x128 (two workgroups per CU, so one
+// workgroup's epilogue overlaps the other's MFMAs) is as fast or faster
+// (2048x4096x1024 + bias + GELU: 140.9 against 146.8 us).  One refinement:
+// when 128x128 would leave at most one tile per CU, 64x128 (two tiles per
+// CU) is taken instead -- on the 2048x2048x1024 attention scores 124.9
+// against 121.1 TFLOP/s.  Results: plain 4096^3, 8192x1024 and 2048x4096
+// -> 128x256; fused C5 products -> 128x128; 2048x2048 -> 64x128; 2048x1024
+// -> 128x64 (the three Q/K/V products of one batch: 768 tiles).  Unaligned
+// shapes and shapes the tiles do not divide take the bounds-guarded 64x64
+// tile.  `count` same-shape products share the launch.
 const GemmConfig& choose_gemm(forge_runtime* rt, size_t M, size_t N, size_t K, bool aligned,
-                              size_t count = 1) {
+                              bool epilogue, size_t count = 1) {
     const size_t cus = rt->cu_count > 0 ? (size_t)rt->cu_count : 256;
-    struct Candidate {
-        const GemmConfig* cfg;
-        double efficiency;
-    };
-    const Candidate candidates[] = {
-        {&kTile256x128, 1.0}, {&kTile128x128, 0.977}, {&kTile128x64, 0.941}};
     const GemmConfig* best = &kGuard64;
     double best_score = 0.0;
-    for (const Candidate& c : candidates) {
-        const GemmConfig& g = *c.cfg;
-        if (!aligned || M % g.bm || N % g.bn || K % g.bk || M * N >= GEMM_OFF32_MAX) continue;
+    size_t best_tiles = 0;
+    auto fits = [&](const GemmConfig& g) {
+        return aligned && M % g.bm == 0 && N % g.bn == 0 && K % g.bk == 0;
+    };
+    for (int i = epilogue ? 1 : 0; i < 5; i++) {
+        const GemmConfig& g = *kUnguarded[i];
+        if (!fits(g)) continue;
         const size_t t = count * (M / g.bm) * (N / g.bn);
         const size_t rounds = (t + cus - 1) / cus;
-        const double score = c.efficiency * (double)t / (double)(cus * rounds);
+        const double score = kTileEfficiency[i] * (double)t / (double)(cus * rounds);
         if (score > best_score + 1e-9) {
-            best = c.cfg;
+            best = kUnguarded[i];
             best_score = score;
+            best_tiles = t;
         }
     }
+    if (best == &kTile128x128 && best_tiles <= cus && fits(kTile64x128)) best = &kTile64x128;
     return *best;
 }
 
-// Split-K plan for one product, measured on MI355X (bench.py --sweep) over
-// the C3/C4/C5 shapes.  A split pays off when the output has too few tiles
-// to give every CU two waves' worth of work and K is long:
-//   - 256x128 tiles already fill the CUs: split in two only for K >= 8192
-//     (4096x2048x8192: 133.7 vs 131.6 TFLOP/s);
-//   - otherwise, for K >= 2048, four K slices of 256x128 tiles when that
-//     fills the CUs with slices of >= 1024 (2048x2048x4096: 125.0 vs 118.9),
-//     else four slices of 128x128 tiles (2048x1024x2048: 105.7 vs 98.4;
-//     2048x1024x4096: 117.3 vs 100.5);
-//   - no split for K < 2048 (2048x1024x1024: 93.2 unsplit, 85.6 split).
-// Returns the split count and sets *cfg to the tile to use.
+// Split-K plan for one product.  With the four-wave tiles no C3/C4/C5 shape
+// gains from a split (bench.py --sweep: e.g. 2048x1024x4096 122.5 TFLOP/s
+// unsplit against 117.5 in four slices), so products are split only when
+// the chosen tile leaves at least three quarters of the CUs idle: the K
+// slices are doubled while the launch still fits on the CUs and each slice
+// keeps >= 1024 of K (up to eight).  Returns the split count and sets *cfg
+// to the tile to use.
 int choose_splits(forge_runtime* rt, size_t M, size_t N, size_t K, bool aligned,
                   const GemmConfig** cfg) {
     const size_t cus = rt->cu_count > 0 ? (size_t)rt->cu_count : 256;
-    auto fits = [&](const GemmConfig& c, size_t splits) {
-        return aligned && M % c.bm == 0 && N % c.bn == 0 && K % (splits * c.bk) == 0 &&
-               M * N < GEMM_OFF32_MAX;
-    };
-    auto tiles = [&](const GemmConfig& c) { return (M / c.bm) * (N / c.bn); };
-    if (fits(kTile256x128, 1) && tiles(kTile256x128) >= cus) {
-        if (K >= 8192 && fits(kTile256x128, 2)) {
-            *cfg = &kTile256x128;
-            return 2;
-        }
-        return 1;
-    }
-    if (K < 2048) return 1;
-    if (fits(kTile256x128, 4) && tiles(kTile256x128) * 4 >= cus && K / 4 >= 1024) {
-        *cfg = &kTile256x128;
-        return 4;
-    }
-    if (fits(kTile128x128, 4) && K / 4 >= 512) {
-        *cfg = &kTile128x128;
-        return 4;
-    }
-    return 1;
+    // The K slices run as one batched launch, whose instances all fuse the
+    // epilogue.
+    const GemmConfig& g = choose_gemm(rt, M, N, K, aligned, true);
+    if (&g == &kGuard64) return 1;
+    const size_t t = (M / g.bm) * (N / g.bn);
+    if (t * 4 > cus) return 1;
+    int splits = 1;
+    while (splits * 2 <= GEMM_BATCH_MAX && t * (size_t)splits * 2 <= cus &&
+           K % ((size_t)splits * 2 * g.bk) == 0 && K / ((size_t)splits * 2) >= 1024)
+        splits *= 2;
+    if (splits > 1) *cfg = &g;
+    return splits;
 }
 
 const char* gemm_ab(int ta, int tb) {
@@ -656,6 +652,9 @@ forge_status gemm_args(int ta, int tb, forge_slice A, forge_slice B, forge_slice
             return fail(FORGE_EINVAL, "unknown activation %d", ep->activation);
         if (ep->aux_activation < FORGE_ACT_IDENTITY || ep->aux_activation > FORGE_ACT_SILU)
             return fail(FORGE_EINVAL, "unknown aux activation %d", ep->aux_activation);
+        // The unguarded tiles move epilogue operands as 128-bit accesses.
+        for (const forge_slice* e : {&ep->bias, &ep->residual, &ep->aux_mul, &ep->pre_out})
+            if (e->ptr && !aligned16(e->ptr)) al = false;
         a.alpha = ep->alpha;
         a.bias = ep->bias.ptr;
         a.residual = ep->residual.ptr;
@@ -725,9 +724,9 @@ forge_status gemm_dispatch(forge_runtime* rt, forge_stream* s, int ta, int tb, f
     const GemmConfig* split_cfg = nullptr;
     const int splits = choose_splits(rt, M, N, K, aligned, &split_cfg);
     if (splits > 1) return gemm_split_launch(rt, s, ta, tb, a, *split_cfg, splits);
-    const GemmConfig& cfg = choose_gemm(rt, M, N, K, aligned);
-    char name[96];
     const bool epi = !(plain_name && !ta && !tb);
+    const GemmConfig& cfg = choose_gemm(rt, M, N, K, aligned, epi);
+    char name[96];
     snprintf(name, sizeof name, "forge_gemm_%s_%s%s", gemm_ab(ta, tb), cfg.tag,
              epi ? "_e" : "");
     unsigned tiles = (unsigned)(((M + cfg.bm - 1) / cfg.bm) * ((N + cfg.bn - 1) / cfg.bn));
@@ -919,20 +918,26 @@ extern "C" forge_status forge_gemm_f32_tile(forge_runtime* rt, forge_stream* s,
                                             const char* tile_tag, forge_slice A, forge_slice B,
                                             forge_slice C, size_t M, size_t N, size_t K) {
     if (!rt || !tile_tag) return fail(FORGE_EINVAL, "null argument");
-    unsigned bm = 0, bn = 0, bk = 0, wm = 0, wn = 0;
+    unsigned bm = 0, bn = 0, bk = 0, threads = 256;
+    bool guarded = false;
     char tail[8] = {0};
-    int got = sscanf(tile_tag, "%ux%ux%u_%ux%u%7s", &bm, &bn, &bk, &wm, &wn, tail);
-    if (got < 5 || bm == 0 || bn == 0 || bk == 0 || wm == 0 || wn == 0 || wm * wn > 16)
+    if (sscanf(tile_tag, "%ux%ux%u_%7s", &bm, &bn, &bk, tail) != 4 || bm == 0 || bn == 0 ||
+        bk == 0)
         return fail(FORGE_EINVAL, "bad tile tag %s", tile_tag);
-    const bool guarded = strcmp(tail, "_g") == 0;
-    if (got == 6 && !guarded) return fail(FORGE_EINVAL, "bad tile tag %s", tile_tag);
+    if (strcmp(tail, "x") == 0) {
+        // Four-wave instance <BM>x<BN>x<BK>_x.
+    } else if (strcmp(tail, "2x2_g") == 0) {
+        guarded = true;
+    } else {
+        return fail(FORGE_EINVAL, "bad tile tag %s", tile_tag);
+    }
     if (!fits_int(M) || !fits_int(N) || !fits_int(K))
         return fail(FORGE_EINVAL, "gemm dimensions exceed 2^31-1");
     FORGE_TRY(need(A, M * K, "gemm A"));
     FORGE_TRY(need(B, K * N, "gemm B"));
     FORGE_TRY(need(C, M * N, "gemm C"));
     if (!guarded && (M % bm || N % bn || K % bk || !aligned16(A.ptr) || !aligned16(B.ptr) ||
-                     !aligned16(C.ptr) || K % 4 || N % 4 || M * N >= GEMM_OFF32_MAX))
+                     !aligned16(C.ptr) || K % 4 || N % 4))
         return fail(FORGE_EINVAL, "shape %zux%zux%zu does not fit unguarded tile %s", M, N, K,
                     tile_tag);
     if (M == 0 || N == 0) return FORGE_OK;
@@ -951,7 +956,7 @@ extern "C" forge_status forge_gemm_f32_tile(forge_runtime* rt, forge_stream* s,
     snprintf(name, sizeof name, "forge_gemm_nn_%s", tile_tag);
     unsigned tiles = (unsigned)(((M + bm - 1) / bm) * ((N + bn - 1) / bn));
     void* args[] = {&a};
-    return launch(rt, s, name, dim3(tiles), dim3(wm * wn * 64), 0, args);
+    return launch(rt, s, name, dim3(tiles), dim3(threads), 0, args);
 }
 
 extern "C" forge_status forge_gemm_f32_split(forge_runtime* rt, forge_stream* s,
@@ -960,20 +965,44 @@ extern "C" forge_status forge_gemm_f32_split(forge_runtime* rt, forge_stream* s,
                                              size_t K) {
     if (!rt || !tile_tag) return fail(FORGE_EINVAL, "null argument");
     const GemmConfig* cfg = nullptr;
-    for (const GemmConfig* c : {&kTile256x128, &kTile128x128, &kTile128x64})
-        if (strcmp(c->tag, tile_tag) == 0) cfg = c;
+    for (const GemmConfig* c : kUnguarded)
+        if (c != &kTile128x256 && strcmp(c->tag, tile_tag) == 0) cfg = c;
     if (!cfg) return fail(FORGE_EINVAL, "tile %s has no batched instance", tile_tag);
     if (splits < 1 || splits > GEMM_BATCH_MAX)
         return fail(FORGE_EINVAL, "splits must be in [1, %d]", GEMM_BATCH_MAX);
     GemmArgs a{};
     bool aligned = false;
     FORGE_TRY(gemm_args(0, 0, A, B, C, M, N, K, nullptr, &a, &aligned));
-    if (!aligned || M % cfg->bm || N % cfg->bn || K % ((size_t)splits * cfg->bk) ||
-        M * N >= GEMM_OFF32_MAX)
+    if (!aligned || M % cfg->bm || N % cfg->bn || K % ((size_t)splits * cfg->bk))
         return fail(FORGE_EINVAL, "shape %zux%zux%zu does not fit tile %s with %d splits", M, N,
                     K, tile_tag, splits);
     if (M == 0 || N == 0) return FORGE_OK;
     return gemm_split_launch(rt, s, 0, 0, a, *cfg, splits);
+}
+
+extern "C" forge_status forge_gemm_ex_f32_tile(forge_runtime* rt, forge_stream* s,
+                                               const char* tile_tag, int trans_a, int trans_b,
+                                               forge_slice A, forge_slice B, forge_slice C,
+                                               size_t M, size_t N, size_t K,
+                                               const forge_gemm_epilogue* ep) {
+    if (!rt || !tile_tag) return fail(FORGE_EINVAL, "null argument");
+    const GemmConfig* cfg = strcmp(tile_tag, kGuard64.tag) == 0 ? &kGuard64 : nullptr;
+    for (const GemmConfig* c : kUnguarded)
+        if (c != &kTile128x256 && strcmp(c->tag, tile_tag) == 0) cfg = c;
+    if (!cfg) return fail(FORGE_EINVAL, "tile %s has no epilogue instance", tile_tag);
+    GemmArgs a{};
+    bool aligned = false;
+    FORGE_TRY(gemm_args(trans_a, trans_b, A, B, C, M, N, K, ep, &a, &aligned));
+    if (cfg != &kGuard64 && (!aligned || M % cfg->bm || N % cfg->bn || K % cfg->bk))
+        return fail(FORGE_EINVAL, "shape %zux%zux%zu does not fit unguarded tile %s", M, N, K,
+                    tile_tag);
+    if (M == 0 || N == 0) return FORGE_OK;
+    char name[96];
+    snprintf(name, sizeof name, "forge_gemm_%s_%s_e", gemm_ab(trans_a, trans_b), cfg->tag);
+    const unsigned tiles =
+        (unsigned)(((M + cfg->bm - 1) / cfg->bm) * ((N + cfg->bn - 1) / cfg->bn));
+    void* args[] = {&a};
+    return launch(rt, s, name, dim3(tiles), dim3(cfg->threads), 0, args);
 }
 
 extern "C" forge_status forge_gemm_batch_f32(forge_runtime* rt, forge_stream* s, int trans_a,
@@ -999,12 +1028,12 @@ extern "C" forge_status forge_gemm_batch_f32(forge_runtime* rt, forge_stream* s,
         if (z < (size_t)GEMM_BATCH_MAX) b.p[z] = a;
     }
     if (count == 0 || M == 0 || N == 0) return FORGE_OK;
-    const GemmConfig& cfg = choose_gemm(rt, M, N, K, all_aligned, count);
+    const GemmConfig& cfg = choose_gemm(rt, M, N, K, all_aligned, true, count);
     const GemmConfig* split_cfg = nullptr;
     // Shapes the single-product path splits in K are dispatched one by one,
     // so every product equals its forge_gemm_ex_f32 result bit for bit.
     const bool split = choose_splits(rt, M, N, K, all_aligned, &split_cfg) > 1;
-    if (count > (size_t)GEMM_BATCH_MAX || cfg.bm == kGuard64.bm || split) {
+    if (count > (size_t)GEMM_BATCH_MAX || &cfg == &kGuard64 || split) {
         for (size_t z = 0; z < count; z++)
             FORGE_TRY(gemm_dispatch(rt, s, trans_a, trans_b, problems[z].A, problems[z].B,
                                     problems[z].C, M, N, K, &problems[z].epilogue, false));

@@ -223,6 +223,13 @@ class Runtime:
         call("forge_gemm_batch_f32", self.handle, stream, int(trans_a), int(trans_b), M, N, K,
              len(problems), arr)
 
+    def gemm_ex_tile(self, tile, A, B, C, M, N, K, trans_a=False, trans_b=False, stream=None,
+                     **epilogue) -> None:
+        """forge_gemm_ex_f32 through one named tile instance (testing)."""
+        ep = _epilogue(**epilogue)
+        call("forge_gemm_ex_f32_tile", self.handle, stream, tile.encode(), int(trans_a),
+             int(trans_b), A.slice, B.slice, C.slice, M, N, K, byref(ep))
+
     def gemm_split(self, tile, splits, A, B, C, M, N, K, stream=None) -> None:
         call("forge_gemm_f32_split", self.handle, stream, tile.encode(), splits, A.slice,
              B.slice, C.slice, M, N, K)

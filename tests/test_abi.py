@@ -63,13 +63,14 @@ def test_status_strings_and_errors_without_device():
 def dispatcher_kernel_names():
     """Every kernel name runtime.cpp can build (mirrors its naming rules)."""
     names = []
+    tiles = ("128x128x32_x", "128x64x32_x", "64x128x32_x", "64x64x32_x")
     for ab in ("nn", "nt", "tn", "tt"):
-        for tag in ("256x128x16_4x2", "128x128x16_4x2", "128x64x16_2x2", "64x64x16_2x2_g"):
+        for tag in tiles + ("64x64x16_2x2_g",):
             names.append(f"forge_gemm_{ab}_{tag}_e")
-    for tag in ("256x128x16_4x2", "128x128x16_4x2", "128x64x16_2x2", "64x64x16_2x2_g"):
+    for tag in tiles + ("128x256x32_x", "64x64x16_2x2_g"):
         names.append(f"forge_gemm_nn_{tag}")
     for ab in ("nn", "nt", "tn"):
-        for tag in ("256x128x16_4x2", "128x128x16_4x2", "128x64x16_2x2"):
+        for tag in tiles:
             names.append(f"forge_gemm_batch_{ab}_{tag}")
     names += ["forge_gemm_splitk_reduce_v", "forge_gemm_splitk_reduce_s"]
     for op in ("softmax", "layer_norm", "rms_norm", "softmax_bwd", "layer_norm_bwd", "rms_norm_bwd"):

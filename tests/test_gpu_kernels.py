@@ -122,7 +122,7 @@ def test_gemm_full_size_sampled_rows(rt, M, N, K):
 def test_gemm_epilogue_matches_unfused_bit_exact(rt, M, N, K, ta, tb):
     """Fused bias + residual + aux + activation + update equals the unfused
     launch sequence of Linear::affine_on/activate_on/learn_on bit for bit.
-    256x128x2048 is computed as four K slices, so the split-K reduction's
+    256x128x2048 is computed as two K slices, so the split-K reduction's
     epilogue is covered too."""
     say(f"gemm epilogue M={M} N={N} K={K} ta={ta} tb={tb}")
     A = orc.uniform((K, M) if ta else (M, K), 7)
@@ -477,11 +477,12 @@ def test_softmax_bwd_scaled_equals_bwd_then_scale(rt):
     assert np.array_equal(a.numpy(), b.numpy())
 
 
-@pytest.mark.parametrize("tile,splits,M,N,K", [("256x128x16_4x2", 2, 256, 128, 512),
-                                               ("128x128x16_4x2", 4, 256, 256, 1024),
-                                               ("128x64x16_2x2", 3, 128, 128, 96),
-                                               ("128x128x16_4x2", 8, 128, 128, 128),
-                                               ("128x64x16_2x2", 1, 128, 64, 64)])
+@pytest.mark.parametrize("tile,splits,M,N,K", [("64x128x32_x", 2, 256, 256, 512),
+                                               ("128x128x32_x", 4, 256, 256, 1024),
+                                               ("128x64x32_x", 3, 128, 128, 192),
+                                               ("128x128x32_x", 8, 128, 128, 256),
+                                               ("64x64x32_x", 5, 128, 64, 320),
+                                               ("128x64x32_x", 1, 128, 64, 64)])
 def test_gemm_split_k_vs_oracle(rt, tile, splits, M, N, K):
     """K slices summed in slice order: the same bar as any GEMM; one slice is
     the plain product bit for bit."""
@@ -500,6 +501,42 @@ def test_gemm_split_k_vs_oracle(rt, tile, splits, M, N, K):
         assert np.array_equal(C, plain.numpy())
     with pytest.raises(oxforge.ForgeError):
         rt.gemm_split(tile, splits, dA, dB, dC, M, N, K + 16 * splits + 8)
+
+
+TILES = ["128x128x32_x", "128x64x32_x", "64x128x32_x", "64x64x32_x", "64x64x16_2x2_g"]
+
+
+@pytest.mark.parametrize("tile", TILES)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_every_tile_instance(rt, tile, ta, tb):
+    """Each fused-epilogue instance the dispatcher can pick, at a shape that
+    is two tiles by two and three K slabs: the product within the GEMM bar
+    of the f64 oracle, and the epilogue (bias, residual, GELU, pre-activation
+    store) bit-identical to the same steps applied to the plain product."""
+    bm, bn = (int(x) for x in tile.split("x")[:2])
+    M, N, K = 2 * bm, 2 * bn, 96
+    say(f"gemm tile {tile} ta={ta} tb={tb} {M}x{N}x{K}")
+    A = orc.uniform((K, M) if ta else (M, K), 31)
+    B = orc.uniform((N, K) if tb else (K, N), 32)
+    bias, res = orc.uniform((N,), 33), orc.uniform((M, N), 34)
+    dA, dB, dbias, dres = rt.array(A), rt.array(B), rt.array(bias), rt.array(res)
+    dZ, dY, dpre = rt.empty((M, N)), rt.empty((M, N)), rt.empty((M, N))
+    rt.gemm_ex_tile(tile, dA, dB, dZ, M, N, K, trans_a=ta, trans_b=tb)
+    Z = dZ.numpy()
+    ref = orc.gemm_f64(A, B, ta, tb)
+    absprod = np.abs(op_a(A, ta)).astype(np.float64) @ np.abs(op_a(B, tb)).astype(np.float64)
+    rel_max, comp = gemm_errors(Z, ref, absprod)
+    assert rel_max <= 1e-4 and comp <= 1e-4, (rel_max, comp)
+    rt.gemm_ex_tile(tile, dA, dB, dY, M, N, K, trans_a=ta, trans_b=tb, bias=dbias, residual=dres,
+                    activation=oxforge.ACT_GELU, pre_out=dpre)
+    pre = (Z + bias[None, :]) + res
+    assert np.array_equal(dpre.numpy(), pre)
+    expect = rt.array(pre)
+    rt.map(expect, oxforge.MAP_GELU, 0.0)
+    assert np.array_equal(dY.numpy(), expect.numpy())
+    if tile.endswith("_x"):  # unguarded tiles refuse shapes they do not divide
+        with pytest.raises(oxforge.ForgeError):
+            rt.gemm_ex_tile(tile, dA, dB, dZ, M - 1, N, K, trans_a=ta, trans_b=tb)
 
 
 @pytest.mark.parametrize("M,N,K", [(256, 128, 192), (70, 50, 33)])
