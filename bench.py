@@ -127,6 +127,50 @@ def secondary(rt, orc, steps, warmup, extended):
         b.recycle()
 
     out.update(secondary_rows(rt, orc, steps, warmup, extended))
+    out.update(secondary_rows_at_scale(rt, orc, steps, warmup))
+    return out
+
+
+def secondary_rows_at_scale(rt, orc, steps, warmup):
+    """The same row and streaming kernels on X [65536, 1024] (256 MiB per
+    operand, two rotating sets: 512 MiB, beyond the 256 MiB MALL).  At the
+    C2 size a launch lasts 7-15 us and its ramp-up and drain are a large
+    part of it; here the kernels run long enough to show the bandwidth they
+    sustain."""
+    import oxforge
+
+    out = {}
+    rows, cols, sets = 65536, 1024, 2
+    X = 4 * rows * cols
+    log("row ops 65536x1024")
+    xs = rotating(rt, orc, (rows, cols), sets, 2)
+    gs = rotating(rt, orc, (rows, cols), sets, 3)
+    ds = [rt.empty((rows, cols)) for _ in range(sets)]
+    gam = rt.array(orc.normal((cols,), 4, 1.0, 0.1))
+    bet = rt.array(orc.normal((cols,), 5, 0.0, 0.1))
+    dgam, dbet = rt.empty((cols,)), rt.empty((cols,))
+    cases = {
+        "softmax_fwd": (2 * X, lambda i: rt.softmax_rows(xs[i % sets], rows, cols)),
+        "layer_norm_fwd": (2 * X, lambda i: rt.layer_norm(xs[i % sets], rows, cols, gam, bet)),
+        "rms_norm_fwd": (2 * X, lambda i: rt.rms_norm(xs[i % sets], rows, cols, gam)),
+        "softmax_bwd": (3 * X, lambda i: rt.softmax_rows_bwd(xs[i % sets], gs[i % sets],
+                                                             ds[i % sets], rows, cols)),
+        "layer_norm_bwd": (3 * X, lambda i: rt.layer_norm_bwd(xs[i % sets], gs[i % sets],
+                                                              ds[i % sets], rows, cols, gam,
+                                                              dgam, dbet)),
+        "rms_norm_bwd": (3 * X, lambda i: rt.rms_norm_bwd(xs[i % sets], gs[i % sets],
+                                                          ds[i % sets], rows, cols, gam, dgam)),
+        "binary_add": (3 * X, lambda i: rt.binary(xs[i % sets], gs[i % sets], ds[i % sets],
+                                                  oxforge.ADD)),
+        "map_scale": (2 * X, lambda i: rt.map(ds[i % sets], oxforge.MAP_SCALE, 1.0)),
+    }
+    for name, (nbytes, fn) in cases.items():
+        ms = time_launches(rt, fn, max(steps, 32), warmup)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[f"{name}_65536x1024"] = {"gbs": round(gbs, 1), "us": round(ms * 1e3, 1),
+                                     "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
+    for b in xs + gs + ds:
+        b.recycle()
     return out
 
 

@@ -200,6 +200,14 @@ unsigned grid_for(long long work_items, long long per_block, unsigned cap) {
     return (unsigned)g;
 }
 
+// Grid of the vectorised streaming kernels (elementwise.hpp stream_f4) for
+// n4 float4 items: one item per thread below 4M items (64 MiB), four per
+// thread above, at most 8192 workgroups (grid-stride beyond).
+unsigned stream_grid(long long n4) {
+    const long long per_block = n4 < (4ll << 20) ? EW_THREADS : EW_THREADS * 4;
+    return grid_for(n4, per_block, 8192);
+}
+
 std::string default_module_path() {
     if (const char* env = getenv("OXFORGE_KERNELS")) return env;
     Dl_info info;
@@ -1175,7 +1183,7 @@ extern "C" forge_status forge_binary(forge_runtime* rt, forge_stream* s, forge_s
     char name[64];
     snprintf(name, sizeof name, "forge_binary_%s_%s", nm, vec ? "v" : "s");
     long long nn = (long long)n;
-    unsigned g = grid_for(vec ? nn / 4 + 1 : nn, EW_THREADS, 8192);
+    unsigned g = vec ? stream_grid(nn / 4 + 1) : grid_for(nn, EW_THREADS, 8192);
     return launch_args(rt, s, name, dim3(g), dim3(EW_THREADS), 0, (const float*)l.ptr,
                        (const float*)r.ptr, o.ptr, nn);
 }
@@ -1192,7 +1200,7 @@ extern "C" forge_status forge_binary_assign(forge_runtime* rt, forge_stream* s, 
     char name[64];
     snprintf(name, sizeof name, "forge_binary_assign_%s_%s", nm, vec ? "v" : "s");
     long long nn = (long long)n;
-    unsigned g = grid_for(vec ? nn / 4 + 1 : nn, EW_THREADS, 8192);
+    unsigned g = vec ? stream_grid(nn / 4 + 1) : grid_for(nn, EW_THREADS, 8192);
     return launch_args(rt, s, name, dim3(g), dim3(EW_THREADS), 0, t.ptr, (const float*)r.ptr, nn);
 }
 
@@ -1204,7 +1212,7 @@ extern "C" forge_status forge_sgd_update(forge_runtime* rt, forge_stream* s, for
     if (n == 0) return FORGE_OK;
     bool vec = aligned16(param.ptr) && aligned16(grad.ptr);
     long long nn = (long long)n;
-    unsigned g = grid_for(vec ? nn / 4 + 1 : nn, EW_THREADS, 8192);
+    unsigned g = vec ? stream_grid(nn / 4 + 1) : grid_for(nn, EW_THREADS, 8192);
     return launch_args(rt, s, vec ? "forge_sgd_v" : "forge_sgd_s", dim3(g), dim3(EW_THREADS), 0,
                        param.ptr, (const float*)grad.ptr, nn, lr);
 }
@@ -1243,7 +1251,7 @@ extern "C" forge_status forge_map(forge_runtime* rt, forge_stream* s, forge_slic
     char name[64];
     snprintf(name, sizeof name, "forge_map_%s_%s", nm, vec ? "v" : "s");
     long long nn = (long long)n;
-    unsigned g = grid_for(vec ? nn / 4 + 1 : nn, EW_THREADS, 8192);
+    unsigned g = vec ? stream_grid(nn / 4 + 1) : grid_for(nn, EW_THREADS, 8192);
     return launch_args(rt, s, name, dim3(g), dim3(EW_THREADS), 0, x.ptr, nn, p0);
 }
 
@@ -1330,7 +1338,7 @@ extern "C" forge_status forge_activation_backward(forge_runtime* rt, forge_strea
     bool vec = aligned16(dy.ptr) && aligned16(z.ptr) && aligned16(g.ptr);
     long long nn = (long long)n;
     int a = (int)act;
-    unsigned grid = grid_for(vec ? nn / 4 + 1 : nn, EW_THREADS, 8192);
+    unsigned grid = vec ? stream_grid(nn / 4 + 1) : grid_for(nn, EW_THREADS, 8192);
     return launch_args(rt, s, vec ? "forge_act_backward_v" : "forge_act_backward_s", dim3(grid),
                        dim3(EW_THREADS), 0, (const float*)dy.ptr, (const float*)z.ptr, g.ptr, nn,
                        a);
