@@ -1,13 +1,13 @@
 // gemm.hpp -- fp32 GEMM on CDNA4 matrix cores: the shared GEMM argument
 // structs, tile ordering and split-K reduction, and the bounds-guarded
 // kernel body that serves shapes or alignments the unguarded four-wave tiles
-// (gemm_x.hpp) cannot take.
+// (gemm_x.hpp) cannot take: any M, N, K and any alignment.
 //
 // Replaces matrix_multiply_device (reference gemm.rs:202-373, TF32 mma.sync)
 // with true fp32 v_mfma_f32_32x32x2_f32.  Semantics follow the strict-fp32
 // kernel gemm.rs:15-129: C = A * B, row-major, C overwritten, f32 accumulate.
 //
-// Structure
+// Structure of the guarded body
 //   - A workgroup computes a BM x BN tile with WARPS_M x WARPS_N waves; each
 //     wave owns a (BM/WARPS_M) x (BN/WARPS_N) sub-tile made of 32x32 MFMA
 //     blocks whose accumulators live in VGPRs.
@@ -88,11 +88,6 @@ struct GemmBatchArgs {
     int tiles;  // tiles per problem
 };
 
-// Loads a ROWS x COLS tile (COLS contiguous in global memory) into registers,
-// COLS/4 four-float vectors per row, dealt over NT threads.  GUARD zero-fills
-// outside [vr, vc) and uses scalar loads (no alignment assumption).  The
-// staging registers are the native 4-float vector f4 so they stay in VGPRs.
-
 // The fused epilogue on one element z of the product at (row, col), idx =
 // row * ldc + col: alpha, bias, residual, aux multiply (or act'(aux)),
 // pre-activation store, activation, then store or SGD update.  Each step is
@@ -120,10 +115,14 @@ struct TileShape {
     static_assert(TOTAL % NT == 0, "tile must divide evenly over threads");
 };
 
-template <int ROWS, int COLS, int NT, bool GUARD>
-__device__ __forceinline__ void tile_load(f4* __restrict__ v,
-                                          const float* __restrict__ g, long long ld,
-                                          int vr, int vc) {
+// Loads a ROWS x COLS tile (COLS contiguous in global memory) into registers,
+// COLS/4 four-float vectors per row, dealt over NT threads, zero-filling
+// outside [vr, vc) with scalar loads (no alignment assumption).  The staging
+// registers are the native 4-float vector f4 so they stay in VGPRs.
+template <int ROWS, int COLS, int NT>
+__device__ __forceinline__ void tile_load_guarded(f4* __restrict__ v,
+                                                  const float* __restrict__ g, long long ld,
+                                                  int vr, int vc) {
     using S = TileShape<ROWS, COLS, NT>;
 #pragma unroll
     for (int i = 0; i < S::PER_THREAD; i++) {
@@ -131,15 +130,11 @@ __device__ __forceinline__ void tile_load(f4* __restrict__ v,
         const int r = f / S::F4_PER_ROW;
         const int c = (f % S::F4_PER_ROW) * 4;
         const float* q = g + (long long)r * ld + c;
-        if constexpr (!GUARD) {
-            v[i] = *reinterpret_cast<const f4*>(q);
-        } else {
-            const bool rok = r < vr;
-            v[i].x = (rok && c + 0 < vc) ? q[0] : 0.0f;
-            v[i].y = (rok && c + 1 < vc) ? q[1] : 0.0f;
-            v[i].z = (rok && c + 2 < vc) ? q[2] : 0.0f;
-            v[i].w = (rok && c + 3 < vc) ? q[3] : 0.0f;
-        }
+        const bool rok = r < vr;
+        v[i].x = (rok && c + 0 < vc) ? q[0] : 0.0f;
+        v[i].y = (rok && c + 1 < vc) ? q[1] : 0.0f;
+        v[i].z = (rok && c + 2 < vc) ? q[2] : 0.0f;
+        v[i].w = (rok && c + 3 < vc) ? q[3] : 0.0f;
     }
 }
 
@@ -178,9 +173,8 @@ __device__ __forceinline__ void load_frag(const float* __restrict__ s, int row,
     }
 }
 
-template <int BM, int BN, int BK, int WARPS_M, int WARPS_N, bool TA, bool TB,
-          bool GUARD, bool EPI>
-__device__ __forceinline__ void gemm_body(const GemmArgs& p, int logical) {
+template <int BM, int BN, int BK, int WARPS_M, int WARPS_N, bool TA, bool TB, bool EPI>
+__device__ __forceinline__ void gemm_body_guarded(const GemmArgs& p, int logical) {
     constexpr int NT = WARPS_M * WARPS_N * 64;
     constexpr int WM = BM / WARPS_M, WN = BN / WARPS_N;
     constexpr int FM = WM / 32, FN = WN / 32;
@@ -229,10 +223,10 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p, int logical) {
 #define FORGE_LOAD_SLAB(KT_)                                                   \
     do {                                                                       \
         const int kv_ = p.K - (KT_) * BK;                                      \
-        tile_load<A_ROWS, A_COLS, NT, GUARD>(ra, a_base + (KT_) * a_kstride, p.lda, \
-                                             TA ? kv_ : a_vr, TA ? a_vc : kv_);      \
-        tile_load<B_ROWS, B_COLS, NT, GUARD>(rb, b_base + (KT_) * b_kstride, p.ldb, \
-                                             TB ? b_vr : kv_, TB ? kv_ : b_vc);      \
+        tile_load_guarded<A_ROWS, A_COLS, NT>(ra, a_base + (KT_) * a_kstride, p.lda, \
+                                              TA ? kv_ : a_vr, TA ? a_vc : kv_);     \
+        tile_load_guarded<B_ROWS, B_COLS, NT>(rb, b_base + (KT_) * b_kstride, p.ldb, \
+                                              TB ? b_vr : kv_, TB ? kv_ : b_vc);     \
     } while (0)
     if (KT > 0) {
         FORGE_LOAD_SLAB(0);
@@ -285,24 +279,17 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p, int logical) {
         for (int j = 0; j < FN; j++) {
             v16f& a = acc[i][j];
             const int col = col_base + j * 32;
-            // Visits the 16 accumulators of block (i, j) as (r, row, EL(ptr)),
-            // EL(ptr) being the element (row, col) of an [M, ldc] operand.
-            // Guarded tiles skip elements outside the matrix and address with
-            // 64-bit indices; unguarded tiles (matrices below 2^30 elements,
-            // checked by the host) use a 32-bit byte offset from the
-            // operand's base, so each address takes one VGPR instead of two.
+            // Visits the 16 accumulators of block (i, j) inside the matrix as
+            // (r, row, EL(ptr)), EL(ptr) being the element (row, col) of an
+            // [M, ldc] operand.
 #define FORGE_EPI_EACH(BODY)                                                     \
     _Pragma("unroll") for (int r = 0; r < 16; r++) {                             \
         const int row = row_base + i * 32 + 8 * (r >> 2) + (r & 3);              \
-        if (GUARD && (row >= p.M || col >= p.N)) continue;                       \
+        if (row >= p.M || col >= p.N) continue;                                  \
         const long long idx = (long long)row * p.ldc + col;                      \
-        const unsigned boff = ((unsigned)row * (unsigned)p.ldc + (unsigned)col) * 4u; \
-        (void)idx; (void)boff;                                                   \
         BODY;                                                                    \
     }
-#define EL(ptr) (*(GUARD ? (ptr) + idx                                           \
-                         : reinterpret_cast<float*>(reinterpret_cast<char*>(     \
-                               const_cast<float*>(ptr)) + boff)))
+#define EL(ptr) (*((ptr) + idx))
             // The same, one element at a time: the scheduler may not
             // interleave the (long) activation code of several elements,
             // which would need registers for all of them at once.
@@ -315,7 +302,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p, int logical) {
                 // order (alpha, bias, residual, aux, pre_out, activation, store
                 // or update) is that of gemm_epilogue_store.
                 if (p.alpha != 1.0f) FORGE_EPI_EACH(a[r] = p.alpha * a[r]);
-                if (p.bias && (!GUARD || col < p.N)) {
+                if (p.bias && col < p.N) {
                     const float b = p.bias[col];
                     FORGE_EPI_EACH(a[r] = a[r] + b);
                 }
@@ -350,20 +337,11 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& p, int logical) {
     }
 }
 
-// One GEMM per launch: grid = tiles.
-template <int BM, int BN, int BK, int WARPS_M, int WARPS_N, bool TA, bool TB,
-          bool GUARD, bool EPI>
-__device__ __forceinline__ void gemm_single(const GemmArgs& p) {
-    gemm_body<BM, BN, BK, WARPS_M, WARPS_N, TA, TB, GUARD, EPI>(
+// One guarded GEMM per launch: grid = tiles.
+template <int BM, int BN, int BK, int WARPS_M, int WARPS_N, bool TA, bool TB, bool EPI>
+__device__ __forceinline__ void gemm_single_guarded(const GemmArgs& p) {
+    gemm_body_guarded<BM, BN, BK, WARPS_M, WARPS_N, TA, TB, EPI>(
         p, xcd_logical(blockIdx.x, gridDim.x));
-}
-
-// A batch of GEMMs per launch: grid = count * tiles.
-template <int BM, int BN, int BK, int WARPS_M, int WARPS_N, bool TA, bool TB>
-__device__ __forceinline__ void gemm_batch(const GemmBatchArgs& b) {
-    const int logical = xcd_logical(blockIdx.x, gridDim.x);
-    const int z = logical / b.tiles;
-    gemm_body<BM, BN, BK, WARPS_M, WARPS_N, TA, TB, false, true>(b.p[z], logical - z * b.tiles);
 }
 
 // Sum of the split-K partial products P[s] ([splits][M][N], row pitch N) in

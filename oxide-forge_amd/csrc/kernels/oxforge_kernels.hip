@@ -21,9 +21,9 @@ using namespace forge;
     FORGE_KERNEL void __launch_bounds__(256) NAME(GemmArgs p) {               \
         gemm_single_x<BM, BN, BK, TA, TB, EPI>(p);                             \
     }
-#define GEMM_KERNEL(NAME, BM, BN, BK, WMW, WNW, TA, TB, GUARD, EPI)          \
+#define GEMM_GUARDED_KERNEL(NAME, BM, BN, BK, WMW, WNW, TA, TB, EPI)        \
     FORGE_KERNEL void __launch_bounds__(WMW * WNW * 64) NAME(GemmArgs p) {   \
-        gemm_single<BM, BN, BK, WMW, WNW, TA, TB, GUARD, EPI>(p);            \
+        gemm_single_guarded<BM, BN, BK, WMW, WNW, TA, TB, EPI>(p);           \
     }
 
 // Epilogue instances: the unguarded tiles the dispatcher chooses from (by
@@ -33,7 +33,7 @@ using namespace forge;
     GEMM_X_KERNEL(forge_gemm_##AB##_128x64x32_x_e, 128, 64, 32, TA, TB, true)        \
     GEMM_X_KERNEL(forge_gemm_##AB##_64x128x32_x_e, 64, 128, 32, TA, TB, true)        \
     GEMM_X_KERNEL(forge_gemm_##AB##_64x64x32_x_e, 64, 64, 32, TA, TB, true)          \
-    GEMM_KERNEL(forge_gemm_##AB##_64x64x16_2x2_g_e, 64, 64, 16, 2, 2, TA, TB, true, true)
+    GEMM_GUARDED_KERNEL(forge_gemm_##AB##_64x64x16_2x2_g_e, 64, 64, 16, 2, 2, TA, TB, true)
 
 GEMM_FAMILY(nn, false, false)
 GEMM_FAMILY(nt, false, true)
@@ -77,7 +77,7 @@ GEMM_X_KERNEL(forge_gemm_nn_128x128x64_x, 128, 128, 64, false, false, false)
 GEMM_X_KERNEL(forge_gemm_nn_128x64x32_x, 128, 64, 32, false, false, false)
 GEMM_X_KERNEL(forge_gemm_nn_64x128x32_x, 64, 128, 32, false, false, false)
 GEMM_X_KERNEL(forge_gemm_nn_64x64x32_x, 64, 64, 32, false, false, false)
-GEMM_KERNEL(forge_gemm_nn_64x64x16_2x2_g, 64, 64, 16, 2, 2, false, false, true, false)
+GEMM_GUARDED_KERNEL(forge_gemm_nn_64x64x16_2x2_g, 64, 64, 16, 2, 2, false, false, false)
 
 // ------------------------------------------------------------------- rows
 #define ROW_KERNEL(NAME, OP, VPT, PARTIALS) \
