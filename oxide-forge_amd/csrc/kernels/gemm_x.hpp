@@ -174,9 +174,17 @@ struct XReads {
     static constexpr int N = KC ? F : 4 * (F / XVec<F>::W);
 };
 
-template <int BM, int BN, int BK, bool TA, bool TB, bool EPI>
+// KS = 2 splits K inside the workgroup: eight waves in two groups of four,
+// group g multiplying the g-th half of the slabs into its own accumulators
+// through its own two LDS stages.  The halves are added (first half +
+// second half) before the epilogue.  It gives a CU two waves per SIMD when
+// the output has only one tile per CU.  The sum order differs from KS = 1,
+// so a shape computes with one KS everywhere (the host's choice depends on
+// the shape only).
+template <int BM, int BN, int BK, int KS, bool TA, bool TB, bool EPI>
 __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
-    constexpr int NT = 256;
+    static_assert(KS == 1 || KS == 2, "one or two K groups");
+    constexpr int NT = 256;  // threads of one K group
     constexpr int TM = BM / 2, TN = BN / 2;
     constexpr int FM = TM / 16, FN = TN / 16;
     constexpr int CH = BK / 16;
@@ -192,11 +200,11 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     using SB = XSlab<B_ROWS, B_COLS, B_KC>;
     constexpr int DMA_PER_STAGE = SA::PER_WAVE + SB::PER_WAVE;
     static_assert(CH % 2 == 0, "slabs hold an even number of 16-wide chunks");
-    // The two slab stages, reused by the epilogue for each wave's TM x TN
-    // sub-tile of C (row pitch CP).
+    // The two slab stages of each K group, reused by the epilogue for each
+    // wave's TM x TN sub-tile of C (row pitch CP).
     constexpr int CP = TN + 4;
-    constexpr int SMEM = 2 * STAGE > 4 * TM * CP ? 2 * STAGE : 4 * TM * CP;
-    __shared__ __attribute__((aligned(1024))) float smem[SMEM];
+    constexpr int SMEM = KS * 2 * STAGE > KS * 4 * TM * CP ? KS * 2 * STAGE : KS * 4 * TM * CP;
+    __shared__ __attribute__((aligned(1024))) float smem_all[SMEM];
 
     const int num_m = p.M / BM, num_n = p.N / BN;
     int tm, tn;
@@ -204,14 +212,18 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     const int m0 = tm * BM, n0 = tn * BN;
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int kg = KS == 1 ? 0 : (int)(threadIdx.x >> 8);  // K group
+    const int wave = (threadIdx.x >> 6) & 3;                // wave within the group
     const int wm = wave >> 1, wn = wave & 1;
     const int l16 = lane & 15, kq = lane >> 4;
+    float* const smem = smem_all + kg * (2 * STAGE);
 
-    const float* a_base = TA ? p.A + m0 : p.A + (long long)m0 * p.lda;
-    const float* b_base = TB ? p.B + (long long)n0 * p.ldb : p.B + n0;
+    // Slabs of this K group: [kg * KT, (kg + 1) * KT) of the K / BK slabs.
+    const int KT = p.K / BK / KS;
     const long long a_kstride = TA ? (long long)BK * p.lda : BK;
     const long long b_kstride = TB ? BK : (long long)BK * p.ldb;
+    const float* a_base = (TA ? p.A + m0 : p.A + (long long)m0 * p.lda) + kg * KT * a_kstride;
+    const float* b_base = (TB ? p.B + (long long)n0 * p.ldb : p.B + n0) + kg * KT * b_kstride;
 
     v4f acc[FM][FN];
 #pragma unroll
@@ -224,7 +236,6 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     const int a_off = wm * TM, b_off = wn * TN;
     float fa[2][FM * 4], fb[2][FN * 4];
 
-    const int KT = p.K / BK;
     auto issue = [&](int k_slab, int stage) {
         float* d = smem + stage * STAGE;
         x_dma_slab<A_ROWS, A_COLS, A_KC>(d, a_base + k_slab * a_kstride, p.lda, wave, lane);
@@ -324,8 +335,11 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     // back row by row: four consecutive columns per lane, so operands and
     // results move as 128-bit accesses and the fused steps are one compact
     // loop instead of code unrolled over every accumulator.
+    // With two K groups each sub-tile is written twice (once per group),
+    // and each group then finishes half of its rows, adding the groups'
+    // values in group order.
     __syncthreads();  // every wave is done with the slab stages
-    float* cw = smem + wave * (TM * CP);
+    float* cw = smem_all + (kg * 4 + wave) * (TM * CP);
     if constexpr (!B_KC && XVec<FN>::W == 4) {
 #pragma unroll
         for (int i = 0; i < FM; i++)
@@ -350,9 +364,13 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
                     cw[rr * CP + x_index<B_KC, FN>(0, j, l16)] = acc[i][j][r];
             }
     }
+    if constexpr (KS == 2) __syncthreads();  // both groups' halves written
+    const float* c0 = smem_all + wave * (TM * CP);  // group 0's copy of the sub-tile
     const int row0 = m0 + a_off, col0 = n0 + b_off;
     constexpr int F4_ROW = TN / 4;
-    constexpr int ITER = TM * F4_ROW / 64;  // 128-bit groups per lane
+    constexpr int ROWS = TM / KS;  // sub-tile rows this wave finishes
+    const int rbase = kg * ROWS;
+    constexpr int ITER = ROWS * F4_ROW / 64;  // 128-bit groups per lane
     constexpr int NB = ITER < 4 ? ITER : 4;  // groups whose operands load together
     static_assert(ITER % NB == 0, "epilogue batches");
     const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -366,8 +384,12 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
 #pragma unroll
         for (int u = 0; u < NB; u++) {
             const int q = lane + 64 * (b0 + u);
-            const int rr = q / F4_ROW, c4 = q % F4_ROW;
-            z[u] = *reinterpret_cast<const f4*>(cw + rr * CP + 4 * c4);
+            const int rr = rbase + q / F4_ROW, c4 = q % F4_ROW;
+            z[u] = *reinterpret_cast<const f4*>(c0 + rr * CP + 4 * c4);
+            if constexpr (KS == 2) {
+                const f4 h = *reinterpret_cast<const f4*>(c0 + 4 * TM * CP + rr * CP + 4 * c4);
+                z[u] = f4{z[u].x + h.x, z[u].y + h.y, z[u].z + h.z, z[u].w + h.w};
+            }
             col[u] = col0 + 4 * c4;
             idx[u] = (long long)(row0 + rr) * p.ldc + col[u];
             res[u] = mul[u] = old[u] = zero;
@@ -423,16 +445,16 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     }
 }
 
-template <int BM, int BN, int BK, bool TA, bool TB, bool EPI>
+template <int BM, int BN, int BK, int KS, bool TA, bool TB, bool EPI>
 __device__ __forceinline__ void gemm_single_x(const GemmArgs& p) {
-    gemm_body_x<BM, BN, BK, TA, TB, EPI>(p, xcd_logical(blockIdx.x, gridDim.x));
+    gemm_body_x<BM, BN, BK, KS, TA, TB, EPI>(p, xcd_logical(blockIdx.x, gridDim.x));
 }
 
 template <int BM, int BN, int BK, bool TA, bool TB>
 __device__ __forceinline__ void gemm_batch_x(const GemmBatchArgs& b) {
     const int logical = xcd_logical(blockIdx.x, gridDim.x);
     const int z = logical / b.tiles;
-    gemm_body_x<BM, BN, BK, TA, TB, true>(b.p[z], logical - z * b.tiles);
+    gemm_body_x<BM, BN, BK, 1, TA, TB, true>(b.p[z], logical - z * b.tiles);
 }
 
 }  // namespace forge

@@ -544,6 +544,7 @@ namespace {
 struct GemmConfig {
     const char* tag;  // e.g. "128x256x32_x"
     int bm, bn, bk, threads;
+    int ks = 1;       // K groups inside the workgroup (K % (bk * ks) == 0)
 };
 
 const GemmConfig kTile128x256 = {"128x256x32_x", 128, 256, 32, 256};
@@ -552,6 +553,10 @@ const GemmConfig kTile128x64 = {"128x64x32_x", 128, 64, 32, 256};
 const GemmConfig kTile64x128 = {"64x128x32_x", 64, 128, 32, 256};
 const GemmConfig kTile64x64 = {"64x64x32_x", 64, 64, 32, 256};
 const GemmConfig kGuard64 = {"64x64x16_2x2_g", 64, 64, 16, 256};
+// Eight-wave variants with K split over two wave groups (fused epilogue and
+// plain NN instances; no batched ones).
+const GemmConfig kTile128x64k2 = {"128x64x32_k2_x", 128, 64, 32, 512, 2};
+const GemmConfig kTile64x128k2 = {"64x128x32_k2_x", 64, 128, 32, 512, 2};
 
 // Unguarded tiles, largest first, and their measured full-device
 // efficiency relative to 128x256 (4096^3 on MI355X: 140.6, 138.5, 134.7,
@@ -575,13 +580,13 @@ const double kTileEfficiency[] = {1.0, 0.985, 0.958, 0.951, 0.86};
 // shapes and shapes the tiles do not divide take the bounds-guarded 64x64
 // tile.  `count` same-shape products share the launch.
 const GemmConfig& choose_gemm(forge_runtime* rt, size_t M, size_t N, size_t K, bool aligned,
-                              bool epilogue, size_t count = 1) {
+                              bool epilogue, size_t count = 1, bool allow_k2 = false) {
     const size_t cus = rt->cu_count > 0 ? (size_t)rt->cu_count : 256;
     const GemmConfig* best = &kGuard64;
     double best_score = 0.0;
     size_t best_tiles = 0;
     auto fits = [&](const GemmConfig& g) {
-        return aligned && M % g.bm == 0 && N % g.bn == 0 && K % g.bk == 0;
+        return aligned && M % g.bm == 0 && N % g.bn == 0 && K % ((size_t)g.bk * g.ks) == 0;
     };
     for (int i = epilogue ? 1 : 0; i < 5; i++) {
         const GemmConfig& g = *kUnguarded[i];
@@ -595,7 +600,18 @@ const GemmConfig& choose_gemm(forge_runtime* rt, size_t M, size_t N, size_t K, b
             best_tiles = t;
         }
     }
-    if (best == &kTile128x128 && best_tiles <= cus && fits(kTile64x128)) best = &kTile64x128;
+    if (best == &kTile128x128 && best_tiles <= cus && fits(kTile64x128)) {
+        best = &kTile64x128;
+        best_tiles *= 2;
+    }
+    // One 128x64 or 64x128 tile per CU: split K over two wave groups instead
+    // (two waves per SIMD).  2048x1024x{1024,2048,4096} + bias: 111.1,
+    // 121.2 and 126.2 TFLOP/s against 103.0, 113.0 and 117.7.  Not for
+    // batched launches (no such instance) or products the caller splits in K.
+    if (allow_k2 && best_tiles <= cus && (best == &kTile128x64 || best == &kTile64x128)) {
+        if (fits(kTile64x128k2)) best = &kTile64x128k2;
+        else if (fits(kTile128x64k2)) best = &kTile128x64k2;
+    }
     return *best;
 }
 
@@ -733,7 +749,7 @@ forge_status gemm_dispatch(forge_runtime* rt, forge_stream* s, int ta, int tb, f
     const int splits = choose_splits(rt, M, N, K, aligned, &split_cfg);
     if (splits > 1) return gemm_split_launch(rt, s, ta, tb, a, *split_cfg, splits);
     const bool epi = !(plain_name && !ta && !tb);
-    const GemmConfig& cfg = choose_gemm(rt, M, N, K, aligned, epi);
+    const GemmConfig& cfg = choose_gemm(rt, M, N, K, aligned, epi, 1, true);
     char name[96];
     snprintf(name, sizeof name, "forge_gemm_%s_%s%s", gemm_ab(ta, tb), cfg.tag,
              epi ? "_e" : "");
@@ -926,7 +942,7 @@ extern "C" forge_status forge_gemm_f32_tile(forge_runtime* rt, forge_stream* s,
                                             const char* tile_tag, forge_slice A, forge_slice B,
                                             forge_slice C, size_t M, size_t N, size_t K) {
     if (!rt || !tile_tag) return fail(FORGE_EINVAL, "null argument");
-    unsigned bm = 0, bn = 0, bk = 0, threads = 256;
+    unsigned bm = 0, bn = 0, bk = 0, threads = 256, ks = 1;
     bool guarded = false;
     char tail[8] = {0};
     if (sscanf(tile_tag, "%ux%ux%u_%7s", &bm, &bn, &bk, tail) != 4 || bm == 0 || bn == 0 ||
@@ -934,6 +950,9 @@ extern "C" forge_status forge_gemm_f32_tile(forge_runtime* rt, forge_stream* s,
         return fail(FORGE_EINVAL, "bad tile tag %s", tile_tag);
     if (strcmp(tail, "x") == 0) {
         // Four-wave instance <BM>x<BN>x<BK>_x.
+    } else if (strcmp(tail, "k2_x") == 0) {
+        threads = 512;  // eight waves, K over two groups
+        ks = 2;
     } else if (strcmp(tail, "2x2_g") == 0) {
         guarded = true;
     } else {
@@ -944,8 +963,8 @@ extern "C" forge_status forge_gemm_f32_tile(forge_runtime* rt, forge_stream* s,
     FORGE_TRY(need(A, M * K, "gemm A"));
     FORGE_TRY(need(B, K * N, "gemm B"));
     FORGE_TRY(need(C, M * N, "gemm C"));
-    if (!guarded && (M % bm || N % bn || K % bk || !aligned16(A.ptr) || !aligned16(B.ptr) ||
-                     !aligned16(C.ptr) || K % 4 || N % 4))
+    if (!guarded && (M % bm || N % bn || K % (bk * ks) || !aligned16(A.ptr) ||
+                     !aligned16(B.ptr) || !aligned16(C.ptr) || K % 4 || N % 4))
         return fail(FORGE_EINVAL, "shape %zux%zux%zu does not fit unguarded tile %s", M, N, K,
                     tile_tag);
     if (M == 0 || N == 0) return FORGE_OK;
@@ -994,14 +1013,17 @@ extern "C" forge_status forge_gemm_ex_f32_tile(forge_runtime* rt, forge_stream* 
                                                size_t M, size_t N, size_t K,
                                                const forge_gemm_epilogue* ep) {
     if (!rt || !tile_tag) return fail(FORGE_EINVAL, "null argument");
-    const GemmConfig* cfg = strcmp(tile_tag, kGuard64.tag) == 0 ? &kGuard64 : nullptr;
+    const GemmConfig* cfg = nullptr;
+    for (const GemmConfig* c : {&kGuard64, &kTile128x64k2, &kTile64x128k2})
+        if (strcmp(c->tag, tile_tag) == 0) cfg = c;
     for (const GemmConfig* c : kUnguarded)
         if (c != &kTile128x256 && strcmp(c->tag, tile_tag) == 0) cfg = c;
     if (!cfg) return fail(FORGE_EINVAL, "tile %s has no epilogue instance", tile_tag);
     GemmArgs a{};
     bool aligned = false;
     FORGE_TRY(gemm_args(trans_a, trans_b, A, B, C, M, N, K, ep, &a, &aligned));
-    if (cfg != &kGuard64 && (!aligned || M % cfg->bm || N % cfg->bn || K % cfg->bk))
+    if (cfg != &kGuard64 &&
+        (!aligned || M % cfg->bm || N % cfg->bn || K % ((size_t)cfg->bk * cfg->ks)))
         return fail(FORGE_EINVAL, "shape %zux%zux%zu does not fit unguarded tile %s", M, N, K,
                     tile_tag);
     if (M == 0 || N == 0) return FORGE_OK;
@@ -1038,9 +1060,11 @@ extern "C" forge_status forge_gemm_batch_f32(forge_runtime* rt, forge_stream* s,
     if (count == 0 || M == 0 || N == 0) return FORGE_OK;
     const GemmConfig& cfg = choose_gemm(rt, M, N, K, all_aligned, true, count);
     const GemmConfig* split_cfg = nullptr;
-    // Shapes the single-product path splits in K are dispatched one by one,
-    // so every product equals its forge_gemm_ex_f32 result bit for bit.
-    const bool split = choose_splits(rt, M, N, K, all_aligned, &split_cfg) > 1;
+    // Shapes the single-product path splits in K (into slices, or over two
+    // wave groups) are dispatched one by one, so every product equals its
+    // forge_gemm_ex_f32 result bit for bit.
+    const bool split = choose_splits(rt, M, N, K, all_aligned, &split_cfg) > 1 ||
+                       choose_gemm(rt, M, N, K, all_aligned, true, 1, true).ks > 1;
     if (count > (size_t)GEMM_BATCH_MAX || &cfg == &kGuard64 || split) {
         for (size_t z = 0; z < count; z++)
             FORGE_TRY(gemm_dispatch(rt, s, trans_a, trans_b, problems[z].A, problems[z].B,
