@@ -443,59 +443,71 @@ __device__ __forceinline__ void reduce_body(const float* __restrict__ x, long lo
 
 // ------------------------------------------------------------- transpose
 
-// out[c, r] = in[r, c] for in [rows, cols] (layout.rs:8-55).  64x64 tiles
-// through LDS with a 65-float pitch: the float4 row loads and the column
-// reads that assemble each float4 store are both bank-conflict free.
-constexpr int TR_TILE = 64;
-constexpr int TR_PITCH = TR_TILE + 1;
+// out[c, r] = in[r, c] for in [rows, cols] (layout.rs:8-55).  A workgroup of
+// 256 threads moves one 64 x TC tile through LDS (pitch TC + 1).  Each wave
+// load instruction covers 4 input rows x 16 float4, and each wave store covers
+// 4 output rows x 16 float4, so with the odd pitch both the scalar LDS stores
+// and the column reads that assemble each float4 store are bank-conflict
+// free.  TC = 256 (1 KiB contiguous per input row) is the unguarded path when
+// cols allows it: wider input rows per tile keep HBM busier than 64x64 tiles
+// (about 5.2 against 4.8 TB/s at [8192, 4096]); TC = 64 serves every other
+// shape, GUARD for edges and unaligned views.
+constexpr int TR_ROWS = 64;
 
-template <bool GUARD>
+template <int TC, bool GUARD>
 __device__ __forceinline__ void transpose_body(const float* __restrict__ in,
                                                float* __restrict__ out, int rows,
                                                int cols) {
-    __shared__ float tile[TR_TILE * TR_PITCH];
+    static_assert(TC % 64 == 0 && (!GUARD || TC == 64), "tile width");
+    constexpr int P = TC + 1, Q = TC / 64;
+    __shared__ float tile[TR_ROWS * P];
     const int t = threadIdx.x;  // 256 threads
-    const int tiles_c = (cols + TR_TILE - 1) / TR_TILE;
+    const int tiles_c = (cols + TC - 1) / TC;
     const int tr = blockIdx.x / tiles_c, tc = blockIdx.x % tiles_c;
-    const int r0 = tr * TR_TILE, c0 = tc * TR_TILE;
-    const int sub = t & 15;  // float4 slot inside a 64-wide tile row
+    const int r0 = tr * TR_ROWS, c0 = tc * TC;
+    const int sub = t & 15;  // float4 slot inside 64 columns
+    const int rr = t >> 4;   // 0..15
+    float4 v[4 * Q];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int lr = (t >> 4) + 16 * i;
-        const int r = r0 + lr, c = c0 + sub * 4;
-        float4 v;
+    for (int i = 0; i < 4 * Q; i++) {
+        const int lr = rr + 16 * (i / Q), lc = 64 * (i % Q) + 4 * sub;
+        const int r = r0 + lr, c = c0 + lc;
         if constexpr (!GUARD) {
-            v = *reinterpret_cast<const float4*>(in + (long long)r * cols + c);
+            v[i] = *reinterpret_cast<const float4*>(in + (long long)r * cols + c);
         } else {
             const float* p = in + (long long)r * cols + c;
             const bool ok = r < rows;
-            v.x = (ok && c + 0 < cols) ? p[0] : 0.0f;
-            v.y = (ok && c + 1 < cols) ? p[1] : 0.0f;
-            v.z = (ok && c + 2 < cols) ? p[2] : 0.0f;
-            v.w = (ok && c + 3 < cols) ? p[3] : 0.0f;
+            v[i].x = (ok && c + 0 < cols) ? p[0] : 0.0f;
+            v[i].y = (ok && c + 1 < cols) ? p[1] : 0.0f;
+            v[i].z = (ok && c + 2 < cols) ? p[2] : 0.0f;
+            v[i].w = (ok && c + 3 < cols) ? p[3] : 0.0f;
         }
-        float* s = tile + lr * TR_PITCH + sub * 4;
-        s[0] = v.x; s[1] = v.y; s[2] = v.z; s[3] = v.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 4 * Q; i++) {
+        const int lr = rr + 16 * (i / Q), lc = 64 * (i % Q) + 4 * sub;
+        float* s = tile + lr * P + lc;
+        s[0] = v[i].x; s[1] = v[i].y; s[2] = v[i].z; s[3] = v[i].w;
     }
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int lc = (t >> 4) + 16 * i;  // input column = output row
-        const int lr = sub * 4;            // first of four input rows
-        float4 v;
-        v.x = tile[(lr + 0) * TR_PITCH + lc];
-        v.y = tile[(lr + 1) * TR_PITCH + lc];
-        v.z = tile[(lr + 2) * TR_PITCH + lc];
-        v.w = tile[(lr + 3) * TR_PITCH + lc];
+    for (int i = 0; i < 4 * Q; i++) {
+        const int lc = rr + 16 * i;  // input column = output row
+        const int lr = sub * 4;      // first of four input rows
+        float4 w;
+        w.x = tile[(lr + 0) * P + lc];
+        w.y = tile[(lr + 1) * P + lc];
+        w.z = tile[(lr + 2) * P + lc];
+        w.w = tile[(lr + 3) * P + lc];
         const int orow = c0 + lc, ocol = r0 + lr;
         if constexpr (!GUARD) {
-            *reinterpret_cast<float4*>(out + (long long)orow * rows + ocol) = v;
+            *reinterpret_cast<float4*>(out + (long long)orow * rows + ocol) = w;
         } else if (orow < cols) {
             float* p = out + (long long)orow * rows + ocol;
-            if (ocol + 0 < rows) p[0] = v.x;
-            if (ocol + 1 < rows) p[1] = v.y;
-            if (ocol + 2 < rows) p[2] = v.z;
-            if (ocol + 3 < rows) p[3] = v.w;
+            if (ocol + 0 < rows) p[0] = w.x;
+            if (ocol + 1 < rows) p[1] = w.y;
+            if (ocol + 2 < rows) p[2] = w.z;
+            if (ocol + 3 < rows) p[3] = w.w;
         }
     }
 }

@@ -233,9 +233,12 @@ FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_reduce_sum(const float* x,
 FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_reduce_max(const float* x, long long n, float* out) {
     reduce_body<true>(x, n, out);
 }
+FORGE_KERNEL void __launch_bounds__(256) forge_transpose_w(const float* in, float* out, int rows, int cols) {
+    transpose_body<256, false>(in, out, rows, cols);
+}
 FORGE_KERNEL void __launch_bounds__(256) forge_transpose(const float* in, float* out, int rows, int cols) {
-    transpose_body<false>(in, out, rows, cols);
+    transpose_body<64, false>(in, out, rows, cols);
 }
 FORGE_KERNEL void __launch_bounds__(256) forge_transpose_g(const float* in, float* out, int rows, int cols) {
-    transpose_body<true>(in, out, rows, cols);
+    transpose_body<64, true>(in, out, rows, cols);
 }

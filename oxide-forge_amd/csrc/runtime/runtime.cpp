@@ -1086,11 +1086,15 @@ extern "C" forge_status forge_transpose_f32(forge_runtime* rt, forge_stream* s, 
     FORGE_TRY(need(in, rows * cols, "transpose in"));
     FORGE_TRY(need(out, rows * cols, "transpose out"));
     if (rows == 0 || cols == 0) return FORGE_OK;
-    bool fast = aligned16(in.ptr) && aligned16(out.ptr) && rows % 64 == 0 && cols % 64 == 0;
-    unsigned tiles = (unsigned)(((rows + 63) / 64) * ((cols + 63) / 64));
+    // 64x256 tiles when the shape divides, 64x64 otherwise, guarded 64x64
+    // for edges and views not 16-byte aligned.
+    const bool fast = aligned16(in.ptr) && aligned16(out.ptr) && rows % 64 == 0 && cols % 64 == 0;
+    const bool wide = fast && cols % 256 == 0;
+    const size_t tc = wide ? 256 : 64;
+    unsigned tiles = (unsigned)(((rows + 63) / 64) * ((cols + tc - 1) / tc));
     int r = (int)rows, c = (int)cols;
-    return launch_args(rt, s, fast ? "forge_transpose" : "forge_transpose_g", dim3(tiles),
-                       dim3(256), 0, (const float*)in.ptr, out.ptr, r, c);
+    const char* name = wide ? "forge_transpose_w" : fast ? "forge_transpose" : "forge_transpose_g";
+    return launch_args(rt, s, name, dim3(tiles), dim3(256), 0, (const float*)in.ptr, out.ptr, r, c);
 }
 
 extern "C" forge_status forge_softmax_rows(forge_runtime* rt, forge_stream* s, forge_slice x,

@@ -178,7 +178,8 @@ def test_gemm_epilogue_matches_unfused_bit_exact(rt, M, N, K, ta, tb):
 
 # -------------------------------------------------------------- transpose
 @pytest.mark.parametrize("rows,cols", [(64, 64), (128, 256), (17, 33), (1, 100), (100, 1),
-                                       (65, 129), (0, 5), (8192, 4096)])
+                                       (65, 129), (0, 5), (192, 768), (256, 1280),
+                                       (8192, 4096)])
 def test_transpose_bit_exact(rt, rows, cols):
     say(f"transpose {rows}x{cols}")
     x = orc.uniform((rows, cols), rows + cols)
