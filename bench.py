@@ -486,7 +486,7 @@ def main() -> int:
     M = N = K = 4096
     log("gemm 4096^3")
     tflops, ms = gemm_tflops(rt, orc, M, N, K, args.steps, args.warmup)
-    kernel = "forge_gemm_nn_128x256x32_x"
+    kernel = rt.gemm_kernel_name(M, N, K)
     traffic = load_traffic(kernel)
     line = {
         "metric": METRIC,

@@ -229,9 +229,9 @@ forge_status forge_gemm_ex_f32(forge_runtime *rt, forge_stream *stream,
  * 128x64x32, 64x128x32, 64x64x32), "<BM>x<BN>x<BK>_k2_x" for the eight-wave
  * tiles that split K over two wave groups (128x64x32, 64x128x32,
  * 128x128x32; K % (2 BK) == 0) or "64x64x16_2x2_g" for the guarded one.
- * Unguarded tiles require M % BM == N % BN == K % BK == 0 and 16-byte
- * aligned operands; anything else is FORGE_EINVAL.  Used by the benchmark's
- * tile sweep. */
+ * Unguarded tiles require M % BM == N % BN == K % BK == 0, 16-byte aligned
+ * operands and K, N <= 2^21; anything else is FORGE_EINVAL.  Used by the
+ * benchmark's tile sweep. */
 forge_status forge_gemm_f32_tile(forge_runtime *rt, forge_stream *stream,
                                  const char *tile_tag, forge_slice A,
                                  forge_slice B, forge_slice C, size_t M,
@@ -258,6 +258,17 @@ forge_status forge_gemm_ex_f32_tile(forge_runtime *rt, forge_stream *stream,
                                     forge_slice A, forge_slice B, forge_slice C,
                                     size_t M, size_t N, size_t K,
                                     const forge_gemm_epilogue *epilogue);
+
+/* Diagnostic entry point (no reference counterpart): the name of the kernel
+ * that forge_gemm_f32 (fused = 0) or forge_gemm_ex_f32 (fused = 1) launches
+ * for a product of this shape and these transposes with 16-byte aligned
+ * operands, written NUL-terminated to name (cap bytes; a name that does not
+ * fit is FORGE_EINVAL).  A product computed as K slices is reported as
+ * "<batched slice kernel>/split<N>".  Lets benchmarks and profiles name the
+ * kernel they measure. */
+forge_status forge_gemm_kernel_name(forge_runtime *rt, int trans_a, int trans_b,
+                                    size_t M, size_t N, size_t K, int fused,
+                                    char *name, size_t cap);
 
 /* One product of a batch: operands and its own fused epilogue. */
 typedef struct forge_gemm_problem {

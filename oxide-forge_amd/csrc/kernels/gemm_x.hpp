@@ -76,69 +76,120 @@ __device__ __forceinline__ int x_swz(int row) {
 template <int ROWS, int COLS, bool SWZ>
 struct XSlab {
     static constexpr int P = COLS / 4;
+    static constexpr int RPI = 64 / P;          // rows per wave instruction
     static constexpr int INSTR = ROWS * P / 64;  // wave instructions per slab
     static constexpr int PER_WAVE = INSTR / 4;
+    static_assert(P <= 64 && 64 % P == 0, "a wave instruction fills whole rows");
     static_assert(INSTR % 4 == 0, "slab must split evenly over four waves");
 };
 
+// Slab loads of one operand (buffer_load_dwordx4 ... lds).  A lane's byte
+// offset from the first row its instruction fills (its row within the
+// instruction times the row pitch, plus its swizzled piece) does not depend
+// on the slab, so it is computed once (the vector offset); the buffer
+// descriptor (the slab's first element), the instruction's row offset (the
+// scalar offset) and the LDS destination (M0) are wave-uniform and live in
+// scalar registers.  The main loop then spends no vector instructions on
+// addresses: each vector instruction between MFMAs costs the matrix pipe
+// several cycles, scalar ones do not.  Row pitches up to 2^21 floats keep
+// the offsets (at most 256 rows into the slab) below 2^31 bytes; the host
+// sends larger ones to the guarded kernel.
 template <int ROWS, int COLS, bool SWZ>
-__device__ __forceinline__ void x_dma_slab(float* lds, const float* __restrict__ g, long long ld,
-                                           int wave, int lane) {
+struct XDma {
     using S = XSlab<ROWS, COLS, SWZ>;
-#pragma unroll
-    for (int i = 0; i < S::PER_WAVE; i++) {
-        const int inst = wave * S::PER_WAVE + i;
-        const int q = inst * 64 + lane;
-        const int row = q / S::P;
-        const int piece = (q % S::P) ^ x_swz<S::P, SWZ>(row);
-        __builtin_amdgcn_global_load_lds(
-            (const void*)(g + (long long)row * ld + 4 * piece),
-            (void __attribute__((address_space(3)))*)(lds + inst * 256), 16, 0, 0);
-    }
-}
+    unsigned off[S::PER_WAVE];
 
-// Operand fragments of one 16-wide k chunk from a slab laid out by
-// x_dma_slab: frag[b * 4 + s] is block b's value at sub-step s.
-template <bool KC, int ROWS, int BK, int F>
-__device__ __forceinline__ void x_load_frag_dma(const float* __restrict__ s, int base, int chunk,
-                                                int l16, int kq, float (&frag)[F * 4]) {
-    if constexpr (KC) {
-        constexpr int P = BK / 4;
+    __device__ __forceinline__ void init(long long ld, int wave, int lane) {
 #pragma unroll
-        for (int b = 0; b < F; b++) {
-            const int row = base + 16 * b + l16;
-            const int piece = (chunk * 4 + kq) ^ x_swz<P, true>(row);
-            const f4 v = *reinterpret_cast<const f4*>(s + row * BK + 4 * piece);
-            frag[b * 4 + 0] = v.x;
-            frag[b * 4 + 1] = v.y;
-            frag[b * 4 + 2] = v.z;
-            frag[b * 4 + 3] = v.w;
+        for (int i = 0; i < S::PER_WAVE; i++) {
+            const int inst = wave * S::PER_WAVE + i;
+            const int r = lane / S::P;
+            const int piece = (lane % S::P) ^ x_swz<S::P, SWZ>(inst * S::RPI + r);
+            off[i] = (unsigned)(r * ld + 4 * piece) * 4u;
         }
-    } else {
-        constexpr int W = XVec<F>::W;
+    }
+    // Slab starting at g (wave-uniform) into LDS at lds (wave-uniform).
+    __device__ __forceinline__ void load(float* lds, const float* __restrict__ g, long long ld,
+                                         int wave) const {
+        // Raw buffer, no range limit below 4 GiB; 0x00020000 is the gfx9
+        // word 3 (32-bit data format, no swizzle).
+        const __amdgpu_buffer_rsrc_t rsrc =
+            __builtin_amdgcn_make_buffer_rsrc((void*)g, (short)0, -1, 0x00020000);
 #pragma unroll
-        for (int st = 0; st < 4; st++) {
-            const float* row = s + (chunk * 16 + 4 * kq + st) * ROWS + base;
+        for (int i = 0; i < S::PER_WAVE; i++) {
+            const int inst = wave * S::PER_WAVE + i;
+            const unsigned row_bytes = (unsigned)(inst * S::RPI) * (unsigned)ld * 4u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rsrc, (void __attribute__((address_space(3)))*)(lds + inst * 256), 16, off[i],
+                row_bytes, 0, 0);
+        }
+    }
+};
+
+// Operand fragments of one 16-wide k chunk from a slab laid out by XDma:
+// frag[b * 4 + s] is block b's value at sub-step s.  The lane's offset (in
+// floats, from the start of the LDS array) is precomputed per stage and
+// chunk, so each read is one base register plus an immediate.
+template <bool KC, int ROWS, int BK, int F>
+struct XFrag {
+    static constexpr int CH = BK / 16;
+    int off[2][CH];
+
+    // stage0: LDS offset of this operand in stage 0; stride: between stages;
+    // base: the wave's first row (k-contiguous, a multiple of 16) or column.
+    __device__ __forceinline__ void init(int stage0, int stride, int base, int l16, int kq) {
 #pragma unroll
-            for (int g = 0; g < F / W; g++) {
-                const float* q = row + 16 * W * g + W * l16;
-                if constexpr (W == 4) {
-                    const f4 v = *reinterpret_cast<const f4*>(q);
-                    frag[(4 * g + 0) * 4 + st] = v.x;
-                    frag[(4 * g + 1) * 4 + st] = v.y;
-                    frag[(4 * g + 2) * 4 + st] = v.z;
-                    frag[(4 * g + 3) * 4 + st] = v.w;
-                } else if constexpr (W == 2) {
-                    const float2 v = *reinterpret_cast<const float2*>(q);
-                    frag[(2 * g + 0) * 4 + st] = v.x;
-                    frag[(2 * g + 1) * 4 + st] = v.y;
+        for (int st = 0; st < 2; st++)
+#pragma unroll
+            for (int c = 0; c < CH; c++) {
+                if constexpr (KC) {
+                    // Rows base + 16 b + l16 all have the swizzle of row l16.
+                    off[st][c] = stage0 + st * stride + (base + l16) * BK +
+                                 4 * ((c * 4 + kq) ^ x_swz<BK / 4, true>(l16));
                 } else {
-                    frag[g * 4 + st] = q[0];
+                    off[st][c] = stage0 + st * stride + (c * 16 + 4 * kq) * ROWS + base +
+                                 XVec<F>::W * l16;
+                }
+            }
+    }
+    // stage and chunk are constants once the caller's loops are unrolled.
+    __device__ __forceinline__ void load(const float* __restrict__ lds, int stage, int chunk,
+                                         float (&frag)[F * 4]) const {
+        const float* s = lds + off[stage][chunk];
+        if constexpr (KC) {
+#pragma unroll
+            for (int b = 0; b < F; b++) {
+                const f4 v = *reinterpret_cast<const f4*>(s + 16 * b * BK);
+                frag[b * 4 + 0] = v.x;
+                frag[b * 4 + 1] = v.y;
+                frag[b * 4 + 2] = v.z;
+                frag[b * 4 + 3] = v.w;
+            }
+        } else {
+            constexpr int W = XVec<F>::W;
+#pragma unroll
+            for (int st = 0; st < 4; st++) {
+#pragma unroll
+                for (int g = 0; g < F / W; g++) {
+                    const float* q = s + st * ROWS + 16 * W * g;
+                    if constexpr (W == 4) {
+                        const f4 v = *reinterpret_cast<const f4*>(q);
+                        frag[(4 * g + 0) * 4 + st] = v.x;
+                        frag[(4 * g + 1) * 4 + st] = v.y;
+                        frag[(4 * g + 2) * 4 + st] = v.z;
+                        frag[(4 * g + 3) * 4 + st] = v.w;
+                    } else if constexpr (W == 2) {
+                        const float2 v = *reinterpret_cast<const float2*>(q);
+                        frag[(2 * g + 0) * 4 + st] = v.x;
+                        frag[(2 * g + 1) * 4 + st] = v.y;
+                    } else {
+                        frag[g * 4 + st] = q[0];
+                    }
                 }
             }
         }
     }
-}
+};
 
 // s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding).
 template <int N>
@@ -174,6 +225,62 @@ struct XReads {
     static constexpr int N = KC ? F : 4 * (F / XVec<F>::W);
 };
 
+// Fused epilogue of one 128-bit group of C at flat index idx, column col:
+// the operands (residual, aux, old C) are loaded first so a batch of groups
+// has its reads in flight together, then per element alpha, bias,
+// residual, aux (or act'(aux)), pre-activation store, activation, and store
+// or SGD update -- the order of gemm_epilogue_store, each one rounded f32
+// operation.
+template <bool EPI>
+__device__ __forceinline__ void x_epi_load(const GemmArgs& p, long long idx, f4& res, f4& mul,
+                                           f4& old) {
+    res = mul = old = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (EPI) {
+        if (p.residual) res = *reinterpret_cast<const f4*>(p.residual + idx);
+        if (p.aux) mul = *reinterpret_cast<const f4*>(p.aux + idx);
+        if (p.update) old = *reinterpret_cast<const f4*>(p.C + idx);
+    }
+}
+
+template <bool EPI>
+__device__ __forceinline__ void x_epi_store(const GemmArgs& p, f4 z, f4 res, f4 mul, f4 old,
+                                            int col, long long idx) {
+    float y[4] = {z.x, z.y, z.z, z.w};
+    if constexpr (EPI) {
+        if (p.alpha != 1.0f)
+#pragma unroll
+            for (int e = 0; e < 4; e++) y[e] = p.alpha * y[e];
+        if (p.bias) {
+            const f4 v = *reinterpret_cast<const f4*>(p.bias + col);
+            y[0] = y[0] + v.x; y[1] = y[1] + v.y; y[2] = y[2] + v.z; y[3] = y[3] + v.w;
+        }
+        if (p.residual) {
+            y[0] = y[0] + res.x; y[1] = y[1] + res.y; y[2] = y[2] + res.z; y[3] = y[3] + res.w;
+        }
+        if (p.aux) {
+            const float m[4] = {mul.x, mul.y, mul.z, mul.w};
+            if (p.aux_act) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) y[e] = y[e] * activate_derivative(p.aux_act, m[e]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) y[e] = y[e] * m[e];
+            }
+        }
+        if (p.pre_out) *reinterpret_cast<f4*>(p.pre_out + idx) = f4{y[0], y[1], y[2], y[3]};
+        if (p.act != ACT_IDENTITY)
+#pragma unroll
+            for (int e = 0; e < 4; e++) y[e] = activate(p.act, y[e]);
+        if (p.update) {
+            y[0] = old.x - p.update_scale * y[0];
+            y[1] = old.y - p.update_scale * y[1];
+            y[2] = old.z - p.update_scale * y[2];
+            y[3] = old.w - p.update_scale * y[3];
+        }
+    }
+    *reinterpret_cast<f4*>(p.C + idx) = f4{y[0], y[1], y[2], y[3]};
+}
+
 // KS = 2 splits K inside the workgroup: eight waves in two groups of four,
 // group g multiplying the g-th half of the slabs into its own accumulators
 // through its own two LDS stages.  The halves are added (first half +
@@ -201,9 +308,15 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     constexpr int DMA_PER_STAGE = SA::PER_WAVE + SB::PER_WAVE;
     static_assert(CH % 2 == 0, "slabs hold an even number of 16-wide chunks");
     // The two slab stages of each K group, reused by the epilogue for each
-    // wave's TM x TN sub-tile of C (row pitch CP).
+    // wave's TM x TN sub-tile of C (row pitch CP).  A sub-tile too large for
+    // LDS (128 x 128 per wave) goes out in EP passes of TM / EP rows; its
+    // accumulator blocks must then be row-contiguous (k-contiguous A).
     constexpr int CP = TN + 4;
-    constexpr int SMEM = KS * 2 * STAGE > KS * 4 * TM * CP ? KS * 2 * STAGE : KS * 4 * TM * CP;
+    constexpr int EP = KS * 4 * TM * CP * 4 > 160 * 1024 ? 2 : 1;
+    static_assert(EP == 1 || (KS == 1 && A_KC && FM % EP == 0), "multi-pass epilogue shape");
+    constexpr int EPI_ELEMS = KS * 4 * (TM / EP) * CP;
+    constexpr int SMEM = KS * 2 * STAGE > EPI_ELEMS ? KS * 2 * STAGE : EPI_ELEMS;
+    static_assert(SMEM * 4 <= 160 * 1024, "LDS budget");
     __shared__ __attribute__((aligned(1024))) float smem_all[SMEM];
 
     const int num_m = p.M / BM, num_n = p.N / BN;
@@ -212,8 +325,9 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     const int m0 = tm * BM, n0 = tn * BN;
 
     const int lane = threadIdx.x & 63;
-    const int kg = KS == 1 ? 0 : (int)(threadIdx.x >> 8);  // K group
-    const int wave = (threadIdx.x >> 6) & 3;                // wave within the group
+    // K group and wave within the group, wave-uniform (scalar registers).
+    const int kg = KS == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8));
+    const int wave = __builtin_amdgcn_readfirstlane((int)((threadIdx.x >> 6) & 3));
     const int wm = wave >> 1, wn = wave & 1;
     const int l16 = lane & 15, kq = lane >> 4;
     float* const smem = smem_all + kg * (2 * STAGE);
@@ -236,16 +350,23 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     const int a_off = wm * TM, b_off = wn * TN;
     float fa[2][FM * 4], fb[2][FN * 4];
 
+    XDma<A_ROWS, A_COLS, A_KC> dma_a;
+    XDma<B_ROWS, B_COLS, B_KC> dma_b;
+    dma_a.init(p.lda, wave, lane);
+    dma_b.init(p.ldb, wave, lane);
+    XFrag<A_KC, A_KC ? BK : BM, BK, FM> rd_a;
+    XFrag<B_KC, B_KC ? BK : BN, BK, FN> rd_b;
+    rd_a.init(kg * (2 * STAGE), STAGE, a_off, l16, kq);
+    rd_b.init(kg * (2 * STAGE) + A_ELEMS, STAGE, b_off, l16, kq);
+
     auto issue = [&](int k_slab, int stage) {
         float* d = smem + stage * STAGE;
-        x_dma_slab<A_ROWS, A_COLS, A_KC>(d, a_base + k_slab * a_kstride, p.lda, wave, lane);
-        x_dma_slab<B_ROWS, B_COLS, B_KC>(d + A_ELEMS, b_base + k_slab * b_kstride, p.ldb, wave,
-                                         lane);
+        dma_a.load(d, a_base + k_slab * a_kstride, p.lda, wave);
+        dma_b.load(d + A_ELEMS, b_base + k_slab * b_kstride, p.ldb, wave);
     };
-    auto frags = [&](const float* st, int chunk, int slot) {
-        x_load_frag_dma<A_KC, A_KC ? BK : BM, BK, FM>(st, a_off, chunk, l16, kq, fa[slot]);
-        x_load_frag_dma<B_KC, B_KC ? BK : BN, BK, FN>(st + A_ELEMS, b_off, chunk, l16, kq,
-                                                      fb[slot]);
+    auto frags = [&](int stage, int chunk, int slot) {
+        rd_a.load(smem_all, stage, chunk, fa[slot]);
+        rd_b.load(smem_all, stage, chunk, fb[slot]);
     };
     auto mfmas = [&](int slot, int st0, int st1) {
 #pragma unroll
@@ -273,22 +394,24 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
         } else {
             x_barrier<0>();
         }
-        frags(smem, 0, 0);
+        frags(0, 0, 0);
     }
 
-    // Slab kt lives in stage kt % 2.  Its last chunk is split: after the
-    // first half of its MFMAs every wave has finished reading the stage
-    // (the operands are in registers), so after one barrier the next slab's
-    // first operands are read and the slab after next is loaded into this
-    // stage while the second half of the MFMAs runs.  Every path through
-    // the loop body is the same instruction stream (no branches), which
-    // keeps the accumulators in place; the load issued in the last
-    // iteration repeats slab KT - 1 into the stage that is no longer read.
+    // Slab kt lives in stage kt % 2; the loop handles two slabs per
+    // iteration so that every stage (and so every LDS address offset) is a
+    // constant.  A slab's last chunk is split: after the first half of its
+    // MFMAs every wave has finished reading the stage (the operands are in
+    // registers), so after one barrier the next slab's first operands are
+    // read and the slab after next is loaded into this stage while the
+    // second half of the MFMAs runs.  The loop body is the same instruction
+    // stream in every iteration (no branches), which keeps the
+    // accumulators in place; a load past the last slab repeats slab KT - 1
+    // into the stage that is no longer read.
     constexpr int LAST = (CH - 1) & 1;
-    auto early_chunks = [&](const float* sa) {
+    auto early_chunks = [&](int stage) {
 #pragma unroll
         for (int c = 0; c + 1 < CH; c++) {
-            frags(sa, c + 1, (c + 1) & 1);
+            frags(stage, c + 1, (c + 1) & 1);
             mfmas(c & 1, 0, 4);
 #pragma unroll
             for (int r = 0; r < NREAD; r++) {
@@ -299,31 +422,45 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    for (int kt = 0; kt + 1 < KT; kt++) {
-        early_chunks(smem + (kt & 1) * STAGE);
+    // One slab that has a successor; issue_next: load slab kt + 2 (else no
+    // load is left to issue).
+    auto body = [&](int kt, int stage, bool issue_next) {
+        early_chunks(stage);
         mfmas(LAST, 0, 2);
         __builtin_amdgcn_sched_barrier(0);
         // Slab kt + 1 was loaded one stage ago and is the only load in
         // flight; after the barrier no wave has an LDS read of slab kt
         // outstanding.
         x_barrier_all();
-        frags(smem + ((kt + 1) & 1) * STAGE, 0, 0);
-        issue(min(kt + 2, KT - 1), kt & 1);
+        frags(stage ^ 1, 0, 0);
+        if (issue_next) issue(min(kt + 2, KT - 1), stage);
         mfmas(LAST, 2, 4);
 #pragma unroll
         for (int r = 0; r < NREAD; r++) {
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         }
+        if (issue_next) {
 #pragma unroll
-        for (int r = 0; r < NDMA; r++) {
-            __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);  // one slab load
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            for (int r = 0; r < NDMA; r++) {
+                __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);  // one slab load
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
+    };
+    int kt = 0;
+    for (; kt + 2 < KT; kt += 2) {
+        body(kt, 0, true);
+        body(kt + 1, 1, true);
     }
-    if (KT > 0) {
-        early_chunks(smem + ((KT - 1) & 1) * STAGE);
+    // The last one or two slabs.
+    if (KT - kt == 2) {
+        body(kt, 0, false);
+        early_chunks(1);
+        mfmas(LAST, 0, 4);
+    } else if (KT - kt == 1) {
+        early_chunks(0);
         mfmas(LAST, 0, 4);
     }
     // No slab load may still be writing LDS when the workgroup ends.
@@ -339,110 +476,75 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     // and each group then finishes half of its rows, adding the groups'
     // values in group order.
     __syncthreads();  // every wave is done with the slab stages
-    float* cw = smem_all + (kg * 4 + wave) * (TM * CP);
-    if constexpr (!B_KC && XVec<FN>::W == 4) {
+    constexpr int PR = TM / EP;  // sub-tile rows per pass
+    float* cw = smem_all + (kg * 4 + wave) * (PR * CP);
+    const float* c0 = smem_all + wave * (PR * CP);  // group 0's copy of the sub-tile
 #pragma unroll
-        for (int i = 0; i < FM; i++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int rr = x_index<A_KC, FM>(0, i, 4 * kq + r);
-#pragma unroll
-                for (int g = 0; g < FN / 4; g++) {
-                    const f4 v = {acc[i][4 * g + 0][r], acc[i][4 * g + 1][r],
-                                  acc[i][4 * g + 2][r], acc[i][4 * g + 3][r]};
-                    *reinterpret_cast<f4*>(cw + rr * CP + 64 * g + 4 * l16) = v;
-                }
-            }
-    } else {
-#pragma unroll
-        for (int i = 0; i < FM; i++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int rr = x_index<A_KC, FM>(0, i, 4 * kq + r);
-#pragma unroll
-                for (int j = 0; j < FN; j++)
-                    cw[rr * CP + x_index<B_KC, FN>(0, j, l16)] = acc[i][j][r];
-            }
-    }
-    if constexpr (KS == 2) __syncthreads();  // both groups' halves written
-    const float* c0 = smem_all + wave * (TM * CP);  // group 0's copy of the sub-tile
-    const int row0 = m0 + a_off, col0 = n0 + b_off;
-    constexpr int F4_ROW = TN / 4;
-    constexpr int ROWS = TM / KS;  // sub-tile rows this wave finishes
-    const int rbase = kg * ROWS;
-    constexpr int ITER = ROWS * F4_ROW / 64;  // 128-bit groups per lane
-    constexpr int NB = ITER < 4 ? ITER : 4;  // groups whose operands load together
-    static_assert(ITER % NB == 0, "epilogue batches");
-    const f4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 1
-    for (int b0 = 0; b0 < ITER; b0 += NB) {
-        // Loads of a batch first, so NB global reads per operand are in
-        // flight together.
-        f4 z[NB], res[NB], mul[NB], old[NB];
-        long long idx[NB];
-        int col[NB];
-#pragma unroll
-        for (int u = 0; u < NB; u++) {
-            const int q = lane + 64 * (b0 + u);
-            const int rr = rbase + q / F4_ROW, c4 = q % F4_ROW;
-            z[u] = *reinterpret_cast<const f4*>(c0 + rr * CP + 4 * c4);
-            if constexpr (KS == 2) {
-                const f4 h = *reinterpret_cast<const f4*>(c0 + 4 * TM * CP + rr * CP + 4 * c4);
-                z[u] = f4{z[u].x + h.x, z[u].y + h.y, z[u].z + h.z, z[u].w + h.w};
-            }
-            col[u] = col0 + 4 * c4;
-            idx[u] = (long long)(row0 + rr) * p.ldc + col[u];
-            res[u] = mul[u] = old[u] = zero;
-            if constexpr (EPI) {
-                if (p.residual) res[u] = *reinterpret_cast<const f4*>(p.residual + idx[u]);
-                if (p.aux) mul[u] = *reinterpret_cast<const f4*>(p.aux + idx[u]);
-                if (p.update) old[u] = *reinterpret_cast<const f4*>(p.C + idx[u]);
-            }
+    for (int pass = 0; pass < EP; pass++) {
+        if (pass > 0) {
+            // The wave's reads of the previous pass precede its writes of this
+            // one: LDS executes one wave's accesses in order, and the empty asm
+            // keeps the compiler from moving them.
+            asm volatile("" ::: "memory");
         }
+        if constexpr (!B_KC && XVec<FN>::W == 4) {
 #pragma unroll
-        for (int u = 0; u < NB; u++) {
-            float y[4] = {z[u].x, z[u].y, z[u].z, z[u].w};
-            if constexpr (EPI) {
-                // Per element: alpha, bias, residual, aux (or act'(aux)),
-                // pre-activation store, activation, store or SGD update --
-                // the order of gemm_epilogue_store, each one rounded f32
-                // operation.
-                if (p.alpha != 1.0f)
+            for (int i = pass * (FM / EP); i < (pass + 1) * (FM / EP); i++)
 #pragma unroll
-                    for (int e = 0; e < 4; e++) y[e] = p.alpha * y[e];
-                if (p.bias) {
-                    const f4 v = *reinterpret_cast<const f4*>(p.bias + col[u]);
-                    y[0] = y[0] + v.x; y[1] = y[1] + v.y; y[2] = y[2] + v.z; y[3] = y[3] + v.w;
-                }
-                if (p.residual) {
-                    y[0] = y[0] + res[u].x; y[1] = y[1] + res[u].y;
-                    y[2] = y[2] + res[u].z; y[3] = y[3] + res[u].w;
-                }
-                if (p.aux) {
-                    const float m[4] = {mul[u].x, mul[u].y, mul[u].z, mul[u].w};
-                    if (p.aux_act) {
+                for (int r = 0; r < 4; r++) {
+                    const int rr = x_index<A_KC, FM>(0, i, 4 * kq + r) - pass * PR;
 #pragma unroll
-                        for (int e = 0; e < 4; e++) y[e] = y[e] * activate_derivative(p.aux_act, m[e]);
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 4; e++) y[e] = y[e] * m[e];
+                    for (int g = 0; g < FN / 4; g++) {
+                        const f4 v = {acc[i][4 * g + 0][r], acc[i][4 * g + 1][r],
+                                      acc[i][4 * g + 2][r], acc[i][4 * g + 3][r]};
+                        *reinterpret_cast<f4*>(cw + rr * CP + 64 * g + 4 * l16) = v;
                     }
                 }
-                if (p.pre_out)
-                    *reinterpret_cast<f4*>(p.pre_out + idx[u]) = f4{y[0], y[1], y[2], y[3]};
-                if (p.act != ACT_IDENTITY)
+        } else {
 #pragma unroll
-                    for (int e = 0; e < 4; e++) y[e] = activate(p.act, y[e]);
-                if (p.update) {
-                    y[0] = old[u].x - p.update_scale * y[0];
-                    y[1] = old[u].y - p.update_scale * y[1];
-                    y[2] = old[u].z - p.update_scale * y[2];
-                    y[3] = old[u].w - p.update_scale * y[3];
+            for (int i = pass * (FM / EP); i < (pass + 1) * (FM / EP); i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int rr = x_index<A_KC, FM>(0, i, 4 * kq + r) - pass * PR;
+#pragma unroll
+                    for (int j = 0; j < FN; j++)
+                        cw[rr * CP + x_index<B_KC, FN>(0, j, l16)] = acc[i][j][r];
                 }
-            }
-            *reinterpret_cast<f4*>(p.C + idx[u]) = f4{y[0], y[1], y[2], y[3]};
         }
-    }
+        if constexpr (KS == 2) __syncthreads();  // both groups' halves written
+        asm volatile("" ::: "memory");
+        const int row0 = m0 + a_off + pass * PR, col0 = n0 + b_off;
+        constexpr int F4_ROW = TN / 4;
+        constexpr int ROWS = PR / KS;  // sub-tile rows this wave finishes
+        const int rbase = kg * ROWS;
+        constexpr int ITER = ROWS * F4_ROW / 64;  // 128-bit groups per lane
+        constexpr int NB = ITER < 4 ? ITER : 4;  // groups whose operands load together
+        static_assert(ITER % NB == 0, "epilogue batches");
+#pragma unroll 1
+        for (int b0 = 0; b0 < ITER; b0 += NB) {
+            // Loads of a batch first, so NB global reads per operand are in
+            // flight together.
+            f4 z[NB], res[NB], mul[NB], old[NB];
+            long long idx[NB];
+            int col[NB];
+#pragma unroll
+            for (int u = 0; u < NB; u++) {
+                const int q = lane + 64 * (b0 + u);
+                const int rr = rbase + q / F4_ROW, c4 = q % F4_ROW;
+                z[u] = *reinterpret_cast<const f4*>(c0 + rr * CP + 4 * c4);
+                if constexpr (KS == 2) {
+                    const f4 h = *reinterpret_cast<const f4*>(c0 + 4 * PR * CP + rr * CP + 4 * c4);
+                    z[u] = f4{z[u].x + h.x, z[u].y + h.y, z[u].z + h.z, z[u].w + h.w};
+                }
+                col[u] = col0 + 4 * c4;
+                idx[u] = (long long)(row0 + rr) * p.ldc + col[u];
+                x_epi_load<EPI>(p, idx[u], res[u], mul[u], old[u]);
+            }
+#pragma unroll
+            for (int u = 0; u < NB; u++)
+                x_epi_store<EPI>(p, z[u], res[u], mul[u], old[u], col[u], idx[u]);
+        }
+    }  // pass
 }
 
 template <int BM, int BN, int BK, int KS, bool TA, bool TB, bool EPI>

@@ -17,8 +17,11 @@ using namespace forge;
 //   tile <BM>x<BN>x<BK>_x: the unguarded four-wave kernel (gemm_x.hpp);
 //   tile 64x64x16_2x2_g: the bounds-guarded kernel for any shape and
 //   alignment (gemm.hpp); _e: fused epilogue.
+// Tiles up to 128 x 128 with 32-wide slabs leave LDS for two workgroups per
+// CU; their registers are held to what two waves per SIMD allow.
+#define GEMM_X_OCC(BM, BN, BK) ((BM) * (BN) <= 128 * 128 && ((BM) + (BN)) * (BK) <= 256 * 32 ? 2 : 1)
 #define GEMM_X_KERNEL(NAME, BM, BN, BK, TA, TB, EPI)                          \
-    FORGE_KERNEL void __launch_bounds__(256) NAME(GemmArgs p) {               \
+    FORGE_KERNEL void __launch_bounds__(256, GEMM_X_OCC(BM, BN, BK)) NAME(GemmArgs p) { \
         gemm_single_x<BM, BN, BK, 1, TA, TB, EPI>(p);                          \
     }
 // The same with K split over two wave groups (tile tag ..._k2_x).
@@ -51,7 +54,7 @@ GEMM_FAMILY(tt, true, true)
 // products per launch, each with its own operands and epilogue.  They serve
 // the Q/K/V projections and the K slices of split-K products.
 #define GEMM_BATCH_KERNEL(NAME, BM, BN, BK, TA, TB)                                    \
-    FORGE_KERNEL void __launch_bounds__(256) NAME(GemmBatchArgs b) {                 \
+    FORGE_KERNEL void __launch_bounds__(256, GEMM_X_OCC(BM, BN, BK)) NAME(GemmBatchArgs b) { \
         gemm_batch_x<BM, BN, BK, TA, TB>(b);                                         \
     }
 #define GEMM_BATCH_FAMILY(AB, TA, TB)                                                   \

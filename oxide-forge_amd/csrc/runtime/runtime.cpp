@@ -113,6 +113,7 @@ struct forge_runtime {
     forge_stream primary;
     hipModule_t module = nullptr;
     std::unordered_map<std::string, hipFunction_t> functions;
+    std::unordered_map<std::string, int> occupancy;  // GEMM kernels: workgroups per CU
     std::unordered_map<size_t, std::vector<float*>> pool;
     std::vector<forge_stream*> streams;
     int cu_count = 0;
@@ -547,6 +548,11 @@ struct GemmConfig {
     int ks = 1;       // K groups inside the workgroup (K % (bk * ks) == 0)
 };
 
+const char* gemm_ab(int ta, int tb) {
+    static const char ab[2][2][3] = {{"nn", "nt"}, {"tn", "tt"}};
+    return ab[ta ? 1 : 0][tb ? 1 : 0];
+}
+
 const GemmConfig kTile128x256 = {"128x256x32_x", 128, 256, 32, 256};
 const GemmConfig kTile128x128 = {"128x128x32_x", 128, 128, 32, 256};
 const GemmConfig kTile128x64 = {"128x64x32_x", 128, 64, 32, 256};
@@ -554,63 +560,79 @@ const GemmConfig kTile64x128 = {"64x128x32_x", 64, 128, 32, 256};
 const GemmConfig kTile64x64 = {"64x64x32_x", 64, 64, 32, 256};
 const GemmConfig kGuard64 = {"64x64x16_2x2_g", 64, 64, 16, 256};
 // Eight-wave variants with K split over two wave groups (fused epilogue and
-// plain NN instances; no batched ones).
+// plain NN instances; no batched ones).  Reached through the tile-forcing
+// entry points only.
 const GemmConfig kTile128x64k2 = {"128x64x32_k2_x", 128, 64, 32, 512, 2};
 const GemmConfig kTile64x128k2 = {"64x128x32_k2_x", 64, 128, 32, 512, 2};
 
-// Unguarded tiles, largest first, and their measured full-device
-// efficiency relative to 128x256 (4096^3 on MI355X: 140.6, 138.5, 134.7,
-// 133.8 and 121 TFLOP/s).  All but 128x256 have fused-epilogue and batched
-// instances; 128x256 has a plain one.
+// Unguarded tiles, largest first, and their measured efficiency relative to
+// the best (4096^3 plain on MI355X: 146.4, 150.7, 151.3, 151.6 and 149.6
+// TFLOP/s).  All but 128x256 have fused-epilogue and batched instances;
+// 128x256 has a plain NN one.
 const GemmConfig* const kUnguarded[] = {&kTile128x256, &kTile128x128, &kTile128x64,
                                         &kTile64x128, &kTile64x64};
-const double kTileEfficiency[] = {1.0, 0.985, 0.958, 0.951, 0.86};
+const double kTileEfficiency[] = {0.966, 0.994, 0.998, 1.0, 0.987};
 
-// Tile choice: the best efficiency x balance, where t tiles occupy
-// ceil(t / CUs) rounds and the balance is t / (CUs * ceil(t / CUs)); ties go
-// to the larger tile.  128x256 (one workgroup per CU) serves plain products
-// only: with a fused epilogue, 128x128 (two workgroups per CU, so one
-// workgroup's epilogue overlaps the other's MFMAs) is as fast or faster
-// (2048x4096x1024 + bias + GELU: 140.9 against 146.8 us).  One refinement:
-// when 128x128 would leave at most one tile per CU, 64x128 (two tiles per
-// CU) is taken instead -- on the 2048x2048x1024 attention scores 124.9
-// against 121.1 TFLOP/s.  Results: plain 4096^3, 8192x1024 and 2048x4096
-// -> 128x256; fused C5 products -> 128x128; 2048x2048 -> 64x128; 2048x1024
-// -> 128x64 (the three Q/K/V products of one batch: 768 tiles).  Unaligned
-// shapes and shapes the tiles do not divide take the bounds-guarded 64x64
-// tile.  `count` same-shape products share the launch.
-const GemmConfig& choose_gemm(forge_runtime* rt, size_t M, size_t N, size_t K, bool aligned,
-                              bool epilogue, size_t count = 1, bool allow_k2 = false) {
+enum class GemmKind { Plain, Epilogue, Batch };
+
+// Kernel that runs a tile: plain NN (forge_gemm_nn_<tile>), fused epilogue
+// (forge_gemm_<ab>_<tile>_e) or batched (forge_gemm_batch_<ab>_<tile>).
+void gemm_kernel_name(char* out, size_t cap, GemmKind kind, int ta, int tb,
+                      const GemmConfig& cfg) {
+    if (kind == GemmKind::Batch)
+        snprintf(out, cap, "forge_gemm_batch_%s_%s", gemm_ab(ta, tb), cfg.tag);
+    else
+        snprintf(out, cap, "forge_gemm_%s_%s%s", gemm_ab(ta, tb), cfg.tag,
+                 kind == GemmKind::Epilogue ? "_e" : "");
+}
+
+// Workgroups of a kernel that one CU holds at once (its registers and LDS),
+// from the loaded code object; cached per kernel.
+int gemm_occupancy(forge_runtime* rt, const char* name, int threads) {
+    auto it = rt->occupancy.find(name);
+    if (it != rt->occupancy.end()) return it->second;
+    int blocks = 1;
+    hipFunction_t f = nullptr;
+    if (get_function(rt, name, &f) == FORGE_OK &&
+        hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, f, threads, 0) != hipSuccess)
+        blocks = 1;
+    blocks = blocks < 1 ? 1 : blocks;
+    rt->occupancy.emplace(name, blocks);
+    return blocks;
+}
+
+// Tile choice: the best efficiency x balance; ties go to the larger tile.
+// With occ workgroups of a tile resident per CU, t tiles that all fit at
+// once (t <= CUs * occ) spread over the CUs, balance t / (CUs * ceil(t /
+// CUs)); more than that run in waves of CUs * occ, balance t / (CUs * occ *
+// ceil(t / (CUs * occ))).  (2048 tiles of 128x64, three per CU: 151.3
+// TFLOP/s; 1024 of them: 121, where 128x128, two per CU, gives 148.)
+// Results: 4096^3, 8192x1024, the 2048x4096 FFN and the C5 products ->
+// 128x128; 2048x2048 (attention scores) and 2048x1024 products -> 64x128.
+// Unaligned shapes and shapes the tiles do not divide take the
+// bounds-guarded 64x64 tile.  `count` same-shape products share the launch
+// (kind Batch).
+const GemmConfig& choose_gemm(forge_runtime* rt, int ta, int tb, size_t M, size_t N, size_t K,
+                              bool aligned, GemmKind kind, size_t count = 1) {
     const size_t cus = rt->cu_count > 0 ? (size_t)rt->cu_count : 256;
     const GemmConfig* best = &kGuard64;
     double best_score = 0.0;
-    size_t best_tiles = 0;
-    auto fits = [&](const GemmConfig& g) {
-        return aligned && M % g.bm == 0 && N % g.bn == 0 && K % ((size_t)g.bk * g.ks) == 0;
-    };
-    for (int i = epilogue ? 1 : 0; i < 5; i++) {
+    const bool plain_nn = kind == GemmKind::Plain && !ta && !tb;
+    for (int i = plain_nn ? 0 : 1; i < 5; i++) {
         const GemmConfig& g = *kUnguarded[i];
-        if (!fits(g)) continue;
+        if (!aligned || M % g.bm || N % g.bn || K % ((size_t)g.bk * g.ks)) continue;
+        char name[96];
+        gemm_kernel_name(name, sizeof name, kind, ta, tb, g);
+        const size_t slots = cus * (size_t)gemm_occupancy(rt, name, g.threads);
         const size_t t = count * (M / g.bm) * (N / g.bn);
-        const size_t rounds = (t + cus - 1) / cus;
-        const double score = kTileEfficiency[i] * (double)t / (double)(cus * rounds);
+        const double balance =
+            t <= slots ? (double)t / (double)(cus * ((t + cus - 1) / cus))
+                       : (double)t / (double)(slots * ((t + slots - 1) / slots));
+        const double score = kTileEfficiency[i] * balance;
         if (score > best_score + 1e-9) {
             best = kUnguarded[i];
             best_score = score;
-            best_tiles = t;
         }
-    }
-    if (best == &kTile128x128 && best_tiles <= cus && fits(kTile64x128)) {
-        best = &kTile64x128;
-        best_tiles *= 2;
-    }
-    // One 128x64 or 64x128 tile per CU: split K over two wave groups instead
-    // (two waves per SIMD).  2048x1024x{1024,2048,4096} + bias: 111.1,
-    // 121.2 and 126.2 TFLOP/s against 103.0, 113.0 and 117.7.  Not for
-    // batched launches (no such instance) or products the caller splits in K.
-    if (allow_k2 && best_tiles <= cus && (best == &kTile128x64 || best == &kTile64x128)) {
-        if (fits(kTile64x128k2)) best = &kTile64x128k2;
-        else if (fits(kTile128x64k2)) best = &kTile128x64k2;
     }
     return *best;
 }
@@ -622,12 +644,11 @@ const GemmConfig& choose_gemm(forge_runtime* rt, size_t M, size_t N, size_t K, b
 // slices are doubled while the launch still fits on the CUs and each slice
 // keeps >= 1024 of K (up to eight).  Returns the split count and sets *cfg
 // to the tile to use.
-int choose_splits(forge_runtime* rt, size_t M, size_t N, size_t K, bool aligned,
+int choose_splits(forge_runtime* rt, int ta, int tb, size_t M, size_t N, size_t K, bool aligned,
                   const GemmConfig** cfg) {
     const size_t cus = rt->cu_count > 0 ? (size_t)rt->cu_count : 256;
-    // The K slices run as one batched launch, whose instances all fuse the
-    // epilogue.
-    const GemmConfig& g = choose_gemm(rt, M, N, K, aligned, true);
+    // The K slices run as one batched launch.
+    const GemmConfig& g = choose_gemm(rt, ta, tb, M, N, K, aligned, GemmKind::Batch);
     if (&g == &kGuard64) return 1;
     const size_t t = (M / g.bm) * (N / g.bn);
     if (t * 4 > cus) return 1;
@@ -639,10 +660,7 @@ int choose_splits(forge_runtime* rt, size_t M, size_t N, size_t K, bool aligned,
     return splits;
 }
 
-const char* gemm_ab(int ta, int tb) {
-    static const char ab[2][2][3] = {{"nn", "nt"}, {"tn", "tt"}};
-    return ab[ta ? 1 : 0][tb ? 1 : 0];
-}
+constexpr long long kUnguardedMaxPitch = 1LL << 21;
 
 // Validates one product and fills its kernel arguments; *aligned reports
 // whether the unguarded tiles may read the operands.
@@ -665,8 +683,10 @@ forge_status gemm_args(int ta, int tb, forge_slice A, forge_slice B, forge_slice
     a.ldb = tb ? (long long)K : (long long)N;
     a.ldc = (long long)N;
     a.alpha = 1.0f;
+    // The unguarded tiles also keep their slab offsets (up to 256 rows of
+    // an operand) below 2^31 bytes: row pitches up to 2^21 floats.
     bool al = aligned16(A.ptr) && aligned16(B.ptr) && aligned16(C.ptr) && a.lda % 4 == 0 &&
-              a.ldb % 4 == 0;
+              a.ldb % 4 == 0 && a.lda <= kUnguardedMaxPitch && a.ldb <= kUnguardedMaxPitch;
     if (ep) {
         FORGE_TRY(need_opt(ep->bias, N, "gemm bias"));
         FORGE_TRY(need_opt(ep->residual, M * N, "gemm residual"));
@@ -746,13 +766,12 @@ forge_status gemm_dispatch(forge_runtime* rt, forge_stream* s, int ta, int tb, f
     FORGE_TRY(gemm_args(ta, tb, A, B, C, M, N, K, ep, &a, &aligned));
     if (M == 0 || N == 0) return FORGE_OK;
     const GemmConfig* split_cfg = nullptr;
-    const int splits = choose_splits(rt, M, N, K, aligned, &split_cfg);
+    const int splits = choose_splits(rt, ta, tb, M, N, K, aligned, &split_cfg);
     if (splits > 1) return gemm_split_launch(rt, s, ta, tb, a, *split_cfg, splits);
-    const bool epi = !(plain_name && !ta && !tb);
-    const GemmConfig& cfg = choose_gemm(rt, M, N, K, aligned, epi, 1, true);
+    const GemmKind kind = plain_name && !ta && !tb ? GemmKind::Plain : GemmKind::Epilogue;
+    const GemmConfig& cfg = choose_gemm(rt, ta, tb, M, N, K, aligned, kind);
     char name[96];
-    snprintf(name, sizeof name, "forge_gemm_%s_%s%s", gemm_ab(ta, tb), cfg.tag,
-             epi ? "_e" : "");
+    gemm_kernel_name(name, sizeof name, kind, ta, tb, cfg);
     unsigned tiles = (unsigned)(((M + cfg.bm - 1) / cfg.bm) * ((N + cfg.bn - 1) / cfg.bn));
     void* args[] = {&a};
     return launch(rt, s, name, dim3(tiles), dim3(cfg.threads), 0, args);
@@ -964,7 +983,8 @@ extern "C" forge_status forge_gemm_f32_tile(forge_runtime* rt, forge_stream* s,
     FORGE_TRY(need(B, K * N, "gemm B"));
     FORGE_TRY(need(C, M * N, "gemm C"));
     if (!guarded && (M % bm || N % bn || K % (bk * ks) || !aligned16(A.ptr) ||
-                     !aligned16(B.ptr) || !aligned16(C.ptr) || K % 4 || N % 4))
+                     !aligned16(B.ptr) || !aligned16(C.ptr) || K % 4 || N % 4 ||
+                     (long long)K > kUnguardedMaxPitch || (long long)N > kUnguardedMaxPitch))
         return fail(FORGE_EINVAL, "shape %zux%zux%zu does not fit unguarded tile %s", M, N, K,
                     tile_tag);
     if (M == 0 || N == 0) return FORGE_OK;
@@ -1035,6 +1055,34 @@ extern "C" forge_status forge_gemm_ex_f32_tile(forge_runtime* rt, forge_stream* 
     return launch(rt, s, name, dim3(tiles), dim3(cfg->threads), 0, args);
 }
 
+extern "C" forge_status forge_gemm_kernel_name(forge_runtime* rt, int trans_a, int trans_b,
+                                               size_t M, size_t N, size_t K, int fused,
+                                               char* name, size_t cap) {
+    if (!rt || !name || cap == 0) return fail(FORGE_EINVAL, "null argument");
+    if (!fits_int(M) || !fits_int(N) || !fits_int(K))
+        return fail(FORGE_EINVAL, "gemm dimensions exceed 2^31-1");
+    const int ta = trans_a ? 1 : 0, tb = trans_b ? 1 : 0;
+    const long long lda = ta ? (long long)M : (long long)K;
+    const long long ldb = tb ? (long long)K : (long long)N;
+    const bool aligned = lda % 4 == 0 && ldb % 4 == 0 && lda <= kUnguardedMaxPitch &&
+                         ldb <= kUnguardedMaxPitch;
+    const GemmConfig* split_cfg = nullptr;
+    const int splits = choose_splits(rt, ta, tb, M, N, K, aligned, &split_cfg);
+    char kernel[96];
+    int n = 0;
+    if (splits > 1) {
+        gemm_kernel_name(kernel, sizeof kernel, GemmKind::Batch, ta, tb, *split_cfg);
+        n = snprintf(name, cap, "%s/split%d", kernel, splits);
+    } else {
+        const GemmKind kind = !fused && !ta && !tb ? GemmKind::Plain : GemmKind::Epilogue;
+        gemm_kernel_name(kernel, sizeof kernel, kind, ta, tb,
+                         choose_gemm(rt, ta, tb, M, N, K, aligned, kind));
+        n = snprintf(name, cap, "%s", kernel);
+    }
+    if (n < 0 || (size_t)n >= cap) return fail(FORGE_EINVAL, "name buffer of %zu bytes too small", cap);
+    return FORGE_OK;
+}
+
 extern "C" forge_status forge_gemm_batch_f32(forge_runtime* rt, forge_stream* s, int trans_a,
                                              int trans_b, size_t M, size_t N, size_t K,
                                              size_t count, const forge_gemm_problem* problems) {
@@ -1058,13 +1106,12 @@ extern "C" forge_status forge_gemm_batch_f32(forge_runtime* rt, forge_stream* s,
         if (z < (size_t)GEMM_BATCH_MAX) b.p[z] = a;
     }
     if (count == 0 || M == 0 || N == 0) return FORGE_OK;
-    const GemmConfig& cfg = choose_gemm(rt, M, N, K, all_aligned, true, count);
+    const GemmConfig& cfg =
+        choose_gemm(rt, trans_a, trans_b, M, N, K, all_aligned, GemmKind::Batch, count);
     const GemmConfig* split_cfg = nullptr;
-    // Shapes the single-product path splits in K (into slices, or over two
-    // wave groups) are dispatched one by one, so every product equals its
-    // forge_gemm_ex_f32 result bit for bit.
-    const bool split = choose_splits(rt, M, N, K, all_aligned, &split_cfg) > 1 ||
-                       choose_gemm(rt, M, N, K, all_aligned, true, 1, true).ks > 1;
+    // Shapes the single-product path splits in K are dispatched one by one,
+    // so every product equals its forge_gemm_ex_f32 result bit for bit.
+    const bool split = choose_splits(rt, trans_a, trans_b, M, N, K, all_aligned, &split_cfg) > 1;
     if (count > (size_t)GEMM_BATCH_MAX || &cfg == &kGuard64 || split) {
         for (size_t z = 0; z < count; z++)
             FORGE_TRY(gemm_dispatch(rt, s, trans_a, trans_b, problems[z].A, problems[z].B,
@@ -1074,7 +1121,7 @@ extern "C" forge_status forge_gemm_batch_f32(forge_runtime* rt, forge_stream* s,
     b.count = (int)count;
     b.tiles = (int)((M / cfg.bm) * (N / cfg.bn));
     char name[96];
-    snprintf(name, sizeof name, "forge_gemm_batch_%s_%s", gemm_ab(trans_a, trans_b), cfg.tag);
+    gemm_kernel_name(name, sizeof name, GemmKind::Batch, trans_a, trans_b, cfg);
     void* args[] = {&b};
     return launch(rt, s, name, dim3((unsigned)(b.tiles * count)), dim3(cfg.threads), 0, args);
 }

@@ -223,6 +223,19 @@ class Runtime:
         call("forge_gemm_batch_f32", self.handle, stream, int(trans_a), int(trans_b), M, N, K,
              len(problems), arr)
 
+    def gemm_tile(self, tile, A, B, C, M, N, K, stream=None) -> None:
+        """forge_gemm_f32 through one named plain tile instance (tuning)."""
+        call("forge_gemm_f32_tile", self.handle, stream, tile.encode(), A.slice, B.slice,
+             C.slice, M, N, K)
+
+    def gemm_kernel_name(self, M, N, K, trans_a=False, trans_b=False, fused=False) -> str:
+        """Kernel gemm (fused=False) or gemm_ex (fused=True) launches for this
+        shape with aligned operands ("<kernel>/split<N>" when split in K)."""
+        buf = ctypes.create_string_buffer(128)
+        call("forge_gemm_kernel_name", self.handle, int(trans_a), int(trans_b), M, N, K,
+             int(fused), buf, len(buf))
+        return buf.value.decode()
+
     def gemm_ex_tile(self, tile, A, B, C, M, N, K, trans_a=False, trans_b=False, stream=None,
                      **epilogue) -> None:
         """forge_gemm_ex_f32 through one named tile instance (testing)."""

@@ -113,6 +113,8 @@ SIGNATURES = {
                              c_size_t],
     "forge_gemm_ex_f32_tile": [RT, ST, c_char_p, c_int, c_int, Slice, Slice, Slice, c_size_t,
                                c_size_t, c_size_t, POINTER(GemmEpilogue)],
+    "forge_gemm_kernel_name": [RT, c_int, c_int, c_size_t, c_size_t, c_size_t, c_int, c_char_p,
+                               c_size_t],
     "forge_gemm_batch_f32": [RT, ST, c_int, c_int, c_size_t, c_size_t, c_size_t, c_size_t,
                              POINTER(GemmProblem)],
     "forge_transpose_f32": [RT, ST, Slice, Slice, c_size_t, c_size_t],

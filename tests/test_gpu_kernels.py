@@ -542,6 +542,35 @@ def test_gemm_every_tile_instance(rt, tile, ta, tb):
             rt.gemm_ex_tile(tile, dA, dB, dZ, M - 1, N, K, trans_a=ta, trans_b=tb)
 
 
+@pytest.mark.parametrize("M,N,K,ta,tb,fused", [(4096, 4096, 4096, 0, 0, 0),
+                                                (2048, 2048, 1024, 0, 1, 1),
+                                                (2048, 1024, 4096, 0, 0, 1),
+                                                (4096, 2048, 2048, 1, 0, 1),
+                                                (256, 256, 512, 1, 1, 1),
+                                                (96, 80, 40, 0, 0, 0)])
+def test_gemm_kernel_name_names_the_kernel_that_runs(rt, M, N, K, ta, tb, fused):
+    """forge_gemm_kernel_name reports the dispatcher's choice: the product
+    through that tile instance equals the dispatched product bit for bit."""
+    name = rt.gemm_kernel_name(M, N, K, ta, tb, fused)
+    say(f"gemm kernel name {M}x{N}x{K} ta={ta} tb={tb} fused={fused}: {name}")
+    ab = ("t" if ta else "n") + ("t" if tb else "n")
+    prefix = f"forge_gemm_{ab}_"
+    assert name.startswith(prefix) and "/split" not in name, name
+    plain = not fused and ab == "nn"
+    assert name.endswith("_e") != plain, name
+    tag = name[len(prefix):].removesuffix("_e")
+    A = orc.uniform((K, M) if ta else (M, K), 41)
+    B = orc.uniform((N, K) if tb else (K, N), 42)
+    dA, dB, dC, dT = rt.array(A), rt.array(B), rt.empty((M, N)), rt.empty((M, N))
+    if plain:
+        rt.gemm(dA, dB, dC, M, N, K)
+        rt.gemm_tile(tag, dA, dB, dT, M, N, K)
+    else:
+        rt.gemm_ex(dA, dB, dC, M, N, K, trans_a=ta, trans_b=tb)
+        rt.gemm_ex_tile(tag, dA, dB, dT, M, N, K, trans_a=ta, trans_b=tb)
+    assert np.array_equal(dC.numpy(), dT.numpy())
+
+
 @pytest.mark.parametrize("M,N,K", [(256, 128, 192), (70, 50, 33)])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_gemm_batch_bit_identical_to_single(rt, M, N, K, ta, tb):
