@@ -230,7 +230,9 @@ forge_status forge_gemm_ex_f32(forge_runtime *rt, forge_stream *stream,
  * tiles that split K over two wave groups (128x64x32, 64x128x32,
  * 128x128x32; K % (2 BK) == 0) or "64x64x16_2x2_g" for the guarded one.
  * Unguarded tiles require M % BM == N % BN == K % BK == 0, 16-byte aligned
- * operands and K, N <= 2^21; anything else is FORGE_EINVAL.  Used by the
+ * operands and K, N <= 2^21; anything else is FORGE_EINVAL.  A suffix
+ * "@<n>" (1..16) lets a CU hold at most n of the launch's workgroups (the
+ * launch reserves extra LDS); results do not depend on it.  Used by the
  * benchmark's tile sweep. */
 forge_status forge_gemm_f32_tile(forge_runtime *rt, forge_stream *stream,
                                  const char *tile_tag, forge_slice A,
@@ -252,7 +254,7 @@ forge_status forge_gemm_f32_split(forge_runtime *rt, forge_stream *stream,
  * "128x64x32_x", "64x128x32_x", "64x64x32_x", "128x64x32_k2_x",
  * "64x128x32_k2_x" or "64x64x16_2x2_g"), so every
  * instance the dispatcher can pick is testable at small shapes.  The same
- * shape and alignment rules as forge_gemm_f32_tile. */
+ * shape, alignment and "@<n>" rules as forge_gemm_f32_tile. */
 forge_status forge_gemm_ex_f32_tile(forge_runtime *rt, forge_stream *stream,
                                     const char *tile_tag, int trans_a, int trans_b,
                                     forge_slice A, forge_slice B, forge_slice C,
@@ -263,9 +265,10 @@ forge_status forge_gemm_ex_f32_tile(forge_runtime *rt, forge_stream *stream,
  * that forge_gemm_f32 (fused = 0) or forge_gemm_ex_f32 (fused = 1) launches
  * for a product of this shape and these transposes with 16-byte aligned
  * operands, written NUL-terminated to name (cap bytes; a name that does not
- * fit is FORGE_EINVAL).  A product computed as K slices is reported as
- * "<batched slice kernel>/split<N>".  Lets benchmarks and profiles name the
- * kernel they measure. */
+ * fit is FORGE_EINVAL).  A launch that lets a CU hold at most n of its
+ * workgroups is reported as "<kernel>@<n>", a product computed as K slices
+ * as "<batched slice kernel>/split<N>".  Lets benchmarks and profiles name
+ * the kernel they measure. */
 forge_status forge_gemm_kernel_name(forge_runtime *rt, int trans_a, int trans_b,
                                     size_t M, size_t N, size_t K, int fused,
                                     char *name, size_t cap);

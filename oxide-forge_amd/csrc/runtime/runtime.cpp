@@ -566,12 +566,18 @@ const GemmConfig kTile128x64k2 = {"128x64x32_k2_x", 128, 64, 32, 512, 2};
 const GemmConfig kTile64x128k2 = {"64x128x32_k2_x", 64, 128, 32, 512, 2};
 
 // Unguarded tiles, largest first, and their measured efficiency relative to
-// the best (4096^3 plain on MI355X: 146.4, 150.7, 151.3, 151.6 and 149.6
-// TFLOP/s).  All but 128x256 have fused-epilogue and batched instances;
-// 128x256 has a plain NN one.
+// 128x128 on large shapes with every CU holding two or more workgroups
+// (MI355X, e.g. 4096x4096x2048 plain: 148.9, 146.0, 145.4 and 138.3
+// TFLOP/s for 128x128, 64x128 and 128x64 at two per CU, and 64x64).  All
+// but 128x256 have fused-epilogue and batched instances; 128x256 has a
+// plain NN one.
 const GemmConfig* const kUnguarded[] = {&kTile128x256, &kTile128x128, &kTile128x64,
                                         &kTile64x128, &kTile64x64};
-const double kTileEfficiency[] = {0.966, 0.994, 0.998, 1.0, 0.987};
+const double kTileEfficiency[] = {0.975, 1.0, 0.98, 0.985, 0.94};
+// A CU that holds a single four-wave workgroup has one wave per SIMD, which
+// hides less: 2048x2048x1024 as 256 tiles of 128x128 runs at 133 TFLOP/s,
+// as 512 tiles of 64x128 at 139.
+constexpr double kSingleWorkgroupFactor = 0.96;
 
 enum class GemmKind { Plain, Epilogue, Batch };
 
@@ -601,21 +607,46 @@ int gemm_occupancy(forge_runtime* rt, const char* name, int threads) {
     return blocks;
 }
 
-// Tile choice: the best efficiency x balance; ties go to the larger tile.
-// With occ workgroups of a tile resident per CU, t tiles that all fit at
-// once (t <= CUs * occ) spread over the CUs, balance t / (CUs * ceil(t /
-// CUs)); more than that run in waves of CUs * occ, balance t / (CUs * occ *
-// ceil(t / (CUs * occ))).  (2048 tiles of 128x64, three per CU: 151.3
-// TFLOP/s; 1024 of them: 121, where 128x128, two per CU, gives 148.)
-// Results: 4096^3, 8192x1024, the 2048x4096 FFN and the C5 products ->
-// 128x128; 2048x2048 (attention scores) and 2048x1024 products -> 64x128.
-// Unaligned shapes and shapes the tiles do not divide take the
-// bounds-guarded 64x64 tile.  `count` same-shape products share the launch
-// (kind Batch).
-const GemmConfig& choose_gemm(forge_runtime* rt, int ta, int tb, size_t M, size_t N, size_t K,
-                              bool aligned, GemmKind kind, size_t count = 1) {
+// Dynamic LDS that limits a kernel to `cap` resident workgroups per CU (its
+// static LDS plus this fills 1 / cap of the CU's LDS); 0 when the kernel's
+// own LDS already allows no more.
+forge_status occupancy_cap_shmem(forge_runtime* rt, const char* name, int cap, size_t* out) {
+    hipFunction_t f = nullptr;
+    FORGE_TRY(get_function(rt, name, &f));
+    int static_lds = 0, lds_cu = 0;
+    HIP_TRY(hipFuncGetAttribute(&static_lds, HIP_FUNC_ATTRIBUTE_SHARED_SIZE_BYTES, f));
+    HIP_TRY(hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
+                                  rt->device));
+    const int total = (lds_cu / cap) & ~511;
+    *out = total > static_lds ? (size_t)(total - static_lds) : 0;
+    return FORGE_OK;
+}
+
+// A tile and how many of its workgroups a CU may hold (cap 0: as many as
+// its registers and LDS allow; otherwise the launch reserves extra LDS).
+struct GemmPlan {
+    const GemmConfig* cfg;
+    int cap;
+};
+
+// Tile choice: the best efficiency x balance over the tiles and, for each,
+// the number c of workgroups a CU may hold (from what fits down to one).
+// t tiles that all fit at once (t <= CUs * c) spread over the CUs, balance
+// t / (CUs * ceil(t / CUs)); more than that run in waves of CUs * c,
+// balance t / (CUs * c * ceil(t / (CUs * c))).  The last of a wave's tiles
+// do not spread evenly over the CUs: 1024 tiles of 64x128 at three per CU
+// run at 120 TFLOP/s, at two per CU (exact waves) at 147.  A CU left with
+// a single four-wave workgroup scores kSingleWorkgroupFactor less.  Ties go
+// to the larger tile, then to the larger c.  Results on the C3-C5 shapes:
+// 4096^3, 8192x1024, 2048x4096 and the C5 products -> 128x128; 2048x2048
+// and 2048x1024 products -> 64x128 (the three C4 Q/K/V products of one
+// batch: 768 tiles at three per CU).  Unaligned shapes and shapes the
+// tiles do not divide take the bounds-guarded 64x64 tile.  `count`
+// same-shape products share the launch (kind Batch).
+GemmPlan choose_gemm(forge_runtime* rt, int ta, int tb, size_t M, size_t N, size_t K,
+                     bool aligned, GemmKind kind, size_t count = 1) {
     const size_t cus = rt->cu_count > 0 ? (size_t)rt->cu_count : 256;
-    const GemmConfig* best = &kGuard64;
+    GemmPlan best{&kGuard64, 0};
     double best_score = 0.0;
     const bool plain_nn = kind == GemmKind::Plain && !ta && !tb;
     for (int i = plain_nn ? 0 : 1; i < 5; i++) {
@@ -623,18 +654,24 @@ const GemmConfig& choose_gemm(forge_runtime* rt, int ta, int tb, size_t M, size_
         if (!aligned || M % g.bm || N % g.bn || K % ((size_t)g.bk * g.ks)) continue;
         char name[96];
         gemm_kernel_name(name, sizeof name, kind, ta, tb, g);
-        const size_t slots = cus * (size_t)gemm_occupancy(rt, name, g.threads);
+        const int occ = gemm_occupancy(rt, name, g.threads);
         const size_t t = count * (M / g.bm) * (N / g.bn);
-        const double balance =
-            t <= slots ? (double)t / (double)(cus * ((t + cus - 1) / cus))
-                       : (double)t / (double)(slots * ((t + slots - 1) / slots));
-        const double score = kTileEfficiency[i] * balance;
-        if (score > best_score + 1e-9) {
-            best = kUnguarded[i];
-            best_score = score;
+        for (int c = occ; c >= 1; c--) {
+            const size_t slots = cus * (size_t)c;
+            const size_t per_cu = (t + cus - 1) / cus;
+            const double balance =
+                t <= slots ? (double)t / (double)(cus * per_cu)
+                           : (double)t / (double)(slots * ((t + slots - 1) / slots));
+            const bool single = occ > 1 && (c == 1 || per_cu == 1);
+            const double score =
+                kTileEfficiency[i] * balance * (single ? kSingleWorkgroupFactor : 1.0);
+            if (score > best_score + 1e-9) {
+                best = {&g, c == occ ? 0 : c};
+                best_score = score;
+            }
         }
     }
-    return *best;
+    return best;
 }
 
 // Split-K plan for one product.  With the four-wave tiles no C3/C4/C5 shape
@@ -648,7 +685,7 @@ int choose_splits(forge_runtime* rt, int ta, int tb, size_t M, size_t N, size_t 
                   const GemmConfig** cfg) {
     const size_t cus = rt->cu_count > 0 ? (size_t)rt->cu_count : 256;
     // The K slices run as one batched launch.
-    const GemmConfig& g = choose_gemm(rt, ta, tb, M, N, K, aligned, GemmKind::Batch);
+    const GemmConfig& g = *choose_gemm(rt, ta, tb, M, N, K, aligned, GemmKind::Batch).cfg;
     if (&g == &kGuard64) return 1;
     const size_t t = (M / g.bm) * (N / g.bn);
     if (t * 4 > cus) return 1;
@@ -769,12 +806,15 @@ forge_status gemm_dispatch(forge_runtime* rt, forge_stream* s, int ta, int tb, f
     const int splits = choose_splits(rt, ta, tb, M, N, K, aligned, &split_cfg);
     if (splits > 1) return gemm_split_launch(rt, s, ta, tb, a, *split_cfg, splits);
     const GemmKind kind = plain_name && !ta && !tb ? GemmKind::Plain : GemmKind::Epilogue;
-    const GemmConfig& cfg = choose_gemm(rt, ta, tb, M, N, K, aligned, kind);
+    const GemmPlan plan = choose_gemm(rt, ta, tb, M, N, K, aligned, kind);
+    const GemmConfig& cfg = *plan.cfg;
     char name[96];
     gemm_kernel_name(name, sizeof name, kind, ta, tb, cfg);
+    size_t shmem = 0;
+    if (plan.cap) FORGE_TRY(occupancy_cap_shmem(rt, name, plan.cap, &shmem));
     unsigned tiles = (unsigned)(((M + cfg.bm - 1) / cfg.bm) * ((N + cfg.bn - 1) / cfg.bn));
     void* args[] = {&a};
-    return launch(rt, s, name, dim3(tiles), dim3(cfg.threads), 0, args);
+    return launch(rt, s, name, dim3(tiles), dim3(cfg.threads), shmem, args);
 }
 
 const char* binop_name(forge_binary_op op) {
@@ -957,10 +997,27 @@ extern "C" forge_status forge_gemm_ex_f32(forge_runtime* rt, forge_stream* s, in
     return gemm_dispatch(rt, s, trans_a != 0, trans_b != 0, A, B, C, M, N, K, ep, false);
 }
 
+// "<tile>" or "<tile>@<n>" (at most n workgroups per CU; 0 = no limit).
+forge_status split_tile_tag(const char* in, char* tag, size_t cap_bytes, int* cap) {
+    const char* at = strchr(in, '@');
+    const size_t len = at ? (size_t)(at - in) : strlen(in);
+    if (len >= cap_bytes) return fail(FORGE_EINVAL, "bad tile tag %s", in);
+    memcpy(tag, in, len);
+    tag[len] = 0;
+    *cap = 0;
+    if (at && (sscanf(at + 1, "%d", cap) != 1 || *cap < 1 || *cap > 16))
+        return fail(FORGE_EINVAL, "bad occupancy cap in %s", in);
+    return FORGE_OK;
+}
+
 extern "C" forge_status forge_gemm_f32_tile(forge_runtime* rt, forge_stream* s,
-                                            const char* tile_tag, forge_slice A, forge_slice B,
-                                            forge_slice C, size_t M, size_t N, size_t K) {
-    if (!rt || !tile_tag) return fail(FORGE_EINVAL, "null argument");
+                                            const char* tile_tag_in, forge_slice A,
+                                            forge_slice B, forge_slice C, size_t M, size_t N,
+                                            size_t K) {
+    if (!rt || !tile_tag_in) return fail(FORGE_EINVAL, "null argument");
+    char tile_tag[32];
+    int cap = 0;
+    FORGE_TRY(split_tile_tag(tile_tag_in, tile_tag, sizeof tile_tag, &cap));
     unsigned bm = 0, bn = 0, bk = 0, threads = 256, ks = 1;
     bool guarded = false;
     char tail[8] = {0};
@@ -1001,9 +1058,11 @@ extern "C" forge_status forge_gemm_f32_tile(forge_runtime* rt, forge_stream* s,
     a.alpha = 1.0f;
     char name[96];
     snprintf(name, sizeof name, "forge_gemm_nn_%s", tile_tag);
+    size_t shmem = 0;
+    if (cap) FORGE_TRY(occupancy_cap_shmem(rt, name, cap, &shmem));
     unsigned tiles = (unsigned)(((M + bm - 1) / bm) * ((N + bn - 1) / bn));
     void* args[] = {&a};
-    return launch(rt, s, name, dim3(tiles), dim3(threads), 0, args);
+    return launch(rt, s, name, dim3(tiles), dim3(threads), shmem, args);
 }
 
 extern "C" forge_status forge_gemm_f32_split(forge_runtime* rt, forge_stream* s,
@@ -1028,11 +1087,14 @@ extern "C" forge_status forge_gemm_f32_split(forge_runtime* rt, forge_stream* s,
 }
 
 extern "C" forge_status forge_gemm_ex_f32_tile(forge_runtime* rt, forge_stream* s,
-                                               const char* tile_tag, int trans_a, int trans_b,
+                                               const char* tile_tag_in, int trans_a, int trans_b,
                                                forge_slice A, forge_slice B, forge_slice C,
                                                size_t M, size_t N, size_t K,
                                                const forge_gemm_epilogue* ep) {
-    if (!rt || !tile_tag) return fail(FORGE_EINVAL, "null argument");
+    if (!rt || !tile_tag_in) return fail(FORGE_EINVAL, "null argument");
+    char tile_tag[32];
+    int cap = 0;
+    FORGE_TRY(split_tile_tag(tile_tag_in, tile_tag, sizeof tile_tag, &cap));
     const GemmConfig* cfg = nullptr;
     for (const GemmConfig* c : {&kGuard64, &kTile128x64k2, &kTile64x128k2})
         if (strcmp(c->tag, tile_tag) == 0) cfg = c;
@@ -1049,10 +1111,12 @@ extern "C" forge_status forge_gemm_ex_f32_tile(forge_runtime* rt, forge_stream* 
     if (M == 0 || N == 0) return FORGE_OK;
     char name[96];
     snprintf(name, sizeof name, "forge_gemm_%s_%s_e", gemm_ab(trans_a, trans_b), cfg->tag);
+    size_t shmem = 0;
+    if (cap) FORGE_TRY(occupancy_cap_shmem(rt, name, cap, &shmem));
     const unsigned tiles =
         (unsigned)(((M + cfg->bm - 1) / cfg->bm) * ((N + cfg->bn - 1) / cfg->bn));
     void* args[] = {&a};
-    return launch(rt, s, name, dim3(tiles), dim3(cfg->threads), 0, args);
+    return launch(rt, s, name, dim3(tiles), dim3(cfg->threads), shmem, args);
 }
 
 extern "C" forge_status forge_gemm_kernel_name(forge_runtime* rt, int trans_a, int trans_b,
@@ -1075,9 +1139,10 @@ extern "C" forge_status forge_gemm_kernel_name(forge_runtime* rt, int trans_a, i
         n = snprintf(name, cap, "%s/split%d", kernel, splits);
     } else {
         const GemmKind kind = !fused && !ta && !tb ? GemmKind::Plain : GemmKind::Epilogue;
-        gemm_kernel_name(kernel, sizeof kernel, kind, ta, tb,
-                         choose_gemm(rt, ta, tb, M, N, K, aligned, kind));
-        n = snprintf(name, cap, "%s", kernel);
+        const GemmPlan plan = choose_gemm(rt, ta, tb, M, N, K, aligned, kind);
+        gemm_kernel_name(kernel, sizeof kernel, kind, ta, tb, *plan.cfg);
+        n = plan.cap ? snprintf(name, cap, "%s@%d", kernel, plan.cap)
+                     : snprintf(name, cap, "%s", kernel);
     }
     if (n < 0 || (size_t)n >= cap) return fail(FORGE_EINVAL, "name buffer of %zu bytes too small", cap);
     return FORGE_OK;
@@ -1106,8 +1171,9 @@ extern "C" forge_status forge_gemm_batch_f32(forge_runtime* rt, forge_stream* s,
         if (z < (size_t)GEMM_BATCH_MAX) b.p[z] = a;
     }
     if (count == 0 || M == 0 || N == 0) return FORGE_OK;
-    const GemmConfig& cfg =
+    const GemmPlan plan =
         choose_gemm(rt, trans_a, trans_b, M, N, K, all_aligned, GemmKind::Batch, count);
+    const GemmConfig& cfg = *plan.cfg;
     const GemmConfig* split_cfg = nullptr;
     // Shapes the single-product path splits in K are dispatched one by one,
     // so every product equals its forge_gemm_ex_f32 result bit for bit.
@@ -1122,8 +1188,11 @@ extern "C" forge_status forge_gemm_batch_f32(forge_runtime* rt, forge_stream* s,
     b.tiles = (int)((M / cfg.bm) * (N / cfg.bn));
     char name[96];
     gemm_kernel_name(name, sizeof name, GemmKind::Batch, trans_a, trans_b, cfg);
+    size_t shmem = 0;
+    if (plan.cap) FORGE_TRY(occupancy_cap_shmem(rt, name, plan.cap, &shmem));
     void* args[] = {&b};
-    return launch(rt, s, name, dim3((unsigned)(b.tiles * count)), dim3(cfg.threads), 0, args);
+    return launch(rt, s, name, dim3((unsigned)(b.tiles * count)), dim3(cfg.threads), shmem,
+                  args);
 }
 
 extern "C" forge_status forge_transpose_f32(forge_runtime* rt, forge_stream* s, forge_slice in,

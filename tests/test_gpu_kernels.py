@@ -544,6 +544,7 @@ def test_gemm_every_tile_instance(rt, tile, ta, tb):
 
 @pytest.mark.parametrize("M,N,K,ta,tb,fused", [(4096, 4096, 4096, 0, 0, 0),
                                                 (2048, 2048, 1024, 0, 1, 1),
+                                                (4096, 1024, 2048, 0, 0, 0),
                                                 (2048, 1024, 4096, 0, 0, 1),
                                                 (4096, 2048, 2048, 1, 0, 1),
                                                 (256, 256, 512, 1, 1, 1),
@@ -556,9 +557,10 @@ def test_gemm_kernel_name_names_the_kernel_that_runs(rt, M, N, K, ta, tb, fused)
     ab = ("t" if ta else "n") + ("t" if tb else "n")
     prefix = f"forge_gemm_{ab}_"
     assert name.startswith(prefix) and "/split" not in name, name
+    kernel, _, cap = name.partition("@")
     plain = not fused and ab == "nn"
-    assert name.endswith("_e") != plain, name
-    tag = name[len(prefix):].removesuffix("_e")
+    assert kernel.endswith("_e") != plain, name
+    tag = kernel[len(prefix):].removesuffix("_e") + (f"@{cap}" if cap else "")
     A = orc.uniform((K, M) if ta else (M, K), 41)
     B = orc.uniform((N, K) if tb else (K, N), 42)
     dA, dB, dC, dT = rt.array(A), rt.array(B), rt.empty((M, N)), rt.empty((M, N))
@@ -569,6 +571,29 @@ def test_gemm_kernel_name_names_the_kernel_that_runs(rt, M, N, K, ta, tb, fused)
         rt.gemm_ex(dA, dB, dC, M, N, K, trans_a=ta, trans_b=tb)
         rt.gemm_ex_tile(tag, dA, dB, dT, M, N, K, trans_a=ta, trans_b=tb)
     assert np.array_equal(dC.numpy(), dT.numpy())
+
+
+@pytest.mark.parametrize("tile", ["64x128x32_x@2", "128x128x32_x@1", "64x64x32_x@3",
+                                  "128x64x32_x@2"])
+def test_gemm_occupancy_cap_keeps_results(rt, tile):
+    """A launch that lets a CU hold fewer workgroups computes the same
+    product bit for bit, plain and with a fused epilogue; malformed caps are
+    refused."""
+    M, N, K = 512, 512, 256
+    say(f"gemm occupancy cap {tile}")
+    base = tile.partition("@")[0]
+    A, B, bias = orc.uniform((M, K), 51), orc.uniform((K, N), 52), orc.uniform((N,), 53)
+    dA, dB, dbias = rt.array(A), rt.array(B), rt.array(bias)
+    out = [rt.empty((M, N)) for _ in range(4)]
+    rt.gemm_tile(base, dA, dB, out[0], M, N, K)
+    rt.gemm_tile(tile, dA, dB, out[1], M, N, K)
+    rt.gemm_ex_tile(base, dA, dB, out[2], M, N, K, bias=dbias, activation=oxforge.ACT_GELU)
+    rt.gemm_ex_tile(tile, dA, dB, out[3], M, N, K, bias=dbias, activation=oxforge.ACT_GELU)
+    assert np.array_equal(out[0].numpy(), out[1].numpy())
+    assert np.array_equal(out[2].numpy(), out[3].numpy())
+    for bad in (base + "@0", base + "@17", base + "@x"):
+        with pytest.raises(oxforge.ForgeError):
+            rt.gemm_tile(bad, dA, dB, out[1], M, N, K)
 
 
 @pytest.mark.parametrize("M,N,K", [(256, 128, 192), (70, 50, 33)])
