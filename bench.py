@@ -344,9 +344,8 @@ def sweep(rt, orc, steps, warmup):
         A = orc.uniform((M, K), 3)
         B = orc.uniform((K, N), 4)
         dA, dB, dC = rt.array(A), rt.array(B), rt.empty((M, N))
-        for tag in ["128x256x32_x", "256x128x32_x", "128x128x32_x", "128x128x64_x",
-                    "128x64x32_x", "64x128x32_x", "64x64x32_x", "128x64x32_k2_x",
-                    "64x128x32_k2_x", "128x128x32_k2_x"]:
+        for tag in ["128x256x32_x", "128x128x32_x", "128x64x32_x", "128x64x32_x@2",
+                    "64x128x32_x", "64x128x32_x@2", "64x64x32_x"]:
             key = f"{M}x{N}x{K}:{tag}"
 
             def fn(i, tag=tag.encode()):

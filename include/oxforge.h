@@ -225,10 +225,8 @@ forge_status forge_gemm_ex_f32(forge_runtime *rt, forge_stream *stream,
 
 /* Tuning entry point (no reference counterpart): forge_gemm_f32 with an
  * explicit plain tile instance: "<BM>x<BN>x<BK>_x" for the unguarded
- * four-wave tiles (128x256x32, 256x128x32, 128x128x32, 128x128x64,
- * 128x64x32, 64x128x32, 64x64x32), "<BM>x<BN>x<BK>_k2_x" for the eight-wave
- * tiles that split K over two wave groups (128x64x32, 64x128x32,
- * 128x128x32; K % (2 BK) == 0) or "64x64x16_2x2_g" for the guarded one.
+ * four-wave tiles (128x256x32, 128x128x32, 128x64x32, 64x128x32, 64x64x32)
+ * or "64x64x16_2x2_g" for the guarded one.
  * Unguarded tiles require M % BM == N % BN == K % BK == 0, 16-byte aligned
  * operands and K, N <= 2^21; anything else is FORGE_EINVAL.  A suffix
  * "@<n>" (1..16) lets a CU hold at most n of the launch's workgroups (the
@@ -251,8 +249,7 @@ forge_status forge_gemm_f32_split(forge_runtime *rt, forge_stream *stream,
 
 /* Testing entry point (no reference counterpart): forge_gemm_ex_f32 through
  * the fused-epilogue instance of one named tile ("128x128x32_x",
- * "128x64x32_x", "64x128x32_x", "64x64x32_x", "128x64x32_k2_x",
- * "64x128x32_k2_x" or "64x64x16_2x2_g"), so every
+ * "128x64x32_x", "64x128x32_x", "64x64x32_x" or "64x64x16_2x2_g"), so every
  * instance the dispatcher can pick is testable at small shapes.  The same
  * shape, alignment and "@<n>" rules as forge_gemm_f32_tile. */
 forge_status forge_gemm_ex_f32_tile(forge_runtime *rt, forge_stream *stream,

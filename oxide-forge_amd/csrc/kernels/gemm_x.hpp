@@ -3,7 +3,7 @@
 //
 // Same contract as gemm_body (gemm.hpp): C = A * B row-major, f32 accumulate,
 // the same fused epilogue; unguarded (M % BM == N % BN == K % BK == 0,
-// 16-byte aligned operands).
+// 16-byte aligned operands, row pitches up to 2^21 floats).
 //
 // Structure
 //   - A workgroup of four waves (2 x 2) computes a BM x BN tile; each wave
@@ -18,13 +18,18 @@
 //     read belong to four different blocks: block 4g + e holds rows (or
 //     columns) base + 64 g + 4 i + e for MFMA index i.  The epilogue undoes
 //     this mapping, and the four columns of a lane become one 128-bit store.
-//   - K advances in BK slabs through two LDS buffers.  The next slab is
-//     loaded from global memory into registers while the current one is
-//     multiplied, then written to the other buffer: one barrier per slab.
-//     Operand reads for chunk c + 1 are issued before the MFMAs of chunk c.
-//   - LDS keeps the global orientation of each slab with a 4-float row pad:
-//     k-contiguous rows then start 4 banks apart, so sixteen lanes reading
-//     sixteen rows hit distinct banks; m/n-contiguous reads are contiguous.
+//   - K advances in BK slabs through two LDS stages, loaded straight from
+//     global memory into LDS (XDma) one slab ahead.  Slab kt + 1 is waited
+//     for, and slab kt + 2 requested, in the middle of slab kt's last chunk.
+//   - The main loop issues no vector instructions besides the MFMAs, the
+//     LDS operand reads and the slab loads: every address is a precomputed
+//     per-lane offset plus scalar registers and immediates.  On gfx950 each
+//     other vector instruction between MFMAs costs the matrix pipe about
+//     seven cycles (a loop of 128 MFMAs with 32 added VALU instructions
+//     runs at 92% of the MFMA rate, with 64 at 89%); scalar instructions
+//     cost nothing.
+//   - The epilogue goes through LDS: each wave writes its sub-tile there and
+//     streams it back as 128-bit rows with the fused steps.
 #pragma once
 #include "gemm.hpp"
 
@@ -281,17 +286,8 @@ __device__ __forceinline__ void x_epi_store(const GemmArgs& p, f4 z, f4 res, f4 
     *reinterpret_cast<f4*>(p.C + idx) = f4{y[0], y[1], y[2], y[3]};
 }
 
-// KS = 2 splits K inside the workgroup: eight waves in two groups of four,
-// group g multiplying the g-th half of the slabs into its own accumulators
-// through its own two LDS stages.  The halves are added (first half +
-// second half) before the epilogue.  It gives a CU two waves per SIMD when
-// the output has only one tile per CU.  The sum order differs from KS = 1,
-// so a shape computes with one KS everywhere (the host's choice depends on
-// the shape only).
-template <int BM, int BN, int BK, int KS, bool TA, bool TB, bool EPI>
+template <int BM, int BN, int BK, bool TA, bool TB, bool EPI>
 __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
-    static_assert(KS == 1 || KS == 2, "one or two K groups");
-    constexpr int NT = 256;  // threads of one K group
     constexpr int TM = BM / 2, TN = BN / 2;
     constexpr int FM = TM / 16, FN = TN / 16;
     constexpr int CH = BK / 16;
@@ -307,15 +303,11 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     using SB = XSlab<B_ROWS, B_COLS, B_KC>;
     constexpr int DMA_PER_STAGE = SA::PER_WAVE + SB::PER_WAVE;
     static_assert(CH % 2 == 0, "slabs hold an even number of 16-wide chunks");
-    // The two slab stages of each K group, reused by the epilogue for each
-    // wave's TM x TN sub-tile of C (row pitch CP).  A sub-tile too large for
-    // LDS (128 x 128 per wave) goes out in EP passes of TM / EP rows; its
-    // accumulator blocks must then be row-contiguous (k-contiguous A).
+    // The two slab stages, reused by the epilogue for each wave's TM x TN
+    // sub-tile of C (row pitch CP).
     constexpr int CP = TN + 4;
-    constexpr int EP = KS * 4 * TM * CP * 4 > 160 * 1024 ? 2 : 1;
-    static_assert(EP == 1 || (KS == 1 && A_KC && FM % EP == 0), "multi-pass epilogue shape");
-    constexpr int EPI_ELEMS = KS * 4 * (TM / EP) * CP;
-    constexpr int SMEM = KS * 2 * STAGE > EPI_ELEMS ? KS * 2 * STAGE : EPI_ELEMS;
+    constexpr int EPI_ELEMS = 4 * TM * CP;
+    constexpr int SMEM = 2 * STAGE > EPI_ELEMS ? 2 * STAGE : EPI_ELEMS;
     static_assert(SMEM * 4 <= 160 * 1024, "LDS budget");
     __shared__ __attribute__((aligned(1024))) float smem_all[SMEM];
 
@@ -325,19 +317,16 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     const int m0 = tm * BM, n0 = tn * BN;
 
     const int lane = threadIdx.x & 63;
-    // K group and wave within the group, wave-uniform (scalar registers).
-    const int kg = KS == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8));
-    const int wave = __builtin_amdgcn_readfirstlane((int)((threadIdx.x >> 6) & 3));
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // scalar
     const int wm = wave >> 1, wn = wave & 1;
     const int l16 = lane & 15, kq = lane >> 4;
-    float* const smem = smem_all + kg * (2 * STAGE);
+    float* const smem = smem_all;
 
-    // Slabs of this K group: [kg * KT, (kg + 1) * KT) of the K / BK slabs.
-    const int KT = p.K / BK / KS;
+    const int KT = p.K / BK;
     const long long a_kstride = TA ? (long long)BK * p.lda : BK;
     const long long b_kstride = TB ? BK : (long long)BK * p.ldb;
-    const float* a_base = (TA ? p.A + m0 : p.A + (long long)m0 * p.lda) + kg * KT * a_kstride;
-    const float* b_base = (TB ? p.B + (long long)n0 * p.ldb : p.B + n0) + kg * KT * b_kstride;
+    const float* a_base = TA ? p.A + m0 : p.A + (long long)m0 * p.lda;
+    const float* b_base = TB ? p.B + (long long)n0 * p.ldb : p.B + n0;
 
     v4f acc[FM][FN];
 #pragma unroll
@@ -356,8 +345,8 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     dma_b.init(p.ldb, wave, lane);
     XFrag<A_KC, A_KC ? BK : BM, BK, FM> rd_a;
     XFrag<B_KC, B_KC ? BK : BN, BK, FN> rd_b;
-    rd_a.init(kg * (2 * STAGE), STAGE, a_off, l16, kq);
-    rd_b.init(kg * (2 * STAGE) + A_ELEMS, STAGE, b_off, l16, kq);
+    rd_a.init(0, STAGE, a_off, l16, kq);
+    rd_b.init(A_ELEMS, STAGE, b_off, l16, kq);
 
     auto issue = [&](int k_slab, int stage) {
         float* d = smem + stage * STAGE;
@@ -471,92 +460,72 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     // block is MFMA row 4 kq + r, column l16), then streams the sub-tile
     // back row by row: four consecutive columns per lane, so operands and
     // results move as 128-bit accesses and the fused steps are one compact
-    // loop instead of code unrolled over every accumulator.
-    // With two K groups each sub-tile is written twice (once per group),
-    // and each group then finishes half of its rows, adding the groups'
-    // values in group order.
+    // loop instead of code unrolled over every accumulator.  A wave reads
+    // only what it wrote, and LDS executes one wave's accesses in order.
     __syncthreads();  // every wave is done with the slab stages
-    constexpr int PR = TM / EP;  // sub-tile rows per pass
-    float* cw = smem_all + (kg * 4 + wave) * (PR * CP);
-    const float* c0 = smem_all + wave * (PR * CP);  // group 0's copy of the sub-tile
+    float* const cw = smem_all + wave * (TM * CP);
+    if constexpr (!B_KC && XVec<FN>::W == 4) {
 #pragma unroll
-    for (int pass = 0; pass < EP; pass++) {
-        if (pass > 0) {
-            // The wave's reads of the previous pass precede its writes of this
-            // one: LDS executes one wave's accesses in order, and the empty asm
-            // keeps the compiler from moving them.
-            asm volatile("" ::: "memory");
-        }
-        if constexpr (!B_KC && XVec<FN>::W == 4) {
+        for (int i = 0; i < FM; i++)
 #pragma unroll
-            for (int i = pass * (FM / EP); i < (pass + 1) * (FM / EP); i++)
+            for (int r = 0; r < 4; r++) {
+                const int rr = x_index<A_KC, FM>(0, i, 4 * kq + r);
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int rr = x_index<A_KC, FM>(0, i, 4 * kq + r) - pass * PR;
-#pragma unroll
-                    for (int g = 0; g < FN / 4; g++) {
-                        const f4 v = {acc[i][4 * g + 0][r], acc[i][4 * g + 1][r],
-                                      acc[i][4 * g + 2][r], acc[i][4 * g + 3][r]};
-                        *reinterpret_cast<f4*>(cw + rr * CP + 64 * g + 4 * l16) = v;
-                    }
+                for (int g = 0; g < FN / 4; g++) {
+                    const f4 v = {acc[i][4 * g + 0][r], acc[i][4 * g + 1][r],
+                                  acc[i][4 * g + 2][r], acc[i][4 * g + 3][r]};
+                    *reinterpret_cast<f4*>(cw + rr * CP + 64 * g + 4 * l16) = v;
                 }
-        } else {
-#pragma unroll
-            for (int i = pass * (FM / EP); i < (pass + 1) * (FM / EP); i++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int rr = x_index<A_KC, FM>(0, i, 4 * kq + r) - pass * PR;
-#pragma unroll
-                    for (int j = 0; j < FN; j++)
-                        cw[rr * CP + x_index<B_KC, FN>(0, j, l16)] = acc[i][j][r];
-                }
-        }
-        if constexpr (KS == 2) __syncthreads();  // both groups' halves written
-        asm volatile("" ::: "memory");
-        const int row0 = m0 + a_off + pass * PR, col0 = n0 + b_off;
-        constexpr int F4_ROW = TN / 4;
-        constexpr int ROWS = PR / KS;  // sub-tile rows this wave finishes
-        const int rbase = kg * ROWS;
-        constexpr int ITER = ROWS * F4_ROW / 64;  // 128-bit groups per lane
-        constexpr int NB = ITER < 4 ? ITER : 4;  // groups whose operands load together
-        static_assert(ITER % NB == 0, "epilogue batches");
-#pragma unroll 1
-        for (int b0 = 0; b0 < ITER; b0 += NB) {
-            // Loads of a batch first, so NB global reads per operand are in
-            // flight together.
-            f4 z[NB], res[NB], mul[NB], old[NB];
-            long long idx[NB];
-            int col[NB];
-#pragma unroll
-            for (int u = 0; u < NB; u++) {
-                const int q = lane + 64 * (b0 + u);
-                const int rr = rbase + q / F4_ROW, c4 = q % F4_ROW;
-                z[u] = *reinterpret_cast<const f4*>(c0 + rr * CP + 4 * c4);
-                if constexpr (KS == 2) {
-                    const f4 h = *reinterpret_cast<const f4*>(c0 + 4 * PR * CP + rr * CP + 4 * c4);
-                    z[u] = f4{z[u].x + h.x, z[u].y + h.y, z[u].z + h.z, z[u].w + h.w};
-                }
-                col[u] = col0 + 4 * c4;
-                idx[u] = (long long)(row0 + rr) * p.ldc + col[u];
-                x_epi_load<EPI>(p, idx[u], res[u], mul[u], old[u]);
             }
+    } else {
 #pragma unroll
-            for (int u = 0; u < NB; u++)
-                x_epi_store<EPI>(p, z[u], res[u], mul[u], old[u], col[u], idx[u]);
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int rr = x_index<A_KC, FM>(0, i, 4 * kq + r);
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+                    cw[rr * CP + x_index<B_KC, FN>(0, j, l16)] = acc[i][j][r];
+            }
+    }
+    asm volatile("" ::: "memory");
+    const int row0 = m0 + a_off, col0 = n0 + b_off;
+    constexpr int F4_ROW = TN / 4;
+    constexpr int ITER = TM * F4_ROW / 64;  // 128-bit groups per lane
+    constexpr int NB = ITER < 4 ? ITER : 4;  // groups whose operands load together
+    static_assert(ITER % NB == 0, "epilogue batches");
+#pragma unroll 1
+    for (int b0 = 0; b0 < ITER; b0 += NB) {
+        // Loads of a batch first, so NB global reads per operand are in
+        // flight together.
+        f4 z[NB], res[NB], mul[NB], old[NB];
+        long long idx[NB];
+        int col[NB];
+#pragma unroll
+        for (int u = 0; u < NB; u++) {
+            const int q = lane + 64 * (b0 + u);
+            const int rr = q / F4_ROW, c4 = q % F4_ROW;
+            z[u] = *reinterpret_cast<const f4*>(cw + rr * CP + 4 * c4);
+            col[u] = col0 + 4 * c4;
+            idx[u] = (long long)(row0 + rr) * p.ldc + col[u];
+            x_epi_load<EPI>(p, idx[u], res[u], mul[u], old[u]);
         }
-    }  // pass
+#pragma unroll
+        for (int u = 0; u < NB; u++)
+            x_epi_store<EPI>(p, z[u], res[u], mul[u], old[u], col[u], idx[u]);
+    }
 }
 
-template <int BM, int BN, int BK, int KS, bool TA, bool TB, bool EPI>
+template <int BM, int BN, int BK, bool TA, bool TB, bool EPI>
 __device__ __forceinline__ void gemm_single_x(const GemmArgs& p) {
-    gemm_body_x<BM, BN, BK, KS, TA, TB, EPI>(p, xcd_logical(blockIdx.x, gridDim.x));
+    gemm_body_x<BM, BN, BK, TA, TB, EPI>(p, xcd_logical(blockIdx.x, gridDim.x));
 }
 
 template <int BM, int BN, int BK, bool TA, bool TB>
 __device__ __forceinline__ void gemm_batch_x(const GemmBatchArgs& b) {
     const int logical = xcd_logical(blockIdx.x, gridDim.x);
     const int z = logical / b.tiles;
-    gemm_body_x<BM, BN, BK, 1, TA, TB, true>(b.p[z], logical - z * b.tiles);
+    gemm_body_x<BM, BN, BK, TA, TB, true>(b.p[z], logical - z * b.tiles);
 }
 
 }  // namespace forge

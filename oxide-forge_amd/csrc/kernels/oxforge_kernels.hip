@@ -22,12 +22,7 @@ using namespace forge;
 #define GEMM_X_OCC(BM, BN, BK) ((BM) * (BN) <= 128 * 128 && ((BM) + (BN)) * (BK) <= 256 * 32 ? 2 : 1)
 #define GEMM_X_KERNEL(NAME, BM, BN, BK, TA, TB, EPI)                          \
     FORGE_KERNEL void __launch_bounds__(256, GEMM_X_OCC(BM, BN, BK)) NAME(GemmArgs p) { \
-        gemm_single_x<BM, BN, BK, 1, TA, TB, EPI>(p);                          \
-    }
-// The same with K split over two wave groups (tile tag ..._k2_x).
-#define GEMM_X2_KERNEL(NAME, BM, BN, BK, TA, TB, EPI)                         \
-    FORGE_KERNEL void __launch_bounds__(512) NAME(GemmArgs p) {               \
-        gemm_single_x<BM, BN, BK, 2, TA, TB, EPI>(p);                          \
+        gemm_single_x<BM, BN, BK, TA, TB, EPI>(p);                          \
     }
 #define GEMM_GUARDED_KERNEL(NAME, BM, BN, BK, WMW, WNW, TA, TB, EPI)        \
     FORGE_KERNEL void __launch_bounds__(WMW * WNW * 64) NAME(GemmArgs p) {   \
@@ -41,8 +36,6 @@ using namespace forge;
     GEMM_X_KERNEL(forge_gemm_##AB##_128x64x32_x_e, 128, 64, 32, TA, TB, true)        \
     GEMM_X_KERNEL(forge_gemm_##AB##_64x128x32_x_e, 64, 128, 32, TA, TB, true)        \
     GEMM_X_KERNEL(forge_gemm_##AB##_64x64x32_x_e, 64, 64, 32, TA, TB, true)          \
-    GEMM_X2_KERNEL(forge_gemm_##AB##_128x64x32_k2_x_e, 128, 64, 32, TA, TB, true)    \
-    GEMM_X2_KERNEL(forge_gemm_##AB##_64x128x32_k2_x_e, 64, 128, 32, TA, TB, true)    \
     GEMM_GUARDED_KERNEL(forge_gemm_##AB##_64x64x16_2x2_g_e, 64, 64, 16, 2, 2, TA, TB, true)
 
 GEMM_FAMILY(nn, false, false)
@@ -78,18 +71,12 @@ FORGE_KERNEL void __launch_bounds__(SPLITK_THREADS) forge_gemm_splitk_reduce_s(c
     splitk_reduce_body<false>(P, splits, p);
 }
 
-// Plain C = A * B instances: forge_gemm_f32 (the headline GEMM) and the
-// tile candidates of the bench sweep.
+// Plain C = A * B instances of forge_gemm_f32 (the headline GEMM).
 GEMM_X_KERNEL(forge_gemm_nn_128x256x32_x, 128, 256, 32, false, false, false)
-GEMM_X_KERNEL(forge_gemm_nn_256x128x32_x, 256, 128, 32, false, false, false)
 GEMM_X_KERNEL(forge_gemm_nn_128x128x32_x, 128, 128, 32, false, false, false)
-GEMM_X_KERNEL(forge_gemm_nn_128x128x64_x, 128, 128, 64, false, false, false)
 GEMM_X_KERNEL(forge_gemm_nn_128x64x32_x, 128, 64, 32, false, false, false)
 GEMM_X_KERNEL(forge_gemm_nn_64x128x32_x, 64, 128, 32, false, false, false)
 GEMM_X_KERNEL(forge_gemm_nn_64x64x32_x, 64, 64, 32, false, false, false)
-GEMM_X2_KERNEL(forge_gemm_nn_128x64x32_k2_x, 128, 64, 32, false, false, false)
-GEMM_X2_KERNEL(forge_gemm_nn_64x128x32_k2_x, 64, 128, 32, false, false, false)
-GEMM_X2_KERNEL(forge_gemm_nn_128x128x32_k2_x, 128, 128, 32, false, false, false)
 GEMM_GUARDED_KERNEL(forge_gemm_nn_64x64x16_2x2_g, 64, 64, 16, 2, 2, false, false, false)
 
 // ------------------------------------------------------------------- rows

@@ -543,9 +543,8 @@ extern "C" forge_status forge_fill(forge_runtime* rt, forge_stream* s, forge_sli
 namespace {
 
 struct GemmConfig {
-    const char* tag;  // e.g. "128x256x32_x"
+    const char* tag;  // e.g. "128x128x32_x"
     int bm, bn, bk, threads;
-    int ks = 1;       // K groups inside the workgroup (K % (bk * ks) == 0)
 };
 
 const char* gemm_ab(int ta, int tb) {
@@ -559,11 +558,6 @@ const GemmConfig kTile128x64 = {"128x64x32_x", 128, 64, 32, 256};
 const GemmConfig kTile64x128 = {"64x128x32_x", 64, 128, 32, 256};
 const GemmConfig kTile64x64 = {"64x64x32_x", 64, 64, 32, 256};
 const GemmConfig kGuard64 = {"64x64x16_2x2_g", 64, 64, 16, 256};
-// Eight-wave variants with K split over two wave groups (fused epilogue and
-// plain NN instances; no batched ones).  Reached through the tile-forcing
-// entry points only.
-const GemmConfig kTile128x64k2 = {"128x64x32_k2_x", 128, 64, 32, 512, 2};
-const GemmConfig kTile64x128k2 = {"64x128x32_k2_x", 64, 128, 32, 512, 2};
 
 // Unguarded tiles, largest first, and their measured efficiency relative to
 // 128x128 on large shapes with every CU holding two or more workgroups
@@ -651,7 +645,7 @@ GemmPlan choose_gemm(forge_runtime* rt, int ta, int tb, size_t M, size_t N, size
     const bool plain_nn = kind == GemmKind::Plain && !ta && !tb;
     for (int i = plain_nn ? 0 : 1; i < 5; i++) {
         const GemmConfig& g = *kUnguarded[i];
-        if (!aligned || M % g.bm || N % g.bn || K % ((size_t)g.bk * g.ks)) continue;
+        if (!aligned || M % g.bm || N % g.bn || K % (size_t)g.bk) continue;
         char name[96];
         gemm_kernel_name(name, sizeof name, kind, ta, tb, g);
         const int occ = gemm_occupancy(rt, name, g.threads);
@@ -1018,7 +1012,8 @@ extern "C" forge_status forge_gemm_f32_tile(forge_runtime* rt, forge_stream* s,
     char tile_tag[32];
     int cap = 0;
     FORGE_TRY(split_tile_tag(tile_tag_in, tile_tag, sizeof tile_tag, &cap));
-    unsigned bm = 0, bn = 0, bk = 0, threads = 256, ks = 1;
+    unsigned bm = 0, bn = 0, bk = 0;
+    const unsigned threads = 256;
     bool guarded = false;
     char tail[8] = {0};
     if (sscanf(tile_tag, "%ux%ux%u_%7s", &bm, &bn, &bk, tail) != 4 || bm == 0 || bn == 0 ||
@@ -1026,9 +1021,6 @@ extern "C" forge_status forge_gemm_f32_tile(forge_runtime* rt, forge_stream* s,
         return fail(FORGE_EINVAL, "bad tile tag %s", tile_tag);
     if (strcmp(tail, "x") == 0) {
         // Four-wave instance <BM>x<BN>x<BK>_x.
-    } else if (strcmp(tail, "k2_x") == 0) {
-        threads = 512;  // eight waves, K over two groups
-        ks = 2;
     } else if (strcmp(tail, "2x2_g") == 0) {
         guarded = true;
     } else {
@@ -1039,7 +1031,7 @@ extern "C" forge_status forge_gemm_f32_tile(forge_runtime* rt, forge_stream* s,
     FORGE_TRY(need(A, M * K, "gemm A"));
     FORGE_TRY(need(B, K * N, "gemm B"));
     FORGE_TRY(need(C, M * N, "gemm C"));
-    if (!guarded && (M % bm || N % bn || K % (bk * ks) || !aligned16(A.ptr) ||
+    if (!guarded && (M % bm || N % bn || K % bk || !aligned16(A.ptr) ||
                      !aligned16(B.ptr) || !aligned16(C.ptr) || K % 4 || N % 4 ||
                      (long long)K > kUnguardedMaxPitch || (long long)N > kUnguardedMaxPitch))
         return fail(FORGE_EINVAL, "shape %zux%zux%zu does not fit unguarded tile %s", M, N, K,
@@ -1096,8 +1088,7 @@ extern "C" forge_status forge_gemm_ex_f32_tile(forge_runtime* rt, forge_stream* 
     int cap = 0;
     FORGE_TRY(split_tile_tag(tile_tag_in, tile_tag, sizeof tile_tag, &cap));
     const GemmConfig* cfg = nullptr;
-    for (const GemmConfig* c : {&kGuard64, &kTile128x64k2, &kTile64x128k2})
-        if (strcmp(c->tag, tile_tag) == 0) cfg = c;
+    if (strcmp(kGuard64.tag, tile_tag) == 0) cfg = &kGuard64;
     for (const GemmConfig* c : kUnguarded)
         if (c != &kTile128x256 && strcmp(c->tag, tile_tag) == 0) cfg = c;
     if (!cfg) return fail(FORGE_EINVAL, "tile %s has no epilogue instance", tile_tag);
@@ -1105,7 +1096,7 @@ extern "C" forge_status forge_gemm_ex_f32_tile(forge_runtime* rt, forge_stream* 
     bool aligned = false;
     FORGE_TRY(gemm_args(trans_a, trans_b, A, B, C, M, N, K, ep, &a, &aligned));
     if (cfg != &kGuard64 &&
-        (!aligned || M % cfg->bm || N % cfg->bn || K % ((size_t)cfg->bk * cfg->ks)))
+        (!aligned || M % cfg->bm || N % cfg->bn || K % (size_t)cfg->bk))
         return fail(FORGE_EINVAL, "shape %zux%zux%zu does not fit unguarded tile %s", M, N, K,
                     tile_tag);
     if (M == 0 || N == 0) return FORGE_OK;

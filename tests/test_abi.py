@@ -64,11 +64,10 @@ def dispatcher_kernel_names():
     """Every kernel name runtime.cpp can build (mirrors its naming rules)."""
     names = []
     tiles = ("128x128x32_x", "128x64x32_x", "64x128x32_x", "64x64x32_x")
-    k2 = ("128x64x32_k2_x", "64x128x32_k2_x")
     for ab in ("nn", "nt", "tn", "tt"):
-        for tag in tiles + k2 + ("64x64x16_2x2_g",):
+        for tag in tiles + ("64x64x16_2x2_g",):
             names.append(f"forge_gemm_{ab}_{tag}_e")
-    for tag in tiles + k2 + ("128x256x32_x", "64x64x16_2x2_g"):
+    for tag in tiles + ("128x256x32_x", "64x64x16_2x2_g"):
         names.append(f"forge_gemm_nn_{tag}")
     for ab in ("nn", "nt", "tn"):
         for tag in tiles:

@@ -504,16 +504,15 @@ def test_gemm_split_k_vs_oracle(rt, tile, splits, M, N, K):
         rt.gemm_split(tile, splits, dA, dB, dC, M, N, K + 16 * splits + 8)
 
 
-TILES = ["128x128x32_x", "128x64x32_x", "64x128x32_x", "64x64x32_x", "128x64x32_k2_x",
-         "64x128x32_k2_x", "64x64x16_2x2_g"]
+TILES = ["128x128x32_x", "128x64x32_x", "64x128x32_x", "64x64x32_x", "64x64x16_2x2_g"]
 
 
 @pytest.mark.parametrize("tile", TILES)
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_gemm_every_tile_instance(rt, tile, ta, tb):
     """Each fused-epilogue instance the dispatcher can pick, at a shape that
-    is two tiles by two and six K slabs (three per wave group for the _k2
-    tiles): the product within the GEMM bar of the f64 oracle, and the
+    is two tiles by two and six K slabs: the product within the GEMM bar of
+    the f64 oracle, and the
     epilogue (bias, residual, GELU, pre-activation store) bit-identical to
     the same steps applied to the plain product."""
     bm, bn = (int(x) for x in tile.split("x")[:2])
