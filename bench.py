@@ -149,6 +149,7 @@ def secondary_rows_at_scale(rt, orc, steps, warmup):
     gam = rt.array(orc.normal((cols,), 4, 1.0, 0.1))
     bet = rt.array(orc.normal((cols,), 5, 0.0, 0.1))
     dgam, dbet = rt.empty((cols,)), rt.empty((cols,))
+    rvec = rt.array(orc.normal((cols,), 6))
     cases = {
         "softmax_fwd": (2 * X, lambda i: rt.softmax_rows(xs[i % sets], rows, cols)),
         "layer_norm_fwd": (2 * X, lambda i: rt.layer_norm(xs[i % sets], rows, cols, gam, bet)),
@@ -163,6 +164,8 @@ def secondary_rows_at_scale(rt, orc, steps, warmup):
         "binary_add": (3 * X, lambda i: rt.binary(xs[i % sets], gs[i % sets], ds[i % sets],
                                                   oxforge.ADD)),
         "map_scale": (2 * X, lambda i: rt.map(ds[i % sets], oxforge.MAP_SCALE, 1.0)),
+        "by_rows_add": (2 * X, lambda i: rt.binary_assign_by_rows(ds[i % sets], rvec, rows, cols,
+                                                                  oxforge.ADD)),
     }
     for name, (nbytes, fn) in cases.items():
         ms = time_launches(rt, fn, max(steps, 32), warmup)

@@ -68,6 +68,20 @@ __device__ __forceinline__ float4 load_stream(const float* p) {
     return make_float4(v.x, v.y, v.z, v.w);
 }
 
+// Outputs of at least STREAM_NT_MIN floats (64 MiB) are stored
+// non-temporally: they do not fit the 256 MiB MALL beside their inputs, and
+// write-allocating them there costs bandwidth (6.59 against 5.80 TB/s for an
+// in-place float4 scale of 256 MiB on MI355X).  Smaller ones keep cached
+// stores (at 16 MiB non-temporal ones are 4% slower).
+constexpr long long STREAM_NT_MIN = 16ll << 20;
+
+__device__ __forceinline__ void store_f4(float* p, float4 v, bool nt) {
+    if (nt)
+        __builtin_nontemporal_store(f4{v.x, v.y, v.z, v.w}, reinterpret_cast<f4*>(p));
+    else
+        *reinterpret_cast<float4*>(p) = v;
+}
+
 // BinaryOp (cuda.rs:3-10) applied as one rounded f32 operation
 // (elementwise.rs:5-13).
 enum BinOp { OP_ADD = 0, OP_SUB = 1, OP_MUL = 2, OP_DIV = 3 };

@@ -138,6 +138,7 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
     // kernels, whose grid is capped at one workgroup per CU).  Wider
     // workgroups would not leave the registers for it.
     constexpr bool PREFETCH = PARTIALS && WAVES <= 8;
+    const bool nt = (long long)a.rows * cols >= STREAM_NT_MIN;
     const int stride = gridDim.x * WAVES;
     int row = blockIdx.x * WAVES + wave;
     float4 nv[PREFETCH ? VPT : 1], ng[(PREFETCH && BWD) ? VPT : 1];
@@ -180,7 +181,7 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                 if (ok[i]) {
                     float4 o;
                     F4_APPLY(o, v[i], v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv);
-                    *reinterpret_cast<float4*>(a.y + base + (i * 64 + lane) * 4) = o;
+                    store_f4(a.y + base + (i * 64 + lane) * 4, o, nt);
                 }
             }
         } else if constexpr (OP == ROW_LAYER_NORM || OP == ROW_LAYER_NORM_BWD) {
@@ -217,7 +218,7 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                         const float4 b4 = beta4(i);
                         F4_APPLY(o, o, o.x + b4.x, o.y + b4.y, o.z + b4.z, o.w + b4.w);
                     }
-                    *reinterpret_cast<float4*>(a.y + base + c) = o;
+                    store_f4(a.y + base + c, o, nt);
                 }
             } else {
                 // row.rs:302-346: A = sum g, B = sum g*xhat,
@@ -260,7 +261,7 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                              scale * (n * gg.y - sa - xh.y * sb),
                              scale * (n * gg.z - sa - xh.z * sb),
                              scale * (n * gg.w - sa - xh.w * sb));
-                    *reinterpret_cast<float4*>(a.y + base + c) = o;
+                    store_f4(a.y + base + c, o, nt);
                     if constexpr (PARTIALS) {
                         pg[i].x += g[i].x * xh.x; pg[i].y += g[i].y * xh.y;
                         pg[i].z += g[i].z * xh.z; pg[i].w += g[i].w * xh.w;
@@ -286,7 +287,7 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                     const float4 gm = gamma4(i);
                     F4_APPLY(o, o, o.x * gm.x, o.y * gm.y, o.z * gm.z, o.w * gm.w);
                 }
-                *reinterpret_cast<float4*>(a.y + base + c) = o;
+                store_f4(a.y + base + c, o, nt);
             }
         } else if constexpr (OP == ROW_SOFTMAX_BWD) {
             // row.rs:216-236: s = sum p*g; dx = p * (g - s).
@@ -303,7 +304,7 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                          v[i].z * (g[i].z - s), v[i].w * (g[i].w - s));
                 if (a.scale != 1.0f)
                     F4_APPLY(o, o, o.x * a.scale, o.y * a.scale, o.z * a.scale, o.w * a.scale);
-                *reinterpret_cast<float4*>(a.y + base + (i * 64 + lane) * 4) = o;
+                store_f4(a.y + base + (i * 64 + lane) * 4, o, nt);
             }
         } else if constexpr (OP == ROW_RMS_NORM_BWD) {
             // row.rs:416-467: inv = 1/sqrt(q/n + eps), c = d/n*inv^3,
@@ -339,7 +340,7 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                 float4 o;
                 F4_APPLY(o, v[i], gg.x * inv - v[i].x * corr, gg.y * inv - v[i].y * corr,
                          gg.z * inv - v[i].z * corr, gg.w * inv - v[i].w * corr);
-                *reinterpret_cast<float4*>(a.y + base + c) = o;
+                store_f4(a.y + base + c, o, nt);
                 if constexpr (PARTIALS) {
                     pg[i].x += g[i].x * (v[i].x * inv); pg[i].y += g[i].y * (v[i].y * inv);
                     pg[i].z += g[i].z * (v[i].z * inv); pg[i].w += g[i].w * (v[i].w * inv);

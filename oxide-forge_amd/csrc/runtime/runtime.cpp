@@ -202,12 +202,8 @@ unsigned grid_for(long long work_items, long long per_block, unsigned cap) {
 }
 
 // Grid of the vectorised streaming kernels (elementwise.hpp stream_f4) for
-// n4 float4 items: one item per thread below 4M items (64 MiB), four per
-// thread above, at most 8192 workgroups (grid-stride beyond).
-unsigned stream_grid(long long n4) {
-    const long long per_block = n4 < (4ll << 20) ? EW_THREADS : EW_THREADS * 4;
-    return grid_for(n4, per_block, 8192);
-}
+// n4 float4 items: one item per thread.
+unsigned stream_grid(long long n4) { return grid_for(n4, EW_THREADS, 1u << 30); }
 
 std::string default_module_path() {
     if (const char* env = getenv("OXFORGE_KERNELS")) return env;
