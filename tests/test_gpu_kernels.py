@@ -288,9 +288,73 @@ def test_row_ops_unaligned_views(rt):
     assert np.max(np.abs(v.numpy() - orc.softmax_rows(x[1:].reshape(12, 40)))) <= TOL_ROW
 
 
+# Outputs of 16M floats (64 MiB) and more are stored non-temporally; the
+# shapes above stay below that, these two tests cover the other path.
+NT_ROWS, NT_COLS = 16384, 1024
+
+
+@pytest.mark.parametrize("affine", [False, True])
+def test_row_kernels_at_nontemporal_size(rt, affine):
+    rows, cols = NT_ROWS, NT_COLS
+    say(f"row kernels {rows}x{cols} affine={affine}")
+    x, dy = orc.normal((rows, cols), 21), orc.normal((rows, cols), 22)
+    gam = orc.normal((cols,), 23, 1.0, 0.1) if affine else None
+    bet = orc.normal((cols,), 24, 0.0, 0.1) if affine else None
+    dgam = rt.array(gam) if affine else None
+    dbet = rt.array(bet) if affine else None
+    col_tol = TOL_ROW * np.sqrt(rows)
+    d = rt.array(x)
+    rt.softmax_rows(d, rows, cols)
+    p = d.numpy()
+    assert np.max(np.abs(p - orc.softmax_rows(x))) <= TOL_ROW
+    dp, dg, dd = rt.array(p), rt.array(dy), rt.empty((rows, cols))
+    rt.softmax_rows_bwd(dp, dg, dd, rows, cols)
+    assert np.max(np.abs(dd.numpy() - orc.softmax_rows_backward(p, dy))) <= TOL_ROW
+    d = rt.array(x)
+    rt.layer_norm(d, rows, cols, gamma=dgam, beta=dbet)
+    assert np.max(np.abs(d.numpy() - orc.layer_norm(x, gam, bet))) <= TOL_ROW
+    dX, dDY, dDX = rt.array(x), rt.array(dy), rt.empty((rows, cols))
+    pg, pb = rt.empty((cols,)), rt.empty((cols,))
+    rt.layer_norm_bwd(dX, dDY, dDX, rows, cols, gamma=dgam, dgamma=pg, dbeta=pb)
+    rdx, rdg, rdb = orc.layer_norm_backward(x, dy, gam, want_params=True)
+    assert np.max(np.abs(dDX.numpy() - rdx)) <= TOL_ROW
+    assert np.max(np.abs(pg.numpy() - rdg)) <= col_tol
+    assert np.max(np.abs(pb.numpy() - rdb)) <= col_tol
+    d = rt.array(x)
+    rt.rms_norm(d, rows, cols, gamma=dgam)
+    assert np.max(np.abs(d.numpy() - orc.rms_norm(x, gam))) <= TOL_ROW
+    rt.rms_norm_bwd(dX, dDY, dDX, rows, cols, gamma=dgam, dgamma=pg)
+    rdx, rdg = orc.rms_norm_backward(x, dy, gam, want_params=True)
+    assert np.max(np.abs(dDX.numpy() - rdx)) <= TOL_ROW
+    assert np.max(np.abs(pg.numpy() - rdg)) <= col_tol
+
+
 # ------------------------------------------------------------ elementwise
 OPS = [(oxforge.ADD, np.add), (oxforge.SUB, np.subtract), (oxforge.MUL, np.multiply),
        (oxforge.DIV, np.divide)]
+
+
+def test_streaming_kernels_at_nontemporal_size(rt):
+    """Binary ops, maps, SGD and the row broadcast stay bit-exact on the
+    non-temporal store path."""
+    rows, cols = NT_ROWS, NT_COLS
+    n = rows * cols
+    say(f"streaming kernels n={n}")
+    a, b = orc.normal((n,), 11), orc.normal((n,), 12)
+    da, db, do = rt.array(a), rt.array(b), rt.empty((n,))
+    rt.binary(da, db, do, oxforge.ADD)
+    assert np.array_equal(do.numpy(), a + b)
+    rt.binary_assign(da, db, oxforge.MUL)
+    assert np.array_equal(da.numpy(), a * b)
+    rt.map(db, oxforge.MAP_SCALE, 0.37)
+    assert np.array_equal(db.numpy(), np.float32(0.37) * b)
+    dp, dgr = rt.array(a), rt.array(b)
+    rt.sgd_update(dp, dgr, 0.01)
+    assert np.array_equal(dp.numpy(), a - np.float32(0.01) * b)
+    row = orc.normal((cols,), 13)
+    dm = rt.array(a.reshape(rows, cols))
+    rt.binary_assign_by_rows(dm, rt.array(row), rows, cols, oxforge.ADD)
+    assert np.array_equal(dm.numpy(), a.reshape(rows, cols) + row[None, :])
 
 
 @pytest.mark.parametrize("op,fn", OPS)
