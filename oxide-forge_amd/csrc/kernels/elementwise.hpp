@@ -351,6 +351,59 @@ __device__ __forceinline__ void sum_cols_final_body(const float* __restrict__ m,
     }
 }
 
+// The same final pass for 16-byte aligned float4 columns.  A workgroup of
+// 256 threads owns 16 columns (four float4 groups q); thread t = 4 s + q
+// sums rows s, s + 64, s + 128, ... of group q with four rows' loads in
+// flight, then the 64 row-slot sums of each group are added in LDS by a
+// fixed tree.  The order depends only on the shape.  With the short
+// matrices this pass sees (the first pass's or the norm backward's partial
+// rows, at most a few hundred) a launch is mostly load latency: one round
+// of loads per 256 rows on 4 x more workgroups than the scalar pass.
+constexpr int SUMCOL_FINAL_V_THREADS = 256;
+constexpr int SUMCOL_FINAL_V_COLS = 16;
+
+__device__ __forceinline__ void sum_cols_final_v_body(const float* __restrict__ m,
+                                                      float* __restrict__ out, int rows,
+                                                      int cols) {
+    constexpr int SLOTS = SUMCOL_FINAL_V_THREADS / 4;
+    __shared__ float4 part[SLOTS][4];
+    const int q = threadIdx.x & 3, s = threadIdx.x >> 2;
+    const int c = blockIdx.x * SUMCOL_FINAL_V_COLS + 4 * q;
+    const bool in = c < cols;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (in) {
+        const float* p = m + c;
+        int r = s;
+        for (; r + 3 * SLOTS < rows; r += 4 * SLOTS) {
+            float4 u[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                u[j] = *reinterpret_cast<const float4*>(p + (long long)(r + j * SLOTS) * cols);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                acc.x += u[j].x; acc.y += u[j].y; acc.z += u[j].z; acc.w += u[j].w;
+            }
+        }
+        for (; r < rows; r += SLOTS) {
+            const float4 u = *reinterpret_cast<const float4*>(p + (long long)r * cols);
+            acc.x += u.x; acc.y += u.y; acc.z += u.z; acc.w += u.w;
+        }
+    }
+    part[s][q] = acc;
+    __syncthreads();
+#pragma unroll
+    for (int st = SLOTS / 2; st > 0; st >>= 1) {
+        if (s < st) {
+            const float4 u = part[s + st][q];
+            float4 t = part[s][q];
+            t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+            part[s][q] = t;
+        }
+        __syncthreads();
+    }
+    if (s == 0 && in) *reinterpret_cast<float4*>(out + c) = part[0][q];
+}
+
 // Row sums: one wave per row (row.rs:16-53).
 template <bool VEC>
 __device__ __forceinline__ void sum_rows_body(const float* __restrict__ m,

@@ -209,6 +209,15 @@ FORGE_KERNEL void __launch_bounds__(SUMCOL_FINAL_WAVES * 64) forge_sum_cols_fina
     if (blockIdx.y == 0) sum_cols_final_body(m0, out0, rows, cols);
     else sum_cols_final_body(m1, out1, rows, cols);
 }
+FORGE_KERNEL void __launch_bounds__(SUMCOL_FINAL_V_THREADS) forge_sum_cols_final_v(
+    const float* m, float* out, int rows, int cols) {
+    sum_cols_final_v_body(m, out, rows, cols);
+}
+FORGE_KERNEL void __launch_bounds__(SUMCOL_FINAL_V_THREADS) forge_sum_cols_final2_v(
+    const float* m0, float* out0, const float* m1, float* out1, int rows, int cols) {
+    if (blockIdx.y == 0) sum_cols_final_v_body(m0, out0, rows, cols);
+    else sum_cols_final_v_body(m1, out1, rows, cols);
+}
 FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_sum_rows_v(const float* m, float* out, int rows,
                                                                  int cols) {
     sum_rows_body<true>(m, out, rows, cols);

@@ -850,6 +850,8 @@ int row_vpt(size_t cols, bool aligned) {
 // forge_sum_cols_final.  The chunking depends only on the shape, so the
 // result is deterministic.
 constexpr int SUMCOL_FINAL_MAX_ROWS = 512;
+constexpr int SUMCOL_FINAL_V_THREADS = 256;  // elementwise.hpp SUMCOL_FINAL_V_THREADS
+constexpr int SUMCOL_FINAL_V_COLS = 16;      // elementwise.hpp SUMCOL_FINAL_V_COLS
 
 size_t sum_cols_chunks(size_t rows, size_t cols, bool vec) {
     if (rows <= (size_t)SUMCOL_FINAL_MAX_ROWS) return 1;
@@ -870,27 +872,37 @@ size_t sum_cols_scratch(size_t rows, size_t cols) {
     return c > 1 ? c * cols : 0;
 }
 
+// Final column-sum pass over a matrix of at most SUMCOL_FINAL_MAX_ROWS rows:
+// float4 columns when m and out are 16-byte aligned and cols % 4 == 0.
+bool sum_cols_final_vec(const float* m, const float* out, int cols) {
+    return aligned16(m) && aligned16(out) && cols % 4 == 0;
+}
+
+forge_status sum_cols_final_launch(forge_runtime* rt, forge_stream* s, const float* m,
+                                   float* out, int rows, int cols) {
+    if (sum_cols_final_vec(m, out, cols))
+        return launch_args(rt, s, "forge_sum_cols_final_v",
+                           dim3((unsigned)((cols + SUMCOL_FINAL_V_COLS - 1) / SUMCOL_FINAL_V_COLS)),
+                           dim3(SUMCOL_FINAL_V_THREADS), 0, m, out, rows, cols);
+    return launch_args(rt, s, "forge_sum_cols_final", dim3((unsigned)((cols + 63) / 64)),
+                       dim3(1024), 0, m, out, rows, cols);
+}
+
 // scratch: sum_cols_scratch(rows, cols) floats that do not overlap m/out.
 forge_status sum_cols_impl(forge_runtime* rt, forge_stream* s, const float* m, float* out,
                            size_t rows, size_t cols, float* scratch) {
     if (cols == 0) return FORGE_OK;
     int c = (int)cols;
-    unsigned gfinal = (unsigned)((cols + 63) / 64);
     const bool vec = sum_cols_vec(m, cols);
     size_t chunks = sum_cols_chunks(rows, cols, vec);
-    if (chunks == 1) {
-        int r = (int)rows;
-        return launch_args(rt, s, "forge_sum_cols_final", dim3(gfinal), dim3(1024), 0, m, out, r, c);
-    }
+    if (chunks == 1) return sum_cols_final_launch(rt, s, m, out, (int)rows, c);
     int rpc = (int)((rows + chunks - 1) / chunks);
     chunks = (rows + rpc - 1) / rpc;
     int r = (int)rows;
     unsigned gx = (unsigned)((cols + (vec ? 255 : 63)) / (vec ? 256 : 64));
     FORGE_TRY(launch_args(rt, s, vec ? "forge_sum_cols_v" : "forge_sum_cols_s",
                           dim3(gx, (unsigned)chunks), dim3(256), 0, m, scratch, r, c, rpc));
-    int ch = (int)chunks;
-    return launch_args(rt, s, "forge_sum_cols_final", dim3(gfinal), dim3(1024), 0,
-                       (const float*)scratch, out, ch, c);
+    return sum_cols_final_launch(rt, s, scratch, out, (int)chunks, c);
 }
 
 
@@ -954,6 +966,11 @@ forge_status row_launch(forge_runtime* rt, forge_stream* s, const char* op, RowA
     if (dgamma && dbeta && sum_cols_chunks(prow, (size_t)a.cols, true) == 1) {
         // Both column sums fit one final pass: one launch for the pair.
         int r = (int)prow, c = a.cols;
+        if (sum_cols_final_vec(a.pgamma, dgamma, c) && sum_cols_final_vec(a.pbeta, dbeta, c))
+            return launch_args(rt, s, "forge_sum_cols_final2_v",
+                               dim3((unsigned)((c + SUMCOL_FINAL_V_COLS - 1) / SUMCOL_FINAL_V_COLS), 2),
+                               dim3(SUMCOL_FINAL_V_THREADS), 0, (const float*)a.pgamma, dgamma,
+                               (const float*)a.pbeta, dbeta, r, c);
         unsigned gfinal = (unsigned)((a.cols + 63) / 64);
         return launch_args(rt, s, "forge_sum_cols_final2", dim3(gfinal, 2), dim3(1024), 0,
                            (const float*)a.pgamma, dgamma, (const float*)a.pbeta, dbeta, r, c);

@@ -91,6 +91,7 @@ def dispatcher_kernel_names():
               "forge_count_neq", "forge_sgd_v", "forge_sgd_s"]
     names += ["forge_fill_v", "forge_fill_s", "forge_fill_seq", "forge_causal_mask",
               "forge_sum_cols_v", "forge_sum_cols_s", "forge_sum_cols_final", "forge_sum_cols_final2",
+              "forge_sum_cols_final_v", "forge_sum_cols_final2_v",
               "forge_sum_rows_v", "forge_sum_rows_s", "forge_reduce_sum", "forge_reduce_max",
               "forge_transpose", "forge_transpose_w", "forge_transpose_g"]
     return names

@@ -288,6 +288,48 @@ def test_row_ops_unaligned_views(rt):
     assert np.max(np.abs(v.numpy() - orc.softmax_rows(x[1:].reshape(12, 40)))) <= TOL_ROW
 
 
+def test_norm_bwd_column_sums_across_launches(rt):
+    """dgamma / dbeta: per-workgroup partial rows, then one final column-sum
+    pass (float4 columns when the outputs are 16-byte aligned, scalar
+    otherwise).  Launches of different grids in a row, requests of dgamma or
+    dbeta alone and unaligned outputs must each match the oracle, and a
+    repeated launch must reproduce its result bit for bit."""
+    cols = 1024
+    gam_h = orc.normal((cols,), 31, 1.0, 0.1)
+    dgam = rt.array(gam_h)
+    for rows in (4096, 8, 100, 1600, 4096, 1, 2056):
+        say(f"norm bwd column sums rows={rows}")
+        x, dy = orc.normal((rows, cols), 32 + rows), orc.normal((rows, cols), 33 + rows)
+        dX, dDY, dDX = rt.array(x), rt.array(dy), rt.empty((rows, cols))
+        tol = TOL_ROW * max(1.0, np.sqrt(rows))
+        rdx, rdg, rdb = orc.layer_norm_backward(x, dy, gam_h, want_params=True)
+        runs = []
+        for _ in range(2):
+            pg, pb = rt.empty((cols,)), rt.empty((cols,))
+            rt.layer_norm_bwd(dX, dDY, dDX, rows, cols, gamma=dgam, dgamma=pg, dbeta=pb)
+            runs.append((pg.numpy(), pb.numpy()))
+        assert np.array_equal(runs[0][0], runs[1][0]) and np.array_equal(runs[0][1], runs[1][1])
+        assert np.max(np.abs(runs[0][0] - rdg)) <= tol
+        assert np.max(np.abs(runs[0][1] - rdb)) <= tol
+        assert np.max(np.abs(dDX.numpy() - rdx)) <= TOL_ROW
+        only_g, only_b = rt.empty((cols,)), rt.empty((cols,))
+        rt.layer_norm_bwd(dX, dDY, dDX, rows, cols, gamma=dgam, dgamma=only_g)
+        rt.layer_norm_bwd(dX, dDY, dDX, rows, cols, gamma=dgam, dbeta=only_b)
+        assert np.array_equal(only_g.numpy(), runs[0][0])
+        assert np.array_equal(only_b.numpy(), runs[0][1])
+        # dgamma / dbeta not 16-byte aligned: the separate column-sum pass.
+        ub = rt.empty((2 * cols + 2,))
+        ug, ubt = ub.view(1, (cols,)), ub.view(cols + 2, (cols,))
+        rt.layer_norm_bwd(dX, dDY, dDX, rows, cols, gamma=dgam, dgamma=ug, dbeta=ubt)
+        assert np.max(np.abs(ug.numpy() - rdg)) <= tol
+        assert np.max(np.abs(ubt.numpy() - rdb)) <= tol
+        rdx, rdg = orc.rms_norm_backward(x, dy, gam_h, want_params=True)
+        rg = rt.empty((cols,))
+        rt.rms_norm_bwd(dX, dDY, dDX, rows, cols, gamma=dgam, dgamma=rg)
+        assert np.max(np.abs(rg.numpy() - rdg)) <= tol
+        assert np.max(np.abs(dDX.numpy() - rdx)) <= TOL_ROW
+
+
 # Outputs of 16M floats (64 MiB) and more are stored non-temporally; the
 # shapes above stay below that, these two tests cover the other path.
 NT_ROWS, NT_COLS = 16384, 1024
@@ -412,8 +454,11 @@ def test_maps(rt, op, p0):
 
 # Column sums take one pass up to 512 rows and two passes above: (512, 64)
 # and (513, 64) sit on either side, (600, 33) is the unaligned two-pass path.
+# The final pass reads float4 columns, 16 per workgroup, when cols % 4 == 0:
+# (200, 36), (70, 1000) and (257, 20) leave a partial last workgroup.
 @pytest.mark.parametrize("rows,cols", [(4096, 1024), (3, 7), (300, 33), (600, 33), (512, 64),
-                                       (513, 64), (1, 1), (4096, 8192)])
+                                       (513, 64), (1, 1), (4096, 8192), (200, 36), (70, 1000),
+                                       (257, 20), (1, 4)])
 def test_sum_rows_cols(rt, rows, cols):
     say(f"sum rows/cols {rows}x{cols}")
     m = np.random.default_rng(rows).integers(-50, 51, (rows, cols)).astype(np.float32)
