@@ -104,26 +104,33 @@ enum Act { ACT_IDENTITY = 0, ACT_GELU = 1, ACT_RELU = 2, ACT_SILU = 3 };
 
 // GELU in the tanh form of linear.rs:26-43, 0.5 x (1 + tanh(u)) with
 // u = GELU_SCALE (x + GELU_CUBIC x^3), evaluated through the identity
-// 0.5 (1 + tanh(u)) = s = 1 / (1 + exp(-2u)): the hardware exponential
-// (__expf: v_exp_f32 of the argument times log2 e) and the hardware
-// reciprocal instead of tanhf, which makes the activation epilogue of the
-// GEMM several times cheaper; the identity also avoids tanh's cancellation
-// in 1 + tanh(u) for negative u.  __expf's error grows with the argument
-// (the rounding of 2u log2 e), but where it matters e is large and the
-// result x / (1 + e) is tiny: within 2e-6 (relative, plus 2e-6 absolute) of
-// the f64 formula over x ~ N(0, 2) and at the extremes (x = +-inf give the
-// reference's inf and NaN).
+// 0.5 (1 + tanh(u)) = s = 1 / (1 + exp(-2u)) = 1 / (1 + 2^t),
+// t = -2 log2(e) u = x (GELU_T1 + GELU_T3 x^2): the hardware base-2
+// exponential (v_exp_f32) and reciprocal instead of tanhf.  The two
+// constants fold -2 log2(e) into the reference's f32 constants (computed in
+// double, rounded once), so the exponent takes four operations instead of
+// seven; the activation epilogue of the GEMM is several times cheaper than
+// with tanhf, and the identity avoids tanh's cancellation in 1 + tanh(u) for
+// negative u.  The error of 2^t grows with |t|, but where it matters 2^t is
+// large and the result x / (1 + 2^t) is tiny: within 2e-6 (relative, plus
+// 2e-6 absolute) of the f64 formula over x ~ N(0, 2) and at the extremes
+// (x = +-inf give the reference's inf and NaN).
+constexpr float GELU_T1 = -2.302208185195923f;   // -2 log2(e) GELU_SCALE
+constexpr float GELU_T3 = -0.10294323414564133f; // GELU_T1 GELU_CUBIC
+
+__device__ __forceinline__ float gelu_exp2_arg(float x) {
+    return x * (GELU_T1 + GELU_T3 * (x * x));
+}
+
 __device__ __forceinline__ float gelu(float x) {
-    const float u = GELU_SCALE * (x + GELU_CUBIC * x * x * x);
-    const float e = __expf(-2.0f * u);
+    const float e = __builtin_amdgcn_exp2f(gelu_exp2_arg(x));
     return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 // d/dx of the above: 0.5 (1 + t) + 0.5 x (1 - t^2) u' with t = tanh(u)
 // becomes s + 2 x s (1 - s) u', and 1 - s = e s (1 where e overflows).
 __device__ __forceinline__ float gelu_derivative(float x) {
-    const float u = GELU_SCALE * (x + GELU_CUBIC * x * x * x);
-    const float e = __expf(-2.0f * u);
+    const float e = __builtin_amdgcn_exp2f(gelu_exp2_arg(x));
     const float s = __builtin_amdgcn_rcpf(1.0f + e);
     const float one_minus_s = __builtin_isinf(e) ? 1.0f : e * s;
     const float inner_derivative = GELU_SCALE + GELU_DERIVATIVE_QUADRATIC * x * x;

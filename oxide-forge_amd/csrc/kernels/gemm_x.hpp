@@ -247,43 +247,112 @@ __device__ __forceinline__ void x_epi_load(const GemmArgs& p, long long idx, f4&
     }
 }
 
-template <bool EPI>
-__device__ __forceinline__ void x_epi_store(const GemmArgs& p, f4 z, f4 res, f4 mul, f4 old,
-                                            int col, long long idx) {
-    float y[4] = {z.x, z.y, z.z, z.w};
+// The fused steps of NB groups at once.  bias: this lane's four bias values
+// (its columns are the same in every group, so they are loaded once per
+// tile).  Each choice of step (activation, derivative) is made once for the
+// NB groups rather than per element, so the arithmetic of all 4 NB values
+// is one straight run of instructions.
+template <int NB>
+__device__ __forceinline__ void x_epi_apply(int act, float (&y)[4 * NB]) {
+    switch (act) {
+    case ACT_GELU:
+#pragma unroll
+        for (int i = 0; i < 4 * NB; i++) y[i] = gelu(y[i]);
+        break;
+    case ACT_RELU:
+#pragma unroll
+        for (int i = 0; i < 4 * NB; i++) y[i] = relu(y[i]);
+        break;
+    case ACT_SILU:
+#pragma unroll
+        for (int i = 0; i < 4 * NB; i++) y[i] = silu(y[i]);
+        break;
+    default:
+        break;
+    }
+}
+
+template <int NB>
+__device__ __forceinline__ void x_epi_aux(int aux_act, float (&y)[4 * NB],
+                                          const float (&m)[4 * NB]) {
+    switch (aux_act) {
+    case ACT_IDENTITY:
+#pragma unroll
+        for (int i = 0; i < 4 * NB; i++) y[i] = y[i] * m[i];
+        break;
+    case ACT_GELU:
+#pragma unroll
+        for (int i = 0; i < 4 * NB; i++) y[i] = y[i] * gelu_derivative(m[i]);
+        break;
+    case ACT_RELU:
+#pragma unroll
+        for (int i = 0; i < 4 * NB; i++) y[i] = y[i] * relu_derivative(m[i]);
+        break;
+    case ACT_SILU:
+#pragma unroll
+        for (int i = 0; i < 4 * NB; i++) y[i] = y[i] * silu_derivative(m[i]);
+        break;
+    default:
+#pragma unroll
+        for (int i = 0; i < 4 * NB; i++) y[i] = y[i] * activate_derivative(aux_act, m[i]);
+        break;
+    }
+}
+
+template <bool EPI, int NB>
+__device__ __forceinline__ void x_epi_store(const GemmArgs& p, const f4 (&z)[NB],
+                                            const f4 (&res)[NB], const f4 (&mul)[NB],
+                                            const f4 (&old)[NB], f4 bias,
+                                            const long long (&idx)[NB]) {
+    float y[4 * NB];
+#pragma unroll
+    for (int u = 0; u < NB; u++) {
+        y[4 * u + 0] = z[u].x; y[4 * u + 1] = z[u].y;
+        y[4 * u + 2] = z[u].z; y[4 * u + 3] = z[u].w;
+    }
     if constexpr (EPI) {
         if (p.alpha != 1.0f)
 #pragma unroll
-            for (int e = 0; e < 4; e++) y[e] = p.alpha * y[e];
-        if (p.bias) {
-            const f4 v = *reinterpret_cast<const f4*>(p.bias + col);
-            y[0] = y[0] + v.x; y[1] = y[1] + v.y; y[2] = y[2] + v.z; y[3] = y[3] + v.w;
-        }
-        if (p.residual) {
-            y[0] = y[0] + res.x; y[1] = y[1] + res.y; y[2] = y[2] + res.z; y[3] = y[3] + res.w;
-        }
-        if (p.aux) {
-            const float m[4] = {mul.x, mul.y, mul.z, mul.w};
-            if (p.aux_act) {
+            for (int i = 0; i < 4 * NB; i++) y[i] = p.alpha * y[i];
+        if (p.bias)
 #pragma unroll
-                for (int e = 0; e < 4; e++) y[e] = y[e] * activate_derivative(p.aux_act, m[e]);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; e++) y[e] = y[e] * m[e];
+            for (int u = 0; u < NB; u++) {
+                y[4 * u + 0] = y[4 * u + 0] + bias.x; y[4 * u + 1] = y[4 * u + 1] + bias.y;
+                y[4 * u + 2] = y[4 * u + 2] + bias.z; y[4 * u + 3] = y[4 * u + 3] + bias.w;
             }
-        }
-        if (p.pre_out) *reinterpret_cast<f4*>(p.pre_out + idx) = f4{y[0], y[1], y[2], y[3]};
-        if (p.act != ACT_IDENTITY)
+        if (p.residual)
 #pragma unroll
-            for (int e = 0; e < 4; e++) y[e] = activate(p.act, y[e]);
-        if (p.update) {
-            y[0] = old.x - p.update_scale * y[0];
-            y[1] = old.y - p.update_scale * y[1];
-            y[2] = old.z - p.update_scale * y[2];
-            y[3] = old.w - p.update_scale * y[3];
+            for (int u = 0; u < NB; u++) {
+                y[4 * u + 0] = y[4 * u + 0] + res[u].x; y[4 * u + 1] = y[4 * u + 1] + res[u].y;
+                y[4 * u + 2] = y[4 * u + 2] + res[u].z; y[4 * u + 3] = y[4 * u + 3] + res[u].w;
+            }
+        if (p.aux) {
+            float m[4 * NB];
+#pragma unroll
+            for (int u = 0; u < NB; u++) {
+                m[4 * u + 0] = mul[u].x; m[4 * u + 1] = mul[u].y;
+                m[4 * u + 2] = mul[u].z; m[4 * u + 3] = mul[u].w;
+            }
+            x_epi_aux<NB>(p.aux_act, y, m);
         }
+        if (p.pre_out)
+#pragma unroll
+            for (int u = 0; u < NB; u++)
+                *reinterpret_cast<f4*>(p.pre_out + idx[u]) =
+                    f4{y[4 * u], y[4 * u + 1], y[4 * u + 2], y[4 * u + 3]};
+        if (p.act != ACT_IDENTITY) x_epi_apply<NB>(p.act, y);
+        if (p.update)
+#pragma unroll
+            for (int u = 0; u < NB; u++) {
+                y[4 * u + 0] = old[u].x - p.update_scale * y[4 * u + 0];
+                y[4 * u + 1] = old[u].y - p.update_scale * y[4 * u + 1];
+                y[4 * u + 2] = old[u].z - p.update_scale * y[4 * u + 2];
+                y[4 * u + 3] = old[u].w - p.update_scale * y[4 * u + 3];
+            }
     }
-    *reinterpret_cast<f4*>(p.C + idx) = f4{y[0], y[1], y[2], y[3]};
+#pragma unroll
+    for (int u = 0; u < NB; u++)
+        *reinterpret_cast<f4*>(p.C + idx[u]) = f4{y[4 * u], y[4 * u + 1], y[4 * u + 2], y[4 * u + 3]};
 }
 
 template <int BM, int BN, int BK, bool TA, bool TB, bool EPI>
@@ -455,6 +524,19 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     // No slab load may still be writing LDS when the workgroup ends.
     x_wait_vmcnt<0>();
 
+    // Epilogue columns of this lane: group q = lane + 64 k of a TN-wide
+    // sub-tile row covers columns 4 (q % F4_ROW) onwards, and F4_ROW divides
+    // 64, so every group of the lane has the same four columns.  Their bias
+    // is loaded here, while the accumulators go through LDS.
+    constexpr int F4_ROW = TN / 4;
+    static_assert(64 % F4_ROW == 0, "a lane's epilogue columns repeat every group");
+    const int row0 = m0 + a_off, col0 = n0 + b_off;
+    const int lane_col = col0 + 4 * (lane % F4_ROW);
+    f4 bias4 = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (EPI) {
+        if (p.bias) bias4 = *reinterpret_cast<const f4*>(p.bias + lane_col);
+    }
+
     // Epilogue through LDS.  Each wave writes its accumulators as a plain
     // TM x TN sub-tile into its own LDS region (accumulator r of a 16x16
     // block is MFMA row 4 kq + r, column l16), then streams the sub-tile
@@ -489,8 +571,6 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
             }
     }
     asm volatile("" ::: "memory");
-    const int row0 = m0 + a_off, col0 = n0 + b_off;
-    constexpr int F4_ROW = TN / 4;
     constexpr int ITER = TM * F4_ROW / 64;  // 128-bit groups per lane
     constexpr int NB = ITER < 4 ? ITER : 4;  // groups whose operands load together
     static_assert(ITER % NB == 0, "epilogue batches");
@@ -500,19 +580,15 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
         // flight together.
         f4 z[NB], res[NB], mul[NB], old[NB];
         long long idx[NB];
-        int col[NB];
 #pragma unroll
         for (int u = 0; u < NB; u++) {
             const int q = lane + 64 * (b0 + u);
             const int rr = q / F4_ROW, c4 = q % F4_ROW;
             z[u] = *reinterpret_cast<const f4*>(cw + rr * CP + 4 * c4);
-            col[u] = col0 + 4 * c4;
-            idx[u] = (long long)(row0 + rr) * p.ldc + col[u];
+            idx[u] = (long long)(row0 + rr) * p.ldc + lane_col;
             x_epi_load<EPI>(p, idx[u], res[u], mul[u], old[u]);
         }
-#pragma unroll
-        for (int u = 0; u < NB; u++)
-            x_epi_store<EPI>(p, z[u], res[u], mul[u], old[u], col[u], idx[u]);
+        x_epi_store<EPI, NB>(p, z, res, mul, old, bias4, idx);
     }
 }
 
