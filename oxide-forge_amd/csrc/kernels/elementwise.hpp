@@ -415,12 +415,16 @@ __device__ __forceinline__ void sum_rows_body(const float* __restrict__ m,
     for (int r = blockIdx.x * waves + wave; r < rows; r += gridDim.x * waves) {
         const float* p = m + (long long)r * cols;
         float s = 0.0f;
+        // Unrolled so that four loads per lane are in flight; the sum is
+        // still taken in column order.
         if constexpr (VEC) {
+#pragma unroll 4
             for (int c4 = lane; c4 < cols / 4; c4 += 64) {
-                const float4 a = reinterpret_cast<const float4*>(p)[c4];
+                const float4 a = load_stream(p + 4 * c4);
                 s += (a.x + a.y) + (a.z + a.w);
             }
         } else {
+#pragma unroll 4
             for (int c = lane; c < cols; c += 64) s += p[c];
         }
         s = wave_sum(s);
