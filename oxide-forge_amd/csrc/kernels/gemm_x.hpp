@@ -78,14 +78,14 @@ __device__ __forceinline__ int x_swz(int row) {
     return 0;
 }
 
-template <int ROWS, int COLS, bool SWZ>
+template <int ROWS, int COLS, bool SWZ, int NW = 4>
 struct XSlab {
     static constexpr int P = COLS / 4;
     static constexpr int RPI = 64 / P;          // rows per wave instruction
     static constexpr int INSTR = ROWS * P / 64;  // wave instructions per slab
-    static constexpr int PER_WAVE = INSTR / 4;
+    static constexpr int PER_WAVE = INSTR / NW;
     static_assert(P <= 64 && 64 % P == 0, "a wave instruction fills whole rows");
-    static_assert(INSTR % 4 == 0, "slab must split evenly over four waves");
+    static_assert(INSTR % NW == 0, "slab must split evenly over the waves");
 };
 
 // Slab loads of one operand (buffer_load_dwordx4 ... lds).  A lane's byte
@@ -99,9 +99,9 @@ struct XSlab {
 // several cycles, scalar ones do not.  Row pitches up to 2^21 floats keep
 // the offsets (at most 256 rows into the slab) below 2^31 bytes; the host
 // sends larger ones to the guarded kernel.
-template <int ROWS, int COLS, bool SWZ>
+template <int ROWS, int COLS, bool SWZ, int NW = 4>
 struct XDma {
-    using S = XSlab<ROWS, COLS, SWZ>;
+    using S = XSlab<ROWS, COLS, SWZ, NW>;
     unsigned off[S::PER_WAVE];
 
     __device__ __forceinline__ void init(long long ld, int wave, int lane) {
@@ -355,9 +355,10 @@ __device__ __forceinline__ void x_epi_store(const GemmArgs& p, const f4 (&z)[NB]
         *reinterpret_cast<f4*>(p.C + idx[u]) = f4{y[4 * u], y[4 * u + 1], y[4 * u + 2], y[4 * u + 3]};
 }
 
-template <int BM, int BN, int BK, bool TA, bool TB, bool EPI>
+template <int BM, int BN, int BK, bool TA, bool TB, bool EPI, int WM = 2, int WN = 2>
 __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
-    constexpr int TM = BM / 2, TN = BN / 2;
+    constexpr int NW = WM * WN;  // waves: WM x WN sub-tiles of TM x TN
+    constexpr int TM = BM / WM, TN = BN / WN;
     constexpr int FM = TM / 16, FN = TN / 16;
     constexpr int CH = BK / 16;
     static_assert(TM % 16 == 0 && TN % 16 == 0 && BK % 16 == 0, "tile shape");
@@ -368,14 +369,14 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     constexpr int A_ELEMS = A_ROWS * A_COLS;
     constexpr int B_ELEMS = B_ROWS * B_COLS;
     constexpr int STAGE = A_ELEMS + B_ELEMS;
-    using SA = XSlab<A_ROWS, A_COLS, A_KC>;
-    using SB = XSlab<B_ROWS, B_COLS, B_KC>;
+    using SA = XSlab<A_ROWS, A_COLS, A_KC, NW>;
+    using SB = XSlab<B_ROWS, B_COLS, B_KC, NW>;
     constexpr int DMA_PER_STAGE = SA::PER_WAVE + SB::PER_WAVE;
     static_assert(CH % 2 == 0, "slabs hold an even number of 16-wide chunks");
     // The two slab stages, reused by the epilogue for each wave's TM x TN
     // sub-tile of C (row pitch CP).
     constexpr int CP = TN + 4;
-    constexpr int EPI_ELEMS = 4 * TM * CP;
+    constexpr int EPI_ELEMS = NW * TM * CP;
     constexpr int SMEM = 2 * STAGE > EPI_ELEMS ? 2 * STAGE : EPI_ELEMS;
     static_assert(SMEM * 4 <= 160 * 1024, "LDS budget");
     __shared__ __attribute__((aligned(1024))) float smem_all[SMEM];
@@ -387,7 +388,7 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // scalar
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
     const int l16 = lane & 15, kq = lane >> 4;
     float* const smem = smem_all;
 
@@ -408,8 +409,8 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     const int a_off = wm * TM, b_off = wn * TN;
     float fa[2][FM * 4], fb[2][FN * 4];
 
-    XDma<A_ROWS, A_COLS, A_KC> dma_a;
-    XDma<B_ROWS, B_COLS, B_KC> dma_b;
+    XDma<A_ROWS, A_COLS, A_KC, NW> dma_a;
+    XDma<B_ROWS, B_COLS, B_KC, NW> dma_b;
     dma_a.init(p.lda, wave, lane);
     dma_b.init(p.ldb, wave, lane);
     XFrag<A_KC, A_KC ? BK : BM, BK, FM> rd_a;
@@ -592,16 +593,16 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     }
 }
 
-template <int BM, int BN, int BK, bool TA, bool TB, bool EPI>
+template <int BM, int BN, int BK, bool TA, bool TB, bool EPI, int WM = 2, int WN = 2>
 __device__ __forceinline__ void gemm_single_x(const GemmArgs& p) {
-    gemm_body_x<BM, BN, BK, TA, TB, EPI>(p, xcd_logical(blockIdx.x, gridDim.x));
+    gemm_body_x<BM, BN, BK, TA, TB, EPI, WM, WN>(p, xcd_logical(blockIdx.x, gridDim.x));
 }
 
-template <int BM, int BN, int BK, bool TA, bool TB>
+template <int BM, int BN, int BK, bool TA, bool TB, int WM = 2, int WN = 2>
 __device__ __forceinline__ void gemm_batch_x(const GemmBatchArgs& b) {
     const int logical = xcd_logical(blockIdx.x, gridDim.x);
     const int z = logical / b.tiles;
-    gemm_body_x<BM, BN, BK, TA, TB, true>(b.p[z], logical - z * b.tiles);
+    gemm_body_x<BM, BN, BK, TA, TB, true, WM, WN>(b.p[z], logical - z * b.tiles);
 }
 
 }  // namespace forge

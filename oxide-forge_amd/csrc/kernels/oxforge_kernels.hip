@@ -71,6 +71,25 @@ FORGE_KERNEL void __launch_bounds__(SPLITK_THREADS) forge_gemm_splitk_reduce_s(c
     splitk_reduce_body<false>(P, splits, p);
 }
 
+// Eight-wave 64 x 128 tile (4 x 2 waves of 16 x 64): two waves per SIMD
+// where a product leaves one tile per CU.
+#define GEMM_X8_KERNEL(NAME, TA, TB, EPI)                                           \
+    FORGE_KERNEL void __launch_bounds__(512, 1) NAME(GemmArgs p) {                  \
+        gemm_single_x<64, 128, 32, TA, TB, EPI, 4, 2>(p);                          \
+    }
+GEMM_X8_KERNEL(forge_gemm_nn_64x128x32_x8, false, false, false)
+GEMM_X8_KERNEL(forge_gemm_nn_64x128x32_x8_e, false, false, true)
+GEMM_X8_KERNEL(forge_gemm_nt_64x128x32_x8_e, false, true, true)
+GEMM_X8_KERNEL(forge_gemm_tn_64x128x32_x8_e, true, false, true)
+GEMM_X8_KERNEL(forge_gemm_tt_64x128x32_x8_e, true, true, true)
+#define GEMM_X8_BATCH_KERNEL(NAME, TA, TB)                                            \
+    FORGE_KERNEL void __launch_bounds__(512, 1) NAME(GemmBatchArgs b) {               \
+        gemm_batch_x<64, 128, 32, TA, TB, 4, 2>(b);                                 \
+    }
+GEMM_X8_BATCH_KERNEL(forge_gemm_batch_nn_64x128x32_x8, false, false)
+GEMM_X8_BATCH_KERNEL(forge_gemm_batch_nt_64x128x32_x8, false, true)
+GEMM_X8_BATCH_KERNEL(forge_gemm_batch_tn_64x128x32_x8, true, false)
+
 // Plain C = A * B instances of forge_gemm_f32 (the headline GEMM).
 GEMM_X_KERNEL(forge_gemm_nn_128x256x32_x, 128, 256, 32, false, false, false)
 GEMM_X_KERNEL(forge_gemm_nn_128x128x32_x, 128, 128, 32, false, false, false)

@@ -553,6 +553,7 @@ const GemmConfig kTile128x128 = {"128x128x32_x", 128, 128, 32, 256};
 const GemmConfig kTile128x64 = {"128x64x32_x", 128, 64, 32, 256};
 const GemmConfig kTile64x128 = {"64x128x32_x", 64, 128, 32, 256};
 const GemmConfig kTile64x64 = {"64x64x32_x", 64, 64, 32, 256};
+const GemmConfig kTile64x128w8 = {"64x128x32_x8", 64, 128, 32, 512};
 const GemmConfig kGuard64 = {"64x64x16_2x2_g", 64, 64, 16, 256};
 
 // Unguarded tiles, largest first, and their measured efficiency relative to
@@ -561,9 +562,20 @@ const GemmConfig kGuard64 = {"64x64x16_2x2_g", 64, 64, 16, 256};
 // TFLOP/s for 128x128, 64x128 and 128x64 at two per CU, and 64x64).  All
 // but 128x256 have fused-epilogue and batched instances; 128x256 has a
 // plain NN one.
+// The eight-wave 64x128 tile (two waves per SIMD) serves plain products
+// (forge_gemm_f32): 4096^3 at 150.2-150.7 TFLOP/s against 149.6-149.8 for
+// 128x128 on one device, 8192x1024x4096 at 150.0 against 148.5.  Fused
+// products keep the four-wave tiles: although the eight-wave tile also ran
+// faster on most C4/C5 NN and NT products in isolation (2048x1024x4096 with
+// bias 143.9 against 141.6), the C4 forward was no faster with it (0.521 ms
+// both ways) and the C5 step 0.5% slower (11.54 against 11.48 ms); batched
+// Q/K/V lost 7% (98.3 against 92.0 us at C4), and TN products, whose
+// transposed A it reads 32 bits at a time (16-row wave sub-tiles), lost
+// 0.3-1%.
 const GemmConfig* const kUnguarded[] = {&kTile128x256, &kTile128x128, &kTile128x64,
-                                        &kTile64x128, &kTile64x64};
-const double kTileEfficiency[] = {0.975, 1.0, 0.98, 0.985, 0.94};
+                                        &kTile64x128, &kTile64x64, &kTile64x128w8};
+const double kTileEfficiency[] = {0.975, 1.0, 0.98, 0.985, 0.94, 1.005};
+constexpr int kUnguardedCount = 6;
 // A CU that holds a single four-wave workgroup has one wave per SIMD, which
 // hides less: 2048x2048x1024 as 256 tiles of 128x128 runs at 133 TFLOP/s,
 // as 512 tiles of 64x128 at 139.
@@ -626,11 +638,12 @@ struct GemmPlan {
 // balance t / (CUs * c * ceil(t / (CUs * c))).  The last of a wave's tiles
 // do not spread evenly over the CUs: 1024 tiles of 64x128 at three per CU
 // run at 120 TFLOP/s, at two per CU (exact waves) at 147.  A CU left with
-// a single four-wave workgroup scores kSingleWorkgroupFactor less.  Ties go
-// to the larger tile, then to the larger c.  Results on the C3-C5 shapes:
-// 4096^3, 8192x1024, 2048x4096 and the C5 products -> 128x128; 2048x2048
-// and 2048x1024 products -> 64x128 (the three C4 Q/K/V products of one
-// batch: 768 tiles at three per CU).  Unaligned shapes and shapes the
+// a single four-wave workgroup scores kSingleWorkgroupFactor less (an
+// eight-wave one does not: it has two waves per SIMD).  Ties go to the
+// larger tile, then to the larger c.  Results on the C3-C5 shapes: plain
+// 4096^3 and 8192x1024x4096 -> the eight-wave 64x128; fused 2048x4096 and
+// the C5 products -> 128x128; 2048x2048 and 2048x1024 products -> 64x128
+// (the three C4 Q/K/V products of one batch: 768 tiles at three per CU).  Unaligned shapes and shapes the
 // tiles do not divide take the bounds-guarded 64x64 tile.  `count`
 // same-shape products share the launch (kind Batch).
 GemmPlan choose_gemm(forge_runtime* rt, int ta, int tb, size_t M, size_t N, size_t K,
@@ -639,9 +652,10 @@ GemmPlan choose_gemm(forge_runtime* rt, int ta, int tb, size_t M, size_t N, size
     GemmPlan best{&kGuard64, 0};
     double best_score = 0.0;
     const bool plain_nn = kind == GemmKind::Plain && !ta && !tb;
-    for (int i = plain_nn ? 0 : 1; i < 5; i++) {
+    for (int i = plain_nn ? 0 : 1; i < kUnguardedCount; i++) {
         const GemmConfig& g = *kUnguarded[i];
         if (!aligned || M % g.bm || N % g.bn || K % (size_t)g.bk) continue;
+        if (&g == &kTile64x128w8 && kind != GemmKind::Plain) continue;
         char name[96];
         gemm_kernel_name(name, sizeof name, kind, ta, tb, g);
         const int occ = gemm_occupancy(rt, name, g.threads);
@@ -652,7 +666,8 @@ GemmPlan choose_gemm(forge_runtime* rt, int ta, int tb, size_t M, size_t N, size
             const double balance =
                 t <= slots ? (double)t / (double)(cus * per_cu)
                            : (double)t / (double)(slots * ((t + slots - 1) / slots));
-            const bool single = occ > 1 && (c == 1 || per_cu == 1);
+            // (an eight-wave workgroup alone on a CU still has two waves per SIMD)
+            const bool single = g.threads == 256 && occ > 1 && (c == 1 || per_cu == 1);
             const double score =
                 kTileEfficiency[i] * balance * (single ? kSingleWorkgroupFactor : 1.0);
             if (score > best_score + 1e-9) {
@@ -1026,7 +1041,7 @@ extern "C" forge_status forge_gemm_f32_tile(forge_runtime* rt, forge_stream* s,
     int cap = 0;
     FORGE_TRY(split_tile_tag(tile_tag_in, tile_tag, sizeof tile_tag, &cap));
     unsigned bm = 0, bn = 0, bk = 0;
-    const unsigned threads = 256;
+    unsigned threads = 256;
     bool guarded = false;
     char tail[8] = {0};
     if (sscanf(tile_tag, "%ux%ux%u_%7s", &bm, &bn, &bk, tail) != 4 || bm == 0 || bn == 0 ||
@@ -1034,6 +1049,8 @@ extern "C" forge_status forge_gemm_f32_tile(forge_runtime* rt, forge_stream* s,
         return fail(FORGE_EINVAL, "bad tile tag %s", tile_tag);
     if (strcmp(tail, "x") == 0) {
         // Four-wave instance <BM>x<BN>x<BK>_x.
+    } else if (strcmp(tail, "x8") == 0) {
+        threads = 512;  // eight-wave instance
     } else if (strcmp(tail, "2x2_g") == 0) {
         guarded = true;
     } else {

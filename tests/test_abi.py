@@ -72,6 +72,10 @@ def dispatcher_kernel_names():
     for ab in ("nn", "nt", "tn"):
         for tag in tiles:
             names.append(f"forge_gemm_batch_{ab}_{tag}")
+    # eight-wave 64x128 tile: plain NN, every epilogue kind, batched NN/NT/TN
+    names.append("forge_gemm_nn_64x128x32_x8")
+    names += [f"forge_gemm_{ab}_64x128x32_x8_e" for ab in ("nn", "nt", "tn", "tt")]
+    names += [f"forge_gemm_batch_{ab}_64x128x32_x8" for ab in ("nn", "nt", "tn")]
     names += ["forge_gemm_splitk_reduce_v", "forge_gemm_splitk_reduce_s"]
     for op in ("softmax", "layer_norm", "rms_norm", "softmax_bwd", "layer_norm_bwd", "rms_norm_bwd"):
         for v in (1, 2, 4, 8, 16):

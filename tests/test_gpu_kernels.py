@@ -592,7 +592,8 @@ def test_softmax_bwd_scaled_equals_bwd_then_scale(rt):
                                                ("128x64x32_x", 3, 128, 128, 192),
                                                ("128x128x32_x", 8, 128, 128, 256),
                                                ("64x64x32_x", 5, 128, 64, 320),
-                                               ("128x64x32_x", 1, 128, 64, 64)])
+                                               ("128x64x32_x", 1, 128, 64, 64),
+                                               ("64x128x32_x8", 3, 128, 256, 288)])
 def test_gemm_split_k_vs_oracle(rt, tile, splits, M, N, K):
     """K slices summed in slice order: the same bar as any GEMM; one slice is
     the plain product bit for bit."""
@@ -613,7 +614,8 @@ def test_gemm_split_k_vs_oracle(rt, tile, splits, M, N, K):
         rt.gemm_split(tile, splits, dA, dB, dC, M, N, K + 16 * splits + 8)
 
 
-TILES = ["128x128x32_x", "128x64x32_x", "64x128x32_x", "64x64x32_x", "64x64x16_2x2_g"]
+TILES = ["128x128x32_x", "128x64x32_x", "64x128x32_x", "64x64x32_x", "64x128x32_x8",
+         "64x64x16_2x2_g"]
 
 
 @pytest.mark.parametrize("tile", TILES)
@@ -645,7 +647,7 @@ def test_gemm_every_tile_instance(rt, tile, ta, tb):
     expect = rt.array(pre)
     rt.map(expect, oxforge.MAP_GELU, 0.0)
     assert np.array_equal(dY.numpy(), expect.numpy())
-    if tile.endswith("_x"):  # unguarded tiles refuse shapes they do not divide
+    if "_x" in tile:  # unguarded tiles refuse shapes they do not divide
         with pytest.raises(oxforge.ForgeError):
             rt.gemm_ex_tile(tile, dA, dB, dZ, M - 1, N, K, trans_a=ta, trans_b=tb)
 
@@ -682,7 +684,7 @@ def test_gemm_kernel_name_names_the_kernel_that_runs(rt, M, N, K, ta, tb, fused)
 
 
 @pytest.mark.parametrize("tile", ["64x128x32_x@2", "128x128x32_x@1", "64x64x32_x@3",
-                                  "128x64x32_x@2"])
+                                  "128x64x32_x@2", "64x128x32_x8@1"])
 def test_gemm_occupancy_cap_keeps_results(rt, tile):
     """A launch that lets a CU hold fewer workgroups computes the same
     product bit for bit, plain and with a fused epilogue; malformed caps are
