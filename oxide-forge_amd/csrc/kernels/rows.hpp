@@ -67,18 +67,36 @@ __device__ __forceinline__ float max4(float4 a) {
 // Loads row `row` into the register arrays of the register path (fill
 // values past cols: -FLT_MAX for softmax, 0 otherwise).  Streaming loads:
 // the forward kernels overwrite the row in place.
+// Row `row` into the register arrays of the register path, as loaded:
+// every lane loads (past cols it reloads the row's first float4), and
+// row_mask then puts the fill values (-FLT_MAX for softmax, 0 otherwise)
+// past cols.  The two steps are apart so that a prefetched row is masked
+// only when it is used: loads under a lane-mask branch, or a select right
+// after them, make the wave wait for the loads at once (and, with loads
+// under branches, for every memory operation in flight, its own stores of
+// the previous row included).  Streaming loads: the forward kernels
+// overwrite the row in place.
 template <int OP, int VPT, bool BWD>
 __device__ __forceinline__ void row_load(const RowArgs& a, int row, int lane, float4* v,
                                          float4* g) {
     const long long base = (long long)row * a.cols;
-    const float fill = (OP == ROW_SOFTMAX) ? -FLT_MAX : 0.0f;
 #pragma unroll
     for (int i = 0; i < VPT; i++) {
         const int c = (i * 64 + lane) * 4;
-        const bool ok = c < a.cols;
-        v[i] = ok ? load_stream(a.x + base + c) : make_float4(fill, fill, fill, fill);
+        const long long at = base + (c < a.cols ? c : 0);
+        v[i] = load_stream(a.x + at);
+        if constexpr (BWD) g[i] = load_stream(a.dy + at);
+    }
+}
+
+template <int OP, int VPT, bool BWD>
+__device__ __forceinline__ void row_mask(const bool* ok, float4* v, float4* g) {
+    const float fill = (OP == ROW_SOFTMAX) ? -FLT_MAX : 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; i++) {
+        if (!ok[i]) v[i] = make_float4(fill, fill, fill, fill);
         if constexpr (BWD)
-            g[i] = ok ? load_stream(a.dy + base + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (!ok[i]) g[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
 }
 
@@ -90,7 +108,7 @@ __device__ __forceinline__ void row_load(const RowArgs& a, int row, int lane, fl
 template <int OP, int VPT, bool PARTIALS, int WAVES = ROW_WAVES>
 __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
     const int lane = lane_id();
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // scalar
     const int cols = a.cols;
     const float n = (float)cols;
     constexpr bool BWD = OP >= ROW_SOFTMAX_BWD;
@@ -155,9 +173,11 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                 v[i] = nv[i];
                 if constexpr (BWD) g[i] = ng[i];
             }
+            row_mask<OP, VPT, BWD>(ok, v, g);
             if (row + stride < a.rows) row_load<OP, VPT, BWD>(a, row + stride, lane, nv, ng);
         } else {
             row_load<OP, VPT, BWD>(a, row, lane, v, g);
+            row_mask<OP, VPT, BWD>(ok, v, g);
         }
 
         if constexpr (OP == ROW_SOFTMAX) {
