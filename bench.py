@@ -348,7 +348,7 @@ def sweep(rt, orc, steps, warmup):
         B = orc.uniform((K, N), 4)
         dA, dB, dC = rt.array(A), rt.array(B), rt.empty((M, N))
         for tag in ["128x256x32_x", "128x128x32_x", "128x64x32_x", "128x64x32_x@2",
-                    "64x128x32_x", "64x128x32_x@2", "64x64x32_x"]:
+                    "64x128x32_x", "64x128x32_x@2", "64x128x32_x8", "64x64x32_x"]:
             key = f"{M}x{N}x{K}:{tag}"
 
             def fn(i, tag=tag.encode()):
