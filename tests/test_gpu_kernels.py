@@ -487,6 +487,53 @@ def test_reduce_sum_max(rt, n):
     assert out.numpy()[0] == x.max()
 
 
+def test_empty_shapes_and_oversized_dimensions(rt):
+    """Zero rows, zero columns and zero-length spans launch nothing harmful
+    and leave the reference's identities: column sums of no rows (and
+    dgamma / dbeta of no rows) are zero, the full sum of an empty span is 0
+    and its max f32::MIN (span.rs:302-321, as the oracle's pins check).
+    Dimensions beyond 2^31 - 1 are refused before any launch."""
+    say("empty shapes")
+    cols = 64
+    buf = rt.array(np.full(4 * cols, 7.0, np.float32))
+    empty = rt.empty((0,))
+    gam = rt.array(np.ones(cols, np.float32))
+    for rows, c in ((0, cols), (5, 0), (0, 0)):
+        rt.softmax_rows(empty, rows, c)
+        rt.layer_norm(empty, rows, c, gamma=gam)
+        rt.rms_norm(empty, rows, c, gamma=gam)
+        rt.softmax_rows_bwd(empty, empty, empty, rows, c)
+    dg, db = rt.array(np.full(cols, 3.0, np.float32)), rt.array(np.full(cols, 3.0, np.float32))
+    rt.layer_norm_bwd(empty, empty, empty, 0, cols, gamma=gam, dgamma=dg, dbeta=db)
+    assert np.all(dg.numpy() == 0) and np.all(db.numpy() == 0)
+    dg2 = rt.array(np.full(cols, 3.0, np.float32))
+    rt.rms_norm_bwd(empty, empty, empty, 0, cols, gamma=gam, dgamma=dg2)
+    assert np.all(dg2.numpy() == 0)
+    sc = rt.array(np.full(cols, 3.0, np.float32))
+    rt.sum_cols(empty, sc, 0, cols)
+    assert np.all(sc.numpy() == 0)
+    rt.sum_rows(empty, sc, 0, cols)
+    out = rt.empty((1,))
+    rt.reduce_sum(empty, out, n=0)
+    assert out.numpy()[0] == 0.0
+    rt.reduce_max(empty, out, n=0)
+    assert out.numpy()[0] == np.finfo(np.float32).min
+    rt.binary(buf, buf, buf, oxforge.ADD, n=0)
+    rt.map(buf, oxforge.MAP_SCALE, 2.0, n=0)
+    rt.transpose(empty, empty, 0, cols)
+    rt.gemm(empty, buf, empty, 0, 8, 8)
+    rt.gemm(buf, empty, empty, 8, 0, 8)
+    rt.sync()
+    assert np.all(buf.numpy() == 7.0)  # nothing was written
+    big = 1 << 31
+    for fn in (lambda: rt.softmax_rows(buf, big, 1), lambda: rt.layer_norm(buf, 1, big),
+               lambda: rt.sum_rows(buf, buf, big, 1), lambda: rt.sum_cols(buf, buf, 1, big),
+               lambda: rt.transpose(buf, buf, big, 1), lambda: rt.gemm(buf, buf, buf, big, 1, 1)):
+        with pytest.raises(oxforge.ForgeError) as e:
+            fn()
+        assert e.value.status == 1
+
+
 def test_fills_and_causal_mask(rt):
     say("fills")
     d = rt.empty((1000,))
