@@ -225,8 +225,9 @@ forge_status forge_gemm_ex_f32(forge_runtime *rt, forge_stream *stream,
 
 /* Tuning entry point (no reference counterpart): forge_gemm_f32 with an
  * explicit plain tile instance: "<BM>x<BN>x<BK>_x" for the unguarded
- * four-wave tiles (128x256x32, 128x128x32, 128x64x32, 64x128x32, 64x64x32)
- * or "64x64x16_2x2_g" for the guarded one.
+ * four-wave tiles (128x256x32, 128x128x32, 128x64x32, 64x128x32, 64x64x32),
+ * "64x128x32_x8" for the unguarded eight-wave tile, or "64x64x16_2x2_g" for
+ * the guarded one.
  * Unguarded tiles require M % BM == N % BN == K % BK == 0, 16-byte aligned
  * operands and K, N <= 2^21; anything else is FORGE_EINVAL.  A suffix
  * "@<n>" (1..16) lets a CU hold at most n of the launch's workgroups (the
@@ -239,7 +240,8 @@ forge_status forge_gemm_f32_tile(forge_runtime *rt, forge_stream *stream,
 
 /* Tuning entry point (no reference counterpart): forge_gemm_f32 computed as
  * `splits` K slices (one batched launch) plus a reduction in slice order,
- * with tile "128x128x32_x", "128x64x32_x", "64x128x32_x" or "64x64x32_x".
+ * with tile "128x128x32_x", "128x64x32_x", "64x128x32_x", "64x64x32_x" or
+ * "64x128x32_x8".
  * Requires M % BM == N % BN == K % (splits * BK) == 0, 16-byte aligned
  * operands and 1 <= splits <= 8.  Used by the benchmark's sweep. */
 forge_status forge_gemm_f32_split(forge_runtime *rt, forge_stream *stream,
@@ -249,8 +251,9 @@ forge_status forge_gemm_f32_split(forge_runtime *rt, forge_stream *stream,
 
 /* Testing entry point (no reference counterpart): forge_gemm_ex_f32 through
  * the fused-epilogue instance of one named tile ("128x128x32_x",
- * "128x64x32_x", "64x128x32_x", "64x64x32_x" or "64x64x16_2x2_g"), so every
- * instance the dispatcher can pick is testable at small shapes.  The same
+ * "128x64x32_x", "64x128x32_x", "64x64x32_x", "64x128x32_x8" or
+ * "64x64x16_2x2_g"), so every instance the dispatcher can pick is testable
+ * at small shapes.  The same
  * shape, alignment and "@<n>" rules as forge_gemm_f32_tile. */
 forge_status forge_gemm_ex_f32_tile(forge_runtime *rt, forge_stream *stream,
                                     const char *tile_tag, int trans_a, int trans_b,
