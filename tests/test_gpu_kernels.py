@@ -421,8 +421,11 @@ def test_binary_unaligned_bit_exact(rt):
     assert np.array_equal(do.numpy()[1:], a[1:] * b[1:])
 
 
+# One row per grid y index up to 65535; (70001, 8) and (65536, 12) also
+# take the loop over further rows (vector and scalar instances).
 @pytest.mark.parametrize("op,fn", OPS)
-@pytest.mark.parametrize("rows,cols", [(4096, 1024), (3, 5), (70, 33), (1, 4)])
+@pytest.mark.parametrize("rows,cols", [(4096, 1024), (3, 5), (70, 33), (1, 4), (70001, 8),
+                                       (65536, 12), (65537, 7)])
 def test_by_rows_bit_exact(rt, op, fn, rows, cols):
     say(f"by_rows op={op} {rows}x{cols}")
     m = orc.normal((rows, cols), 3)
