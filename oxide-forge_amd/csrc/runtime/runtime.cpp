@@ -529,7 +529,7 @@ extern "C" forge_status forge_fill(forge_runtime* rt, forge_stream* s, forge_sli
     if (!x.ptr || x.len == 0) return FORGE_OK;
     long long n = (long long)x.len;
     bool vec = aligned16(x.ptr);
-    unsigned g = grid_for(vec ? n / 4 + 1 : n, EW_THREADS, 4096);
+    unsigned g = vec ? stream_grid(n / 4 + 1) : grid_for(n, EW_THREADS, 8192);
     return launch_args(rt, s, vec ? "forge_fill_v" : "forge_fill_s", dim3(g), dim3(EW_THREADS), 0,
                        x.ptr, n, value);
 }
