@@ -428,6 +428,8 @@ def profile_workload(rt, orc, name, steps, warmup):
         return {"workload": name, "ms": round(ms, 4)}
     if name == "rows":
         return {"workload": name, "results": secondary_rows(rt, orc, steps, warmup)}
+    if name == "rows65536":
+        return {"workload": name, "results": secondary_rows_at_scale(rt, orc, steps, warmup)}
     raise SystemExit(f"unknown profile workload {name}")
 
 
@@ -465,7 +467,7 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--profile", default=None,
                     help="run only one workload (gemm4096, gemm8192x1024, copy, transpose, rows, "
-                         "c4, c5) for rocprofv3")
+                         "rows65536, c4, c5) for rocprofv3")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))

@@ -242,49 +242,46 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                 }
             } else {
                 // row.rs:302-346: A = sum g, B = sum g*xhat,
-                // dx = r/n * (n*g - A - xhat*B), g = dy (* gamma).  v holds
-                // x - mean; xhat and g are recomputed per use to keep the
-                // register footprint at two row copies.
+                // dx = r/n * (n*g - A - xhat*B), g = dy (* gamma).  xhat
+                // (in place of x - mean) and g are computed once and kept;
+                // products and their sums are fused multiply-adds (the
+                // backward is otherwise VALU-heavy: 535 vector instructions
+                // per 1024-wide row with separate multiplies and adds).
+                float4 gg[VPT];
                 float sa = 0.0f, sb = 0.0f;
 #pragma unroll
                 for (int i = 0; i < VPT; i++) {
-                    if (!ok[i]) continue;
-                    const int c = (i * 64 + lane) * 4;
-                    float4 gg = g[i];
+                    gg[i] = g[i];
                     if (a.gamma) {
                         const float4 gm = gamma4(i);
-                        F4_APPLY(gg, g[i], g[i].x * gm.x, g[i].y * gm.y, g[i].z * gm.z,
+                        F4_APPLY(gg[i], g[i], g[i].x * gm.x, g[i].y * gm.y, g[i].z * gm.z,
                                  g[i].w * gm.w);
                     }
-                    sa += sum4(gg);
-                    sb += (gg.x * (v[i].x * rstd) + gg.y * (v[i].y * rstd)) +
-                          (gg.z * (v[i].z * rstd) + gg.w * (v[i].w * rstd));
+                    F4_APPLY(v[i], v[i], v[i].x * rstd, v[i].y * rstd, v[i].z * rstd,
+                             v[i].w * rstd);
+                    if (!ok[i]) continue;
+                    sa += sum4(gg[i]);
+                    sb += fmaf(gg[i].x, v[i].x, gg[i].y * v[i].y) +
+                          fmaf(gg[i].z, v[i].z, gg[i].w * v[i].w);
                 }
                 sa = wave_sum(sa);
                 sb = wave_sum(sb);
-                const float scale = rstd / n;
+                const float scale = rstd / n, nsa = -sa, nsb = -sb;
 #pragma unroll
                 for (int i = 0; i < VPT; i++) {
                     if (!ok[i]) continue;
                     const int c = (i * 64 + lane) * 4;
-                    float4 gg = g[i];
-                    if (a.gamma) {
-                        const float4 gm = gamma4(i);
-                        F4_APPLY(gg, g[i], g[i].x * gm.x, g[i].y * gm.y, g[i].z * gm.z,
-                                 g[i].w * gm.w);
-                    }
-                    float4 xh;
-                    F4_APPLY(xh, v[i], v[i].x * rstd, v[i].y * rstd, v[i].z * rstd,
-                             v[i].w * rstd);
                     float4 o;
-                    F4_APPLY(o, xh, scale * (n * gg.x - sa - xh.x * sb),
-                             scale * (n * gg.y - sa - xh.y * sb),
-                             scale * (n * gg.z - sa - xh.z * sb),
-                             scale * (n * gg.w - sa - xh.w * sb));
+                    F4_APPLY(o, v[i], scale * fmaf(v[i].x, nsb, fmaf(n, gg[i].x, nsa)),
+                             scale * fmaf(v[i].y, nsb, fmaf(n, gg[i].y, nsa)),
+                             scale * fmaf(v[i].z, nsb, fmaf(n, gg[i].z, nsa)),
+                             scale * fmaf(v[i].w, nsb, fmaf(n, gg[i].w, nsa)));
                     store_f4(a.y + base + c, o, nt);
                     if constexpr (PARTIALS) {
-                        pg[i].x += g[i].x * xh.x; pg[i].y += g[i].y * xh.y;
-                        pg[i].z += g[i].z * xh.z; pg[i].w += g[i].w * xh.w;
+                        pg[i].x = fmaf(g[i].x, v[i].x, pg[i].x);
+                        pg[i].y = fmaf(g[i].y, v[i].y, pg[i].y);
+                        pg[i].z = fmaf(g[i].z, v[i].z, pg[i].z);
+                        pg[i].w = fmaf(g[i].w, v[i].w, pg[i].w);
                         pb[i].x += g[i].x; pb[i].y += g[i].y;
                         pb[i].z += g[i].z; pb[i].w += g[i].w;
                     }
@@ -328,42 +325,41 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
             }
         } else if constexpr (OP == ROW_RMS_NORM_BWD) {
             // row.rs:416-467: inv = 1/sqrt(q/n + eps), c = d/n*inv^3,
-            // dx = g*inv - x*c, g = dy (* gamma).
+            // dx = g*inv - x*c, g = dy (* gamma); g is computed once and
+            // kept, products and their sums are fused multiply-adds.
+            float4 gg[VPT];
             float q = 0.0f, d = 0.0f;
 #pragma unroll
             for (int i = 0; i < VPT; i++) {
-                const int c = (i * 64 + lane) * 4;
-                float4 gg = g[i];
+                gg[i] = g[i];
                 if (a.gamma && ok[i]) {
                     const float4 gm = gamma4(i);
-                    F4_APPLY(gg, g[i], g[i].x * gm.x, g[i].y * gm.y, g[i].z * gm.z,
+                    F4_APPLY(gg[i], g[i], g[i].x * gm.x, g[i].y * gm.y, g[i].z * gm.z,
                              g[i].w * gm.w);
                 }
-                q += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
-                d += (v[i].x * gg.x + v[i].y * gg.y) + (v[i].z * gg.z + v[i].w * gg.w);
+                q += fmaf(v[i].x, v[i].x, v[i].y * v[i].y) + fmaf(v[i].z, v[i].z, v[i].w * v[i].w);
+                d += fmaf(v[i].x, gg[i].x, v[i].y * gg[i].y) +
+                     fmaf(v[i].z, gg[i].z, v[i].w * gg[i].w);
             }
             q = wave_sum(q);
             d = wave_sum(d);
             const float rms = sqrtf(q / n + a.eps);
             const float inv = 1.0f / rms;
-            const float corr = d / n * inv * inv * inv;
+            const float ncorr = -(d / n * inv * inv * inv);
 #pragma unroll
             for (int i = 0; i < VPT; i++) {
                 if (!ok[i]) continue;
                 const int c = (i * 64 + lane) * 4;
-                float4 gg = g[i];
-                if (a.gamma) {
-                    const float4 gm = gamma4(i);
-                    F4_APPLY(gg, g[i], g[i].x * gm.x, g[i].y * gm.y, g[i].z * gm.z,
-                             g[i].w * gm.w);
-                }
                 float4 o;
-                F4_APPLY(o, v[i], gg.x * inv - v[i].x * corr, gg.y * inv - v[i].y * corr,
-                         gg.z * inv - v[i].z * corr, gg.w * inv - v[i].w * corr);
+                F4_APPLY(o, v[i], fmaf(v[i].x, ncorr, gg[i].x * inv),
+                         fmaf(v[i].y, ncorr, gg[i].y * inv), fmaf(v[i].z, ncorr, gg[i].z * inv),
+                         fmaf(v[i].w, ncorr, gg[i].w * inv));
                 store_f4(a.y + base + c, o, nt);
                 if constexpr (PARTIALS) {
-                    pg[i].x += g[i].x * (v[i].x * inv); pg[i].y += g[i].y * (v[i].y * inv);
-                    pg[i].z += g[i].z * (v[i].z * inv); pg[i].w += g[i].w * (v[i].w * inv);
+                    pg[i].x = fmaf(g[i].x, v[i].x * inv, pg[i].x);
+                    pg[i].y = fmaf(g[i].y, v[i].y * inv, pg[i].y);
+                    pg[i].z = fmaf(g[i].z, v[i].z * inv, pg[i].z);
+                    pg[i].w = fmaf(g[i].w, v[i].w * inv, pg[i].w);
                 }
             }
         }
