@@ -1,4 +1,5 @@
-// gemm_x.hpp -- fp32 GEMM on CDNA4 matrix cores, four-wave layout with
+// gemm_x.hpp -- fp32 GEMM on CDNA4 matrix cores, WM x WN wave layout
+// (2 x 2, or 4 x 2 for the eight-wave 64x128 tile) with
 // v_mfma_f32_16x16x4_f32 and 128-bit LDS operand reads.
 //
 // Same contract as gemm_body (gemm.hpp): C = A * B row-major, f32 accumulate,
@@ -6,9 +7,11 @@
 // 16-byte aligned operands, row pitches up to 2^21 floats).
 //
 // Structure
-//   - A workgroup of four waves (2 x 2) computes a BM x BN tile; each wave
-//     owns a (BM/2) x (BN/2) sub-tile of FM x FN blocks of 16 x 16, whose
-//     accumulators (four floats per lane per block) stay in registers.
+//   - A workgroup of WM x WN waves computes a BM x BN tile; each wave owns a
+//     (BM/WM) x (BN/WN) sub-tile of FM x FN blocks of 16 x 16, whose
+//     accumulators (four floats per lane per block) stay in registers.  The
+//     slab loads split evenly over all the waves.  Eight waves keep two
+//     waves per SIMD where a CU holds a single workgroup.
 //   - One MFMA sums four k values, lane group kq = lane / 16 supplying one.
 //     Inside a 16-wide k chunk, sub-step s (0..3) gives lane group kq the
 //     value k = 4 kq + s.  A lane's operands for a whole chunk are therefore
