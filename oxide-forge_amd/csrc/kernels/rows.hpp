@@ -117,7 +117,9 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
     constexpr bool USES_BETA = OP == ROW_LAYER_NORM;
     // gamma/beta are the same for every row: load them once, before the first
     // row's reductions, so their latency is not exposed per row.
-    constexpr bool PRELOAD = USES_GAMMA && VPT <= 8;
+    // (not in the 8-float4 partial kernels: with the prefetched row and the
+    // column partials, 32 more registers would spill)
+    constexpr bool PRELOAD = USES_GAMMA && VPT <= 8 && !(PARTIALS && VPT >= 8);
     float4 gm[PRELOAD ? VPT : 1], bt[(PRELOAD && USES_BETA) ? VPT : 1];
     if constexpr (PRELOAD) {
 #pragma unroll
@@ -142,6 +144,16 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
     };
     static_assert(!PARTIALS || OP == ROW_LAYER_NORM_BWD || OP == ROW_RMS_NORM_BWD,
                   "only the norm backward kernels produce column partials");
+    // The backward's g = dy * gamma for float4 group i of the current row.  Kept in registers between the two passes where
+    // that fits: at 8 float4 per lane the partial kernels would otherwise
+    // exceed 256 VGPRs and spill (the LayerNorm backward at [4096,2048]
+    // took 38.7 us spilling against 23-28 us recomputing).
+    constexpr bool KEEP_G = VPT <= 4;
+    auto gdy = [&](int i, float4 dy) -> float4 {
+        if (!a.gamma) return dy;
+        const float4 gm = gamma4(i);
+        return make_float4(dy.x * gm.x, dy.y * gm.y, dy.z * gm.z, dy.w * gm.w);
+    };
 
     float4 pg[PARTIALS ? VPT : 1], pb[PARTIALS ? VPT : 1];
     if constexpr (PARTIALS) {
@@ -247,22 +259,17 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                 // products and their sums are fused multiply-adds (the
                 // backward is otherwise VALU-heavy: 535 vector instructions
                 // per 1024-wide row with separate multiplies and adds).
-                float4 gg[VPT];
+                float4 keep[KEEP_G ? VPT : 1];
                 float sa = 0.0f, sb = 0.0f;
 #pragma unroll
                 for (int i = 0; i < VPT; i++) {
-                    gg[i] = g[i];
-                    if (a.gamma) {
-                        const float4 gm = gamma4(i);
-                        F4_APPLY(gg[i], g[i], g[i].x * gm.x, g[i].y * gm.y, g[i].z * gm.z,
-                                 g[i].w * gm.w);
-                    }
+                    const float4 gi = gdy(i, g[i]);
+                    if constexpr (KEEP_G) keep[i] = gi;
                     F4_APPLY(v[i], v[i], v[i].x * rstd, v[i].y * rstd, v[i].z * rstd,
                              v[i].w * rstd);
                     if (!ok[i]) continue;
-                    sa += sum4(gg[i]);
-                    sb += fmaf(gg[i].x, v[i].x, gg[i].y * v[i].y) +
-                          fmaf(gg[i].z, v[i].z, gg[i].w * v[i].w);
+                    sa += sum4(gi);
+                    sb += fmaf(gi.x, v[i].x, gi.y * v[i].y) + fmaf(gi.z, v[i].z, gi.w * v[i].w);
                 }
                 sa = wave_sum(sa);
                 sb = wave_sum(sb);
@@ -271,11 +278,14 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                 for (int i = 0; i < VPT; i++) {
                     if (!ok[i]) continue;
                     const int c = (i * 64 + lane) * 4;
+                    float4 gi;
+                    if constexpr (KEEP_G) gi = keep[i];
+                    else gi = gdy(i, g[i]);
                     float4 o;
-                    F4_APPLY(o, v[i], scale * fmaf(v[i].x, nsb, fmaf(n, gg[i].x, nsa)),
-                             scale * fmaf(v[i].y, nsb, fmaf(n, gg[i].y, nsa)),
-                             scale * fmaf(v[i].z, nsb, fmaf(n, gg[i].z, nsa)),
-                             scale * fmaf(v[i].w, nsb, fmaf(n, gg[i].w, nsa)));
+                    F4_APPLY(o, v[i], scale * fmaf(v[i].x, nsb, fmaf(n, gi.x, nsa)),
+                             scale * fmaf(v[i].y, nsb, fmaf(n, gi.y, nsa)),
+                             scale * fmaf(v[i].z, nsb, fmaf(n, gi.z, nsa)),
+                             scale * fmaf(v[i].w, nsb, fmaf(n, gi.w, nsa)));
                     store_f4(a.y + base + c, o, nt);
                     if constexpr (PARTIALS) {
                         pg[i].x = fmaf(g[i].x, v[i].x, pg[i].x);
@@ -327,19 +337,14 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
             // row.rs:416-467: inv = 1/sqrt(q/n + eps), c = d/n*inv^3,
             // dx = g*inv - x*c, g = dy (* gamma); g is computed once and
             // kept, products and their sums are fused multiply-adds.
-            float4 gg[VPT];
+            float4 keep[KEEP_G ? VPT : 1];
             float q = 0.0f, d = 0.0f;
 #pragma unroll
             for (int i = 0; i < VPT; i++) {
-                gg[i] = g[i];
-                if (a.gamma && ok[i]) {
-                    const float4 gm = gamma4(i);
-                    F4_APPLY(gg[i], g[i], g[i].x * gm.x, g[i].y * gm.y, g[i].z * gm.z,
-                             g[i].w * gm.w);
-                }
+                const float4 gi = gdy(i, g[i]);
+                if constexpr (KEEP_G) keep[i] = gi;
                 q += fmaf(v[i].x, v[i].x, v[i].y * v[i].y) + fmaf(v[i].z, v[i].z, v[i].w * v[i].w);
-                d += fmaf(v[i].x, gg[i].x, v[i].y * gg[i].y) +
-                     fmaf(v[i].z, gg[i].z, v[i].w * gg[i].w);
+                d += fmaf(v[i].x, gi.x, v[i].y * gi.y) + fmaf(v[i].z, gi.z, v[i].w * gi.w);
             }
             q = wave_sum(q);
             d = wave_sum(d);
@@ -350,10 +355,12 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
             for (int i = 0; i < VPT; i++) {
                 if (!ok[i]) continue;
                 const int c = (i * 64 + lane) * 4;
+                float4 gi;
+                if constexpr (KEEP_G) gi = keep[i];
+                else gi = gdy(i, g[i]);
                 float4 o;
-                F4_APPLY(o, v[i], fmaf(v[i].x, ncorr, gg[i].x * inv),
-                         fmaf(v[i].y, ncorr, gg[i].y * inv), fmaf(v[i].z, ncorr, gg[i].z * inv),
-                         fmaf(v[i].w, ncorr, gg[i].w * inv));
+                F4_APPLY(o, v[i], fmaf(v[i].x, ncorr, gi.x * inv), fmaf(v[i].y, ncorr, gi.y * inv),
+                         fmaf(v[i].z, ncorr, gi.z * inv), fmaf(v[i].w, ncorr, gi.w * inv));
                 store_f4(a.y + base + c, o, nt);
                 if constexpr (PARTIALS) {
                     pg[i].x = fmaf(g[i].x, v[i].x * inv, pg[i].x);
