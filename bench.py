@@ -10,11 +10,13 @@ GEMM, the [8192,4096] transpose and the C2 row / elementwise kernels (GB/s,
 rotating over >= 512 MiB of buffers so the 256 MiB MALL cannot serve them),
 and the transformer executors when built.
 
-The CPU baseline is the oracle (oracle/oxforge_oracle.c, f64-accumulate
-GEMM) on a bounded sample of the same workload, multithreaded on the host;
-with the secondary figures, the transformer layer's host tokens/s (one C4
-forward and one C5 training step of oracle/executors.py in numpy float64)
-is reported beside the GPU's.
+The CPU baseline is the C mirror (oracle/oxforge_oracle.c: f64-accumulate
+GEMM, row kernels) on bounded samples of the same workloads, one thread per
+CPU the host grants this process (nproc and the share are both reported);
+with the secondary figures, the transformer layer's host tokens/s (C4
+forward through the C mirror, C5 training step through oracle/executors.py
+in numpy float64) is reported beside the GPU's.  Inputs come from
+oxforge.synth; the oracle is imported only by the CPU legs.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
        [--no-secondary] [--sweep]
@@ -30,6 +32,8 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "oxide-forge_amd"))
 sys.path.insert(0, ROOT)
+
+from oxforge import synth  # noqa: E402  (seeded inputs; the package, not the oracle)
 
 METRIC = "f32 GEMM TFLOP/s (% fp32-MFMA peak); transformer layer tokens/sec, 1 GPU"
 PEAK_FP32_MFMA_TFLOPS = 157.3
@@ -88,9 +92,9 @@ def load_traffic(kernel: str):
         return None
 
 
-def gemm_tflops(rt, orc, M, N, K, steps, warmup, seed=3):
-    A = orc.uniform((M, K), seed)
-    B = orc.uniform((K, N), seed + 1)
+def gemm_tflops(rt, M, N, K, steps, warmup, seed=3):
+    A = synth.uniform((M, K), seed)
+    B = synth.uniform((K, N), seed + 1)
     dA, dB, dC = rt.array(A), rt.array(B), rt.empty((M, N))
     ms = time_launches(rt, lambda i: rt.gemm(dA, dB, dC, M, N, K), steps, warmup)
     for d in (dA, dB, dC):
@@ -98,8 +102,8 @@ def gemm_tflops(rt, orc, M, N, K, steps, warmup, seed=3):
     return 2.0 * M * N * K / (ms * 1e-3) / 1e12, ms
 
 
-def rotating(rt, orc, shape, sets, seed):
-    base = rt.array(orc.normal(shape, seed))
+def rotating(rt, shape, sets, seed):
+    base = rt.array(synth.normal(shape, seed))
     bufs = [base]
     for _ in range(sets - 1):
         b = rt.empty(shape)
@@ -108,16 +112,16 @@ def rotating(rt, orc, shape, sets, seed):
     return bufs
 
 
-def secondary(rt, orc, steps, warmup, extended):
+def secondary(rt, steps, warmup, extended):
     out = {}
     log("gemm 8192x1024x4096")
-    t, ms = gemm_tflops(rt, orc, 8192, 1024, 4096, steps, warmup)
+    t, ms = gemm_tflops(rt, 8192, 1024, 4096, steps, warmup)
     out["gemm_8192x1024x4096"] = {"tflops": round(t, 2), "ms": round(ms, 4),
                                   "frac_mfma_peak": round(t / PEAK_FP32_MFMA_TFLOPS, 4)}
 
     log("transpose 8192x4096")
     R, C = 8192, 4096
-    xs = rotating(rt, orc, (R, C), 2, 21)
+    xs = rotating(rt, (R, C), 2, 21)
     ys = [rt.empty((C, R)) for _ in range(2)]
     ms = time_launches(rt, lambda i: rt.transpose(xs[i % 2], ys[i % 2], R, C), max(steps, 64),
                        warmup)
@@ -126,12 +130,12 @@ def secondary(rt, orc, steps, warmup, extended):
     for b in xs + ys:
         b.recycle()
 
-    out.update(secondary_rows(rt, orc, steps, warmup, extended))
-    out.update(secondary_rows_at_scale(rt, orc, steps, warmup))
+    out.update(secondary_rows(rt, steps, warmup, extended))
+    out.update(secondary_rows_at_scale(rt, steps, warmup))
     return out
 
 
-def secondary_rows_at_scale(rt, orc, steps, warmup):
+def secondary_rows_at_scale(rt, steps, warmup):
     """The same row and streaming kernels on X [65536, 1024] (256 MiB per
     operand, two rotating sets: 512 MiB, beyond the 256 MiB MALL).  At the
     C2 size a launch lasts 7-15 us and its ramp-up and drain are a large
@@ -143,13 +147,13 @@ def secondary_rows_at_scale(rt, orc, steps, warmup):
     rows, cols, sets = 65536, 1024, 2
     X = 4 * rows * cols
     log("row ops 65536x1024")
-    xs = rotating(rt, orc, (rows, cols), sets, 2)
-    gs = rotating(rt, orc, (rows, cols), sets, 3)
+    xs = rotating(rt, (rows, cols), sets, 2)
+    gs = rotating(rt, (rows, cols), sets, 3)
     ds = [rt.empty((rows, cols)) for _ in range(sets)]
-    gam = rt.array(orc.normal((cols,), 4, 1.0, 0.1))
-    bet = rt.array(orc.normal((cols,), 5, 0.0, 0.1))
+    gam = rt.array(synth.normal((cols,), 4, 1.0, 0.1))
+    bet = rt.array(synth.normal((cols,), 5, 0.0, 0.1))
     dgam, dbet = rt.empty((cols,)), rt.empty((cols,))
-    rvec = rt.array(orc.normal((cols,), 6))
+    rvec = rt.array(synth.normal((cols,), 6))
     cases = {
         "softmax_fwd": (2 * X, lambda i: rt.softmax_rows(xs[i % sets], rows, cols)),
         "layer_norm_fwd": (2 * X, lambda i: rt.layer_norm(xs[i % sets], rows, cols, gam, bet)),
@@ -177,7 +181,7 @@ def secondary_rows_at_scale(rt, orc, steps, warmup):
     return out
 
 
-def secondary_rows(rt, orc, steps, warmup, extended=True):
+def secondary_rows(rt, steps, warmup, extended=True):
     """C2 row / elementwise kernels on X [4096, 1024], 32 rotating buffer
     sets (512 MiB per operand) so the MALL cannot serve them."""
     import oxforge
@@ -186,13 +190,13 @@ def secondary_rows(rt, orc, steps, warmup, extended=True):
     rows, cols, sets = 4096, 1024, 32
     X = 4 * rows * cols
     log("row ops 4096x1024")
-    xs = rotating(rt, orc, (rows, cols), sets, 2)
-    gs = rotating(rt, orc, (rows, cols), sets, 3)
+    xs = rotating(rt, (rows, cols), sets, 2)
+    gs = rotating(rt, (rows, cols), sets, 3)
     ds = [rt.empty((rows, cols)) for _ in range(sets)]
-    gam = rt.array(orc.normal((cols,), 4, 1.0, 0.1))
-    bet = rt.array(orc.normal((cols,), 5, 0.0, 0.1))
+    gam = rt.array(synth.normal((cols,), 4, 1.0, 0.1))
+    bet = rt.array(synth.normal((cols,), 5, 0.0, 0.1))
     dgam, dbet = rt.empty((cols,)), rt.empty((cols,))
-    rvec = rt.array(orc.normal((cols,), 6))
+    rvec = rt.array(synth.normal((cols,), 6))
     rsum = rt.empty((rows,))
     cases = {
         "softmax_fwd": (2 * X, lambda i: rt.softmax_rows(xs[i % sets], rows, cols)),
@@ -228,24 +232,24 @@ def secondary_rows(rt, orc, steps, warmup, extended=True):
     return out
 
 
-def transformer_params(orc, S, H, F, O, seed, affine):
-    p = {"WQ": orc.xavier(H, H, seed), "WK": orc.xavier(H, H, seed + 1),
-         "WV": orc.xavier(H, H, seed + 2), "POS": orc.xavier(S, H, seed + 3),
-         "W1": orc.xavier(H, F, seed + 4), "W2": orc.xavier(F, H, seed + 5),
-         "WO": orc.xavier(H, O, seed + 6)}
+def transformer_params(S, H, F, O, seed, affine):
+    p = {"WQ": synth.xavier(H, H, seed), "WK": synth.xavier(H, H, seed + 1),
+         "WV": synth.xavier(H, H, seed + 2), "POS": synth.xavier(S, H, seed + 3),
+         "W1": synth.xavier(H, F, seed + 4), "W2": synth.xavier(F, H, seed + 5),
+         "WO": synth.xavier(H, O, seed + 6)}
     import numpy as np
 
     for k, n in (("BQ", H), ("BK", H), ("BV", H), ("B1", F), ("B2", H), ("BO", O)):
         p[k] = np.zeros(n, np.float32)
     if affine:
-        p["G1"] = orc.normal((H,), seed + 20, 1.0, 0.1)
-        p["G2"] = orc.normal((H,), seed + 21, 1.0, 0.1)
-        p["BE1"] = orc.normal((H,), seed + 22, 0.0, 0.1)
-        p["BE2"] = orc.normal((H,), seed + 23, 0.0, 0.1)
+        p["G1"] = synth.normal((H,), seed + 20, 1.0, 0.1)
+        p["G2"] = synth.normal((H,), seed + 21, 1.0, 0.1)
+        p["BE1"] = synth.normal((H,), seed + 22, 0.0, 0.1)
+        p["BE2"] = synth.normal((H,), seed + 23, 0.0, 0.1)
     return p
 
 
-def transformers(rt, orc, steps, warmup):
+def transformers(rt, steps, warmup):
     """C4 inference forward and C5 training step, tokens/s."""
     from oxforge import net
 
@@ -253,9 +257,9 @@ def transformers(rt, orc, steps, warmup):
     # C4: seq 2048, hidden 1024, FFN 4096 GELU, out 1024, RMSNorm, inference.
     S, H, F, O = 2048, 1024, 4096, 1024
     log("transformer C4 inference")
-    T = net.Transformer(rt, transformer_params(orc, S, H, F, O, 4, False), S, H, F, O, net.RMS,
-                        net.ENCODER_INFERENCE, qkv_streams=True)
-    X = rt.array(orc.normal((S, H), 4))
+    T = net.Transformer(rt, transformer_params(S, H, F, O, 4, False), S, H, F, O, net.RMS,
+                        net.ENCODER_INFERENCE, qkv_streams=False)
+    X = rt.array(synth.normal((S, H), 4))
     Y = rt.empty((S, O))
     ms = time_launches(rt, lambda i: T.forward(X, Y), steps, warmup)
     flops = 2.0 * S * H * H * 3 + 2.0 * S * S * H * 2 + 2.0 * S * H * F * 2 + 2.0 * S * H * O
@@ -269,10 +273,10 @@ def transformers(rt, orc, steps, warmup):
     # C5: seq 4096, hidden 2048, FFN 8192 GELU, out 2048, LayerNorm, training.
     S, H, F, O = 4096, 2048, 8192, 2048
     log("transformer C5 training step")
-    T = net.Transformer(rt, transformer_params(orc, S, H, F, O, 5, True), S, H, F, O, net.LAYER,
+    T = net.Transformer(rt, transformer_params(S, H, F, O, 5, True), S, H, F, O, net.LAYER,
                         net.ENCODER_TRAINING)
-    X = rt.array(orc.normal((S, H), 5))
-    dY = rt.array(orc.normal((S, O), 6))
+    X = rt.array(synth.normal((S, H), 5))
+    dY = rt.array(synth.normal((S, O), 6))
     Y = rt.empty((S, O))
     dX = rt.empty((S, H))
 
@@ -293,42 +297,72 @@ def transformers(rt, orc, steps, warmup):
     return out
 
 
-def cpu_transformer_baseline(orc):
-    """The transformer layer on the host: oracle/executors.py (numpy float64
-    over the host BLAS, at most 16 threads), one full C4 forward and one full
-    C5 training step (forward + backward) on the same synthetic inputs as
-    the GPU runs.  A reported baseline, not the optimisation target."""
+def host_cpus() -> dict:
+    """CPUs of the host and the share this process may use: nproc
+    (os.cpu_count), the affinity mask, and the cgroup v2 CPU quota
+    (cpu.max) when one is set.  The baselines run one thread per usable CPU:
+    min(affinity, quota)."""
+    nproc = os.cpu_count() or 1
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = nproc
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()[:2]
+        if q != "max":
+            quota = float(q) / float(period)
+    except (OSError, ValueError):
+        pass
+    usable = affinity if quota is None else max(1, min(affinity, int(quota + 0.5)))
+    return {"nproc": nproc, "affinity_cpus": affinity, "cgroup_quota_cpus": quota,
+            "threads": usable}
+
+
+def cpu_transformer_baseline():
+    """The transformer layer on the host, on the same synthetic inputs as the
+    GPU runs, one thread per usable CPU:
+      - C4 forward: the C mirror (oracle/oxforge_oracle.c kernels composed in
+        the reference's launch order, f32 with f64-accumulated products);
+      - C5 training step: oracle/executors.py forward + backward (numpy
+        float64 over the host BLAS; the C mirror has no backward composition).
+    A reported baseline, not the optimisation target."""
     from threadpoolctl import threadpool_info, threadpool_limits
 
     from oracle import executors as ex
+    from oracle import oracle as orc
 
-    threads = min(16, os.cpu_count() or 1)
+    cpus = host_cpus()
+    threads = cpus["threads"]
+    orc.set_threads(threads)
     out = {}
+    S, H, F, O = 2048, 1024, 4096, 1024
+    p = transformer_params(S, H, F, O, 4, False)
+    X = synth.normal((S, H), 4)
+    t0 = time.perf_counter()
+    orc.transformer_forward(p, X, rms=True)
+    c4 = time.perf_counter() - t0
     with threadpool_limits(limits=threads, user_api="blas"):
         used = max([i["num_threads"] for i in threadpool_info() if i["user_api"] == "blas"],
                    default=1)
-        S, H, F, O = 2048, 1024, 4096, 1024
-        p = transformer_params(orc, S, H, F, O, 4, False)
-        X = orc.normal((S, H), 4)
-        t0 = time.perf_counter()
-        ex.transformer_forward(p, X, ex.RMS)
-        c4 = time.perf_counter() - t0
         S, H, F, O = 4096, 2048, 8192, 2048
-        p = transformer_params(orc, S, H, F, O, 5, True)
-        X, dY = orc.normal((S, H), 5), orc.normal((S, O), 6)
+        p = transformer_params(S, H, F, O, 5, True)
+        X, dY = synth.normal((S, H), 5), synth.normal((S, O), 6)
         t0 = time.perf_counter()
         _, cache = ex.transformer_forward(p, X, ex.LAYER)
         ex.transformer_backward(p, cache, dY, ex.LAYER)
         c5 = time.perf_counter() - t0
     out["c4_inference_tokens_per_s"] = round(2048 / c4, 1)
     out["c5_training_tokens_per_s"] = round(4096 / c5, 1)
-    out.update({"cores": used, "kind": "port",
-                "sample": f"one C4 forward ({c4:.1f} s) and one C5 training step ({c5:.1f} s) "
-                          f"of oracle/executors.py (numpy float64, {used} BLAS threads)"})
+    out.update({"cores": threads, "nproc": cpus["nproc"], "kind": "port",
+                "sample": f"one C4 forward of the C mirror ({c4:.1f} s, {threads} threads) and "
+                          f"one C5 training step of oracle/executors.py ({c5:.1f} s, numpy "
+                          f"float64, {used} BLAS threads)"})
     return out
 
 
-def sweep(rt, orc, steps, warmup):
+def sweep(rt, steps, warmup):
     """Times every plain GEMM tile instance and the split-K candidates on the
     C3, C4 and C5 GEMM shapes."""
     import oxforge
@@ -344,8 +378,8 @@ def sweep(rt, orc, steps, warmup):
               (4096, 2048, 2048), (4096, 4096, 2048), (4096, 2048, 4096), (4096, 8192, 2048),
               (4096, 2048, 8192), (2048, 2048, 4096), (2048, 8192, 4096)]
     for (M, N, K) in shapes:
-        A = orc.uniform((M, K), 3)
-        B = orc.uniform((K, N), 4)
+        A = synth.uniform((M, K), 3)
+        B = synth.uniform((K, N), 4)
         dA, dB, dC = rt.array(A), rt.array(B), rt.empty((M, N))
         for tag in ["128x256x32_x", "128x128x32_x", "128x64x32_x", "128x64x32_x@2",
                     "64x128x32_x", "64x128x32_x@2", "64x128x32_x8", "64x64x32_x"]:
@@ -379,7 +413,7 @@ def sweep(rt, orc, steps, warmup):
     return res
 
 
-def profile_workload(rt, orc, name, steps, warmup):
+def profile_workload(rt, name, steps, warmup):
     """Runs one workload `steps` times (for rocprofv3 runs) and returns its
     average time.  copy: an identity map over 256 MiB (reads and writes
     exactly 256 MiB per launch), the calibration kernel for FETCH_SIZE and
@@ -389,7 +423,7 @@ def profile_workload(rt, orc, name, steps, warmup):
 
     if name in ("gemm4096", "gemm8192x1024"):
         M, N, K = (4096, 4096, 4096) if name == "gemm4096" else (8192, 1024, 4096)
-        t, ms = gemm_tflops(rt, orc, M, N, K, steps, warmup)
+        t, ms = gemm_tflops(rt, M, N, K, steps, warmup)
         return {"workload": name, "ms": round(ms, 5), "tflops": round(t, 3)}
     if name == "copy":
         # x = x * 1.0 with the scale a kernel argument: one read and one
@@ -402,21 +436,21 @@ def profile_workload(rt, orc, name, steps, warmup):
                 "gbs": round(2 * 4 * n / (ms * 1e-3) / 1e9, 1)}
     if name == "transpose":
         R, C = 8192, 4096
-        x, y = rt.array(orc.uniform((R, C), 21)), rt.empty((C, R))
+        x, y = rt.array(synth.uniform((R, C), 21)), rt.empty((C, R))
         ms = time_launches(rt, lambda i: rt.transpose(x, y, R, C), steps, warmup)
         return {"workload": name, "ms": round(ms, 5)}
     if name in ("c4", "c5"):
         if name == "c4":
             S, H, F, O = 2048, 1024, 4096, 1024
-            T = net.Transformer(rt, transformer_params(orc, S, H, F, O, 4, False), S, H, F, O,
-                                net.RMS, net.ENCODER_INFERENCE, qkv_streams=True)
-            X, Y = rt.array(orc.normal((S, H), 4)), rt.empty((S, O))
+            T = net.Transformer(rt, transformer_params(S, H, F, O, 4, False), S, H, F, O,
+                                net.RMS, net.ENCODER_INFERENCE, qkv_streams=False)
+            X, Y = rt.array(synth.normal((S, H), 4)), rt.empty((S, O))
             ms = time_launches(rt, lambda i: T.forward(X, Y), steps, warmup)
         else:
             S, H, F, O = 4096, 2048, 8192, 2048
-            T = net.Transformer(rt, transformer_params(orc, S, H, F, O, 5, True), S, H, F, O,
+            T = net.Transformer(rt, transformer_params(S, H, F, O, 5, True), S, H, F, O,
                                 net.LAYER, net.ENCODER_TRAINING)
-            X, dY = rt.array(orc.normal((S, H), 5)), rt.array(orc.normal((S, O), 6))
+            X, dY = rt.array(synth.normal((S, H), 5)), rt.array(synth.normal((S, O), 6))
             Y, dX = rt.empty((S, O)), rt.empty((S, H))
 
             def step(i):
@@ -427,33 +461,65 @@ def profile_workload(rt, orc, name, steps, warmup):
         T.close()
         return {"workload": name, "ms": round(ms, 4)}
     if name == "rows":
-        return {"workload": name, "results": secondary_rows(rt, orc, steps, warmup)}
+        return {"workload": name, "results": secondary_rows(rt, steps, warmup)}
     if name == "rows65536":
-        return {"workload": name, "results": secondary_rows_at_scale(rt, orc, steps, warmup)}
+        return {"workload": name, "results": secondary_rows_at_scale(rt, steps, warmup)}
     raise SystemExit(f"unknown profile workload {name}")
 
 
-def cpu_baseline(orc, M, N, K):
-    """Oracle GEMM (f64 accumulate, all host threads up to 16) on 256 of the
-    M rows; scaled to TFLOP/s of the same workload."""
-    threads = min(16, os.cpu_count() or 1)
+def cpu_baseline(M, N, K):
+    """The C mirror (oracle/oxforge_oracle.c) on the host, one thread per
+    usable CPU (host_cpus), on bounded samples of the GPU's workloads:
+      - headline: the f64-accumulate GEMM over consecutive 512-row blocks of
+        the same M x N x K product until about 10 s have been timed (or the
+        whole product is done), scaled to TFLOP/s;
+      - row ops: C2 softmax forward (2X bytes) and LayerNorm backward with
+        dgamma/dbeta (3X bytes) on X [4096, 1024], each repeated for about
+        3 s, in GB/s of the same algorithmic bytes the GPU figures use."""
+    from oracle import oracle as orc
+
+    cpus = host_cpus()
+    threads = cpus["threads"]
     orc.set_threads(threads)
     rows = 512
-    A = orc.uniform((rows, K), 3)
-    B = orc.uniform((K, N), 4)
-    # Repeat the 512-row block until about 10 s of CPU work has been timed.
+    A = synth.uniform((M, K), 3)
+    B = synth.uniform((K, N), 4)
     t0 = time.perf_counter()
-    reps = 0
-    while True:
-        orc.gemm(A, B)
-        reps += 1
-        dt = time.perf_counter() - t0
-        if dt >= 10.0 or reps * rows >= 8 * M:
+    blocks = 0
+    while blocks * rows < M:
+        orc.gemm(A[blocks * rows:(blocks + 1) * rows], B)
+        blocks += 1
+        if time.perf_counter() - t0 >= 10.0:
             break
-    return {"value": round(2.0 * reps * rows * N * K / dt / 1e12, 5), "unit": "TFLOP/s",
-            "cores": threads, "kind": "port",
-            "sample": f"{reps} x {rows} rows of the {M}x{N}x{K} GEMM (oracle, f64 accumulate, "
-                      f"{threads} threads), {dt:.1f} s"}
+    dt = time.perf_counter() - t0
+    tflops = 2.0 * blocks * rows * N * K / dt / 1e12
+
+    r, c = 4096, 1024
+    X = 4 * r * c
+    x = synth.normal((r, c), 2)
+    dy = synth.normal((r, c), 3)
+    gam = synth.normal((c,), 4, 1.0, 0.1)
+    xs = x.copy()  # softmax runs in place, as on the GPU
+    row_ops = {}
+    for name, nbytes, fn in (
+            ("softmax_fwd", 2 * X, lambda: orc.lib().orc_softmax_rows(orc._p(xs), r, c)),
+            ("layer_norm_bwd", 3 * X, lambda: orc.layer_norm_backward(x, dy, gam, want_params=True))):
+        t1 = time.perf_counter()
+        reps = 0
+        while True:
+            fn()
+            reps += 1
+            el = time.perf_counter() - t1
+            if el >= 3.0:
+                break
+        row_ops[f"{name}_4096x1024_gbs"] = round(nbytes * reps / el / 1e9, 2)
+    return {"value": round(tflops, 5), "unit": "TFLOP/s", "cores": threads,
+            "nproc": cpus["nproc"], "affinity_cpus": cpus["affinity_cpus"],
+            "cgroup_quota_cpus": cpus["cgroup_quota_cpus"], "kind": "port",
+            "sample": f"{blocks} of {M // rows} 512-row blocks of the {M}x{N}x{K} GEMM "
+                      f"(C mirror, f64 accumulate, {threads} threads), {dt:.1f} s; row ops "
+                      f"on [4096,1024] about 3 s each",
+            "row_ops": row_ops}
 
 
 def main() -> int:
@@ -477,19 +543,18 @@ def main() -> int:
         return 2
 
     import oxforge
-    from oracle import oracle as orc
 
     rt = oxforge.Runtime(0)
     props = rt.props()
     log(f"device {props}")
     if args.profile:
-        res = profile_workload(rt, orc, args.profile, args.steps, args.warmup)
+        res = profile_workload(rt, args.profile, args.steps, args.warmup)
         rt.close()
         print(json.dumps(res), flush=True)
         return 0
     M = N = K = 4096
     log("gemm 4096^3")
-    tflops, ms = gemm_tflops(rt, orc, M, N, K, args.steps, args.warmup)
+    tflops, ms = gemm_tflops(rt, M, N, K, args.steps, args.warmup)
     kernel = rt.gemm_kernel_name(M, N, K)
     traffic = load_traffic(kernel)
     line = {
@@ -512,16 +577,16 @@ def main() -> int:
                      "frac": round(tflops / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": traffic},
     }
     if not args.no_secondary:
-        line["secondary"] = secondary(rt, orc, args.steps, args.warmup, args.extended)
-        line["secondary"].update(transformers(rt, orc, args.steps, args.warmup))
+        line["secondary"] = secondary(rt, args.steps, args.warmup, args.extended)
+        line["secondary"].update(transformers(rt, args.steps, args.warmup))
     if args.sweep:
-        line["sweep"] = sweep(rt, orc, args.steps, args.warmup)
+        line["sweep"] = sweep(rt, args.steps, args.warmup)
     if not args.no_cpu:
         log("cpu baseline")
-        line["cpu_baseline"] = cpu_baseline(orc, M, N, K)
+        line["cpu_baseline"] = cpu_baseline(M, N, K)
         if "secondary" in line:
             log("cpu baseline: transformer layer")
-            line["secondary"]["cpu_baseline_transformer"] = cpu_transformer_baseline(orc)
+            line["secondary"]["cpu_baseline_transformer"] = cpu_transformer_baseline()
     rt.close()
     print(json.dumps(line), flush=True)
     return 0

@@ -408,7 +408,8 @@ forge_status forge_fill_seq(forge_runtime *rt, forge_stream *stream,
 forge_status forge_fill_random(forge_runtime *rt, forge_stream *stream,
                                forge_slice x, size_t n, uint32_t seed);
 /* Vector::equals (vector.rs:117-136 -> reduction.rs:132-174): out[0] = the
- * number of positions i < n with l[i] != r[i] (0 means equal).  Every
+ * number of positions i < n with l[i] != r[i] (0 means equal), counted in
+ * integers and stored as the nearest f32 (exact up to 2^24).  Every
  * element is compared (the reference kernel reports block 0 only). */
 forge_status forge_compare(forge_runtime *rt, forge_stream *stream,
                            forge_slice l, forge_slice r, size_t n,

@@ -96,7 +96,11 @@ typedef struct forge_transformer_desc {
     size_t seq, hidden, ffn, out;
     int norm_type;      /* 0 = NormType::Rms, 1 = NormType::Layer         */
     int kind;           /* forge_transformer_kind                        */
-    int qkv_streams;    /* inference: 1 = Q/K/V on three forked streams   */
+    int qkv_streams;    /* inference kinds: 1 = Q/K/V each on one of three
+                         * forked streams, joined before the scores and
+                         * before A.V (attention.rs:65-102); 0 = one batched
+                         * GEMM launch on the primary stream.  Results are
+                         * bit-identical.  The training kind always batches. */
     int ffn_activation; /* forge_activation of W1 (W2 and WO: identity)   */
 } forge_transformer_desc;
 

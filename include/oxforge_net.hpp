@@ -429,11 +429,14 @@ struct Normalization {
                     Vector* dgamma = nullptr, Vector* dbeta = nullptr) const;
 };
 
-// QkvProjection (attention.rs:15-145).
-// QkvProjection (attention.rs:15-144).  The reference runs the three
-// projections on three forked streams; here they are one batched GEMM launch
-// on the primary stream (same results, no cross-queue fork and joins), and
-// `streams` is accepted for interface compatibility only.
+// QkvProjection (attention.rs:15-144).  With `streams` (three streams of
+// CudaRuntime::create_extra_streams) the three projections run as the
+// reference runs them: the streams fork from the primary stream, Q, K and V
+// each run on their own stream, wait_for_query_key joins the first two and
+// wait_for_value the third.  Without streams they are one batched GEMM
+// launch on the primary stream (three launches when the shapes differ):
+// the faster choice on MI355X, where a cross-queue fork costs about 24 us
+// and a join about 7 us of idle device.  Both give bit-identical results.
 class QkvProjection {
 public:
     QkvProjection(Linear query, Linear key, Linear value,
@@ -451,6 +454,7 @@ public:
 private:
     Linear query_, key_, value_;
     std::optional<std::vector<CudaStream>> streams_;
+    bool joined_qk_ = true, joined_v_ = true;  // no projection pending on the streams
 };
 
 // Gradients of the single-head Post-Norm block (the explicit-gradient

@@ -9,7 +9,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_double, c_float, c_int, c_size_t, c_uint64
+from ctypes import POINTER, c_double, c_float, c_int, c_size_t
 
 import numpy as np
 
@@ -55,8 +55,6 @@ def lib():
             "orc_causal_mask": ([_F, c_size_t, c_size_t], None),
             "orc_activation_backward": ([_F, _F, _F, c_size_t, c_int], None),
             "orc_fill_random": ([_F, c_size_t, ctypes.c_uint32], None),
-            "orc_fill_uniform": ([_F, c_size_t, c_uint64, c_float, c_float], None),
-            "orc_fill_normal": ([_F, c_size_t, c_uint64, c_float, c_float], None),
         }
         for name, (args, res) in sig.items():
             fn = getattr(L, name)
@@ -82,24 +80,6 @@ def set_threads(n: int) -> None:
 
 
 # ------------------------------------------------------------- synthetic data
-def uniform(shape, seed: int, lo: float = -1.0, hi: float = 1.0) -> np.ndarray:
-    out = np.empty(shape, dtype=np.float32)
-    lib().orc_fill_uniform(_p(out), out.size, seed, lo, hi)
-    return out
-
-
-def normal(shape, seed: int, mu: float = 0.0, sigma: float = 1.0) -> np.ndarray:
-    out = np.empty(shape, dtype=np.float32)
-    lib().orc_fill_normal(_p(out), out.size, seed, mu, sigma)
-    return out
-
-
-def xavier(fan_in: int, fan_out: int, seed: int) -> np.ndarray:
-    """Xavier-uniform U(+-sqrt(6/(fan_in+fan_out))) of shape [fan_in, fan_out]."""
-    lim = float(np.sqrt(6.0 / (fan_in + fan_out)))
-    return uniform((fan_in, fan_out), seed, -lim, lim)
-
-
 # ------------------------------------------------------------------- kernels
 def gemm(A, B, trans_a=False, trans_b=False) -> np.ndarray:
     A, B = _f32(A), _f32(B)
@@ -249,3 +229,31 @@ def causal_mask(m) -> np.ndarray:
     m = _f32(m).copy()
     lib().orc_causal_mask(_p(m), m.shape[0], m.shape[1])
     return m
+
+
+# ------------------------------------------------------------ block forward
+def transformer_forward(p, X, rms=True):
+    """The single-head Post-Norm block forward as the reference launches it
+    (inference.rs:76-108, attention.rs:258-281, 359-401, linear.rs:185-230):
+    every step is one C kernel above, in f32 with f64-accumulated products.
+    p maps slot names (WQ, BQ, WK, BK, WV, BV, POS, W1, B1, W2, B2, WO, BO) to
+    arrays; biases may be None.  The multithreaded host mirror of the layer
+    that bench.py times."""
+    norm = rms_norm if rms else layer_norm
+
+    def linear(x, w, b, act_op=None):
+        z = gemm(x, w)
+        if b is not None:
+            z = binary_assign_by_rows(z, b, ADD)
+        return map_(z, act_op) if act_op is not None else z
+
+    xp = binary(X, p["POS"], ADD)
+    q = linear(xp, p["WQ"], p.get("BQ"))
+    k = linear(xp, p["WK"], p.get("BK"))
+    v = linear(xp, p["WV"], p.get("BV"))
+    s = map_(gemm(q, k, trans_b=True), MAP_SCALE, float(1.0 / np.sqrt(np.float32(q.shape[1]))))
+    pmat = softmax_rows(s)
+    h1 = norm(binary(xp, gemm(pmat, v), ADD))
+    f = linear(linear(h1, p["W1"], p.get("B1"), MAP_GELU), p["W2"], p.get("B2"))
+    h2 = norm(binary(h1, f, ADD))
+    return linear(h2, p["WO"], p.get("BO"))

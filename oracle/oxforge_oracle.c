@@ -480,33 +480,3 @@ void orc_fill_random(float *x, size_t n, uint32_t seed) {
     for (size_t i = 0; i < n; i++)
         x[i] = (float)ref_hash(seed + (uint32_t)i) / (float)UINT32_MAX;
 }
-
-/* --------------------------------------------------------- synthetic data */
-
-static uint64_t splitmix64(uint64_t *state) {
-    uint64_t z = (*state += 0x9E3779B97F4A7C15ull);
-    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-    return z ^ (z >> 31);
-}
-
-void orc_fill_uniform(float *x, size_t n, uint64_t seed, float lo, float hi) {
-    uint64_t s = seed;
-    for (size_t i = 0; i < n; i++) {
-        double u = (double)(splitmix64(&s) >> 40) * (1.0 / 16777216.0);
-        x[i] = (float)((double)lo + ((double)hi - (double)lo) * u);
-    }
-}
-
-void orc_fill_normal(float *x, size_t n, uint64_t seed, float mu, float sigma) {
-    uint64_t s = seed;
-    const double two_pi = 6.283185307179586476925;
-    for (size_t i = 0; i < n; i += 2) {
-        double u1 = ((double)(splitmix64(&s) >> 11) + 1.0) * (1.0 / 9007199254740993.0);
-        double u2 = (double)(splitmix64(&s) >> 11) * (1.0 / 9007199254740992.0);
-        double rad = sqrt(-2.0 * log(u1));
-        x[i] = (float)((double)mu + (double)sigma * rad * cos(two_pi * u2));
-        if (i + 1 < n)
-            x[i + 1] = (float)((double)mu + (double)sigma * rad * sin(two_pi * u2));
-    }
-}

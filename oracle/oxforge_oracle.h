@@ -121,12 +121,6 @@ void orc_fill_random(float *x, size_t n, uint32_t seed);
 void orc_fill_seq(float *x, size_t n, int ascending);
 void orc_causal_mask(float *m, size_t rows, size_t cols);
 
-/* Deterministic synthetic inputs shared by tests and bench:
- * SplitMix64 -> uniform(lo,hi) via a 24-bit mantissa, N(mu,sigma) via
- * Box-Muller.  Not reference code (the reference seeds from rand::random). */
-void orc_fill_uniform(float *x, size_t n, uint64_t seed, float lo, float hi);
-void orc_fill_normal(float *x, size_t n, uint64_t seed, float mu, float sigma);
-
 #ifdef __cplusplus
 }
 #endif

@@ -42,6 +42,16 @@ __device__ __forceinline__ float wave_sum(float v) {
            (readlane(v, 32) + readlane(v, 48));
 }
 
+// Integer sum over the 64 lanes (wraps modulo 2^32); wave-uniform.
+__device__ __forceinline__ unsigned wave_sum_u32(unsigned v) {
+    v += (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, DPP_QUAD_1032, 0xF, 0xF, false);
+    v += (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, DPP_QUAD_2301, 0xF, 0xF, false);
+    v += (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, DPP_ROW_HALF_MIRROR, 0xF, 0xF, false);
+    v += (unsigned)__builtin_amdgcn_update_dpp(0, (int)v, DPP_ROW_MIRROR, 0xF, 0xF, false);
+    return ((unsigned)__builtin_amdgcn_readlane((int)v, 0) + (unsigned)__builtin_amdgcn_readlane((int)v, 16)) +
+           ((unsigned)__builtin_amdgcn_readlane((int)v, 32) + (unsigned)__builtin_amdgcn_readlane((int)v, 48));
+}
+
 // Max over the 64 lanes; the result is wave-uniform.
 __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, dpp_mov<DPP_QUAD_1032>(v));

@@ -251,24 +251,44 @@ __device__ __forceinline__ void act_backward_body(const float* __restrict__ dy,
     }
 }
 
-// Per-workgroup count of positions where l != r (compare_vectors,
-// reduction.rs:132-174, but over every element; the reference keeps only
-// block 0's verdict).  Counts are exact in f32 up to 2^24 per workgroup.
+// Count of positions where l != r (compare_vectors, reduction.rs:132-174,
+// but over every element; the reference keeps only block 0's verdict).
+// Counts are integers throughout: per-workgroup partials in `part` (u32),
+// summed in u64 by count_final_body.  With one workgroup the kernel writes
+// the count itself, as the f32 nearest to it (exact up to 2^24).
 __device__ __forceinline__ void count_neq_body(const float* __restrict__ l,
                                                const float* __restrict__ r, long long n,
+                                               unsigned* __restrict__ part,
                                                float* __restrict__ out) {
-    __shared__ float part[EW_THREADS / 64];
+    __shared__ unsigned wsum[EW_THREADS / 64];
     const long long tid = (long long)blockIdx.x * EW_THREADS + threadIdx.x;
     const long long stride = (long long)gridDim.x * EW_THREADS;
-    float acc = 0.0f;
-    for (long long i = tid; i < n; i += stride) acc += (l[i] == r[i]) ? 0.0f : 1.0f;
-    acc = wave_sum(acc);
-    if (lane_id() == 0) part[threadIdx.x >> 6] = acc;
+    unsigned acc = 0;
+    for (long long i = tid; i < n; i += stride) acc += (l[i] == r[i]) ? 0u : 1u;
+    acc = wave_sum_u32(acc);
+    if (lane_id() == 0) wsum[threadIdx.x >> 6] = acc;
     __syncthreads();
     if (threadIdx.x == 0) {
-        float t = part[0];
-        for (int w = 1; w < (EW_THREADS >> 6); w++) t += part[w];
-        out[blockIdx.x] = t;
+        unsigned long long t = 0;
+        for (int w = 0; w < (EW_THREADS >> 6); w++) t += wsum[w];
+        if (gridDim.x == 1) out[0] = (float)t;
+        else part[blockIdx.x] = (unsigned)t;
+    }
+}
+
+// Sum of `n` u32 partial counts in u64; writes the f32 nearest to the total.
+__device__ __forceinline__ void count_final_body(const unsigned* __restrict__ part, int n,
+                                                 float* __restrict__ out) {
+    __shared__ unsigned long long wsum[EW_THREADS / 64];
+    unsigned long long acc = 0;
+    for (int i = threadIdx.x; i < n; i += EW_THREADS) acc += part[i];
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_down(acc, off, 64);
+    if (lane_id() == 0) wsum[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long t = 0;
+        for (int w = 0; w < (EW_THREADS >> 6); w++) t += wsum[w];
+        out[0] = (float)t;
     }
 }
 

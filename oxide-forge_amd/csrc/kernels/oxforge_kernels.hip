@@ -200,8 +200,13 @@ FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_sgd_s(float* p, const floa
     sgd_body<false>(p, g, n, lr);
 }
 FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_count_neq(const float* l, const float* r,
-                                                                long long n, float* out) {
-    count_neq_body(l, r, n, out);
+                                                                long long n, unsigned* part,
+                                                                float* out) {
+    count_neq_body(l, r, n, part, out);
+}
+FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_count_final(const unsigned* part, int n,
+                                                                  float* out) {
+    count_final_body(part, n, out);
 }
 FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_causal_mask(float* m, int rows, int cols) {
     causal_mask_body(m, rows, cols);

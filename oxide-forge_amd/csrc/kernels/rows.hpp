@@ -64,9 +64,6 @@ __device__ __forceinline__ float max4(float4 a) {
 #define F4_APPLY(dst, a, EXPR_X, EXPR_Y, EXPR_Z, EXPR_W) \
     do { dst.x = (EXPR_X); dst.y = (EXPR_Y); dst.z = (EXPR_Z); dst.w = (EXPR_W); } while (0)
 
-// Loads row `row` into the register arrays of the register path (fill
-// values past cols: -FLT_MAX for softmax, 0 otherwise).  Streaming loads:
-// the forward kernels overwrite the row in place.
 // Row `row` into the register arrays of the register path, as loaded:
 // every lane loads (past cols it reloads the row's first float4), and
 // row_mask then puts the fill values (-FLT_MAX for softmax, 0 otherwise)
@@ -134,23 +131,34 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
         }
     }
     // gamma / beta of float4 column group i (preloaded, or read per use).
+    // Read per use, a group past cols reads the row's first group instead,
+    // so the load stays in bounds wherever a caller evaluates it.
     auto gamma4 = [&](int i) -> float4 {
         if constexpr (PRELOAD) return gm[i];
-        else return *reinterpret_cast<const float4*>(a.gamma + (i * 64 + lane) * 4);
+        else {
+            const int c = (i * 64 + lane) * 4;
+            return *reinterpret_cast<const float4*>(a.gamma + (c < cols ? c : 0));
+        }
     };
     auto beta4 = [&](int i) -> float4 {
         if constexpr (PRELOAD && USES_BETA) return bt[i];
-        else return *reinterpret_cast<const float4*>(a.beta + (i * 64 + lane) * 4);
+        else {
+            const int c = (i * 64 + lane) * 4;
+            return *reinterpret_cast<const float4*>(a.beta + (c < cols ? c : 0));
+        }
     };
     static_assert(!PARTIALS || OP == ROW_LAYER_NORM_BWD || OP == ROW_RMS_NORM_BWD,
                   "only the norm backward kernels produce column partials");
-    // The backward's g = dy * gamma for float4 group i of the current row.  Kept in registers between the two passes where
-    // that fits: at 8 float4 per lane the partial kernels would otherwise
-    // exceed 256 VGPRs and spill (the LayerNorm backward at [4096,2048]
-    // took 38.7 us spilling against 23-28 us recomputing).
+    // The backward's g = dy * gamma for float4 group i of the current row;
+    // past cols (ok false) it is 0 and gamma is not read.  Kept in registers
+    // between the two passes where that fits: at 8 float4 per lane the
+    // partial kernels would otherwise exceed 256 VGPRs and spill (the
+    // LayerNorm backward at [4096,2048] took 38.7 us spilling against
+    // 23-28 us recomputing).
     constexpr bool KEEP_G = VPT <= 4;
-    auto gdy = [&](int i, float4 dy) -> float4 {
+    auto gdy = [&](int i, float4 dy, bool ok) -> float4 {
         if (!a.gamma) return dy;
+        if (!ok) return make_float4(0.f, 0.f, 0.f, 0.f);
         const float4 gm = gamma4(i);
         return make_float4(dy.x * gm.x, dy.y * gm.y, dy.z * gm.z, dy.w * gm.w);
     };
@@ -263,7 +271,7 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                 float sa = 0.0f, sb = 0.0f;
 #pragma unroll
                 for (int i = 0; i < VPT; i++) {
-                    const float4 gi = gdy(i, g[i]);
+                    const float4 gi = gdy(i, g[i], ok[i]);
                     if constexpr (KEEP_G) keep[i] = gi;
                     F4_APPLY(v[i], v[i], v[i].x * rstd, v[i].y * rstd, v[i].z * rstd,
                              v[i].w * rstd);
@@ -280,7 +288,7 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                     const int c = (i * 64 + lane) * 4;
                     float4 gi;
                     if constexpr (KEEP_G) gi = keep[i];
-                    else gi = gdy(i, g[i]);
+                    else gi = gdy(i, g[i], true);
                     float4 o;
                     F4_APPLY(o, v[i], scale * fmaf(v[i].x, nsb, fmaf(n, gi.x, nsa)),
                              scale * fmaf(v[i].y, nsb, fmaf(n, gi.y, nsa)),
@@ -341,7 +349,7 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
             float q = 0.0f, d = 0.0f;
 #pragma unroll
             for (int i = 0; i < VPT; i++) {
-                const float4 gi = gdy(i, g[i]);
+                const float4 gi = gdy(i, g[i], ok[i]);
                 if constexpr (KEEP_G) keep[i] = gi;
                 q += fmaf(v[i].x, v[i].x, v[i].y * v[i].y) + fmaf(v[i].z, v[i].z, v[i].w * v[i].w);
                 d += fmaf(v[i].x, gi.x, v[i].y * gi.y) + fmaf(v[i].z, gi.z, v[i].w * gi.w);
@@ -357,7 +365,7 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                 const int c = (i * 64 + lane) * 4;
                 float4 gi;
                 if constexpr (KEEP_G) gi = keep[i];
-                else gi = gdy(i, g[i]);
+                else gi = gdy(i, g[i], true);
                 float4 o;
                 F4_APPLY(o, v[i], fmaf(v[i].x, ncorr, gi.x * inv), fmaf(v[i].y, ncorr, gi.y * inv),
                          fmaf(v[i].z, ncorr, gi.z * inv), fmaf(v[i].w, ncorr, gi.w * inv));

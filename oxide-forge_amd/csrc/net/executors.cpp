@@ -492,8 +492,6 @@ QkvProjection::QkvProjection(Linear query, Linear key, Linear value,
 
 QkvProjection::Projected QkvProjection::project(const Matrix& query_input,
                                                 const Matrix& key_value_input, CudaRuntime& rt) {
-    // attention.rs:65-94: three Linear::forward, here as one batched launch
-    // on the primary stream when the three products share a shape.
     Projected p;
     Linear* lins[3] = {&query_, &key_, &value_};
     const Matrix* ins[3] = {&query_input, &key_value_input, &key_value_input};
@@ -505,7 +503,16 @@ QkvProjection::Projected QkvProjection::project(const Matrix& query_input,
         same = same && ins[z]->rows() == ins[0]->rows() && ins[z]->cols() == ins[0]->cols() &&
                outs[z]->cols() == outs[0]->cols();
     }
-    if (same) {
+    if (streams_) {
+        // attention.rs:65-94: the extra streams wait for the primary stream,
+        // then Linear::forward of Q, K and V on streams 0, 1 and 2.
+        wait_for_query_key(rt);
+        wait_for_value(rt);
+        rt.fork_streams(*streams_);
+        for (int z = 0; z < 3; z++)
+            lins[z]->forward_into(*ins[z], nullptr, *outs[z], rt, &(*streams_)[z]);
+        joined_qk_ = joined_v_ = false;
+    } else if (same) {
         forge_gemm_problem probs[3];
         for (int z = 0; z < 3; z++) probs[z] = lins[z]->forward_problem(*ins[z], *outs[z]);
         check(forge_gemm_batch_f32(rt.raw(), nullptr, 0, 0, ins[0]->rows(), outs[0]->cols(),
@@ -517,10 +524,20 @@ QkvProjection::Projected QkvProjection::project(const Matrix& query_input,
     return p;
 }
 
-// The projections ran on the primary stream: nothing to join.
-void QkvProjection::wait_for_query_key(CudaRuntime&) {}
+// attention.rs:96-102: the primary stream waits for the Q and K streams,
+// then for the V stream.  Nothing to wait for when the projections ran on
+// the primary stream.
+void QkvProjection::wait_for_query_key(CudaRuntime& rt) {
+    if (joined_qk_) return;
+    rt.join_streams({(*streams_)[0], (*streams_)[1]});
+    joined_qk_ = true;
+}
 
-void QkvProjection::wait_for_value(CudaRuntime&) {}
+void QkvProjection::wait_for_value(CudaRuntime& rt) {
+    if (joined_v_) return;
+    rt.join_streams({(*streams_)[2]});
+    joined_v_ = true;
+}
 
 // ============================================================== Attention
 

@@ -1533,14 +1533,16 @@ extern "C" forge_status forge_compare(forge_runtime* rt, forge_stream* s, forge_
     unsigned g = grid_for(nn, EW_THREADS * 4, 1024);
     if (g == 1)
         return launch_args(rt, s, "forge_count_neq", dim3(1), dim3(EW_THREADS), 0,
-                           (const float*)l.ptr, (const float*)r.ptr, nn, out.ptr);
+                           (const float*)l.ptr, (const float*)r.ptr, nn, (unsigned*)nullptr,
+                           out.ptr);
     float* ws;
     FORGE_TRY(workspace(rt, s, g, &ws));
+    unsigned* part = reinterpret_cast<unsigned*>(ws);
     FORGE_TRY(launch_args(rt, s, "forge_count_neq", dim3(g), dim3(EW_THREADS), 0,
-                          (const float*)l.ptr, (const float*)r.ptr, nn, ws));
-    long long gn = g;
-    return launch_args(rt, s, "forge_reduce_sum", dim3(1), dim3(EW_THREADS), 0, (const float*)ws,
-                       gn, out.ptr);
+                          (const float*)l.ptr, (const float*)r.ptr, nn, part, out.ptr));
+    int gn = (int)g;
+    return launch_args(rt, s, "forge_count_final", dim3(1), dim3(EW_THREADS), 0,
+                       (const unsigned*)part, gn, out.ptr);
 }
 
 extern "C" forge_status forge_fill_seq(forge_runtime* rt, forge_stream* s, forge_slice x, size_t n,

@@ -92,7 +92,7 @@ def dispatcher_kernel_names():
                "exp_shift", "half_sq", "identity"):
         names += [f"forge_map_{op}_v", f"forge_map_{op}_s"]
     names += ["forge_fill_random", "forge_act_backward_v", "forge_act_backward_s",
-              "forge_count_neq", "forge_sgd_v", "forge_sgd_s"]
+              "forge_count_neq", "forge_count_final", "forge_sgd_v", "forge_sgd_s"]
     names += ["forge_fill_v", "forge_fill_s", "forge_fill_seq", "forge_causal_mask",
               "forge_sum_cols_v", "forge_sum_cols_s", "forge_sum_cols_final", "forge_sum_cols_final2",
               "forge_sum_cols_final_v", "forge_sum_cols_final2_v",

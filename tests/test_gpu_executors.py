@@ -13,6 +13,7 @@ import oxforge
 from oracle import executors as ex
 from oracle import oracle as orc
 from oxforge import net
+from oxforge import synth
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-4
@@ -28,16 +29,16 @@ def rel(a, b):
 
 
 def make_params(S, H, F, O, seed, bias=True, affine=True, norm=net.LAYER):
-    p = {"WQ": orc.xavier(H, H, seed), "WK": orc.xavier(H, H, seed + 1),
-         "WV": orc.xavier(H, H, seed + 2), "POS": orc.xavier(S, H, seed + 3),
-         "W1": orc.xavier(H, F, seed + 4), "W2": orc.xavier(F, H, seed + 5),
-         "WO": orc.xavier(H, O, seed + 6)}
+    p = {"WQ": synth.xavier(H, H, seed), "WK": synth.xavier(H, H, seed + 1),
+         "WV": synth.xavier(H, H, seed + 2), "POS": synth.xavier(S, H, seed + 3),
+         "W1": synth.xavier(H, F, seed + 4), "W2": synth.xavier(F, H, seed + 5),
+         "WO": synth.xavier(H, O, seed + 6)}
     for i, (k, n) in enumerate((("BQ", H), ("BK", H), ("BV", H), ("B1", F), ("B2", H), ("BO", O))):
-        p[k] = orc.normal((n,), seed + 10 + i, 0.0, 0.1) if bias else None
-    p["G1"] = orc.normal((H,), seed + 20, 1.0, 0.1) if affine else None
-    p["G2"] = orc.normal((H,), seed + 21, 1.0, 0.1) if affine else None
-    p["BE1"] = orc.normal((H,), seed + 22, 0.0, 0.1) if affine and norm == net.LAYER else None
-    p["BE2"] = orc.normal((H,), seed + 23, 0.0, 0.1) if affine and norm == net.LAYER else None
+        p[k] = synth.normal((n,), seed + 10 + i, 0.0, 0.1) if bias else None
+    p["G1"] = synth.normal((H,), seed + 20, 1.0, 0.1) if affine else None
+    p["G2"] = synth.normal((H,), seed + 21, 1.0, 0.1) if affine else None
+    p["BE1"] = synth.normal((H,), seed + 22, 0.0, 0.1) if affine and norm == net.LAYER else None
+    p["BE2"] = synth.normal((H,), seed + 23, 0.0, 0.1) if affine and norm == net.LAYER else None
     return p
 
 
@@ -45,8 +46,8 @@ def make_params(S, H, F, O, seed, bias=True, affine=True, norm=net.LAYER):
 def test_linear_c1_identity_no_bias(rt):
     """X [256,128] x W [128,64], identity, no bias."""
     say("linear C1")
-    X = orc.uniform((256, 128), 1)
-    W = orc.uniform((128, 64), 2)
+    X = synth.uniform((256, 128), 1)
+    W = synth.uniform((128, 64), 2)
     lin = net.Linear(rt, W)
     Y = lin.forward(rt.array(X)).numpy()
     ref, _ = ex.linear_forward(X, W)
@@ -57,9 +58,9 @@ def test_linear_c1_identity_no_bias(rt):
 def test_linear_forward_backward_learn(rt, act):
     say(f"linear act={act}")
     M, I, O = 96, 80, 48
-    X, W = orc.uniform((M, I), 3), orc.uniform((I, O), 4)
-    b, R = orc.uniform((O,), 5), orc.uniform((M, O), 6)
-    dY = orc.normal((M, O), 7)
+    X, W = synth.uniform((M, I), 3), synth.uniform((I, O), 4)
+    b, R = synth.uniform((O,), 5), synth.uniform((M, O), 6)
+    dY = synth.normal((M, O), 7)
     lin = net.Linear(rt, W, b, act)
     dX_, dR = rt.array(X), rt.array(R)
     pre = rt.empty((M, O))
@@ -81,7 +82,7 @@ def test_linear_forward_backward_learn(rt, act):
 
 
 def test_loss_rows(rt):
-    O, T = orc.normal((37, 21), 1), orc.normal((37, 21), 2)
+    O, T = synth.normal((37, 21), 1), synth.normal((37, 21), 2)
     out = rt.empty((37,))
     net.loss_rows(rt, rt.array(O), rt.array(T), out)
     assert rel(out.numpy(), ex.loss_rows(O, T)) <= 1e-5
@@ -94,9 +95,9 @@ def test_mlp_training(rt, res_range):
     dims = {None: [64, 96, 80, 48], (0, 2): [64, 96, 64, 48], (1, 3): [64, 96, 80, 96],
             (0, 3): [64, 96, 80, 64]}[res_range]
     acts = [1, 3, 0]
-    layers = [(orc.xavier(dims[i], dims[i + 1], 10 + i), orc.normal((dims[i + 1],), 20 + i, 0, 0.1),
+    layers = [(synth.xavier(dims[i], dims[i + 1], 10 + i), synth.normal((dims[i + 1],), 20 + i, 0, 0.1),
                acts[i]) for i in range(3)]
-    X, dY = orc.normal((50, dims[0]), 1), orc.normal((50, dims[-1]), 2)
+    X, dY = synth.normal((50, dims[0]), 1), synth.normal((50, dims[-1]), 2)
     m = net.Mlp(rt, layers, res_range, training=True)
     Y = m.forward(rt.array(X)).numpy()
     ref, ins, pres = ex.mlp_forward(layers, X, res_range)
@@ -129,7 +130,7 @@ def test_transformer_inference(rt, name, S, H, F, O, norm, kind, streams):
         for k in ("BQ", "BK", "BV", "B1", "B2", "BO"):
             n = {"B1": F, "BO": O}.get(k, H)
             p[k] = np.zeros(n, np.float32)
-    X = orc.normal((S, H), 4)
+    X = synth.normal((S, H), 4)
     T = net.Transformer(rt, p, S, H, F, O, norm, kind, streams)
     Y1 = T.forward(rt.array(X)).numpy()
     Y2 = T.forward(rt.array(X)).numpy()
@@ -138,6 +139,28 @@ def test_transformer_inference(rt, name, S, H, F, O, norm, kind, streams):
     err = rel(Y1, ref)
     print(f"  rel err {err:.3e}")
     assert err <= TOL
+
+
+@pytest.mark.parametrize("S,H,F,O,kind", [(64, 64, 256, 64, net.ENCODER_INFERENCE),
+                                           (96, 128, 256, 80, net.DECODER_INFERENCE),
+                                           (2048, 1024, 4096, 1024, net.ENCODER_INFERENCE)])
+def test_qkv_forked_streams_match_batched_bit_exact(rt, S, H, F, O, kind):
+    """qkv_streams=1 runs Q, K and V on three forked streams joined before the
+    scores and before A.V (attention.rs:65-102); qkv_streams=0 runs them as
+    one batched launch.  Same products in the same sum order: bit-identical,
+    on repeated forwards too (the second fork reuses the same streams)."""
+    say(f"qkv streams vs batched S={S} H={H} kind={kind}")
+    p = make_params(S, H, F, O, 41, bias=True, affine=True, norm=net.LAYER)
+    X = synth.normal((S, H), 5)
+    Ts = net.Transformer(rt, p, S, H, F, O, net.LAYER, kind, True)
+    Tb = net.Transformer(rt, p, S, H, F, O, net.LAYER, kind, False)
+    dX = rt.array(X)
+    outs = [Ts.forward(dX).numpy(), Ts.forward(dX).numpy(), Tb.forward(dX).numpy()]
+    assert np.array_equal(outs[0], outs[2]) and np.array_equal(outs[1], outs[2])
+    ref, _ = ex.transformer_forward(p, X, net.LAYER, causal=(kind == net.DECODER_INFERENCE))
+    assert rel(outs[0], ref) <= TOL
+    Ts.close()
+    Tb.close()
 
 
 TRAIN_CASES = [
@@ -152,8 +175,8 @@ TRAIN_CASES = [
 def test_transformer_training_step(rt, name, S, H, F, O, norm, bias, affine):
     say(f"training {name}")
     p = make_params(S, H, F, O, 50, bias=bias, affine=affine, norm=norm)
-    X = orc.normal((S, H), 5)
-    dY = orc.normal((S, O), 6)
+    X = synth.normal((S, H), 5)
+    dY = synth.normal((S, O), 6)
     lr = np.float32(1e-3)
     T = net.Transformer(rt, p, S, H, F, O, norm, net.ENCODER_TRAINING)
     Y = T.forward(rt.array(X)).numpy()
@@ -191,8 +214,8 @@ def test_transformer_training_c5_full_size(rt):
     p = make_params(S, H, F, O, 60, bias=True, affine=True, norm=net.LAYER)
     for k in ("BQ", "BK", "BV", "B1", "B2", "BO"):
         p[k] = np.zeros_like(p[k])
-    X = orc.normal((S, H), 7)
-    dY = orc.normal((S, O), 8)
+    X = synth.normal((S, H), 7)
+    dY = synth.normal((S, O), 8)
     T = net.Transformer(rt, p, S, H, F, O, net.LAYER, net.ENCODER_TRAINING)
     Y = T.forward(rt.array(X)).numpy()
     dXd = rt.empty((S, H))

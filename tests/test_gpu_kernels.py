@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 
 import oxforge
+from oxforge import synth
 from oracle import oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -43,8 +44,8 @@ def op_a(A, ta):
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_gemm_shapes_vs_oracle(rt, M, N, K, ta, tb):
     say(f"gemm M={M} N={N} K={K} ta={ta} tb={tb}")
-    A = orc.uniform((K, M) if ta else (M, K), 1 + M)
-    B = orc.uniform((N, K) if tb else (K, N), 2 + N)
+    A = synth.uniform((K, M) if ta else (M, K), 1 + M)
+    B = synth.uniform((N, K) if tb else (K, N), 2 + N)
     dA, dB, dC = rt.array(A), rt.array(B), rt.empty((M, N))
     if ta or tb:
         rt.gemm_ex(dA, dB, dC, M, N, K, trans_a=ta, trans_b=tb)
@@ -73,7 +74,7 @@ def test_gemm_small_integers_bit_exact(rt):
 
 def test_gemm_permutation_bit_exact(rt):
     say("gemm permutation 256x256x256")
-    A = orc.uniform((256, 256), 5)
+    A = synth.uniform((256, 256), 5)
     perm = np.random.default_rng(1).permutation(256)
     P = np.zeros((256, 256), np.float32)
     P[np.arange(256), perm] = 1.0
@@ -99,8 +100,8 @@ def test_gemm_short_slice_rejected(rt):
 @pytest.mark.parametrize("M,N,K", [(4096, 4096, 4096), (8192, 1024, 4096)])
 def test_gemm_full_size_sampled_rows(rt, M, N, K):
     say(f"gemm full size {M}x{N}x{K}")
-    A = orc.uniform((M, K), 3)
-    B = orc.uniform((K, N), 4)
+    A = synth.uniform((M, K), 3)
+    B = synth.uniform((K, N), 4)
     dA, dB, dC = rt.array(A), rt.array(B), rt.empty((M, N))
     rt.gemm(dA, dB, dC, M, N, K)
     C = dC.numpy()
@@ -125,12 +126,12 @@ def test_gemm_epilogue_matches_unfused_bit_exact(rt, M, N, K, ta, tb):
     256x128x2048 is computed as two K slices, so the split-K reduction's
     epilogue is covered too."""
     say(f"gemm epilogue M={M} N={N} K={K} ta={ta} tb={tb}")
-    A = orc.uniform((K, M) if ta else (M, K), 7)
-    B = orc.uniform((N, K) if tb else (K, N), 8)
-    bias = orc.uniform((N,), 9)
-    res = orc.uniform((M, N), 10)
-    aux = orc.uniform((M, N), 11)
-    W = orc.uniform((M, N), 12)
+    A = synth.uniform((K, M) if ta else (M, K), 7)
+    B = synth.uniform((N, K) if tb else (K, N), 8)
+    bias = synth.uniform((N,), 9)
+    res = synth.uniform((M, N), 10)
+    aux = synth.uniform((M, N), 11)
+    W = synth.uniform((M, N), 12)
     dA, dB = rt.array(A), rt.array(B)
     dbias, dres, daux = rt.array(bias), rt.array(res), rt.array(aux)
     for act, mop in [(oxforge.ACT_IDENTITY, None), (oxforge.ACT_GELU, oxforge.MAP_GELU),
@@ -182,7 +183,7 @@ def test_gemm_epilogue_matches_unfused_bit_exact(rt, M, N, K, ta, tb):
                                        (8192, 4096)])
 def test_transpose_bit_exact(rt, rows, cols):
     say(f"transpose {rows}x{cols}")
-    x = orc.uniform((rows, cols), rows + cols)
+    x = synth.uniform((rows, cols), rows + cols)
     dx, dt = rt.array(x), rt.empty((cols, rows))
     rt.transpose(dx, dt, rows, cols)
     t = dt.numpy()
@@ -195,7 +196,7 @@ def test_transpose_bit_exact(rt, rows, cols):
 
 def test_transpose_unaligned_view(rt):
     say("transpose unaligned view")
-    x = orc.uniform((1 + 40 * 24,), 3)
+    x = synth.uniform((1 + 40 * 24,), 3)
     dx = rt.array(x)
     v = dx.view(1, (40, 24))
     dt = rt.empty((24, 40))
@@ -211,8 +212,8 @@ ROW_SHAPES = [(4096, 1024), (5, 1), (7, 3), (33, 63), (9, 100), (64, 256), (17, 
 @pytest.mark.parametrize("rows,cols", ROW_SHAPES)
 def test_softmax_fwd_bwd(rt, rows, cols):
     say(f"softmax {rows}x{cols}")
-    x = orc.normal((rows, cols), 2)
-    g = orc.normal((rows, cols), 3)
+    x = synth.normal((rows, cols), 2)
+    g = synth.normal((rows, cols), 3)
     dx = rt.array(x)
     rt.softmax_rows(dx, rows, cols)
     p = dx.numpy()
@@ -226,10 +227,10 @@ def test_softmax_fwd_bwd(rt, rows, cols):
 @pytest.mark.parametrize("affine", [False, True])
 def test_layer_norm_fwd_bwd(rt, rows, cols, affine):
     say(f"layer_norm {rows}x{cols} affine={affine}")
-    x = orc.normal((rows, cols), 2)
-    dy = orc.normal((rows, cols), 3)
-    gam = orc.normal((cols,), 4, 1.0, 0.1) if affine else None
-    bet = orc.normal((cols,), 5, 0.0, 0.1) if affine else None
+    x = synth.normal((rows, cols), 2)
+    dy = synth.normal((rows, cols), 3)
+    gam = synth.normal((cols,), 4, 1.0, 0.1) if affine else None
+    bet = synth.normal((cols,), 5, 0.0, 0.1) if affine else None
     dgam = rt.array(gam) if affine else None
     dbet = rt.array(bet) if affine else None
     d = rt.array(x)
@@ -250,9 +251,9 @@ def test_layer_norm_fwd_bwd(rt, rows, cols, affine):
 @pytest.mark.parametrize("affine", [False, True])
 def test_rms_norm_fwd_bwd(rt, rows, cols, affine):
     say(f"rms_norm {rows}x{cols} affine={affine}")
-    x = orc.normal((rows, cols), 6)
-    dy = orc.normal((rows, cols), 7)
-    gam = orc.normal((cols,), 8, 1.0, 0.1) if affine else None
+    x = synth.normal((rows, cols), 6)
+    dy = synth.normal((rows, cols), 7)
+    gam = synth.normal((cols,), 8, 1.0, 0.1) if affine else None
     dgam = rt.array(gam) if affine else None
     d = rt.array(x)
     rt.rms_norm(d, rows, cols, gamma=dgam)
@@ -267,7 +268,7 @@ def test_rms_norm_fwd_bwd(rt, rows, cols, affine):
 def test_row_ops_reduce_to_reference_at_unit_affine(rt):
     """gamma = 1, beta = 0 reproduces the reference (no-affine) kernels bit for bit."""
     say("unit affine")
-    x = orc.normal((64, 1024), 9)
+    x = synth.normal((64, 1024), 9)
     ones, zeros = rt.array(np.ones(1024, np.float32)), rt.array(np.zeros(1024, np.float32))
     a, b = rt.array(x), rt.array(x)
     rt.layer_norm(a, 64, 1024)
@@ -281,7 +282,7 @@ def test_row_ops_reduce_to_reference_at_unit_affine(rt):
 
 def test_row_ops_unaligned_views(rt):
     say("row ops unaligned views")
-    x = orc.normal((1 + 12 * 40,), 10)
+    x = synth.normal((1 + 12 * 40,), 10)
     d = rt.array(x)
     v = d.view(1, (12, 40))
     rt.softmax_rows(v, 12, 40)
@@ -295,11 +296,11 @@ def test_norm_bwd_column_sums_across_launches(rt):
     dbeta alone and unaligned outputs must each match the oracle, and a
     repeated launch must reproduce its result bit for bit."""
     cols = 1024
-    gam_h = orc.normal((cols,), 31, 1.0, 0.1)
+    gam_h = synth.normal((cols,), 31, 1.0, 0.1)
     dgam = rt.array(gam_h)
     for rows in (4096, 8, 100, 1600, 4096, 1, 2056):
         say(f"norm bwd column sums rows={rows}")
-        x, dy = orc.normal((rows, cols), 32 + rows), orc.normal((rows, cols), 33 + rows)
+        x, dy = synth.normal((rows, cols), 32 + rows), synth.normal((rows, cols), 33 + rows)
         dX, dDY, dDX = rt.array(x), rt.array(dy), rt.empty((rows, cols))
         tol = TOL_ROW * max(1.0, np.sqrt(rows))
         rdx, rdg, rdb = orc.layer_norm_backward(x, dy, gam_h, want_params=True)
@@ -330,6 +331,52 @@ def test_norm_bwd_column_sums_across_launches(rt):
         assert np.max(np.abs(dDX.numpy() - rdx)) <= TOL_ROW
 
 
+# Aligned widths with cols % 4 == 0 that are not a multiple of 256 leave
+# lanes past the row end in the register kernels (v8, v16 and their
+# partial instances read gamma per use).  gamma sits in a buffer whose tail
+# past cols holds NaN: a kernel that read or used gamma beyond the row would
+# turn the row's results into NaN.
+MASKED_LANE_SHAPES = [(8, 1028), (8, 1540), (4, 2052), (4, 3000), (64, 1028), (300, 1540)]
+
+
+@pytest.mark.parametrize("rows,cols", MASKED_LANE_SHAPES)
+@pytest.mark.parametrize("params", [False, True])
+def test_norms_masked_lanes_read_no_gamma_past_row(rt, rows, cols, params):
+    say(f"norms masked lanes {rows}x{cols} params={params}")
+    pad = 4096
+    x = synth.normal((rows, cols), 41 + cols)
+    dy = synth.normal((rows, cols), 42 + cols)
+    gam = synth.normal((cols,), 43, 1.0, 0.1)
+    bet = synth.normal((cols,), 44, 0.0, 0.1)
+    gbuf = rt.array(np.concatenate([gam, np.full(pad, np.nan, np.float32)]))
+    bbuf = rt.array(np.concatenate([bet, np.full(pad, np.nan, np.float32)]))
+    dgam, dbet = gbuf.view(0, (cols,)), bbuf.view(0, (cols,))
+    tol = TOL_ROW * max(1.0, np.sqrt(rows))
+
+    d = rt.array(x)
+    rt.layer_norm(d, rows, cols, gamma=dgam, beta=dbet)
+    assert np.max(np.abs(d.numpy() - orc.layer_norm(x, gam, bet))) <= TOL_ROW
+    d = rt.array(x)
+    rt.rms_norm(d, rows, cols, gamma=dgam)
+    assert np.max(np.abs(d.numpy() - orc.rms_norm(x, gam))) <= TOL_ROW
+
+    dX, dDY, dDX = rt.array(x), rt.array(dy), rt.empty((rows, cols))
+    rdx, rdg, rdb = orc.layer_norm_backward(x, dy, gam, want_params=True)
+    pg, pb = (rt.empty((cols,)), rt.empty((cols,))) if params else (None, None)
+    rt.layer_norm_bwd(dX, dDY, dDX, rows, cols, gamma=dgam, dgamma=pg, dbeta=pb)
+    assert np.max(np.abs(dDX.numpy() - rdx)) <= TOL_ROW
+    if params:
+        assert np.max(np.abs(pg.numpy() - rdg)) <= tol
+        assert np.max(np.abs(pb.numpy() - rdb)) <= tol
+
+    rdx, rdg = orc.rms_norm_backward(x, dy, gam, want_params=True)
+    rg = rt.empty((cols,)) if params else None
+    rt.rms_norm_bwd(dX, dDY, dDX, rows, cols, gamma=dgam, dgamma=rg)
+    assert np.max(np.abs(dDX.numpy() - rdx)) <= TOL_ROW
+    if params:
+        assert np.max(np.abs(rg.numpy() - rdg)) <= tol
+
+
 # Outputs of 16M floats (64 MiB) and more are stored non-temporally; the
 # shapes above stay below that, these two tests cover the other path.
 NT_ROWS, NT_COLS = 16384, 1024
@@ -339,9 +386,9 @@ NT_ROWS, NT_COLS = 16384, 1024
 def test_row_kernels_at_nontemporal_size(rt, affine):
     rows, cols = NT_ROWS, NT_COLS
     say(f"row kernels {rows}x{cols} affine={affine}")
-    x, dy = orc.normal((rows, cols), 21), orc.normal((rows, cols), 22)
-    gam = orc.normal((cols,), 23, 1.0, 0.1) if affine else None
-    bet = orc.normal((cols,), 24, 0.0, 0.1) if affine else None
+    x, dy = synth.normal((rows, cols), 21), synth.normal((rows, cols), 22)
+    gam = synth.normal((cols,), 23, 1.0, 0.1) if affine else None
+    bet = synth.normal((cols,), 24, 0.0, 0.1) if affine else None
     dgam = rt.array(gam) if affine else None
     dbet = rt.array(bet) if affine else None
     col_tol = TOL_ROW * np.sqrt(rows)
@@ -382,7 +429,7 @@ def test_streaming_kernels_at_nontemporal_size(rt):
     rows, cols = NT_ROWS, NT_COLS
     n = rows * cols
     say(f"streaming kernels n={n}")
-    a, b = orc.normal((n,), 11), orc.normal((n,), 12)
+    a, b = synth.normal((n,), 11), synth.normal((n,), 12)
     da, db, do = rt.array(a), rt.array(b), rt.empty((n,))
     rt.binary(da, db, do, oxforge.ADD)
     assert np.array_equal(do.numpy(), a + b)
@@ -393,7 +440,7 @@ def test_streaming_kernels_at_nontemporal_size(rt):
     dp, dgr = rt.array(a), rt.array(b)
     rt.sgd_update(dp, dgr, 0.01)
     assert np.array_equal(dp.numpy(), a - np.float32(0.01) * b)
-    row = orc.normal((cols,), 13)
+    row = synth.normal((cols,), 13)
     dm = rt.array(a.reshape(rows, cols))
     rt.binary_assign_by_rows(dm, rt.array(row), rows, cols, oxforge.ADD)
     assert np.array_equal(dm.numpy(), a.reshape(rows, cols) + row[None, :])
@@ -403,8 +450,8 @@ def test_streaming_kernels_at_nontemporal_size(rt):
 @pytest.mark.parametrize("n", [4096 * 1024, 1, 7, 1001])
 def test_binary_bit_exact(rt, op, fn, n):
     say(f"binary op={op} n={n}")
-    a = orc.normal((n,), 1)
-    b = orc.normal((n,), 2)
+    a = synth.normal((n,), 1)
+    b = synth.normal((n,), 2)
     da, db, do = rt.array(a), rt.array(b), rt.empty((n,))
     rt.binary(da, db, do, op)
     assert np.array_equal(do.numpy(), fn(a, b))
@@ -414,8 +461,8 @@ def test_binary_bit_exact(rt, op, fn, n):
 
 def test_binary_unaligned_bit_exact(rt):
     say("binary unaligned")
-    a = orc.normal((1001,), 1)
-    b = orc.normal((1001,), 2)
+    a = synth.normal((1001,), 1)
+    b = synth.normal((1001,), 2)
     da, db, do = rt.array(a), rt.array(b), rt.empty((1001,))
     rt.binary(da.view(1, (1000,)), db.view(1, (1000,)), do.view(1, (1000,)), oxforge.MUL)
     assert np.array_equal(do.numpy()[1:], a[1:] * b[1:])
@@ -428,8 +475,8 @@ def test_binary_unaligned_bit_exact(rt):
                                        (65536, 12), (65537, 7)])
 def test_by_rows_bit_exact(rt, op, fn, rows, cols):
     say(f"by_rows op={op} {rows}x{cols}")
-    m = orc.normal((rows, cols), 3)
-    row = orc.normal((cols,), 4)
+    m = synth.normal((rows, cols), 3)
+    row = synth.normal((cols,), 4)
     dm, dr = rt.array(m), rt.array(row)
     rt.binary_assign_by_rows(dm, dr, rows, cols, op)
     assert np.array_equal(dm.numpy(), fn(m, row[None, :]))
@@ -444,7 +491,7 @@ TRANS_MAPS = [(oxforge.MAP_GELU, 0.0), (oxforge.MAP_GELU_D, 0.0), (oxforge.MAP_S
 @pytest.mark.parametrize("op,p0", EXACT_MAPS + TRANS_MAPS)
 def test_maps(rt, op, p0):
     say(f"map op={op}")
-    x = orc.normal((4096 * 1024 + 3,), 5, 0.0, 2.0)
+    x = synth.normal((4096 * 1024 + 3,), 5, 0.0, 2.0)
     d = rt.array(x)
     rt.map(d, op, p0)
     ref = orc.map_(x, op, p0)
@@ -471,7 +518,7 @@ def test_sum_rows_cols(rt, rows, cols):
     # integer inputs: every partial sum is exact, so any order is bit-exact
     assert np.array_equal(dr.numpy(), m.astype(np.int64).sum(axis=1).astype(np.float32))
     assert np.array_equal(dc.numpy(), m.astype(np.int64).sum(axis=0).astype(np.float32))
-    mf = orc.normal((rows, cols), 6)
+    mf = synth.normal((rows, cols), 6)
     dm2 = rt.array(mf)
     rt.sum_cols(dm2, dc, rows, cols)
     rt.sum_rows(dm2, dr, rows, cols)
@@ -548,7 +595,7 @@ def test_fills_and_causal_mask(rt):
     assert np.all(d.numpy() == 2.5)
     z = rt.zeros((77,))
     assert np.all(z.numpy() == 0)
-    m = orc.normal((300, 257), 1)
+    m = synth.normal((300, 257), 1)
     dm = rt.array(m)
     rt.causal_mask(dm, 300, 257)
     assert np.array_equal(dm.numpy(), orc.causal_mask(m))
@@ -571,8 +618,8 @@ def test_streams_fork_join(rt):
     stream then consumes all three results (QkvProjection::project order)."""
     say("streams fork/join")
     streams = rt.streams_create(3)
-    A = orc.uniform((256, 512), 1)
-    Ws = [orc.uniform((512, 256), 10 + i) for i in range(3)]
+    A = synth.uniform((256, 512), 1)
+    Ws = [synth.uniform((512, 256), 10 + i) for i in range(3)]
     dA = rt.array(A)
     dWs = [rt.array(w) for w in Ws]
     outs = [rt.empty((256, 256)) for _ in range(3)]
@@ -601,8 +648,8 @@ def test_fill_random_bit_exact(rt):
                                      (0, orc.MAP_IDENTITY)])
 def test_activation_backward(rt, act, dop):
     say(f"activation_backward act={act}")
-    dy = orc.normal((1001,), 1)
-    z = orc.normal((1001,), 2, 0.0, 2.0)
+    dy = synth.normal((1001,), 1)
+    z = synth.normal((1001,), 2, 0.0, 2.0)
     g = rt.empty((1001,))
     rt.activation_backward(rt.array(dy), rt.array(z), g, act)
     if act == 0:
@@ -614,7 +661,7 @@ def test_activation_backward(rt, act, dop):
 
 def test_compare_counts_every_mismatch(rt):
     say("compare")
-    a = orc.normal((300_000,), 1)
+    a = synth.normal((300_000,), 1)
     b = a.copy()
     b[[0, 1023, 1024, 299_999]] += 1.0
     out = rt.empty((1,))
@@ -626,8 +673,8 @@ def test_compare_counts_every_mismatch(rt):
 
 def test_softmax_bwd_scaled_equals_bwd_then_scale(rt):
     say("softmax_bwd_scaled")
-    p = orc.softmax_rows(orc.normal((64, 300), 1))
-    g = orc.normal((64, 300), 2)
+    p = orc.softmax_rows(synth.normal((64, 300), 1))
+    g = synth.normal((64, 300), 2)
     s = np.float32(1.0 / np.sqrt(np.float32(1024)))
     dp, dg = rt.array(p), rt.array(g)
     a, b = rt.empty((64, 300)), rt.empty((64, 300))
@@ -648,7 +695,7 @@ def test_gemm_split_k_vs_oracle(rt, tile, splits, M, N, K):
     """K slices summed in slice order: the same bar as any GEMM; one slice is
     the plain product bit for bit."""
     say(f"gemm split-K {tile} splits={splits} {M}x{N}x{K}")
-    A, B = orc.uniform((M, K), 5), orc.uniform((K, N), 6)
+    A, B = synth.uniform((M, K), 5), synth.uniform((K, N), 6)
     dA, dB, dC = rt.array(A), rt.array(B), rt.empty((M, N))
     rt.gemm_split(tile, splits, dA, dB, dC, M, N, K)
     C = dC.numpy()
@@ -679,9 +726,9 @@ def test_gemm_every_tile_instance(rt, tile, ta, tb):
     bm, bn = (int(x) for x in tile.split("x")[:2])
     M, N, K = 2 * bm, 2 * bn, 192
     say(f"gemm tile {tile} ta={ta} tb={tb} {M}x{N}x{K}")
-    A = orc.uniform((K, M) if ta else (M, K), 31)
-    B = orc.uniform((N, K) if tb else (K, N), 32)
-    bias, res = orc.uniform((N,), 33), orc.uniform((M, N), 34)
+    A = synth.uniform((K, M) if ta else (M, K), 31)
+    B = synth.uniform((N, K) if tb else (K, N), 32)
+    bias, res = synth.uniform((N,), 33), synth.uniform((M, N), 34)
     dA, dB, dbias, dres = rt.array(A), rt.array(B), rt.array(bias), rt.array(res)
     dZ, dY, dpre = rt.empty((M, N)), rt.empty((M, N)), rt.empty((M, N))
     rt.gemm_ex_tile(tile, dA, dB, dZ, M, N, K, trans_a=ta, trans_b=tb)
@@ -721,8 +768,8 @@ def test_gemm_kernel_name_names_the_kernel_that_runs(rt, M, N, K, ta, tb, fused)
     plain = not fused and ab == "nn"
     assert kernel.endswith("_e") != plain, name
     tag = kernel[len(prefix):].removesuffix("_e") + (f"@{cap}" if cap else "")
-    A = orc.uniform((K, M) if ta else (M, K), 41)
-    B = orc.uniform((N, K) if tb else (K, N), 42)
+    A = synth.uniform((K, M) if ta else (M, K), 41)
+    B = synth.uniform((N, K) if tb else (K, N), 42)
     dA, dB, dC, dT = rt.array(A), rt.array(B), rt.empty((M, N)), rt.empty((M, N))
     if plain:
         rt.gemm(dA, dB, dC, M, N, K)
@@ -742,7 +789,7 @@ def test_gemm_occupancy_cap_keeps_results(rt, tile):
     M, N, K = 512, 512, 256
     say(f"gemm occupancy cap {tile}")
     base = tile.partition("@")[0]
-    A, B, bias = orc.uniform((M, K), 51), orc.uniform((K, N), 52), orc.uniform((N,), 53)
+    A, B, bias = synth.uniform((M, K), 51), synth.uniform((K, N), 52), synth.uniform((N,), 53)
     dA, dB, dbias = rt.array(A), rt.array(B), rt.array(bias)
     out = [rt.empty((M, N)) for _ in range(4)]
     rt.gemm_tile(base, dA, dB, out[0], M, N, K)
@@ -797,7 +844,7 @@ def test_sgd_update_bit_exact(rt, n):
     """param - lr * grad with two roundings, as the reference's clone / scale /
     subtract sequence (linear.rs:385-390)."""
     say(f"sgd_update n={n}")
-    p, g = orc.normal((n,), 1), orc.normal((n,), 2)
+    p, g = synth.normal((n,), 1), synth.normal((n,), 2)
     lr = np.float32(3e-3)
     dp = rt.array(p)
     rt.sgd_update(dp, rt.array(g), float(lr))
@@ -812,8 +859,8 @@ def test_sgd_update_bit_exact(rt, n):
 @pytest.mark.parametrize("rows,cols", [(64, 1024), (33, 70)])
 def test_norm_out_of_place_equals_in_place(rt, rows, cols):
     say(f"norm out-of-place {rows}x{cols}")
-    x = orc.normal((rows, cols), 3)
-    gm, bt = orc.normal((cols,), 4, 1.0, 0.1), orc.normal((cols,), 5, 0.0, 0.1)
+    x = synth.normal((rows, cols), 3)
+    gm, bt = synth.normal((cols,), 4, 1.0, 0.1), synth.normal((cols,), 5, 0.0, 0.1)
     dgm, dbt = rt.array(gm), rt.array(bt)
     for name, args in (("layer", (dgm, dbt)), ("rms", (dgm,))):
         src, inplace, out = rt.array(x), rt.array(x), rt.empty((rows, cols))
@@ -832,9 +879,9 @@ def test_transposed_operands_bit_identical_to_materialised_transpose(rt, M, N, K
     """NT/TN GEMMs read A^T/B^T in place; the products equal the reference's
     transpose-then-GEMM sequence bit for bit."""
     say(f"nt/tn vs transpose {M}x{N}x{K}")
-    At = orc.uniform((K, M), 1)
-    Bt = orc.uniform((N, K), 2)
-    B = orc.uniform((K, N), 3)
+    At = synth.uniform((K, M), 1)
+    Bt = synth.uniform((N, K), 2)
+    B = synth.uniform((K, N), 3)
     dAt, dBt, dB = rt.array(At), rt.array(Bt), rt.array(B)
     dA, dBn = rt.empty((M, K)), rt.empty((K, N))
     rt.transpose(dAt, dA, K, M)

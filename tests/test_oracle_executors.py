@@ -152,3 +152,20 @@ def test_loss_rows_closed_form():
     O = np.array([[1.0, 2.0], [3.0, 5.0]])
     T = np.array([[0.0, 0.0], [3.0, 3.0]])
     assert np.allclose(ex.loss_rows(O, T), [(0.5 + 2.0) / 2, (0 + 2.0) / 2])
+
+
+@pytest.mark.parametrize("rms", [True, False])
+def test_c_mirror_block_forward_matches_f64_executor(rms):
+    """The C-kernel composition of the block forward (oracle.transformer_forward,
+    timed by bench.py as the host baseline) equals the f64 executor oracle to
+    f32 rounding: same wiring, same score scale, same activation."""
+    from oracle import oracle as orc
+
+    S, H, F, O = 24, 16, 40, 12
+    p64 = params(S, H, F, O, seed=3, affine=False)
+    p = {k: (None if v is None else v.astype(np.float32)) for k, v in p64.items()}
+    X = rnd(9, S, H, scale=1.0).astype(np.float32)
+    got = orc.transformer_forward(p, X, rms=rms)
+    ref, _ = ex.transformer_forward(p, X, ex.RMS if rms else ex.LAYER)
+    assert got.shape == (S, O)
+    assert np.max(np.abs(got - ref)) <= 1e-5 * max(1.0, np.abs(ref).max())

@@ -255,14 +255,6 @@ def test_fills_and_mask():
     assert np.array_equal(m, ref)
 
 
-def test_synthetic_generators_are_deterministic():
-    a = orc.uniform((1000,), 5)
-    assert np.array_equal(a, orc.uniform((1000,), 5))
-    assert a.min() >= -1 and a.max() < 1 and abs(a.mean()) < 0.1
-    n = orc.normal((20000,), 6)
-    assert abs(n.mean()) < 0.03 and abs(n.std() - 1) < 0.03
-
-
 def test_fill_random_hash_restated_independently():
     # common.rs:3-9 in wrapping u32 arithmetic, restated with numpy uint64
     # masks; elementwise.rs:40-41 divides by u32::MAX as f32.
