@@ -335,6 +335,23 @@ forge_status forge_layer_norm_bwd(forge_runtime *rt, forge_stream *stream,
                                   forge_slice gamma, forge_slice dx,
                                   forge_slice dgamma, forge_slice dbeta,
                                   size_t rows, size_t cols, float eps);
+/* forge_layer_norm_bwd that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, checks and results (bit-identical) as
+ * forge_layer_norm_bwd; the dgamma/dbeta partial rows go to a device scratch
+ * array of 2^21 floats (8 MiB) that each GPU holds until the process ends,
+ * instead of the stream's workspace.  Shapes whose partial rows need more
+ * are FORGE_EINVAL; at any row count, 16-byte-aligned rows with cols % 4 ==
+ * 0 fit up to 2048 columns and other rows up to 1024.  The array is shared by every call
+ * on one GPU, from every runtime and stream: calls that overlap on one GPU
+ * race and must be serialised by the caller.  Nothing in it needs to start
+ * at zero (every partial row is written before it is read). */
+forge_status forge_layer_norm_bwd_noalloc(forge_runtime *rt, forge_stream *stream,
+                                          forge_slice x, forge_slice dy,
+                                          forge_slice gamma, forge_slice dx,
+                                          forge_slice dgamma, forge_slice dbeta,
+                                          size_t rows, size_t cols, float eps);
 /* Matrix::rms_norm (norm.rs:50-69 -> row.rs:349-396), in place. */
 forge_status forge_rms_norm_rows(forge_runtime *rt, forge_stream *stream,
                                  forge_slice x, forge_slice gamma, size_t rows,

@@ -8,6 +8,7 @@
 // alignment (the reference chooses its launch geometry in the container
 // layer, e.g. matrix.rs:133-176 and norm.rs:8-24).
 #include "oxforge.h"
+#include "noalloc_scratch.h"
 
 #include <hip/hip_runtime_api.h>
 #include <dlfcn.h>
@@ -120,6 +121,10 @@ struct forge_runtime {
     size_t lds_bytes = 0;
     int clock_khz = 0;
     char arch[256] = {0};
+    // Device address of this device's no-allocation scratch array
+    // (noalloc_scratch.hip), resolved at creation; null if that failed.
+    float* noalloc_scratch = nullptr;
+    hipError_t noalloc_status = hipSuccess;
 };
 
 namespace {
@@ -285,6 +290,10 @@ extern "C" forge_status forge_runtime_create(int device, const char* module_path
         rt->clock_khz = prop.clockRate;
         snprintf(rt->arch, sizeof rt->arch, "%s", prop.gcnArchName);
     }
+    // Once per runtime, with the device current: the address of the device's
+    // copy of the no-allocation scratch array.  A failure here disables only
+    // forge_layer_norm_bwd_noalloc, which then reports it.
+    rt->noalloc_status = forge_internal_noalloc_scratch(&rt->noalloc_scratch);
     *out = rt;
     return FORGE_OK;
 }
@@ -935,9 +944,12 @@ unsigned norm_bwd_blocks(forge_runtime* rt) {
 
 // Shared launcher of the six row kernels.  For the norm backward kernels
 // with dgamma/dbeta requested, the partial rows land in the stream's
-// workspace and are summed by sum_cols_impl.
+// workspace and are summed by sum_cols_impl; with `scratch` given they land
+// there instead (scratch_len floats, nothing is allocated) and a shape that
+// needs more is FORGE_EINVAL.
 forge_status row_launch(forge_runtime* rt, forge_stream* s, const char* op, RowArgs a,
-                        float* dgamma, float* dbeta) {
+                        float* dgamma, float* dbeta, float* scratch = nullptr,
+                        size_t scratch_len = 0) {
     if (a.rows == 0 || a.cols == 0) {
         if (dgamma) FORGE_TRY(forge_fill(rt, s, forge_slice{dgamma, (size_t)a.cols}, 0.0f));
         if (dbeta) FORGE_TRY(forge_fill(rt, s, forge_slice{dbeta, (size_t)a.cols}, 0.0f));
@@ -962,7 +974,17 @@ forge_status row_launch(forge_runtime* rt, forge_stream* s, const char* op, RowA
         grid = std::min<unsigned>(blocks_needed, norm_bwd_blocks(rt));
         prow = vpt ? grid : (size_t)grid * ROW_WAVES;
         size_t per = prow * (size_t)a.cols;
-        FORGE_TRY(workspace(rt, s, per * 2 + sum_cols_scratch(prow, (size_t)a.cols), &ws));
+        const size_t need = per * 2 + sum_cols_scratch(prow, (size_t)a.cols);
+        if (scratch) {
+            if (need > scratch_len)
+                return fail(FORGE_EINVAL,
+                            "%s with dgamma/dbeta at [%d, %d] needs %zu floats of scratch; the "
+                            "no-allocation scratch holds %zu",
+                            op, a.rows, a.cols, need, scratch_len);
+            ws = scratch;
+        } else {
+            FORGE_TRY(workspace(rt, s, need, &ws));
+        }
         a.pgamma = dgamma ? ws : nullptr;
         a.pbeta = dbeta ? ws + per : nullptr;
         if (vpt) shmem = (size_t)waves * (size_t)a.cols * sizeof(float);
@@ -1286,11 +1308,11 @@ extern "C" forge_status forge_layer_norm_rows(forge_runtime* rt, forge_stream* s
     return forge_layer_norm_rows_out(rt, s, x, x, gamma, beta, rows, cols, eps);
 }
 
-extern "C" forge_status forge_layer_norm_bwd(forge_runtime* rt, forge_stream* s, forge_slice x,
-                                             forge_slice dy, forge_slice gamma, forge_slice dx,
-                                             forge_slice dgamma, forge_slice dbeta, size_t rows,
-                                             size_t cols, float eps) {
-    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+namespace {
+forge_status layer_norm_bwd_impl(forge_runtime* rt, forge_stream* s, forge_slice x,
+                                 forge_slice dy, forge_slice gamma, forge_slice dx,
+                                 forge_slice dgamma, forge_slice dbeta, size_t rows, size_t cols,
+                                 float eps, float* scratch, size_t scratch_len) {
     FORGE_TRY(check_rows(rows, cols));
     FORGE_TRY(need(x, rows * cols, "layer_norm_bwd x"));
     FORGE_TRY(need(dy, rows * cols, "layer_norm_bwd dy"));
@@ -1299,7 +1321,30 @@ extern "C" forge_status forge_layer_norm_bwd(forge_runtime* rt, forge_stream* s,
     FORGE_TRY(need_opt(dgamma, cols, "layer_norm_bwd dgamma"));
     FORGE_TRY(need_opt(dbeta, cols, "layer_norm_bwd dbeta"));
     RowArgs a{x.ptr, dx.ptr, dy.ptr, gamma.ptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, eps, 1.0f};
-    return row_launch(rt, s, "layer_norm_bwd", a, dgamma.ptr, dbeta.ptr);
+    return row_launch(rt, s, "layer_norm_bwd", a, dgamma.ptr, dbeta.ptr, scratch, scratch_len);
+}
+}  // namespace
+
+extern "C" forge_status forge_layer_norm_bwd(forge_runtime* rt, forge_stream* s, forge_slice x,
+                                             forge_slice dy, forge_slice gamma, forge_slice dx,
+                                             forge_slice dgamma, forge_slice dbeta, size_t rows,
+                                             size_t cols, float eps) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    return layer_norm_bwd_impl(rt, s, x, dy, gamma, dx, dgamma, dbeta, rows, cols, eps, nullptr,
+                               0);
+}
+
+extern "C" forge_status forge_layer_norm_bwd_noalloc(forge_runtime* rt, forge_stream* s,
+                                                     forge_slice x, forge_slice dy,
+                                                     forge_slice gamma, forge_slice dx,
+                                                     forge_slice dgamma, forge_slice dbeta,
+                                                     size_t rows, size_t cols, float eps) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    if (!rt->noalloc_scratch)
+        return fail(FORGE_EHIP, "no-allocation scratch unavailable: hipGetSymbolAddress: %s",
+                    hipGetErrorString(rt->noalloc_status));
+    return layer_norm_bwd_impl(rt, s, x, dy, gamma, dx, dgamma, dbeta, rows, cols, eps,
+                               rt->noalloc_scratch, FORGE_NOALLOC_SCRATCH_FLOATS);
 }
 
 extern "C" forge_status forge_rms_norm_rows_out(forge_runtime* rt, forge_stream* s,

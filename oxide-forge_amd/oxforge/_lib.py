@@ -125,6 +125,8 @@ SIGNATURES = {
                                   c_float],
     "forge_layer_norm_bwd": [RT, ST, Slice, Slice, Slice, Slice, Slice, Slice, c_size_t,
                              c_size_t, c_float],
+    "forge_layer_norm_bwd_noalloc": [RT, ST, Slice, Slice, Slice, Slice, Slice, Slice, c_size_t,
+                                     c_size_t, c_float],
     "forge_rms_norm_rows": [RT, ST, Slice, Slice, c_size_t, c_size_t, c_float],
     "forge_rms_norm_rows_out": [RT, ST, Slice, Slice, Slice, c_size_t, c_size_t, c_float],
     "forge_rms_norm_bwd": [RT, ST, Slice, Slice, Slice, Slice, Slice, c_size_t, c_size_t,
