@@ -135,7 +135,7 @@ def secondary(rt, steps, warmup, extended):
     return out
 
 
-def secondary_rows_at_scale(rt, steps, warmup):
+def secondary_rows_at_scale(rt, steps, warmup, min_launches=32):
     """The same row and streaming kernels on X [65536, 1024] (256 MiB per
     operand, two rotating sets: 512 MiB, beyond the 256 MiB MALL).  At the
     C2 size a launch lasts 7-15 us and its ramp-up and drain are a large
@@ -172,7 +172,7 @@ def secondary_rows_at_scale(rt, steps, warmup):
                                                                   oxforge.ADD)),
     }
     for name, (nbytes, fn) in cases.items():
-        ms = time_launches(rt, fn, max(steps, 32), warmup)
+        ms = time_launches(rt, fn, max(steps, min_launches), warmup)
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[f"{name}_65536x1024"] = {"gbs": round(gbs, 1), "us": round(ms * 1e3, 1),
                                      "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
@@ -181,7 +181,7 @@ def secondary_rows_at_scale(rt, steps, warmup):
     return out
 
 
-def secondary_rows(rt, steps, warmup, extended=True):
+def secondary_rows(rt, steps, warmup, extended=True, min_launches=256):
     """C2 row / elementwise kernels on X [4096, 1024], 32 rotating buffer
     sets (512 MiB per operand) so the MALL cannot serve them."""
     import oxforge
@@ -223,7 +223,7 @@ def secondary_rows(rt, steps, warmup, extended=True):
     # one-off idle gap before the first launch reaches the emptied queue
     # (host launch latency after the synchronisation) is amortised.
     for name, (nbytes, fn) in cases.items():
-        ms = time_launches(rt, fn, max(steps, 256), warmup)
+        ms = time_launches(rt, fn, max(steps, min_launches), warmup)
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[f"{name}_4096x1024"] = {"gbs": round(gbs, 1), "us": round(ms * 1e3, 2),
                                     "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
@@ -461,9 +461,10 @@ def profile_workload(rt, name, steps, warmup):
         T.close()
         return {"workload": name, "ms": round(ms, 4)}
     if name == "rows":
-        return {"workload": name, "results": secondary_rows(rt, steps, warmup)}
+        return {"workload": name, "results": secondary_rows(rt, steps, warmup, min_launches=1)}
     if name == "rows65536":
-        return {"workload": name, "results": secondary_rows_at_scale(rt, steps, warmup)}
+        return {"workload": name,
+                "results": secondary_rows_at_scale(rt, steps, warmup, min_launches=1)}
     raise SystemExit(f"unknown profile workload {name}")
 
 

@@ -414,6 +414,11 @@ forge_status forge_sum_cols(forge_runtime *rt, forge_stream *stream,
  * caller reads it back when it needs the scalar). */
 forge_status forge_reduce_sum(forge_runtime *rt, forge_stream *stream,
                               forge_slice x, size_t n, forge_slice out);
+/* DeviceSpan::map_sum (span.rs:144-149, 335-359 -> reduction.rs:43-91):
+ * out[0] = sum over i < n of f(x[i]) on the device, f one of the map
+ * functors of forge_map (the closures the reference passes); 0 for n == 0. */
+forge_status forge_map_sum(forge_runtime *rt, forge_stream *stream, forge_slice x,
+                           size_t n, forge_map_op op, float p0, forge_slice out);
 forge_status forge_reduce_max(forge_runtime *rt, forge_stream *stream,
                               forge_slice x, size_t n, forge_slice out);
 

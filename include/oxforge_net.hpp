@@ -108,6 +108,100 @@ private:
     forge_slice s_{nullptr, 0};
 };
 
+// ------------------------------------------------------------------ spans
+// The closures the reference passes to for_each / map_sum (span.rs:261-299,
+// elementwise.rs:70-79, reduction.rs:43-91) are device code compiled into
+// its kernels; here they are the functor set of forge_map: x * p0, x + p0,
+// GELU and its derivative, ReLU, SiLU (and derivatives), exp(x - p0),
+// 0.5 x^2, identity.
+struct MapFn {
+    forge_map_op op;
+    float p0;
+    static MapFn scale(float v) { return {FORGE_MAP_SCALE, v}; }
+    static MapFn add(float v) { return {FORGE_MAP_ADD, v}; }
+    static MapFn exp_shift(float m) { return {FORGE_MAP_EXP_SHIFT, m}; }
+    static MapFn half_square() { return {FORGE_MAP_HALF_SQ, 0.0f}; }
+    static MapFn identity() { return {FORGE_MAP_IDENTITY, 0.0f}; }
+    static MapFn of(forge_map_op op, float p0 = 0.0f) { return {op, p0}; }
+};
+
+class DeviceSpanMut;
+
+// DeviceSpan<'a, f32> (span.rs:82-160): a non-owning, read-only view of
+// `len` floats of a DeviceBuffer from `offset`.  Dropping it frees nothing;
+// it must not outlive the buffer it views (the reference's borrow).
+class DeviceSpan {
+public:
+    // span.rs:88-98 with check_range (span.rs:412-416): offset and
+    // offset + len within the buffer, else Error (the reference panics).
+    static DeviceSpan from_buffer(const DeviceBuffer& buffer, size_t offset, size_t len);
+    // span.rs:120-122: the whole buffer in chunks of chunk_size (the last
+    // may be shorter); chunk_size 0 is an Error.
+    static std::vector<DeviceSpan> chunks(const DeviceBuffer& buffer, size_t chunk_size);
+
+    size_t len() const { return s_.len; }
+    bool is_empty() const { return s_.len == 0; }
+    // The {ptr, len} kernel argument (DeviceSliceDescriptor, span.rs:7-11).
+    forge_slice descriptor() const { return s_; }
+    // Copies into a new pool buffer on the primary stream (span.rs:124-133).
+    DeviceBuffer to_buffer(CudaRuntime& rt) const;
+    DeviceBuffer to_buffer_async(CudaRuntime& rt) const;
+    // Host scalars (span.rs:135-149, 301-359): empty spans give 0 (sum,
+    // map_sum) and f32::MIN (max).
+    float sum(CudaRuntime& rt) const;
+    float max(CudaRuntime& rt) const;
+    float map_sum(CudaRuntime& rt, MapFn f) const;
+
+private:
+    explicit DeviceSpan(forge_slice s) : s_(s) {}
+    friend class DeviceSpanMut;
+    forge_slice s_;
+};
+
+// DeviceSpanMut<'a, f32> (span.rs:161-299): the exclusive, writable view.
+class DeviceSpanMut {
+public:
+    static DeviceSpanMut from_buffer(DeviceBuffer& buffer, size_t offset, size_t len);
+    static std::vector<DeviceSpanMut> chunks(DeviceBuffer& buffer, size_t chunk_size);
+
+    size_t len() const { return s_.len; }
+    bool is_empty() const { return s_.len == 0; }
+    forge_slice descriptor() const { return s_; }
+    DeviceSpan into_span() const { return DeviceSpan(s_); }
+    DeviceBuffer to_buffer(CudaRuntime& rt) const;
+    DeviceBuffer to_buffer_async(CudaRuntime& rt) const;
+    // x = f(x) in place (span.rs:245-279); nothing is launched when empty.
+    void for_each(CudaRuntime& rt, MapFn f);
+    void for_each_on(CudaRuntime& rt, const CudaStream* stream, MapFn f);
+    void scale(float value, CudaRuntime& rt) { for_each(rt, MapFn::scale(value)); }
+    float sum(CudaRuntime& rt) const { return into_span().sum(rt); }
+    float max(CudaRuntime& rt) const { return into_span().max(rt); }
+    float map_sum(CudaRuntime& rt, MapFn f) const { return into_span().map_sum(rt, f); }
+
+private:
+    explicit DeviceSpanMut(forge_slice s) : s_(s) {}
+    forge_slice s_;
+};
+
+// VectorView<'a> (container.rs:17-19, vector_view.rs:6-47): a row of a
+// Matrix (Matrix::row_views) or any span, with the Vector operations.
+class VectorView {
+public:
+    explicit VectorView(DeviceSpanMut span) : span_(span) {}
+    size_t len() const { return span_.len(); }
+    void add_scalar(float value, CudaRuntime& rt) { span_.for_each(rt, MapFn::add(value)); }
+    void scale(float value, CudaRuntime& rt) { span_.scale(value, rt); }
+    void for_each(CudaRuntime& rt, MapFn f) { span_.for_each(rt, f); }
+    float sum(CudaRuntime& rt) const { return span_.sum(rt); }
+    float map_sum(CudaRuntime& rt, MapFn f) const { return span_.map_sum(rt, f); }
+    // vector_view.rs:41-46: max, exp(x - max), sum, scale by 1 / sum.
+    void softmax(CudaRuntime& rt);
+    DeviceSpanMut& span() { return span_; }
+
+private:
+    DeviceSpanMut span_;
+};
+
 // ------------------------------------------------------------- containers
 // Vector (container.rs:13-15, vector.rs, vector_runtime.rs).
 class Vector {
@@ -118,6 +212,11 @@ public:
     Vector& operator=(Vector&&) = default;
 
     size_t len() const { return buffer_.len(); }
+    // vector.rs:11-17.
+    DeviceSpan as_span() const { return DeviceSpan::from_buffer(buffer_, 0, buffer_.len()); }
+    DeviceSpan span(size_t offset, size_t len) const {
+        return DeviceSpan::from_buffer(buffer_, offset, len);
+    }
     std::vector<float> to_host(CudaRuntime& rt) const;
     void add_scalar(float value, CudaRuntime& rt);
     void scale(float value, CudaRuntime& rt);
@@ -152,6 +251,8 @@ public:
     Matrix& operator=(Matrix&&) = default;
 
     std::vector<float> to_host(CudaRuntime& rt) const;
+    // convert.rs:8-13: one view per row, in row order.
+    std::vector<VectorView> row_views();
     size_t rows() const { return rows_; }
     size_t cols() const { return cols_; }
     size_t len() const { return buffer_.len(); }
@@ -211,6 +312,8 @@ public:
     // (CudaStream::join(primary), e.g. linear.rs:126).
     void stream_join_primary(const CudaStream* waiter);
     DeviceBuffer concat_buffers(const std::vector<const DeviceBuffer*>& buffers);
+    // span.rs:483-523: the spans' elements back to back in a new buffer.
+    DeviceBuffer concat_buffers_from_span(const std::vector<DeviceSpan>& spans);
     DeviceBuffer clone_buffer(const DeviceBuffer& buffer);
 
     // Matrix constructors and operations.

@@ -476,6 +476,27 @@ __device__ __forceinline__ void reduce_body(const float* __restrict__ x, long lo
     }
 }
 
+// slice_map_sum (reduction.rs:43-91): per-workgroup partial sums of f(x)
+// for one of the map functors, in the reduce_body order; the partials are
+// then summed by reduce_body.
+template <int OP>
+__device__ __forceinline__ void map_sum_body(const float* __restrict__ x, long long n, float p0,
+                                             float* __restrict__ out) {
+    __shared__ float part[EW_THREADS / 64];
+    const long long tid = (long long)blockIdx.x * EW_THREADS + threadIdx.x;
+    const long long stride = (long long)gridDim.x * EW_THREADS;
+    float acc = 0.0f;
+    for (long long i = tid; i < n; i += stride) acc += map_one<OP>(x[i], p0);
+    acc = wave_sum(acc);
+    if (lane_id() == 0) part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float t = part[0];
+        for (int w = 1; w < (EW_THREADS >> 6); w++) t += part[w];
+        out[blockIdx.x] = t;
+    }
+}
+
 // ------------------------------------------------------------- transpose
 
 // out[c, r] = in[r, c] for in [rows, cols] (layout.rs:8-55).  A workgroup of

@@ -109,19 +109,24 @@ GEMM_GUARDED_KERNEL(forge_gemm_nn_64x64x16_2x2_g, 64, 64, 16, 2, 2, false, false
     ROW_KERNEL(forge_row_##OPNAME##_v16, OP, 16, false)           \
     FORGE_KERNEL void __launch_bounds__(256) forge_row_##OPNAME##_loop(RowArgs a) { row_kernel_loop<OP>(a); }
 // Norm backward instances that also emit per-workgroup dgamma/dbeta
-// partials: 8 waves per workgroup, each walking its rows with the next row
-// prefetched (measured on MI355X at [4096,1024]: 8 waves x 256 workgroups,
-// two rows per wave, beats 16 waves or one row per wave by 1.5-3 us).  The
-// runtime launches them with ROW_PARTIAL_WAVES * 64 threads.
-#define ROW_PARTIAL_KERNEL(NAME, OP, VPT)                                               \
-    FORGE_KERNEL void __launch_bounds__(ROW_PARTIAL_WAVES * 64) NAME(RowArgs a) {       \
-        row_kernel_reg<OP, VPT, true, ROW_PARTIAL_WAVES>(a);                            \
+// partials, one workgroup per CU, each wave walking its rows grid-stride:
+//   _p:  8 waves; at 1, 2 and 8 float4 per lane the next row is prefetched
+//        into registers, at 4 it is not (measured on MI355X, [2048..32768,
+//        1024]: 0.5-2% faster without);
+//   _p4: 4 waves, no prefetch, for 4 float4 per lane and at least 256 rows
+//        per CU ([65536,1024]: LayerNorm backward 133.5 against 135.1 us
+//        with 8 waves and 138.5 with 8 waves and prefetch).
+// The runtime launches them with WAVES * 64 threads.
+#define ROW_PARTIAL_KERNEL(NAME, OP, VPT, W, PF)                                         \
+    FORGE_KERNEL void __launch_bounds__(W * 64) NAME(RowArgs a) {                        \
+        row_kernel_reg<OP, VPT, true, W, PF>(a);                                         \
     }
-#define ROW_PARTIAL_KERNELS(OPNAME, OP)                           \
-    ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v1_p, OP, 1)          \
-    ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v2_p, OP, 2)          \
-    ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v4_p, OP, 4)          \
-    ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v8_p, OP, 8)
+#define ROW_PARTIAL_KERNELS(OPNAME, OP)                                                  \
+    ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v1_p, OP, 1, ROW_PARTIAL_WAVES, true)        \
+    ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v2_p, OP, 2, ROW_PARTIAL_WAVES, true)        \
+    ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v4_p, OP, 4, ROW_PARTIAL_WAVES, false)       \
+    ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v4_p4, OP, 4, 4, false)                      \
+    ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v8_p, OP, 8, ROW_PARTIAL_WAVES, true)
 
 ROW_KERNELS(softmax, ROW_SOFTMAX)
 ROW_KERNELS(layer_norm, ROW_LAYER_NORM)
@@ -131,6 +136,7 @@ ROW_KERNELS(layer_norm_bwd, ROW_LAYER_NORM_BWD)
 ROW_KERNELS(rms_norm_bwd, ROW_RMS_NORM_BWD)
 ROW_PARTIAL_KERNELS(layer_norm_bwd, ROW_LAYER_NORM_BWD)
 ROW_PARTIAL_KERNELS(rms_norm_bwd, ROW_RMS_NORM_BWD)
+
 
 // ------------------------------------------------------------ elementwise
 #define BINARY_KERNELS(OPNAME, OP)                                                          \
@@ -158,17 +164,22 @@ BINARY_KERNELS(div, OP_DIV)
     FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_map_##OPNAME##_s(         \
         float* x, long long n, float p0) { map_body<OP, false>(x, n, p0); }
 
-MAP_KERNELS(scale, MAP_SCALE)
-MAP_KERNELS(add, MAP_ADD)
-MAP_KERNELS(gelu, MAP_GELU)
-MAP_KERNELS(gelu_d, MAP_GELU_D)
-MAP_KERNELS(relu, MAP_RELU)
-MAP_KERNELS(relu_d, MAP_RELU_D)
-MAP_KERNELS(silu, MAP_SILU)
-MAP_KERNELS(silu_d, MAP_SILU_D)
-MAP_KERNELS(exp_shift, MAP_EXP_SHIFT)
-MAP_KERNELS(half_sq, MAP_HALF_SQ)
-MAP_KERNELS(identity, MAP_IDENTITY)
+#define MAP_SUM_KERNEL(OPNAME, OP)                                                    \
+    FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_map_sum_##OPNAME(              \
+        const float* x, long long n, float p0, float* out) { map_sum_body<OP>(x, n, p0, out); }
+#define MAP_KERNELS_ALL(OPNAME, OP) MAP_KERNELS(OPNAME, OP) MAP_SUM_KERNEL(OPNAME, OP)
+
+MAP_KERNELS_ALL(scale, MAP_SCALE)
+MAP_KERNELS_ALL(add, MAP_ADD)
+MAP_KERNELS_ALL(gelu, MAP_GELU)
+MAP_KERNELS_ALL(gelu_d, MAP_GELU_D)
+MAP_KERNELS_ALL(relu, MAP_RELU)
+MAP_KERNELS_ALL(relu_d, MAP_RELU_D)
+MAP_KERNELS_ALL(silu, MAP_SILU)
+MAP_KERNELS_ALL(silu_d, MAP_SILU_D)
+MAP_KERNELS_ALL(exp_shift, MAP_EXP_SHIFT)
+MAP_KERNELS_ALL(half_sq, MAP_HALF_SQ)
+MAP_KERNELS_ALL(identity, MAP_IDENTITY)
 
 FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_fill_v(float* x, long long n, float v) {
     fill_body<true>(x, n, v);

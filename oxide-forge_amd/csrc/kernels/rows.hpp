@@ -102,7 +102,8 @@ __device__ __forceinline__ void row_mask(const bool* ok, float4* v, float4* g) {
 // grid-stride.  The partial-producing backward kernels with at most 8 waves
 // walk several rows per wave, so they prefetch the next row's registers
 // before reducing the current one.
-template <int OP, int VPT, bool PARTIALS, int WAVES = ROW_WAVES>
+template <int OP, int VPT, bool PARTIALS, int WAVES = ROW_WAVES,
+          bool PREFETCH = PARTIALS && WAVES <= 8>
 __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // scalar
@@ -175,7 +176,6 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
     // Prefetch the next row when a wave walks several rows (the partial
     // kernels, whose grid is capped at one workgroup per CU).  Wider
     // workgroups would not leave the registers for it.
-    constexpr bool PREFETCH = PARTIALS && WAVES <= 8;
     const bool nt = (long long)a.rows * cols >= STREAM_NT_MIN;
     const int stride = gridDim.x * WAVES;
     int row = blockIdx.x * WAVES + wave;

@@ -3,6 +3,7 @@
 // Mirrors src/cuda/runtime.rs, src/cuda/span.rs and src/cuda/container/*.rs.
 // Every device operation is one call into include/oxforge.h; shape checks
 // that the reference makes with assert! throw oxforge::Error here.
+#include <algorithm>
 #include <cstring>
 #include <random>
 
@@ -44,6 +45,126 @@ DeviceBuffer& DeviceBuffer::operator=(DeviceBuffer&& o) noexcept {
 
 DeviceBuffer::~DeviceBuffer() {
     if (rt_ && s_.ptr) (void)forge_recycle(rt_->raw(), s_);
+}
+
+// ------------------------------------------------------------------ spans
+
+// span.rs:412-416.
+static void check_range(size_t buffer_len, size_t offset, size_t len) {
+    require(offset <= buffer_len, "device span offset out of bounds");
+    require(len <= buffer_len - offset, "device span exceeds its buffer");
+}
+
+// span.rs:427-439: [0, len) in chunks of chunk_size, the last one shorter.
+static std::vector<forge_slice> split_slices(float* base, size_t len, size_t chunk_size) {
+    require(chunk_size > 0, "device span chunk size must be non-zero");
+    std::vector<forge_slice> out;
+    out.reserve((len + chunk_size - 1) / chunk_size);
+    for (size_t off = 0; off < len; off += chunk_size)
+        out.push_back(forge_slice{base + off, std::min(chunk_size, len - off)});
+    return out;
+}
+
+static DeviceBuffer copy_span(CudaRuntime& rt, forge_slice s) {
+    DeviceBuffer out = rt.get_uninit_buffer(s.len);
+    if (s.len) check(forge_memcpy_d2d(rt.raw(), nullptr, out.slice(), s, s.len), "span to_buffer");
+    return out;
+}
+
+// A device scalar read back to the host: the reference's reduce_*_buffer
+// ends with to_host_vec (span.rs:361-411).
+static float scalar_to_host(CudaRuntime& rt, const DeviceBuffer& out) {
+    float h = 0.0f;
+    check(forge_memcpy_d2h(rt.raw(), &h, out.slice(), 1), "reduce to host");
+    return h;
+}
+
+DeviceSpan DeviceSpan::from_buffer(const DeviceBuffer& buffer, size_t offset, size_t len) {
+    check_range(buffer.len(), offset, len);
+    return DeviceSpan(forge_slice{buffer.ptr() + offset, len});
+}
+
+std::vector<DeviceSpan> DeviceSpan::chunks(const DeviceBuffer& buffer, size_t chunk_size) {
+    std::vector<DeviceSpan> out;
+    for (forge_slice s : split_slices(buffer.ptr(), buffer.len(), chunk_size))
+        out.push_back(DeviceSpan(s));
+    return out;
+}
+
+DeviceBuffer DeviceSpan::to_buffer(CudaRuntime& rt) const { return copy_span(rt, s_); }
+DeviceBuffer DeviceSpan::to_buffer_async(CudaRuntime& rt) const { return copy_span(rt, s_); }
+
+float DeviceSpan::sum(CudaRuntime& rt) const {
+    if (s_.len == 0) return 0.0f;  // span.rs:302-304
+    DeviceBuffer out = rt.get_uninit_buffer(1);
+    check(forge_reduce_sum(rt.raw(), nullptr, s_, s_.len, out.slice()), "DeviceSpan::sum");
+    return scalar_to_host(rt, out);
+}
+
+float DeviceSpan::max(CudaRuntime& rt) const {
+    if (s_.len == 0) return -3.40282347e38f;  // f32::MIN, span.rs:319-321
+    DeviceBuffer out = rt.get_uninit_buffer(1);
+    check(forge_reduce_max(rt.raw(), nullptr, s_, s_.len, out.slice()), "DeviceSpan::max");
+    return scalar_to_host(rt, out);
+}
+
+float DeviceSpan::map_sum(CudaRuntime& rt, MapFn f) const {
+    if (s_.len == 0) return 0.0f;  // span.rs:339-341
+    DeviceBuffer out = rt.get_uninit_buffer(1);
+    check(forge_map_sum(rt.raw(), nullptr, s_, s_.len, f.op, f.p0, out.slice()),
+          "DeviceSpan::map_sum");
+    return scalar_to_host(rt, out);
+}
+
+DeviceSpanMut DeviceSpanMut::from_buffer(DeviceBuffer& buffer, size_t offset, size_t len) {
+    check_range(buffer.len(), offset, len);
+    return DeviceSpanMut(forge_slice{buffer.ptr() + offset, len});
+}
+
+std::vector<DeviceSpanMut> DeviceSpanMut::chunks(DeviceBuffer& buffer, size_t chunk_size) {
+    std::vector<DeviceSpanMut> out;
+    for (forge_slice s : split_slices(buffer.ptr(), buffer.len(), chunk_size))
+        out.push_back(DeviceSpanMut(s));
+    return out;
+}
+
+DeviceBuffer DeviceSpanMut::to_buffer(CudaRuntime& rt) const { return copy_span(rt, s_); }
+DeviceBuffer DeviceSpanMut::to_buffer_async(CudaRuntime& rt) const { return copy_span(rt, s_); }
+
+void DeviceSpanMut::for_each(CudaRuntime& rt, MapFn f) { for_each_on(rt, nullptr, f); }
+
+void DeviceSpanMut::for_each_on(CudaRuntime& rt, const CudaStream* stream, MapFn f) {
+    if (s_.len == 0) return;  // span.rs:266-268
+    check(forge_map(rt.raw(), stream_raw(stream), s_, s_.len, f.op, f.p0), "for_each");
+}
+
+void VectorView::softmax(CudaRuntime& rt) {
+    const float m = span_.max(rt);
+    span_.for_each(rt, MapFn::exp_shift(m));
+    const float total = span_.sum(rt);
+    span_.scale(1.0f / total, rt);
+}
+
+std::vector<VectorView> Matrix::row_views() {
+    std::vector<VectorView> out;
+    if (cols_ == 0) return out;
+    for (DeviceSpanMut& s : DeviceSpanMut::chunks(buffer_, cols_)) out.push_back(VectorView(s));
+    return out;
+}
+
+DeviceBuffer CudaRuntime::concat_buffers_from_span(const std::vector<DeviceSpan>& spans) {
+    size_t total = 0;
+    for (const DeviceSpan& s : spans) total += s.len();
+    DeviceBuffer result = get_uninit_buffer(total);
+    size_t offset = 0;
+    for (const DeviceSpan& s : spans) {
+        if (s.len() == 0) continue;
+        forge_slice dst{result.ptr() + offset, s.len()};
+        check(forge_memcpy_d2d(rt_, nullptr, dst, s.descriptor(), s.len()),
+              "concat_buffers_from_span");
+        offset += s.len();
+    }
+    return result;
 }
 
 // ---------------------------------------------------------------- runtime

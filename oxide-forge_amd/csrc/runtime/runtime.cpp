@@ -963,7 +963,10 @@ forge_status row_launch(forge_runtime* rt, forge_stream* s, const char* op, RowA
     char name[80];
     // Waves per workgroup: the register partial kernels use ROW_PARTIAL_WAVES
     // (one LDS-combined partial row per workgroup); everything else ROW_WAVES.
-    const int waves = (partials && vpt) ? ROW_PARTIAL_WAVES : ROW_WAVES;
+    // At 4 float4 per lane and at least 256 rows per CU the partial kernel
+    // runs 4 waves per workgroup (the _p4 instance).
+    const bool p4 = partials && vpt == 4 && (size_t)a.rows >= 256 * (size_t)rt->cu_count;
+    const int waves = (partials && vpt) ? (p4 ? 4 : ROW_PARTIAL_WAVES) : ROW_WAVES;
     unsigned blocks_needed = (unsigned)((a.rows + waves - 1) / waves);
     unsigned grid;
     size_t shmem = 0;
@@ -988,7 +991,7 @@ forge_status row_launch(forge_runtime* rt, forge_stream* s, const char* op, RowA
         a.pgamma = dgamma ? ws : nullptr;
         a.pbeta = dbeta ? ws + per : nullptr;
         if (vpt) shmem = (size_t)waves * (size_t)a.cols * sizeof(float);
-        if (vpt) snprintf(name, sizeof name, "forge_row_%s_v%d_p", op, vpt);
+        if (vpt) snprintf(name, sizeof name, "forge_row_%s_v%d_p%s", op, vpt, p4 ? "4" : "");
         else snprintf(name, sizeof name, "forge_row_%s_loop", op);
     } else {
         grid = std::min<unsigned>(blocks_needed, 1u << 20);
@@ -1513,6 +1516,29 @@ forge_status reduce_impl(forge_runtime* rt, forge_stream* s, forge_slice x, size
     return launch_args(rt, s, name, dim3(1), dim3(EW_THREADS), 0, (const float*)ws, gn, out.ptr);
 }
 }  // namespace
+
+extern "C" forge_status forge_map_sum(forge_runtime* rt, forge_stream* s, forge_slice x,
+                                      size_t n, forge_map_op op, float p0, forge_slice out) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    const char* nm = map_name(op);
+    if (!nm) return fail(FORGE_EINVAL, "unknown map op %d", (int)op);
+    FORGE_TRY(need(x, n, "map_sum x"));
+    FORGE_TRY(need(out, 1, "map_sum out"));
+    char name[64];
+    snprintf(name, sizeof name, "forge_map_sum_%s", nm);
+    long long nn = (long long)n;
+    unsigned g = grid_for(nn, EW_THREADS * 4, 1024);
+    if (g == 1)
+        return launch_args(rt, s, name, dim3(1), dim3(EW_THREADS), 0, (const float*)x.ptr, nn, p0,
+                           out.ptr);
+    float* ws;
+    FORGE_TRY(workspace(rt, s, g, &ws));
+    FORGE_TRY(launch_args(rt, s, name, dim3(g), dim3(EW_THREADS), 0, (const float*)x.ptr, nn, p0,
+                          ws));
+    long long gn = g;
+    return launch_args(rt, s, "forge_reduce_sum", dim3(1), dim3(EW_THREADS), 0, (const float*)ws,
+                       gn, out.ptr);
+}
 
 extern "C" forge_status forge_reduce_sum(forge_runtime* rt, forge_stream* s, forge_slice x,
                                          size_t n, forge_slice out) {

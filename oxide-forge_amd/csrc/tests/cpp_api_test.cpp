@@ -12,6 +12,7 @@
 
 #include <unistd.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -58,7 +59,21 @@ static void group(const char* name, int before) {
     std::printf("%s %s\n", g_failures == before ? "PASS" : "FAIL", name);
 }
 
-int main() {
+// The span group's inputs and results, for the oracle comparison of
+// tests/test_gpu_cpp_api.py (written when a dump directory is given).
+static void dump(const std::string& path, const std::vector<float>& v) {
+    FILE* f = std::fopen(path.c_str(), "wb");
+    if (!f) {
+        std::printf("FAIL cannot write %s\n", path.c_str());
+        g_failures++;
+        return;
+    }
+    std::fwrite(v.data(), sizeof(float), v.size(), f);
+    std::fclose(f);
+}
+
+int main(int argc, char** argv) {
+    const std::string dump_dir = argc > 1 ? argv[1] : "";
     int dev = 0;
     if (forge_device_count(&dev) != FORGE_OK || dev == 0) {
         std::printf("no GPU\n");
@@ -513,6 +528,95 @@ int main() {
         for (const char* suffix : {".toml", ".bin", "_lin.toml", "_lin.bin"})
             std::remove((base + suffix).c_str());
         group("checkpoint", f);
+    }
+
+    // ----------------------------------------------- spans and row views
+    {
+        int f = g_failures;
+        const size_t rows = 6, cols = 1000;
+        std::vector<float> h = uniform(rows * cols, 11);
+        for (float& x : h) x *= 4.0f;
+        Matrix m = R.matrix_from_host(h, rows, cols);
+        std::vector<VectorView> views = m.row_views();
+        CHECK(views.size() == rows, "row_views count");
+        for (auto& v : views) CHECK(v.len() == cols, "row view length");
+        // map_sum of every row with six functors (checked against the oracle
+        // by the Python test), plus exact cases checked here.
+        const MapFn fns[] = {MapFn::identity(), MapFn::scale(0.5f), MapFn::add(1.25f),
+                             MapFn::half_square(), MapFn::exp_shift(0.3f),
+                             MapFn::of(FORGE_MAP_GELU)};
+        std::vector<float> sums;
+        for (auto& v : views)
+            for (const MapFn& fn : fns) sums.push_back(v.map_sum(R, fn));
+        for (size_t r = 0; r < rows; r++) {
+            double ref = 0;
+            for (size_t c = 0; c < cols; c++) ref += h[r * cols + c];
+            CHECK(std::fabs(sums[r * 6] - views[r].sum(R)) <= 1e-6 * (1 + std::fabs(ref)),
+                  "map_sum(identity) == sum");
+        }
+        for (auto& v : views) v.softmax(R);
+        std::vector<float> sm = m.to_host(R);
+        for (size_t r = 0; r < rows; r++) {
+            double mx = -1e30, z = 0, t = 0, err = 0;
+            for (size_t c = 0; c < cols; c++) mx = std::fmax(mx, h[r * cols + c]);
+            for (size_t c = 0; c < cols; c++) z += std::exp((double)h[r * cols + c] - mx);
+            for (size_t c = 0; c < cols; c++) {
+                double ref = std::exp((double)h[r * cols + c] - mx) / z;
+                err = std::fmax(err, std::fabs(ref - sm[r * cols + c]));
+                t += sm[r * cols + c];
+            }
+            CHECK(err <= 1e-5 && std::fabs(t - 1.0) <= 1e-4, "VectorView::softmax row");
+        }
+        if (!dump_dir.empty()) {
+            dump(dump_dir + "/spans_input.f32", h);
+            dump(dump_dir + "/spans_softmax.f32", sm);
+            dump(dump_dir + "/spans_map_sum.f32", sums);
+        }
+
+        // Vector spans (vector.rs:11-17), copies, chunks and concatenation.
+        std::vector<float> hv = iota(1000);
+        Vector vec = R.vector_from_host(hv);
+        DeviceSpan sp = vec.span(10, 100);
+        CHECK(sp.len() == 100 && vec.as_span().len() == 1000, "span lengths");
+        DeviceBuffer copy = sp.to_buffer(R);
+        std::vector<float> got(100);
+        check(forge_memcpy_d2h(R.raw(), got.data(), copy.slice(), 100), "span copy");
+        CHECK(std::equal(got.begin(), got.end(), hv.begin() + 10), "DeviceSpan::to_buffer");
+        float exact = 0, mx = -1e30f;
+        for (size_t i = 10; i < 110; i++) exact += hv[i], mx = std::fmax(mx, hv[i]);
+        CHECK(sp.sum(R) == exact && sp.max(R) == mx, "span sum/max (integers: exact)");
+        CHECK(sp.map_sum(R, MapFn::scale(2.0f)) == 2 * exact, "span map_sum exact");
+        std::vector<DeviceSpan> ch = DeviceSpan::chunks(vec.buffer(), 300);
+        CHECK(ch.size() == 4 && ch[3].len() == 100 && ch[0].len() == 300, "chunks");
+        DeviceBuffer cat = R.concat_buffers_from_span({ch[3], ch[0]});
+        std::vector<float> hc(400);
+        check(forge_memcpy_d2h(R.raw(), hc.data(), cat.slice(), 400), "concat copy");
+        CHECK(std::equal(hc.begin(), hc.begin() + 100, hv.begin() + 900) &&
+                  std::equal(hc.begin() + 100, hc.end(), hv.begin()),
+              "concat_buffers_from_span");
+        DeviceSpan empty = vec.span(1000, 0);
+        CHECK(empty.sum(R) == 0.0f && empty.max(R) == -3.40282347e38f &&
+                  empty.map_sum(R, MapFn::add(1.0f)) == 0.0f,
+              "empty span identities");
+        bool refused = false;
+        try {
+            (void)vec.span(990, 20);
+        } catch (const Error& e) {
+            refused = e.status() == FORGE_EINVAL;
+        }
+        CHECK(refused, "span past the buffer refused");
+        // A mutable sub-span changes only its own range.
+        DeviceSpanMut mut = DeviceSpanMut::from_buffer(vec.buffer(), 100, 50);
+        mut.scale(3.0f, R);
+        mut.for_each(R, MapFn::add(1.0f));
+        std::vector<float> after = vec.to_host(R);
+        bool ok = true;
+        for (size_t i = 0; i < 1000; i++) {
+            float want = (i >= 100 && i < 150) ? hv[i] * 3.0f + 1.0f : hv[i];
+            ok = ok && after[i] == want;
+        }
+        CHECK(ok, "DeviceSpanMut::for_each on a sub-span");
+        group("spans", f);
     }
 
     R.sync();

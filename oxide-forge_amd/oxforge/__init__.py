@@ -308,6 +308,10 @@ class Runtime:
         call("forge_reduce_sum", self.handle, stream, x.slice, x.size if n is None else n,
              out.slice)
 
+    def map_sum(self, x, out, op, p0=0.0, n=None, stream=None) -> None:
+        call("forge_map_sum", self.handle, stream, x.slice, x.size if n is None else n, op, p0,
+             out.slice)
+
     def reduce_max(self, x, out, n=None, stream=None) -> None:
         call("forge_reduce_max", self.handle, stream, x.slice, x.size if n is None else n,
              out.slice)

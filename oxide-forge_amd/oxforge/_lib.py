@@ -138,6 +138,7 @@ SIGNATURES = {
     "forge_sum_rows": [RT, ST, Slice, Slice, c_size_t, c_size_t],
     "forge_sum_cols": [RT, ST, Slice, Slice, c_size_t, c_size_t],
     "forge_reduce_sum": [RT, ST, Slice, c_size_t, Slice],
+    "forge_map_sum": [RT, ST, Slice, c_size_t, c_int, c_float, Slice],
     "forge_reduce_max": [RT, ST, Slice, c_size_t, Slice],
     "forge_fill_seq": [RT, ST, Slice, c_size_t, c_int],
     "forge_causal_mask": [RT, ST, Slice, c_size_t, c_size_t],

@@ -84,13 +84,14 @@ def dispatcher_kernel_names():
     for op in ("layer_norm_bwd", "rms_norm_bwd"):
         for v in (1, 2, 4, 8):
             names.append(f"forge_row_{op}_v{v}_p")
+        names.append(f"forge_row_{op}_v4_p4")
     for op in ("add", "sub", "mul", "div"):
         for k in ("binary", "binary_assign", "by_rows"):
             for s in ("v", "s"):
                 names.append(f"forge_{k}_{op}_{s}")
     for op in ("scale", "add", "gelu", "gelu_d", "relu", "relu_d", "silu", "silu_d",
                "exp_shift", "half_sq", "identity"):
-        names += [f"forge_map_{op}_v", f"forge_map_{op}_s"]
+        names += [f"forge_map_{op}_v", f"forge_map_{op}_s", f"forge_map_sum_{op}"]
     names += ["forge_fill_random", "forge_act_backward_v", "forge_act_backward_s",
               "forge_count_neq", "forge_count_final", "forge_sgd_v", "forge_sgd_s"]
     names += ["forge_fill_v", "forge_fill_s", "forge_fill_seq", "forge_causal_mask",

@@ -418,6 +418,34 @@ def test_row_kernels_at_nontemporal_size(rt, affine):
     assert np.max(np.abs(pg.numpy() - rdg)) <= col_tol
 
 
+def test_norm_bwd_partials_at_scale_four_wave_instance(rt):
+    """[65536, 1024] takes the four-wave partial instance (_p4: 256 rows per
+    CU and more).  dx against the oracle on every row; dgamma / dbeta (sums
+    over 65536 rows) at 1e-5 sqrt(rows); the measured relative error of
+    dgamma / dbeta is printed."""
+    rows, cols = 65536, 1024
+    say(f"norm bwd partials {rows}x{cols}")
+    x, dy = synth.normal((rows, cols), 51), synth.normal((rows, cols), 52)
+    gam = synth.normal((cols,), 53, 1.0, 0.1)
+    dgam = rt.array(gam)
+    dX, dDY, dDX = rt.array(x), rt.array(dy), rt.empty((rows, cols))
+    pg, pb = rt.empty((cols,)), rt.empty((cols,))
+    col_tol = TOL_ROW * np.sqrt(rows)
+    rt.layer_norm_bwd(dX, dDY, dDX, rows, cols, gamma=dgam, dgamma=pg, dbeta=pb)
+    rdx, rdg, rdb = orc.layer_norm_backward(x, dy, gam, want_params=True)
+    assert np.max(np.abs(dDX.numpy() - rdx)) <= TOL_ROW
+    g, b = pg.numpy(), pb.numpy()
+    print(f"  LN dgamma max abs err {np.max(np.abs(g - rdg)):.2e} (max |dgamma| "
+          f"{np.max(np.abs(rdg)):.2e}), dbeta {np.max(np.abs(b - rdb)):.2e}")
+    assert np.max(np.abs(g - rdg)) <= col_tol and np.max(np.abs(b - rdb)) <= col_tol
+    rt.rms_norm_bwd(dX, dDY, dDX, rows, cols, gamma=dgam, dgamma=pg)
+    rdx, rdg = orc.rms_norm_backward(x, dy, gam, want_params=True)
+    assert np.max(np.abs(dDX.numpy() - rdx)) <= TOL_ROW
+    assert np.max(np.abs(pg.numpy() - rdg)) <= col_tol
+    for d in (dgam, dX, dDY, dDX, pg, pb):
+        d.recycle()
+
+
 # ------------------------------------------------------------ elementwise
 OPS = [(oxforge.ADD, np.add), (oxforge.SUB, np.subtract), (oxforge.MUL, np.multiply),
        (oxforge.DIV, np.divide)]
@@ -535,6 +563,30 @@ def test_reduce_sum_max(rt, n):
     assert out.numpy()[0] == float(x.astype(np.int64).sum())
     rt.reduce_max(dx, out)
     assert out.numpy()[0] == x.max()
+
+
+@pytest.mark.parametrize("op,p0", EXACT_MAPS + TRANS_MAPS)
+@pytest.mark.parametrize("n", [0, 1, 1001, 4096 * 1024 + 3])
+def test_map_sum(rt, op, p0, n):
+    """forge_map_sum (DeviceSpan::map_sum, span.rs:144-149 -> reduction.rs:
+    43-91) against the f64 sum of the oracle's per-element map: within 1e-6
+    of the sum of magnitudes (f32 accumulation over n terms in a fixed tree
+    order).  Short integer-valued inputs with the exact functors are
+    bit-exact.  An empty span sums to 0."""
+    say(f"map_sum op={op} n={n}")
+    x = synth.normal((n,), 7, 0.0, 2.0)
+    dx, out = rt.array(x), rt.array(np.full((1,), np.nan, np.float32))
+    rt.map_sum(dx, out, op, p0)
+    mapped = orc.map_(x, op, p0).astype(np.float64) if n else np.zeros(0)
+    got = float(out.numpy()[0])
+    assert abs(got - mapped.sum()) <= 1e-6 * max(1.0, np.abs(mapped).sum()), (got, mapped.sum())
+    # Short integer-valued spans: every partial sum is exact in f32.
+    if (op, p0) in EXACT_MAPS and op != oxforge.MAP_SCALE and 0 < n <= 1001:
+        xi = np.random.default_rng(n).integers(-30, 31, n).astype(np.float32)
+        dx.upload(xi)
+        rt.map_sum(dx, out, op, p0)
+        exact = orc.map_(xi, op, p0).astype(np.float64).sum()
+        assert float(out.numpy()[0]) == exact
 
 
 def test_empty_shapes_and_oversized_dimensions(rt):
