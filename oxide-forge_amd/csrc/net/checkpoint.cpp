@@ -42,6 +42,11 @@ struct Table {
     std::map<std::string, Value> values;
     std::map<std::string, std::unique_ptr<Table>> tables;
     std::map<std::string, std::vector<std::unique_ptr<Table>>> arrays;
+    // How the table came to exist.  TOML 1.0 allows a table to be defined
+    // once: by its [header], by dotted keys, or as an inline table; a table
+    // created only as the parent of another header may get its own header
+    // later.
+    bool by_header = false, by_dotted_key = false, is_inline = false;
 
     bool has_key(const std::string& k) const {
         return values.count(k) || tables.count(k) || arrays.count(k);
@@ -76,13 +81,20 @@ public:
                 auto path = split_key(l.substr(1, l.size() - 2));
                 Table* t = root.get();
                 for (const auto& seg : path) t = child(t, seg);
+                if (t->by_header || t->by_dotted_key || t->is_inline)
+                    fail("table '" + join(path) + "' defined twice");
+                t->by_header = true;
                 cur = t;
             } else {
                 size_t eq = find_unquoted(l, '=');
                 if (eq == std::string::npos) fail("expected key = value");
                 auto path = split_key(l.substr(0, eq));
                 Table* t = cur;
-                for (size_t i = 0; i + 1 < path.size(); i++) t = child(t, path[i]);
+                for (size_t i = 0; i + 1 < path.size(); i++) {
+                    t = child(t, path[i]);
+                    if (t->by_header) fail("table '" + path[i] + "' defined twice");
+                    t->by_dotted_key = true;
+                }
                 size_t pos = 0;
                 std::string rest = trim(l.substr(eq + 1));
                 assign(t, path.back(), rest, pos);
@@ -167,11 +179,20 @@ private:
         return out;
     }
 
+    static std::string join(const std::vector<std::string>& path) {
+        std::string out;
+        for (const auto& seg : path) out += (out.empty() ? "" : ".") + seg;
+        return out;
+    }
+
     // The sub-table `name` of t: an existing table, the last element of an
-    // array of tables, or a new table.
+    // array of tables, or a new table.  Inline tables are closed.
     Table* child(Table* t, const std::string& name) const {
         auto it = t->tables.find(name);
-        if (it != t->tables.end()) return it->second.get();
+        if (it != t->tables.end()) {
+            if (it->second->is_inline) fail("inline table '" + name + "' cannot be extended");
+            return it->second.get();
+        }
         auto at = t->arrays.find(name);
         if (at != t->arrays.end()) {
             if (at->second.empty()) fail("empty array of tables");
@@ -188,6 +209,7 @@ private:
         if (pos < s.size() && s[pos] == '{') {
             auto& slot = t->tables[key];
             slot = std::make_unique<Table>();
+            slot->is_inline = true;
             pos++;
             skip_ws(s, pos);
             if (pos < s.size() && s[pos] == '}') {
@@ -273,10 +295,15 @@ private:
                 unsigned long long d = (unsigned long long)(s[pos] - '0');
                 if (acc > (~0ull - d) / 10) fail("integer overflow");
                 acc = acc * 10 + d;
+            } else if (pos == start || pos + 1 >= s.size() || !isdigit((unsigned char)s[pos - 1]) ||
+                       !isdigit((unsigned char)s[pos + 1])) {
+                // TOML: each underscore between two digits.
+                fail("misplaced underscore in integer");
             }
             pos++;
         }
         if (pos == start) fail("unsupported value (only integers, strings and booleans)");
+        if (s[start] == '0' && pos - start > 1) fail("leading zeros are not allowed in integers");
         if (pos < s.size() && (s[pos] == '.' || s[pos] == 'e' || s[pos] == 'E'))
             fail("floating-point values are not part of the format");
         if (acc > (unsigned long long)LLONG_MAX) fail("integer overflow");

@@ -290,6 +290,10 @@ def test_toml_syntax_accepted(tmp_path):
     ("data_bytes = -160", "non-negative"),
     ("[linear", "bad table header"),
     ("data_bytes = 99999999999999999999999", "integer overflow"),
+    ("data_bytes = 0160", "leading zeros"),
+    ("data_bytes = 1__60", "underscore"),
+    ("data_bytes = 160_", "underscore"),
+    ("data_bytes = _160", "underscore"),
 ])
 def test_toml_syntax_rejected(tmp_path, bad, part):
     path, _ = cases(tmp_path)[0]
@@ -298,6 +302,47 @@ def test_toml_syntax_rejected(tmp_path, bad, part):
         f.write(text)
     status, msg = status_of(lambda: net.inspect(path))
     assert status == _lib.FORGE_EINVAL and part in msg, msg
+
+
+@pytest.mark.parametrize("tail,part", [
+    ("[linear]\n", "defined twice"),
+    ("[linear.weights]\n", "defined twice"),
+])
+def test_toml_table_defined_twice_rejected(tmp_path, tail, part):
+    """A second [header] for a table, or a header for a table that dotted keys
+    or an inline table already defined, is refused (TOML 1.0; tomli, an
+    independent parser, refuses the same documents)."""
+    path, _ = cases(tmp_path)[0]
+    text = open(path + ".toml").read() + tail
+    with pytest.raises(tomli.TOMLDecodeError):
+        tomli.loads(text)
+    with open(path + ".toml", "w") as f:
+        f.write(text)
+    status, msg = status_of(lambda: net.inspect(path))
+    assert status == _lib.FORGE_EINVAL and part in msg, msg
+
+
+def test_toml_header_after_dotted_keys_rejected(tmp_path):
+    """linear.weights defined by dotted keys inside [linear], then given its
+    own header: refused, as tomli refuses it."""
+    path, _ = cases(tmp_path)[0]
+    text = open(path + ".toml").read()
+    text = text.replace("[linear.weights]\nrows = 7\ncols = 5\nbyte_start = 0\nbyte_end = 140\n",
+                        "")
+    text = text.replace('activation = "gelu"\n',
+                        'activation = "gelu"\nweights.rows = 7\nweights.cols = 5\n'
+                        'weights.byte_start = 0\nweights.byte_end = 140\n')
+    assert tomli.loads(text)["linear"]["weights"]["byte_end"] == 140
+    with open(path + ".toml", "w") as f:
+        f.write(text)
+    assert net.inspect(path) == ("linear", 160)
+    bad = text + "[linear.weights]\n"
+    with pytest.raises(tomli.TOMLDecodeError):
+        tomli.loads(bad)
+    with open(path + ".toml", "w") as f:
+        f.write(bad)
+    status, msg = status_of(lambda: net.inspect(path))
+    assert status == _lib.FORGE_EINVAL and "defined twice" in msg, msg
 
 
 def test_inspect_survives_mutated_files(tmp_path):
