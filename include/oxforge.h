@@ -335,6 +335,19 @@ forge_status forge_layer_norm_bwd(forge_runtime *rt, forge_stream *stream,
                                   forge_slice gamma, forge_slice dx,
                                   forge_slice dgamma, forge_slice dbeta,
                                   size_t rows, size_t cols, float eps);
+/* forge_layer_norm_bwd followed by the SGD step of the norm's own
+ * parameters, as the training step applies it (the affine extension's
+ * gamma/beta take Linear::learn's update, linear.rs:385-390): dx is computed
+ * with the gamma given, then gamma -= lr * dgamma and beta -= lr * dbeta
+ * (each a rounded product then a rounded difference, bit-identical to
+ * forge_layer_norm_bwd then forge_sgd_update) in the final column-sum pass,
+ * so the two separate update launches disappear.  gamma and beta (updated in
+ * place) and the gradient outputs dgamma/dbeta are each optional. */
+forge_status forge_layer_norm_bwd_sgd(forge_runtime *rt, forge_stream *stream,
+                                      forge_slice x, forge_slice dy, forge_slice gamma,
+                                      forge_slice beta, forge_slice dx,
+                                      forge_slice dgamma, forge_slice dbeta,
+                                      size_t rows, size_t cols, float eps, float lr);
 /* forge_layer_norm_bwd that allocates nothing.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
@@ -366,6 +379,12 @@ forge_status forge_rms_norm_bwd(forge_runtime *rt, forge_stream *stream,
                                 forge_slice gamma, forge_slice dx,
                                 forge_slice dgamma, size_t rows, size_t cols,
                                 float eps);
+/* forge_rms_norm_bwd followed by gamma -= lr * dgamma in its final
+ * column-sum pass (as forge_layer_norm_bwd_sgd). */
+forge_status forge_rms_norm_bwd_sgd(forge_runtime *rt, forge_stream *stream,
+                                    forge_slice x, forge_slice dy, forge_slice gamma,
+                                    forge_slice dx, forge_slice dgamma, size_t rows,
+                                    size_t cols, float eps, float lr);
 
 /* matrix_binary / vector_binary (matrix.rs:194-219 -> elementwise.rs:45-56):
  * o = l op r over n elements.  Bit-exact. */
@@ -409,6 +428,14 @@ forge_status forge_sum_rows(forge_runtime *rt, forge_stream *stream,
 forge_status forge_sum_cols(forge_runtime *rt, forge_stream *stream,
                             forge_slice m, forge_slice out, size_t rows,
                             size_t cols);
+/* Column sums of m [rows, cols] and the SGD step of a bias in one pass: the
+ * bias gradient of Linear::backward (linear.rs:267-272) and the bias update
+ * of Linear::learn (linear.rs:385-390), param -= lr * sum with the same two
+ * roundings as forge_sgd_update.  out (the sums) and param are each
+ * optional. */
+forge_status forge_sum_cols_sgd(forge_runtime *rt, forge_stream *stream, forge_slice m,
+                                size_t rows, size_t cols, forge_slice out,
+                                forge_slice param, float lr);
 /* Vector::sum / Vector::max (span.rs:301-333 -> reduction.rs:4-41,93-130):
  * full reduction of x into out[0] on the device (no host round trip; the
  * caller reads it back when it needs the scalar). */

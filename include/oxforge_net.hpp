@@ -426,7 +426,15 @@ public:
     // learn that also stores dW (and db) when given, for explicit gradients.
     void learn_keep(const Matrix& input, const Matrix& gradient, const Vector* bias_gradient,
                     float learning_rate, Matrix* weight_gradient, CudaRuntime& rt,
-                    const CudaStream* stream);
+                    const CudaStream* stream, bool bias_step = true);
+    // learn_keep with the bias gradient formed here: the weight update as a
+    // fused GEMM, then the column sums of `gradient` and the bias's SGD step
+    // in one pass (forge_sum_cols_sgd); the sums are kept in
+    // *bias_gradient_out when given.  Same results as computing the bias
+    // gradient first and calling learn_keep.
+    void learn_from_gradient(const Matrix& input, const Matrix& gradient, float learning_rate,
+                             Matrix* weight_gradient, std::optional<Vector>* bias_gradient_out,
+                             CudaRuntime& rt, const CudaStream* stream);
     // input_gradient accumulated onto `accumulate` (dX + accumulate, one
     // rounded add per element, written into `accumulate`).
     void input_gradient_accumulate(const Matrix& gradient, Matrix& accumulate, CudaRuntime& rt,
@@ -530,6 +538,10 @@ struct Normalization {
     void forward_into(const Matrix& src, Matrix& dst, CudaRuntime& rt) const;
     Matrix backward(const Matrix& input, const Matrix& output_gradient, CudaRuntime& rt,
                     Vector* dgamma = nullptr, Vector* dbeta = nullptr) const;
+    // backward, then the SGD step of this norm's gamma/beta (when present)
+    // in the same final pass; dgamma/dbeta optional gradient outputs.
+    Matrix backward_step(const Matrix& input, const Matrix& output_gradient, float learning_rate,
+                         CudaRuntime& rt, Vector* dgamma = nullptr, Vector* dbeta = nullptr);
 };
 
 // QkvProjection (attention.rs:15-144).  With `streams` (three streams of
@@ -579,8 +591,10 @@ public:
     Matrix forward_mask(const Matrix& query_input, const Matrix& key_value_input,
                         CudaRuntime& rt);
     Matrix forward_self_training(Matrix input, CudaRuntime& rt);
+    // With `input_gradient` given, the returned gradient is written there
+    // (same shape as the attention input) and an empty Matrix is returned.
     Matrix backward_self(const Matrix& output_gradient, float learning_rate, CudaRuntime& rt,
-                         TransformerGrads* grads = nullptr);
+                         TransformerGrads* grads = nullptr, Matrix* input_gradient = nullptr);
     void normalize(Matrix& m, CudaRuntime& rt, const Normalization* norm = nullptr) const;
     Normalization& normalization() { return norm_; }
     QkvProjection& qkv() { return qkv_; }
@@ -654,6 +668,10 @@ public:
     // Same update, and every gradient exposed in `grads`.
     Matrix backward_grads(const Matrix& output_gradient, float learning_rate, CudaRuntime& rt,
                           TransformerGrads& grads);
+    // backward / backward_grads (grads may be null) with the input gradient
+    // written into `input_gradient` ([seq, hidden]) instead of a new matrix.
+    void backward_into(const Matrix& output_gradient, float learning_rate, CudaRuntime& rt,
+                       Matrix& input_gradient, TransformerGrads* grads = nullptr);
     Attention& attention() { return attention_; }
     TrainingMlp& fcs() { return fcs_; }
     Linear& output() { return output_; }
@@ -662,7 +680,7 @@ public:
 
 private:
     Matrix backward_impl(const Matrix& output_gradient, float learning_rate, CudaRuntime& rt,
-                         TransformerGrads* grads);
+                         TransformerGrads* grads, Matrix* input_gradient = nullptr);
     struct Cache {
         Matrix second_pre_norm, encoded;
     };

@@ -347,13 +347,40 @@ __device__ __forceinline__ void sum_cols_body(const float* __restrict__ m,
     }
 }
 
+// The final passes write the column sums to `out` (when not null) and,
+// when `param` is not null, apply the SGD step of that parameter vector in
+// the same pass: param -= lr * sum with the two roundings of the reference's
+// clone-scale-subtract (linear.rs:385-390).
+struct ColSumOut {
+    float* out;
+    float* param;
+    float lr;
+};
+
+__device__ __forceinline__ void colsum_store(const ColSumOut& o, int c, float v) {
+    if (o.out) o.out[c] = v;
+    if (o.param) o.param[c] = o.param[c] - o.lr * v;
+}
+
+__device__ __forceinline__ void colsum_store4(const ColSumOut& o, int c, float4 v) {
+    if (o.out) *reinterpret_cast<float4*>(o.out + c) = v;
+    if (o.param) {
+        float4 p = *reinterpret_cast<const float4*>(o.param + c);
+        p.x = p.x - o.lr * v.x;
+        p.y = p.y - o.lr * v.y;
+        p.z = p.z - o.lr * v.z;
+        p.w = p.w - o.lr * v.w;
+        *reinterpret_cast<float4*>(o.param + c) = p;
+    }
+}
+
 // Column sums, final pass over a short matrix (the first pass's partial
 // rows, or any matrix of few rows): 16 waves per workgroup each take every
 // 16th row of 64 columns, then add in LDS in wave order.
 constexpr int SUMCOL_FINAL_WAVES = 16;
 
 __device__ __forceinline__ void sum_cols_final_body(const float* __restrict__ m,
-                                                    float* __restrict__ out, int rows, int cols) {
+                                                    const ColSumOut& o, int rows, int cols) {
     __shared__ float part[SUMCOL_FINAL_WAVES][64];
     const int lane = lane_id(), wave = threadIdx.x >> 6;
     const int c = blockIdx.x * 64 + lane;
@@ -367,7 +394,7 @@ __device__ __forceinline__ void sum_cols_final_body(const float* __restrict__ m,
     if (wave == 0 && c < cols) {
         float t = part[0][lane];
         for (int w = 1; w < SUMCOL_FINAL_WAVES; w++) t += part[w][lane];
-        out[c] = t;
+        colsum_store(o, c, t);
     }
 }
 
@@ -383,8 +410,7 @@ constexpr int SUMCOL_FINAL_V_THREADS = 256;
 constexpr int SUMCOL_FINAL_V_COLS = 16;
 
 __device__ __forceinline__ void sum_cols_final_v_body(const float* __restrict__ m,
-                                                      float* __restrict__ out, int rows,
-                                                      int cols) {
+                                                      const ColSumOut& o, int rows, int cols) {
     constexpr int SLOTS = SUMCOL_FINAL_V_THREADS / 4;
     __shared__ float4 part[SLOTS][4];
     const int q = threadIdx.x & 3, s = threadIdx.x >> 2;
@@ -421,7 +447,7 @@ __device__ __forceinline__ void sum_cols_final_v_body(const float* __restrict__ 
         }
         __syncthreads();
     }
-    if (s == 0 && in) *reinterpret_cast<float4*>(out + c) = part[0][q];
+    if (s == 0 && in) colsum_store4(o, c, part[0][q]);
 }
 
 // Row sums: one wave per row (row.rs:16-53).

@@ -232,26 +232,27 @@ FORGE_KERNEL void __launch_bounds__(SUMCOL_WAVES * 64) forge_sum_cols_s(const fl
                                                                        int rows_per_chunk) {
     sum_cols_body<false>(m, out, rows, cols, rows_per_chunk);
 }
-FORGE_KERNEL void __launch_bounds__(SUMCOL_FINAL_WAVES * 64) forge_sum_cols_final(const float* m,
-                                                                                 float* out,
-                                                                                 int rows, int cols) {
-    sum_cols_final_body(m, out, rows, cols);
+// Final column-sum passes (ColSumOut: sums to `out`, and optionally the SGD
+// step of a parameter vector).  The *2 instances do two independent column
+// sums in one launch, blockIdx.y selecting the pair: dgamma and dbeta of the
+// LayerNorm backward.
+FORGE_KERNEL void __launch_bounds__(SUMCOL_FINAL_WAVES * 64) forge_sum_cols_final(
+    const float* m, ColSumOut o, int rows, int cols) {
+    sum_cols_final_body(m, o, rows, cols);
 }
-// Two independent column sums in one launch (blockIdx.y selects the pair):
-// dgamma and dbeta of the LayerNorm backward.
 FORGE_KERNEL void __launch_bounds__(SUMCOL_FINAL_WAVES * 64) forge_sum_cols_final2(
-    const float* m0, float* out0, const float* m1, float* out1, int rows, int cols) {
-    if (blockIdx.y == 0) sum_cols_final_body(m0, out0, rows, cols);
-    else sum_cols_final_body(m1, out1, rows, cols);
+    const float* m0, ColSumOut o0, const float* m1, ColSumOut o1, int rows, int cols) {
+    if (blockIdx.y == 0) sum_cols_final_body(m0, o0, rows, cols);
+    else sum_cols_final_body(m1, o1, rows, cols);
 }
 FORGE_KERNEL void __launch_bounds__(SUMCOL_FINAL_V_THREADS) forge_sum_cols_final_v(
-    const float* m, float* out, int rows, int cols) {
-    sum_cols_final_v_body(m, out, rows, cols);
+    const float* m, ColSumOut o, int rows, int cols) {
+    sum_cols_final_v_body(m, o, rows, cols);
 }
 FORGE_KERNEL void __launch_bounds__(SUMCOL_FINAL_V_THREADS) forge_sum_cols_final2_v(
-    const float* m0, float* out0, const float* m1, float* out1, int rows, int cols) {
-    if (blockIdx.y == 0) sum_cols_final_v_body(m0, out0, rows, cols);
-    else sum_cols_final_v_body(m1, out1, rows, cols);
+    const float* m0, ColSumOut o0, const float* m1, ColSumOut o1, int rows, int cols) {
+    if (blockIdx.y == 0) sum_cols_final_v_body(m0, o0, rows, cols);
+    else sum_cols_final_v_body(m1, o1, rows, cols);
 }
 FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_sum_rows_v(const float* m, float* out, int rows,
                                                                  int cols) {

@@ -45,11 +45,10 @@ static Matrix norm_backward_step(Normalization& norm, const Matrix& input,
                                  std::optional<Vector>* out_beta) {
     const size_t cols = input.cols();
     std::optional<Vector> dg, db;
-    if (norm.gamma || want) dg = Vector(rt.get_uninit_buffer(cols));
-    if (norm.kind == NormType::Layer && (norm.beta || want)) db = Vector(rt.get_uninit_buffer(cols));
-    Matrix dx = norm.backward(input, output_gradient, rt, dg ? &*dg : nullptr, db ? &*db : nullptr);
-    if (norm.gamma) sgd_vector(rt, *norm.gamma, *dg, lr);
-    if (norm.beta) sgd_vector(rt, *norm.beta, *db, lr);
+    if (want) dg = Vector(rt.get_uninit_buffer(cols));
+    if (norm.kind == NormType::Layer && want) db = Vector(rt.get_uninit_buffer(cols));
+    Matrix dx = norm.backward_step(input, output_gradient, lr, rt, dg ? &*dg : nullptr,
+                                   db ? &*db : nullptr);
     if (want) {
         *out_gamma = std::move(dg);
         *out_beta = std::move(db);
@@ -176,7 +175,7 @@ Vector Linear::loss_rows(const Matrix& output, const Matrix& target, CudaRuntime
 
 void Linear::learn_keep(const Matrix& input, const Matrix& gradient, const Vector* bias_gradient,
                         float learning_rate, Matrix* weight_gradient, CudaRuntime& rt,
-                        const CudaStream* stream) {
+                        const CudaStream* stream, bool bias_step) {
     // linear.rs:373-415: W -= lr * (X^T G) as one TN GEMM whose epilogue
     // scales by lr and subtracts from W; b -= lr * db.
     require(input.rows() == gradient.rows(), "input.rows() == gradient.rows()");
@@ -194,10 +193,27 @@ void Linear::learn_keep(const Matrix& input, const Matrix& gradient, const Vecto
     }
     rt.gemm_ex(stream, true, false, input, gradient, weights_.slice(), weights_.rows(),
                weights_.cols(), input.rows(), ep);
-    if (bias_) {
+    if (bias_ && bias_step) {
         require(bias_gradient != nullptr, "missing bias gradient for biased Linear");
         sgd_vector(rt, *bias_, *bias_gradient, learning_rate, stream);
     }
+}
+
+void Linear::learn_from_gradient(const Matrix& input, const Matrix& gradient,
+                                 float learning_rate, Matrix* weight_gradient,
+                                 std::optional<Vector>* bias_gradient_out, CudaRuntime& rt,
+                                 const CudaStream* stream) {
+    learn_keep(input, gradient, nullptr, learning_rate, weight_gradient, rt, stream,
+               /*bias_step=*/false);
+    if (!bias_) return;
+    forge_slice out{nullptr, 0};
+    if (bias_gradient_out) {
+        *bias_gradient_out = Vector(rt.get_uninit_buffer(gradient.cols()));
+        out = (*bias_gradient_out)->slice();
+    }
+    check(forge_sum_cols_sgd(rt.raw(), stream_raw(stream), gradient.slice(), gradient.rows(),
+                             gradient.cols(), out, bias_->slice(), learning_rate),
+          "bias gradient and update");
 }
 
 void Linear::learn(const Matrix& input, const Matrix& gradient, const Vector* bias_gradient,
@@ -340,9 +356,10 @@ Matrix MlpExecutor::backward(const std::vector<Matrix>& layer_inputs,
             layer_grad_owned = std::move(gb.first);
             bias_gradient = std::move(gb.second);
             layer_gradient = &*layer_grad_owned;
-        } else if (layer.bias()) {
-            bias_gradient = rt.matrix_sum_cols(*layer_gradient);
         }
+        // The bias gradient of a layer whose G arrived pre-multiplied is formed
+        // at the update, with the bias's SGD step (learn_from_gradient).
+        const bool defer_bias = layer.bias() && !bias_gradient;
 
         // Input gradient G * W^T (+ act' of the previous layer, fused).
         const bool skip_now = (residual_index && *residual_index == index) ||
@@ -381,9 +398,14 @@ Matrix MlpExecutor::backward(const std::vector<Matrix>& layer_inputs,
                 rt.new_uninit_matrix(layer.weights().rows(), layer.weights().cols());
             wg = &(*weight_gradients)[index];
         }
-        layer.learn_keep(layer_inputs[index], *layer_gradient,
-                         bias_gradient ? &*bias_gradient : nullptr, learning_rate, wg, rt,
-                         nullptr);
+        if (defer_bias) {
+            layer.learn_from_gradient(layer_inputs[index], *layer_gradient, learning_rate, wg,
+                                      bias_gradients ? &bias_gradient : nullptr, rt, nullptr);
+        } else {
+            layer.learn_keep(layer_inputs[index], *layer_gradient,
+                             bias_gradient ? &*bias_gradient : nullptr, learning_rate, wg, rt,
+                             nullptr);
+        }
         if (bias_gradients) (*bias_gradients)[index] = std::move(bias_gradient);
 
         grad_owned = std::move(input_gradient);
@@ -477,6 +499,29 @@ Matrix Normalization::backward(const Matrix& input, const Matrix& output_gradien
     else
         check(forge_rms_norm_bwd(rt.raw(), nullptr, input.slice(), output_gradient.slice(), g,
                                  out.slice(), dg, input.rows(), input.cols(), eps),
+              "rms_norm_backward");
+    return out;
+}
+
+Matrix Normalization::backward_step(const Matrix& input, const Matrix& output_gradient,
+                                    float learning_rate, CudaRuntime& rt, Vector* dgamma,
+                                    Vector* dbeta) {
+    require(input.rows() == output_gradient.rows() && input.cols() == output_gradient.cols(),
+            "norm backward shapes");
+    Matrix out = rt.new_uninit_matrix(input.rows(), input.cols());
+    forge_slice g = gamma ? gamma->slice() : forge_slice{nullptr, 0};
+    forge_slice b = beta ? beta->slice() : forge_slice{nullptr, 0};
+    forge_slice dg = dgamma ? dgamma->slice() : forge_slice{nullptr, 0};
+    forge_slice db = dbeta ? dbeta->slice() : forge_slice{nullptr, 0};
+    if (kind == NormType::Layer)
+        check(forge_layer_norm_bwd_sgd(rt.raw(), nullptr, input.slice(), output_gradient.slice(), g,
+                                       b, out.slice(), dg, db, input.rows(), input.cols(), eps,
+                                       learning_rate),
+              "layer_norm_backward");
+    else
+        check(forge_rms_norm_bwd_sgd(rt.raw(), nullptr, input.slice(), output_gradient.slice(), g,
+                                     out.slice(), dg, input.rows(), input.cols(), eps,
+                                     learning_rate),
               "rms_norm_backward");
     return out;
 }
@@ -625,7 +670,8 @@ Matrix Attention::forward_self_training(Matrix input, CudaRuntime& rt) {
 }
 
 Matrix Attention::backward_self(const Matrix& output_gradient, float learning_rate,
-                                CudaRuntime& rt, TransformerGrads* grads) {
+                                CudaRuntime& rt, TransformerGrads* grads,
+                                Matrix* input_gradient) {
     // attention.rs:283-321 with the QKV part of attention.rs:104-144.
     require(cache_.has_value(), "attention forward must run before backward");
     Cache& c = *cache_;
@@ -679,9 +725,8 @@ Matrix Attention::backward_self(const Matrix& output_gradient, float learning_ra
             g_owned = std::move(gb.first);
             db = std::move(gb.second);
             g = &*g_owned;
-        } else if (lin.bias()) {
-            db = rt.matrix_sum_cols(*g);
         }
+        const bool defer_bias = lin.bias() && !db;
         if (!projection_gradient) projection_gradient = lin.input_gradient(*g, rt, nullptr);
         else lin.input_gradient_accumulate(*g, *projection_gradient, rt, nullptr);
         Matrix* wg = nullptr;
@@ -689,8 +734,22 @@ Matrix Attention::backward_self(const Matrix& output_gradient, float learning_ra
             grads->weights[i] = rt.new_uninit_matrix(lin.weights().rows(), lin.weights().cols());
             wg = &grads->weights[i];
         }
-        lin.learn_keep(c.input, *g, db ? &*db : nullptr, learning_rate, wg, rt, nullptr);
+        if (defer_bias)
+            lin.learn_from_gradient(c.input, *g, learning_rate, wg, grads ? &db : nullptr, rt,
+                                    nullptr);
+        else
+            lin.learn_keep(c.input, *g, db ? &*db : nullptr, learning_rate, wg, rt, nullptr);
         if (grads) grads->biases[i] = std::move(db);
+    }
+    if (input_gradient) {
+        require(input_gradient->rows() == residual_gradient.rows() &&
+                    input_gradient->cols() == residual_gradient.cols(),
+                "input gradient shape");
+        check(forge_binary(rt.raw(), nullptr, residual_gradient.slice(),
+                           projection_gradient->slice(), input_gradient->slice(),
+                           residual_gradient.len(), FORGE_ADD),
+              "attention input gradient");
+        return Matrix();
     }
     residual_gradient.binary_assign(*projection_gradient, BinaryOp::Add, rt);
     return residual_gradient;
@@ -801,8 +860,15 @@ Matrix TrainingTransformer::backward_grads(const Matrix& output_gradient, float 
     return backward_impl(output_gradient, learning_rate, rt, &grads);
 }
 
+void TrainingTransformer::backward_into(const Matrix& output_gradient, float learning_rate,
+                                        CudaRuntime& rt, Matrix& input_gradient,
+                                        TransformerGrads* grads) {
+    (void)backward_impl(output_gradient, learning_rate, rt, grads, &input_gradient);
+}
+
 Matrix TrainingTransformer::backward_impl(const Matrix& output_gradient, float learning_rate,
-                                          CudaRuntime& rt, TransformerGrads* grads) {
+                                          CudaRuntime& rt, TransformerGrads* grads,
+                                          Matrix* input_gradient) {
     // encoder.rs:133-186.
     require(cache_.has_value(), "forward must run before backward");
     Cache& c = *cache_;
@@ -824,9 +890,8 @@ Matrix TrainingTransformer::backward_impl(const Matrix& output_gradient, float l
         g_owned = std::move(gb.first);
         db_o = std::move(gb.second);
         g_o = &*g_owned;
-    } else if (output_.bias()) {
-        db_o = rt.matrix_sum_cols(output_gradient);
     }
+    const bool defer_bias = output_.bias() && !db_o;
     Matrix encoded_gradient = output_.input_gradient(*g_o, rt, nullptr);
     Matrix* wg_o = nullptr;
     if (grads) {
@@ -834,8 +899,12 @@ Matrix TrainingTransformer::backward_impl(const Matrix& output_gradient, float l
             rt.new_uninit_matrix(output_.weights().rows(), output_.weights().cols());
         wg_o = &grads->weights[3 + n_ffn];
     }
-    output_.learn_keep(c.encoded, *g_o, db_o ? &*db_o : nullptr, learning_rate, wg_o, rt,
-                       nullptr);
+    if (defer_bias)
+        output_.learn_from_gradient(c.encoded, *g_o, learning_rate, wg_o, grads ? &db_o : nullptr,
+                                    rt, nullptr);
+    else
+        output_.learn_keep(c.encoded, *g_o, db_o ? &*db_o : nullptr, learning_rate, wg_o, rt,
+                           nullptr);
     if (grads) grads->biases[3 + n_ffn] = std::move(db_o);
 
     // Second norm (its gamma/beta, when present, take the SGD step too).
@@ -860,8 +929,9 @@ Matrix TrainingTransformer::backward_impl(const Matrix& output_gradient, float l
     second_gradient = Matrix();
 
     // Attention (fills grads->weights[0..3) and the first norm).
-    Matrix positioned_gradient =
-        attention_.backward_self(first_output_gradient, learning_rate, rt, grads);
+    Matrix positioned_owned =
+        attention_.backward_self(first_output_gradient, learning_rate, rt, grads, input_gradient);
+    Matrix& positioned_gradient = input_gradient ? *input_gradient : positioned_owned;
 
     // Position matrix: P -= lr * dXp (encoder.rs:180-184: clone, scale,
     // subtract) as one fused update.  dXp is not scaled in place, so it is
@@ -873,7 +943,7 @@ Matrix TrainingTransformer::backward_impl(const Matrix& output_gradient, float l
                            position_.len(), learning_rate),
           "position update");
     if (grads) grads->position = rt.clone_matrix(positioned_gradient);
-    return positioned_gradient;
+    return positioned_owned;
 }
 
 }  // namespace encoder

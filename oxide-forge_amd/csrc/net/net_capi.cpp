@@ -403,9 +403,16 @@ extern "C" forge_status forge_net_transformer_backward(forge_net_model* m, forge
         need(dy, d.seq * d.out, "transformer dy");
         Matrix DY(DeviceBuffer(nullptr, forge_slice{dy.ptr, d.seq * d.out}), d.seq, d.out);
         TransformerGrads g;
-        Matrix DX = grads ? m->enc_train->backward_grads(DY, lr, rt, g)
-                          : m->enc_train->backward(DY, lr, rt);
-        if (present(dx)) copy_out(rt, dx, DX, "transformer dx");
+        if (present(dx)) {
+            // The input gradient goes straight into the caller's buffer.
+            need(dx, d.seq * d.hidden, "transformer dx");
+            Matrix DX(DeviceBuffer(nullptr, forge_slice{dx.ptr, d.seq * d.hidden}), d.seq,
+                      d.hidden);
+            m->enc_train->backward_into(DY, lr, rt, DX, grads ? &g : nullptr);
+        } else {
+            Matrix DX = grads ? m->enc_train->backward_grads(DY, lr, rt, g)
+                              : m->enc_train->backward(DY, lr, rt);
+        }
         if (grads) {
             const int wslot[6] = {FORGE_TP_WQ, FORGE_TP_WK, FORGE_TP_WV, FORGE_TP_W1, FORGE_TP_W2,
                                   FORGE_TP_WO};

@@ -88,6 +88,15 @@ struct RowArgs {
     float scale;
 };
 
+// Must match forge::ColSumOut in csrc/kernels/elementwise.hpp: where a final
+// column-sum pass writes (out, when not null) and the parameter vector whose
+// SGD step it applies (param -= lr * sum, when not null).
+struct ColSumOut {
+    float* out;
+    float* param;
+    float lr;
+};
+
 constexpr int ROW_WAVES = 4;   // rows.hpp ROW_WAVES
 constexpr int ROW_PARTIAL_WAVES = 8;  // rows.hpp ROW_PARTIAL_WAVES
 constexpr int EW_THREADS = 256;  // elementwise.hpp EW_THREADS
@@ -898,36 +907,39 @@ size_t sum_cols_scratch(size_t rows, size_t cols) {
 }
 
 // Final column-sum pass over a matrix of at most SUMCOL_FINAL_MAX_ROWS rows:
-// float4 columns when m and out are 16-byte aligned and cols % 4 == 0.
-bool sum_cols_final_vec(const float* m, const float* out, int cols) {
-    return aligned16(m) && aligned16(out) && cols % 4 == 0;
+// float4 columns when m, the outputs and the parameter are 16-byte aligned
+// and cols % 4 == 0.
+bool sum_cols_final_vec(const float* m, const ColSumOut& o, int cols) {
+    return aligned16(m) && (!o.out || aligned16(o.out)) && (!o.param || aligned16(o.param)) &&
+           cols % 4 == 0;
 }
 
 forge_status sum_cols_final_launch(forge_runtime* rt, forge_stream* s, const float* m,
-                                   float* out, int rows, int cols) {
-    if (sum_cols_final_vec(m, out, cols))
+                                   ColSumOut o, int rows, int cols) {
+    if (sum_cols_final_vec(m, o, cols))
         return launch_args(rt, s, "forge_sum_cols_final_v",
                            dim3((unsigned)((cols + SUMCOL_FINAL_V_COLS - 1) / SUMCOL_FINAL_V_COLS)),
-                           dim3(SUMCOL_FINAL_V_THREADS), 0, m, out, rows, cols);
+                           dim3(SUMCOL_FINAL_V_THREADS), 0, m, o, rows, cols);
     return launch_args(rt, s, "forge_sum_cols_final", dim3((unsigned)((cols + 63) / 64)),
-                       dim3(1024), 0, m, out, rows, cols);
+                       dim3(1024), 0, m, o, rows, cols);
 }
 
-// scratch: sum_cols_scratch(rows, cols) floats that do not overlap m/out.
-forge_status sum_cols_impl(forge_runtime* rt, forge_stream* s, const float* m, float* out,
+// scratch: sum_cols_scratch(rows, cols) floats that do not overlap m or the
+// outputs.
+forge_status sum_cols_impl(forge_runtime* rt, forge_stream* s, const float* m, ColSumOut o,
                            size_t rows, size_t cols, float* scratch) {
     if (cols == 0) return FORGE_OK;
     int c = (int)cols;
     const bool vec = sum_cols_vec(m, cols);
     size_t chunks = sum_cols_chunks(rows, cols, vec);
-    if (chunks == 1) return sum_cols_final_launch(rt, s, m, out, (int)rows, c);
+    if (chunks == 1) return sum_cols_final_launch(rt, s, m, o, (int)rows, c);
     int rpc = (int)((rows + chunks - 1) / chunks);
     chunks = (rows + rpc - 1) / rpc;
     int r = (int)rows;
     unsigned gx = (unsigned)((cols + (vec ? 255 : 63)) / (vec ? 256 : 64));
     FORGE_TRY(launch_args(rt, s, vec ? "forge_sum_cols_v" : "forge_sum_cols_s",
                           dim3(gx, (unsigned)chunks), dim3(256), 0, m, scratch, r, c, rpc));
-    return sum_cols_final_launch(rt, s, scratch, out, (int)chunks, c);
+    return sum_cols_final_launch(rt, s, scratch, o, (int)chunks, c);
 }
 
 
@@ -947,18 +959,29 @@ unsigned norm_bwd_blocks(forge_runtime* rt) {
 // workspace and are summed by sum_cols_impl; with `scratch` given they land
 // there instead (scratch_len floats, nothing is allocated) and a shape that
 // needs more is FORGE_EINVAL.
+// The SGD step of the norm's own parameters, applied by the final column-sum
+// pass of its backward (gamma/beta null: no step).
+struct NormSgd {
+    float* gamma = nullptr;
+    float* beta = nullptr;
+    float lr = 0.0f;
+};
+
 forge_status row_launch(forge_runtime* rt, forge_stream* s, const char* op, RowArgs a,
                         float* dgamma, float* dbeta, float* scratch = nullptr,
-                        size_t scratch_len = 0) {
+                        size_t scratch_len = 0, NormSgd sgd = NormSgd()) {
     if (a.rows == 0 || a.cols == 0) {
+        // No rows: zero gradients, and the SGD step leaves the parameters.
         if (dgamma) FORGE_TRY(forge_fill(rt, s, forge_slice{dgamma, (size_t)a.cols}, 0.0f));
         if (dbeta) FORGE_TRY(forge_fill(rt, s, forge_slice{dbeta, (size_t)a.cols}, 0.0f));
         return FORGE_OK;
     }
+    const ColSumOut og{dgamma, sgd.gamma, sgd.lr}, ob{dbeta, sgd.beta, sgd.lr};
+    const bool want_g = dgamma || sgd.gamma, want_b = dbeta || sgd.beta;
     bool aligned = aligned16(a.x) && aligned16(a.y) && (!a.dy || aligned16(a.dy)) &&
                    (!a.gamma || aligned16(a.gamma)) && (!a.beta || aligned16(a.beta));
     int vpt = row_vpt((size_t)a.cols, aligned);
-    const bool partials = dgamma || dbeta;
+    const bool partials = want_g || want_b;
     if (partials && vpt > 8) vpt = 0;  // register path with partials: <= 8 float4
     char name[80];
     // Waves per workgroup: the register partial kernels use ROW_PARTIAL_WAVES
@@ -988,8 +1011,8 @@ forge_status row_launch(forge_runtime* rt, forge_stream* s, const char* op, RowA
         } else {
             FORGE_TRY(workspace(rt, s, need, &ws));
         }
-        a.pgamma = dgamma ? ws : nullptr;
-        a.pbeta = dbeta ? ws + per : nullptr;
+        a.pgamma = want_g ? ws : nullptr;
+        a.pbeta = want_b ? ws + per : nullptr;
         if (vpt) shmem = (size_t)waves * (size_t)a.cols * sizeof(float);
         if (vpt) snprintf(name, sizeof name, "forge_row_%s_v%d_p%s", op, vpt, p4 ? "4" : "");
         else snprintf(name, sizeof name, "forge_row_%s_loop", op);
@@ -1004,22 +1027,22 @@ forge_status row_launch(forge_runtime* rt, forge_stream* s, const char* op, RowA
     void* args[] = {&a};
     FORGE_TRY(launch(rt, s, name, dim3(grid), dim3(waves * 64), shmem, args));
     float* chunk_scratch = ws ? ws + 2 * prow * (size_t)a.cols : nullptr;
-    if (dgamma && dbeta && sum_cols_chunks(prow, (size_t)a.cols, true) == 1) {
+    if (want_g && want_b && sum_cols_chunks(prow, (size_t)a.cols, true) == 1) {
         // Both column sums fit one final pass: one launch for the pair.
         int r = (int)prow, c = a.cols;
-        if (sum_cols_final_vec(a.pgamma, dgamma, c) && sum_cols_final_vec(a.pbeta, dbeta, c))
+        if (sum_cols_final_vec(a.pgamma, og, c) && sum_cols_final_vec(a.pbeta, ob, c))
             return launch_args(rt, s, "forge_sum_cols_final2_v",
                                dim3((unsigned)((c + SUMCOL_FINAL_V_COLS - 1) / SUMCOL_FINAL_V_COLS), 2),
-                               dim3(SUMCOL_FINAL_V_THREADS), 0, (const float*)a.pgamma, dgamma,
-                               (const float*)a.pbeta, dbeta, r, c);
+                               dim3(SUMCOL_FINAL_V_THREADS), 0, (const float*)a.pgamma, og,
+                               (const float*)a.pbeta, ob, r, c);
         unsigned gfinal = (unsigned)((a.cols + 63) / 64);
         return launch_args(rt, s, "forge_sum_cols_final2", dim3(gfinal, 2), dim3(1024), 0,
-                           (const float*)a.pgamma, dgamma, (const float*)a.pbeta, dbeta, r, c);
+                           (const float*)a.pgamma, og, (const float*)a.pbeta, ob, r, c);
     }
-    if (dgamma)
-        FORGE_TRY(sum_cols_impl(rt, s, a.pgamma, dgamma, prow, (size_t)a.cols, chunk_scratch));
-    if (dbeta)
-        FORGE_TRY(sum_cols_impl(rt, s, a.pbeta, dbeta, prow, (size_t)a.cols, chunk_scratch));
+    if (want_g)
+        FORGE_TRY(sum_cols_impl(rt, s, a.pgamma, og, prow, (size_t)a.cols, chunk_scratch));
+    if (want_b)
+        FORGE_TRY(sum_cols_impl(rt, s, a.pbeta, ob, prow, (size_t)a.cols, chunk_scratch));
     return FORGE_OK;
 }
 
@@ -1337,6 +1360,29 @@ extern "C" forge_status forge_layer_norm_bwd(forge_runtime* rt, forge_stream* s,
                                0);
 }
 
+extern "C" forge_status forge_layer_norm_bwd_sgd(forge_runtime* rt, forge_stream* s,
+                                                 forge_slice x, forge_slice dy,
+                                                 forge_slice gamma, forge_slice beta,
+                                                 forge_slice dx, forge_slice dgamma,
+                                                 forge_slice dbeta, size_t rows, size_t cols,
+                                                 float eps, float lr) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    FORGE_TRY(check_rows(rows, cols));
+    FORGE_TRY(need(x, rows * cols, "layer_norm_bwd x"));
+    FORGE_TRY(need(dy, rows * cols, "layer_norm_bwd dy"));
+    FORGE_TRY(need(dx, rows * cols, "layer_norm_bwd dx"));
+    FORGE_TRY(need_opt(gamma, cols, "layer_norm_bwd gamma"));
+    FORGE_TRY(need_opt(beta, cols, "layer_norm_bwd beta"));
+    FORGE_TRY(need_opt(dgamma, cols, "layer_norm_bwd dgamma"));
+    FORGE_TRY(need_opt(dbeta, cols, "layer_norm_bwd dbeta"));
+    RowArgs a{x.ptr, dx.ptr, dy.ptr, gamma.ptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, eps, 1.0f};
+    NormSgd sgd;
+    sgd.gamma = gamma.ptr;
+    sgd.beta = beta.ptr;
+    sgd.lr = lr;
+    return row_launch(rt, s, "layer_norm_bwd", a, dgamma.ptr, dbeta.ptr, nullptr, 0, sgd);
+}
+
 extern "C" forge_status forge_layer_norm_bwd_noalloc(forge_runtime* rt, forge_stream* s,
                                                      forge_slice x, forge_slice dy,
                                                      forge_slice gamma, forge_slice dx,
@@ -1382,6 +1428,24 @@ extern "C" forge_status forge_rms_norm_bwd(forge_runtime* rt, forge_stream* s, f
     FORGE_TRY(need_opt(dgamma, cols, "rms_norm_bwd dgamma"));
     RowArgs a{x.ptr, dx.ptr, dy.ptr, gamma.ptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, eps, 1.0f};
     return row_launch(rt, s, "rms_norm_bwd", a, dgamma.ptr, nullptr);
+}
+
+extern "C" forge_status forge_rms_norm_bwd_sgd(forge_runtime* rt, forge_stream* s, forge_slice x,
+                                               forge_slice dy, forge_slice gamma, forge_slice dx,
+                                               forge_slice dgamma, size_t rows, size_t cols,
+                                               float eps, float lr) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    FORGE_TRY(check_rows(rows, cols));
+    FORGE_TRY(need(x, rows * cols, "rms_norm_bwd x"));
+    FORGE_TRY(need(dy, rows * cols, "rms_norm_bwd dy"));
+    FORGE_TRY(need(dx, rows * cols, "rms_norm_bwd dx"));
+    FORGE_TRY(need_opt(gamma, cols, "rms_norm_bwd gamma"));
+    FORGE_TRY(need_opt(dgamma, cols, "rms_norm_bwd dgamma"));
+    RowArgs a{x.ptr, dx.ptr, dy.ptr, gamma.ptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, eps, 1.0f};
+    NormSgd sgd;
+    sgd.gamma = gamma.ptr;
+    sgd.lr = lr;
+    return row_launch(rt, s, "rms_norm_bwd", a, dgamma.ptr, nullptr, nullptr, 0, sgd);
 }
 
 extern "C" forge_status forge_binary(forge_runtime* rt, forge_stream* s, forge_slice l,
@@ -1494,7 +1558,26 @@ extern "C" forge_status forge_sum_cols(forge_runtime* rt, forge_stream* s, forge
     float* scratch = nullptr;
     size_t need_ws = sum_cols_scratch(rows, cols);
     if (need_ws) FORGE_TRY(workspace(rt, s, need_ws, &scratch));
-    return sum_cols_impl(rt, s, m.ptr, out.ptr, rows, cols, scratch);
+    return sum_cols_impl(rt, s, m.ptr, ColSumOut{out.ptr, nullptr, 0.0f}, rows, cols, scratch);
+}
+
+extern "C" forge_status forge_sum_cols_sgd(forge_runtime* rt, forge_stream* s, forge_slice m,
+                                           size_t rows, size_t cols, forge_slice out,
+                                           forge_slice param, float lr) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    FORGE_TRY(check_rows(rows, cols));
+    FORGE_TRY(need(m, rows * cols, "sum_cols_sgd m"));
+    FORGE_TRY(need_opt(out, cols, "sum_cols_sgd out"));
+    FORGE_TRY(need_opt(param, cols, "sum_cols_sgd param"));
+    if (rows == 0) {
+        // Sums of no rows are zero; the step leaves the parameter as it is.
+        if (out.ptr) return forge_fill(rt, s, forge_slice{out.ptr, cols}, 0.0f);
+        return FORGE_OK;
+    }
+    float* scratch = nullptr;
+    size_t need_ws = sum_cols_scratch(rows, cols);
+    if (need_ws) FORGE_TRY(workspace(rt, s, need_ws, &scratch));
+    return sum_cols_impl(rt, s, m.ptr, ColSumOut{out.ptr, param.ptr, lr}, rows, cols, scratch);
 }
 
 namespace {

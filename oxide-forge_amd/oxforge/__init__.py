@@ -271,6 +271,20 @@ class Runtime:
         call("forge_layer_norm_bwd", self.handle, stream, x.slice, dy.slice, _sl(gamma),
              dx.slice, _sl(dgamma), _sl(dbeta), rows, cols, eps)
 
+    def layer_norm_bwd_sgd(self, x, dy, dx, rows, cols, lr, gamma=None, beta=None, dgamma=None,
+                           dbeta=None, eps=1e-5, stream=None) -> None:
+        call("forge_layer_norm_bwd_sgd", self.handle, stream, x.slice, dy.slice, _sl(gamma),
+             _sl(beta), dx.slice, _sl(dgamma), _sl(dbeta), rows, cols, eps, lr)
+
+    def rms_norm_bwd_sgd(self, x, dy, dx, rows, cols, lr, gamma=None, dgamma=None, eps=1e-5,
+                         stream=None) -> None:
+        call("forge_rms_norm_bwd_sgd", self.handle, stream, x.slice, dy.slice, _sl(gamma),
+             dx.slice, _sl(dgamma), rows, cols, eps, lr)
+
+    def sum_cols_sgd(self, m, rows, cols, lr, out=None, param=None, stream=None) -> None:
+        call("forge_sum_cols_sgd", self.handle, stream, m.slice, rows, cols, _sl(out), _sl(param),
+             lr)
+
     def rms_norm(self, x, rows, cols, gamma=None, eps=1e-5, stream=None) -> None:
         call("forge_rms_norm_rows", self.handle, stream, x.slice, _sl(gamma), rows, cols, eps)
 

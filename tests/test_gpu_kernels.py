@@ -105,10 +105,21 @@ def test_gemm_full_size_sampled_rows(rt, M, N, K):
     dA, dB, dC = rt.array(A), rt.array(B), rt.empty((M, N))
     rt.gemm(dA, dB, dC, M, N, K)
     C = dC.numpy()
-    rows = np.sort(np.random.default_rng(M).choice(M, 48, replace=False))
+    # One row in every 64-row band (at a different offset in each band) and
+    # 64 columns spread over N, each against the f64 oracle: every row band
+    # and every 64-column group of output tiles is checked somewhere.
+    bands = M // 64
+    rows = np.arange(bands) * 64 + (np.arange(bands) * 37) % 64
     ref = orc.gemm_f64(np.ascontiguousarray(A[rows]), B)
     absprod = np.abs(A[rows]).astype(np.float64) @ np.abs(B).astype(np.float64)
     rel_max, comp = gemm_errors(C[rows], ref, absprod)
+    assert rel_max <= 1e-4 and comp <= 1e-4, (rel_max, comp)
+    cols = np.arange(64) * (N // 64) + (np.arange(64) * 11) % (N // 64)
+    Bc = np.ascontiguousarray(B[:, cols])
+    ref = orc.gemm_f64(A, Bc)
+    absprod = np.abs(A).astype(np.float64) @ np.abs(Bc).astype(np.float64)
+    rel_max, comp = gemm_errors(np.ascontiguousarray(C[:, cols]), ref, absprod)
+    print(f"  sampled rows and columns: max rel err {rel_max:.2e}, componentwise {comp:.2e}")
     assert rel_max <= 1e-4 and comp <= 1e-4, (rel_max, comp)
     # every tile was written: row sums against A @ (B @ 1) in f64
     ones = B.astype(np.float64).sum(axis=1)
@@ -241,6 +252,10 @@ def test_layer_norm_fwd_bwd(rt, rows, cols, affine):
     rt.layer_norm_bwd(dX, dDY, dDX, rows, cols, gamma=dgam, dgamma=pg, dbeta=pb)
     rdx, rdg, rdb = orc.layer_norm_backward(x, dy, gam, want_params=True)
     assert np.max(np.abs(dDX.numpy() - rdx)) <= TOL_ROW
+    if affine and rows == 4096:
+        eg, eb = np.max(np.abs(pg.numpy() - rdg)), np.max(np.abs(pb.numpy() - rdb))
+        print(f"  C2 dgamma max abs err {eg:.2e} (rel to max {eg / np.max(np.abs(rdg)):.2e}), "
+              f"dbeta {eb:.2e} (rel {eb / np.max(np.abs(rdb)):.2e})")
     # column sums over `rows` terms: tolerance scales with sqrt(rows)
     tol = TOL_ROW * max(1.0, np.sqrt(rows))
     assert np.max(np.abs(pg.numpy() - rdg)) <= tol
@@ -444,6 +459,71 @@ def test_norm_bwd_partials_at_scale_four_wave_instance(rt):
     assert np.max(np.abs(pg.numpy() - rdg)) <= col_tol
     for d in (dgam, dX, dDY, dDX, pg, pb):
         d.recycle()
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 2048), (300, 1024), (600, 33), (513, 64), (7, 5),
+                                       (0, 16)])
+def test_sum_cols_sgd_matches_separate_launches(rt, rows, cols):
+    """forge_sum_cols_sgd (column sums and the bias SGD step in the final
+    pass) against forge_sum_cols then forge_sgd_update: bit for bit, with
+    and without the sums kept, with and without the parameter."""
+    say(f"sum_cols_sgd {rows}x{cols}")
+    m = synth.normal((max(rows, 1), cols), 61)[:rows]
+    b = synth.normal((cols,), 62)
+    lr = 1e-3
+    dm = rt.array(np.ascontiguousarray(m)) if rows else rt.empty((0,))
+    ref_s, ref_p = rt.empty((cols,)), rt.array(b)
+    rt.sum_cols(dm, ref_s, rows, cols)
+    rt.sgd_update(ref_p, ref_s, lr)
+    for keep, upd in ((True, True), (False, True), (True, False)):
+        out = rt.array(np.full(cols, np.nan, np.float32)) if keep else None
+        par = rt.array(b) if upd else None
+        rt.sum_cols_sgd(dm, rows, cols, lr, out=out, param=par)
+        if keep:
+            assert np.array_equal(out.numpy(), ref_s.numpy())
+        if upd:
+            assert np.array_equal(par.numpy(), ref_p.numpy())
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 1024), (4096, 2048), (65536, 1024), (33, 1001),
+                                       (0, 64)])
+def test_norm_bwd_sgd_matches_separate_launches(rt, rows, cols):
+    """forge_layer_norm_bwd_sgd / forge_rms_norm_bwd_sgd against the norm
+    backward then forge_sgd_update on gamma and beta: dx, the gradients and
+    the updated parameters bit for bit (dx uses the gamma from before the
+    step)."""
+    say(f"norm bwd sgd {rows}x{cols}")
+    x = synth.normal((max(rows, 1), cols), 63)[:rows]
+    dy = synth.normal((max(rows, 1), cols), 64)[:rows]
+    gam, bet = synth.normal((cols,), 65, 1.0, 0.1), synth.normal((cols,), 66, 0.0, 0.1)
+    lr = 1e-3
+    n = rows * cols
+    dX = rt.array(np.ascontiguousarray(x)) if n else rt.empty((0,))
+    dDY = rt.array(np.ascontiguousarray(dy)) if n else rt.empty((0,))
+    # reference: separate launches
+    g0, b0 = rt.array(gam), rt.array(bet)
+    rdx, rdg, rdb = rt.empty((max(n, 1),)), rt.empty((cols,)), rt.empty((cols,))
+    rt.layer_norm_bwd(dX, dDY, rdx, rows, cols, gamma=g0, dgamma=rdg, dbeta=rdb)
+    rt.sgd_update(g0, rdg, lr)
+    rt.sgd_update(b0, rdb, lr)
+    g1, b1 = rt.array(gam), rt.array(bet)
+    fdx, fdg, fdb = rt.empty((max(n, 1),)), rt.empty((cols,)), rt.empty((cols,))
+    rt.layer_norm_bwd_sgd(dX, dDY, fdx, rows, cols, lr, gamma=g1, beta=b1, dgamma=fdg, dbeta=fdb)
+    assert np.array_equal(fdx.numpy()[:n], rdx.numpy()[:n])
+    for u, v in ((fdg, rdg), (fdb, rdb), (g1, g0), (b1, b0)):
+        assert np.array_equal(u.numpy(), v.numpy())
+    # the step alone, no gradient outputs
+    g2, b2 = rt.array(gam), rt.array(bet)
+    rt.layer_norm_bwd_sgd(dX, dDY, fdx, rows, cols, lr, gamma=g2, beta=b2)
+    assert np.array_equal(g2.numpy(), g0.numpy()) and np.array_equal(b2.numpy(), b0.numpy())
+    # RMSNorm
+    g0 = rt.array(gam)
+    rt.rms_norm_bwd(dX, dDY, rdx, rows, cols, gamma=g0, dgamma=rdg)
+    rt.sgd_update(g0, rdg, lr)
+    g1 = rt.array(gam)
+    rt.rms_norm_bwd_sgd(dX, dDY, fdx, rows, cols, lr, gamma=g1, dgamma=fdg)
+    assert np.array_equal(fdx.numpy()[:n], rdx.numpy()[:n])
+    assert np.array_equal(fdg.numpy(), rdg.numpy()) and np.array_equal(g1.numpy(), g0.numpy())
 
 
 # ------------------------------------------------------------ elementwise
