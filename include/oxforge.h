@@ -466,6 +466,11 @@ forge_status forge_compare(forge_runtime *rt, forge_stream *stream,
 /* Matrix::causal_mask (matrix.rs:79-92 -> row.rs:5-14). */
 forge_status forge_causal_mask(forge_runtime *rt, forge_stream *stream,
                                forge_slice m, size_t rows, size_t cols);
+/* The causal mask of rows first_row .. first_row + rows - 1 of a score
+ * matrix, held in m [rows, cols]: M[r, c] = -inf for c > first_row + r (the
+ * query-chunked attention masks one chunk of rows at a time). */
+forge_status forge_causal_mask_rows(forge_runtime *rt, forge_stream *stream, forge_slice m,
+                                    size_t rows, size_t cols, size_t first_row);
 
 #ifdef __cplusplus
 }

@@ -123,6 +123,11 @@ forge_status forge_net_transformer_backward(forge_net_model *m, forge_slice dy,
 /* Device view of a current parameter ({NULL,0} if absent). */
 forge_status forge_net_transformer_param(forge_net_model *m, int slot,
                                          forge_slice *out);
+/* Attention::set_max_score_bytes: the largest [seq, seq] score matrix held
+ * at once (default 1 GiB); above it attention runs in chunks of query rows
+ * and the training step recomputes each chunk's probabilities in backward.
+ * No counterpart in the reference, which always forms the whole matrix. */
+forge_status forge_net_transformer_set_score_bytes(forge_net_model *m, size_t bytes);
 
 /* ------------------------------------------------------------ checkpoint */
 

@@ -598,16 +598,29 @@ public:
     void normalize(Matrix& m, CudaRuntime& rt, const Normalization* norm = nullptr) const;
     Normalization& normalization() { return norm_; }
     QkvProjection& qkv() { return qkv_; }
+    // Largest score matrix (bytes) held at once.  A [S, Sk] score matrix
+    // above it is never formed: the scores, probabilities and their
+    // gradients are computed for one chunk of query rows at a time (a
+    // multiple of 64 rows, at least 64), and the training step recomputes
+    // each chunk's probabilities in backward instead of caching S x Sk.
+    // Default 1 GiB (S = Sk = 16384 still unchunked).
+    void set_max_score_bytes(size_t bytes) { max_score_bytes_ = bytes; }
+    size_t max_score_bytes() const { return max_score_bytes_; }
 
 private:
     Matrix attention_value(QkvProjection::Projected projected, const Matrix& residual, bool mask,
                            CudaRuntime& rt);
+    // out = softmax(scale Q K^T (masked)) V + residual in query chunks.
+    void chunked_forward(const Matrix& q, const Matrix& k, const Matrix& v,
+                         const Matrix& residual, bool mask, size_t chunk, Matrix& out,
+                         CudaRuntime& rt);
     struct Cache {
         Matrix input, query, key, value, probabilities, pre_norm;
     };
     QkvProjection qkv_;
     Normalization norm_;
     std::optional<Cache> cache_;
+    size_t max_score_bytes_ = size_t(1) << 30;
 };
 
 // InferenceBlock (inference.rs:26-108).

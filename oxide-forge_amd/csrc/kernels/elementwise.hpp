@@ -292,12 +292,13 @@ __device__ __forceinline__ void count_final_body(const unsigned* __restrict__ pa
     }
 }
 
-// row.rs:5-14: M[r, c] = -inf for c > r.
-__device__ __forceinline__ void causal_mask_body(float* m, int rows, int cols) {
+// row.rs:5-14: M[r, c] = -inf for c > r, where row r of m is row
+// first_row + r of the whole score matrix (first_row = 0: the reference).
+__device__ __forceinline__ void causal_mask_body(float* m, int rows, int cols, int first_row) {
     for (int r = blockIdx.y; r < rows; r += gridDim.y)
         for (int c = blockIdx.x * EW_THREADS + threadIdx.x; c < cols;
              c += gridDim.x * EW_THREADS)
-            if (c > r) m[(long long)r * cols + c] = -INFINITY;
+            if (c > first_row + r) m[(long long)r * cols + c] = -INFINITY;
 }
 
 // ------------------------------------------------------------ reductions

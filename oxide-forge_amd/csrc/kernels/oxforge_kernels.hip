@@ -219,8 +219,9 @@ FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_count_final(const unsigned
                                                                   float* out) {
     count_final_body(part, n, out);
 }
-FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_causal_mask(float* m, int rows, int cols) {
-    causal_mask_body(m, rows, cols);
+FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_causal_mask(float* m, int rows, int cols,
+                                                                  int first_row) {
+    causal_mask_body(m, rows, cols, first_row);
 }
 FORGE_KERNEL void __launch_bounds__(SUMCOL_WAVES * 64) forge_sum_cols_v(const float* m, float* out,
                                                                        int rows, int cols,

@@ -600,6 +600,52 @@ static float score_scale(size_t query_cols) {
     return 1.0f / std::sqrt((float)query_cols);
 }
 
+// Query rows per score chunk: all of them while S x Sk floats fit the
+// budget, else the largest multiple of 64 rows that does (at least 64).
+static size_t score_chunk_rows(size_t S, size_t Sk, size_t budget_bytes) {
+    const size_t row_bytes = Sk * sizeof(float);
+    if (row_bytes == 0 || S <= budget_bytes / row_bytes) return S;
+    return std::max<size_t>(64, budget_bytes / row_bytes / 64 * 64);
+}
+
+// Rows r0 .. r0 + n - 1 of a row-major matrix as a slice.
+static forge_slice rows_of(const Matrix& m, size_t r0, size_t n) {
+    return forge_slice{m.buffer().ptr() + r0 * m.cols(), n * m.cols()};
+}
+
+static void gemm_slices(CudaRuntime& rt, bool ta, bool tb, forge_slice a, forge_slice b,
+                        forge_slice c, size_t m, size_t n, size_t k,
+                        const forge_gemm_epilogue& ep, const char* what) {
+    check(forge_gemm_ex_f32(rt.raw(), nullptr, ta ? 1 : 0, tb ? 1 : 0, a, b, c, m, n, k, &ep),
+          what);
+}
+
+void Attention::chunked_forward(const Matrix& q, const Matrix& k, const Matrix& v,
+                                const Matrix& residual, bool mask, size_t chunk, Matrix& out,
+                                CudaRuntime& rt) {
+    // attention.rs:359-387 one chunk of query rows at a time: the chunk's
+    // scores (NT GEMM, scale fused), mask, softmax, then its rows of
+    // P V + residual.  Each output row is the same sum as in the unchunked
+    // products.
+    const size_t S = q.rows(), Sk = k.rows(), D = q.cols(), H = v.cols();
+    Matrix scores = rt.new_uninit_matrix(std::min(chunk, S), Sk);
+    forge_gemm_epilogue ep = plain_epilogue();
+    ep.alpha = score_scale(D);
+    for (size_t r0 = 0; r0 < S; r0 += chunk) {
+        const size_t n = std::min(chunk, S - r0);
+        const forge_slice sc{scores.buffer().ptr(), n * Sk};
+        gemm_slices(rt, false, true, rows_of(q, r0, n), k.slice(), sc, n, Sk, D, ep,
+                    "attention scores");
+        if (mask)
+            check(forge_causal_mask_rows(rt.raw(), nullptr, sc, n, Sk, r0), "causal_mask");
+        check(forge_softmax_rows(rt.raw(), nullptr, sc, n, Sk), "softmax_rows");
+        forge_gemm_epilogue ep2 = plain_epilogue();
+        ep2.residual = rows_of(residual, r0, n);
+        gemm_slices(rt, false, false, sc, v.slice(), rows_of(out, r0, n), n, H, Sk, ep2,
+                    "attention value");
+    }
+}
+
 Matrix Attention::attention_value(QkvProjection::Projected projected, const Matrix& residual,
                                   bool mask, CudaRuntime& rt) {
     // attention.rs:336-387: S = Q K^T / sqrt(d) as one NT GEMM with the
@@ -609,6 +655,16 @@ Matrix Attention::attention_value(QkvProjection::Projected projected, const Matr
     const Matrix& q = projected.query;
     const Matrix& k = projected.key;
     require(q.cols() == k.cols(), "query/key widths");
+    const size_t chunk = score_chunk_rows(q.rows(), k.rows(), max_score_bytes_);
+    if (chunk < q.rows()) {
+        qkv_.wait_for_value(rt);
+        const Matrix& v = projected.value;
+        require(v.rows() == k.rows(), "value rows == key rows");
+        require(residual.rows() == q.rows() && residual.cols() == v.cols(), "residual shape");
+        Matrix out = rt.new_uninit_matrix(q.rows(), v.cols());
+        chunked_forward(q, k, v, residual, mask, chunk, out, rt);
+        return out;
+    }
     Matrix scores = rt.new_uninit_matrix(q.rows(), k.rows());
     forge_gemm_epilogue ep = plain_epilogue();
     ep.alpha = score_scale(q.cols());
@@ -648,6 +704,18 @@ Matrix Attention::forward_self_training(Matrix input, CudaRuntime& rt) {
     // attention.rs:258-281: keeps input, Q, K, V, P and the pre-norm sum.
     QkvProjection::Projected p = qkv_.project(input, input, rt);
     qkv_.wait_for_query_key(rt);
+    const size_t chunk = score_chunk_rows(p.query.rows(), p.key.rows(), max_score_bytes_);
+    if (chunk < p.query.rows()) {
+        // P is not cached: backward recomputes it chunk by chunk.
+        qkv_.wait_for_value(rt);
+        Matrix pre_norm = rt.new_uninit_matrix(p.query.rows(), p.value.cols());
+        chunked_forward(p.query, p.key, p.value, input, false, chunk, pre_norm, rt);
+        Matrix output = rt.new_uninit_matrix(pre_norm.rows(), pre_norm.cols());
+        norm_.forward_into(pre_norm, output, rt);
+        cache_ = Cache{std::move(input), std::move(p.query), std::move(p.key), std::move(p.value),
+                       Matrix(), std::move(pre_norm)};
+        return output;
+    }
     Matrix probabilities = rt.new_uninit_matrix(p.query.rows(), p.key.rows());
     forge_gemm_epilogue ep = plain_epilogue();
     ep.alpha = score_scale(p.query.cols());
@@ -685,29 +753,68 @@ Matrix Attention::backward_self(const Matrix& output_gradient, float learning_ra
                            grads ? &grads->norm1_gamma : nullptr,
                            grads ? &grads->norm1_beta : nullptr);
 
-    // dP = R V^T (NT), dV = P^T R (TN).
-    Matrix probabilities_gradient = rt.new_uninit_matrix(S, Sk);
-    rt.gemm_ex(nullptr, false, true, residual_gradient, c.value, probabilities_gradient.slice(),
-               S, Sk, H, plain_epilogue());
-    Matrix value_gradient = rt.new_uninit_matrix(Sk, H);
-    rt.gemm_ex(nullptr, true, false, c.probabilities, residual_gradient, value_gradient.slice(),
-               Sk, H, S, plain_epilogue());
-    // dS = softmax_bwd(P, dP) / sqrt(d), fused.
-    Matrix score_gradient = rt.new_uninit_matrix(S, Sk);
-    check(forge_softmax_rows_bwd_scaled(rt.raw(), nullptr, c.probabilities.slice(),
-                                        probabilities_gradient.slice(), score_gradient.slice(),
-                                        S, Sk, score_scale(c.query.cols())),
-          "softmax_rows_backward");
-    probabilities_gradient = Matrix();
-    // dQ = dS K (NN), dK = dS^T Q (TN).
     const size_t D = c.query.cols();
-    Matrix query_gradient = rt.new_uninit_matrix(S, D);
-    rt.gemm_ex(nullptr, false, false, score_gradient, c.key, query_gradient.slice(), S, D, Sk,
-               plain_epilogue());
-    Matrix key_gradient = rt.new_uninit_matrix(Sk, D);
-    rt.gemm_ex(nullptr, true, false, score_gradient, c.query, key_gradient.slice(), Sk, D, S,
-               plain_epilogue());
-    score_gradient = Matrix();
+    Matrix query_gradient, key_gradient, value_gradient;
+    if (c.probabilities.len() == 0 && S > 0 && Sk > 0) {
+        // Chunked: per chunk of query rows, P recomputed as in the forward,
+        // then dP = R V^T, dV += P^T R, dS = softmax_bwd(P, dP) / sqrt(d),
+        // dQ = dS K, dK += dS^T Q; dV and dK sum the chunks in order.
+        const size_t chunk = score_chunk_rows(S, Sk, max_score_bytes_);
+        const size_t cr = std::min(chunk, S);
+        Matrix p_c = rt.new_uninit_matrix(cr, Sk), dp_c = rt.new_uninit_matrix(cr, Sk),
+               ds_c = rt.new_uninit_matrix(cr, Sk);
+        query_gradient = rt.new_uninit_matrix(S, D);
+        key_gradient = rt.new_uninit_matrix(Sk, D);
+        value_gradient = rt.new_uninit_matrix(Sk, H);
+        const float scale = score_scale(D);
+        for (size_t r0 = 0; r0 < S; r0 += chunk) {
+            const size_t n = std::min(chunk, S - r0);
+            const forge_slice ps{p_c.buffer().ptr(), n * Sk}, dps{dp_c.buffer().ptr(), n * Sk},
+                dss{ds_c.buffer().ptr(), n * Sk};
+            forge_gemm_epilogue ep = plain_epilogue();
+            ep.alpha = scale;
+            gemm_slices(rt, false, true, rows_of(c.query, r0, n), c.key.slice(), ps, n, Sk, D, ep,
+                        "attention scores");
+            check(forge_softmax_rows(rt.raw(), nullptr, ps, n, Sk), "softmax_rows");
+            gemm_slices(rt, false, true, rows_of(residual_gradient, r0, n), c.value.slice(), dps,
+                        n, Sk, H, plain_epilogue(), "dP");
+            forge_gemm_epilogue acc = plain_epilogue();
+            if (r0 > 0) acc.residual = value_gradient.slice();
+            gemm_slices(rt, true, false, ps, rows_of(residual_gradient, r0, n),
+                        value_gradient.slice(), Sk, H, n, acc, "dV");
+            check(forge_softmax_rows_bwd_scaled(rt.raw(), nullptr, ps, dps, dss, n, Sk, scale),
+                  "softmax_rows_backward");
+            gemm_slices(rt, false, false, dss, c.key.slice(), rows_of(query_gradient, r0, n), n,
+                        D, Sk, plain_epilogue(), "dQ");
+            forge_gemm_epilogue acck = plain_epilogue();
+            if (r0 > 0) acck.residual = key_gradient.slice();
+            gemm_slices(rt, true, false, dss, rows_of(c.query, r0, n), key_gradient.slice(), Sk,
+                        D, n, acck, "dK");
+        }
+    } else {
+        // dP = R V^T (NT), dV = P^T R (TN).
+        Matrix probabilities_gradient = rt.new_uninit_matrix(S, Sk);
+        rt.gemm_ex(nullptr, false, true, residual_gradient, c.value, probabilities_gradient.slice(),
+                   S, Sk, H, plain_epilogue());
+        value_gradient = rt.new_uninit_matrix(Sk, H);
+        rt.gemm_ex(nullptr, true, false, c.probabilities, residual_gradient, value_gradient.slice(),
+                   Sk, H, S, plain_epilogue());
+        // dS = softmax_bwd(P, dP) / sqrt(d), fused.
+        Matrix score_gradient = rt.new_uninit_matrix(S, Sk);
+        check(forge_softmax_rows_bwd_scaled(rt.raw(), nullptr, c.probabilities.slice(),
+                                            probabilities_gradient.slice(), score_gradient.slice(),
+                                            S, Sk, score_scale(c.query.cols())),
+              "softmax_rows_backward");
+        probabilities_gradient = Matrix();
+        // dQ = dS K (NN), dK = dS^T Q (TN).
+        query_gradient = rt.new_uninit_matrix(S, D);
+        rt.gemm_ex(nullptr, false, false, score_gradient, c.key, query_gradient.slice(), S, D, Sk,
+                   plain_epilogue());
+        key_gradient = rt.new_uninit_matrix(Sk, D);
+        rt.gemm_ex(nullptr, true, false, score_gradient, c.query, key_gradient.slice(), Sk, D, S,
+                   plain_epilogue());
+        score_gradient = Matrix();
+    }
 
     // QkvProjection::backward_self: per projection dX accumulates and W, b
     // are updated (dW, db kept when grads are requested).

@@ -436,6 +436,11 @@ extern "C" forge_status forge_net_transformer_backward(forge_net_model* m, forge
     });
 }
 
+extern "C" forge_status forge_net_transformer_set_score_bytes(forge_net_model* m, size_t bytes) {
+    if (!m || (!m->enc_inf && !m->enc_train && !m->dec_inf)) return FORGE_EINVAL;
+    return guard([&] { parts_of(m).attention->set_max_score_bytes(bytes); });
+}
+
 extern "C" forge_status forge_net_transformer_param(forge_net_model* m, int slot,
                                                     forge_slice* out) {
     if (!m || !out || (!m->enc_inf && !m->enc_train && !m->dec_inf)) return FORGE_EINVAL;

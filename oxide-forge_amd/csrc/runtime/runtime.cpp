@@ -1710,14 +1710,23 @@ extern "C" forge_status forge_fill_seq(forge_runtime* rt, forge_stream* s, forge
                        dim3(EW_THREADS), 0, x.ptr, nn, asc);
 }
 
-extern "C" forge_status forge_causal_mask(forge_runtime* rt, forge_stream* s, forge_slice m,
-                                          size_t rows, size_t cols) {
+extern "C" forge_status forge_causal_mask_rows(forge_runtime* rt, forge_stream* s,
+                                               forge_slice m, size_t rows, size_t cols,
+                                               size_t first_row) {
     if (!rt) return fail(FORGE_EINVAL, "runtime is null");
     FORGE_TRY(check_rows(rows, cols));
+    if (!fits_int(first_row) || !fits_int(first_row + rows))
+        return fail(FORGE_EINVAL, "first_row + rows exceeds 2^31-1");
     FORGE_TRY(need(m, rows * cols, "causal_mask m"));
     if (rows == 0 || cols == 0) return FORGE_OK;
     unsigned gx = (unsigned)std::min<size_t>((cols + EW_THREADS - 1) / EW_THREADS, 64);
     unsigned gy = (unsigned)std::min<size_t>(rows, 65535);
-    int r = (int)rows, c = (int)cols;
-    return launch_args(rt, s, "forge_causal_mask", dim3(gx, gy), dim3(EW_THREADS), 0, m.ptr, r, c);
+    int r = (int)rows, c = (int)cols, f = (int)first_row;
+    return launch_args(rt, s, "forge_causal_mask", dim3(gx, gy), dim3(EW_THREADS), 0, m.ptr, r, c,
+                       f);
+}
+
+extern "C" forge_status forge_causal_mask(forge_runtime* rt, forge_stream* s, forge_slice m,
+                                          size_t rows, size_t cols) {
+    return forge_causal_mask_rows(rt, s, m, rows, cols, 0);
 }

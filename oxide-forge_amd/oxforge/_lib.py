@@ -147,6 +147,7 @@ SIGNATURES = {
     "forge_reduce_max": [RT, ST, Slice, c_size_t, Slice],
     "forge_fill_seq": [RT, ST, Slice, c_size_t, c_int],
     "forge_causal_mask": [RT, ST, Slice, c_size_t, c_size_t],
+    "forge_causal_mask_rows": [RT, ST, Slice, c_size_t, c_size_t, c_size_t],
     "forge_softmax_rows_bwd_scaled": [RT, ST, Slice, Slice, Slice, c_size_t, c_size_t, c_float],
     "forge_activation_backward": [RT, ST, Slice, Slice, Slice, c_size_t, c_int],
     "forge_sgd_update": [RT, ST, Slice, Slice, c_size_t, c_float],

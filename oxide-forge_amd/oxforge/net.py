@@ -45,6 +45,7 @@ SIGNATURES = {
     "forge_net_transformer_forward": [c_void_p, Slice, Slice],
     "forge_net_transformer_backward": [c_void_p, Slice, c_float, Slice, POINTER(Slice)],
     "forge_net_transformer_param": [c_void_p, c_int, POINTER(Slice)],
+    "forge_net_transformer_set_score_bytes": [c_void_p, c_size_t],
     "forge_net_checkpoint_save": [c_void_p, c_char_p],
     "forge_net_checkpoint_load": [c_void_p, c_char_p, c_int, POINTER(c_void_p)],
     "forge_checkpoint_inspect": [c_char_p, c_char_p, c_size_t, POINTER(c_uint64)],
@@ -241,6 +242,11 @@ class Transformer(_Model):
             gptr = (Slice * len(TP_SLOTS))(*[grads[k].slice for k in TP_SLOTS])
         call("forge_net_transformer_backward", self.h, dY.slice, lr, _sl(dX), gptr)
         return grads
+
+    def set_score_bytes(self, nbytes):
+        """Largest [seq, seq] score matrix held at once; above it attention
+        runs in chunks of query rows (Attention::set_max_score_bytes)."""
+        call("forge_net_transformer_set_score_bytes", self.h, nbytes)
 
     def param(self, name):
         sl = Slice()

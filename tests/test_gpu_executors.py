@@ -163,6 +163,66 @@ def test_qkv_forked_streams_match_batched_bit_exact(rt, S, H, F, O, kind):
     Tb.close()
 
 
+@pytest.mark.parametrize("kind", [net.ENCODER_INFERENCE, net.DECODER_INFERENCE])
+@pytest.mark.parametrize("chunk_rows", [64, 128])
+def test_query_chunked_attention_forward(rt, kind, chunk_rows):
+    """With a score budget below seq x seq, attention runs one chunk of
+    query rows at a time (320 rows: five chunks of 64, or 128 + 128 + 64; the
+    decoder's causal mask offset per chunk).  Each output row is the same
+    sequence of rounded operations as unchunked, so the forward is
+    bit-identical to the unchunked one, and matches the f64 oracle."""
+    S, H, F, O = 320, 64, 128, 48
+    say(f"chunked attention forward kind={kind} chunk={chunk_rows}")
+    p = make_params(S, H, F, O, 42, bias=True, affine=True, norm=net.LAYER)
+    X = synth.normal((S, H), 9)
+    Tc = net.Transformer(rt, p, S, H, F, O, net.LAYER, kind)
+    Tu = net.Transformer(rt, p, S, H, F, O, net.LAYER, kind)
+    Tc.set_score_bytes(chunk_rows * S * 4)
+    dX = rt.array(X)
+    yc, yu = Tc.forward(dX).numpy(), Tu.forward(dX).numpy()
+    assert np.array_equal(yc, yu)
+    ref, _ = ex.transformer_forward(p, X, net.LAYER, causal=(kind == net.DECODER_INFERENCE))
+    assert rel(yc, ref) <= TOL
+    Tc.close()
+    Tu.close()
+
+
+@pytest.mark.parametrize("S,chunk_rows", [(320, 64), (320, 128), (512, 192)])
+def test_query_chunked_attention_training_step(rt, S, chunk_rows):
+    """Training with the score budget below seq x seq: the forward keeps no
+    probabilities and backward recomputes them per chunk (dV and dK summed
+    over the chunks in order).  The forward output is bit-identical to the
+    unchunked step; dX and every parameter gradient match the f64 oracle, and
+    the unchunked step's to within 1e-5 relative."""
+    H, F, O = 64, 128, 48
+    say(f"chunked attention training S={S} chunk={chunk_rows}")
+    p = make_params(S, H, F, O, 43, bias=True, affine=True, norm=net.LAYER)
+    X = synth.normal((S, H), 10)
+    dY = synth.normal((S, O), 11)
+    lr = 1e-3
+    Tc = net.Transformer(rt, p, S, H, F, O, net.LAYER, net.ENCODER_TRAINING)
+    Tu = net.Transformer(rt, p, S, H, F, O, net.LAYER, net.ENCODER_TRAINING)
+    Tc.set_score_bytes(chunk_rows * S * 4)
+    yc, yu = Tc.forward(rt.array(X)).numpy(), Tu.forward(rt.array(X)).numpy()
+    assert np.array_equal(yc, yu)
+    dxc, dxu = rt.empty((S, H)), rt.empty((S, H))
+    gc = Tc.backward(rt.array(dY), lr, dxc, want_grads=True)
+    gu = Tu.backward(rt.array(dY), lr, dxu, want_grads=True)
+    _, cache = ex.transformer_forward(p, X, net.LAYER)
+    rdX, rg = ex.transformer_backward(p, cache, dY, net.LAYER)
+    assert rel(dxc.numpy(), rdX) <= TOL
+    assert rel(dxc.numpy(), dxu.numpy()) <= 1e-5
+    for k in net.TP_SLOTS:
+        g = gc[k].numpy()
+        if k == "BK":
+            assert np.max(np.abs(g)) / np.max(np.abs(rg["BV"])) <= TOL
+            continue
+        assert rel(g, rg[k]) <= TOL, k
+        assert rel(g, gu[k].numpy()) <= 1e-5, k
+    Tc.close()
+    Tu.close()
+
+
 TRAIN_CASES = [
     ("layer small", 64, 64, 256, 64, net.LAYER, True, True),
     ("rms small no-bias", 48, 32, 96, 40, net.RMS, False, True),
