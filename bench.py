@@ -371,14 +371,7 @@ def sweep(rt, steps, warmup):
 
     lib = oxforge.load()
     res = {}
-    shapes = [(4096, 4096, 4096), (8192, 1024, 4096),
-              # C4 GEMMs: QKV/out, QK^T, AV, FFN1, FFN2
-              (2048, 1024, 1024), (2048, 2048, 1024), (2048, 1024, 2048), (2048, 4096, 1024),
-              (2048, 1024, 4096),
-              # C5 GEMMs
-              (4096, 2048, 2048), (4096, 4096, 2048), (4096, 2048, 4096), (4096, 8192, 2048),
-              (4096, 2048, 8192), (2048, 2048, 4096), (2048, 8192, 4096)]
-    for (M, N, K) in shapes:
+    for (M, N, K) in GEMM_SHAPES:
         A = synth.uniform((M, K), 3)
         B = synth.uniform((K, N), 4)
         dA, dB, dC = rt.array(A), rt.array(B), rt.empty((M, N))
@@ -412,6 +405,49 @@ def sweep(rt, steps, warmup):
         for d in (dA, dB, dC):
             d.recycle()
     return res
+
+
+GEMM_SHAPES = [(4096, 4096, 4096), (8192, 1024, 4096),
+               # C4 GEMMs: QKV/out, QK^T, AV, FFN1, FFN2
+               (2048, 1024, 1024), (2048, 2048, 1024), (2048, 1024, 2048), (2048, 4096, 1024),
+               (2048, 1024, 4096),
+               # C5 GEMMs
+               (4096, 2048, 2048), (4096, 4096, 2048), (4096, 2048, 4096), (4096, 8192, 2048),
+               (4096, 2048, 8192)]
+
+
+def vendor_gemm(steps, warmup):
+    """The vendor library on the same plain products, for comparison only:
+    torch.mm on the GPU (hipBLASLt / rocBLAS as PyTorch dispatches it) in
+    strict fp32 (TF32 off), timed with events on torch's current stream over
+    `steps` launches after a spin-up, as time_launches does."""
+    import torch
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    torch.backends.cudnn.allow_tf32 = False
+    res = {}
+    dev = torch.device("cuda:0")
+    for (M, N, K) in GEMM_SHAPES:
+        a = torch.from_numpy(synth.uniform((M, K), 3)).to(dev)
+        b = torch.from_numpy(synth.uniform((K, N), 4)).to(dev)
+        c = torch.empty((M, N), device=dev)
+        t0 = time.perf_counter()
+        i = 0
+        while i < warmup or time.perf_counter() - t0 < SPIN_UP_S:
+            torch.mm(a, b, out=c)
+            i += 1
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            torch.mm(a, b, out=c)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        res[f"{M}x{N}x{K}"] = round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 2)
+        log(f"vendor {M}x{N}x{K}: {res[f'{M}x{N}x{K}']} TFLOP/s")
+        del a, b, c
+    return {"library": f"torch {torch.__version__} torch.mm, fp32 (TF32 off)", "tflops": res}
 
 
 def profile_workload(rt, name, steps, warmup):
@@ -463,6 +499,12 @@ def profile_workload(rt, name, steps, warmup):
             ms = time_launches(rt, step, steps, warmup)
         T.close()
         return {"workload": name, "ms": round(ms, 4)}
+    if name == "gemms":
+        ours = {}
+        for (M, N, K) in GEMM_SHAPES:
+            t, _ = gemm_tflops(rt, M, N, K, steps, warmup)
+            ours[f"{M}x{N}x{K}"] = {"tflops": round(t, 2), "kernel": rt.gemm_kernel_name(M, N, K)}
+        return {"workload": name, "results": ours}
     if name == "rows":
         return {"workload": name, "results": secondary_rows(rt, steps, warmup, min_launches=1)}
     if name == "rows65536":
@@ -536,8 +578,9 @@ def main() -> int:
     ap.add_argument("--extended", action="store_true")
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--profile", default=None,
-                    help="run only one workload (gemm4096, gemm8192x1024, copy, transpose, rows, "
-                         "rows65536, c4, c5) for rocprofv3")
+                    help="run only one workload (gemm4096, gemm8192x1024, gemms, copy, transpose, "
+                         "rows, rows65536, c4, c5) for rocprofv3, or vendor (torch.mm on the same "
+                         "GEMM shapes, in a process without this build's runtime)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -545,6 +588,13 @@ def main() -> int:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE "
               f"{world}); this build has no multi-GPU path.", file=sys.stderr)
         return 2
+
+    if args.profile == "vendor":
+        # torch's own HIP runtime: in a process of its own (a second HIP
+        # runtime beside this build's finds no device).
+        print(json.dumps({"workload": "vendor", "results": vendor_gemm(args.steps, args.warmup)}),
+              flush=True)
+        return 0
 
     import oxforge
 
