@@ -268,6 +268,26 @@ def test_fill_random_hash_restated_independently():
     assert np.array_equal(orc.fill_random(5000, seed), ref)
 
 
+def test_fill_random_hash_known_answers():
+    # Hand-derived values of common.rs:3-9 (wrapping u32):
+    #   x=1: 1 + (1<<13) = 0x2001; 0x2001>>17 = 0; 0x2001 * (0x2001<<5) =
+    #        8193 * 262176 = 2148007968 (< 2^32).
+    #   x=2: 0x4002; >>17 = 0; 16386 * 524352 = 8592031872 = 2*2^32 + 2097280.
+    #   x=0xFFFFFFFF: + (x<<13 = 0xFFFFE000) wraps to 0xFFFFDFFF; minus
+    #        (0xFFFFDFFF>>17 = 0x7FFF) = 0xFFFF6000 = -40960; x<<5 = 0xFFEC0000
+    #        = -1310720; product 53687091200 = 12*2^32 + 0x80000000.
+    # elementwise.rs:40-41 hashes seed + index (wrapping) and divides by
+    # u32::MAX as f32 (= 2^32), so 0x80000000 maps to exactly 0.5.
+    two32 = np.float32(4294967295.0)
+    got = orc.fill_random(3, 0)
+    assert got[0] == 0.0
+    assert got[1] == np.float32(2148007968) / two32
+    assert got[2] == np.float32(2097280) / two32
+    wrap = orc.fill_random(2, 0xFFFFFFFF)
+    assert wrap[0] == np.float32(0.5)
+    assert wrap[1] == 0.0  # seed + 1 wraps to 0
+
+
 def test_activation_backward_is_dy_times_derivative():
     r = rng(11)
     dy = r.normal(0, 1, 500).astype(np.float32)
