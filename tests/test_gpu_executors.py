@@ -2,8 +2,8 @@
 training step) against the f64 executor oracle (oracle/executors.py).
 
 Bar: max|GPU - oracle| / max|oracle| <= 1e-4 for every output, input
-gradient and parameter gradient (the north star's GEMM/attention bound,
-applied to the whole composition); the SGD update is checked bit-exactly as
+gradient and parameter gradient (the GEMM/attention bound, applied to the
+whole composition); the SGD update is checked bit-exactly as
 W_new == fl(W - fl(lr * dW)) from the returned f32 gradient.
 """
 import numpy as np

@@ -1,6 +1,6 @@
 """GPU parity of every kernel behind the C ABI against the CPU oracle.
 
-Bars (from the task's north star):
+Bars:
   - transpose, copy, broadcast, binary ops, fills: bit-exact;
   - GEMM: max|C - C64| / max|C64| <= 1e-4 and componentwise
     |C - C64| / (|A| |B|) <= 1e-4 against an f64-accumulated oracle, and
@@ -8,7 +8,7 @@ Bars (from the task's north star):
     permutations);
   - softmax and norms, forward and backward: <= 1e-5 absolute;
   - maps built on tanhf/expf: <= 2e-6 absolute + relative.
-Full BASELINE sizes are covered directly (row ops, transpose) or through
+The full benchmark sizes are covered directly (row ops, transpose) or through
 sampled rows checked against the f64 oracle (GEMM).
 """
 import numpy as np
