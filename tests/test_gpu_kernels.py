@@ -1025,3 +1025,75 @@ def test_transposed_operands_bit_identical_to_materialised_transpose(rt, M, N, K
     rt.gemm_ex(dA, dBt, c1, M, N, K, trans_b=True)
     rt.gemm_ex(dA, dBn, c2, M, N, K)
     assert np.array_equal(c1.numpy(), c2.numpy())
+
+
+def test_zero_sized_inputs(rt):
+    """Every entry point accepts zero-sized shapes (the reference's spans
+    and matrices may be empty, span.rs:302-359) and writes only what the
+    empty case defines: a sum over no elements or rows is 0, a max over
+    none is f32::MIN (span.rs:319-321), and a norm backward over no rows
+    gives zero dgamma / dbeta and leaves gamma / beta where its SGD step
+    would move them.  Everything else is left as it was."""
+    say("zero-sized inputs")
+    sent = np.full(16, 7.0, np.float32)
+    a, b, o = rt.array(sent), rt.array(sent), rt.array(sent)
+
+    def untouched(*xs):
+        return all(np.array_equal(x.numpy(), sent) for x in xs)
+
+    rt.binary(a, b, o, oxforge.ADD, n=0)
+    rt.binary_assign(o, a, oxforge.MUL, n=0)
+    rt.map(o, oxforge.MAP_GELU, n=0)
+    rt.fill_seq(o, n=0)
+    rt.fill_random(o, 5, n=0)
+    rt.sgd_update(o, a, 0.1, n=0)
+    rt.activation_backward(a, b, o, oxforge.ACT_GELU, n=0)
+    rt.copy(o, a, n=0)
+    for M, N, K in ((0, 4, 4), (4, 0, 4)):
+        rt.gemm(a, b, o, M, N, K)
+    assert untouched(a, b, o)
+    for rows, cols in ((0, 4), (4, 0)):
+        rt.softmax_rows(o, rows, cols)
+        rt.layer_norm(o, rows, cols, a, b)
+        rt.rms_norm(o, rows, cols, a)
+        rt.softmax_rows_bwd(a, b, o, rows, cols)
+        rt.binary_assign_by_rows(o, a, rows, cols, oxforge.ADD)
+        rt.causal_mask(o, rows, cols)
+        rt.transpose(a, o, rows, cols)
+        rt.layer_norm_bwd(a, b, o, rows, cols)
+        rt.rms_norm_bwd(a, b, o, rows, cols)
+        assert untouched(a, b, o), (rows, cols)
+
+    # Sums over empty ranges are zero; the max over none is f32::MIN.
+    s = rt.array(sent)
+    rt.sum_rows(a, s, 4, 0)
+    assert np.array_equal(s.numpy()[:4], np.zeros(4, np.float32))
+    assert np.array_equal(s.numpy()[4:], sent[4:])
+    s = rt.array(sent)
+    rt.sum_cols(a, s, 0, 4)
+    assert np.array_equal(s.numpy()[:4], np.zeros(4, np.float32))
+    assert np.array_equal(s.numpy()[4:], sent[4:])
+    s = rt.array(sent)
+    rt.reduce_sum(a, s, n=0)
+    rt.map_sum(a, s.view(1, (1,)), oxforge.MAP_HALF_SQ, n=0)
+    rt.compare(a, b, s.view(2, (1,)), n=0)
+    rt.reduce_max(a, s.view(3, (1,)), n=0)
+    assert np.array_equal(s.numpy()[:4], np.array([0, 0, 0, -3.4028235e38], np.float32))
+
+    # Norm backward over no rows: zero gradients; the SGD step leaves the
+    # parameters as they are.
+    gam, bet, dg, db = rt.array(sent), rt.array(sent), rt.array(sent), rt.array(sent)
+    rt.layer_norm_bwd(a, b, o, 0, 4, gam, dg, db)
+    assert np.array_equal(dg.numpy()[:4], np.zeros(4, np.float32))
+    assert np.array_equal(db.numpy()[:4], np.zeros(4, np.float32))
+    dg, db = rt.array(sent), rt.array(sent)
+    rt.layer_norm_bwd_sgd(a, b, o, 0, 4, 0.5, gam, bet, dg, db)
+    rt.rms_norm_bwd_sgd(a, b, o, 0, 4, 0.5, gam, dg)
+    assert np.array_equal(dg.numpy()[:4], np.zeros(4, np.float32))
+    assert np.array_equal(db.numpy()[:4], np.zeros(4, np.float32))
+    assert untouched(gam, bet, o)
+    s = rt.array(sent)
+    prm = rt.array(sent)
+    rt.sum_cols_sgd(a, 0, 4, 0.5, out=s, param=prm)
+    assert np.array_equal(s.numpy()[:4], np.zeros(4, np.float32))
+    assert untouched(prm)
