@@ -45,7 +45,8 @@ GEMM_FAMILY(tt, true, true)
 
 // Batched instances (forge_gemm_batch_<ab>_<tile>): several same-shape
 // products per launch, each with its own operands and epilogue.  They serve
-// the Q/K/V projections and the K slices of split-K products.
+// the Q/K/V projections, forge_gemm_batch_f32 and the K slices of split-K
+// products, so every operand layout has them.
 #define GEMM_BATCH_KERNEL(NAME, BM, BN, BK, TA, TB)                                    \
     FORGE_KERNEL void __launch_bounds__(256, GEMM_X_OCC(BM, BN, BK)) NAME(GemmBatchArgs b) { \
         gemm_batch_x<BM, BN, BK, TA, TB>(b);                                         \
@@ -58,6 +59,7 @@ GEMM_FAMILY(tt, true, true)
 GEMM_BATCH_FAMILY(nn, false, false)
 GEMM_BATCH_FAMILY(nt, false, true)
 GEMM_BATCH_FAMILY(tn, true, false)
+GEMM_BATCH_FAMILY(tt, true, true)
 
 // Split-K: sum of the partial products in split order, then the epilogue.
 FORGE_KERNEL void __launch_bounds__(SPLITK_THREADS) forge_gemm_splitk_reduce_v(const float* P,

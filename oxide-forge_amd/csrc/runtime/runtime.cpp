@@ -1228,13 +1228,6 @@ extern "C" forge_status forge_gemm_batch_f32(forge_runtime* rt, forge_stream* s,
                                              size_t count, const forge_gemm_problem* problems) {
     if (!rt) return fail(FORGE_EINVAL, "runtime is null");
     if (count > 0 && !problems) return fail(FORGE_EINVAL, "problems is null");
-    if (trans_a && trans_b) {
-        // No batched TT instance: one launch per product.
-        for (size_t z = 0; z < count; z++)
-            FORGE_TRY(gemm_dispatch(rt, s, 1, 1, problems[z].A, problems[z].B, problems[z].C, M,
-                                    N, K, &problems[z].epilogue, false));
-        return FORGE_OK;
-    }
     GemmBatchArgs b{};
     bool all_aligned = true;
     for (size_t z = 0; z < count; z++) {

@@ -69,7 +69,8 @@ def dispatcher_kernel_names():
             names.append(f"forge_gemm_{ab}_{tag}_e")
     for tag in tiles + ("128x256x32_x", "64x64x16_2x2_g"):
         names.append(f"forge_gemm_nn_{tag}")
-    for ab in ("nn", "nt", "tn"):
+    # batched (forge_gemm_batch_f32, Q/K/V and split-K slices): every layout
+    for ab in ("nn", "nt", "tn", "tt"):
         for tag in tiles:
             names.append(f"forge_gemm_batch_{ab}_{tag}")
     # eight-wave 64x128 tile: plain NN, every epilogue kind, batched NN/NT/TN

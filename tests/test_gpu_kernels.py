@@ -60,6 +60,26 @@ def test_gemm_shapes_vs_oracle(rt, M, N, K, ta, tb):
         d.recycle()
 
 
+@pytest.mark.parametrize("M,N,K", [(64, 128, 65536), (33, 65, 40001)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
+def test_gemm_long_k_vs_oracle(rt, M, N, K, ta, tb):
+    """Long reductions: 65536 (the unguarded tiles, 2048 slabs) and 40001
+    (the guarded tile, a ragged last slab) products per output element,
+    against the f64-accumulated oracle at the same bars."""
+    say(f"gemm long K M={M} N={N} K={K} ta={ta} tb={tb}")
+    A = synth.uniform((K, M) if ta else (M, K), 7)
+    B = synth.uniform((N, K) if tb else (K, N), 8)
+    dA, dB, dC = rt.array(A), rt.array(B), rt.empty((M, N))
+    rt.gemm_ex(dA, dB, dC, M, N, K, trans_a=ta, trans_b=tb)
+    ref = orc.gemm_f64(A, B, ta, tb)
+    absprod = np.abs(op_a(A, ta)).astype(np.float64) @ np.abs(op_a(B, tb)).astype(np.float64)
+    rel_max, comp = gemm_errors(dC.numpy(), ref, absprod)
+    print(f"  long K {M}x{N}x{K}: rel_max {rel_max:.2e}, componentwise {comp:.2e}")
+    assert rel_max <= 1e-4 and comp <= 1e-4, (rel_max, comp)
+    for d in (dA, dB, dC):
+        d.recycle()
+
+
 def test_gemm_small_integers_bit_exact(rt):
     say("gemm small integers 512x384x4096")
     r = np.random.default_rng(0)
@@ -217,7 +237,7 @@ def test_transpose_unaligned_view(rt):
 
 # ---------------------------------------------------------------- row ops
 ROW_SHAPES = [(4096, 1024), (5, 1), (7, 3), (33, 63), (9, 100), (64, 256), (17, 1000),
-              (8, 1025), (16, 2048), (8, 4096), (4, 5000), (3, 9000)]
+              (8, 1025), (16, 2048), (8, 4096), (4, 5000), (3, 9000), (2, 65536)]
 
 
 @pytest.mark.parametrize("rows,cols", ROW_SHAPES)
