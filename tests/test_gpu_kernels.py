@@ -61,7 +61,7 @@ def test_gemm_shapes_vs_oracle(rt, M, N, K, ta, tb):
 
 
 @pytest.mark.parametrize("M,N,K", [(64, 128, 65536), (33, 65, 40001)])
-@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_gemm_long_k_vs_oracle(rt, M, N, K, ta, tb):
     """Long reductions: 65536 (the unguarded tiles, 2048 slabs) and 40001
     (the guarded tile, a ragged last slab) products per output element,
@@ -149,7 +149,7 @@ def test_gemm_full_size_sampled_rows(rt, M, N, K):
         d.recycle()
 
 
-@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
 @pytest.mark.parametrize("M,N,K", [(256, 128, 64), (50, 70, 33), (256, 128, 2048)])
 def test_gemm_epilogue_matches_unfused_bit_exact(rt, M, N, K, ta, tb):
     """Fused bias + residual + aux + activation + update equals the unfused
