@@ -301,3 +301,38 @@ def test_transformer_training_c5_full_size(rt):
     print("  " + " ".join(f"{k}={v:.1e}" for k, v in errs.items()))
     bad = {k: v for k, v in errs.items() if v > TOL}
     assert not bad, bad
+
+
+@pytest.mark.parametrize("act", [ex.IDENTITY, ex.RELU, ex.SILU])
+@pytest.mark.parametrize("norm", [net.LAYER, net.RMS])
+def test_transformer_ffn_activations(rt, act, norm):
+    """The FFN's first layer with each activation the reference offers
+    (linear.rs:21-70) besides GELU: encoder and decoder forward, and the
+    training step's gradients and SGD identity, against the f64 oracle."""
+    S, H, F, O = 64, 64, 192, 48
+    say(f"ffn activation {act} norm {norm}")
+    p = make_params(S, H, F, O, 60 + act, bias=True, affine=True, norm=norm)
+    X = synth.normal((S, H), 7)
+    for kind in (net.ENCODER_INFERENCE, net.DECODER_INFERENCE):
+        T = net.Transformer(rt, p, S, H, F, O, norm, kind, ffn_activation=act)
+        Y = T.forward(rt.array(X)).numpy()
+        ref, _ = ex.transformer_forward(p, X, norm, act, causal=(kind == net.DECODER_INFERENCE))
+        assert rel(Y, ref) <= TOL, kind
+        T.close()
+    dY = synth.normal((S, O), 8)
+    lr = np.float32(1e-3)
+    T = net.Transformer(rt, p, S, H, F, O, norm, net.ENCODER_TRAINING, ffn_activation=act)
+    Y = T.forward(rt.array(X)).numpy()
+    ref, cache = ex.transformer_forward(p, X, norm, act)
+    assert rel(Y, ref) <= TOL
+    dXd = rt.empty((S, H))
+    grads = T.backward(rt.array(dY), float(lr), dXd, want_grads=True)
+    rdX, rg = ex.transformer_backward(p, cache, dY, norm, act)
+    assert rel(dXd.numpy(), rdX) <= TOL
+    for k in net.TP_SLOTS:
+        if rg.get(k) is None or p.get(k) is None or k == "BK":
+            continue
+        g = grads[k].numpy()
+        assert rel(g, rg[k]) <= TOL, k
+        assert np.array_equal(T.param(k), p[k] - lr * g), f"SGD update of {k}"
+    T.close()
