@@ -1117,3 +1117,59 @@ def test_zero_sized_inputs(rt):
     rt.sum_cols_sgd(a, 0, 4, 0.5, out=s, param=prm)
     assert np.array_equal(s.numpy()[:4], np.zeros(4, np.float32))
     assert untouched(prm)
+
+
+def hash_fill(seed, start, count):
+    """forge_fill_random's values at indices start .. start + count - 1:
+    common.rs:3-9 on the wrapping u32 seed + index, divided by u32::MAX as
+    f32 (elementwise.rs:40-41), restated in numpy."""
+    x = (np.uint64(seed) + np.arange(start, start + count, dtype=np.uint64)) & 0xFFFFFFFF
+    x = (x + (x << 13)) & 0xFFFFFFFF
+    x = (x - (x >> 17)) & 0xFFFFFFFF
+    x = (x * ((x << 5) & 0xFFFFFFFF)) & 0xFFFFFFFF
+    return x.astype(np.float32) / np.float32(4294967295.0)
+
+
+def test_operands_beyond_4gib(rt):
+    """Operands of 4.0018 GiB (1,074,266,112 floats), filled on the device:
+    rows and elements past the 4 GiB byte offset go through the GEMM (A of
+    [262272, 4096]), the row kernels ([1049088, 1024]) and the streaming
+    kernels at the same bars as everywhere else, checked on sampled rows."""
+    n = 262272 * 4096
+    say(f"operands beyond 4 GiB: {n} floats")
+    a, b, c = rt.empty((n,)), rt.empty((n,)), rt.empty((n,))
+    rt.fill_random(a, 11)
+    rt.fill_random(b, 12)
+
+    # GEMM: A [262272, 4096] x B [4096, 64].
+    M, K, N = 262272, 4096, 64
+    B = synth.uniform((K, N), 13)
+    dB, dC = rt.array(B), rt.empty((M, N))
+    rt.gemm(a, dB, dC, M, N, K)
+    for r in (0, 262143, 262144, 262271):  # 262144 * 4096 * 4 B = 4 GiB
+        Ar = hash_fill(11, r * K, K)
+        ref = Ar.astype(np.float64) @ B.astype(np.float64)
+        got = dC.view(r * N, (N,)).numpy().astype(np.float64)
+        absprod = np.abs(Ar).astype(np.float64) @ np.abs(B).astype(np.float64)
+        assert np.max(np.abs(got - ref) / absprod) <= 1e-4, r
+
+    # Streaming: c = a + b, bit-exact past 2^30 floats.
+    rt.binary(a, b, c, oxforge.ADD)
+    for start in (0, 2**30 - 8, n - 4096):
+        want = hash_fill(11, start, 4096) + hash_fill(12, start, 4096)
+        assert np.array_equal(c.view(start, (4096,)).numpy(), want), start
+
+    # Row kernels on [1049088, 1024]: softmax in place, LayerNorm backward.
+    rows, cols = 1049088, 1024
+    rt.layer_norm_bwd(a, b, c, rows, cols)
+    for r in (0, 1048575, 1048576, rows - 1):  # row 1048576 starts at 4 GiB
+        x, dy = hash_fill(11, r * cols, cols)[None, :], hash_fill(12, r * cols, cols)[None, :]
+        dx = c.view(r * cols, (1, cols)).numpy()
+        assert np.max(np.abs(dx - orc.layer_norm_backward(x, dy, None))) <= TOL_ROW, r
+    rt.softmax_rows(a, rows, cols)
+    for r in (0, 1048576, rows - 1):
+        x = hash_fill(11, r * cols, cols)[None, :]
+        got = a.view(r * cols, (1, cols)).numpy()
+        assert np.max(np.abs(got - orc.softmax_rows(x))) <= TOL_ROW, r
+    for d in (a, b, c, dB, dC):
+        d.recycle()
