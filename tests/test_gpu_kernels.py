@@ -1173,3 +1173,25 @@ def test_operands_beyond_4gib(rt):
         assert np.max(np.abs(got - orc.softmax_rows(x))) <= TOL_ROW, r
     for d in (a, b, c, dB, dC):
         d.recycle()
+
+
+def test_gemm_pitch_beyond_unguarded_limit(rt):
+    """A row pitch above 2^21 floats (A^T of [64, 2^21 + 64] in a TN
+    product) goes to the bounds-guarded kernel, whose offsets are 64-bit;
+    rows on both sides of the 2^21 boundary match the f64 oracle."""
+    M, N, K = 2**21 + 64, 64, 64
+    say(f"gemm pitch {M} (tn)")
+    assert "_g" in rt.gemm_kernel_name(M, N, K, trans_a=True, fused=True)
+    at = rt.empty((K, M))
+    rt.fill_random(at, 21)
+    B = synth.uniform((K, N), 22)
+    dB, dC = rt.array(B), rt.empty((M, N))
+    rt.gemm_ex(at, dB, dC, M, N, K, trans_a=True)
+    for m in (0, 2**21 - 1, 2**21, M - 1):
+        a_row = np.array([hash_fill(21, k * M + m, 1)[0] for k in range(K)], np.float32)
+        ref = a_row.astype(np.float64) @ B.astype(np.float64)
+        absprod = np.abs(a_row).astype(np.float64) @ np.abs(B).astype(np.float64)
+        got = dC.view(m * N, (N,)).numpy().astype(np.float64)
+        assert np.max(np.abs(got - ref) / absprod) <= 1e-4, m
+    for d in (at, dB, dC):
+        d.recycle()
