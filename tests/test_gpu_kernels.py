@@ -453,12 +453,13 @@ def test_row_kernels_at_nontemporal_size(rt, affine):
     assert np.max(np.abs(pg.numpy() - rdg)) <= col_tol
 
 
-def test_norm_bwd_partials_at_scale_four_wave_instance(rt):
+@pytest.mark.parametrize("rows,cols", [(65536, 1024), (65537, 1000)])
+def test_norm_bwd_partials_at_scale_four_wave_instance(rt, rows, cols):
     """[65536, 1024] takes the four-wave partial instance (_p4: 256 rows per
-    CU and more).  dx against the oracle on every row; dgamma / dbeta (sums
-    over 65536 rows) at 1e-5 sqrt(rows); the measured relative error of
-    dgamma / dbeta is printed."""
-    rows, cols = 65536, 1024
+    CU and more; two workgroups per CU for the LayerNorm backward), and so
+    does [65537, 1000] with a ragged last row block and masked lanes.  dx
+    against the oracle on every row; dgamma / dbeta (sums over the rows) at
+    1e-5 sqrt(rows); the measured error of dgamma / dbeta is printed."""
     say(f"norm bwd partials {rows}x{cols}")
     x, dy = synth.normal((rows, cols), 51), synth.normal((rows, cols), 52)
     gam = synth.normal((cols,), 53, 1.0, 0.1)
