@@ -132,3 +132,74 @@ def test_row_kernels_random_shapes(rt, seed):
         assert np.max(np.abs(pg.numpy() - rdg)) <= col_tol
         for d in bufs + [pg, pb] + [d for d in (dgam, dbet) if d is not None]:
             d.recycle()
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_transformer_random_configs(rt, seed):
+    """Random single-block configurations: sequence, hidden, FFN and output
+    sizes (ragged ones take the guarded GEMM), LayerNorm or RMSNorm with or
+    without gamma / beta, biases or none, each FFN activation, encoder or
+    decoder inference (with or without forked Q/K/V streams) or the
+    training step, and a score budget that forces query-chunked attention
+    about half the time; output, input gradient and every parameter
+    gradient against the f64 oracle at 1e-4 of the largest value, and the
+    SGD identity on every updated parameter."""
+    from oracle import executors as ex
+    from oxforge import net
+
+    def rel(a, b):
+        b = np.asarray(b, np.float64)
+        return float(np.max(np.abs(np.asarray(a, np.float64) - b)) /
+                     max(np.max(np.abs(b)), 1e-30))
+
+    rng = np.random.default_rng(3000 + seed)
+    for case in range(6):
+        S, H = int(rng.integers(2, 300)), int(rng.integers(8, 97))
+        F, O = int(rng.integers(4, 257)), int(rng.integers(4, 81))
+        norm = int(rng.choice([net.LAYER, net.RMS]))
+        act = int(rng.integers(0, 4))
+        bias, affine = bool(rng.random() < 0.6), bool(rng.random() < 0.6)
+        kind = int(rng.choice([net.ENCODER_INFERENCE, net.DECODER_INFERENCE,
+                               net.ENCODER_TRAINING]))
+        streams = bool(rng.random() < 0.5) and kind != net.ENCODER_TRAINING
+        chunked = bool(rng.random() < 0.5)
+        say(f"seed {seed} case {case}: S={S} H={H} F={F} O={O} norm={norm} act={act} "
+            f"bias={bias} affine={affine} kind={kind} streams={streams} chunked={chunked}")
+        ps = int(rng.integers(0, 1 << 20))
+        p = {"WQ": synth.xavier(H, H, ps), "WK": synth.xavier(H, H, ps + 1),
+             "WV": synth.xavier(H, H, ps + 2), "POS": synth.xavier(S, H, ps + 3),
+             "W1": synth.xavier(H, F, ps + 4), "W2": synth.xavier(F, H, ps + 5),
+             "WO": synth.xavier(H, O, ps + 6)}
+        for i, (k, n) in enumerate((("BQ", H), ("BK", H), ("BV", H), ("B1", F), ("B2", H),
+                                    ("BO", O))):
+            p[k] = synth.normal((n,), ps + 10 + i, 0.0, 0.1) if bias else None
+        for i, k in enumerate(("G1", "G2")):
+            p[k] = synth.normal((H,), ps + 20 + i, 1.0, 0.1) if affine else None
+        for i, k in enumerate(("BE1", "BE2")):
+            p[k] = (synth.normal((H,), ps + 22 + i, 0.0, 0.1)
+                    if affine and norm == net.LAYER else None)
+        X = synth.normal((S, H), ps + 30)
+        T = net.Transformer(rt, p, S, H, F, O, norm, kind, streams, ffn_activation=act)
+        if chunked:
+            T.set_score_bytes(64 * S * 4)  # chunks of 64 query rows
+        Y = T.forward(rt.array(X)).numpy()
+        ref, cache = ex.transformer_forward(p, X, norm, act,
+                                            causal=(kind == net.DECODER_INFERENCE))
+        assert rel(Y, ref) <= 1e-4, "forward"
+        if kind == net.ENCODER_TRAINING:
+            dY = synth.normal((S, O), ps + 31)
+            lr = np.float32(1e-3)
+            dX = rt.empty((S, H))
+            grads = T.backward(rt.array(dY), float(lr), dX, want_grads=True)
+            rdX, rg = ex.transformer_backward(p, cache, dY, norm, act)
+            assert rel(dX.numpy(), rdX) <= 1e-4, "dX"
+            for k in net.TP_SLOTS:
+                if rg.get(k) is None or p.get(k) is None:
+                    continue
+                g = grads[k].numpy()
+                if k == "BK":  # zero in exact arithmetic (softmax shift invariance)
+                    assert np.max(np.abs(g)) <= 1e-4 * max(np.max(np.abs(rg["BV"])), 1e-30)
+                else:
+                    assert rel(g, rg[k]) <= 1e-4, k
+                assert np.array_equal(T.param(k), p[k] - lr * g), f"SGD update of {k}"
+        T.close()
