@@ -1196,3 +1196,63 @@ def test_gemm_pitch_beyond_unguarded_limit(rt):
         assert np.max(np.abs(got - ref) / absprod) <= 1e-4, m
     for d in (at, dB, dC):
         d.recycle()
+
+
+def test_runtime_plumbing(rt):
+    """Device properties, events, stream waits and destruction, forge_free
+    and the causal mask on a block of query rows (the chunked-attention
+    form of row.rs:5-14): results against host arithmetic or the oracle."""
+    from oxforge._lib import call
+
+    say("runtime plumbing")
+    props = rt.props()
+    assert props["cu_count"] > 0 and props["lds_bytes"] >= 65536
+    assert props["arch"].startswith("gfx950")
+
+    # Events bracket device work on a stream; elapsed time is positive and
+    # the recorded work is complete once it is read.
+    x = rt.array(np.zeros(1 << 20, np.float32))
+    e0, e1 = rt.event(), rt.event()
+    rt.record(e0)
+    for _ in range(8):
+        rt.map(x, oxforge.MAP_ADD, 1.0)
+    rt.record(e1)
+    assert rt.elapsed_ms(e0, e1) > 0.0
+    assert np.array_equal(x.numpy(), np.full(1 << 20, 8.0, np.float32))
+    rt.event_destroy(e0)
+    rt.event_destroy(e1)
+
+    # A stream waits for work queued on another; destroyed streams are gone.
+    s1, s2 = rt.streams_create(2)
+    y = rt.array(np.zeros(1 << 20, np.float32))
+    rt.sync()  # the upload is ordered on the primary stream only
+    for _ in range(4):
+        rt.map(y, oxforge.MAP_ADD, 1.0, stream=s1)
+    rt.stream_wait(s2, s1)
+    rt.map(y, oxforge.MAP_SCALE, 2.0, stream=s2)
+    rt.sync(s2)
+    assert np.array_equal(y.numpy(), np.full(1 << 20, 8.0, np.float32))
+    for s in (s1, s2):
+        call("forge_stream_destroy", rt.handle, s)
+
+    # forge_free releases a buffer instead of returning it to the pool.
+    n = 12345
+    a, b = rt.empty((n,)), rt.empty((n,))
+    held = rt.pool_count(n)
+    rt.free(a)
+    assert rt.pool_count(n) == held
+    b.recycle()
+    assert rt.pool_count(n) == held + 1
+
+    # The causal mask of query rows r0 .. r0 + rows - 1 of an [S, S] score
+    # matrix equals those rows of the full mask.
+    S, cols = 200, 200
+    full = synth.normal((S, cols), 9)
+    ref = orc.causal_mask(full)
+    for r0, rows in ((0, 64), (64, 64), (128, 72), (199, 1)):
+        blk = rt.array(full[r0:r0 + rows])
+        call("forge_causal_mask_rows", rt.handle, None, blk.slice, rows, cols, r0)
+        assert np.array_equal(blk.numpy(), ref[r0:r0 + rows]), r0
+    with pytest.raises(oxforge.ForgeError):
+        blk = rt.empty((2, 4))
+        call("forge_causal_mask_rows", rt.handle, None, blk.slice, 2, 4, 2**31 - 2)
