@@ -1256,3 +1256,30 @@ def test_runtime_plumbing(rt):
     with pytest.raises(oxforge.ForgeError):
         blk = rt.empty((2, 4))
         call("forge_causal_mask_rows", rt.handle, None, blk.slice, 2, 4, 2**31 - 2)
+
+
+@pytest.mark.parametrize("cols", [64, 1000, 4096, 5000])
+def test_row_kernels_special_values(rt, cols):
+    """Rows holding NaN, +inf, -inf or one constant value: the GPU's NaN and
+    infinity positions equal the oracle's (the reference's arithmetic: a
+    NaN or +inf poisons a softmax or LayerNorm row, -inf only zeroes its
+    softmax entry, a constant row normalises to zeros), and finite entries
+    meet the usual bar."""
+    say(f"row special values cols={cols}")
+    x = synth.normal((6, cols), 31)
+    x[0, 5] = np.nan
+    x[1, :] = 3.0
+    x[2, 7] = np.inf
+    x[3, 9] = -np.inf
+    x[4, 1] = np.inf
+    x[4, 2] = -np.inf
+    for name, fn, ref in (("softmax", lambda d: rt.softmax_rows(d, 6, cols), orc.softmax_rows(x)),
+                          ("layer_norm", lambda d: rt.layer_norm(d, 6, cols), orc.layer_norm(x)),
+                          ("rms_norm", lambda d: rt.rms_norm(d, 6, cols), orc.rms_norm(x))):
+        d = rt.array(x)
+        fn(d)
+        got = d.numpy()
+        assert np.array_equal(np.isnan(got), np.isnan(ref)), name
+        assert np.array_equal(np.isinf(got), np.isinf(ref)), name
+        fin = np.isfinite(ref)
+        assert np.max(np.abs(got[fin] - ref[fin]), initial=0.0) <= TOL_ROW, name
