@@ -505,12 +505,57 @@ def profile_workload(rt, name, steps, warmup):
             t, _ = gemm_tflops(rt, M, N, K, steps, warmup)
             ours[f"{M}x{N}x{K}"] = {"tflops": round(t, 2), "kernel": rt.gemm_kernel_name(M, N, K)}
         return {"workload": name, "results": ours}
+    if name == "ksweep":
+        return {"workload": name, "results": gemm_k_sweep(rt, steps, warmup)}
     if name == "rows":
         return {"workload": name, "results": secondary_rows(rt, steps, warmup, min_launches=1)}
     if name == "rows65536":
         return {"workload": name,
                 "results": secondary_rows_at_scale(rt, steps, warmup, min_launches=1)}
     raise SystemExit(f"unknown profile workload {name}")
+
+
+KSWEEP_TILES = ("64x128x32_x", "64x128x32_x8", "128x64x32_x")
+KSWEEP_KS = (32, 64, 128, 256, 512, 1024, 2048, 4096)
+
+
+def gemm_k_sweep(rt, steps, warmup):
+    """Plain 2048 x 1024 x K products (one tile per CU) for each tile in
+    KSWEEP_TILES and K in KSWEEP_KS, `steps` launches each after the clock
+    spin-up, with a 4096^3 product between groups so the device never idles
+    (its clock would drop).  Under rocprofv3 --kernel-trace the dispatches
+    give the per-launch cost and the per-slab rate, and `steps` 64-float
+    fills at the end a minimal launch to compare with; the returned event
+    timings are averages that include launch gaps at small K."""
+    M, N, W = 2048, 1024, 4096
+    wa, wb = rt.array(synth.uniform((W, W), 1)), rt.array(synth.uniform((W, W), 2))
+    wc = rt.empty((W, W))
+    ops = {K: (rt.array(synth.uniform((M, K), 5)), rt.array(synth.uniform((K, N), 6)))
+           for K in KSWEEP_KS}
+    C = rt.empty((M, N))
+    time_launches(rt, lambda i: rt.gemm(wa, wb, wc, W, W, W), 1, warmup)
+    res = {}
+    e0, e1 = rt.event(), rt.event()
+    for tag in KSWEEP_TILES:
+        for K, (A, B) in ops.items():
+            rt.gemm(wa, wb, wc, W, W, W)
+            rt.record(e0)
+            for _ in range(steps):
+                rt.gemm_tile(tag, A, B, C, M, N, K)
+            rt.record(e1)
+            res[f"{tag}:K={K}"] = round(rt.elapsed_ms(e0, e1) / steps * 1e3, 2)
+    # A minimal launch for comparison: a 64-float fill.
+    f = rt.empty((64,))
+    rt.gemm(wa, wb, wc, W, W, W)
+    for _ in range(steps):
+        rt.fill(f, 1.0)
+    rt.sync()
+    f.recycle()
+    rt.event_destroy(e0)
+    rt.event_destroy(e1)
+    for d in [wa, wb, wc, C] + [x for ab in ops.values() for x in ab]:
+        d.recycle()
+    return res
 
 
 def cpu_baseline(M, N, K):
@@ -583,9 +628,9 @@ def main() -> int:
     ap.add_argument("--extended", action="store_true")
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--profile", default=None,
-                    help="run only one workload (gemm4096, gemm8192x1024, gemms, copy, transpose, "
-                         "rows, rows65536, c4, c5) for rocprofv3, or vendor (torch.mm on the same "
-                         "GEMM shapes, in a process without this build's runtime)")
+                    help="run only one workload (gemm4096, gemm8192x1024, gemms, ksweep, copy, "
+                         "transpose, rows, rows65536, c4, c5) for rocprofv3, or vendor (torch.mm "
+                         "on the same GEMM shapes, in a process without this build's runtime)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))

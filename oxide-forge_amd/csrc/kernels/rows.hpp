@@ -34,6 +34,7 @@ struct RowArgs {
     int rows, cols;
     float eps;
     float scale;         // softmax backward: dx *= scale (1 = reference kernel)
+    int nt_stores;       // 1: non-temporal stores at any size (set by the host)
 };
 
 enum RowOp {
@@ -176,7 +177,7 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
     // Prefetch the next row when a wave walks several rows (the partial
     // kernels, whose grid is capped at one workgroup per CU).  Wider
     // workgroups would not leave the registers for it.
-    const bool nt = (long long)a.rows * cols >= STREAM_NT_MIN;
+    const bool nt = a.nt_stores || (long long)a.rows * cols >= STREAM_NT_MIN;
     const int stride = gridDim.x * WAVES;
     int row = blockIdx.x * WAVES + wave;
     float4 nv[PREFETCH ? VPT : 1], ng[(PREFETCH && BWD) ? VPT : 1];
