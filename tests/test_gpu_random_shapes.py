@@ -203,3 +203,55 @@ def test_transformer_random_configs(rt, seed):
                     assert rel(g, rg[k]) <= 1e-4, k
                 assert np.array_equal(T.param(k), p[k] - lr * g), f"SGD update of {k}"
         T.close()
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_mlp_random_configs(rt, seed):
+    """Random MLPs (mlp.rs:14-269): 1-5 layers of random widths, each
+    activation, biases or none, with or without a residual range
+    [start, end) (the input of layer start added to the output of layer
+    end - 1, so the two widths match); inference output, and for the
+    training executor the input gradient and the SGD identity of every
+    weight and bias, against the f64 oracle."""
+    from oracle import executors as ex
+    from oxforge import net
+
+    def rel(a, b):
+        b = np.asarray(b, np.float64)
+        return float(np.max(np.abs(np.asarray(a, np.float64) - b)) /
+                     max(np.max(np.abs(b)), 1e-30))
+
+    rng = np.random.default_rng(4000 + seed)
+    for case in range(6):
+        L = int(rng.integers(1, 6))
+        dims = [int(rng.integers(1, 200)) for _ in range(L + 1)]
+        res = None
+        if L >= 1 and rng.random() < 0.5:
+            start = int(rng.integers(0, L))
+            end = int(rng.integers(start + 1, L + 1))
+            dims[end] = dims[start]
+            res = (start, end)
+        rows = int(rng.integers(1, 300))
+        ps = int(rng.integers(0, 1 << 20))
+        layers = [(synth.xavier(dims[i], dims[i + 1], ps + i),
+                   synth.normal((dims[i + 1],), ps + 50 + i, 0.0, 0.1) if rng.random() < 0.7 else None,
+                   int(rng.integers(0, 4))) for i in range(L)]
+        training = bool(rng.random() < 0.5)
+        say(f"seed {seed} case {case}: dims={dims} res={res} rows={rows} training={training} "
+            f"acts={[a for _, _, a in layers]}")
+        X = synth.normal((rows, dims[0]), ps + 99)
+        m = net.Mlp(rt, layers, res, training=training)
+        Y = m.forward(rt.array(X)).numpy()
+        ref, ins, pres = ex.mlp_forward(layers, X, res)
+        assert rel(Y, ref) <= 1e-4, "forward"
+        if training:
+            dY = synth.normal((rows, dims[-1]), ps + 98)
+            lr = np.float32(1e-2)
+            dX = m.backward(rt.array(dY), float(lr)).numpy()
+            rdX, dWs, dbs = ex.mlp_backward(layers, ins, pres, dY, res)
+            assert rel(dX, rdX) <= 1e-4, "dX"
+            for i, (W, b, _) in enumerate(layers):
+                assert rel(m.param(i, 0), W - lr * dWs[i]) <= 1e-4, f"W{i}"
+                if b is not None:
+                    assert rel(m.param(i, 1), b - lr * dbs[i]) <= 1e-4, f"b{i}"
+        m.close()
