@@ -82,7 +82,9 @@ __device__ __forceinline__ float4 load_stream(const float* p) {
 // non-temporally: they do not fit the 256 MiB MALL beside their inputs, and
 // write-allocating them there costs bandwidth (6.59 against 5.80 TB/s for an
 // in-place float4 scale of 256 MiB on MI355X).  Smaller ones keep cached
-// stores (at 16 MiB non-temporal ones are 4% slower).
+// stores (at 16 MiB non-temporal ones are 4% slower for that scale), except
+// where a kernel measured faster without (the GEMM epilogue, the softmax and
+// RMSNorm forward).
 constexpr long long STREAM_NT_MIN = 16ll << 20;
 
 __device__ __forceinline__ void store_f4(float* p, float4 v, bool nt) {

@@ -174,10 +174,12 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
         }
     }
 
+    // Non-temporal stores from STREAM_NT_MIN on, or at any size when the
+    // host asks (RowArgs::nt_stores: the softmax and RMSNorm forward).
+    const bool nt = a.nt_stores || (long long)a.rows * cols >= STREAM_NT_MIN;
     // Prefetch the next row when a wave walks several rows (the partial
     // kernels, whose grid is capped at one workgroup per CU).  Wider
     // workgroups would not leave the registers for it.
-    const bool nt = a.nt_stores || (long long)a.rows * cols >= STREAM_NT_MIN;
     const int stride = gridDim.x * WAVES;
     int row = blockIdx.x * WAVES + wave;
     float4 nv[PREFETCH ? VPT : 1], ng[(PREFETCH && BWD) ? VPT : 1];
