@@ -120,7 +120,12 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
     // column partials, 32 more registers would spill)
     constexpr bool PRELOAD = USES_GAMMA && VPT <= 8 && !(PARTIALS && VPT >= 8);
     float4 gm[PRELOAD ? VPT : 1], bt[(PRELOAD && USES_BETA) ? VPT : 1];
-    if constexpr (PRELOAD) {
+    // RMSNorm forward issues gamma's loads after the first row's (waits are
+    // in issue order, and the row's reduction needs only the row): at
+    // [4096,1024] 7.17 -> 6.81 us.  LayerNorm forward, which also loads
+    // beta, measured slower that way (7.78 -> 8.01 us) and loads first.
+    constexpr bool LATE_PRELOAD = PRELOAD && OP == ROW_RMS_NORM;
+    auto preload = [&]() {
 #pragma unroll
         for (int i = 0; i < VPT; i++) {
             const int c = (i * 64 + lane) * 4;
@@ -131,7 +136,9 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                 bt[i] = (a.beta && in) ? *reinterpret_cast<const float4*>(a.beta + c)
                                        : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-    }
+    };
+    if constexpr (PRELOAD && !LATE_PRELOAD) preload();
+    bool first = true;
     // gamma / beta of float4 column group i (preloaded, or read per use).
     // Read per use, a group past cols reads the row's first group instead,
     // so the load stays in bounds wherever a caller evaluates it.
@@ -200,6 +207,10 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
             if (row + stride < a.rows) row_load<OP, VPT, BWD>(a, row + stride, lane, nv, ng);
         } else {
             row_load<OP, VPT, BWD>(a, row, lane, v, g);
+            if constexpr (LATE_PRELOAD) {
+                if (first) preload();
+                first = false;
+            }
             row_mask<OP, VPT, BWD>(ok, v, g);
         }
 
