@@ -52,8 +52,9 @@ def time_launches(rt, fn, steps: int, warmup: int, stream=None) -> float:
 
     Warmup runs at least `warmup` launches and at least SPIN_UP_S seconds of
     the same work: the MI355X raises its clocks over the first tens of
-    milliseconds of sustained load (a GEMM dispatch drops from 1.31 ms to
-    1.03 ms over its first ~25 launches), and the timed steps should see
+    milliseconds of sustained load (a 4096^3 GEMM dispatch drops from about
+    1.1-1.2 ms to 0.95 ms over its first ~20 launches, and to 0.90 ms in the
+    steady state), and the timed steps should see
     the steady state."""
     t0 = time.perf_counter()
     i = 0
