@@ -14,7 +14,13 @@
 //     waves per SIMD where a CU holds a single workgroup.
 //   - One MFMA sums four k values, lane group kq = lane / 16 supplying one.
 //     Inside a 16-wide k chunk, sub-step s (0..3) gives lane group kq the
-//     value k = 4 kq + s.  A lane's operands for a whole chunk are therefore
+//     value k = 4 kq + s.  (Built with -DFORGE_GEMM_MF=32, wave sub-tiles of
+//     32 or more rows and columns use 32 x 32 blocks and
+//     v_mfma_f32_32x32x2_f32 instead: two lane groups, 8-wide chunks,
+//     k = 4 kh + s, the same slabs and reads otherwise.  It gives the same
+//     results to within rounding and ran slower on the 2048-row products and
+//     in the transformer layers, so the default build keeps 16 x 16.)
+//     A lane's operands for a whole chunk are therefore
 //     one 128-bit LDS read per block for an operand that is k-contiguous in
 //     LDS (A, or B^T), and one 128-bit read per sub-step for an operand that
 //     is m/n-contiguous (B, or A^T).  For the latter the four floats of a
@@ -50,13 +56,13 @@ struct XVec {
 // Row (or column) of MFMA index i of block b in a wave sub-tile starting at
 // base: k-contiguous operands keep blocks contiguous, m/n-contiguous ones
 // interleave them W at a time.
-template <bool KC, int F>
+template <bool KC, int F, int MF = 16>
 __device__ __forceinline__ int x_index(int base, int b, int i) {
     if constexpr (KC) {
-        return base + 16 * b + i;
+        return base + MF * b + i;
     } else {
         constexpr int W = XVec<F>::W;
-        return base + 16 * W * (b / W) + W * i + (b % W);
+        return base + MF * W * (b / W) + W * i + (b % W);
     }
 }
 
@@ -138,25 +144,27 @@ struct XDma {
 // frag[b * 4 + s] is block b's value at sub-step s.  The lane's offset (in
 // floats, from the start of the LDS array) is precomputed per stage and
 // chunk, so each read is one base register plus an immediate.
-template <bool KC, int ROWS, int BK, int F>
+template <bool KC, int ROWS, int BK, int F, int MF = 16>
 struct XFrag {
-    static constexpr int CH = BK / 16;
+    static constexpr int KCH = 4 * (64 / MF);  // k values per chunk
+    static constexpr int CH = BK / KCH;
     int off[2][CH];
 
     // stage0: LDS offset of this operand in stage 0; stride: between stages;
-    // base: the wave's first row (k-contiguous, a multiple of 16) or column.
-    __device__ __forceinline__ void init(int stage0, int stride, int base, int l16, int kq) {
+    // base: the wave's first row (k-contiguous, a multiple of 16) or column;
+    // lr, kg: the lane's row in an MFMA block and its k group.
+    __device__ __forceinline__ void init(int stage0, int stride, int base, int lr, int kg) {
 #pragma unroll
         for (int st = 0; st < 2; st++)
 #pragma unroll
             for (int c = 0; c < CH; c++) {
                 if constexpr (KC) {
-                    // Rows base + 16 b + l16 all have the swizzle of row l16.
-                    off[st][c] = stage0 + st * stride + (base + l16) * BK +
-                                 4 * ((c * 4 + kq) ^ x_swz<BK / 4, true>(l16));
+                    // Rows base + MF b + lr all have the swizzle of row lr.
+                    off[st][c] = stage0 + st * stride + (base + lr) * BK +
+                                 4 * ((c * (KCH / 4) + kg) ^ x_swz<BK / 4, true>(lr));
                 } else {
-                    off[st][c] = stage0 + st * stride + (c * 16 + 4 * kq) * ROWS + base +
-                                 XVec<F>::W * l16;
+                    off[st][c] = stage0 + st * stride + (c * KCH + 4 * kg) * ROWS + base +
+                                 XVec<F>::W * lr;
                 }
             }
     }
@@ -167,7 +175,7 @@ struct XFrag {
         if constexpr (KC) {
 #pragma unroll
             for (int b = 0; b < F; b++) {
-                const f4 v = *reinterpret_cast<const f4*>(s + 16 * b * BK);
+                const f4 v = *reinterpret_cast<const f4*>(s + MF * b * BK);
                 frag[b * 4 + 0] = v.x;
                 frag[b * 4 + 1] = v.y;
                 frag[b * 4 + 2] = v.z;
@@ -179,7 +187,7 @@ struct XFrag {
             for (int st = 0; st < 4; st++) {
 #pragma unroll
                 for (int g = 0; g < F / W; g++) {
-                    const float* q = s + st * ROWS + 16 * W * g;
+                    const float* q = s + st * ROWS + MF * W * g;
                     if constexpr (W == 4) {
                         const f4 v = *reinterpret_cast<const f4*>(q);
                         frag[(4 * g + 0) * 4 + st] = v.x;
@@ -362,13 +370,24 @@ __device__ __forceinline__ void x_epi_store(const GemmArgs& p, const f4 (&z)[NB]
                                     reinterpret_cast<f4*>(p.C + idx[u]));
 }
 
+#ifndef FORGE_GEMM_MF
+#define FORGE_GEMM_MF 16
+#endif
+
 template <int BM, int BN, int BK, bool TA, bool TB, bool EPI, int WM = 2, int WN = 2>
 __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     constexpr int NW = WM * WN;  // waves: WM x WN sub-tiles of TM x TN
     constexpr int TM = BM / WM, TN = BN / WN;
-    constexpr int FM = TM / 16, FN = TN / 16;
-    constexpr int CH = BK / 16;
-    static_assert(TM % 16 == 0 && TN % 16 == 0 && BK % 16 == 0, "tile shape");
+    // MFMA block: 16 x 16 (v_mfma_f32_16x16x4_f32, four k per instruction,
+    // four lane groups) or 32 x 32 (v_mfma_f32_32x32x2_f32, two k, two
+    // lane groups).
+    constexpr int MF = (FORGE_GEMM_MF == 32 && TM % 32 == 0 && TN % 32 == 0) ? 32 : 16;
+    constexpr int FM = TM / MF, FN = TN / MF;
+    constexpr int KCH = 4 * (64 / MF);  // k values per chunk (four sub-steps)
+    constexpr int CH = BK / KCH;
+    constexpr int NACC = MF * MF / 64;  // accumulators per lane per block
+    typedef float vacc __attribute__((ext_vector_type(NACC)));
+    static_assert(TM % MF == 0 && TN % MF == 0 && BK % KCH == 0, "tile shape");
     constexpr bool A_KC = !TA, B_KC = TB;
 
     constexpr int A_ROWS = TA ? BK : BM, A_COLS = TA ? BM : BK;
@@ -396,7 +415,7 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // scalar
     const int wm = wave / WN, wn = wave % WN;
-    const int l16 = lane & 15, kq = lane >> 4;
+    const int lr = lane & (MF - 1), kg = lane >> (MF == 16 ? 4 : 5);
     float* const smem = smem_all;
 
     const int KT = p.K / BK;
@@ -405,11 +424,11 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     const float* a_base = TA ? p.A + m0 : p.A + (long long)m0 * p.lda;
     const float* b_base = TB ? p.B + (long long)n0 * p.ldb : p.B + n0;
 
-    v4f acc[FM][FN];
+    vacc acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int j = 0; j < FN; j++) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < FN; j++) acc[i][j] = (vacc)(0.0f);
 
     // Fragment origins inside a slab: the wave's first row (KC) or column
     // offset (MC) of its sub-tile.
@@ -420,10 +439,10 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     XDma<B_ROWS, B_COLS, B_KC, NW> dma_b;
     dma_a.init(p.lda, wave, lane);
     dma_b.init(p.ldb, wave, lane);
-    XFrag<A_KC, A_KC ? BK : BM, BK, FM> rd_a;
-    XFrag<B_KC, B_KC ? BK : BN, BK, FN> rd_b;
-    rd_a.init(0, STAGE, a_off, l16, kq);
-    rd_b.init(A_ELEMS, STAGE, b_off, l16, kq);
+    XFrag<A_KC, A_KC ? BK : BM, BK, FM, MF> rd_a;
+    XFrag<B_KC, B_KC ? BK : BN, BK, FN, MF> rd_b;
+    rd_a.init(0, STAGE, a_off, lr, kg);
+    rd_b.init(A_ELEMS, STAGE, b_off, lr, kg);
 
     auto issue = [&](int k_slab, int stage) {
         float* d = smem + stage * STAGE;
@@ -440,9 +459,14 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
-                for (int j = 0; j < FN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-                        fa[slot][i * 4 + st], fb[slot][j * 4 + st], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < FN; j++) {
+                    if constexpr (MF == 32)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                            fa[slot][i * 4 + st], fb[slot][j * 4 + st], acc[i][j], 0, 0, 0);
+                    else
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                            fa[slot][i * 4 + st], fb[slot][j * 4 + st], acc[i][j], 0, 0, 0);
+                }
     };
     // Instruction counts that the schedule below interleaves.
     constexpr int NMFMA = 4 * FM * FN;  // per chunk
@@ -546,36 +570,39 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     }
 
     // Epilogue through LDS.  Each wave writes its accumulators as a plain
-    // TM x TN sub-tile into its own LDS region (accumulator r of a 16x16
-    // block is MFMA row 4 kq + r, column l16), then streams the sub-tile
+    // TM x TN sub-tile into its own LDS region (accumulator r at MFMA row
+    // acc_row(r), column lane % MF), then streams the sub-tile
     // back row by row: four consecutive columns per lane, so operands and
     // results move as 128-bit accesses and the fused steps are one compact
     // loop instead of code unrolled over every accumulator.  A wave reads
     // only what it wrote, and LDS executes one wave's accesses in order.
     __syncthreads();  // every wave is done with the slab stages
     float* const cw = smem_all + wave * (TM * CP);
+    // MFMA row of accumulator r: 4 kg + r in a 16 x 16 block; in a 32 x 32
+    // block, 8 (r / 4) + 4 kg + r % 4.
+    auto acc_row = [&](int r) { return MF == 16 ? 4 * kg + r : 8 * (r >> 2) + 4 * kg + (r & 3); };
     if constexpr (!B_KC && XVec<FN>::W == 4) {
 #pragma unroll
         for (int i = 0; i < FM; i++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int rr = x_index<A_KC, FM>(0, i, 4 * kq + r);
+            for (int r = 0; r < NACC; r++) {
+                const int rr = x_index<A_KC, FM, MF>(0, i, acc_row(r));
 #pragma unroll
                 for (int g = 0; g < FN / 4; g++) {
                     const f4 v = {acc[i][4 * g + 0][r], acc[i][4 * g + 1][r],
                                   acc[i][4 * g + 2][r], acc[i][4 * g + 3][r]};
-                    *reinterpret_cast<f4*>(cw + rr * CP + 64 * g + 4 * l16) = v;
+                    *reinterpret_cast<f4*>(cw + rr * CP + 4 * MF * g + 4 * lr) = v;
                 }
             }
     } else {
 #pragma unroll
         for (int i = 0; i < FM; i++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int rr = x_index<A_KC, FM>(0, i, 4 * kq + r);
+            for (int r = 0; r < NACC; r++) {
+                const int rr = x_index<A_KC, FM, MF>(0, i, acc_row(r));
 #pragma unroll
                 for (int j = 0; j < FN; j++)
-                    cw[rr * CP + x_index<B_KC, FN>(0, j, l16)] = acc[i][j][r];
+                    cw[rr * CP + x_index<B_KC, FN, MF>(0, j, lr)] = acc[i][j][r];
             }
     }
     asm volatile("" ::: "memory");
