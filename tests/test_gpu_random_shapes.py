@@ -4,11 +4,17 @@ register or looping row path, masked lanes, unaligned views, partial-sum
 grids) meet the same bars on shapes no list names.  Bars as in
 test_gpu_kernels.py: GEMM max|C - C64| / max|C64| <= 1e-4 and componentwise
 |C - C64| / (|A| |B|) <= 1e-4; row kernels 1e-5 absolute, column sums
-1e-5 sqrt(rows)."""
+1e-5 sqrt(rows).  The LayerNorm forward and the LayerNorm / RMSNorm
+backward dx are held to the larger of 1e-5 and twice the rounding bound of
+their f32 formula (rowbounds.py): on rows whose values nearly coincide, r =
+1/sqrt(var + eps) amplifies the f32 rounding of the mean past 1e-5 in any
+f32 evaluation, the reference's included; at north_star's distribution the
+bound is below 1e-5 and the bar is unchanged."""
 import numpy as np
 import pytest
 
 import oxforge
+import rowbounds as rb
 from oxforge import synth
 from oracle import oracle as orc
 
@@ -30,6 +36,18 @@ def _dim(rng, hi):
     elif r < 0.5:
         d = max(32, d // 32 * 32)
     return d
+
+
+def within(got, ref, bound):
+    """|got - ref| <= max(1e-5, 2 * bound) everywhere; prints the worst
+    element when it is not."""
+    err = np.abs(np.asarray(got, np.float64) - ref)
+    tol = rb.tolerance(bound, TOL_ROW)
+    if np.all(err <= tol):
+        return True
+    i = np.unravel_index(np.argmax(err / tol), err.shape)
+    print(f"  worst element {i}: error {err[i]:.3g}, tolerance {tol[i]:.3g}", flush=True)
+    return False
 
 
 def _view(rt, host, off):
@@ -113,7 +131,8 @@ def test_row_kernels_random_shapes(rt, seed):
 
         v = view(x)
         rt.layer_norm(v, rows, cols, dgam, dbet)
-        assert np.max(np.abs(v.numpy() - orc.layer_norm(x, gam, bet))) <= TOL_ROW
+        assert within(v.numpy(), orc.layer_norm(x, gam, bet),
+                      rb.layer_norm_forward_bound(x, gam, bet))
         v = view(x)
         rt.rms_norm(v, rows, cols, dgam)
         assert np.max(np.abs(v.numpy() - orc.rms_norm(x, gam))) <= TOL_ROW
@@ -123,15 +142,61 @@ def test_row_kernels_random_shapes(rt, seed):
         pg, pb = rt.empty((cols,)), rt.empty((cols,))
         rt.layer_norm_bwd(view(x), view(dy), dx, rows, cols, gamma=dgam, dgamma=pg, dbeta=pb)
         rdx, rdg, rdb = orc.layer_norm_backward(x, dy, gam, want_params=True)
-        assert np.max(np.abs(dx.numpy() - rdx)) <= TOL_ROW
+        assert within(dx.numpy(), rdx, rb.layer_norm_backward_bound(x, dy, gam))
         assert np.max(np.abs(pg.numpy() - rdg)) <= col_tol
         assert np.max(np.abs(pb.numpy() - rdb)) <= col_tol
         rt.rms_norm_bwd(view(x), view(dy), dx, rows, cols, gamma=dgam, dgamma=pg)
         rdx, rdg = orc.rms_norm_backward(x, dy, gam, want_params=True)
-        assert np.max(np.abs(dx.numpy() - rdx)) <= TOL_ROW
+        assert within(dx.numpy(), rdx, rb.rms_norm_backward_bound(x, dy, gam))
         assert np.max(np.abs(pg.numpy() - rdg)) <= col_tol
         for d in bufs + [pg, pb] + [d for d in (dgam, dbet) if d is not None]:
             d.recycle()
+
+
+@pytest.mark.parametrize("cols", [1, 2, 3, 5, 8, 33, 64, 256, 1024, 3000])
+def test_row_norms_ill_conditioned(rt, cols):
+    """Rows whose values nearly or exactly coincide, with means up to 30
+    (r up to 1/sqrt(eps)), on the register path (aligned, cols % 4 == 0) and
+    the looping path (a view one float off): the norms against the oracle
+    within the rounding bounds of their f32 formulas (the column sums are
+    left to the other tests: on such rows they inherit the same
+    amplification)."""
+    rng = np.random.default_rng(500 + cols)
+    rows = 64
+    for spread in (1e-2, 1e-4, 0.0):
+        for off in (0, 1):
+            affine = off == 0
+            say(f"ill-conditioned {rows}x{cols} spread={spread} off={off} affine={affine}")
+            m = rng.normal(0, 1, (rows, 1)) * rng.choice([1, 3, 10, 30], (rows, 1))
+            x = (m + spread * rng.normal(0, 1, (rows, cols))).astype(np.float32)
+            dy = rng.normal(0, 1, (rows, cols)).astype(np.float32)
+            gam = (1 + 0.1 * rng.normal(0, 1, cols)).astype(np.float32) if affine else None
+            bet = (0.1 * rng.normal(0, 1, cols)).astype(np.float32) if affine else None
+            dgam = rt.array(gam) if affine else None
+            dbet = rt.array(bet) if affine else None
+            bufs = []
+
+            def view(h):
+                b, v = _view(rt, h, off)
+                bufs.append(b)
+                return v
+
+            v = view(x)
+            rt.layer_norm(v, rows, cols, dgam, dbet)
+            assert within(v.numpy(), orc.layer_norm(x, gam, bet),
+                          rb.layer_norm_forward_bound(x, gam, bet))
+            v = view(x)
+            rt.rms_norm(v, rows, cols, dgam)
+            assert np.max(np.abs(v.numpy() - orc.rms_norm(x, gam))) <= TOL_ROW
+            dx = view(np.zeros_like(x))
+            rt.layer_norm_bwd(view(x), view(dy), dx, rows, cols, gamma=dgam)
+            assert within(dx.numpy(), orc.layer_norm_backward(x, dy, gam),
+                          rb.layer_norm_backward_bound(x, dy, gam))
+            rt.rms_norm_bwd(view(x), view(dy), dx, rows, cols, gamma=dgam)
+            assert within(dx.numpy(), orc.rms_norm_backward(x, dy, gam),
+                          rb.rms_norm_backward_bound(x, dy, gam))
+            for d in bufs + [d for d in (dgam, dbet) if d is not None]:
+                d.recycle()
 
 
 @pytest.mark.parametrize("seed", range(4))
