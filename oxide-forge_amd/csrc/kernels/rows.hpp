@@ -35,6 +35,7 @@ struct RowArgs {
     float eps;
     float scale;         // softmax backward: dx *= scale (1 = reference kernel)
     int nt_stores;       // 1: non-temporal stores at any size (set by the host)
+    int lds_params;      // 1: LayerNorm forward stages gamma/beta in LDS (set by the host)
 };
 
 enum RowOp {
@@ -123,7 +124,8 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
     // RMSNorm forward issues gamma's loads after the first row's (waits are
     // in issue order, and the row's reduction needs only the row): at
     // [4096,1024] 7.17 -> 6.81 us.  LayerNorm forward, which also loads
-    // beta, measured slower that way (7.78 -> 8.01 us) and loads first.
+    // beta, measured slower that way (7.78 -> 8.01 us); it stages both
+    // through LDS (below).
     constexpr bool LATE_PRELOAD = PRELOAD && OP == ROW_RMS_NORM;
     auto preload = [&]() {
 #pragma unroll
@@ -137,7 +139,39 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                                        : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     };
-    if constexpr (PRELOAD && !LATE_PRELOAD) preload();
+    // LayerNorm forward below 64 MiB (the host sets lds_params) stages
+    // gamma/beta in LDS once per workgroup instead of loading them per wave
+    // (a quarter of the loads): [4096,1024] 8.16 -> 7.88 us, faster in each
+    // of twelve paired runs; issuing the first row's loads before the
+    // staging was slower (8.52).  At [65536,1024] the staging cost 1.3%
+    // (84.5 -> 85.6 us, five paired runs), so larger launches load per wave.
+    // The barrier is outside the row loop and lds_params is uniform, so
+    // every wave reaches it.
+    constexpr bool LDS_PARAMS = PRELOAD && OP == ROW_LAYER_NORM && !PARTIALS;
+    if constexpr (LDS_PARAMS) {
+        if (a.lds_params) {
+            __shared__ float4 sgb[2 * VPT * 64];
+            for (int t = threadIdx.x; t < VPT * 64; t += WAVES * 64) {
+                const int c = t * 4;
+                const bool in = c < cols;
+                sgb[t] = (a.gamma && in) ? *reinterpret_cast<const float4*>(a.gamma + c)
+                                         : make_float4(1.f, 1.f, 1.f, 1.f);
+                sgb[VPT * 64 + t] = (a.beta && in)
+                                        ? *reinterpret_cast<const float4*>(a.beta + c)
+                                        : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < VPT; i++) {
+                gm[i] = sgb[i * 64 + lane];
+                bt[i] = sgb[VPT * 64 + i * 64 + lane];
+            }
+        } else {
+            preload();
+        }
+    } else if constexpr (PRELOAD && !LATE_PRELOAD) {
+        preload();
+    }
     bool first = true;
     // gamma / beta of float4 column group i (preloaded, or read per use).
     // Read per use, a group past cols reads the row's first group instead,

@@ -86,8 +86,13 @@ struct RowArgs {
     int rows, cols;
     float eps;
     float scale;
-    int nt_stores = 0;  // set by row_launch
+    int nt_stores = 0;   // set by row_launch
+    int lds_params = 0;  // set by row_launch
 };
+
+// LayerNorm forward stages gamma/beta in LDS below this many elements
+// (rows.hpp; the same 64 MiB as STREAM_NT_MIN in common.hpp).
+constexpr long long kRowLdsParamsMax = 16ll << 20;
 
 // Must match forge::ColSumOut in csrc/kernels/elementwise.hpp: where a final
 // column-sum pass writes (out, when not null) and the parameter vector whose
@@ -983,6 +988,8 @@ forge_status row_launch(forge_runtime* rt, forge_stream* s, const char* op, RowA
     // 1-2% slower with it, so they, like everything else, store
     // non-temporally from 64 MiB on.
     a.nt_stores = (strcmp(op, "softmax") == 0 || strcmp(op, "rms_norm") == 0) ? 1 : 0;
+    a.lds_params =
+        (strcmp(op, "layer_norm") == 0 && (long long)a.rows * a.cols < kRowLdsParamsMax) ? 1 : 0;
     const ColSumOut og{dgamma, sgd.gamma, sgd.lr}, ob{dbeta, sgd.beta, sgd.lr};
     const bool want_g = dgamma || sgd.gamma, want_b = dbeta || sgd.beta;
     bool aligned = aligned16(a.x) && aligned16(a.y) && (!a.dy || aligned16(a.dy)) &&
