@@ -453,6 +453,26 @@ def test_row_kernels_at_nontemporal_size(rt, affine):
     assert np.max(np.abs(pg.numpy() - rdg)) <= col_tol
 
 
+def test_layer_norm_forward_both_parameter_paths(rt):
+    """LayerNorm forward below 2^24 elements stages gamma/beta in LDS once per
+    workgroup, from 2^24 on each wave loads them: [16383, 1024] and
+    [16384, 1024] take one path each.  Both against the oracle, and the rows
+    they share bit for bit (only where gamma/beta are read from differs)."""
+    cols = 1024
+    x = synth.normal((16384, cols), 71)
+    gam, bet = synth.normal((cols,), 72, 1.0, 0.1), synth.normal((cols,), 73, 0.0, 0.1)
+    dgam, dbet = rt.array(gam), rt.array(bet)
+    out = {}
+    for rows in (16383, 16384):
+        say(f"layer norm forward {rows}x{cols}")
+        d = rt.array(x[:rows])
+        rt.layer_norm(d, rows, cols, gamma=dgam, beta=dbet)
+        out[rows] = d.numpy()
+        assert np.max(np.abs(out[rows] - orc.layer_norm(x[:rows], gam, bet))) <= TOL_ROW
+        d.recycle()
+    assert np.array_equal(out[16383], out[16384][:16383])
+
+
 @pytest.mark.parametrize("rows,cols", [(65536, 1024), (65537, 1000)])
 def test_norm_bwd_partials_at_scale_four_wave_instance(rt, rows, cols):
     """[65536, 1024] takes the four-wave partial instance (_p4: 256 rows per
