@@ -8,8 +8,8 @@ row's mean is then amplified by r (forward) or r^2 (backward): the
 LayerNorm backward of the two-column row [-0.2205, -0.2578] has r = 53,
 and an f32 evaluation of the reference's formula lands 4.7e-5 from the f64
 value.  No f32 implementation meets a fixed 1e-5 absolute bar on such rows;
-north_star's bar is stated for X ~ N(0,1) at 1024 columns, where these
-bounds stay below it (test_rowbounds.py), so the bar is unchanged there.
+the bar is meant for X ~ N(0,1) at 1024 columns, where these bounds stay
+below it (test_rowbounds.py), so it is unchanged there.
 
 The bounds propagate one rounding (unit roundoff u = 2^-24) per f32
 operation of the kernels' evaluation order.  A row sum passes a term through

@@ -1,8 +1,8 @@
 """CPU checks of the row-norm tolerances (rowbounds.py) that the random-shape
 GPU tests apply where a fixed 1e-5 bar is below what f32 arithmetic can
 reach:
-- at north_star's distribution (X ~ N(0,1), 1024 columns) the tolerance is
-  the fixed bar itself;
+- at the distribution the fixed bar is set for (X ~ N(0,1), 1024 columns)
+  the tolerance is the fixed bar itself;
 - the kernels' f32 evaluation (f32rows.py, their order of operations) stays
   inside it on ill-conditioned rows: near-constant and constant rows with
   means up to 30, on the looping and the register path;
@@ -28,7 +28,7 @@ def c2_like(rows=256, cols=1024):
     return x, dy, gam, bet
 
 
-def test_fixed_bar_unchanged_at_north_star_distribution():
+def test_fixed_bar_unchanged_at_standard_normal_rows():
     x, dy, gam, bet = c2_like()
     for b in (rb.layer_norm_forward_bound(x, gam, bet), rb.layer_norm_backward_bound(x, dy, gam),
               rb.rms_norm_backward_bound(x, dy, gam)):
