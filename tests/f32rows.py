@@ -27,8 +27,9 @@ def wave_sum(v):
 
 
 def _fma(a, b, c):
-    # f32 * f32 is exact in f64; the f64 sum rounds once more only when its
-    # exponents differ widely, which the checks here do not reach
+    # f32 * f32 is exact in f64; the f64 sum can round before the rounding to
+    # f32 when the exponents differ by more than about 29 bits, where this
+    # may differ from a fused multiply-add by one unit in the last place
     return (np.asarray(a, np.float64) * b + c).astype(f)
 
 
