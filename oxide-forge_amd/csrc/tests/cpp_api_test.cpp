@@ -457,6 +457,104 @@ int main(int argc, char** argv) {
         group("executors", f);
     }
 
+    // ----------------------------------------------------- cross attention
+    // Attention::forward / forward_mask with query and key/value inputs of
+    // different row counts (attention.rs:221-241): norm(Xq + softmax(Q K^T /
+    // sqrt(d)) V), Q from Xq, K and V from Xkv, against a double-precision
+    // host evaluation; with the Q/K/V projections batched and on three
+    // forked streams (bit-identical to each other).
+    {
+        int f = g_failures;
+        const size_t Sq = 40, Sk = 72, H = 32, D = 16;
+        auto host_lin = [&](size_t in, size_t out, uint64_t seed, std::vector<float>& w,
+                            std::vector<float>& b) {
+            w = uniform(in * out, seed);
+            for (auto& v : w) v *= 0.3f;
+            b = uniform(out, seed + 100);
+        };
+        std::vector<float> wq, bq, wk, bk, wv, bv;
+        host_lin(H, D, 71, wq, bq);
+        host_lin(H, D, 72, wk, bk);
+        host_lin(H, H, 73, wv, bv);
+        const std::vector<float> xq = uniform(Sq * H, 74), xkv = uniform(Sk * H, 75);
+        auto make = [&](bool streams) {
+            auto lin = [&](const std::vector<float>& w, const std::vector<float>& b, size_t in,
+                           size_t out) {
+                return Linear(R.matrix_from_host(w, in, out), R.vector_from_host(b),
+                              Activation::Identity);
+            };
+            Normalization n;
+            n.kind = NormType::Layer;
+            std::optional<std::vector<CudaStream>> s;
+            if (streams) s = R.create_extra_streams(3);
+            return Attention(lin(wq, bq, H, D), lin(wk, bk, H, D), lin(wv, bv, H, H), std::move(s),
+                             std::move(n));
+        };
+        // host reference
+        auto proj = [](const std::vector<float>& x, size_t rows, size_t in,
+                       const std::vector<float>& w, const std::vector<float>& b, size_t out) {
+            std::vector<double> y(rows * out);
+            for (size_t r = 0; r < rows; r++)
+                for (size_t c = 0; c < out; c++) {
+                    double s = b[c];
+                    for (size_t k = 0; k < in; k++) s += (double)x[r * in + k] * w[k * out + c];
+                    y[r * out + c] = s;
+                }
+            return y;
+        };
+        const auto Q = proj(xq, Sq, H, wq, bq, D), K = proj(xkv, Sk, H, wk, bk, D),
+                   V = proj(xkv, Sk, H, wv, bv, H);
+        auto reference = [&](bool mask) {
+            std::vector<double> out(Sq * H);
+            const double scale = 1.0 / std::sqrt((double)D);
+            for (size_t r = 0; r < Sq; r++) {
+                std::vector<double> p(Sk);
+                double m = -1e300;
+                for (size_t c = 0; c < Sk; c++) {
+                    double s = 0.0;
+                    for (size_t k = 0; k < D; k++) s += Q[r * D + k] * K[c * D + k];
+                    p[c] = (mask && c > r) ? -1e300 : s * scale;
+                    m = std::max(m, p[c]);
+                }
+                double z = 0.0;
+                for (size_t c = 0; c < Sk; c++) z += (p[c] = (p[c] <= -1e299) ? 0.0 : std::exp(p[c] - m));
+                std::vector<double> a(H);
+                for (size_t h = 0; h < H; h++) {
+                    double s = 0.0;
+                    for (size_t c = 0; c < Sk; c++) s += p[c] / z * V[c * H + h];
+                    a[h] = xq[r * H + h] + s;
+                }
+                double mu = 0.0, var = 0.0;
+                for (double t : a) mu += t;
+                mu /= H;
+                for (double t : a) var += (t - mu) * (t - mu);
+                var /= H;
+                for (size_t h = 0; h < H; h++) out[r * H + h] = (a[h] - mu) / std::sqrt(var + 1e-5);
+            }
+            return out;
+        };
+        Matrix Xq = R.matrix_from_host(xq, Sq, H), Xkv = R.matrix_from_host(xkv, Sk, H);
+        for (bool mask : {false, true}) {
+            const auto want = reference(mask);
+            std::vector<float> got[2];
+            for (int streams = 0; streams < 2; streams++) {
+                Attention attn = make(streams == 1);
+                Matrix y = mask ? attn.forward_mask(Xq, Xkv, R) : attn.forward(Xq, Xkv, R);
+                CHECK(y.rows() == Sq && y.cols() == H, "cross attention shape");
+                got[streams] = y.to_host(R);
+            }
+            double err = 0.0, big = 0.0;
+            for (size_t i = 0; i < want.size(); i++) {
+                err = std::max(err, std::fabs(got[0][i] - want[i]));
+                big = std::max(big, std::fabs(want[i]));
+            }
+            CHECK(err / big <= 1e-4, mask ? "cross attention (masked) vs host" :
+                                            "cross attention vs host");
+            CHECK(got[0] == got[1], "cross attention: forked streams = batched");
+        }
+        group("cross attention", f);
+    }
+
     // ---------------------------------------------------------- checkpoint
     // Shapes only the C++ API can hold: a three-layer feed-forward network
     // with a residual, query/key narrower than the embedding.
