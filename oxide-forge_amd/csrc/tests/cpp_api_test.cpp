@@ -457,6 +457,89 @@ int main(int argc, char** argv) {
         group("executors", f);
     }
 
+    // ---------------------------------------------------- runtime wrappers
+    // The element-wise Matrix / Vector operations (matrix.rs:178-253,
+    // vector_runtime.rs:76-117), the device-slice constructors, and the *_on
+    // variants on a forked stream, against host f32 arithmetic (one rounding
+    // per element: bit for bit), exact integer sums and an f64 product.
+    {
+        int f = g_failures;
+        const size_t r = 7, c = 9, n = 5;
+        const std::vector<float> ha = uniform(r * c, 81);
+        std::vector<float> hb = uniform(r * c, 82);
+        for (auto& v : hb) v = v < 0.0f ? v - 0.5f : v + 0.5f;  // away from zero
+        auto host = [&](BinaryOp op) {
+            std::vector<float> o(r * c);
+            for (size_t i = 0; i < o.size(); i++) {
+                const float x = ha[i], y = hb[i];
+                o[i] = op == BinaryOp::Add ? x + y
+                       : op == BinaryOp::Sub ? x - y
+                       : op == BinaryOp::Mul ? x * y
+                                             : x / y;
+            }
+            return o;
+        };
+        Matrix A = R.matrix_from_host(ha, r, c), B = R.matrix_from_host(hb, r, c);
+        CHECK(R.matrix_add(A, B).to_host(R) == host(BinaryOp::Add), "matrix_add");
+        CHECK(R.matrix_sub(A, B).to_host(R) == host(BinaryOp::Sub), "matrix_sub");
+        CHECK(R.matrix_mul(A, B).to_host(R) == host(BinaryOp::Mul), "matrix_mul");
+        CHECK(R.matrix_div(A, B).to_host(R) == host(BinaryOp::Div), "matrix_div");
+        Vector va = R.vector_from_host(ha), vb = R.vector_from_host(hb);
+        CHECK(R.vector_add(va, vb).to_host(R) == host(BinaryOp::Add), "vector_add");
+        CHECK(R.vector_sub(va, vb).to_host(R) == host(BinaryOp::Sub), "vector_sub");
+        CHECK(R.vector_mul(va, vb).to_host(R) == host(BinaryOp::Mul), "vector_mul");
+        CHECK(R.vector_div(va, vb).to_host(R) == host(BinaryOp::Div), "vector_div");
+        CHECK(R.vector_binary(va, vb, BinaryOp::Div).to_host(R) == host(BinaryOp::Div),
+              "vector_binary");
+        CHECK(R.matrix_from_device(A.slice(), r, c).to_host(R) == ha, "matrix_from_device");
+        CHECK(R.vector_from_device(vb.slice()).to_host(R) == hb, "vector_from_device");
+
+        // *_on on a forked stream, joined before the results are read.
+        std::vector<float> hi(r * c), hw = uniform(c * n, 83), hrow = uniform(c, 84);
+        for (size_t i = 0; i < hi.size(); i++) hi[i] = (float)((int)(i * 7 % 23) - 11);
+        Matrix I = R.matrix_from_host(hi, r, c), W = R.matrix_from_host(hw, c, n);
+        Matrix out = R.new_uninit_matrix(r, n), M2 = R.clone_matrix(A), M3 = R.clone_matrix(A);
+        Vector row = R.vector_from_host(hrow), v2 = R.clone_vector(va);
+        auto st = R.create_extra_streams(1);
+        R.fork_streams(st);
+        const CudaStream* s = &st[0];
+        Matrix cm = R.clone_matrix_on(A, s);
+        Vector cv = R.clone_vector_on(vb, s);
+        Vector sums = R.matrix_sum_rows_on(I, s);
+        Matrix prod = R.matrix_binary_on(s, A, B, BinaryOp::Mul);
+        R.matrix_multiply_into_on(s, A, W, out);
+        v2.scale_on(2.0f, R, s);
+        M2.binary_assign_on(B, BinaryOp::Sub, R, s);
+        M3.binary_assign_by_rows_on(row, BinaryOp::Add, R, s);
+        R.join_streams(st);
+        R.sync();
+        CHECK(cm.to_host(R) == ha && cv.to_host(R) == hb, "clone_*_on");
+        std::vector<float> want_sums(r, 0.0f);
+        for (size_t i = 0; i < r; i++)
+            for (size_t j = 0; j < c; j++) want_sums[i] += hi[i * c + j];
+        CHECK(sums.to_host(R) == want_sums, "matrix_sum_rows_on (integers, exact)");
+        CHECK(prod.to_host(R) == host(BinaryOp::Mul), "matrix_binary_on");
+        CHECK(M2.to_host(R) == host(BinaryOp::Sub), "binary_assign_on");
+        std::vector<float> want_row(r * c), want_scale(r * c);
+        for (size_t i = 0; i < r * c; i++) {
+            want_row[i] = ha[i] + hrow[i % c];
+            want_scale[i] = ha[i] * 2.0f;
+        }
+        CHECK(M3.to_host(R) == want_row, "binary_assign_by_rows_on");
+        CHECK(v2.to_host(R) == want_scale, "scale_on");
+        const auto got = out.to_host(R);
+        double err = 0.0, big = 0.0;
+        for (size_t i = 0; i < r; i++)
+            for (size_t j = 0; j < n; j++) {
+                double s64 = 0.0;
+                for (size_t k = 0; k < c; k++) s64 += (double)ha[i * c + k] * hw[k * n + j];
+                err = std::max(err, std::fabs(got[i * n + j] - s64));
+                big = std::max(big, std::fabs(s64));
+            }
+        CHECK(err / big <= 1e-5, "matrix_multiply_into_on");
+        group("runtime wrappers", f);
+    }
+
     // ----------------------------------------------------- cross attention
     // Attention::forward / forward_mask with query and key/value inputs of
     // different row counts (attention.rs:221-241): norm(Xq + softmax(Q K^T /
