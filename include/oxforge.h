@@ -52,6 +52,13 @@ typedef struct forge_slice {
     size_t len;
 } forge_slice;
 
+/* The same descriptor over u32 elements (DeviceSliceMutDescriptor<u32>, the
+ * result buffer of compare_vectors, reduction.rs:132-136). */
+typedef struct forge_slice_u32 {
+    uint32_t *ptr;
+    size_t len;
+} forge_slice_u32;
+
 /* BinaryOp, #[repr(u8)] (cuda.rs:3-10). */
 typedef enum forge_binary_op {
     FORGE_ADD = 0,
@@ -157,6 +164,18 @@ forge_status forge_free(forge_runtime *rt, forge_slice buf);
 forge_status forge_reserve(forge_runtime *rt, size_t n, size_t count);
 /* Buffers currently held by the pool for size n (for tests). */
 forge_status forge_pool_count(forge_runtime *rt, size_t n, size_t *count);
+
+/* get_u32_uninit_buffer (runtime.rs:57-60): a new uninitialised buffer of n
+ * u32 values.  Not pooled (the reference allocates it on its stream and
+ * frees it on drop); n == 0 yields {NULL, 0}. */
+forge_status forge_alloc_u32(forge_runtime *rt, size_t n, forge_slice_u32 *out);
+/* Drop of a DeviceBuffer<u32>: waits for the primary stream, then releases
+ * the memory. */
+forge_status forge_free_u32(forge_runtime *rt, forge_slice_u32 buf);
+/* to_host_vec of a DeviceBuffer<u32> (vector.rs:134): device -> host;
+ * blocks until done. */
+forge_status forge_memcpy_d2h_u32(forge_runtime *rt, uint32_t *dst,
+                                  forge_slice_u32 src, size_t n);
 
 /* DeviceBuffer::from_host (matrix.rs:107): host -> device, ordered on the
  * primary stream; returns once the host buffer may be reused. */
@@ -463,6 +482,13 @@ forge_status forge_fill_random(forge_runtime *rt, forge_stream *stream,
 forge_status forge_compare(forge_runtime *rt, forge_stream *stream,
                            forge_slice l, forge_slice r, size_t n,
                            forge_slice out);
+/* forge_compare into the reference's u32 result buffer (vector.rs:121-135,
+ * compare_vectors writing DeviceSliceMutDescriptor<u32>): out[0] = the
+ * number of positions i < n with l[i] != r[i], exact up to 2^32 - 1 and
+ * saturating there (0 means equal). */
+forge_status forge_compare_u32(forge_runtime *rt, forge_stream *stream,
+                               forge_slice l, forge_slice r, size_t n,
+                               forge_slice_u32 out);
 /* Matrix::causal_mask (matrix.rs:79-92 -> row.rs:5-14). */
 forge_status forge_causal_mask(forge_runtime *rt, forge_stream *stream,
                                forge_slice m, size_t rows, size_t cols);

@@ -41,43 +41,14 @@ namespace checkpoint {
 
 constexpr uint32_t FORMAT_VERSION = 1;  // model.rs:17
 
-// metadata.rs:5-18.
-struct MatrixMetadata {
-    size_t rows = 0, cols = 0;
-    uint64_t byte_start = 0, byte_end = 0;
-};
-struct VectorMetadata {
-    size_t len = 0;
-    uint64_t byte_start = 0, byte_end = 0;
-};
-// linear.rs:79-86.
-struct LinearMetadata {
-    size_t input_neurons = 0, output_neurons = 0;
-    Activation activation = Activation::Identity;
-    MatrixMetadata weights;
-    std::optional<VectorMetadata> bias;
-};
-// mlp.rs:21-34.
-struct ResidualMetadata {
-    size_t start = 0, end = 0;
-};
-struct MlpMetadata {
-    size_t layer_count = 0;
-    Loss loss = Loss::MeanSquaredError;
-    std::optional<ResidualMetadata> residual;
-    std::vector<LinearMetadata> layers;
-};
-// inference.rs:12-24, plus the gamma/beta extension.
-struct TransformerMetadata {
-    size_t block_count = 1;
-    bool attention_residual = true, feed_forward_residual = true;
-    NormType normalization = NormType::Layer;
-    MatrixMetadata position;
-    LinearMetadata query, key, value;
-    MlpMetadata feed_forward;
-    LinearMetadata output;
-    std::optional<VectorMetadata> norm1_gamma, norm1_beta, norm2_gamma, norm2_beta;
-};
+// The metadata types of the executors' get_meta_data (oxforge_net.hpp:
+// metadata.rs:5-18, linear.rs:79-86, mlp.rs:21-34, inference.rs:12-24).
+using oxforge::LinearMetadata;
+using oxforge::MatrixMetadata;
+using oxforge::MlpMetadata;
+using oxforge::ResidualMetadata;
+using oxforge::TransformerMetadata;
+using oxforge::VectorMetadata;
 
 // model.rs:53-207 entry points.
 void dump_linear(Linear& model, const std::string& path, CudaRuntime& rt);

@@ -59,14 +59,106 @@ void check(forge_status status, const char* what);
 // BinaryOp (cuda.rs:3-10).
 enum class BinaryOp : uint8_t { Add = 0, Sub = 1, Mul = 2, Div = 3 };
 
-// InitType (runtime.rs:6-22).
-enum class InitType { Sequence, Reserve, Random, Zero };
+// InitType (runtime.rs:6-22): the four kinds as enumerators
+// (InitType::Zero, ...) with the reference's is_zero().
+class InitType {
+public:
+    enum Kind { Sequence, Reserve, Random, Zero };
+    constexpr InitType(Kind kind) : kind_(kind) {}
+    // runtime.rs:14-21: true for Zero only.
+    constexpr bool is_zero() const { return kind_ == Zero; }
+    constexpr operator Kind() const { return kind_; }
+
+private:
+    Kind kind_;
+};
 
 // NormType (transformer.rs:7-13); Layer is the default.
 enum class NormType { Rms, Layer };
 
 // Activation (linear.rs:12-19).
 enum class Activation { Identity = 0, Gelu = 1, Relu = 2, Silu = 3 };
+
+// Loss (mlp.rs:8-12).
+enum class Loss { MeanSquaredError };
+
+// ---------------------------------------------------------------- metadata
+// The parameter descriptions of get_meta_data and the host copies of
+// get_data (src/net/metadata.rs, linear.rs:79-114, mlp.rs:21-34, 99-119,
+// transformer/inference.rs:12-24, 52-73): what the checkpoint writer
+// serialises.  Byte ranges count f32 parameters in model order.
+
+// metadata.rs:5-18.
+struct MatrixMetadata {
+    size_t rows = 0, cols = 0;
+    uint64_t byte_start = 0, byte_end = 0;
+    bool operator==(const MatrixMetadata& o) const {
+        return rows == o.rows && cols == o.cols && byte_start == o.byte_start &&
+               byte_end == o.byte_end;
+    }
+};
+struct VectorMetadata {
+    size_t len = 0;
+    uint64_t byte_start = 0, byte_end = 0;
+    bool operator==(const VectorMetadata& o) const {
+        return len == o.len && byte_start == o.byte_start && byte_end == o.byte_end;
+    }
+};
+
+// MetadataCursor (metadata.rs:20-68): hands out consecutive byte ranges of
+// rows * cols (or len) f32 values from position 0.  An element or byte count
+// that overflows throws Error (the reference panics).
+class MetadataCursor {
+public:
+    MetadataCursor() = default;
+    MatrixMetadata matrix(size_t rows, size_t cols);
+    VectorMetadata vector(size_t len);
+    uint64_t data_bytes() const { return position_; }
+
+private:
+    void reserve(size_t elements, uint64_t* start, uint64_t* end);
+    uint64_t position_ = 0;
+};
+
+// HostData (metadata.rs:69-82): one parameter's values copied to the host.
+class HostData {
+public:
+    explicit HostData(std::vector<float> values) : values_(std::move(values)) {}
+    const std::vector<float>& values() const { return values_; }
+
+private:
+    std::vector<float> values_;
+};
+
+// linear.rs:79-86.
+struct LinearMetadata {
+    size_t input_neurons = 0, output_neurons = 0;
+    Activation activation = Activation::Identity;
+    MatrixMetadata weights;
+    std::optional<VectorMetadata> bias;
+};
+// mlp.rs:21-34.
+struct ResidualMetadata {
+    size_t start = 0, end = 0;
+};
+struct MlpMetadata {
+    size_t layer_count = 0;
+    Loss loss = Loss::MeanSquaredError;
+    std::optional<ResidualMetadata> residual;
+    std::vector<LinearMetadata> layers;
+};
+// inference.rs:12-24, plus the gamma/beta extension: the norms' parameters,
+// when a norm has them, after the output projection.
+struct TransformerMetadata {
+    size_t block_count = 1;
+    bool attention_residual = true, feed_forward_residual = true;
+    NormType normalization = NormType::Layer;
+    MatrixMetadata position;
+    LinearMetadata query, key, value;
+    MlpMetadata feed_forward;
+    LinearMetadata output;
+    std::optional<VectorMetadata> norm1_gamma, norm1_beta, norm2_gamma, norm2_beta;
+};
 
 class CudaRuntime;
 
@@ -106,6 +198,32 @@ public:
 private:
     CudaRuntime* rt_ = nullptr;
     forge_slice s_{nullptr, 0};
+};
+
+// DeviceBuffer<u32> as CudaRuntime::get_u32_uninit_buffer returns it
+// (runtime.rs:57-60): its own allocation, not pooled, released on drop.
+class DeviceBufferU32 {
+public:
+    DeviceBufferU32() = default;
+    DeviceBufferU32(CudaRuntime* rt, forge_slice_u32 s) : rt_(rt), s_(s) {}
+    DeviceBufferU32(const DeviceBufferU32&) = delete;
+    DeviceBufferU32& operator=(const DeviceBufferU32&) = delete;
+    DeviceBufferU32(DeviceBufferU32&& o) noexcept : rt_(o.rt_), s_(o.s_) {
+        o.s_ = forge_slice_u32{nullptr, 0};
+    }
+    DeviceBufferU32& operator=(DeviceBufferU32&& o) noexcept;
+    ~DeviceBufferU32();
+
+    size_t len() const { return s_.len; }
+    bool is_empty() const { return s_.len == 0; }
+    uint32_t* ptr() const { return s_.ptr; }
+    forge_slice_u32 slice() const { return s_; }
+    // to_host_vec (vector.rs:134); blocks until the copy is done.
+    std::vector<uint32_t> to_host(CudaRuntime& rt) const;
+
+private:
+    CudaRuntime* rt_ = nullptr;
+    forge_slice_u32 s_{nullptr, 0};
 };
 
 // ------------------------------------------------------------------ spans
@@ -298,6 +416,8 @@ public:
     forge_runtime* raw() const { return rt_; }
 
     DeviceBuffer get_uninit_buffer(size_t size);
+    // runtime.rs:57-60: an uninitialised u32 buffer (not from the pool).
+    DeviceBufferU32 get_u32_uninit_buffer(size_t size);
     DeviceBuffer get_zerod_buffer(size_t size);
     void reserve_buffers(size_t size, size_t count);
     void recycle_buffer(DeviceBuffer&& buffer);
@@ -315,6 +435,9 @@ public:
     // span.rs:483-523: the spans' elements back to back in a new buffer.
     DeviceBuffer concat_buffers_from_span(const std::vector<DeviceSpan>& spans);
     DeviceBuffer clone_buffer(const DeviceBuffer& buffer);
+    // runtime.rs:184-186: the span's elements in a new pool buffer, copied
+    // on the primary stream (span.to_buffer_async).
+    DeviceBuffer span_to_buffer_async(const DeviceSpan& span);
 
     // Matrix constructors and operations.
     Matrix matrix_from_host(const std::vector<float>& values, size_t rows, size_t cols);
@@ -392,6 +515,12 @@ class Linear {
 public:
     Linear(Matrix weights, std::optional<Vector> bias, Activation activation);
 
+    // linear.rs:97-105: shapes, activation and the byte ranges of the
+    // weights, then the bias when there is one.
+    LinearMetadata get_meta_data(MetadataCursor& cursor) const;
+    // linear.rs:107-114: host copies of the weights and the bias (if any).
+    std::vector<HostData> get_data(CudaRuntime& rt) const;
+
     Matrix forward(const Matrix& input, const Matrix* residual, CudaRuntime& rt,
                    const CudaStream* stream);
     Matrix affine(const Matrix& input, const Matrix* residual, CudaRuntime& rt,
@@ -452,14 +581,23 @@ private:
     Activation activation_;
 };
 
-enum class Loss { MeanSquaredError };
-
 // MlpExecutor (mlp.rs:14-169).  res_range = [start, end): residual from the
 // input of layer `start` to the output of layer `end - 1`.
 class MlpExecutor {
 public:
     MlpExecutor(std::vector<Linear> layers, std::optional<std::pair<size_t, size_t>> res_range,
                 Loss loss = Loss::MeanSquaredError);
+    // mlp.rs:37-51 (MlpExecutor::new is the constructor with the default
+    // loss): at least one layer, and start < end <= layers for a residual.
+    static MlpExecutor with_loss(std::vector<Linear> layers,
+                                 std::optional<std::pair<size_t, size_t>> res_range, Loss loss) {
+        return MlpExecutor(std::move(layers), res_range, loss);
+    }
+    // mlp.rs:99-112: layer count, loss, residual range, then each layer's
+    // metadata in order.
+    MlpMetadata get_meta_data(MetadataCursor& cursor) const;
+    // mlp.rs:114-119: every layer's get_data, in order.
+    std::vector<HostData> get_data(CudaRuntime& rt) const;
     Matrix forward(const Matrix& input, CudaRuntime& rt);
     // forward with an extra residual added to the final layer's output
     // (fused into its epilogue); used by the transformer blocks.
@@ -491,6 +629,16 @@ public:
     InferenceMLP(std::vector<Linear> layers, std::optional<std::pair<size_t, size_t>> res_range,
                  Loss loss = Loss::MeanSquaredError)
         : executor_(std::move(layers), res_range, loss) {}
+    // mlp.rs:180-184.
+    static InferenceMLP with_loss(std::vector<Linear> layers,
+                                  std::optional<std::pair<size_t, size_t>> res_range, Loss loss) {
+        return InferenceMLP(std::move(layers), res_range, loss);
+    }
+    // mlp.rs:186-192.
+    MlpMetadata get_meta_data(MetadataCursor& cursor) const {
+        return executor_.get_meta_data(cursor);
+    }
+    std::vector<HostData> get_data(CudaRuntime& rt) const { return executor_.get_data(rt); }
     Loss loss() const { return executor_.loss(); }
     Matrix forward(const Matrix& input, CudaRuntime& rt) { return executor_.forward(input, rt); }
     MlpExecutor& executor() { return executor_; }
@@ -507,6 +655,16 @@ public:
     TrainingMlp(std::vector<Linear> layers, std::optional<std::pair<size_t, size_t>> res_range,
                 Loss loss = Loss::MeanSquaredError)
         : executor_(std::move(layers), res_range, loss) {}
+    // mlp.rs:214-219.
+    static TrainingMlp with_loss(std::vector<Linear> layers,
+                                 std::optional<std::pair<size_t, size_t>> res_range, Loss loss) {
+        return TrainingMlp(std::move(layers), res_range, loss);
+    }
+    // mlp.rs:221-228.
+    MlpMetadata get_meta_data(MetadataCursor& cursor) const {
+        return executor_.get_meta_data(cursor);
+    }
+    std::vector<HostData> get_data(CudaRuntime& rt) const { return executor_.get_data(rt); }
     Loss loss() const { return executor_.loss(); }
     Matrix forward(Matrix input, CudaRuntime& rt);
     // forward whose output also adds the MLP's own input (fused into the
@@ -565,6 +723,9 @@ public:
     Linear& query() { return query_; }
     Linear& key() { return key_; }
     Linear& value() { return value_; }
+    const Linear& query() const { return query_; }
+    const Linear& key() const { return key_; }
+    const Linear& value() const { return value_; }
 
 private:
     Linear query_, key_, value_;
@@ -598,6 +759,8 @@ public:
     void normalize(Matrix& m, CudaRuntime& rt, const Normalization* norm = nullptr) const;
     Normalization& normalization() { return norm_; }
     QkvProjection& qkv() { return qkv_; }
+    const Normalization& normalization() const { return norm_; }
+    const QkvProjection& qkv() const { return qkv_; }
     // Largest score matrix (bytes) held at once.  A [S, Sk] score matrix
     // above it is never formed: the scores, probabilities and their
     // gradients are computed for one chunk of query rows at a time (a
@@ -633,6 +796,11 @@ public:
     Matrix forward_mask(const Matrix& input, CudaRuntime& rt);
     // The same, with the output projection written into `output`.
     void forward_into(const Matrix& input, Matrix& output, CudaRuntime& rt, bool mask = false);
+    // inference.rs:52-73: Q, K, V, position, the feed-forward layers and the
+    // output projection, in that order (then the norms' gamma/beta, the
+    // extension, when present).
+    TransformerMetadata get_meta_data(MetadataCursor& cursor) const;
+    std::vector<HostData> get_data(CudaRuntime& rt) const;
     Attention& attention() { return attention_; }
     Normalization& norm2() { return norm2_; }
     Matrix& position() { return position_; }
@@ -660,6 +828,11 @@ public:
     void forward_into(const Matrix& input, Matrix& output, CudaRuntime& rt) {
         block_.forward_into(input, output, rt, false);
     }
+    // encoder.rs:45-51.
+    TransformerMetadata get_meta_data(MetadataCursor& cursor) const {
+        return block_.get_meta_data(cursor);
+    }
+    std::vector<HostData> get_data(CudaRuntime& rt) const { return block_.get_data(rt); }
     InferenceBlock& block() { return block_; }
 
 private:
@@ -685,6 +858,9 @@ public:
     // written into `input_gradient` ([seq, hidden]) instead of a new matrix.
     void backward_into(const Matrix& output_gradient, float learning_rate, CudaRuntime& rt,
                        Matrix& input_gradient, TransformerGrads* grads = nullptr);
+    // encoder.rs:90-112 (the same layout as the inference block).
+    TransformerMetadata get_meta_data(MetadataCursor& cursor) const;
+    std::vector<HostData> get_data(CudaRuntime& rt) const;
     Attention& attention() { return attention_; }
     TrainingMlp& fcs() { return fcs_; }
     Linear& output() { return output_; }
@@ -719,6 +895,11 @@ public:
     void forward_into(const Matrix& input, Matrix& output, CudaRuntime& rt) {
         block_.forward_into(input, output, rt, true);
     }
+    // decoder.rs:42-48.
+    TransformerMetadata get_meta_data(MetadataCursor& cursor) const {
+        return block_.get_meta_data(cursor);
+    }
+    std::vector<HostData> get_data(CudaRuntime& rt) const { return block_.get_data(rt); }
     InferenceBlock& block() { return block_; }
 
 private:

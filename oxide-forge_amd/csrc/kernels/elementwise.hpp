@@ -251,15 +251,23 @@ __device__ __forceinline__ void act_backward_body(const float* __restrict__ dy,
     }
 }
 
+// A count as the output type: the f32 nearest to it (exact up to 2^24), or
+// the u32 count saturated at 2^32 - 1.
+__device__ __forceinline__ void store_count(float* out, unsigned long long t) { out[0] = (float)t; }
+__device__ __forceinline__ void store_count(unsigned* out, unsigned long long t) {
+    out[0] = t > 0xFFFFFFFFull ? 0xFFFFFFFFu : (unsigned)t;
+}
+
 // Count of positions where l != r (compare_vectors, reduction.rs:132-174,
 // but over every element; the reference keeps only block 0's verdict).
 // Counts are integers throughout: per-workgroup partials in `part` (u32),
 // summed in u64 by count_final_body.  With one workgroup the kernel writes
-// the count itself, as the f32 nearest to it (exact up to 2^24).
+// the count itself (store_count).
+template <typename T>
 __device__ __forceinline__ void count_neq_body(const float* __restrict__ l,
                                                const float* __restrict__ r, long long n,
                                                unsigned* __restrict__ part,
-                                               float* __restrict__ out) {
+                                               T* __restrict__ out) {
     __shared__ unsigned wsum[EW_THREADS / 64];
     const long long tid = (long long)blockIdx.x * EW_THREADS + threadIdx.x;
     const long long stride = (long long)gridDim.x * EW_THREADS;
@@ -271,14 +279,15 @@ __device__ __forceinline__ void count_neq_body(const float* __restrict__ l,
     if (threadIdx.x == 0) {
         unsigned long long t = 0;
         for (int w = 0; w < (EW_THREADS >> 6); w++) t += wsum[w];
-        if (gridDim.x == 1) out[0] = (float)t;
+        if (gridDim.x == 1) store_count(out, t);
         else part[blockIdx.x] = (unsigned)t;
     }
 }
 
-// Sum of `n` u32 partial counts in u64; writes the f32 nearest to the total.
+// Sum of `n` u32 partial counts in u64, stored by store_count.
+template <typename T>
 __device__ __forceinline__ void count_final_body(const unsigned* __restrict__ part, int n,
-                                                 float* __restrict__ out) {
+                                                 T* __restrict__ out) {
     __shared__ unsigned long long wsum[EW_THREADS / 64];
     unsigned long long acc = 0;
     for (int i = threadIdx.x; i < n; i += EW_THREADS) acc += part[i];
@@ -288,7 +297,7 @@ __device__ __forceinline__ void count_final_body(const unsigned* __restrict__ pa
     if (threadIdx.x == 0) {
         unsigned long long t = 0;
         for (int w = 0; w < (EW_THREADS >> 6); w++) t += wsum[w];
-        out[0] = (float)t;
+        store_count(out, t);
     }
 }
 

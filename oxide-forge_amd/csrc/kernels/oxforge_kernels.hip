@@ -221,6 +221,15 @@ FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_count_final(const unsigned
                                                                   float* out) {
     count_final_body(part, n, out);
 }
+FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_count_neq_u32(const float* l, const float* r,
+                                                                    long long n, unsigned* part,
+                                                                    unsigned* out) {
+    count_neq_body(l, r, n, part, out);
+}
+FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_count_final_u32(const unsigned* part, int n,
+                                                                      unsigned* out) {
+    count_final_body(part, n, out);
+}
 FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_causal_mask(float* m, int rows, int cols,
                                                                   int first_row) {
     causal_mask_body(m, rows, cols, first_row);

@@ -629,11 +629,9 @@ void write_text(const std::string& path, const std::string& text) {
 
 // ------------------------------------------------------------- parameters
 
-// Host copies of the parameters, in checkpoint order.
+// Host copies of the parameters, in checkpoint order (the models' get_data).
 struct Parameters {
-    std::vector<std::vector<float>> blocks;
-    void add(const Matrix& m, CudaRuntime& rt) { blocks.push_back(m.to_host(rt)); }
-    void add(const Vector& v, CudaRuntime& rt) { blocks.push_back(v.to_host(rt)); }
+    std::vector<HostData> blocks;
 };
 
 void write_parameters(const std::string& path, const Parameters& params, uint64_t expected) {
@@ -641,9 +639,10 @@ void write_parameters(const std::string& path, const Parameters& params, uint64_
     std::ofstream f(path, std::ios::binary | std::ios::trunc);
     if (!f) io_error("cannot create " + path);
     uint64_t written = 0;
-    for (const auto& b : params.blocks) {
-        f.write(reinterpret_cast<const char*>(b.data()), (std::streamsize)(b.size() * 4));
-        written += (uint64_t)b.size() * 4;
+    for (const HostData& b : params.blocks) {
+        const std::vector<float>& v = b.values();
+        f.write(reinterpret_cast<const char*>(v.data()), (std::streamsize)(v.size() * 4));
+        written += (uint64_t)v.size() * 4;
     }
     f.flush();
     if (!f) io_error("cannot write " + path);
@@ -683,75 +682,6 @@ private:
 };
 
 // ------------------------------------------------ model <-> metadata
-
-struct Cursor {
-    uint64_t position = 0;
-    MatrixMetadata matrix(size_t rows, size_t cols) {
-        MatrixMetadata m{rows, cols, position, position + (uint64_t)rows * cols * 4};
-        position = m.byte_end;
-        return m;
-    }
-    VectorMetadata vector(size_t len) {
-        VectorMetadata v{len, position, position + (uint64_t)len * 4};
-        position = v.byte_end;
-        return v;
-    }
-};
-
-LinearMetadata linear_meta(Linear& l, Cursor& c, Parameters* p, CudaRuntime& rt) {
-    // linear.rs:97-114.
-    LinearMetadata m;
-    m.input_neurons = l.weights().rows();
-    m.output_neurons = l.weights().cols();
-    m.activation = l.activation();
-    m.weights = c.matrix(l.weights().rows(), l.weights().cols());
-    if (p) p->add(l.weights(), rt);
-    if (l.bias()) {
-        m.bias = c.vector(l.bias()->len());
-        if (p) p->add(*l.bias(), rt);
-    }
-    return m;
-}
-
-MlpMetadata mlp_meta(MlpExecutor& e, Cursor& c, Parameters* p, CudaRuntime& rt) {
-    // mlp.rs:99-119.
-    MlpMetadata m;
-    m.layer_count = e.len();
-    m.loss = e.loss();
-    if (e.res_range()) m.residual = ResidualMetadata{e.res_range()->first, e.res_range()->second};
-    for (auto& l : e.layers()) m.layers.push_back(linear_meta(l, c, p, rt));
-    return m;
-}
-
-void norm_meta(const Normalization& n, std::optional<VectorMetadata>* g,
-               std::optional<VectorMetadata>* b, Cursor& c, Parameters* p, CudaRuntime& rt) {
-    if (n.gamma) {
-        *g = c.vector(n.gamma->len());
-        if (p) p->add(*n.gamma, rt);
-    }
-    if (n.beta) {
-        *b = c.vector(n.beta->len());
-        if (p) p->add(*n.beta, rt);
-    }
-}
-
-TransformerMetadata transformer_meta(QkvProjection& qkv, Normalization& norm1, Matrix& position,
-                                     MlpExecutor& fcs, Linear& output, Normalization& norm2,
-                                     Cursor& c, Parameters* p, CudaRuntime& rt) {
-    // encoder.rs:90-112 (Q, K, V, position, FFN, output), then the norms.
-    TransformerMetadata m;
-    m.normalization = norm1.kind;
-    m.query = linear_meta(qkv.query(), c, p, rt);
-    m.key = linear_meta(qkv.key(), c, p, rt);
-    m.value = linear_meta(qkv.value(), c, p, rt);
-    m.position = c.matrix(position.rows(), position.cols());
-    if (p) p->add(position, rt);
-    m.feed_forward = mlp_meta(fcs, c, p, rt);
-    m.output = linear_meta(output, c, p, rt);
-    norm_meta(norm1, &m.norm1_gamma, &m.norm1_beta, c, p, rt);
-    norm_meta(norm2, &m.norm2_gamma, &m.norm2_beta, c, p, rt);
-    return m;
-}
 
 Linear load_linear_params(const LinearMetadata& m, ParameterReader& r, CudaRuntime& rt) {
     std::vector<float> w = r.read(m.weights.byte_start, m.weights.byte_end,
@@ -842,9 +772,9 @@ std::string transformer_body(const TransformerMetadata& m) {
 }
 
 void dump_mlp_executor(MlpExecutor& e, const std::string& path, CudaRuntime& rt) {
-    Cursor c;
-    Parameters p;
-    MlpMetadata m = mlp_meta(e, c, &p, rt);
+    MetadataCursor c;
+    MlpMetadata m = e.get_meta_data(c);
+    Parameters p{e.get_data(rt)};
     RangeValidator r;
     validate_mlp(m, r);
     dump(path, "mlp", mlp_body(m), r.position, p);
@@ -907,11 +837,9 @@ LoadedTransformer load_transformer_file(const std::string& path, CudaRuntime& rt
 }
 
 void dump_block(InferenceBlock& b, const std::string& path, CudaRuntime& rt) {
-    Cursor c;
-    Parameters p;
-    TransformerMetadata m =
-        transformer_meta(b.attention().qkv(), b.attention().normalization(), b.position(),
-                         b.fcs().executor(), b.output(), b.norm2(), c, &p, rt);
+    MetadataCursor c;
+    TransformerMetadata m = b.get_meta_data(c);
+    Parameters p{b.get_data(rt)};
     RangeValidator r;
     validate_transformer(m, r);
     dump(path, "transformer", transformer_body(m), r.position, p);
@@ -922,9 +850,9 @@ void dump_block(InferenceBlock& b, const std::string& path, CudaRuntime& rt) {
 // ================================================================ public
 
 void dump_linear(Linear& model, const std::string& path, CudaRuntime& rt) {
-    Cursor c;
-    Parameters p;
-    LinearMetadata m = linear_meta(model, c, &p, rt);
+    MetadataCursor c;
+    LinearMetadata m = model.get_meta_data(c);
+    Parameters p{model.get_data(rt)};
     RangeValidator r;
     validate_linear(m, r);
     dump(path, "linear", linear_body(m), r.position, p);
@@ -977,11 +905,9 @@ encoder::InferenceTransformer load_transformer(const std::string& path, CudaRunt
 
 void dump_training_transformer(encoder::TrainingTransformer& model, const std::string& path,
                                CudaRuntime& rt) {
-    Cursor c;
-    Parameters p;
-    TransformerMetadata m = transformer_meta(
-        model.attention().qkv(), model.attention().normalization(), model.position(),
-        model.fcs().executor(), model.output(), model.norm2(), c, &p, rt);
+    MetadataCursor c;
+    TransformerMetadata m = model.get_meta_data(c);
+    Parameters p{model.get_data(rt)};
     RangeValidator r;
     validate_transformer(m, r);
     dump(path, "transformer", transformer_body(m), r.position, p);

@@ -63,6 +63,26 @@ Linear::Linear(Matrix weights, std::optional<Vector> bias, Activation activation
     if (bias_) require(bias_->len() == weights_.cols(), "bias.len() == weights.cols()");
 }
 
+LinearMetadata Linear::get_meta_data(MetadataCursor& cursor) const {
+    // linear.rs:97-105.
+    LinearMetadata m;
+    m.input_neurons = weights_.rows();
+    m.output_neurons = weights_.cols();
+    m.activation = activation_;
+    m.weights = cursor.matrix(weights_.rows(), weights_.cols());
+    if (bias_) m.bias = cursor.vector(bias_->len());
+    return m;
+}
+
+std::vector<HostData> Linear::get_data(CudaRuntime& rt) const {
+    // linear.rs:107-114.
+    std::vector<HostData> data;
+    data.reserve(bias_ ? 2 : 1);
+    data.emplace_back(weights_.to_host(rt));
+    if (bias_) data.emplace_back(bias_->to_host(rt));
+    return data;
+}
+
 Matrix Linear::forward_keep(const Matrix& input, const Matrix* residual, Matrix* pre_activation,
                             CudaRuntime& rt, const CudaStream* stream) {
     // linear.rs:116-132 -> affine_on (185-206) + activate_on (225-230).
@@ -277,6 +297,24 @@ MlpExecutor::MlpExecutor(std::vector<Linear> layers,
     if (res_range_)
         require(res_range_->first < res_range_->second && res_range_->second <= layers_.size(),
                 "invalid residual range");
+}
+
+MlpMetadata MlpExecutor::get_meta_data(MetadataCursor& cursor) const {
+    // mlp.rs:99-112.
+    MlpMetadata m;
+    m.layer_count = layers_.size();
+    m.loss = loss_;
+    if (res_range_) m.residual = ResidualMetadata{res_range_->first, res_range_->second};
+    for (const Linear& l : layers_) m.layers.push_back(l.get_meta_data(cursor));
+    return m;
+}
+
+std::vector<HostData> MlpExecutor::get_data(CudaRuntime& rt) const {
+    // mlp.rs:114-119.
+    std::vector<HostData> data;
+    for (const Linear& l : layers_)
+        for (HostData& d : l.get_data(rt)) data.push_back(std::move(d));
+    return data;
 }
 
 Matrix MlpExecutor::forward(const Matrix& input, CudaRuntime& rt) {
@@ -862,6 +900,52 @@ Matrix Attention::backward_self(const Matrix& output_gradient, float learning_ra
     return residual_gradient;
 }
 
+// ============================================= transformer metadata / data
+
+// inference.rs:52-73 and encoder.rs:90-112: Q, K, V, the position matrix,
+// the feed-forward layers and the output projection, then (the gamma/beta
+// extension) each norm's gamma and beta that exist, first norm first.
+static TransformerMetadata transformer_meta_data(const Attention& attention,
+                                                 const Matrix& position, const MlpExecutor& fcs,
+                                                 const Linear& output, const Normalization& norm2,
+                                                 MetadataCursor& cursor) {
+    TransformerMetadata m;
+    m.normalization = attention.norm_type();
+    m.query = attention.qkv().query().get_meta_data(cursor);
+    m.key = attention.qkv().key().get_meta_data(cursor);
+    m.value = attention.qkv().value().get_meta_data(cursor);
+    m.position = cursor.matrix(position.rows(), position.cols());
+    m.feed_forward = fcs.get_meta_data(cursor);
+    m.output = output.get_meta_data(cursor);
+    const Normalization& norm1 = attention.normalization();
+    if (norm1.gamma) m.norm1_gamma = cursor.vector(norm1.gamma->len());
+    if (norm1.beta) m.norm1_beta = cursor.vector(norm1.beta->len());
+    if (norm2.gamma) m.norm2_gamma = cursor.vector(norm2.gamma->len());
+    if (norm2.beta) m.norm2_beta = cursor.vector(norm2.beta->len());
+    return m;
+}
+
+static std::vector<HostData> transformer_data(const Attention& attention, const Matrix& position,
+                                              const MlpExecutor& fcs, const Linear& output,
+                                              const Normalization& norm2, CudaRuntime& rt) {
+    std::vector<HostData> data;
+    auto append = [&data](std::vector<HostData> more) {
+        for (HostData& d : more) data.push_back(std::move(d));
+    };
+    append(attention.qkv().query().get_data(rt));
+    append(attention.qkv().key().get_data(rt));
+    append(attention.qkv().value().get_data(rt));
+    data.emplace_back(position.to_host(rt));
+    append(fcs.get_data(rt));
+    append(output.get_data(rt));
+    const Normalization& norm1 = attention.normalization();
+    for (const Normalization* n : {&norm1, &norm2}) {
+        if (n->gamma) data.emplace_back(n->gamma->to_host(rt));
+        if (n->beta) data.emplace_back(n->beta->to_host(rt));
+    }
+    return data;
+}
+
 // ========================================================= InferenceBlock
 
 static Normalization default_norm(NormType kind) {
@@ -878,6 +962,14 @@ InferenceBlock::InferenceBlock(Linear query, Linear key, Linear value, Matrix po
                  default_norm(norm_type)),
       position_(std::move(position)), fcs_(std::move(fcs)), output_(std::move(output)),
       norm2_(norm2 ? std::move(*norm2) : default_norm(norm_type)) {}
+
+TransformerMetadata InferenceBlock::get_meta_data(MetadataCursor& cursor) const {
+    return transformer_meta_data(attention_, position_, fcs_.executor(), output_, norm2_, cursor);
+}
+
+std::vector<HostData> InferenceBlock::get_data(CudaRuntime& rt) const {
+    return transformer_data(attention_, position_, fcs_.executor(), output_, norm2_, rt);
+}
 
 Matrix InferenceBlock::forward(const Matrix& input, CudaRuntime& rt) {
     // inference.rs:76-80.
@@ -938,6 +1030,14 @@ TrainingTransformer::TrainingTransformer(Linear q, Linear k, Linear v, Matrix po
                  norm1 ? std::move(*norm1) : default_norm(norm_type)),
       position_(std::move(position)), fcs_(std::move(fcs)), output_(std::move(output)),
       norm2_(norm2 ? std::move(*norm2) : default_norm(norm_type)) {}
+
+TransformerMetadata TrainingTransformer::get_meta_data(MetadataCursor& cursor) const {
+    return transformer_meta_data(attention_, position_, fcs_.executor(), output_, norm2_, cursor);
+}
+
+std::vector<HostData> TrainingTransformer::get_data(CudaRuntime& rt) const {
+    return transformer_data(attention_, position_, fcs_.executor(), output_, norm2_, rt);
+}
 
 Matrix TrainingTransformer::forward(const Matrix& input, CudaRuntime& rt) {
     Matrix output = rt.new_uninit_matrix(input.rows(), output_.weights().cols());

@@ -4,6 +4,7 @@
 // Every device operation is one call into include/oxforge.h; shape checks
 // that the reference makes with assert! throw oxforge::Error here.
 #include <algorithm>
+#include <cstdint>
 #include <cstring>
 #include <random>
 
@@ -45,6 +46,58 @@ DeviceBuffer& DeviceBuffer::operator=(DeviceBuffer&& o) noexcept {
 
 DeviceBuffer::~DeviceBuffer() {
     if (rt_ && s_.ptr) (void)forge_recycle(rt_->raw(), s_);
+}
+
+DeviceBufferU32& DeviceBufferU32::operator=(DeviceBufferU32&& o) noexcept {
+    if (this != &o) {
+        if (rt_ && s_.ptr) (void)forge_free_u32(rt_->raw(), s_);
+        rt_ = o.rt_;
+        s_ = o.s_;
+        o.s_ = forge_slice_u32{nullptr, 0};
+    }
+    return *this;
+}
+
+DeviceBufferU32::~DeviceBufferU32() {
+    if (rt_ && s_.ptr) (void)forge_free_u32(rt_->raw(), s_);
+}
+
+std::vector<uint32_t> DeviceBufferU32::to_host(CudaRuntime& rt) const {
+    std::vector<uint32_t> out(s_.len);
+    check(forge_memcpy_d2h_u32(rt.raw(), out.data(), s_, s_.len), "to_host_vec");
+    return out;
+}
+
+// --------------------------------------------------------------- metadata
+
+// metadata.rs:56-67: the next `elements` f32 values' byte range.
+void MetadataCursor::reserve(size_t elements, uint64_t* start, uint64_t* end) {
+    if ((uint64_t)elements > UINT64_MAX / 4)
+        throw Error(FORGE_EINVAL, "parameter byte length overflow");
+    const uint64_t bytes = (uint64_t)elements * 4;
+    if (position_ > UINT64_MAX - bytes) throw Error(FORGE_EINVAL, "checkpoint offset overflow");
+    *start = position_;
+    position_ += bytes;
+    *end = position_;
+}
+
+MatrixMetadata MetadataCursor::matrix(size_t rows, size_t cols) {
+    // metadata.rs:30-41.
+    if (cols != 0 && rows > SIZE_MAX / cols)
+        throw Error(FORGE_EINVAL, "matrix element count overflow");
+    MatrixMetadata m;
+    m.rows = rows;
+    m.cols = cols;
+    reserve(rows * cols, &m.byte_start, &m.byte_end);
+    return m;
+}
+
+VectorMetadata MetadataCursor::vector(size_t len) {
+    // metadata.rs:43-50.
+    VectorMetadata v;
+    v.len = len;
+    reserve(len, &v.byte_start, &v.byte_end);
+    return v;
 }
 
 // ------------------------------------------------------------------ spans
@@ -194,6 +247,12 @@ DeviceBuffer CudaRuntime::get_uninit_buffer(size_t size) {
     return DeviceBuffer(this, s);
 }
 
+DeviceBufferU32 CudaRuntime::get_u32_uninit_buffer(size_t size) {
+    forge_slice_u32 s;
+    check(forge_alloc_u32(rt_, size, &s), "get_u32_uninit_buffer");
+    return DeviceBufferU32(this, s);
+}
+
 DeviceBuffer CudaRuntime::get_zerod_buffer(size_t size) {
     forge_slice s;
     check(forge_alloc_zeroed(rt_, size, &s), "get_zerod_buffer");
@@ -259,6 +318,10 @@ DeviceBuffer CudaRuntime::concat_buffers(const std::vector<const DeviceBuffer*>&
         offset += b->len();
     }
     return result;
+}
+
+DeviceBuffer CudaRuntime::span_to_buffer_async(const DeviceSpan& span) {
+    return span.to_buffer_async(*this);
 }
 
 DeviceBuffer CudaRuntime::clone_buffer(const DeviceBuffer& buffer) {
@@ -632,12 +695,12 @@ float Vector::dot(const Vector& rhs, CudaRuntime& rt) const {
 }
 
 bool Vector::equals(const Vector& rhs, CudaRuntime& rt) const {
+    // vector.rs:117-136: the comparison into a one-element u32 buffer.
     require(len() == rhs.len(), "equals lengths");
-    DeviceBuffer out = rt.get_uninit_buffer(1);
-    check(forge_compare(rt.raw(), nullptr, slice(), rhs.slice(), len(), out.slice()), "equals");
-    float h = 1.0f;
-    check(forge_memcpy_d2h(rt.raw(), &h, out.slice(), 1), "equals to host");
-    return h == 0.0f;
+    DeviceBufferU32 result = rt.get_u32_uninit_buffer(1);
+    check(forge_compare_u32(rt.raw(), nullptr, slice(), rhs.slice(), len(), result.slice()),
+          "equals");
+    return result.to_host(rt)[0] == 0;
 }
 
 // ----------------------------------------------------------------- Matrix

@@ -207,6 +207,13 @@ forge_status need(const forge_slice& s, size_t n, const char* what) {
     return FORGE_OK;
 }
 
+forge_status need(const forge_slice_u32& s, size_t n, const char* what) {
+    if (n > 0 && (s.ptr == nullptr || s.len < n))
+        return fail(FORGE_EINVAL, "%s: u32 slice of %zu elements (ptr %p) is too short for %zu",
+                    what, s.len, (void*)s.ptr, n);
+    return FORGE_OK;
+}
+
 forge_status need_opt(const forge_slice& s, size_t n, const char* what) {
     if (s.ptr == nullptr) return FORGE_OK;
     return need(s, n, what);
@@ -494,6 +501,28 @@ extern "C" forge_status forge_free(forge_runtime* rt, forge_slice buf) {
     return FORGE_OK;
 }
 
+extern "C" forge_status forge_alloc_u32(forge_runtime* rt, size_t n, forge_slice_u32* out) {
+    if (!rt || !out) return fail(FORGE_EINVAL, "null argument");
+    out->ptr = nullptr;
+    out->len = 0;
+    if (n == 0) return FORGE_OK;
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, n * sizeof(uint32_t));
+    if (e != hipSuccess)
+        return fail(FORGE_ENOMEM, "hipMalloc of %zu u32: %s", n, hipGetErrorString(e));
+    out->ptr = static_cast<uint32_t*>(p);
+    out->len = n;
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_free_u32(forge_runtime* rt, forge_slice_u32 buf) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    if (!buf.ptr) return FORGE_OK;
+    HIP_TRY(hipStreamSynchronize(rt->primary.stream));
+    HIP_TRY(hipFree(buf.ptr));
+    return FORGE_OK;
+}
+
 extern "C" forge_status forge_reserve(forge_runtime* rt, size_t n, size_t count) {
     if (!rt) return fail(FORGE_EINVAL, "runtime is null");
     if (n == 0) return FORGE_OK;
@@ -532,6 +561,17 @@ extern "C" forge_status forge_memcpy_d2h(forge_runtime* rt, float* dst, forge_sl
     FORGE_TRY(need(src, n, "memcpy_d2h src"));
     if (n == 0) return FORGE_OK;
     HIP_TRY(hipMemcpyAsync(dst, src.ptr, n * sizeof(float), hipMemcpyDeviceToHost,
+                           rt->primary.stream));
+    HIP_TRY(hipStreamSynchronize(rt->primary.stream));
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_memcpy_d2h_u32(forge_runtime* rt, uint32_t* dst, forge_slice_u32 src,
+                                             size_t n) {
+    if (!rt || (n && !dst)) return fail(FORGE_EINVAL, "null argument");
+    FORGE_TRY(need(src, n, "memcpy_d2h_u32 src"));
+    if (n == 0) return FORGE_OK;
+    HIP_TRY(hipMemcpyAsync(dst, src.ptr, n * sizeof(uint32_t), hipMemcpyDeviceToHost,
                            rt->primary.stream));
     HIP_TRY(hipStreamSynchronize(rt->primary.stream));
     return FORGE_OK;
@@ -1689,26 +1729,44 @@ extern "C" forge_status forge_fill_random(forge_runtime* rt, forge_stream* s, fo
                        dim3(EW_THREADS), 0, x.ptr, nn, sd);
 }
 
+// Mismatch count of l and r over n elements into out[0] (T: float or u32),
+// by the kernels named count and count_final: per-workgroup u32 partials in
+// the stream's workspace, summed by one final workgroup.
+template <typename T>
+static forge_status compare_into(forge_runtime* rt, forge_stream* s, forge_slice l, forge_slice r,
+                                 size_t n, T* out, const char* count, const char* count_final) {
+    long long nn = (long long)n;
+    unsigned g = grid_for(nn, EW_THREADS * 4, 1024);
+    if (g == 1)
+        return launch_args(rt, s, count, dim3(1), dim3(EW_THREADS), 0, (const float*)l.ptr,
+                           (const float*)r.ptr, nn, (unsigned*)nullptr, out);
+    float* ws;
+    FORGE_TRY(workspace(rt, s, g, &ws));
+    unsigned* part = reinterpret_cast<unsigned*>(ws);
+    FORGE_TRY(launch_args(rt, s, count, dim3(g), dim3(EW_THREADS), 0, (const float*)l.ptr,
+                          (const float*)r.ptr, nn, part, out));
+    int gn = (int)g;
+    return launch_args(rt, s, count_final, dim3(1), dim3(EW_THREADS), 0, (const unsigned*)part, gn,
+                       out);
+}
+
 extern "C" forge_status forge_compare(forge_runtime* rt, forge_stream* s, forge_slice l,
                                       forge_slice r, size_t n, forge_slice out) {
     if (!rt) return fail(FORGE_EINVAL, "runtime is null");
     FORGE_TRY(need(l, n, "compare l"));
     FORGE_TRY(need(r, n, "compare r"));
     FORGE_TRY(need(out, 1, "compare out"));
-    long long nn = (long long)n;
-    unsigned g = grid_for(nn, EW_THREADS * 4, 1024);
-    if (g == 1)
-        return launch_args(rt, s, "forge_count_neq", dim3(1), dim3(EW_THREADS), 0,
-                           (const float*)l.ptr, (const float*)r.ptr, nn, (unsigned*)nullptr,
-                           out.ptr);
-    float* ws;
-    FORGE_TRY(workspace(rt, s, g, &ws));
-    unsigned* part = reinterpret_cast<unsigned*>(ws);
-    FORGE_TRY(launch_args(rt, s, "forge_count_neq", dim3(g), dim3(EW_THREADS), 0,
-                          (const float*)l.ptr, (const float*)r.ptr, nn, part, out.ptr));
-    int gn = (int)g;
-    return launch_args(rt, s, "forge_count_final", dim3(1), dim3(EW_THREADS), 0,
-                       (const unsigned*)part, gn, out.ptr);
+    return compare_into(rt, s, l, r, n, out.ptr, "forge_count_neq", "forge_count_final");
+}
+
+extern "C" forge_status forge_compare_u32(forge_runtime* rt, forge_stream* s, forge_slice l,
+                                          forge_slice r, size_t n, forge_slice_u32 out) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    FORGE_TRY(need(l, n, "compare l"));
+    FORGE_TRY(need(r, n, "compare r"));
+    FORGE_TRY(need(out, 1, "compare out"));
+    return compare_into(rt, s, l, r, n, reinterpret_cast<unsigned*>(out.ptr),
+                        "forge_count_neq_u32", "forge_count_final_u32");
 }
 
 extern "C" forge_status forge_fill_seq(forge_runtime* rt, forge_stream* s, forge_slice x, size_t n,

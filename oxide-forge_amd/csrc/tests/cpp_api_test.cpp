@@ -72,7 +72,137 @@ static void dump(const std::string& path, const std::vector<float>& v) {
     std::fclose(f);
 }
 
+// ------------------------------------------------ metadata as JSON
+// get_meta_data results in the field names and nesting of the reference's
+// serde structs (the form oracle/checkpoint.py builds), for the comparison
+// of tests/test_gpu_cpp_api.py.  Absent options are left out, as serde's
+// skip of None in the checkpoint writer.
+static const char* act_name(Activation a) {
+    switch (a) {
+    case Activation::Gelu: return "gelu";
+    case Activation::Relu: return "relu";
+    case Activation::Silu: return "silu";
+    default: return "identity";
+    }
+}
+
+static std::string json(const MatrixMetadata& m) {
+    return "{\"rows\": " + std::to_string(m.rows) + ", \"cols\": " + std::to_string(m.cols) +
+           ", \"byte_start\": " + std::to_string(m.byte_start) +
+           ", \"byte_end\": " + std::to_string(m.byte_end) + "}";
+}
+
+static std::string json(const VectorMetadata& v) {
+    return "{\"len\": " + std::to_string(v.len) + ", \"byte_start\": " +
+           std::to_string(v.byte_start) + ", \"byte_end\": " + std::to_string(v.byte_end) + "}";
+}
+
+static std::string json(const LinearMetadata& l) {
+    std::string s = "{\"input_neurons\": " + std::to_string(l.input_neurons) +
+                    ", \"output_neurons\": " + std::to_string(l.output_neurons) +
+                    ", \"activation\": \"" + act_name(l.activation) + "\", \"weights\": " +
+                    json(l.weights);
+    if (l.bias) s += ", \"bias\": " + json(*l.bias);
+    return s + "}";
+}
+
+static std::string json(const MlpMetadata& m) {
+    std::string s = "{\"layer_count\": " + std::to_string(m.layer_count) +
+                    ", \"loss\": \"mean_squared_error\"";
+    if (m.residual)
+        s += ", \"residual\": {\"start\": " + std::to_string(m.residual->start) +
+             ", \"end\": " + std::to_string(m.residual->end) + "}";
+    s += ", \"layers\": [";
+    for (size_t i = 0; i < m.layers.size(); i++) s += (i ? ", " : "") + json(m.layers[i]);
+    return s + "]}";
+}
+
+static std::string json(const TransformerMetadata& t) {
+    std::string s = "{\"block_count\": " + std::to_string(t.block_count) +
+                    ", \"attention_residual\": " + (t.attention_residual ? "true" : "false") +
+                    ", \"feed_forward_residual\": " +
+                    (t.feed_forward_residual ? "true" : "false") + ", \"normalization\": \"" +
+                    (t.normalization == NormType::Rms ? "rms" : "layer") +
+                    "\", \"position\": " + json(t.position) + ", \"query\": " + json(t.query) +
+                    ", \"key\": " + json(t.key) + ", \"value\": " + json(t.value) +
+                    ", \"feed_forward\": " + json(t.feed_forward) +
+                    ", \"output\": " + json(t.output);
+    const std::pair<const char*, const std::optional<VectorMetadata>*> norms[] = {
+        {"norm1_gamma", &t.norm1_gamma}, {"norm1_beta", &t.norm1_beta},
+        {"norm2_gamma", &t.norm2_gamma}, {"norm2_beta", &t.norm2_beta}};
+    for (const auto& n : norms)
+        if (*n.second) s += std::string(", \"") + n.first + "\": " + json(**n.second);
+    return s + "}";
+}
+
+// Writes <dir>/<name>.json ({"meta": ..., "data_bytes": N}) and
+// <dir>/<name>.f32 (every get_data block back to back).
+static void write_model(const std::string& dir, const std::string& name, const std::string& meta,
+                        uint64_t data_bytes, const std::vector<HostData>& data) {
+    FILE* f = std::fopen((dir + "/" + name + ".json").c_str(), "w");
+    if (!f) {
+        std::printf("FAIL cannot write %s.json\n", name.c_str());
+        g_failures++;
+        return;
+    }
+    std::fprintf(f, "{\"meta\": %s, \"data_bytes\": %llu}\n", meta.c_str(),
+                 (unsigned long long)data_bytes);
+    std::fclose(f);
+    std::vector<float> all;
+    for (const HostData& d : data) all.insert(all.end(), d.values().begin(), d.values().end());
+    dump(dir + "/" + name + ".f32", all);
+}
+
+template <typename M>
+static void describe(const std::string& dir, const std::string& name, const M& model,
+                     CudaRuntime& R) {
+    MetadataCursor cursor;
+    auto meta = model.get_meta_data(cursor);
+    write_model(dir, name, json(meta), cursor.data_bytes(), model.get_data(R));
+}
+
+// --metadata <dir>: loads the checkpoints that tests/test_gpu_cpp_api.py wrote
+// into <dir> with the reference-format writer of the oracle (linear,
+// linear_nobias, mlp, transformer_rms, transformer_layer) into every model
+// type that can hold them and writes what get_meta_data / get_data return.
+static int metadata_mode(const std::string& dir, CudaRuntime& R) {
+    namespace ck = checkpoint;
+    for (const char* name : {"linear", "linear_nobias"}) {
+        Linear l = ck::load_linear(dir + "/" + name, R);
+        describe(dir, std::string(name) + ".Linear", l, R);
+    }
+    {
+        MlpExecutor e = ck::load_mlp(dir + "/mlp", R);
+        describe(dir, "mlp.MlpExecutor", e, R);
+        InferenceMLP i = ck::load_inference_mlp(dir + "/mlp", R);
+        describe(dir, "mlp.InferenceMLP", i, R);
+        TrainingMlp t = ck::load_training_mlp(dir + "/mlp", R);
+        describe(dir, "mlp.TrainingMlp", t, R);
+    }
+    for (const char* name : {"transformer_rms", "transformer_layer"}) {
+        const std::string path = dir + "/" + name;
+        encoder::InferenceTransformer e = ck::load_transformer(path, R);
+        describe(dir, std::string(name) + ".encoder.InferenceTransformer", e, R);
+        encoder::TrainingTransformer t = ck::load_training_transformer(path, R);
+        describe(dir, std::string(name) + ".encoder.TrainingTransformer", t, R);
+        decoder::InferenceTransformer d = ck::load_decoder_transformer(path, R);
+        describe(dir, std::string(name) + ".decoder.InferenceTransformer", d, R);
+    }
+    R.sync();
+    std::printf("%s: %d failed check(s)\n", g_failures ? "FAILED" : "OK", g_failures);
+    return g_failures ? 1 : 0;
+}
+
 int main(int argc, char** argv) {
+    if (argc > 2 && std::string(argv[1]) == "--metadata") {
+        int ndev = 0;
+        if (forge_device_count(&ndev) != FORGE_OK || ndev == 0) {
+            std::printf("no GPU\n");
+            return 2;
+        }
+        auto rt = CudaRuntime::create();
+        return metadata_mode(argv[2], *rt);
+    }
     const std::string dump_dir = argc > 1 ? argv[1] : "";
     int dev = 0;
     if (forge_device_count(&dev) != FORGE_OK || dev == 0) {
@@ -798,6 +928,81 @@ int main(int argc, char** argv) {
         }
         CHECK(ok, "DeviceSpanMut::for_each on a sub-span");
         group("spans", f);
+    }
+
+    // ------------------------------------------- reference API members
+    {
+        int f = g_failures;
+        // InitType::is_zero (runtime.rs:14-21).
+        CHECK(InitType(InitType::Zero).is_zero() && !InitType(InitType::Sequence).is_zero() &&
+                  !InitType(InitType::Reserve).is_zero() && !InitType(InitType::Random).is_zero(),
+              "InitType::is_zero");
+        // MetadataCursor (metadata.rs:20-68): consecutive f32 byte ranges.
+        MetadataCursor c;
+        MatrixMetadata m0 = c.matrix(3, 5);
+        VectorMetadata v0 = c.vector(7);
+        MatrixMetadata m1 = c.matrix(0, 9);
+        CHECK(m0.byte_start == 0 && m0.byte_end == 60 && v0.byte_start == 60 &&
+                  v0.byte_end == 88 && m1.byte_start == 88 && m1.byte_end == 88 &&
+                  c.data_bytes() == 88,
+              "MetadataCursor ranges");
+        bool overflow = false;
+        try {
+            (void)c.matrix(SIZE_MAX / 2, 3);
+        } catch (const Error& e) {
+            overflow = e.status() == FORGE_EINVAL;
+        }
+        CHECK(overflow, "MetadataCursor element overflow refused");
+        // get_u32_uninit_buffer (runtime.rs:57-60) and Vector::equals through
+        // it (vector.rs:117-136), with the mismatch in the last element.
+        DeviceBufferU32 u = R.get_u32_uninit_buffer(5);
+        CHECK(u.len() == 5 && u.ptr() != nullptr, "get_u32_uninit_buffer");
+        CHECK(R.get_u32_uninit_buffer(0).is_empty(), "empty u32 buffer");
+        auto hv = uniform(3000, 21);
+        Vector a = R.vector_from_host(hv);
+        Vector b = R.vector_from_host(hv);
+        CHECK(a.equals(b, R), "equals on equal vectors");
+        hv[2999] += 1.0f;
+        Vector c2 = R.vector_from_host(hv);
+        CHECK(!a.equals(c2, R), "equals sees the last element");
+        forge_slice_u32 count = u.slice();
+        check(forge_compare_u32(R.raw(), nullptr, a.slice(), c2.slice(), 3000, count),
+              "compare_u32");
+        CHECK(u.to_host(R)[0] == 1u, "compare_u32 mismatch count");
+        // span_to_buffer_async (runtime.rs:184-186).
+        DeviceSpan sp = a.span(100, 250);
+        DeviceBuffer copy = R.span_to_buffer_async(sp);
+        std::vector<float> got(250);
+        check(forge_memcpy_d2h(R.raw(), got.data(), copy.slice(), 250), "copy to host");
+        auto want = b.to_host(R);
+        CHECK(copy.len() == 250 && std::equal(got.begin(), got.end(), want.begin() + 100),
+              "span_to_buffer_async");
+        // with_loss constructors (mlp.rs:37-51, 180-184, 214-219).
+        auto lin = [&](size_t in, size_t out, uint64_t seed) {
+            return Linear(R.matrix_from_host(uniform(in * out, seed), in, out), std::nullopt,
+                          Activation::Identity);
+        };
+        std::vector<Linear> l1, l2, l3;
+        l1.push_back(lin(8, 16, 31));
+        l2.push_back(lin(8, 16, 32));
+        l3.push_back(lin(8, 16, 33));
+        MlpExecutor e = MlpExecutor::with_loss(std::move(l1), std::nullopt, Loss::MeanSquaredError);
+        InferenceMLP i = InferenceMLP::with_loss(std::move(l2), std::nullopt, Loss::MeanSquaredError);
+        TrainingMlp t = TrainingMlp::with_loss(std::move(l3), std::nullopt, Loss::MeanSquaredError);
+        CHECK(e.len() == 1 && e.loss() == Loss::MeanSquaredError &&
+                  i.loss() == Loss::MeanSquaredError && t.loss() == Loss::MeanSquaredError,
+              "with_loss constructors");
+        bool bad_range = false;
+        try {
+            std::vector<Linear> l4;
+            l4.push_back(lin(8, 8, 34));
+            (void)MlpExecutor::with_loss(std::move(l4), std::make_pair<size_t, size_t>(1, 1),
+                                         Loss::MeanSquaredError);
+        } catch (const Error& err) {
+            bad_range = err.status() == FORGE_EINVAL;
+        }
+        CHECK(bad_range, "with_loss refuses an empty residual range");
+        group("reference API members", f);
     }
 
     R.sync();

@@ -51,6 +51,12 @@ class Slice(ctypes.Structure):
 NULL_SLICE = Slice(None, 0)
 
 
+class SliceU32(ctypes.Structure):
+    """forge_slice_u32 {uint32_t *ptr; size_t len;}."""
+
+    _fields_ = [("ptr", c_void_p), ("len", c_size_t)]
+
+
 class GemmEpilogue(ctypes.Structure):
     """forge_gemm_epilogue."""
 
@@ -100,6 +106,9 @@ SIGNATURES = {
     "forge_free": [RT, Slice],
     "forge_reserve": [RT, c_size_t, c_size_t],
     "forge_pool_count": [RT, c_size_t, POINTER(c_size_t)],
+    "forge_alloc_u32": [RT, c_size_t, POINTER(SliceU32)],
+    "forge_free_u32": [RT, SliceU32],
+    "forge_memcpy_d2h_u32": [RT, c_void_p, SliceU32, c_size_t],
     "forge_memcpy_h2d": [RT, Slice, c_void_p, c_size_t],
     "forge_memcpy_d2h": [RT, c_void_p, Slice, c_size_t],
     "forge_memcpy_d2d": [RT, ST, Slice, Slice, c_size_t],
@@ -153,6 +162,7 @@ SIGNATURES = {
     "forge_sgd_update": [RT, ST, Slice, Slice, c_size_t, c_float],
     "forge_fill_random": [RT, ST, Slice, c_size_t, ctypes.c_uint32],
     "forge_compare": [RT, ST, Slice, Slice, c_size_t, Slice],
+    "forge_compare_u32": [RT, ST, Slice, Slice, c_size_t, SliceU32],
 }
 
 _RESTYPES = {"forge_status_string": c_char_p, "forge_last_error": c_char_p}

@@ -94,7 +94,8 @@ def dispatcher_kernel_names():
                "exp_shift", "half_sq", "identity"):
         names += [f"forge_map_{op}_v", f"forge_map_{op}_s", f"forge_map_sum_{op}"]
     names += ["forge_fill_random", "forge_act_backward_v", "forge_act_backward_s",
-              "forge_count_neq", "forge_count_final", "forge_sgd_v", "forge_sgd_s"]
+              "forge_count_neq", "forge_count_final", "forge_count_neq_u32",
+              "forge_count_final_u32", "forge_sgd_v", "forge_sgd_s"]
     names += ["forge_fill_v", "forge_fill_s", "forge_fill_seq", "forge_causal_mask",
               "forge_sum_cols_v", "forge_sum_cols_s", "forge_sum_cols_final", "forge_sum_cols_final2",
               "forge_sum_cols_final_v", "forge_sum_cols_final2_v",
