@@ -132,6 +132,13 @@ forge_status forge_streams_join(forge_runtime *rt, size_t n,
 forge_status forge_stream_wait(forge_runtime *rt, forge_stream *waiter,
                                forge_stream *signaler);
 forge_status forge_stream_destroy(forge_runtime *rt, forge_stream *stream);
+/* Diagnostic (no reference counterpart): the length in floats of the
+ * scratch workspace the library holds for `stream` (NULL = primary), which
+ * multi-pass kernels (column sums, norm backward partial rows, split-K
+ * GEMMs, reductions) grow on first need; 0 if nothing on that stream has
+ * needed one.  Lets a test show that an entry point allocated nothing. */
+forge_status forge_stream_workspace_floats(forge_runtime *rt, forge_stream *stream,
+                                           size_t *floats);
 
 /* --------------------------------------------------------------- events */
 
@@ -372,10 +379,14 @@ forge_status forge_layer_norm_bwd_sgd(forge_runtime *rt, forge_stream *stream,
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  Same arguments, checks and results (bit-identical) as
  * forge_layer_norm_bwd; the dgamma/dbeta partial rows go to a device scratch
- * array of 2^21 floats (8 MiB) that each GPU holds until the process ends,
- * instead of the stream's workspace.  Shapes whose partial rows need more
- * are FORGE_EINVAL; at any row count, 16-byte-aligned rows with cols % 4 ==
- * 0 fit up to 2048 columns and other rows up to 1024.  The array is shared by every call
+ * array of 2,162,688 floats (8.25 MiB) that each GPU holds until the process
+ * ends, instead of the stream's workspace.  Shapes whose partial rows need
+ * more are FORGE_EINVAL.  The need grows with the number of partial rows,
+ * one per workgroup (16-byte-aligned rows with cols % 4 == 0 and cols <=
+ * 2048) or per wave (other rows) of a grid of at most one or two workgroups
+ * per CU ($OXFORGE_NORM_BWD_BLOCKS overrides it).  On a device of up to 256
+ * CUs (MI355X) without that override, every row count fits up to 2048
+ * columns for aligned rows and up to 1024 for others.  The array is shared by every call
  * on one GPU, from every runtime and stream: calls that overlap on one GPU
  * race and must be serialised by the caller.  Nothing in it needs to start
  * at zero (every partial row is written before it is read). */

@@ -1,7 +1,7 @@
 // noalloc_scratch.hip -- the device scratch of the no-allocation entry point
 // (forge_layer_norm_bwd_noalloc in include/oxforge.h).
 //
-// A file-scope device array of FORGE_NOALLOC_SCRATCH_FLOATS floats (8 MiB).
+// A file-scope device array of FORGE_NOALLOC_SCRATCH_FLOATS floats (8.25 MiB).
 // Every GPU that the library runs on holds its own copy until the process
 // ends; the HIP runtime places it when this code object is first used on
 // that device.  Host code never passes the array's name to a kernel (on the

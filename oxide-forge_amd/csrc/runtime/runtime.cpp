@@ -419,6 +419,15 @@ extern "C" forge_status forge_stream_destroy(forge_runtime* rt, forge_stream* s)
     return FORGE_OK;
 }
 
+extern "C" forge_status forge_stream_workspace_floats(forge_runtime* rt, forge_stream* s,
+                                                      size_t* floats) {
+    if (!rt || !floats) return fail(FORGE_EINVAL, "null argument");
+    if (s && std::find(rt->streams.begin(), rt->streams.end(), s) == rt->streams.end())
+        return fail(FORGE_EINVAL, "stream not owned by this runtime");
+    *floats = pick(rt, s)->ws.len;
+    return FORGE_OK;
+}
+
 // =================================================================== events
 
 struct forge_event {

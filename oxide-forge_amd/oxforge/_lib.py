@@ -106,6 +106,7 @@ SIGNATURES = {
     "forge_free": [RT, Slice],
     "forge_reserve": [RT, c_size_t, c_size_t],
     "forge_pool_count": [RT, c_size_t, POINTER(c_size_t)],
+    "forge_stream_workspace_floats": [RT, ST, POINTER(c_size_t)],
     "forge_alloc_u32": [RT, c_size_t, POINTER(SliceU32)],
     "forge_free_u32": [RT, SliceU32],
     "forge_memcpy_d2h_u32": [RT, c_void_p, SliceU32, c_size_t],
