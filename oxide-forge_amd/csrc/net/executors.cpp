@@ -664,7 +664,10 @@ void Attention::chunked_forward(const Matrix& q, const Matrix& k, const Matrix& 
     // attention.rs:359-387 one chunk of query rows at a time: the chunk's
     // scores (NT GEMM, scale fused), mask, softmax, then its rows of
     // P V + residual.  Each output row is the same sum as in the unchunked
-    // products.
+    // products while neither product is computed as K slices; a chunk's
+    // P V has few tiles and may be split over Sk (Sk >= 2048, see
+    // choose_splits) where the whole product is not, and then the rows agree
+    // to within rounding.
     const size_t S = q.rows(), Sk = k.rows(), D = q.cols(), H = v.cols();
     Matrix scores = rt.new_uninit_matrix(std::min(chunk, S), Sk);
     forge_gemm_epilogue ep = plain_epilogue();

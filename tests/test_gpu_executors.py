@@ -187,6 +187,30 @@ def test_query_chunked_attention_forward(rt, kind, chunk_rows):
     Tu.close()
 
 
+def test_query_chunked_attention_forward_with_split_products(rt):
+    """S = Sk = 8192 in chunks of 64 query rows: each chunk's P V ([64, 8192]
+    by [8192, 64], one output tile) is computed as K slices, the whole
+    product is not, so the chunked forward agrees with the unchunked one to
+    within rounding (1e-5 relative) rather than bit for bit, and matches the
+    f64 oracle (1e-4)."""
+    S, H, F, O = 8192, 64, 128, 48
+    say(f"chunked attention forward S={S} chunk=64 (split P.V)")
+    assert "split" in rt.gemm_kernel_name(64, H, S, fused=True)
+    assert "split" not in rt.gemm_kernel_name(S, H, S, fused=True)
+    p = make_params(S, H, F, O, 44, bias=True, affine=True, norm=net.LAYER)
+    X = synth.normal((S, H), 12)
+    Tc = net.Transformer(rt, p, S, H, F, O, net.LAYER, net.ENCODER_INFERENCE)
+    Tu = net.Transformer(rt, p, S, H, F, O, net.LAYER, net.ENCODER_INFERENCE)
+    Tc.set_score_bytes(64 * S * 4)
+    dX = rt.array(X)
+    yc, yu = Tc.forward(dX).numpy(), Tu.forward(dX).numpy()
+    Tc.close()
+    Tu.close()
+    assert rel(yc, yu) <= 1e-5
+    ref, _ = ex.transformer_forward(p, X, net.LAYER)
+    assert rel(yc, ref) <= TOL
+
+
 @pytest.mark.parametrize("S,chunk_rows", [(320, 64), (320, 128), (512, 192)])
 def test_query_chunked_attention_training_step(rt, S, chunk_rows):
     """Training with the score budget below seq x seq: the forward keeps no
