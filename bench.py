@@ -5,8 +5,10 @@ Headline (BASELINE.json metric, configs[2]): f32 GEMM C = A * B at
 M = N = K = 4096, TFLOP/s, with its fraction of the fp32-MFMA peak.  A "step"
 is one GEMM launch over inputs already resident in HBM; the timed region is
 bracketed by synchronisation and timed with HIP events on the stream the
-kernel runs on.  Secondary figures in the same JSON line: the 8192x1024x4096
-GEMM, the [8192,4096] transpose and the C2 row / elementwise kernels (GB/s,
+kernel runs on, and every figure is the median over five groups of
+back-to-back launches (time_launches).  Secondary figures in the same JSON
+line: the 8192x1024x4096 GEMM, the [8192,4096] transpose, the C2 row and
+elementwise kernels, the sum-reduce kernels and the column sums (GB/s,
 rotating over >= 512 MiB of buffers so the 256 MiB MALL cannot serve them),
 and the transformer executors when built.
 
@@ -47,15 +49,25 @@ def log(msg: str) -> None:
 SPIN_UP_S = 0.3
 
 
+TIMING_GROUPS = 5
+
+
 def time_launches(rt, fn, steps: int, warmup: int, stream=None) -> float:
-    """Average milliseconds of fn(i) over `steps` launches (events on stream).
+    """Milliseconds per launch of fn(i): the median over TIMING_GROUPS groups
+    of back-to-back launches (`steps` in all) of each group's mean, from HIP
+    events on `stream` recorded only at the group boundaries.
+
+    An event pair around every launch would add about 2.6 us of dispatch
+    idle per launch (measured on MI355X: C2 softmax 6.3 us back to back,
+    8.9 us event-bracketed; a 4096^3 GEMM 903 against 905 us), which is
+    half of a C2 kernel's time, so launches are timed in groups and the
+    median is taken over the groups.
 
     Warmup runs at least `warmup` launches and at least SPIN_UP_S seconds of
     the same work: the MI355X raises its clocks over the first tens of
     milliseconds of sustained load (a 4096^3 GEMM dispatch drops from about
     1.1-1.2 ms to 0.95 ms over its first ~20 launches, and to 0.90 ms in the
-    steady state), and the timed steps should see
-    the steady state."""
+    steady state), and the timed steps should see the steady state."""
     t0 = time.perf_counter()
     i = 0
     while i < warmup or time.perf_counter() - t0 < SPIN_UP_S:
@@ -64,16 +76,21 @@ def time_launches(rt, fn, steps: int, warmup: int, stream=None) -> float:
         if i % 8 == 0:
             rt.sync(stream)
     rt.sync(stream)
-    e0, e1 = rt.event(), rt.event()
-    rt.record(e0, stream)
-    for i in range(steps):
-        fn(i)
-    rt.record(e1, stream)
-    ms = rt.elapsed_ms(e0, e1)
+    groups = max(1, min(TIMING_GROUPS, steps))
+    bounds = [steps * g // groups for g in range(groups + 1)]
+    evs = [rt.event() for _ in range(groups + 1)]
+    rt.record(evs[0], stream)
+    for g in range(groups):
+        for i in range(bounds[g], bounds[g + 1]):
+            fn(i)
+        rt.record(evs[g + 1], stream)
     rt.sync(stream)
-    rt.event_destroy(e0)
-    rt.event_destroy(e1)
-    return ms / steps
+    per = sorted(rt.elapsed_ms(evs[g], evs[g + 1]) / (bounds[g + 1] - bounds[g])
+                 for g in range(groups))
+    for e in evs:
+        rt.event_destroy(e)
+    mid = groups // 2
+    return per[mid] if groups % 2 else 0.5 * (per[mid - 1] + per[mid])
 
 
 def load_traffic(kernel: str):
@@ -200,6 +217,7 @@ def secondary_rows(rt, steps, warmup, extended=True, min_launches=256):
     dgam, dbet = rt.empty((cols,)), rt.empty((cols,))
     rvec = rt.array(synth.normal((cols,), 6))
     rsum = rt.empty((rows,))
+    scalar = rt.empty((1,))
     cases = {
         "softmax_fwd": (2 * X, lambda i: rt.softmax_rows(xs[i % sets], rows, cols)),
         "layer_norm_fwd": (2 * X, lambda i: rt.layer_norm(xs[i % sets], rows, cols, gam, bet)),
@@ -217,19 +235,27 @@ def secondary_rows(rt, steps, warmup, extended=True, min_launches=256):
         "by_rows_add": (2 * X, lambda i: rt.binary_assign_by_rows(ds[i % sets], rvec, rows, cols,
                                                                   oxforge.ADD)),
         "sum_rows": (X, lambda i: rt.sum_rows(xs[i % sets], rsum, rows, cols)),
+        # The configs[1] sum-reduce kernels over the whole of X as one
+        # vector (reduction.rs:4-130 via span.rs:301-411): sum, max and the
+        # map_sum of a functor (0.5 x^2, the MSE loss's), each into one
+        # device scalar; and the column sums of the bias gradients.
+        "reduce_sum": (X, lambda i: rt.reduce_sum(xs[i % sets], scalar)),
+        "reduce_max": (X, lambda i: rt.reduce_max(xs[i % sets], scalar)),
+        "map_sum_half_sq": (X, lambda i: rt.map_sum(xs[i % sets], scalar, oxforge.MAP_HALF_SQ)),
+        "sum_cols": (X, lambda i: rt.sum_cols(xs[i % sets], dgam, rows, cols)),
     }
     if extended:
         cases["map_gelu"] = (2 * X, lambda i: rt.map(ds[i % sets], oxforge.MAP_GELU))
-        cases["sum_cols"] = (X, lambda i: rt.sum_cols(xs[i % sets], dgam, rows, cols))
-    # Each launch is a few microseconds: time at least 256 of them, so the
-    # one-off idle gap before the first launch reaches the emptied queue
-    # (host launch latency after the synchronisation) is amortised.
+    # Each launch is a few microseconds: time at least 256 of them (groups of
+    # about 51), so the one-off idle gap before each group's first launch
+    # reaches the emptied queue (host launch latency after the
+    # synchronisation) and the group's boundary event are amortised.
     for name, (nbytes, fn) in cases.items():
         ms = time_launches(rt, fn, max(steps, min_launches), warmup)
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[f"{name}_4096x1024"] = {"gbs": round(gbs, 1), "us": round(ms * 1e3, 2),
                                     "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}
-    for b in xs + gs + ds:
+    for b in xs + gs + ds + [scalar, rsum]:
         b.recycle()
     return out
 
