@@ -488,18 +488,65 @@ __device__ __forceinline__ void sum_rows_body(const float* __restrict__ m,
     }
 }
 
-// Block-level reduction to one value per workgroup (partials), grid-stride.
-// IS_MAX selects max with identity -FLT_MAX (reduction.rs:93-130) instead of
-// the sum (reduction.rs:4-41).
-template <bool IS_MAX>
-__device__ __forceinline__ void reduce_body(const float* __restrict__ x, long long n,
+// Block-level reduction to one value per workgroup (partials), grid-stride:
+// the sum (reduction.rs:4-41), the max with identity -FLT_MAX
+// (reduction.rs:93-130), or the sum of a map functor's values
+// (slice_map_sum, reduction.rs:43-91).  With VEC (x 16-byte aligned) each
+// lane keeps RED_UNROLL float4 loads in flight per step, one per grid
+// stride, with one accumulator each (a lane's four floats fold in x, y, z,
+// w order); the accumulators fold in order, then the wave and the
+// workgroup.  Without VEC, one float per step.  The order depends only on n
+// and the grid, so results are deterministic.
+constexpr int RED_UNROLL = 4;
+
+template <int OP, bool IS_MAX>
+__device__ __forceinline__ float red_fold(float acc, float v, float p0) {
+    if constexpr (IS_MAX) return fmaxf(acc, v);
+    else return acc + map_one<OP>(v, p0);
+}
+
+template <int OP, bool IS_MAX, bool VEC>
+__device__ __forceinline__ void reduce_body(const float* __restrict__ x, long long n, float p0,
                                             float* __restrict__ out) {
     __shared__ float part[EW_THREADS / 64];
     const long long tid = (long long)blockIdx.x * EW_THREADS + threadIdx.x;
     const long long stride = (long long)gridDim.x * EW_THREADS;
-    float acc = IS_MAX ? -FLT_MAX : 0.0f;
-    for (long long i = tid; i < n; i += stride)
-        acc = IS_MAX ? fmaxf(acc, x[i]) : acc + x[i];
+    constexpr float ident = IS_MAX ? -FLT_MAX : 0.0f;
+    float acc = ident;
+    if constexpr (VEC) {
+        const long long n4 = n / 4;
+        float a[RED_UNROLL];
+#pragma unroll
+        for (int u = 0; u < RED_UNROLL; u++) a[u] = ident;
+        long long i = tid;
+        // Steps whose RED_UNROLL loads are all in range: loads first, then
+        // the folds.
+        for (; i + (RED_UNROLL - 1) * stride < n4; i += RED_UNROLL * stride) {
+            float4 v[RED_UNROLL];
+#pragma unroll
+            for (int u = 0; u < RED_UNROLL; u++) v[u] = load_stream(x + 4 * (i + u * stride));
+#pragma unroll
+            for (int u = 0; u < RED_UNROLL; u++) {
+                a[u] = red_fold<OP, IS_MAX>(a[u], v[u].x, p0);
+                a[u] = red_fold<OP, IS_MAX>(a[u], v[u].y, p0);
+                a[u] = red_fold<OP, IS_MAX>(a[u], v[u].z, p0);
+                a[u] = red_fold<OP, IS_MAX>(a[u], v[u].w, p0);
+            }
+        }
+        for (; i < n4; i += stride) {
+            const float4 v = load_stream(x + 4 * i);
+            a[0] = red_fold<OP, IS_MAX>(a[0], v.x, p0);
+            a[0] = red_fold<OP, IS_MAX>(a[0], v.y, p0);
+            a[0] = red_fold<OP, IS_MAX>(a[0], v.z, p0);
+            a[0] = red_fold<OP, IS_MAX>(a[0], v.w, p0);
+        }
+        for (long long j = n4 * 4 + tid; j < n; j += stride) a[0] = red_fold<OP, IS_MAX>(a[0], x[j], p0);
+        acc = a[0];
+#pragma unroll
+        for (int u = 1; u < RED_UNROLL; u++) acc = IS_MAX ? fmaxf(acc, a[u]) : acc + a[u];
+    } else {
+        for (long long i = tid; i < n; i += stride) acc = red_fold<OP, IS_MAX>(acc, x[i], p0);
+    }
     acc = IS_MAX ? wave_max(acc) : wave_sum(acc);
     const int wave = threadIdx.x >> 6;
     if (lane_id() == 0) part[wave] = acc;
@@ -508,27 +555,6 @@ __device__ __forceinline__ void reduce_body(const float* __restrict__ x, long lo
         float t = part[0];
         for (int w = 1; w < (EW_THREADS >> 6); w++)
             t = IS_MAX ? fmaxf(t, part[w]) : t + part[w];
-        out[blockIdx.x] = t;
-    }
-}
-
-// slice_map_sum (reduction.rs:43-91): per-workgroup partial sums of f(x)
-// for one of the map functors, in the reduce_body order; the partials are
-// then summed by reduce_body.
-template <int OP>
-__device__ __forceinline__ void map_sum_body(const float* __restrict__ x, long long n, float p0,
-                                             float* __restrict__ out) {
-    __shared__ float part[EW_THREADS / 64];
-    const long long tid = (long long)blockIdx.x * EW_THREADS + threadIdx.x;
-    const long long stride = (long long)gridDim.x * EW_THREADS;
-    float acc = 0.0f;
-    for (long long i = tid; i < n; i += stride) acc += map_one<OP>(x[i], p0);
-    acc = wave_sum(acc);
-    if (lane_id() == 0) part[threadIdx.x >> 6] = acc;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float t = part[0];
-        for (int w = 1; w < (EW_THREADS >> 6); w++) t += part[w];
         out[blockIdx.x] = t;
     }
 }

@@ -168,7 +168,13 @@ BINARY_KERNELS(div, OP_DIV)
 
 #define MAP_SUM_KERNEL(OPNAME, OP)                                                    \
     FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_map_sum_##OPNAME(              \
-        const float* x, long long n, float p0, float* out) { map_sum_body<OP>(x, n, p0, out); }
+        const float* x, long long n, float p0, float* out) {                           \
+        reduce_body<OP, false, false>(x, n, p0, out);                                  \
+    }                                                                                  \
+    FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_map_sum_##OPNAME##_v(          \
+        const float* x, long long n, float p0, float* out) {                           \
+        reduce_body<OP, false, true>(x, n, p0, out);                                   \
+    }
 #define MAP_KERNELS_ALL(OPNAME, OP) MAP_KERNELS(OPNAME, OP) MAP_SUM_KERNEL(OPNAME, OP)
 
 MAP_KERNELS_ALL(scale, MAP_SCALE)
@@ -275,10 +281,18 @@ FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_sum_rows_s(const float* m,
     sum_rows_body<false>(m, out, rows, cols);
 }
 FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_reduce_sum(const float* x, long long n, float* out) {
-    reduce_body<false>(x, n, out);
+    reduce_body<MAP_IDENTITY, false, false>(x, n, 0.0f, out);
 }
 FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_reduce_max(const float* x, long long n, float* out) {
-    reduce_body<true>(x, n, out);
+    reduce_body<MAP_IDENTITY, true, false>(x, n, 0.0f, out);
+}
+FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_reduce_sum_v(const float* x, long long n,
+                                                                   float* out) {
+    reduce_body<MAP_IDENTITY, false, true>(x, n, 0.0f, out);
+}
+FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_reduce_max_v(const float* x, long long n,
+                                                                   float* out) {
+    reduce_body<MAP_IDENTITY, true, true>(x, n, 0.0f, out);
 }
 FORGE_KERNEL void __launch_bounds__(256) forge_transpose_w(const float* in, float* out, int rows, int cols) {
     transpose_body<256, false>(in, out, rows, cols);

@@ -1642,22 +1642,40 @@ extern "C" forge_status forge_sum_cols_sgd(forge_runtime* rt, forge_stream* s, f
 }
 
 namespace {
+// Full reduction of x [n] into out[0]: per-workgroup partials of `kernel`
+// (with "_v" appended when x is 16-byte aligned: RED_UNROLL float4 per lane
+// per step), then one workgroup of `final_kernel` over the partials.  args0
+// is the functor's scalar for map_sum kernels (has_p0).
+forge_status reduce_launch(forge_runtime* rt, forge_stream* s, forge_slice x, size_t n,
+                           forge_slice out, const char* kernel, const char* final_kernel,
+                           bool has_p0, float p0) {
+    FORGE_TRY(need(x, n, "reduce x"));
+    FORGE_TRY(need(out, 1, "reduce out"));
+    const bool vec = aligned16(x.ptr);
+    char name[64], fin[64];
+    snprintf(name, sizeof name, "%s%s", kernel, vec ? "_v" : "");
+    snprintf(fin, sizeof fin, "%s_v", final_kernel);
+    long long nn = (long long)n;
+    // VEC: RED_UNROLL (4) float4 per lane in flight; scalar: 4 floats per lane.
+    const unsigned g = grid_for(vec ? (nn + 3) / 4 : nn, EW_THREADS * 4, 1024);
+    auto run = [&](const char* k, unsigned grid, const float* src, long long cnt, float* dst) {
+        if (has_p0) return launch_args(rt, s, k, dim3(grid), dim3(EW_THREADS), 0, src, cnt, p0, dst);
+        return launch_args(rt, s, k, dim3(grid), dim3(EW_THREADS), 0, src, cnt, dst);
+    };
+    if (g == 1) return run(name, 1, (const float*)x.ptr, nn, out.ptr);
+    float* ws;
+    FORGE_TRY(workspace(rt, s, g, &ws));
+    FORGE_TRY(run(name, g, (const float*)x.ptr, nn, ws));
+    // The partials (aligned workspace) fold with the plain sum or max.
+    long long gn = g;
+    return launch_args(rt, s, fin, dim3(1), dim3(EW_THREADS), 0, (const float*)ws, gn, out.ptr);
+}
+
 forge_status reduce_impl(forge_runtime* rt, forge_stream* s, forge_slice x, size_t n,
                          forge_slice out, bool is_max) {
     if (!rt) return fail(FORGE_EINVAL, "runtime is null");
-    FORGE_TRY(need(x, n, "reduce x"));
-    FORGE_TRY(need(out, 1, "reduce out"));
     const char* name = is_max ? "forge_reduce_max" : "forge_reduce_sum";
-    long long nn = (long long)n;
-    unsigned g = grid_for(nn, EW_THREADS * 4, 1024);
-    if (g == 1)
-        return launch_args(rt, s, name, dim3(1), dim3(EW_THREADS), 0, (const float*)x.ptr, nn,
-                           out.ptr);
-    float* ws;
-    FORGE_TRY(workspace(rt, s, g, &ws));
-    FORGE_TRY(launch_args(rt, s, name, dim3(g), dim3(EW_THREADS), 0, (const float*)x.ptr, nn, ws));
-    long long gn = g;
-    return launch_args(rt, s, name, dim3(1), dim3(EW_THREADS), 0, (const float*)ws, gn, out.ptr);
+    return reduce_launch(rt, s, x, n, out, name, name, false, 0.0f);
 }
 }  // namespace
 
@@ -1666,22 +1684,9 @@ extern "C" forge_status forge_map_sum(forge_runtime* rt, forge_stream* s, forge_
     if (!rt) return fail(FORGE_EINVAL, "runtime is null");
     const char* nm = map_name(op);
     if (!nm) return fail(FORGE_EINVAL, "unknown map op %d", (int)op);
-    FORGE_TRY(need(x, n, "map_sum x"));
-    FORGE_TRY(need(out, 1, "map_sum out"));
     char name[64];
     snprintf(name, sizeof name, "forge_map_sum_%s", nm);
-    long long nn = (long long)n;
-    unsigned g = grid_for(nn, EW_THREADS * 4, 1024);
-    if (g == 1)
-        return launch_args(rt, s, name, dim3(1), dim3(EW_THREADS), 0, (const float*)x.ptr, nn, p0,
-                           out.ptr);
-    float* ws;
-    FORGE_TRY(workspace(rt, s, g, &ws));
-    FORGE_TRY(launch_args(rt, s, name, dim3(g), dim3(EW_THREADS), 0, (const float*)x.ptr, nn, p0,
-                          ws));
-    long long gn = g;
-    return launch_args(rt, s, "forge_reduce_sum", dim3(1), dim3(EW_THREADS), 0, (const float*)ws,
-                       gn, out.ptr);
+    return reduce_launch(rt, s, x, n, out, name, "forge_reduce_sum", true, p0);
 }
 
 extern "C" forge_status forge_reduce_sum(forge_runtime* rt, forge_stream* s, forge_slice x,

@@ -92,7 +92,8 @@ def dispatcher_kernel_names():
                 names.append(f"forge_{k}_{op}_{s}")
     for op in ("scale", "add", "gelu", "gelu_d", "relu", "relu_d", "silu", "silu_d",
                "exp_shift", "half_sq", "identity"):
-        names += [f"forge_map_{op}_v", f"forge_map_{op}_s", f"forge_map_sum_{op}"]
+        names += [f"forge_map_{op}_v", f"forge_map_{op}_s", f"forge_map_sum_{op}",
+                  f"forge_map_sum_{op}_v"]
     names += ["forge_fill_random", "forge_act_backward_v", "forge_act_backward_s",
               "forge_count_neq", "forge_count_final", "forge_count_neq_u32",
               "forge_count_final_u32", "forge_sgd_v", "forge_sgd_s"]
@@ -100,6 +101,7 @@ def dispatcher_kernel_names():
               "forge_sum_cols_v", "forge_sum_cols_s", "forge_sum_cols_final", "forge_sum_cols_final2",
               "forge_sum_cols_final_v", "forge_sum_cols_final2_v",
               "forge_sum_rows_v", "forge_sum_rows_s", "forge_reduce_sum", "forge_reduce_max",
+              "forge_reduce_sum_v", "forge_reduce_max_v",
               "forge_transpose", "forge_transpose_w", "forge_transpose_g"]
     return names
 

@@ -686,6 +686,24 @@ def test_reduce_sum_max(rt, n):
     assert out.numpy()[0] == x.max()
 
 
+@pytest.mark.parametrize("n", [5, 4096 * 1024 + 1])
+def test_reduce_sum_max_unaligned_view(rt, n):
+    """The scalar reduction path: a view that starts one float past a
+    16-byte boundary (integer values, so every order is exact)."""
+    say(f"reduce unaligned view n={n}")
+    x = np.random.default_rng(n).integers(-1000, 1001, n).astype(np.float32)
+    base = rt.empty((n + 1,))
+    dx = base.view(1, (n,))
+    dx.upload(x)
+    out = rt.empty((1,))
+    rt.reduce_sum(dx, out)
+    assert out.numpy()[0] == float(x.astype(np.int64).sum())
+    rt.reduce_max(dx, out)
+    assert out.numpy()[0] == x.max()
+    rt.map_sum(dx, out, oxforge.MAP_IDENTITY)
+    assert out.numpy()[0] == float(x.astype(np.int64).sum())
+
+
 @pytest.mark.parametrize("op,p0", EXACT_MAPS + TRANS_MAPS)
 @pytest.mark.parametrize("n", [0, 1, 1001, 4096 * 1024 + 3])
 def test_map_sum(rt, op, p0, n):
