@@ -137,3 +137,42 @@ def rms_norm_backward(x, dy, gamma, eps=1e-5, register=False):
     if register:
         return _fma(x, np.broadcast_to(-c[:, None], x.shape), gi)
     return (gi - (x * c[:, None]).astype(f)).astype(f)
+
+
+def layer_norm_xhat(x, eps=1e-5, register=False):
+    """The f32 xhat = (x - mean) * r of each row, as the kernels form it (the
+    value their dgamma terms multiply)."""
+    x = np.asarray(x, f)
+    rows, n = x.shape
+    nf = f(n)
+    if register:
+        X = _groups(x)
+        ok = _groups(np.ones_like(x)) > 0
+        mean = (wave_sum(_lanes(_sum4(X))) / nf).astype(f)[:, None, None, None]
+        D = np.where(ok, (X - mean).astype(f), f(0))
+        q = wave_sum(_lanes(_sum4((D * D).astype(f))))
+    else:
+        mean = (wave_sum(_lanes_loop(x)) / nf).astype(f)[:, None]
+        D = (x - mean).astype(f)
+        q = wave_sum(_lanes_loop((D * D).astype(f)))
+    r = (f(1) / np.sqrt(((q / nf).astype(f) + f(eps)).astype(f)).astype(f)).astype(f)
+    if register:
+        return _ungroup((D * r[:, None, None, None]).astype(f), n)
+    return (D * r[:, None]).astype(f)
+
+
+def rms_norm_inv(x, eps=1e-5, register=False):
+    """The f32 inv = 1 / sqrt(sum x^2 / n + eps) of each row, as the backward
+    kernels form it."""
+    x = np.asarray(x, f)
+    n = x.shape[1]
+    nf = f(n)
+    if register:
+        X = _groups(x)
+        qq = (_fma(X[..., 0], X[..., 0], (X[..., 1] * X[..., 1]).astype(f))
+              + _fma(X[..., 2], X[..., 2], (X[..., 3] * X[..., 3]).astype(f))).astype(f)
+        q = wave_sum(_lanes(qq))
+    else:
+        q = wave_sum(_lanes_loop((x * x).astype(f)))
+    rms = np.sqrt(((q / nf).astype(f) + f(eps)).astype(f)).astype(f)
+    return (f(1) / rms).astype(f)

@@ -129,3 +129,189 @@ def tolerance(bound, bar=1e-5):
     """Per-element tolerance: the fixed bar, or SAFETY times the bound where
     that is larger."""
     return np.maximum(bar, SAFETY * bound)
+
+
+# ------------------------------------------------------------ column sums
+# dgamma = sum over rows of dy * xhat (RMSNorm: dy * x * inv) and dbeta =
+# sum of dy (the gamma/beta extension of row.rs:239-347, 398-468) are column
+# sums of `rows` terms, taken by the norm backward kernels in a fixed tree:
+#   1. each wave walks its rows grid-stride and accumulates every column in a
+#      register chain (register path: a fused multiply-add per dgamma term;
+#      looping path: the product, then the add);
+#   2. the register path adds its workgroup's waves in LDS, wave 0 first;
+#      the looping path keeps one partial row per wave;
+#   3. a final pass sums the partial rows (a further chunked pass first when
+#      there are more than 512 of them).
+# The bound is the running error bound of that tree: every rounded addition
+# contributes at most u |s| for its exact result s (a first-order bound,
+# Higham, "Accuracy and Stability of Numerical Algorithms", 2nd ed., 4.2),
+# plus each term's own error, which a sum passes on unchanged.  norm_bwd_plan
+# restates the host's choice of grid (runtime.cpp row_launch, sum_cols_impl)
+# so the tree is the one the kernels run.
+
+def norm_bwd_plan(rows, cols, cu_count, layer, aligned=True):
+    """Grid of the dgamma/dbeta partial pass: 'reg' (one partial row per
+    workgroup of `waves` waves) or 'loop' (one per wave of four)."""
+    vpt = 0
+    if aligned and cols % 4 == 0 and cols > 0:
+        for v in (1, 2, 4, 8, 16):
+            if cols <= 256 * v:
+                vpt = v
+                break
+    if vpt > 8:
+        vpt = 0
+    p4 = vpt == 4 and rows >= 256 * cu_count
+    waves = (4 if p4 else 8) if vpt else 4
+    per_cu = 2 if (p4 and layer) else 1
+    grid = min(-(-rows // waves), max(64, cu_count) * per_cu)
+    return {"kind": "reg" if vpt else "loop", "grid": grid, "waves": waves,
+            "partial_rows": grid if vpt else grid * 4}
+
+
+def _sum_cols_chunks(rows, cols, vec):
+    if rows <= 512:
+        return 1
+    per_block = 256 if vec else 64
+    gx = -(-cols // per_block)
+    want = max(1, 8192 // max(1, gx))
+    by_rows = -(-rows // 16)
+    return max(2, min(want, by_rows, 512))
+
+
+def _chains(T, n_chains, first_rounds):
+    """Grid-stride chains: chain c sums rows c, c + n_chains, ... of T
+    [rows, cols] in order.  Returns (the chains' exact sums [n_chains, cols],
+    the sum over every rounded step of |partial sum|); the first step of a
+    chain rounds only when first_rounds (a fused multiply-add from 0)."""
+    rows, cols = T.shape
+    a = -(-rows // n_chains)
+    P = np.zeros((a * n_chains, cols))
+    P[:rows] = T
+    valid = np.zeros(a * n_chains, bool)
+    valid[:rows] = True
+    S = np.cumsum(P.reshape(a, n_chains, cols), axis=0)
+    mask = valid.reshape(a, n_chains)
+    if not first_rounds:
+        mask = mask.copy()
+        mask[0] = False
+    err = (np.abs(S) * mask[:, :, None]).sum(axis=(0, 1))
+    return S[-1], err
+
+
+def _final_pass(Pm, vec):
+    """sum_cols_final_v (64 slots of rows s, s + 64, ..., then a halving
+    tree) or sum_cols_final (16 waves of rows w, w + 16, ..., then waves in
+    order) over Pm [rows, cols]: (sums, sum of |partial sums|)."""
+    slots = 64 if vec else 16
+    S, err = _chains(Pm, slots, False)
+    if vec:
+        st = slots // 2
+        while st:
+            S = S[:st] + S[st:2 * st]
+            err = err + np.abs(S).sum(axis=0)
+            st //= 2
+        return S[0], err
+    C = np.cumsum(S, axis=0)
+    return C[-1], err + np.abs(C[1:]).sum(axis=0)
+
+
+def column_sum_bound(T, exact, plan, out_aligned=True, fma=False):
+    """Bound on |computed - exact column sums| when the kernels sum the
+    terms T [rows, cols] (f64 values of the f32 terms they form) in the tree
+    of `plan`: |sum(T - exact)| (the terms' own error, exact) plus u times
+    every rounded partial sum.  fma: each term is formed inside a fused
+    multiply-add (register path), so a chain's first step rounds too.
+    out_aligned: the outputs are 16-byte aligned (float4 final pass)."""
+    T = np.asarray(T, np.float64)
+    waves_total = plan["grid"] * plan["waves"]
+    L1, err = _chains(T, waves_total, fma and plan["kind"] == "reg")
+    if plan["kind"] == "reg":
+        W = plan["waves"]
+        C = np.cumsum(L1.reshape(plan["grid"], W, -1), axis=1)
+        err = err + np.abs(C[:, 1:]).sum(axis=(0, 1))
+        Pm = C[:, -1]
+    else:
+        Pm = L1
+    # The partial rows sit in aligned scratch: the chunk pass is float4 when
+    # cols % 4 == 0; the final pass also needs aligned outputs.
+    vec = T.shape[1] % 4 == 0
+    prow = Pm.shape[0]
+    chunks = _sum_cols_chunks(prow, T.shape[1], vec)
+    if chunks > 1:
+        rpc = -(-prow // chunks)
+        chunks = -(-prow // rpc)
+        parts = []
+        for y in range(chunks):
+            blk = Pm[y * rpc:(y + 1) * rpc]
+            S, e1 = _chains(blk, 4, False)
+            C = np.cumsum(S, axis=0)
+            err = err + e1 + np.abs(C[1:]).sum(axis=0)
+            parts.append(C[-1])
+        Pm = np.array(parts)
+    _, e2 = _final_pass(Pm, vec and out_aligned)
+    return np.abs((T - np.asarray(exact, np.float64)).sum(axis=0)) + U * (err + e2)
+
+
+def sum_cols_bound(m, aligned=True):
+    """Bound on forge_sum_cols of m [rows, cols] (exact f32 inputs): the
+    chunked first pass when rows > 512, then the final pass."""
+    T = np.asarray(m, np.float64)
+    rows, cols = T.shape
+    vec = aligned and cols % 4 == 0
+    err = np.zeros(cols)
+    Pm = T
+    chunks = _sum_cols_chunks(rows, cols, vec)
+    if chunks > 1:
+        rpc = -(-rows // chunks)
+        parts = []
+        for r0 in range(0, rows, rpc):
+            S, e1 = _chains(T[r0:r0 + rpc], 4, False)
+            C = np.cumsum(S, axis=0)
+            err = err + e1 + np.abs(C[1:]).sum(axis=0)
+            parts.append(C[-1])
+        Pm = np.array(parts)
+    _, e2 = _final_pass(Pm, vec)
+    return U * (err + e2)
+
+
+def layer_norm_param_bounds(x, dy, cu_count, eps=1e-5, aligned=True, out_aligned=True):
+    """Bounds on the kernels' dgamma = sum dy xhat and dbeta = sum dy: the
+    terms use the kernels' own f32 xhat (f32rows.layer_norm_xhat), whose
+    difference from the exact xhat enters exactly."""
+    import f32rows
+
+    x32 = np.asarray(x, np.float32)
+    dy = np.asarray(dy, np.float32).astype(np.float64)
+    rows, n = x32.shape
+    plan = norm_bwd_plan(rows, n, cu_count, True, aligned)
+    reg = plan["kind"] == "reg"
+    xh = f32rows.layer_norm_xhat(x32, eps, register=reg).astype(np.float64)
+    xd = x32.astype(np.float64)
+    mu = xd.mean(axis=1, keepdims=True)
+    exact_xh = (xd - mu) / np.sqrt(((xd - mu) ** 2).mean(axis=1, keepdims=True) + eps)
+    t = dy * xh
+    if not reg:
+        t = t.astype(np.float32).astype(np.float64)  # the product rounds before the add
+    bg = column_sum_bound(t, dy * exact_xh, plan, out_aligned, fma=True)
+    bb = column_sum_bound(dy, dy, plan, out_aligned)
+    return bg, bb
+
+
+def rms_norm_param_bound(x, dy, cu_count, eps=1e-5, aligned=True, out_aligned=True):
+    """Bound on the kernels' dgamma = sum dy (x inv), inv =
+    1/sqrt(sum x^2 / n + eps) per row, with the kernels' f32 inv and x inv."""
+    import f32rows
+
+    x32 = np.asarray(x, np.float32)
+    dy = np.asarray(dy, np.float32).astype(np.float64)
+    rows, n = x32.shape
+    plan = norm_bwd_plan(rows, n, cu_count, False, aligned)
+    reg = plan["kind"] == "reg"
+    inv = f32rows.rms_norm_inv(x32, eps, register=reg)
+    xi = (x32 * inv[:, None]).astype(np.float32).astype(np.float64)
+    xd = x32.astype(np.float64)
+    exact = xd / np.sqrt((xd * xd).mean(axis=1, keepdims=True) + eps)
+    t = dy * xi
+    if not reg:
+        t = t.astype(np.float32).astype(np.float64)
+    return column_sum_bound(t, dy * exact, plan, out_aligned, fma=True)

@@ -123,3 +123,93 @@ def test_planted_mistakes_exceed_tolerance(cols):
         gam, bet = synth.normal((cols,), 3, 1.0, 0.1), synth.normal((cols,), 4, 0.0, 0.1)
     for name, (wrong, ref, tol) in _planted(x, dy, gam, bet).items():
         assert (np.abs(wrong - ref) / tol).max() > 50, name
+
+
+def _tree_f32(T, plan, fma, out_aligned=True):
+    """The kernels' column-sum tree evaluated in f32 (the order of
+    rowbounds.column_sum_bound): wave chains (each step one rounding: a
+    fused multiply-add on the register path), the workgroup's waves in
+    order, the final pass's 64 slots and halving tree (or 16 waves in
+    order)."""
+    f = np.float32
+    T = np.asarray(T, np.float64)
+    rows, cols = T.shape
+    nw = plan["grid"] * plan["waves"]
+    a = -(-rows // nw)
+    pad = np.zeros((a * nw, cols))
+    pad[:rows] = T
+    pad = pad.reshape(a, nw, cols)
+    acc = np.zeros((nw, cols), f)
+    for k in range(a):
+        live = np.arange(nw) + k * nw < rows
+        new = (acc.astype(np.float64) + pad[k]).astype(f)  # one rounding per step
+        acc = np.where(live[:, None], new, acc)
+    if plan["kind"] == "reg":
+        acc = acc.reshape(plan["grid"], plan["waves"], cols)
+        t = acc[:, 0]
+        for w in range(1, plan["waves"]):
+            t = (t + acc[:, w]).astype(f)
+        acc = t
+    prow = acc.shape[0]
+    chunks = rb._sum_cols_chunks(prow, cols, cols % 4 == 0)
+    if chunks > 1:
+        # first pass: chunks of rpc rows, four waves of rows r0 + w, r0 + w + 4,
+        # ..., then the waves in order
+        rpc = -(-prow // chunks)
+        parts = []
+        for r0 in range(0, prow, rpc):
+            blk = acc[r0:r0 + rpc]
+            w4 = np.zeros((4, cols), f)
+            for r in range(blk.shape[0]):
+                w4[r % 4] = (w4[r % 4] + blk[r]).astype(f)
+            t = w4[0]
+            for w in range(1, 4):
+                t = (t + w4[w]).astype(f)
+            parts.append(t)
+        acc = np.array(parts)
+    vec = cols % 4 == 0 and out_aligned
+    slots = 64 if vec else 16
+    s = np.zeros((slots, cols), f)
+    for r in range(acc.shape[0]):
+        s[r % slots] = (s[r % slots] + acc[r]).astype(f)
+    if vec:
+        st = slots // 2
+        while st:
+            s = (s[:st] + s[st:2 * st]).astype(f)
+            st //= 2
+        return s[0]
+    t = s[0]
+    for w in range(1, slots):
+        t = (t + s[w]).astype(f)
+    return t
+
+
+@pytest.mark.parametrize("rows,cols,aligned", [(4096, 256, True), (600, 1001, False),
+                                               (70, 64, True)])
+def test_column_sum_bound_covers_f32_tree_and_catches_a_dropped_row(rows, cols, aligned):
+    """dgamma / dbeta bounds (rowbounds.layer_norm_param_bounds): the f32
+    evaluation of the kernels' summation tree over the kernels' own f32 xhat
+    lands inside the bound on every column, and a planted mistake (the last
+    row's terms left out) exceeds twice the bound."""
+    import f32rows
+
+    x = synth.normal((rows, cols), 5)
+    dy = synth.normal((rows, cols), 6)
+    cu = 256
+    bg, bb = rb.layer_norm_param_bounds(x, dy, cu, aligned=aligned)
+    plan = rb.norm_bwd_plan(rows, cols, cu, True, aligned)
+    reg = plan["kind"] == "reg"
+    xh = f32rows.layer_norm_xhat(x, register=reg).astype(np.float64)
+    t = dy.astype(np.float64) * xh
+    if not reg:
+        t = t.astype(np.float32).astype(np.float64)
+    _, rdg, rdb = orc.layer_norm_backward(x, dy, None, want_params=True)
+    got_g = _tree_f32(t, plan, True).astype(np.float64)
+    got_b = _tree_f32(dy, plan, False).astype(np.float64)
+    assert np.all(np.abs(got_g - rdg) <= bg)
+    assert np.all(np.abs(got_b - rdb) <= bb)
+    # the bound is a rounding bound, not a slack: a missing row is far outside
+    t2 = t.copy()
+    t2[-1] = 0.0
+    bad = _tree_f32(t2, plan, True).astype(np.float64)
+    assert np.any(np.abs(bad - rdg) > rb.SAFETY * bg)
