@@ -241,6 +241,30 @@ typedef struct forge_gemm_epilogue {
     int aux_activation;    /* 0: Z = Z * aux_mul; a forge_activation A:
                               Z = Z * A'(aux_mul), the derivative step of
                               Linear::backward (linear.rs:254-265)         */
+    /* Row statistics: a parameterless RMSNorm (norm.rs:50-69) of the rows
+     * of one product's result folded into the next product.  The divisor of
+     * row r is d_r = sqrt(S_r / row_n + row_eps), S_r the sum of the
+     * row_parts values row_parts_in[r * row_parts ...] (the row_sumsq_out of
+     * the product that formed those rows).  row_div bit 0: Z = Z / d_r right
+     * after alpha (op(A) op(B) with A's rows normalised equals the product
+     * of the raw rows divided by d_r); bit 1: the residual is divided by d_r
+     * before it is added.                                                  */
+    forge_slice row_parts_in; /* [M * row_parts] or {NULL,0}               */
+    size_t row_parts;
+    size_t row_n;
+    float row_eps;
+    int row_div;
+    /* [M * ceil(N / 32)] or {NULL,0}: for each row, the sums of the squares
+     * of the stored C values over each 32-column block.                    */
+    forge_slice row_sumsq_out;
+    /* [N] or {NULL,0}: the column sums of the stored C values (a bias
+     * gradient, linear.rs:267-272); col_sums_param ([N] or {NULL,0}) takes
+     * param -= col_sums_lr * sum (linear.rs:385-390) in the same pass.  The
+     * sums come from per-tile partials written by the product's epilogue and
+     * one final pass over them, in an order fixed by the shape.            */
+    forge_slice col_sums_out;
+    forge_slice col_sums_param;
+    float col_sums_lr;
 } forge_gemm_epilogue;
 
 forge_status forge_gemm_ex_f32(forge_runtime *rt, forge_stream *stream,
@@ -307,7 +331,8 @@ typedef struct forge_gemm_problem {
 
 /* `count` products of the same shape and transposes in one launch, each as
  * forge_gemm_ex_f32 would compute it (bit-identical; shapes that call splits
- * in K run one product at a time).  Replaces the three
+ * in K, and products with row statistics or column sums, run one product at
+ * a time).  Replaces the three
  * forked streams of the Q/K/V projections (attention.rs:65-94) and of their
  * weight updates (attention.rs:104-144): one launch fills the device without
  * the cross-queue event latency of a fork and join. */

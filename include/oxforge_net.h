@@ -128,6 +128,16 @@ forge_status forge_net_transformer_param(forge_net_model *m, int slot,
  * and the training step recomputes each chunk's probabilities in backward.
  * No counterpart in the reference, which always forms the whole matrix. */
 forge_status forge_net_transformer_set_score_bytes(forge_net_model *m, size_t bytes);
+/* InferenceBlock::set_fold_norms for the inference kinds: on (the default)
+ * folds the two parameterless RMSNorms (norm.rs:50-69 at inference.rs:90-108,
+ * attention.rs:243-253) into the products beside them (the producing
+ * product keeps each row's sums of squares, the consuming ones divide by the
+ * row's RMS); off runs the reference's launch order.  Applies when both
+ * norms are RMSNorm without gamma and the feed-forward network has no inner
+ * residual range; otherwise the reference order runs either way.  The
+ * training kind, which caches the normalised rows, is FORGE_EINVAL.  No
+ * counterpart in the reference. */
+forge_status forge_net_transformer_set_fold_norms(forge_net_model *m, int on);
 
 /* ------------------------------------------------------------ checkpoint */
 

@@ -752,6 +752,12 @@ public:
     Matrix forward_mask(const Matrix& query_input, const Matrix& key_value_input,
                         CudaRuntime& rt);
     Matrix forward_self_training(Matrix input, CudaRuntime& rt);
+    // The attention output before its norm (X + A, attention.rs:243-253),
+    // with row_sumsq [rows, ceil(cols / 32)] receiving each row's sums of
+    // squares over 32-column blocks (forge_gemm_epilogue row_sumsq_out), so
+    // that a parameterless RMSNorm can be folded into the next product.
+    Matrix forward_pre_norm(const Matrix& query_input, const Matrix& key_value_input, bool mask,
+                            Matrix& row_sumsq, CudaRuntime& rt);
     // With `input_gradient` given, the returned gradient is written there
     // (same shape as the attention input) and an empty Matrix is returned.
     Matrix backward_self(const Matrix& output_gradient, float learning_rate, CudaRuntime& rt,
@@ -772,11 +778,11 @@ public:
 
 private:
     Matrix attention_value(QkvProjection::Projected projected, const Matrix& residual, bool mask,
-                           CudaRuntime& rt);
+                           CudaRuntime& rt, Matrix* row_sumsq = nullptr);
     // out = softmax(scale Q K^T (masked)) V + residual in query chunks.
     void chunked_forward(const Matrix& q, const Matrix& k, const Matrix& v,
                          const Matrix& residual, bool mask, size_t chunk, Matrix& out,
-                         CudaRuntime& rt);
+                         CudaRuntime& rt, Matrix* row_sumsq = nullptr);
     struct Cache {
         Matrix input, query, key, value, probabilities, pre_norm;
     };
@@ -801,6 +807,18 @@ public:
     // extension, when present).
     TransformerMetadata get_meta_data(MetadataCursor& cursor) const;
     std::vector<HostData> get_data(CudaRuntime& rt) const;
+    // With both norms the reference's parameterless RMSNorm and a feed-forward
+    // network without an inner residual range, the forward folds each norm
+    // into the products on either side of it (on by default): the
+    // attention-value product and the last feed-forward layer also write the
+    // rows' sums of squares; the first feed-forward layer and the output
+    // projection divide their products by the rows' RMS, and the last layer
+    // divides its residual.  Two kernels and their launch boundaries go; the
+    // results agree with the reference's order (normalise, then multiply) to
+    // within rounding.  Off: the reference's launch order.
+    void set_fold_norms(bool on) { fold_norms_ = on; }
+    bool fold_norms() const { return fold_norms_; }
+    bool can_fold_norms() const;
     Attention& attention() { return attention_; }
     Normalization& norm2() { return norm2_; }
     Matrix& position() { return position_; }
@@ -809,11 +827,13 @@ public:
 
 private:
     Matrix finish_forward(Matrix positioned, Matrix x, CudaRuntime& rt, Matrix* target);
+    Matrix forward_folded(const Matrix& input, bool mask, CudaRuntime& rt, Matrix* target);
     Attention attention_;
     Matrix position_;
     InferenceMLP fcs_;
     Linear output_;
     Normalization norm2_;
+    bool fold_norms_ = true;
 };
 
 namespace encoder {

@@ -460,6 +460,36 @@ __device__ __forceinline__ void sum_cols_final_v_body(const float* __restrict__ 
     if (s == 0 && in) colsum_store4(o, c, part[0][q]);
 }
 
+// Row statistics of the GEMM epilogue where the product's own kernel does
+// not form them (the bounds-guarded and split-K paths).
+// d[r] = sqrt(sum of part[r, 0..parts) / n + eps), the partials added in
+// index order: the divisor the unguarded tiles form in their prologue.
+__device__ __forceinline__ void row_rms_parts_body(const float* __restrict__ part, int parts,
+                                                   int rows, int n, float eps,
+                                                   float* __restrict__ d) {
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    const float* p = part + (long long)r * parts;
+    float t = 0.0f;
+    for (int j = 0; j < parts; j++) t += p[j];
+    d[r] = sqrtf(t / (float)n + eps);
+}
+
+// out[r, b] = sum over the columns 32 b .. 32 b + 31 (< cols) of row r of
+// m [rows, ld] of the squares, in column order: row_sumsq_out from C.
+__device__ __forceinline__ void row_sq_parts_body(const float* __restrict__ m, long long ld,
+                                                  int rows, int cols, float* __restrict__ out) {
+    const int parts = (cols + 31) / 32;
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)rows * parts) return;
+    const int r = (int)(i / parts), b = (int)(i % parts);
+    const float* p = m + (long long)r * ld + 32 * b;
+    const int e = min(32, cols - 32 * b);
+    float q = 0.0f;
+    for (int c = 0; c < e; c++) q += p[c] * p[c];
+    out[i] = q;
+}
+
 // Row sums: one wave per row (row.rs:16-53).
 template <bool VEC>
 __device__ __forceinline__ void sum_rows_body(const float* __restrict__ m,

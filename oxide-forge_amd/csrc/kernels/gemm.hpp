@@ -49,7 +49,27 @@ struct GemmArgs {
     int aux_act;            // 0: Z *= aux; ACT_*: Z *= derivative of that act at aux
     int update;             // 0: C = act(Z); 1: C = C - update_scale * act(Z)
     float update_scale;
+    // Row statistics (the RMSNorm of a row folded across a GEMM boundary).
+    // The divisor of row r is d_r = sqrt(sum of row_parts values / row_n +
+    // row_eps): from row_part [M, row_parts] (partial sums of squares that
+    // another product's row_sq wrote), or given directly in row_d [M].
+    // row_div bit 0: Z = Z / d_r right after alpha; bit 1: the residual is
+    // divided by d_r before it is added.
+    const float* row_part;
+    const float* row_d;
+    int row_parts, row_n;
+    float row_eps;
+    int row_div;
+    // [M, N / 32] or null: the sum of the squares of the stored values over
+    // each 32-column block of each row (the unguarded tiles only).
+    float* row_sq;
+    // [M / TM, N] or null: the column sums of the stored values over each
+    // wave's TM rows (the unguarded tiles only; TM = the tile's rows per
+    // wave).
+    float* col_part;
 };
+// The host fills the same layout (runtime.cpp GemmArgs).
+static_assert(sizeof(GemmArgs) == 168, "kernel argument layout");
 
 constexpr int GEMM_GROUP_M = 8;
 constexpr int LDS_PAD = 4;
@@ -92,11 +112,13 @@ struct GemmBatchArgs {
 // row * ldc + col: alpha, bias, residual, aux multiply (or act'(aux)),
 // pre-activation store, activation, then store or SGD update.  Each step is
 // one rounded f32 operation in the reference's launch order.
-__device__ __forceinline__ void gemm_epilogue_store(const GemmArgs& p, long long idx, int col,
-                                                    float z) {
+__device__ __forceinline__ void gemm_epilogue_store(const GemmArgs& p, long long idx, int row,
+                                                    int col, float z) {
     if (p.alpha != 1.0f) z = p.alpha * z;
+    if (p.row_d && (p.row_div & 1)) z = z / p.row_d[row];
     if (p.bias) z = z + p.bias[col];
-    if (p.residual) z = z + p.residual[idx];
+    if (p.residual) z = z + ((p.row_d && (p.row_div & 2)) ? p.residual[idx] / p.row_d[row]
+                                                          : p.residual[idx]);
     if (p.aux) {
         const float m = p.aux_act ? activate_derivative(p.aux_act, p.aux[idx]) : p.aux[idx];
         z = z * m;
@@ -302,11 +324,20 @@ __device__ __forceinline__ void gemm_body_guarded(const GemmArgs& p, int logical
                 // order (alpha, bias, residual, aux, pre_out, activation, store
                 // or update) is that of gemm_epilogue_store.
                 if (p.alpha != 1.0f) FORGE_EPI_EACH(a[r] = p.alpha * a[r]);
+                if (p.row_d && (p.row_div & 1)) {
+                    FORGE_EPI_EACH(a[r] = a[r] / p.row_d[row]);
+                }
                 if (p.bias && col < p.N) {
                     const float b = p.bias[col];
                     FORGE_EPI_EACH(a[r] = a[r] + b);
                 }
-                if (p.residual) FORGE_EPI_EACH(a[r] = a[r] + EL(p.residual));
+                if (p.residual) {
+                    if (p.row_d && (p.row_div & 2)) {
+                        FORGE_EPI_EACH(a[r] = a[r] + EL(p.residual) / p.row_d[row]);
+                    } else {
+                        FORGE_EPI_EACH(a[r] = a[r] + EL(p.residual));
+                    }
+                }
                 if (p.aux) {
                     switch (p.aux_act) {
                     case ACT_GELU: FORGE_EPI_EACH_SEQ(a[r] = a[r] * gelu_derivative(EL(p.aux))); break;
@@ -378,7 +409,7 @@ __device__ __forceinline__ void splitk_reduce_body(const float* __restrict__ P, 
         }
 #pragma unroll
         for (int w = 0; w < W; w++)
-            gemm_epilogue_store(p, (long long)row * p.ldc + col0 + w, col0 + w, z[w]);
+            gemm_epilogue_store(p, (long long)row * p.ldc + col0 + w, row, col0 + w, z[w]);
     }
 }
 

@@ -310,11 +310,21 @@ __device__ __forceinline__ void x_epi_aux(int aux_act, float (&y)[4 * NB],
     }
 }
 
-template <bool EPI, int NB>
+// The row statistics of the fused epilogue.  rinv: 1 / d of each group's
+// row (formed by the workgroup in LDS from row_part); row: the group's
+// global row, for row_sq.
+template <int NB>
+struct XRowStats {
+    float rinv[NB];
+    int row[NB];
+};
+
+template <bool EPI, int NB, bool STATS = false>
 __device__ __forceinline__ void x_epi_store(const GemmArgs& p, const f4 (&z)[NB],
                                             const f4 (&res)[NB], const f4 (&mul)[NB],
                                             const f4 (&old)[NB], f4 bias,
-                                            const long long (&idx)[NB]) {
+                                            const long long (&idx)[NB], const XRowStats<NB>& rs,
+                                            int lane_col, float (&cs)[4]) {
     float y[4 * NB];
 #pragma unroll
     for (int u = 0; u < NB; u++) {
@@ -325,18 +335,37 @@ __device__ __forceinline__ void x_epi_store(const GemmArgs& p, const f4 (&z)[NB]
         if (p.alpha != 1.0f)
 #pragma unroll
             for (int i = 0; i < 4 * NB; i++) y[i] = p.alpha * y[i];
+        // RMSNorm folded across the boundary: (x / d_r) W = (x W) / d_r,
+        // taken as a product with 1 / d_r.
+        if constexpr (STATS) {
+            if (p.row_part && (p.row_div & 1))
+#pragma unroll
+                for (int i = 0; i < 4 * NB; i++) y[i] = y[i] * rs.rinv[i / 4];
+        }
         if (p.bias)
 #pragma unroll
             for (int u = 0; u < NB; u++) {
                 y[4 * u + 0] = y[4 * u + 0] + bias.x; y[4 * u + 1] = y[4 * u + 1] + bias.y;
                 y[4 * u + 2] = y[4 * u + 2] + bias.z; y[4 * u + 3] = y[4 * u + 3] + bias.w;
             }
-        if (p.residual)
+        if (p.residual) {
+            f4 r[NB];
+#pragma unroll
+            for (int u = 0; u < NB; u++) r[u] = res[u];
+            if constexpr (STATS) {
+                if (p.row_part && (p.row_div & 2))
+#pragma unroll
+                    for (int u = 0; u < NB; u++) {
+                        r[u].x = r[u].x * rs.rinv[u]; r[u].y = r[u].y * rs.rinv[u];
+                        r[u].z = r[u].z * rs.rinv[u]; r[u].w = r[u].w * rs.rinv[u];
+                    }
+            }
 #pragma unroll
             for (int u = 0; u < NB; u++) {
-                y[4 * u + 0] = y[4 * u + 0] + res[u].x; y[4 * u + 1] = y[4 * u + 1] + res[u].y;
-                y[4 * u + 2] = y[4 * u + 2] + res[u].z; y[4 * u + 3] = y[4 * u + 3] + res[u].w;
+                y[4 * u + 0] = y[4 * u + 0] + r[u].x; y[4 * u + 1] = y[4 * u + 1] + r[u].y;
+                y[4 * u + 2] = y[4 * u + 2] + r[u].z; y[4 * u + 3] = y[4 * u + 3] + r[u].w;
             }
+        }
         if (p.aux) {
             float m[4 * NB];
 #pragma unroll
@@ -360,6 +389,30 @@ __device__ __forceinline__ void x_epi_store(const GemmArgs& p, const f4 (&z)[NB]
                 y[4 * u + 2] = old[u].z - p.update_scale * y[4 * u + 2];
                 y[4 * u + 3] = old[u].w - p.update_scale * y[4 * u + 3];
             }
+        if (STATS && p.row_sq) {
+            // Sum of squares over each 32-column block of the row: the eight
+            // lanes of a block (consecutive lanes hold consecutive float4
+            // columns of one row) add their four squares, then a xor tree.
+            const int parts = p.N >> 5;
+#pragma unroll
+            for (int u = 0; u < NB; u++) {
+                float q = y[4 * u] * y[4 * u];
+                q = q + y[4 * u + 1] * y[4 * u + 1];
+                q = q + y[4 * u + 2] * y[4 * u + 2];
+                q = q + y[4 * u + 3] * y[4 * u + 3];
+                q = q + __shfl_xor(q, 1, 64);
+                q = q + __shfl_xor(q, 2, 64);
+                q = q + __shfl_xor(q, 4, 64);
+                if ((threadIdx.x & 7) == 0)
+                    p.row_sq[(long long)rs.row[u] * parts + (lane_col >> 5)] = q;
+            }
+        }
+        if (STATS && p.col_part)
+#pragma unroll
+            for (int u = 0; u < NB; u++) {
+                cs[0] = cs[0] + y[4 * u + 0]; cs[1] = cs[1] + y[4 * u + 1];
+                cs[2] = cs[2] + y[4 * u + 2]; cs[3] = cs[3] + y[4 * u + 3];
+            }
     }
     // Results are stored non-temporally, which measured faster than
     // write-allocating stores: C4 forward 0.5252 -> 0.5234 ms, C5 step
@@ -374,8 +427,10 @@ __device__ __forceinline__ void x_epi_store(const GemmArgs& p, const f4 (&z)[NB]
 #define FORGE_GEMM_MF 16
 #endif
 
-template <int BM, int BN, int BK, bool TA, bool TB, bool EPI, int WM = 2, int WN = 2>
+template <int BM, int BN, int BK, bool TA, bool TB, bool EPI, int WM = 2, int WN = 2,
+          bool STATS = false>
 __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
+    static_assert(EPI || !STATS, "row statistics ride on the fused epilogue");
     constexpr int NW = WM * WN;  // waves: WM x WN sub-tiles of TM x TN
     constexpr int TM = BM / WM, TN = BN / WN;
     // MFMA block: 16 x 16 (v_mfma_f32_16x16x4_f32, four k per instruction,
@@ -404,8 +459,10 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     constexpr int CP = TN + 4;
     constexpr int EPI_ELEMS = NW * TM * CP;
     constexpr int SMEM = 2 * STAGE > EPI_ELEMS ? 2 * STAGE : EPI_ELEMS;
-    static_assert(SMEM * 4 <= 160 * 1024, "LDS budget");
-    __shared__ __attribute__((aligned(1024))) float smem_all[SMEM];
+    // The fused epilogue's row scales (row_part) follow the stages.
+    constexpr int ROWD = STATS ? BM : 0;
+    static_assert((SMEM + ROWD) * 4 <= 160 * 1024, "LDS budget");
+    __shared__ __attribute__((aligned(1024))) float smem_all[SMEM + ROWD];
 
     const int num_m = p.M / BM, num_n = p.N / BN;
     int tm, tn;
@@ -474,6 +531,37 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     constexpr int NDMA = DMA_PER_STAGE;  // slab loads per stage
     constexpr int MF_PER_READ = NMFMA / 2 / NREAD > 0 ? NMFMA / 2 / NREAD : 1;
 
+    // Row scales of the folded RMSNorm (row_part): thread t < BM sums row
+    // m0 + t's row_parts partial sums in index order (float4 loads when
+    // row_parts % 4 == 0 and row_part is 16-byte aligned) and stores
+    // 1 / sqrt(sum / n + eps) to LDS.  The block completes before the first
+    // slab is requested: loads still in flight past it would make the launch
+    // wait for all its slab loads before the main loop.
+    if constexpr (STATS) {
+        if (p.row_part && (int)threadIdx.x < BM) {
+            const int parts = p.row_parts;
+            const float* row = p.row_part + (long long)(m0 + (int)threadIdx.x) * parts;
+            float t = 0.0f;
+            if ((parts & 3) == 0 && (reinterpret_cast<uintptr_t>(p.row_part) & 15) == 0) {
+                constexpr int RP_MAX = 8;  // float4 loads in flight per round
+                const f4* src = reinterpret_cast<const f4*>(row);
+                const int rp4 = parts >> 2;
+                for (int j0 = 0; j0 < rp4; j0 += RP_MAX) {
+                    f4 rp[RP_MAX];
+#pragma unroll
+                    for (int j = 0; j < RP_MAX; j++)
+                        if (j0 + j < rp4) rp[j] = src[j0 + j];
+#pragma unroll
+                    for (int j = 0; j < RP_MAX; j++)
+                        if (j0 + j < rp4) t = ((t + rp[j].x) + rp[j].y + rp[j].z) + rp[j].w;
+                }
+            } else {
+                for (int j = 0; j < parts; j++) t += row[j];
+            }
+            smem_all[SMEM + threadIdx.x] = 1.0f / sqrtf(t / (float)p.row_n + p.row_eps);
+        }
+    }
+
     // Prologue: slabs 0 and 1 in flight, slab 0 waited for (K = 0 reads
     // nothing and stores zeros).
     if (KT > 0) {
@@ -486,7 +574,6 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
         }
         frags(0, 0, 0);
     }
-
     // Slab kt lives in stage kt % 2; the loop handles two slabs per
     // iteration so that every stage (and so every LDS address offset) is a
     // constant.  A slab's last chunk is split: after the first half of its
@@ -609,27 +696,49 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     constexpr int ITER = TM * F4_ROW / 64;  // 128-bit groups per lane
     constexpr int NB = ITER < 4 ? ITER : 4;  // groups whose operands load together
     static_assert(ITER % NB == 0, "epilogue batches");
+    float cs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 1
     for (int b0 = 0; b0 < ITER; b0 += NB) {
         // Loads of a batch first, so NB global reads per operand are in
         // flight together.
         f4 z[NB], res[NB], mul[NB], old[NB];
         long long idx[NB];
+        XRowStats<NB> rs;
 #pragma unroll
         for (int u = 0; u < NB; u++) {
             const int q = lane + 64 * (b0 + u);
             const int rr = q / F4_ROW, c4 = q % F4_ROW;
             z[u] = *reinterpret_cast<const f4*>(cw + rr * CP + 4 * c4);
             idx[u] = (long long)(row0 + rr) * p.ldc + lane_col;
+            rs.row[u] = row0 + rr;
+            rs.rinv[u] = 1.0f;
+            if constexpr (STATS) {
+                if (p.row_part) rs.rinv[u] = smem_all[SMEM + a_off + rr];
+            }
             x_epi_load<EPI>(p, idx[u], res[u], mul[u], old[u]);
         }
-        x_epi_store<EPI, NB>(p, z, res, mul, old, bias4, idx);
+        x_epi_store<EPI, NB, STATS>(p, z, res, mul, old, bias4, idx, rs, lane_col, cs);
+    }
+    if constexpr (STATS) {
+        if (p.col_part) {
+            // Lanes l, l + F4_ROW, ... hold the same four columns: a xor tree
+            // over them, then lanes below F4_ROW store this wave's column sums
+            // over its TM rows as partial row tm * WM + wm.
+#pragma unroll
+            for (int off = F4_ROW; off < 64; off <<= 1)
+#pragma unroll
+                for (int c = 0; c < 4; c++) cs[c] = cs[c] + __shfl_xor(cs[c], off, 64);
+            if (lane < F4_ROW)
+                *reinterpret_cast<f4*>(p.col_part + (long long)(tm * WM + wm) * p.N + lane_col) =
+                    f4{cs[0], cs[1], cs[2], cs[3]};
+        }
     }
 }
 
-template <int BM, int BN, int BK, bool TA, bool TB, bool EPI, int WM = 2, int WN = 2>
+template <int BM, int BN, int BK, bool TA, bool TB, bool EPI, int WM = 2, int WN = 2,
+          bool STATS = false>
 __device__ __forceinline__ void gemm_single_x(const GemmArgs& p) {
-    gemm_body_x<BM, BN, BK, TA, TB, EPI, WM, WN>(p, xcd_logical(blockIdx.x, gridDim.x));
+    gemm_body_x<BM, BN, BK, TA, TB, EPI, WM, WN, STATS>(p, xcd_logical(blockIdx.x, gridDim.x));
 }
 
 template <int BM, int BN, int BK, bool TA, bool TB, int WM = 2, int WN = 2>

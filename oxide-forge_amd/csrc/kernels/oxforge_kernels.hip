@@ -43,6 +43,25 @@ GEMM_FAMILY(nt, false, true)
 GEMM_FAMILY(tn, true, false)
 GEMM_FAMILY(tt, true, true)
 
+// Row-statistics instances (forge_gemm_<ab>_<tile>_s): the fused epilogue
+// plus the row scales of a folded RMSNorm, the rows' sums of squares and the
+// column partial sums (forge_gemm_epilogue row_parts_in, row_sumsq_out,
+// col_sums_out).  Separate instances keep the plain fused kernels' code as
+// it is: the statistics code in them cost the C5 step about 0.7%.
+#define GEMM_X_STATS_KERNEL(NAME, BM, BN, BK, TA, TB)                               \
+    FORGE_KERNEL void __launch_bounds__(256, GEMM_X_OCC(BM, BN, BK)) NAME(GemmArgs p) { \
+        gemm_single_x<BM, BN, BK, TA, TB, true, 2, 2, true>(p);                     \
+    }
+#define GEMM_STATS_FAMILY(AB, TA, TB)                                                   \
+    GEMM_X_STATS_KERNEL(forge_gemm_##AB##_128x128x32_x_s, 128, 128, 32, TA, TB)        \
+    GEMM_X_STATS_KERNEL(forge_gemm_##AB##_128x64x32_x_s, 128, 64, 32, TA, TB)          \
+    GEMM_X_STATS_KERNEL(forge_gemm_##AB##_64x128x32_x_s, 64, 128, 32, TA, TB)          \
+    GEMM_X_STATS_KERNEL(forge_gemm_##AB##_64x64x32_x_s, 64, 64, 32, TA, TB)
+GEMM_STATS_FAMILY(nn, false, false)
+GEMM_STATS_FAMILY(nt, false, true)
+GEMM_STATS_FAMILY(tn, true, false)
+GEMM_STATS_FAMILY(tt, true, true)
+
 // Batched instances (forge_gemm_batch_<ab>_<tile>): several same-shape
 // products per launch, each with its own operands and epilogue.  They serve
 // the Q/K/V projections, forge_gemm_batch_f32 and the K slices of split-K
@@ -84,6 +103,14 @@ GEMM_X8_KERNEL(forge_gemm_nn_64x128x32_x8_e, false, false, true)
 GEMM_X8_KERNEL(forge_gemm_nt_64x128x32_x8_e, false, true, true)
 GEMM_X8_KERNEL(forge_gemm_tn_64x128x32_x8_e, true, false, true)
 GEMM_X8_KERNEL(forge_gemm_tt_64x128x32_x8_e, true, true, true)
+#define GEMM_X8_STATS_KERNEL(NAME, TA, TB)                                          \
+    FORGE_KERNEL void __launch_bounds__(512, 1) NAME(GemmArgs p) {                  \
+        gemm_single_x<64, 128, 32, TA, TB, true, 4, 2, true>(p);                   \
+    }
+GEMM_X8_STATS_KERNEL(forge_gemm_nn_64x128x32_x8_s, false, false)
+GEMM_X8_STATS_KERNEL(forge_gemm_nt_64x128x32_x8_s, false, true)
+GEMM_X8_STATS_KERNEL(forge_gemm_tn_64x128x32_x8_s, true, false)
+GEMM_X8_STATS_KERNEL(forge_gemm_tt_64x128x32_x8_s, true, true)
 #define GEMM_X8_BATCH_KERNEL(NAME, TA, TB)                                            \
     FORGE_KERNEL void __launch_bounds__(512, 1) NAME(GemmBatchArgs b) {               \
         gemm_batch_x<64, 128, 32, TA, TB, 4, 2>(b);                                 \
@@ -235,6 +262,14 @@ FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_count_neq_u32(const float*
 FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_count_final_u32(const unsigned* part, int n,
                                                                       unsigned* out) {
     count_final_body(part, n, out);
+}
+FORGE_KERNEL void __launch_bounds__(256) forge_row_rms_parts(const float* part, int parts,
+                                                            int rows, int n, float eps, float* d) {
+    row_rms_parts_body(part, parts, rows, n, eps, d);
+}
+FORGE_KERNEL void __launch_bounds__(256) forge_row_sq_parts(const float* m, long long ld, int rows,
+                                                           int cols, float* out) {
+    row_sq_parts_body(m, ld, rows, cols, out);
 }
 FORGE_KERNEL void __launch_bounds__(EW_THREADS) forge_causal_mask(float* m, int rows, int cols,
                                                                   int first_row) {

@@ -660,7 +660,7 @@ static void gemm_slices(CudaRuntime& rt, bool ta, bool tb, forge_slice a, forge_
 
 void Attention::chunked_forward(const Matrix& q, const Matrix& k, const Matrix& v,
                                 const Matrix& residual, bool mask, size_t chunk, Matrix& out,
-                                CudaRuntime& rt) {
+                                CudaRuntime& rt, Matrix* row_sumsq) {
     // attention.rs:359-387 one chunk of query rows at a time: the chunk's
     // scores (NT GEMM, scale fused), mask, softmax, then its rows of
     // P V + residual.  Each output row is the same sum as in the unchunked
@@ -682,13 +682,14 @@ void Attention::chunked_forward(const Matrix& q, const Matrix& k, const Matrix& 
         check(forge_softmax_rows(rt.raw(), nullptr, sc, n, Sk), "softmax_rows");
         forge_gemm_epilogue ep2 = plain_epilogue();
         ep2.residual = rows_of(residual, r0, n);
+        if (row_sumsq) ep2.row_sumsq_out = rows_of(*row_sumsq, r0, n);
         gemm_slices(rt, false, false, sc, v.slice(), rows_of(out, r0, n), n, H, Sk, ep2,
                     "attention value");
     }
 }
 
 Matrix Attention::attention_value(QkvProjection::Projected projected, const Matrix& residual,
-                                  bool mask, CudaRuntime& rt) {
+                                  bool mask, CudaRuntime& rt, Matrix* row_sumsq) {
     // attention.rs:336-387: S = Q K^T / sqrt(d) as one NT GEMM with the
     // scale in its epilogue; (mask); softmax; A = P V with the residual add
     // of finish_forward (attention.rs:243-253) fused.
@@ -703,7 +704,7 @@ Matrix Attention::attention_value(QkvProjection::Projected projected, const Matr
         require(v.rows() == k.rows(), "value rows == key rows");
         require(residual.rows() == q.rows() && residual.cols() == v.cols(), "residual shape");
         Matrix out = rt.new_uninit_matrix(q.rows(), v.cols());
-        chunked_forward(q, k, v, residual, mask, chunk, out, rt);
+        chunked_forward(q, k, v, residual, mask, chunk, out, rt, row_sumsq);
         return out;
     }
     Matrix scores = rt.new_uninit_matrix(q.rows(), k.rows());
@@ -719,8 +720,20 @@ Matrix Attention::attention_value(QkvProjection::Projected projected, const Matr
     Matrix out = rt.new_uninit_matrix(q.rows(), v.cols());
     forge_gemm_epilogue ep2 = plain_epilogue();
     ep2.residual = residual.slice();
+    if (row_sumsq) ep2.row_sumsq_out = row_sumsq->slice();
     rt.gemm_ex(nullptr, false, false, scores, v, out.slice(), q.rows(), v.cols(), v.rows(), ep2);
     return out;
+}
+
+Matrix Attention::forward_pre_norm(const Matrix& query_input, const Matrix& key_value_input,
+                                   bool mask, Matrix& row_sumsq, CudaRuntime& rt) {
+    // attention.rs:221-241 without the norm: X + A, and the rows' sums of
+    // squares from the attention-value product's epilogue.
+    const size_t parts = (qkv_.value().weights().cols() + 31) / 32;
+    require(row_sumsq.rows() == query_input.rows() && row_sumsq.cols() == parts,
+            "row_sumsq shape");
+    return attention_value(qkv_.project(query_input, key_value_input, rt), query_input, mask, rt,
+                           &row_sumsq);
 }
 
 Matrix Attention::forward(const Matrix& query_input, const Matrix& key_value_input,
@@ -974,8 +987,77 @@ std::vector<HostData> InferenceBlock::get_data(CudaRuntime& rt) const {
     return transformer_data(attention_, position_, fcs_.executor(), output_, norm2_, rt);
 }
 
+bool InferenceBlock::can_fold_norms() const {
+    const Normalization& n1 = attention_.normalization();
+    return n1.kind == NormType::Rms && !n1.gamma && !n1.beta && norm2_.kind == NormType::Rms &&
+           !norm2_.gamma && !norm2_.beta && !fcs_.executor().res_range();
+}
+
+// A Linear's forward (bias, activation) with the row statistics of a
+// folded RMSNorm in its epilogue.
+static void forward_with_row_stats(const Linear& layer, const Matrix& input, Matrix& out,
+                                   const Matrix* residual, const Matrix* parts_in, int row_div,
+                                   size_t row_n, float eps, Matrix* sumsq_out, CudaRuntime& rt) {
+    forge_gemm_problem pr = layer.forward_problem(input, out);
+    forge_gemm_epilogue ep = pr.epilogue;
+    if (residual) ep.residual = residual->slice();
+    if (parts_in) {
+        ep.row_parts_in = parts_in->slice();
+        ep.row_parts = parts_in->cols();
+        ep.row_n = row_n;
+        ep.row_eps = eps;
+        ep.row_div = row_div;
+    }
+    if (sumsq_out) ep.row_sumsq_out = sumsq_out->slice();
+    check(forge_gemm_ex_f32(rt.raw(), nullptr, 0, 0, pr.A, pr.B, pr.C, input.rows(),
+                            out.cols(), input.cols(), &ep),
+          "folded-norm linear");
+}
+
+Matrix InferenceBlock::forward_folded(const Matrix& input, bool mask, CudaRuntime& rt,
+                                      Matrix* target) {
+    // inference.rs:76-108 with both RMSNorms folded: with h1 = pre1 / d1 and
+    // h2 = pre2 / d2 (d the rows' RMS, norm.rs:50-69),
+    //   pre1 = X + A                        (rows' sums of squares kept)
+    //   F    = act((pre1 W1) / d1 + b1) ...  (first FFN layer)
+    //   pre2 = F Wn + bn + pre1 / d1        (last FFN layer, sums kept)
+    //   out  = (pre2 Wo) / d2 + bo.
+    Matrix positioned = rt.matrix_add(input, position_);
+    const size_t S = positioned.rows();
+    const size_t H = attention_.qkv().value().weights().cols();
+    Matrix sq1 = rt.new_uninit_matrix(S, (H + 31) / 32);
+    Matrix pre1 = attention_.forward_pre_norm(positioned, positioned, mask, sq1, rt);
+    positioned = Matrix();
+    std::vector<Linear>& layers = fcs_.executor().layers();
+    const size_t L = layers.size();
+    const float eps1 = attention_.normalization().eps, eps2 = norm2_.eps;
+    Matrix x;  // the current layer's input (pre1 for the first layer)
+    Matrix sq2;
+    for (size_t i = 0; i < L; i++) {
+        const Matrix& in = i == 0 ? pre1 : x;
+        Matrix out = rt.new_uninit_matrix(in.rows(), layers[i].weights().cols());
+        const bool first = i == 0, last = i + 1 == L;
+        int div = (first ? 1 : 0) | (last ? 2 : 0);
+        if (last) sq2 = rt.new_uninit_matrix(S, (out.cols() + 31) / 32);
+        forward_with_row_stats(layers[i], in, out, last ? &pre1 : nullptr, div ? &sq1 : nullptr,
+                               div, H, eps1, last ? &sq2 : nullptr, rt);
+        x = std::move(out);
+    }
+    pre1 = Matrix();
+    sq1 = Matrix();
+    Matrix result;
+    Matrix* dst = target;
+    if (!dst) {
+        result = rt.new_uninit_matrix(S, output_.weights().cols());
+        dst = &result;
+    }
+    forward_with_row_stats(output_, x, *dst, nullptr, &sq2, 1, x.cols(), eps2, nullptr, rt);
+    return result;
+}
+
 Matrix InferenceBlock::forward(const Matrix& input, CudaRuntime& rt) {
     // inference.rs:76-80.
+    if (fold_norms_ && can_fold_norms()) return forward_folded(input, false, rt, nullptr);
     Matrix positioned = rt.matrix_add(input, position_);
     Matrix x = attention_.forward(positioned, positioned, rt);
     return finish_forward(std::move(positioned), std::move(x), rt, nullptr);
@@ -983,6 +1065,7 @@ Matrix InferenceBlock::forward(const Matrix& input, CudaRuntime& rt) {
 
 Matrix InferenceBlock::forward_mask(const Matrix& input, CudaRuntime& rt) {
     // inference.rs:82-88.
+    if (fold_norms_ && can_fold_norms()) return forward_folded(input, true, rt, nullptr);
     Matrix positioned = rt.matrix_add(input, position_);
     Matrix x = attention_.forward_mask(positioned, positioned, rt);
     return finish_forward(std::move(positioned), std::move(x), rt, nullptr);
@@ -990,6 +1073,12 @@ Matrix InferenceBlock::forward_mask(const Matrix& input, CudaRuntime& rt) {
 
 void InferenceBlock::forward_into(const Matrix& input, Matrix& output, CudaRuntime& rt,
                                   bool mask) {
+    if (fold_norms_ && can_fold_norms()) {
+        require(output.rows() == input.rows() && output.cols() == output_.weights().cols(),
+                "output shape");
+        (void)forward_folded(input, mask, rt, &output);
+        return;
+    }
     Matrix positioned = rt.matrix_add(input, position_);
     Matrix x = mask ? attention_.forward_mask(positioned, positioned, rt)
                     : attention_.forward(positioned, positioned, rt);

@@ -441,6 +441,13 @@ extern "C" forge_status forge_net_transformer_set_score_bytes(forge_net_model* m
     return guard([&] { parts_of(m).attention->set_max_score_bytes(bytes); });
 }
 
+extern "C" forge_status forge_net_transformer_set_fold_norms(forge_net_model* m, int on) {
+    if (!m || (!m->enc_inf && !m->dec_inf)) return FORGE_EINVAL;
+    return guard([&] {
+        (m->enc_inf ? m->enc_inf->block() : m->dec_inf->block()).set_fold_norms(on != 0);
+    });
+}
+
 extern "C" forge_status forge_net_transformer_param(forge_net_model* m, int slot,
                                                     forge_slice* out) {
     if (!m || !out || (!m->enc_inf && !m->enc_train && !m->dec_inf)) return FORGE_EINVAL;

@@ -64,7 +64,15 @@ struct GemmArgs {
     int aux_act;
     int update;
     float update_scale;
+    const float* row_part;
+    const float* row_d;
+    int row_parts, row_n;
+    float row_eps;
+    int row_div;
+    float* row_sq;
+    float* col_part;
 };
+static_assert(sizeof(GemmArgs) == 168, "kernel argument layout of forge::GemmArgs");
 
 // Must match forge::GemmBatchArgs in csrc/kernels/gemm.hpp.
 constexpr int GEMM_BATCH_MAX = 8;
@@ -654,17 +662,18 @@ constexpr int kUnguardedCount = 6;
 // as 512 tiles of 64x128 at 139.
 constexpr double kSingleWorkgroupFactor = 0.96;
 
-enum class GemmKind { Plain, Epilogue, Batch };
+enum class GemmKind { Plain, Epilogue, Batch, Stats };
 
 // Kernel that runs a tile: plain NN (forge_gemm_nn_<tile>), fused epilogue
-// (forge_gemm_<ab>_<tile>_e) or batched (forge_gemm_batch_<ab>_<tile>).
+// (forge_gemm_<ab>_<tile>_e), fused epilogue with row statistics and column
+// sums (forge_gemm_<ab>_<tile>_s) or batched (forge_gemm_batch_<ab>_<tile>).
 void gemm_kernel_name(char* out, size_t cap, GemmKind kind, int ta, int tb,
                       const GemmConfig& cfg) {
     if (kind == GemmKind::Batch)
         snprintf(out, cap, "forge_gemm_batch_%s_%s", gemm_ab(ta, tb), cfg.tag);
     else
         snprintf(out, cap, "forge_gemm_%s_%s%s", gemm_ab(ta, tb), cfg.tag,
-                 kind == GemmKind::Epilogue ? "_e" : "");
+                 kind == GemmKind::Epilogue ? "_e" : kind == GemmKind::Stats ? "_s" : "");
 }
 
 // Workgroups of a kernel that one CU holds at once (its registers and LDS),
@@ -823,10 +832,35 @@ forge_status gemm_args(int ta, int tb, forge_slice A, forge_slice B, forge_slice
         a.aux_act = ep->aux_activation;
         a.update = ep->update ? 1 : 0;
         a.update_scale = ep->update_scale;
+        if (ep->row_parts_in.ptr) {
+            if (ep->row_parts == 0 || ep->row_n == 0)
+                return fail(FORGE_EINVAL, "gemm row statistics need row_parts and row_n >= 1");
+            if (ep->row_div < 0 || ep->row_div > 3)
+                return fail(FORGE_EINVAL, "gemm row_div %d is not 0-3", ep->row_div);
+            if (!fits_int(ep->row_parts) || !fits_int(ep->row_n))
+                return fail(FORGE_EINVAL, "gemm row_parts / row_n exceed 2^31-1");
+            FORGE_TRY(need(ep->row_parts_in, M * ep->row_parts, "gemm row_parts_in"));
+            a.row_part = ep->row_parts_in.ptr;
+            a.row_parts = (int)ep->row_parts;
+            a.row_n = (int)ep->row_n;
+            a.row_eps = ep->row_eps;
+            a.row_div = ep->row_div;
+        } else if (ep->row_div) {
+            return fail(FORGE_EINVAL, "gemm row_div without row_parts_in");
+        }
+        FORGE_TRY(need_opt(ep->row_sumsq_out, M * ((N + 31) / 32), "gemm row_sumsq_out"));
+        FORGE_TRY(need_opt(ep->col_sums_out, N, "gemm col_sums_out"));
+        FORGE_TRY(need_opt(ep->col_sums_param, N, "gemm col_sums_param"));
+        a.row_sq = ep->row_sumsq_out.ptr;
     }
     *out = a;
     *aligned = al;
     return FORGE_OK;
+}
+
+bool gemm_has_stats(const forge_gemm_epilogue* ep) {
+    return ep && (ep->row_parts_in.ptr || ep->row_sumsq_out.ptr || ep->col_sums_out.ptr ||
+                  ep->col_sums_param.ptr);
 }
 
 // Split-K: `splits` K slices of the product as one batched launch writing
@@ -834,10 +868,9 @@ forge_status gemm_args(int ta, int tb, forge_slice A, forge_slice B, forge_slice
 // them in slice order and applying a's epilogue.  Requires an unguarded
 // tile and K % (splits * bk) == 0.
 forge_status gemm_split_launch(forge_runtime* rt, forge_stream* s, int ta, int tb,
-                               const GemmArgs& a, const GemmConfig& cfg, int splits) {
+                               const GemmArgs& a, const GemmConfig& cfg, int splits,
+                               float* ws) {
     const size_t mn = (size_t)a.M * (size_t)a.N;
-    float* ws = nullptr;
-    FORGE_TRY(workspace(rt, s, (size_t)splits * mn, &ws));
     const int ks = a.K / splits;
     GemmBatchArgs b{};
     b.count = splits;
@@ -873,26 +906,147 @@ forge_status gemm_split_launch(forge_runtime* rt, forge_stream* s, int ta, int t
                   dim3(grid), dim3(256), 0, rargs);
 }
 
+size_t sum_cols_scratch(size_t rows, size_t cols);
+forge_status sum_cols_impl(forge_runtime* rt, forge_stream* s, const float* m, ColSumOut o,
+                           size_t rows, size_t cols, float* scratch);
+
+// Rows per wave (TM) of a tile: the eight-wave tile is 4 x 2 waves, the
+// four-wave ones 2 x 2.
+int tile_rows_per_wave(const GemmConfig& g) { return g.bm / (g.threads == 512 ? 4 : 2); }
+
+// The epilogue's row statistics and column sums around one product launch
+// (forge_gemm_epilogue row_parts_in, row_sumsq_out, col_sums_*).  On an
+// unguarded tile the _s kernel forms the row scales from row_parts_in
+// itself, writes row_sumsq_out and one partial row of column sums per
+// wave-row of TM rows; on the guarded and split-K paths a small kernel forms
+// the divisors first (row_d) and row_sumsq_out / the column sums are taken
+// from C after the product.  The column sums end with one final pass that
+// also applies the parameter's SGD step.  `ws` is the workspace that follows
+// what the product itself uses.
+struct GemmStatsWork {
+    bool col = false, col_from_c = false, sq_from_c = false;
+    float* col_part = nullptr;
+    size_t col_rows = 0;
+    float* chunk_scratch = nullptr;
+};
+
+size_t gemm_stats_floats(const forge_gemm_epilogue* ep, const GemmArgs& a, bool xtile,
+                         const GemmConfig& cfg) {
+    if (!gemm_has_stats(ep)) return 0;
+    const size_t M = (size_t)a.M, N = (size_t)a.N;
+    size_t n = 0;
+    if (a.row_part && !xtile) n += M;
+    if (ep->col_sums_out.ptr || ep->col_sums_param.ptr) {
+        const size_t rows = xtile ? M / (size_t)tile_rows_per_wave(cfg) : M;
+        if (xtile) n += rows * N;
+        n += sum_cols_scratch(rows, N);
+    }
+    return n;
+}
+
+forge_status gemm_stats_prepare(forge_runtime* rt, forge_stream* s, const forge_gemm_epilogue* ep,
+                                GemmArgs& a, bool xtile, const GemmConfig& cfg, float* ws,
+                                GemmStatsWork* w) {
+    if (!gemm_has_stats(ep)) return FORGE_OK;
+    const size_t M = (size_t)a.M, N = (size_t)a.N;
+    if (a.row_part && !xtile) {
+        float* d = ws;
+        ws += M;
+        int m = a.M, parts = a.row_parts, n = a.row_n;
+        float eps = a.row_eps;
+        FORGE_TRY(launch_args(rt, s, "forge_row_rms_parts", dim3((unsigned)((M + 255) / 256)),
+                              dim3(256), 0, (const float*)a.row_part, parts, m, n, eps, d));
+        a.row_d = d;
+        a.row_part = nullptr;
+    }
+    if (a.row_sq && !xtile) {
+        a.row_sq = nullptr;
+        w->sq_from_c = true;
+    }
+    if (ep->col_sums_out.ptr || ep->col_sums_param.ptr) {
+        w->col = true;
+        if (xtile) {
+            w->col_rows = M / (size_t)tile_rows_per_wave(cfg);
+            w->col_part = ws;
+            ws += w->col_rows * N;
+            a.col_part = w->col_part;
+        } else {
+            w->col_from_c = true;
+            w->col_rows = M;
+        }
+        w->chunk_scratch = ws;
+    }
+    return FORGE_OK;
+}
+
+forge_status gemm_stats_finish(forge_runtime* rt, forge_stream* s, const forge_gemm_epilogue* ep,
+                               const GemmArgs& a, const GemmStatsWork& w) {
+    if (w.sq_from_c) {
+        int m = a.M, n = a.N;
+        long long ldc = a.ldc;
+        const size_t parts = (size_t)((a.N + 31) / 32);
+        FORGE_TRY(launch_args(rt, s, "forge_row_sq_parts",
+                              dim3((unsigned)((parts * (size_t)a.M + 255) / 256)), dim3(256), 0,
+                              (const float*)a.C, ldc, m, n, ep->row_sumsq_out.ptr));
+    }
+    if (w.col) {
+        // C is dense (ldc == N) for every product here.
+        const float* m = w.col_from_c ? a.C : w.col_part;
+        return sum_cols_impl(rt, s, m,
+                             ColSumOut{ep->col_sums_out.ptr, ep->col_sums_param.ptr,
+                                       ep->col_sums_lr},
+                             w.col_rows, (size_t)a.N, w.chunk_scratch);
+    }
+    return FORGE_OK;
+}
+
+// Column sums of no rows are zero and leave the parameter as it is; there
+// are no rows to take statistics of.
+forge_status gemm_stats_empty(forge_runtime* rt, forge_stream* s, const forge_gemm_epilogue* ep,
+                              size_t N) {
+    if (ep && ep->col_sums_out.ptr && N)
+        return forge_fill(rt, s, forge_slice{ep->col_sums_out.ptr, N}, 0.0f);
+    return FORGE_OK;
+}
+
 forge_status gemm_dispatch(forge_runtime* rt, forge_stream* s, int ta, int tb, forge_slice A,
                            forge_slice B, forge_slice C, size_t M, size_t N, size_t K,
                            const forge_gemm_epilogue* ep, bool plain_name) {
     GemmArgs a{};
     bool aligned = false;
     FORGE_TRY(gemm_args(ta, tb, A, B, C, M, N, K, ep, &a, &aligned));
-    if (M == 0 || N == 0) return FORGE_OK;
+    if (M == 0 || N == 0) return gemm_stats_empty(rt, s, ep, N);
     const GemmConfig* split_cfg = nullptr;
     const int splits = choose_splits(rt, ta, tb, M, N, K, aligned, &split_cfg);
-    if (splits > 1) return gemm_split_launch(rt, s, ta, tb, a, *split_cfg, splits);
-    const GemmKind kind = plain_name && !ta && !tb ? GemmKind::Plain : GemmKind::Epilogue;
-    const GemmPlan plan = choose_gemm(rt, ta, tb, M, N, K, aligned, kind);
+    const GemmKind kind = gemm_has_stats(ep)            ? GemmKind::Stats
+                          : plain_name && !ta && !tb ? GemmKind::Plain
+                                                     : GemmKind::Epilogue;
+    const GemmPlan plan = splits > 1 ? GemmPlan{split_cfg, 0}
+                                     : choose_gemm(rt, ta, tb, M, N, K, aligned, kind);
     const GemmConfig& cfg = *plan.cfg;
-    char name[96];
-    gemm_kernel_name(name, sizeof name, kind, ta, tb, cfg);
-    size_t shmem = 0;
-    if (plan.cap) FORGE_TRY(occupancy_cap_shmem(rt, name, plan.cap, &shmem));
-    unsigned tiles = (unsigned)(((M + cfg.bm - 1) / cfg.bm) * ((N + cfg.bn - 1) / cfg.bn));
-    void* args[] = {&a};
-    return launch(rt, s, name, dim3(tiles), dim3(cfg.threads), shmem, args);
+    const bool xtile = splits == 1 && &cfg != &kGuard64;
+    const size_t split_floats = splits > 1 ? (size_t)splits * M * N : 0;
+    const size_t stats_floats = gemm_stats_floats(ep, a, xtile, cfg);
+    float* ws = nullptr;
+    if (split_floats + stats_floats) FORGE_TRY(workspace(rt, s, split_floats + stats_floats, &ws));
+    GemmStatsWork w;
+    FORGE_TRY(gemm_stats_prepare(rt, s, ep, a, xtile, cfg, ws ? ws + split_floats : nullptr, &w));
+    if (splits > 1) {
+        FORGE_TRY(gemm_split_launch(rt, s, ta, tb, a, cfg, splits, ws));
+    } else {
+        char name[96];
+        // The guarded tile has no statistics instance: its fused kernel
+        // divides by row_d per element and the sums come from C.
+        gemm_kernel_name(name, sizeof name, xtile || kind != GemmKind::Stats ? kind
+                                                                              : GemmKind::Epilogue,
+                         ta, tb, cfg);
+        size_t shmem = 0;
+        if (plan.cap) FORGE_TRY(occupancy_cap_shmem(rt, name, plan.cap, &shmem));
+        unsigned tiles = (unsigned)(((M + cfg.bm - 1) / cfg.bm) * ((N + cfg.bn - 1) / cfg.bn));
+        void* args[] = {&a};
+        FORGE_TRY(launch(rt, s, name, dim3(tiles), dim3(cfg.threads), shmem, args));
+    }
+    return gemm_stats_finish(rt, s, ep, a, w);
 }
 
 const char* binop_name(forge_binary_op op) {
@@ -1222,7 +1376,9 @@ extern "C" forge_status forge_gemm_f32_split(forge_runtime* rt, forge_stream* s,
         return fail(FORGE_EINVAL, "shape %zux%zux%zu does not fit tile %s with %d splits", M, N,
                     K, tile_tag, splits);
     if (M == 0 || N == 0) return FORGE_OK;
-    return gemm_split_launch(rt, s, 0, 0, a, *cfg, splits);
+    float* ws = nullptr;
+    FORGE_TRY(workspace(rt, s, (size_t)splits * M * N, &ws));
+    return gemm_split_launch(rt, s, 0, 0, a, *cfg, splits, ws);
 }
 
 extern "C" forge_status forge_gemm_ex_f32_tile(forge_runtime* rt, forge_stream* s,
@@ -1246,15 +1402,23 @@ extern "C" forge_status forge_gemm_ex_f32_tile(forge_runtime* rt, forge_stream* 
         (!aligned || M % cfg->bm || N % cfg->bn || K % (size_t)cfg->bk))
         return fail(FORGE_EINVAL, "shape %zux%zux%zu does not fit unguarded tile %s", M, N, K,
                     tile_tag);
-    if (M == 0 || N == 0) return FORGE_OK;
+    if (M == 0 || N == 0) return gemm_stats_empty(rt, s, ep, N);
+    const bool xtile = cfg != &kGuard64;
+    float* ws = nullptr;
+    const size_t stats_floats = gemm_stats_floats(ep, a, xtile, *cfg);
+    if (stats_floats) FORGE_TRY(workspace(rt, s, stats_floats, &ws));
+    GemmStatsWork w;
+    FORGE_TRY(gemm_stats_prepare(rt, s, ep, a, xtile, *cfg, ws, &w));
     char name[96];
-    snprintf(name, sizeof name, "forge_gemm_%s_%s_e", gemm_ab(trans_a, trans_b), cfg->tag);
+    snprintf(name, sizeof name, "forge_gemm_%s_%s_%s", gemm_ab(trans_a, trans_b), cfg->tag,
+             xtile && gemm_has_stats(ep) ? "s" : "e");
     size_t shmem = 0;
     if (cap) FORGE_TRY(occupancy_cap_shmem(rt, name, cap, &shmem));
     const unsigned tiles =
         (unsigned)(((M + cfg->bm - 1) / cfg->bm) * ((N + cfg->bn - 1) / cfg->bn));
     void* args[] = {&a};
-    return launch(rt, s, name, dim3(tiles), dim3(cfg->threads), shmem, args);
+    FORGE_TRY(launch(rt, s, name, dim3(tiles), dim3(cfg->threads), shmem, args));
+    return gemm_stats_finish(rt, s, ep, a, w);
 }
 
 extern "C" forge_status forge_gemm_kernel_name(forge_runtime* rt, int trans_a, int trans_b,
@@ -1292,13 +1456,14 @@ extern "C" forge_status forge_gemm_batch_f32(forge_runtime* rt, forge_stream* s,
     if (!rt) return fail(FORGE_EINVAL, "runtime is null");
     if (count > 0 && !problems) return fail(FORGE_EINVAL, "problems is null");
     GemmBatchArgs b{};
-    bool all_aligned = true;
+    bool all_aligned = true, stats = false;
     for (size_t z = 0; z < count; z++) {
         GemmArgs a{};
         bool aligned = false;
         FORGE_TRY(gemm_args(trans_a, trans_b, problems[z].A, problems[z].B, problems[z].C, M, N,
                             K, &problems[z].epilogue, &a, &aligned));
         all_aligned = all_aligned && aligned;
+        stats = stats || gemm_has_stats(&problems[z].epilogue);
         if (z < (size_t)GEMM_BATCH_MAX) b.p[z] = a;
     }
     if (count == 0 || M == 0 || N == 0) return FORGE_OK;
@@ -1309,7 +1474,7 @@ extern "C" forge_status forge_gemm_batch_f32(forge_runtime* rt, forge_stream* s,
     // Shapes the single-product path splits in K are dispatched one by one,
     // so every product equals its forge_gemm_ex_f32 result bit for bit.
     const bool split = choose_splits(rt, trans_a, trans_b, M, N, K, all_aligned, &split_cfg) > 1;
-    if (count > (size_t)GEMM_BATCH_MAX || &cfg == &kGuard64 || split) {
+    if (count > (size_t)GEMM_BATCH_MAX || &cfg == &kGuard64 || split || stats) {
         for (size_t z = 0; z < count; z++)
             FORGE_TRY(gemm_dispatch(rt, s, trans_a, trans_b, problems[z].A, problems[z].B,
                                     problems[z].C, M, N, K, &problems[z].epilogue, false));

@@ -86,9 +86,13 @@ def _sl(a) -> Slice:
 
 
 def _epilogue(alpha=1.0, bias=None, residual=None, aux_mul=None, pre_out=None,
-              activation=ACT_IDENTITY, update=False, update_scale=0.0, aux_activation=0):
+              activation=ACT_IDENTITY, update=False, update_scale=0.0, aux_activation=0,
+              row_parts_in=None, row_parts=0, row_n=0, row_eps=1e-5, row_div=0,
+              row_sumsq_out=None, col_sums_out=None, col_sums_param=None, col_sums_lr=0.0):
     return GemmEpilogue(alpha, _sl(bias), _sl(residual), _sl(aux_mul), _sl(pre_out), activation,
-                        1 if update else 0, update_scale, aux_activation)
+                        1 if update else 0, update_scale, aux_activation, _sl(row_parts_in),
+                        row_parts, row_n, row_eps, row_div, _sl(row_sumsq_out), _sl(col_sums_out),
+                        _sl(col_sums_param), col_sums_lr)
 
 
 class Runtime:
@@ -207,11 +211,13 @@ class Runtime:
     def gemm(self, A, B, C, M, N, K, stream=None) -> None:
         call("forge_gemm_f32", self.handle, stream, A.slice, B.slice, C.slice, M, N, K)
 
-    def gemm_ex(self, A, B, C, M, N, K, trans_a=False, trans_b=False, alpha=1.0, bias=None,
-                residual=None, aux_mul=None, pre_out=None, activation=ACT_IDENTITY,
-                update=False, update_scale=0.0, aux_activation=0, stream=None) -> None:
-        ep = _epilogue(alpha, bias, residual, aux_mul, pre_out, activation, update,
-                       update_scale, aux_activation)
+    def gemm_ex(self, A, B, C, M, N, K, trans_a=False, trans_b=False, stream=None,
+                **epilogue) -> None:
+        """forge_gemm_ex_f32; epilogue keywords as _epilogue (alpha, bias,
+        residual, aux_mul, pre_out, activation, update, update_scale,
+        aux_activation, row_parts_in, row_parts, row_n, row_eps, row_div,
+        row_sumsq_out, col_sums_out, col_sums_param, col_sums_lr)."""
+        ep = _epilogue(**epilogue)
         call("forge_gemm_ex_f32", self.handle, stream, int(trans_a), int(trans_b), A.slice,
              B.slice, C.slice, M, N, K, byref(ep))
 

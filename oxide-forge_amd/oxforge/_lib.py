@@ -70,6 +70,15 @@ class GemmEpilogue(ctypes.Structure):
         ("update", c_int),
         ("update_scale", c_float),
         ("aux_activation", c_int),
+        ("row_parts_in", Slice),
+        ("row_parts", c_size_t),
+        ("row_n", c_size_t),
+        ("row_eps", c_float),
+        ("row_div", c_int),
+        ("row_sumsq_out", Slice),
+        ("col_sums_out", Slice),
+        ("col_sums_param", Slice),
+        ("col_sums_lr", c_float),
     ]
 
 

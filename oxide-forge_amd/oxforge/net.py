@@ -46,6 +46,7 @@ SIGNATURES = {
     "forge_net_transformer_backward": [c_void_p, Slice, c_float, Slice, POINTER(Slice)],
     "forge_net_transformer_param": [c_void_p, c_int, POINTER(Slice)],
     "forge_net_transformer_set_score_bytes": [c_void_p, c_size_t],
+    "forge_net_transformer_set_fold_norms": [c_void_p, c_int],
     "forge_net_checkpoint_save": [c_void_p, c_char_p],
     "forge_net_checkpoint_load": [c_void_p, c_char_p, c_int, POINTER(c_void_p)],
     "forge_checkpoint_inspect": [c_char_p, c_char_p, c_size_t, POINTER(c_uint64)],
@@ -247,6 +248,12 @@ class Transformer(_Model):
         """Largest [seq, seq] score matrix held at once; above it attention
         runs in chunks of query rows (Attention::set_max_score_bytes)."""
         call("forge_net_transformer_set_score_bytes", self.h, nbytes)
+
+    def set_fold_norms(self, on):
+        """Inference kinds: fold the parameterless RMSNorms into the
+        neighbouring products (on, the default) or run the reference's
+        launch order (InferenceBlock::set_fold_norms)."""
+        call("forge_net_transformer_set_fold_norms", self.h, 1 if on else 0)
 
     def param(self, name):
         sl = Slice()

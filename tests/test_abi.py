@@ -67,6 +67,9 @@ def dispatcher_kernel_names():
     for ab in ("nn", "nt", "tn", "tt"):
         for tag in tiles + ("64x64x16_2x2_g",):
             names.append(f"forge_gemm_{ab}_{tag}_e")
+        # row statistics / column sums instances of the unguarded tiles
+        for tag in tiles + ("64x128x32_x8",):
+            names.append(f"forge_gemm_{ab}_{tag}_s")
     for tag in tiles + ("128x256x32_x", "64x64x16_2x2_g"):
         names.append(f"forge_gemm_nn_{tag}")
     # batched (forge_gemm_batch_f32, Q/K/V and split-K slices): every layout
@@ -96,7 +99,8 @@ def dispatcher_kernel_names():
                   f"forge_map_sum_{op}_v"]
     names += ["forge_fill_random", "forge_act_backward_v", "forge_act_backward_s",
               "forge_count_neq", "forge_count_final", "forge_count_neq_u32",
-              "forge_count_final_u32", "forge_sgd_v", "forge_sgd_s"]
+              "forge_count_final_u32", "forge_sgd_v", "forge_sgd_s", "forge_row_rms_parts",
+              "forge_row_sq_parts"]
     names += ["forge_fill_v", "forge_fill_s", "forge_fill_seq", "forge_causal_mask",
               "forge_sum_cols_v", "forge_sum_cols_s", "forge_sum_cols_final", "forge_sum_cols_final2",
               "forge_sum_cols_final_v", "forge_sum_cols_final2_v",

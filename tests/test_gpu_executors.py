@@ -141,6 +141,72 @@ def test_transformer_inference(rt, name, S, H, F, O, norm, kind, streams):
     assert err <= TOL
 
 
+FOLD_CASES = [
+    # (S, H, F, O, kind, score_bytes: None = unchunked)
+    (128, 128, 256, 96, net.ENCODER_INFERENCE, None),
+    (128, 128, 256, 96, net.DECODER_INFERENCE, None),
+    (320, 256, 512, 128, net.DECODER_INFERENCE, 64 * 320 * 4),  # chunked attention
+    (70, 48, 100, 36, net.ENCODER_INFERENCE, None),             # guarded tiles
+    (2048, 1024, 4096, 1024, net.ENCODER_INFERENCE, None),      # C4
+]
+
+
+@pytest.mark.parametrize("S,H,F,O,kind,score_bytes", FOLD_CASES)
+def test_rms_norms_folded_into_products(rt, S, H, F, O, kind, score_bytes):
+    """With the reference's parameterless RMSNorms the inference block folds
+    both norms into the products beside them (InferenceBlock::
+    set_fold_norms, inference.rs:76-108 with norm.rs:50-69).  The folded
+    forward matches the f64 oracle (1e-4) and the reference-ordered forward
+    (the same kernels without the fold) to 1e-5 relative; the reference
+    order is still selectable and still matches the oracle.  Covers
+    encoder and decoder, query-chunked attention (the rows' statistics
+    written per chunk) and odd sizes (the guarded tiles, whose statistics
+    come from separate passes)."""
+    say(f"folded RMSNorms S={S} H={H} F={F} O={O} kind={kind} chunked={score_bytes}")
+    full = S == 2048
+    p = make_params(S, H, F, O, 44, bias=not full, affine=False, norm=net.RMS)
+    if full:
+        for k, n in (("BQ", H), ("BK", H), ("BV", H), ("B1", F), ("B2", H), ("BO", O)):
+            p[k] = np.zeros(n, np.float32)
+    X = synth.normal((S, H), 6)
+    Tf = net.Transformer(rt, p, S, H, F, O, net.RMS, kind)
+    Tr = net.Transformer(rt, p, S, H, F, O, net.RMS, kind)
+    Tr.set_fold_norms(False)
+    if score_bytes:
+        Tf.set_score_bytes(score_bytes)
+        Tr.set_score_bytes(score_bytes)
+    dX = rt.array(X)
+    yf, yr = Tf.forward(dX).numpy(), Tr.forward(dX).numpy()
+    Tf.close()
+    Tr.close()
+    ref, _ = ex.transformer_forward(p, X, net.RMS, causal=(kind == net.DECODER_INFERENCE))
+    ef, er, d = rel(yf, ref), rel(yr, ref), rel(yf, yr)
+    print(f"  folded {ef:.2e}, reference order {er:.2e}, folded vs reference order {d:.2e}")
+    assert ef <= TOL and er <= TOL and d <= 1e-5
+
+
+def test_fold_norms_leaves_other_norms_in_reference_order(rt):
+    """The fold applies only to parameterless RMSNorms: with gamma, or with
+    LayerNorm, the forward is the reference-ordered one bit for bit whatever
+    the setting; the training kind refuses the setting."""
+    S, H, F, O = 64, 64, 128, 48
+    for norm, affine in ((net.RMS, True), (net.LAYER, False)):
+        say(f"fold setting with norm={norm} affine={affine}")
+        p = make_params(S, H, F, O, 45, bias=True, affine=affine, norm=norm)
+        X = rt.array(synth.normal((S, H), 7))
+        Ta = net.Transformer(rt, p, S, H, F, O, norm, net.ENCODER_INFERENCE)
+        Tb = net.Transformer(rt, p, S, H, F, O, norm, net.ENCODER_INFERENCE)
+        Tb.set_fold_norms(False)
+        assert np.array_equal(Ta.forward(X).numpy(), Tb.forward(X).numpy())
+        Ta.close()
+        Tb.close()
+    p = make_params(S, H, F, O, 46, bias=True, affine=False, norm=net.RMS)
+    Tt = net.Transformer(rt, p, S, H, F, O, net.RMS, net.ENCODER_TRAINING)
+    with pytest.raises(oxforge.ForgeError):
+        Tt.set_fold_norms(True)
+    Tt.close()
+
+
 @pytest.mark.parametrize("S,H,F,O,kind", [(64, 64, 256, 64, net.ENCODER_INFERENCE),
                                            (96, 128, 256, 80, net.DECODER_INFERENCE),
                                            (2048, 1024, 4096, 1024, net.ENCODER_INFERENCE)])

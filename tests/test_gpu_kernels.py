@@ -965,6 +965,135 @@ def test_gemm_every_tile_instance(rt, tile, ta, tb):
             rt.gemm_ex_tile(tile, dA, dB, dZ, M - 1, N, K, trans_a=ta, trans_b=tb)
 
 
+U32 = 2.0 ** -24
+
+
+def _rms_rows(Y, eps=1e-5):
+    Y = np.asarray(Y, np.float64)
+    return np.sqrt((Y * Y).mean(axis=1, keepdims=True) + eps)
+
+
+def _check_row_sumsq(sq, Y):
+    """sq [M, ceil(N/32)] against the f64 sums of squares of the stored Y
+    over each 32-column block: at most 40 u times the sum (each block sum
+    passes a term through at most 35 roundings: its square, 31 adds)."""
+    Y = np.asarray(Y, np.float64)
+    M, N = Y.shape
+    P = -(-N // 32)
+    pad = np.zeros((M, P * 32))
+    pad[:, :N] = Y * Y
+    ref = pad.reshape(M, P, 32).sum(axis=2)
+    assert sq.shape == (M * P,)
+    assert np.all(np.abs(sq.reshape(M, P) - ref) <= 40 * U32 * ref + 1e-30)
+
+
+def _check_col_sums(sums, Y):
+    """Column sums of the stored Y: within M u times the column's sum of
+    magnitudes (first-order bound for any order of at most M - 1 adds per
+    term, plus the final pass)."""
+    Y = np.asarray(Y, np.float64)
+    M = Y.shape[0]
+    ref = Y.sum(axis=0)
+    assert np.all(np.abs(sums - ref) <= (M + 16) * U32 * np.abs(Y).sum(axis=0))
+
+
+STAT_TILES = TILES + [None]
+
+
+@pytest.mark.parametrize("tile", STAT_TILES)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+@pytest.mark.parametrize("N", [384, 192, 352])
+def test_gemm_epilogue_row_statistics_and_column_sums(rt, tile, ta, tb, N):
+    """The epilogue's row statistics and column sums (forge_gemm_epilogue
+    row_parts_in / row_div / row_sumsq_out / col_sums_*) on every tile
+    instance and through the dispatcher (None): a parameterless RMSNorm of
+    the first product's rows folded into a second product, as the C4 block
+    folds it across its GEMM boundaries (norm.rs:50-69 with
+    inference.rs:90-108):
+      Y1 = op(A) op(B) + R, with the sums of squares of Y1's 32-column blocks;
+      Z  = (Y1 / d) W + b, d_r = sqrt(mean_c Y1[r, c]^2 + eps), divisor
+           formed from those sums (row_div bit 0);
+      Z2 = Y1 W2 + b2 + Y1 / d (bit 1, the residual divided);
+    and the column sums of Z with a parameter's SGD step.  Products within
+    the GEMM bar (1e-4 of the f64 result on the GPU's own Y1); sums within
+    their rounding bounds; the parameter step bit for bit against the
+    returned sums.  N = 192 gives 6 partials per row (the unguarded tiles'
+    scalar row-scale loads), N = 352 shapes no unguarded tile divides."""
+    M, K = 256, 160
+    bn = 64 if tile is None else int(tile.split("x")[1])
+    if tile is not None and N % bn:
+        pytest.skip("the tile does not divide N")
+    say(f"gemm row statistics tile={tile} ta={ta} tb={tb} N={N}")
+    run = (lambda *a, **k: rt.gemm_ex(*a, **k)) if tile is None else \
+        (lambda *a, **k: rt.gemm_ex_tile(tile, *a, **k))
+    A = synth.uniform((K, M) if ta else (M, K), 81)
+    B = synth.uniform((N, K) if tb else (K, N), 82)
+    R = synth.uniform((M, N), 83)
+    W = synth.uniform((N, N), 84)
+    b = synth.uniform((N,), 85)
+    dA, dB, dR, dW, db = (rt.array(v) for v in (A, B, R, W, b))
+    P = -(-N // 32)
+    dY1, sq = rt.empty((M, N)), rt.empty((M * P,))
+    run(dA, dB, dY1, M, N, K, trans_a=ta, trans_b=tb, residual=dR, row_sumsq_out=sq)
+    Y1 = dY1.numpy()
+    ref1 = orc.gemm_f64(A, B, ta, tb) + R
+    assert np.max(np.abs(Y1 - ref1)) / np.max(np.abs(ref1)) <= 1e-4
+    _check_row_sumsq(sq.numpy(), Y1)
+
+    h = Y1.astype(np.float64) / _rms_rows(Y1)
+    dZ, cs, par = rt.empty((M, N)), rt.empty((N,)), rt.array(b)
+    run(dY1, dW, dZ, M, N, N, bias=db, row_parts_in=sq, row_parts=P, row_n=N, row_eps=1e-5,
+        row_div=1, col_sums_out=cs, col_sums_param=par, col_sums_lr=1e-3)
+    Z = dZ.numpy()
+    refz = h @ W.astype(np.float64) + b
+    assert np.max(np.abs(Z - refz)) / np.max(np.abs(refz)) <= 1e-4
+    sums = cs.numpy()
+    _check_col_sums(sums, Z)
+    assert np.array_equal(par.numpy(), b - np.float32(1e-3) * sums)
+
+    dZ2 = rt.empty((M, N))
+    run(dY1, dW, dZ2, M, N, N, bias=db, residual=dY1, row_parts_in=sq, row_parts=P, row_n=N,
+        row_eps=1e-5, row_div=2)
+    refz2 = Y1.astype(np.float64) @ W.astype(np.float64) + b + h
+    Z2 = dZ2.numpy()
+    assert np.max(np.abs(Z2 - refz2)) / np.max(np.abs(refz2)) <= 1e-4
+
+
+def test_gemm_epilogue_statistics_on_split_and_guarded_products(rt):
+    """The same statistics where the dispatcher splits K (a 64 x 128 output
+    over K = 4096) or takes the bounds-guarded tile (odd sizes): the
+    divisors, sums of squares and column sums then come from separate
+    passes over C, with the same results to within rounding; column sums
+    of no rows are zero and leave the parameter."""
+    for M, N, K in ((64, 128, 4096), (70, 50, 33)):
+        name = rt.gemm_kernel_name(M, N, K, fused=True)
+        say(f"gemm statistics {M}x{N}x{K} via {name}")
+        assert ("split" in name) == (K == 4096) and ("2x2_g" in name) == (K == 33)
+        A, B = synth.uniform((M, K), 91), synth.uniform((K, N), 92)
+        W = synth.uniform((N, N), 93)
+        P = -(-N // 32)
+        dA, dB, dW = rt.array(A), rt.array(B), rt.array(W)
+        dY1, sq = rt.empty((M, N)), rt.empty((M * P,))
+        rt.gemm_ex(dA, dB, dY1, M, N, K, row_sumsq_out=sq)
+        Y1 = dY1.numpy()
+        _check_row_sumsq(sq.numpy(), Y1)
+        dZ, cs = rt.empty((M, N)), rt.empty((N,))
+        rt.gemm_ex(dY1, dW, dZ, M, N, N, row_parts_in=sq, row_parts=P, row_n=N, row_eps=1e-5,
+                   row_div=1, col_sums_out=cs)
+        Z = dZ.numpy()
+        refz = Y1.astype(np.float64) / _rms_rows(Y1) @ W.astype(np.float64)
+        assert np.max(np.abs(Z - refz)) / np.max(np.abs(refz)) <= 1e-4
+        _check_col_sums(cs.numpy(), Z)
+    cs = rt.array(np.full(8, 3.0, np.float32))
+    par = rt.array(np.full(8, 2.0, np.float32))
+    empty = rt.empty((0,))
+    rt.gemm_ex(empty, rt.empty((4 * 8,)), empty, 0, 8, 4, col_sums_out=cs, col_sums_param=par,
+               col_sums_lr=0.5)
+    assert np.all(cs.numpy() == 0) and np.all(par.numpy() == 2.0)
+    with pytest.raises(oxforge.ForgeError):  # row_div without row statistics
+        rt.gemm_ex(dA, dB, dY1, 64, 128, 4096, row_div=1)
+
+
 @pytest.mark.parametrize("M,N,K,ta,tb,fused", [(4096, 4096, 4096, 0, 0, 0),
                                                 (2048, 2048, 1024, 0, 1, 1),
                                                 (4096, 1024, 2048, 0, 0, 0),
