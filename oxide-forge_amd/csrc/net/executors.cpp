@@ -370,6 +370,11 @@ Matrix MlpExecutor::backward(const std::vector<Matrix>& layer_inputs,
     std::optional<Matrix> grad_owned;
     bool grad_preactivated = false;
     std::optional<std::pair<size_t, Matrix>> residual_gradient;
+    // A layer whose G was formed in the next layer's input-gradient epilogue
+    // may also have had its bias gradient and SGD step taken there (from the
+    // epilogue's column sums): bias_done, with the sums in carried_bias.
+    bool bias_done = false;
+    std::optional<Vector> carried_bias;
 
     for (size_t step = 0; step < L; step++) {
         const size_t index = L - 1 - step;
@@ -379,7 +384,10 @@ Matrix MlpExecutor::backward(const std::vector<Matrix>& layer_inputs,
 
         // Layer gradient: dY * act'(pre).
         std::optional<Matrix> layer_grad_owned;
-        std::optional<Vector> bias_gradient;
+        std::optional<Vector> bias_gradient = std::move(carried_bias);
+        const bool this_bias_done = bias_done;
+        carried_bias.reset();
+        bias_done = false;
         const Matrix* layer_gradient = grad;
         if (layer.needs_pre_activation() && !grad_preactivated) {
             const Matrix* pre = cached_pre(index);
@@ -396,8 +404,9 @@ Matrix MlpExecutor::backward(const std::vector<Matrix>& layer_inputs,
             layer_gradient = &*layer_grad_owned;
         }
         // The bias gradient of a layer whose G arrived pre-multiplied is formed
-        // at the update, with the bias's SGD step (learn_from_gradient).
-        const bool defer_bias = layer.bias() && !bias_gradient;
+        // at the update, with the bias's SGD step (learn_from_gradient),
+        // unless the previous GEMM's epilogue took it already.
+        const bool defer_bias = layer.bias() && !bias_gradient && !this_bias_done;
 
         // Input gradient G * W^T (+ act' of the previous layer, fused).
         const bool skip_now = (residual_index && *residual_index == index) ||
@@ -417,6 +426,18 @@ Matrix MlpExecutor::backward(const std::vector<Matrix>& layer_inputs,
                         input_gradient_residual->cols() == input_gradient.cols(),
                     "input gradient residual shape");
             ep.residual = input_gradient_residual->slice();
+        }
+        // The epilogue's output is then exactly the previous layer's G: its
+        // column sums are that layer's bias gradient (linear.rs:267-272), and
+        // the bias takes its SGD step (linear.rs:385-390) in the same pass.
+        if (fuse_prev && prev->bias() && !ep.residual.ptr) {
+            if (bias_gradients) {
+                carried_bias = Vector(rt.get_uninit_buffer(prev->bias()->len()));
+                ep.col_sums_out = carried_bias->slice();
+            }
+            ep.col_sums_param = prev->bias()->slice();
+            ep.col_sums_lr = learning_rate;
+            bias_done = true;
         }
         rt.gemm_ex(nullptr, false, true, *layer_gradient, layer.weights(), input_gradient.slice(),
                    layer_gradient->rows(), layer.weights().rows(), layer.weights().cols(), ep);
@@ -442,7 +463,7 @@ Matrix MlpExecutor::backward(const std::vector<Matrix>& layer_inputs,
         } else {
             layer.learn_keep(layer_inputs[index], *layer_gradient,
                              bias_gradient ? &*bias_gradient : nullptr, learning_rate, wg, rt,
-                             nullptr);
+                             nullptr, /*bias_step=*/!this_bias_done);
         }
         if (bias_gradients) (*bias_gradients)[index] = std::move(bias_gradient);
 
@@ -809,6 +830,7 @@ Matrix Attention::backward_self(const Matrix& output_gradient, float learning_ra
 
     const size_t D = c.query.cols();
     Matrix query_gradient, key_gradient, value_gradient;
+    bool bias_taken[3] = {false, false, false};  // bias gradient and step already taken
     if (c.probabilities.len() == 0 && S > 0 && Sk > 0) {
         // Chunked: per chunk of query rows, P recomputed as in the forward,
         // then dP = R V^T, dV += P^T R, dS = softmax_bwd(P, dP) / sqrt(d),
@@ -846,13 +868,29 @@ Matrix Attention::backward_self(const Matrix& output_gradient, float learning_ra
                         D, n, acck, "dK");
         }
     } else {
+        // The projections' G are dQ, dK, dV themselves (identity activation):
+        // their bias gradients and SGD steps come from the column sums of
+        // the GEMMs that form them.
+        auto bias_sums = [&](int i) {
+            forge_gemm_epilogue ep = plain_epilogue();
+            Linear& lin = i == 0 ? qkv_.query() : i == 1 ? qkv_.key() : qkv_.value();
+            if (!lin.bias() || lin.needs_pre_activation()) return ep;
+            if (grads) {
+                grads->biases[i] = Vector(rt.get_uninit_buffer(lin.bias()->len()));
+                ep.col_sums_out = grads->biases[i]->slice();
+            }
+            ep.col_sums_param = lin.bias()->slice();
+            ep.col_sums_lr = learning_rate;
+            bias_taken[i] = true;
+            return ep;
+        };
         // dP = R V^T (NT), dV = P^T R (TN).
         Matrix probabilities_gradient = rt.new_uninit_matrix(S, Sk);
         rt.gemm_ex(nullptr, false, true, residual_gradient, c.value, probabilities_gradient.slice(),
                    S, Sk, H, plain_epilogue());
         value_gradient = rt.new_uninit_matrix(Sk, H);
         rt.gemm_ex(nullptr, true, false, c.probabilities, residual_gradient, value_gradient.slice(),
-                   Sk, H, S, plain_epilogue());
+                   Sk, H, S, bias_sums(2));
         // dS = softmax_bwd(P, dP) / sqrt(d), fused.
         Matrix score_gradient = rt.new_uninit_matrix(S, Sk);
         check(forge_softmax_rows_bwd_scaled(rt.raw(), nullptr, c.probabilities.slice(),
@@ -863,10 +901,10 @@ Matrix Attention::backward_self(const Matrix& output_gradient, float learning_ra
         // dQ = dS K (NN), dK = dS^T Q (TN).
         query_gradient = rt.new_uninit_matrix(S, D);
         rt.gemm_ex(nullptr, false, false, score_gradient, c.key, query_gradient.slice(), S, D, Sk,
-                   plain_epilogue());
+                   bias_sums(0));
         key_gradient = rt.new_uninit_matrix(Sk, D);
         rt.gemm_ex(nullptr, true, false, score_gradient, c.query, key_gradient.slice(), Sk, D, S,
-                   plain_epilogue());
+                   bias_sums(1));
         score_gradient = Matrix();
     }
 
@@ -879,6 +917,7 @@ Matrix Attention::backward_self(const Matrix& output_gradient, float learning_ra
         Linear& lin = *linears[i];
         std::optional<Matrix> g_owned;
         std::optional<Vector> db;
+        if (bias_taken[i] && grads) db = std::move(grads->biases[i]);
         const Matrix* g = projected[i];
         if (lin.needs_pre_activation()) {
             Matrix pre = lin.affine(c.input, nullptr, rt, nullptr);
@@ -887,7 +926,7 @@ Matrix Attention::backward_self(const Matrix& output_gradient, float learning_ra
             db = std::move(gb.second);
             g = &*g_owned;
         }
-        const bool defer_bias = lin.bias() && !db;
+        const bool defer_bias = lin.bias() && !db && !bias_taken[i];
         if (!projection_gradient) projection_gradient = lin.input_gradient(*g, rt, nullptr);
         else lin.input_gradient_accumulate(*g, *projection_gradient, rt, nullptr);
         Matrix* wg = nullptr;
@@ -899,7 +938,8 @@ Matrix Attention::backward_self(const Matrix& output_gradient, float learning_ra
             lin.learn_from_gradient(c.input, *g, learning_rate, wg, grads ? &db : nullptr, rt,
                                     nullptr);
         else
-            lin.learn_keep(c.input, *g, db ? &*db : nullptr, learning_rate, wg, rt, nullptr);
+            lin.learn_keep(c.input, *g, db ? &*db : nullptr, learning_rate, wg, rt, nullptr,
+                           /*bias_step=*/!bias_taken[i]);
         if (grads) grads->biases[i] = std::move(db);
     }
     if (input_gradient) {
