@@ -539,6 +539,24 @@ def profile_workload(rt, name, steps, warmup):
     if name == "rows65536":
         return {"workload": name,
                 "results": secondary_rows_at_scale(rt, steps, warmup, min_launches=1)}
+    if name == "sumcols":
+        # Column sums of the bias-gradient and norm-backward shapes, over
+        # rotating copies (at least 512 MiB, or two) so the MALL cannot
+        # serve them; the first-pass shape follows $OXFORGE_SUMCOL_LOADS and
+        # $OXFORGE_SUMCOL_BLOCKS when they are set.
+        res = {}
+        for rows, cols in ((4096, 1024), (4096, 2048), (65536, 1024), (4096, 8192)):
+            sets = max(2, min(32, (512 << 20) // (4 * rows * cols)))
+            xs = rotating(rt, (rows, cols), sets, 2)
+            out = rt.empty((cols,))
+            ms = time_launches(rt, lambda i: rt.sum_cols(xs[i % sets], out, rows, cols), steps,
+                               warmup)
+            res[f"{rows}x{cols}"] = {"us": round(ms * 1e3, 2),
+                                     "gbs": round(4 * rows * cols / (ms * 1e-3) / 1e9, 1)}
+            for b in xs + [out]:
+                b.recycle()
+        return {"workload": name, "loads": os.environ.get("OXFORGE_SUMCOL_LOADS", "default"),
+                "blocks": os.environ.get("OXFORGE_SUMCOL_BLOCKS", "default"), "results": res}
     raise SystemExit(f"unknown profile workload {name}")
 
 
@@ -656,7 +674,8 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--profile", default=None,
                     help="run only one workload (gemm4096, gemm8192x1024, gemms, ksweep, copy, "
-                         "transpose, rows, rows65536, c4, c5) for rocprofv3, or vendor (torch.mm "
+                         "transpose, rows, rows65536, sumcols, c4, c5) for rocprofv3, or vendor "
+                         "(torch.mm "
                          "on the same GEMM shapes, in a process without this build's runtime)")
     args = ap.parse_args()
 

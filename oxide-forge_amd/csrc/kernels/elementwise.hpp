@@ -460,6 +460,66 @@ __device__ __forceinline__ void sum_cols_final_v_body(const float* __restrict__ 
     if (s == 0 && in) colsum_store4(o, c, part[0][q]);
 }
 
+// Column sums, first pass over 16-byte aligned float4 columns.  Workgroup
+// (x, y) owns the 64 columns 64 x .. 64 x + 63 of the rows of chunk y:
+// thread t = 16 s + q sums the float4 column group q of rows s, s + 16,
+// s + 32, ... of the chunk in order (one chain per row slot s; LOADS loads
+// in flight per batch of 16 LOADS rows), then the 16 slots add by a halving
+// tree in LDS (slot s + st into s for st = 8, 4, 2, 1).  With one chunk
+// that is the result (stored with the SGD step, as the final passes do);
+// otherwise it is the chunk's partial row part[y, :], for
+// forge_sum_cols_final_v.  The order depends only on the shape.
+//
+// A one-launch form, in which the last workgroup of each column group to
+// finish adds the partial rows, needs every workgroup to release its
+// partial row at agent scope first; on gfx950 that release writes back the
+// XCD's L2, and the launch took 25-43 us at [4096,1024] against 7.7 us for
+// the two launches, so the partial rows go through a kernel boundary.
+constexpr int SUMCOL1_THREADS = 256;
+constexpr int SUMCOL1_COLS = 64;
+constexpr int SUMCOL1_SLOTS = SUMCOL1_THREADS / (SUMCOL1_COLS / 4);
+
+__device__ __forceinline__ float4 add4(float4 a, float4 b) {
+    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
+template <int LOADS>
+__device__ __forceinline__ void sum_cols_part_body(const float* __restrict__ m,
+                                                   float* __restrict__ part,
+                                                   const ColSumOut& o, int rows, int cols,
+                                                   int rows_per_chunk) {
+    __shared__ float4 red[SUMCOL1_SLOTS][SUMCOL1_COLS / 4];
+    const int q = threadIdx.x & 15, s = threadIdx.x >> 4;
+    const int c = blockIdx.x * SUMCOL1_COLS + 4 * q;
+    const bool in = c < cols;
+    const int r0 = blockIdx.y * rows_per_chunk;
+    const int r1 = min(rows, r0 + rows_per_chunk);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (in) {
+        for (int b = r0 + s; b < r1; b += SUMCOL1_SLOTS * LOADS) {
+            float4 v[LOADS];
+#pragma unroll
+            for (int j = 0; j < LOADS; j++) {
+                const int r = b + j * SUMCOL1_SLOTS;
+                v[j] = r < r1 ? load_stream(m + (long long)r * cols + c)
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int j = 0; j < LOADS; j++) acc = add4(acc, v[j]);
+        }
+    }
+    red[s][q] = acc;
+    __syncthreads();
+#pragma unroll
+    for (int st = SUMCOL1_SLOTS / 2; st > 0; st >>= 1) {
+        if (s < st) red[s][q] = add4(red[s][q], red[s + st][q]);
+        __syncthreads();
+    }
+    if (s != 0 || !in) return;
+    if (gridDim.y == 1) colsum_store4(o, c, red[0][q]);
+    else *reinterpret_cast<float4*>(part + (long long)blockIdx.y * cols + c) = red[0][q];
+}
+
 // Row statistics of the GEMM epilogue where the product's own kernel does
 // not form them (the bounds-guarded and split-K paths).
 // d[r] = sqrt(sum of part[r, 0..parts) / n + eps), the partials added in

@@ -285,6 +285,15 @@ FORGE_KERNEL void __launch_bounds__(SUMCOL_WAVES * 64) forge_sum_cols_s(const fl
                                                                        int rows_per_chunk) {
     sum_cols_body<false>(m, out, rows, cols, rows_per_chunk);
 }
+// Column sums, first pass over float4 columns, LOADS loads in flight per lane.
+#define SUM_COLS_PART_KERNEL(L)                                                                \
+    FORGE_KERNEL void __launch_bounds__(SUMCOL1_THREADS) forge_sum_cols_p##L(                  \
+        const float* m, float* part, ColSumOut o, int rows, int cols, int rows_per_chunk) {   \
+        sum_cols_part_body<L>(m, part, o, rows, cols, rows_per_chunk);                         \
+    }
+SUM_COLS_PART_KERNEL(4)
+SUM_COLS_PART_KERNEL(8)
+SUM_COLS_PART_KERNEL(16)
 // Final column-sum passes (ColSumOut: sums to `out`, and optionally the SGD
 // step of a parameter vector).  The *2 instances do two independent column
 // sums in one launch, blockIdx.y selecting the pair: dgamma and dbeta of the

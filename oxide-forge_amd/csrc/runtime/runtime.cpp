@@ -373,6 +373,8 @@ extern "C" forge_status forge_streams_create(forge_runtime* rt, size_t n, forge_
         auto* s = new forge_stream();
         if (hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking) != hipSuccess ||
             hipEventCreateWithFlags(&s->event, hipEventDisableTiming) != hipSuccess) {
+            if (s->event) (void)hipEventDestroy(s->event);
+            if (s->stream) (void)hipStreamDestroy(s->stream);
             delete s;
             return fail(FORGE_EHIP, "stream creation failed");
         }
@@ -1086,12 +1088,12 @@ int row_vpt(size_t cols, bool aligned) {
 
 // Column sums of m [rows, cols] into out [cols].  Matrices of at most 512
 // rows take one launch of forge_sum_cols_final (about 3 us on MI355X up to
-// that height, latency-bound); taller ones first reduce
-// chunks of rows into partial rows (forge_sum_cols_v/_s, up to about 8192
-// workgroups, >= 16 rows per chunk: [4096,8192] took 29.0 us this way
-// against 33.0 with 2048 workgroups), then sum the partial rows with
-// forge_sum_cols_final.  The chunking depends only on the shape, so the
-// result is deterministic.
+// that height, latency-bound); taller ones first reduce chunks of rows into
+// partial rows, then sum the partial rows with forge_sum_cols_final.  The
+// first pass is forge_sum_cols_p<loads> when m, the outputs and the columns
+// allow float4 throughout, else forge_sum_cols_v/_s (up to about 8192
+// workgroups, >= 16 rows per chunk).  The chunking depends only on the
+// shape, so the result is deterministic.
 constexpr int SUMCOL_FINAL_MAX_ROWS = 512;
 constexpr int SUMCOL_FINAL_V_THREADS = 256;  // elementwise.hpp SUMCOL_FINAL_V_THREADS
 constexpr int SUMCOL_FINAL_V_COLS = 16;      // elementwise.hpp SUMCOL_FINAL_V_COLS
@@ -1107,11 +1109,55 @@ size_t sum_cols_chunks(size_t rows, size_t cols, bool vec) {
 
 bool sum_cols_vec(const float* m, size_t cols) { return aligned16(m) && cols % 4 == 0; }
 
+// First pass of the float4 column sums (forge_sum_cols_p<loads>,
+// elementwise.hpp): workgroups of 64 columns by `rpc` rows, each lane
+// `loads` float4 loads in flight, about SUMCOL_PART_TARGET workgroups in
+// all and at most SUMCOL_PART_MAX_CHUNKS partial rows, so that
+// forge_sum_cols_final_v adds them in one round of loads.
+// $OXFORGE_SUMCOL_LOADS (4, 8 or 16) and $OXFORGE_SUMCOL_BLOCKS override the
+// two choices (tuning knobs).  On MI355X the sweep of 4/8/16 loads by
+// 256-4096 workgroups moved [4096,1024] only between 7.3 and 7.9 us (two
+// dependent launches), [65536,1024] between 43 and 47 us and [4096,8192]
+// between 25 and 27 us (the previous four-wave first pass: 29 us).
+constexpr int SUMCOL1_COLS = 64;   // elementwise.hpp SUMCOL1_COLS
+constexpr int SUMCOL1_SLOTS = 16;  // elementwise.hpp SUMCOL1_SLOTS
+constexpr size_t SUMCOL_PART_TARGET = 512;
+constexpr size_t SUMCOL_PART_MAX_CHUNKS = 256;
+
+struct SumColsPart {
+    int loads = 16;
+    int rpc = 0;
+    size_t chunks = 0;
+};
+
+long env_knob(const char* name) {
+    const char* v = getenv(name);
+    return v ? strtol(v, nullptr, 10) : 0L;
+}
+
+SumColsPart sum_cols_part_plan(size_t rows, size_t cols) {
+    static const long env_loads = env_knob("OXFORGE_SUMCOL_LOADS");
+    static const long env_blocks = env_knob("OXFORGE_SUMCOL_BLOCKS");
+    SumColsPart p;
+    if (env_loads == 4 || env_loads == 8 || env_loads == 16) p.loads = (int)env_loads;
+    const size_t target = env_blocks > 0 ? (size_t)env_blocks : SUMCOL_PART_TARGET;
+    const size_t gx = (cols + SUMCOL1_COLS - 1) / SUMCOL1_COLS;
+    const size_t batch = (size_t)SUMCOL1_SLOTS * p.loads;
+    const size_t batches = (rows + batch - 1) / batch;
+    size_t chunks = std::max<size_t>(1, target / gx);
+    chunks = std::min(chunks, std::min(batches, SUMCOL_PART_MAX_CHUNKS));
+    const size_t per = (batches + chunks - 1) / chunks;
+    p.rpc = (int)(per * batch);
+    p.chunks = (rows + (size_t)p.rpc - 1) / (size_t)p.rpc;
+    return p;
+}
+
 // Floats of scratch sum_cols_impl needs for this shape.
 size_t sum_cols_scratch(size_t rows, size_t cols) {
     size_t chunks = sum_cols_chunks(rows, cols, true);
     size_t chunks_s = sum_cols_chunks(rows, cols, false);
     size_t c = std::max(chunks, chunks_s);
+    if (c > 1) c = std::max(c, sum_cols_part_plan(rows, cols).chunks);
     return c > 1 ? c * cols : 0;
 }
 
@@ -1142,6 +1188,18 @@ forge_status sum_cols_impl(forge_runtime* rt, forge_stream* s, const float* m, C
     const bool vec = sum_cols_vec(m, cols);
     size_t chunks = sum_cols_chunks(rows, cols, vec);
     if (chunks == 1) return sum_cols_final_launch(rt, s, m, o, (int)rows, c);
+    if (sum_cols_final_vec(m, o, c)) {
+        // float4 first pass; a single chunk stores the sums itself.
+        const SumColsPart p = sum_cols_part_plan(rows, cols);
+        char name[40];
+        snprintf(name, sizeof name, "forge_sum_cols_p%d", p.loads);
+        int r = (int)rows;
+        const unsigned gx = (unsigned)((cols + SUMCOL1_COLS - 1) / SUMCOL1_COLS);
+        FORGE_TRY(launch_args(rt, s, name, dim3(gx, (unsigned)p.chunks), dim3(256), 0, m, scratch,
+                              o, r, c, p.rpc));
+        if (p.chunks == 1) return FORGE_OK;
+        return sum_cols_final_launch(rt, s, scratch, o, (int)p.chunks, c);
+    }
     int rpc = (int)((rows + chunks - 1) / chunks);
     chunks = (rows + rpc - 1) / rpc;
     int r = (int)rows;

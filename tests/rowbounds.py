@@ -141,7 +141,8 @@ def tolerance(bound, bar=1e-5):
 #   2. the register path adds its workgroup's waves in LDS, wave 0 first;
 #      the looping path keeps one partial row per wave;
 #   3. a final pass sums the partial rows (a further chunked pass first when
-#      there are more than 512 of them).
+#      there are more than 512 of them: the float4 first pass when the columns
+#      and outputs allow it).
 # The bound is the running error bound of that tree: every rounded addition
 # contributes at most u |s| for its exact result s (a first-order bound,
 # Higham, "Accuracy and Stability of Numerical Algorithms", 2nd ed., 4.2),
@@ -176,6 +177,53 @@ def _sum_cols_chunks(rows, cols, vec):
     want = max(1, 8192 // max(1, gx))
     by_rows = -(-rows // 16)
     return max(2, min(want, by_rows, 512))
+
+
+def _sum_cols_part_plan(rows, cols, loads=16, target=512):
+    """Grid of the float4 first pass (runtime.cpp sum_cols_part_plan):
+    (rows per chunk, chunks) for workgroups of 64 columns, 16 row slots and
+    `loads` loads per slot per batch."""
+    gx = -(-cols // 64)
+    batch = 16 * loads
+    batches = -(-rows // batch)
+    chunks = min(max(1, target // gx), batches, 256)
+    rpc = -(-batches // chunks) * batch
+    return rpc, -(-rows // rpc)
+
+
+def _uses_part(rows, cols, aligned):
+    """forge_sum_cols' float4 first pass: more than 512 rows of float4
+    columns, every operand 16-byte aligned (runtime.cpp sum_cols_impl)."""
+    return aligned and cols % 4 == 0 and _sum_cols_chunks(rows, cols, True) > 1
+
+
+def _halving(S, err):
+    """Halving tree over the first axis (slot s + st into s for st = n/2,
+    ..., 1): (sums, err plus every rounded partial sum)."""
+    st = S.shape[0] // 2
+    while st:
+        S = S[:st] + S[st:2 * st]
+        err = err + np.abs(S).sum(axis=0)
+        st //= 2
+    return S[0], err
+
+
+def _sum_cols_part(T):
+    """forge_sum_cols_p over T [rows, cols]: per chunk, 16 slot chains (rows
+    s, s + 16, ...) and a halving tree; with several chunks the final pass
+    over the partial rows.  Returns the sum of every rounded partial sum."""
+    rows, cols = T.shape
+    rpc, chunks = _sum_cols_part_plan(rows, cols)
+    err = np.zeros(cols)
+    parts = []
+    for r0 in range(0, rows, rpc):
+        S, e1 = _chains(T[r0:r0 + rpc], 16, False)
+        v, err = _halving(S, err + e1)
+        parts.append(v)
+    if chunks == 1:
+        return err
+    _, e2 = _final_pass(np.array(parts), True)
+    return err + e2
 
 
 def _chains(T, n_chains, first_rounds):
@@ -233,9 +281,13 @@ def column_sum_bound(T, exact, plan, out_aligned=True, fma=False):
     else:
         Pm = L1
     # The partial rows sit in aligned scratch: the chunk pass is float4 when
-    # cols % 4 == 0; the final pass also needs aligned outputs.
+    # cols % 4 == 0; the final pass and the one-launch form also need
+    # aligned outputs.
     vec = T.shape[1] % 4 == 0
     prow = Pm.shape[0]
+    if _uses_part(prow, T.shape[1], out_aligned):
+        err = err + _sum_cols_part(Pm)
+        return np.abs((T - np.asarray(exact, np.float64)).sum(axis=0)) + U * err
     chunks = _sum_cols_chunks(prow, T.shape[1], vec)
     if chunks > 1:
         rpc = -(-prow // chunks)
@@ -254,9 +306,12 @@ def column_sum_bound(T, exact, plan, out_aligned=True, fma=False):
 
 def sum_cols_bound(m, aligned=True):
     """Bound on forge_sum_cols of m [rows, cols] (exact f32 inputs): the
-    chunked first pass when rows > 512, then the final pass."""
+    float4 first pass for more than 512 aligned float4 rows, otherwise the
+    chunked first pass when rows > 512; then the final pass."""
     T = np.asarray(m, np.float64)
     rows, cols = T.shape
+    if _uses_part(rows, cols, aligned):
+        return U * _sum_cols_part(T)
     vec = aligned and cols % 4 == 0
     err = np.zeros(cols)
     Pm = T

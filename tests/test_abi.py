@@ -104,6 +104,7 @@ def dispatcher_kernel_names():
     names += ["forge_fill_v", "forge_fill_s", "forge_fill_seq", "forge_causal_mask",
               "forge_sum_cols_v", "forge_sum_cols_s", "forge_sum_cols_final", "forge_sum_cols_final2",
               "forge_sum_cols_final_v", "forge_sum_cols_final2_v",
+              "forge_sum_cols_p4", "forge_sum_cols_p8", "forge_sum_cols_p16",
               "forge_sum_rows_v", "forge_sum_rows_s", "forge_reduce_sum", "forge_reduce_max",
               "forge_reduce_sum_v", "forge_reduce_max_v",
               "forge_transpose", "forge_transpose_w", "forge_transpose_g"]

@@ -700,6 +700,42 @@ def test_sum_rows_cols(rt, rows, cols):
     assert np.allclose(dr.numpy(), orc.sum_rows(mf), atol=1e-5 * np.sqrt(cols) + 1e-6)
 
 
+# The float4 first pass of the column sums (more than 512 rows, 16-byte
+# aligned float4 columns and outputs): a partial last column group (100
+# columns), a short last chunk (1000 rows), a single chunk that stores the
+# sums itself (65600 columns), and the tall shapes.  Repeated calls, and
+# calls on forked streams with their own workspaces, agree bit for bit.
+@pytest.mark.parametrize("rows,cols", [(1000, 100), (513, 4), (520, 65600), (65536, 1024),
+                                       (4096, 2048)])
+def test_sum_cols_float4_first_pass(rt, rows, cols):
+    say(f"sum_cols float4 first pass {rows}x{cols}")
+    mf = synth.normal((rows, cols), 9)
+    dm = rt.array(mf)
+    first = rt.empty((cols,))
+    rt.sum_cols(dm, first, rows, cols)
+    ref = first.numpy()
+    within_cols(ref, orc.sum_cols(mf), rb.tolerance(rb.sum_cols_bound(mf)), "sum_cols")
+    out = rt.empty((cols,))
+    for _ in range(3):
+        rt.sum_cols(dm, out, rows, cols)
+        assert np.array_equal(out.numpy(), ref)
+    streams = rt.streams_create(2)
+    outs = [rt.empty((cols,)) for _ in streams]
+    rt.streams_fork(streams)
+    for s, o in zip(streams, outs):
+        rt.sum_cols(dm, o, rows, cols, stream=s)
+        rt.sum_cols(dm, o, rows, cols, stream=s)
+    rt.streams_join(streams)
+    for o in outs:
+        assert np.array_equal(o.numpy(), ref)
+    # the SGD form writes the same sums and steps the parameter with them
+    par0 = synth.normal((cols,), 10)
+    par = rt.array(par0)
+    rt.sum_cols_sgd(dm, rows, cols, 0.25, out=out, param=par)
+    assert np.array_equal(out.numpy(), ref)
+    assert np.array_equal(par.numpy(), par0 - np.float32(0.25) * ref)
+
+
 @pytest.mark.parametrize("n", [1, 1000, 4096 * 1024, 10_000_019])
 def test_reduce_sum_max(rt, n):
     say(f"reduce n={n}")

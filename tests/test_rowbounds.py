@@ -125,6 +125,28 @@ def test_planted_mistakes_exceed_tolerance(cols):
         assert (np.abs(wrong - ref) / tol).max() > 50, name
 
 
+def _slots_f32(blk, n=16):
+    """n slot chains (rows s, s + n, ...) in f32, then the halving tree."""
+    f = np.float32
+    s = np.zeros((n, blk.shape[1]), f)
+    for r in range(blk.shape[0]):
+        s[r % n] = (s[r % n] + blk[r]).astype(f)
+    st = n // 2
+    while st:
+        s = (s[:st] + s[st:2 * st]).astype(f)
+        st //= 2
+    return s[0]
+
+
+def _sum_cols_part_f32(acc):
+    """forge_sum_cols_p in f32: per chunk the slot chains and tree, then the
+    float4 final pass (64 slots and the halving tree) over the partial rows."""
+    rows, cols = acc.shape
+    rpc, chunks = rb._sum_cols_part_plan(rows, cols)
+    parts = np.array([_slots_f32(acc[r0:r0 + rpc]) for r0 in range(0, rows, rpc)])
+    return parts[0] if chunks == 1 else _slots_f32(parts, 64)
+
+
 def _tree_f32(T, plan, fma, out_aligned=True):
     """The kernels' column-sum tree evaluated in f32 (the order of
     rowbounds.column_sum_bound): wave chains (each step one rounding: a
@@ -151,6 +173,8 @@ def _tree_f32(T, plan, fma, out_aligned=True):
             t = (t + acc[:, w]).astype(f)
         acc = t
     prow = acc.shape[0]
+    if rb._uses_part(prow, cols, out_aligned):
+        return _sum_cols_part_f32(acc)
     chunks = rb._sum_cols_chunks(prow, cols, cols % 4 == 0)
     if chunks > 1:
         # first pass: chunks of rpc rows, four waves of rows r0 + w, r0 + w + 4,
@@ -185,7 +209,7 @@ def _tree_f32(T, plan, fma, out_aligned=True):
 
 
 @pytest.mark.parametrize("rows,cols,aligned", [(4096, 256, True), (600, 1001, False),
-                                               (70, 64, True)])
+                                               (70, 64, True), (3000, 2560, True)])
 def test_column_sum_bound_covers_f32_tree_and_catches_a_dropped_row(rows, cols, aligned):
     """dgamma / dbeta bounds (rowbounds.layer_norm_param_bounds): the f32
     evaluation of the kernels' summation tree over the kernels' own f32 xhat
