@@ -552,6 +552,10 @@ public:
                       Matrix* pre_activation = nullptr);
     // The GEMM of forward_into as a batch entry (bias and activation fused).
     forge_gemm_problem forward_problem(const Matrix& input, Matrix& output) const;
+    // The weight-update GEMM of learn_keep as a batch entry (W -= lr X^T G,
+    // dW into *weight_gradient when given); the bias is not touched.
+    forge_gemm_problem learn_problem(const Matrix& input, const Matrix& gradient,
+                                     float learning_rate, Matrix* weight_gradient);
     // learn that also stores dW (and db) when given, for explicit gradients.
     void learn_keep(const Matrix& input, const Matrix& gradient, const Vector* bias_gradient,
                     float learning_rate, Matrix* weight_gradient, CudaRuntime& rt,

@@ -193,6 +193,27 @@ Vector Linear::loss_rows(const Matrix& output, const Matrix& target, CudaRuntime
     return row_loss;
 }
 
+forge_gemm_problem Linear::learn_problem(const Matrix& input, const Matrix& gradient,
+                                         float learning_rate, Matrix* weight_gradient) {
+    require(input.rows() == gradient.rows(), "input.rows() == gradient.rows()");
+    require(input.cols() == weights_.rows() && gradient.cols() == weights_.cols(),
+            "learn shapes");
+    forge_gemm_problem pr{};
+    pr.A = input.slice();
+    pr.B = gradient.slice();
+    pr.C = weights_.slice();
+    pr.epilogue = plain_epilogue();
+    pr.epilogue.update = 1;
+    pr.epilogue.update_scale = learning_rate;
+    if (weight_gradient) {
+        require(weight_gradient->rows() == weights_.rows() &&
+                    weight_gradient->cols() == weights_.cols(),
+                "weight gradient shape");
+        pr.epilogue.pre_out = weight_gradient->slice();
+    }
+    return pr;
+}
+
 void Linear::learn_keep(const Matrix& input, const Matrix& gradient, const Vector* bias_gradient,
                         float learning_rate, Matrix* weight_gradient, CudaRuntime& rt,
                         const CudaStream* stream, bool bias_step) {
@@ -913,7 +934,38 @@ Matrix Attention::backward_self(const Matrix& output_gradient, float learning_ra
     std::optional<Matrix> projection_gradient;
     Linear* linears[3] = {&qkv_.query(), &qkv_.key(), &qkv_.value()};
     const Matrix* projected[3] = {&query_gradient, &key_gradient, &value_gradient};
-    for (int i = 0; i < 3; i++) {
+    // With identity projections of one weight shape whose biases (if any)
+    // took their step in the epilogues above, the three weight updates are
+    // one batched launch after the three input gradients.  Each input
+    // gradient reads only its own W, so the order of updates and input
+    // gradients does not change a result.
+    bool batch = true;
+    for (int i = 0; i < 3; i++)
+        batch = batch && !linears[i]->needs_pre_activation() &&
+                (!linears[i]->bias() || bias_taken[i]) &&
+                linears[i]->weights().rows() == linears[0]->weights().rows() &&
+                linears[i]->weights().cols() == linears[0]->weights().cols();
+    if (batch) {
+        forge_gemm_problem probs[3];
+        for (int i = 0; i < 3; i++) {
+            Linear& lin = *linears[i];
+            if (!projection_gradient)
+                projection_gradient = lin.input_gradient(*projected[i], rt, nullptr);
+            else
+                lin.input_gradient_accumulate(*projected[i], *projection_gradient, rt, nullptr);
+            Matrix* wg = nullptr;
+            if (grads) {
+                grads->weights[i] =
+                    rt.new_uninit_matrix(lin.weights().rows(), lin.weights().cols());
+                wg = &grads->weights[i];
+            }
+            probs[i] = lin.learn_problem(c.input, *projected[i], learning_rate, wg);
+        }
+        check(forge_gemm_batch_f32(rt.raw(), nullptr, 1, 0, linears[0]->weights().rows(),
+                                   linears[0]->weights().cols(), c.input.rows(), 3, probs),
+              "qkv weight updates");
+    }
+    for (int i = 0; i < 3 && !batch; i++) {
         Linear& lin = *linears[i];
         std::optional<Matrix> g_owned;
         std::optional<Vector> db;
