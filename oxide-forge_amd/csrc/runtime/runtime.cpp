@@ -1115,10 +1115,10 @@ bool sum_cols_vec(const float* m, size_t cols) { return aligned16(m) && cols % 4
 // all and at most SUMCOL_PART_MAX_CHUNKS partial rows, so that
 // forge_sum_cols_final_v adds them in one round of loads.
 // $OXFORGE_SUMCOL_LOADS (4, 8 or 16) and $OXFORGE_SUMCOL_BLOCKS override the
-// two choices (tuning knobs).  On MI355X the sweep of 4/8/16 loads by
-// 256-4096 workgroups moved [4096,1024] only between 7.3 and 7.9 us (two
-// dependent launches), [65536,1024] between 43 and 47 us and [4096,8192]
-// between 25 and 27 us (the previous four-wave first pass: 29 us).
+// two choices (tuning knobs).  On MI355X a sweep of 4/8/16 loads by
+// 256-2048 workgroups kept [4096,1024] at 7.4-8.3 us (two dependent
+// launches); 16 loads by 512 is within 1% of the best there and at
+// [4096,2048], 3-4% behind it at [65536,1024] and [4096,8192].
 constexpr int SUMCOL1_COLS = 64;   // elementwise.hpp SUMCOL1_COLS
 constexpr int SUMCOL1_SLOTS = 16;  // elementwise.hpp SUMCOL1_SLOTS
 constexpr size_t SUMCOL_PART_TARGET = 512;
