@@ -15,9 +15,9 @@ and the transformer executors when built.
 The CPU baseline is the C mirror (oracle/oxforge_oracle.c: f64-accumulate
 GEMM, row kernels) on bounded samples of the same workloads, one thread per
 CPU the host grants this process (nproc and the share are both reported);
-with the secondary figures, the transformer layer's host tokens/s (C4
-forward through the C mirror, C5 training step through oracle/executors.py
-in numpy float64) is reported beside the GPU's.  Inputs come from
+with the secondary figures, the transformer layer's host tokens/s (one C4
+forward and one C5 training step of the C mirror) is reported beside the
+GPU's.  Inputs come from
 oxforge.synth; the oracle is imported only by the CPU legs.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
@@ -350,15 +350,12 @@ def host_cpus() -> dict:
 
 def cpu_transformer_baseline():
     """The transformer layer on the host, on the same synthetic inputs as the
-    GPU runs, one thread per usable CPU:
-      - C4 forward: the C mirror (oracle/oxforge_oracle.c kernels composed in
-        the reference's launch order, f32 with f64-accumulated products);
-      - C5 training step: oracle/executors.py forward + backward (numpy
-        float64 over the host BLAS; the C mirror has no backward composition).
-    A reported baseline, not the optimisation target."""
-    from threadpoolctl import threadpool_info, threadpool_limits
-
-    from oracle import executors as ex
+    GPU runs, one thread per usable CPU: the C mirror (oracle/oxforge_oracle.c
+    kernels composed in the reference's launch order, f32 with f64-accumulated
+    products) for one C4 forward (oracle.transformer_forward) and one C5
+    training step, forward, backward and every SGD step
+    (oracle.transformer_training_step).  A reported baseline, not the
+    optimisation target."""
     from oracle import oracle as orc
 
     cpus = host_cpus()
@@ -371,22 +368,17 @@ def cpu_transformer_baseline():
     t0 = time.perf_counter()
     orc.transformer_forward(p, X, rms=True)
     c4 = time.perf_counter() - t0
-    with threadpool_limits(limits=threads, user_api="blas"):
-        used = max([i["num_threads"] for i in threadpool_info() if i["user_api"] == "blas"],
-                   default=1)
-        S, H, F, O = 4096, 2048, 8192, 2048
-        p = transformer_params(S, H, F, O, 5, True)
-        X, dY = synth.normal((S, H), 5), synth.normal((S, O), 6)
-        t0 = time.perf_counter()
-        _, cache = ex.transformer_forward(p, X, ex.LAYER)
-        ex.transformer_backward(p, cache, dY, ex.LAYER)
-        c5 = time.perf_counter() - t0
+    S, H, F, O = 4096, 2048, 8192, 2048
+    p = transformer_params(S, H, F, O, 5, True)
+    X, dY = synth.normal((S, H), 5), synth.normal((S, O), 6)
+    t0 = time.perf_counter()
+    orc.transformer_training_step(p, X, dY, 1e-3, rms=False)
+    c5 = time.perf_counter() - t0
     out["c4_inference_tokens_per_s"] = round(2048 / c4, 1)
     out["c5_training_tokens_per_s"] = round(4096 / c5, 1)
     out.update({"cores": threads, "nproc": cpus["nproc"], "kind": "port",
-                "sample": f"one C4 forward of the C mirror ({c4:.1f} s, {threads} threads) and "
-                          f"one C5 training step of oracle/executors.py ({c5:.1f} s, numpy "
-                          f"float64, {used} BLAS threads)"})
+                "sample": f"one C4 forward ({c4:.1f} s) and one C5 training step ({c5:.1f} s) "
+                          f"of the C mirror, {threads} threads"})
     return out
 
 

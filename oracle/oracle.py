@@ -257,3 +257,120 @@ def transformer_forward(p, X, rms=True):
     f = linear(linear(h1, p["W1"], p.get("B1"), MAP_GELU), p["W2"], p.get("B2"))
     h2 = norm(binary(h1, f, ADD))
     return linear(h2, p["WO"], p.get("BO"))
+
+
+# ---------------------------------------------------------- training step
+def transformer_training_step(p, X, dY, lr, rms=False):
+    """One TrainingTransformer step as the reference launches it: forward
+    (encoder.rs:114-131, attention.rs:258-281), backward (encoder.rs:133-186;
+    the output and FFN layers through Linear::backward / input_gradient /
+    learn, linear.rs:232-306, 350-444, with the FFN pre-activation recomputed
+    as mlp.rs:136-139 does; attention.rs:283-321 and the Q/K/V projections of
+    attention.rs:104-144) and every SGD step, each step one C kernel above in
+    f32 with f64-accumulated products, transposes materialised where the
+    reference materialises them.  Norms take the gamma/beta extension (G1,
+    BE1, G2, BE2 in p, None for the reference's parameterless norm).
+
+    Returns (output, dX, grads, new_params): grads keyed like p (each
+    parameter's gradient before its update), new_params the parameters after
+    the step.  The multithreaded host mirror of the C5 layer that bench.py
+    times."""
+    def norm_fwd(x, g, b):
+        return rms_norm(x, g) if rms else layer_norm(x, g, b)
+
+    def norm_bwd(x, dy, g):
+        if rms:
+            dx, dg = rms_norm_backward(x, dy, g, want_params=True)
+            return dx, dg, None
+        return layer_norm_backward(x, dy, g, want_params=True)
+
+    def affine(x, w, b):
+        z = gemm(x, w)
+        return binary_assign_by_rows(z, b, ADD) if b is not None else z
+
+    def sgd(param, grad):
+        # clone, scale by lr, subtract (linear.rs:385-390, encoder.rs:180-184)
+        return binary(param, map_(grad, MAP_SCALE, float(lr)), SUB)
+
+    def bias_grad(g):
+        # transpose, then sum_rows (linear.rs:267-272)
+        return sum_rows(transpose(g))
+
+    def input_gradient(g, w):
+        return gemm(g, transpose(w))  # linear.rs:417-444
+
+    def weight_gradient(x, g):
+        return gemm(transpose(x), g)  # linear.rs:373-384
+
+    grads, new = {}, dict(p)
+    # forward
+    xp = binary(X, p["POS"], ADD)
+    q = affine(xp, p["WQ"], p.get("BQ"))
+    k = affine(xp, p["WK"], p.get("BK"))
+    v = affine(xp, p["WV"], p.get("BV"))
+    scale = float(1.0 / np.sqrt(np.float32(q.shape[1])))
+    pmat = softmax_rows(map_(gemm(q, transpose(k)), MAP_SCALE, scale))
+    pre1 = binary(xp, gemm(pmat, v), ADD)
+    out1 = norm_fwd(pre1, p.get("G1"), p.get("BE1"))
+    h1 = map_(affine(out1, p["W1"], p.get("B1")), MAP_GELU)
+    pre2 = binary(out1, affine(h1, p["W2"], p.get("B2")), ADD)
+    enc = norm_fwd(pre2, p.get("G2"), p.get("BE2"))
+    out = affine(enc, p["WO"], p.get("BO"))
+
+    # output projection (identity activation)
+    g_o = np.array(dY, np.float32, copy=True)
+    if p.get("BO") is not None:
+        grads["BO"] = bias_grad(g_o)
+    d_enc = input_gradient(g_o, p["WO"])
+    grads["WO"] = weight_gradient(enc, g_o)
+    new["WO"] = sgd(p["WO"], grads["WO"])
+    if p.get("BO") is not None:
+        new["BO"] = sgd(p["BO"], grads["BO"])
+    second, grads["G2"], grads["BE2"] = norm_bwd(pre2, d_enc, p.get("G2"))
+
+    # FFN: layer 2 (identity), then layer 1 (GELU, pre-activation recomputed)
+    g2 = second.copy()
+    if p.get("B2") is not None:
+        grads["B2"] = bias_grad(g2)
+    dh1 = input_gradient(g2, p["W2"])
+    grads["W2"] = weight_gradient(h1, g2)
+    new["W2"] = sgd(p["W2"], grads["W2"])
+    if p.get("B2") is not None:
+        new["B2"] = sgd(p["B2"], grads["B2"])
+    z1 = affine(out1, p["W1"], p.get("B1"))
+    g1 = binary(dh1, map_(z1, MAP_GELU_D), MUL)
+    if p.get("B1") is not None:
+        grads["B1"] = bias_grad(g1)
+    d_out1 = input_gradient(g1, p["W1"])
+    grads["W1"] = weight_gradient(out1, g1)
+    new["W1"] = sgd(p["W1"], grads["W1"])
+    if p.get("B1") is not None:
+        new["B1"] = sgd(p["B1"], grads["B1"])
+    first = binary(second, d_out1, ADD)
+
+    # attention
+    r, grads["G1"], grads["BE1"] = norm_bwd(pre1, first, p.get("G1"))
+    dp = gemm(r, transpose(v))
+    dv = gemm(transpose(pmat), r)
+    ds = map_(softmax_rows_backward(pmat, dp), MAP_SCALE, scale)
+    dq = gemm(ds, k)
+    dk = gemm(transpose(ds), q)
+    proj = None
+    for w, b, g in (("WQ", "BQ", dq), ("WK", "BK", dk), ("WV", "BV", dv)):
+        if p.get(b) is not None:
+            grads[b] = bias_grad(g)
+        ig = input_gradient(g, p[w])
+        proj = ig if proj is None else binary(proj, ig, ADD)
+        grads[w] = weight_gradient(xp, g)
+        new[w] = sgd(p[w], grads[w])
+        if p.get(b) is not None:
+            new[b] = sgd(p[b], grads[b])
+    dxp = binary(r, proj, ADD)
+    grads["POS"] = dxp
+    new["POS"] = sgd(p["POS"], dxp)
+    for n in ("G1", "BE1", "G2", "BE2"):
+        if p.get(n) is None:
+            grads[n] = None
+        elif grads.get(n) is not None:
+            new[n] = sgd(p[n], grads[n])
+    return out, dxp, grads, new

@@ -77,64 +77,98 @@ typedef struct {
 
 /* C[i,j] = sum_k opA[i,k] * opB[k,j], f64 accumulate.  The reference kernel
  * (gemm.rs:15-129 strict fp32; gemm.rs:202-373 TF32) overwrites C with the
- * product and takes no alpha/beta (gemm.rs:117-128, 362-372). */
-static void gemm_rows(void *p, size_t i0, size_t i1) {
+ * product and takes no alpha/beta (gemm.rs:117-128, 362-372).  Every output
+ * sums k = 0 .. K-1 in order; the loops are blocked over GEMM_RB rows and
+ * GEMM_CB columns (each B row segment serves GEMM_RB rows from cache), which
+ * changes no sum.  Work is split over blocks of GEMM_RB rows. */
+#define GEMM_RB ((size_t)8)
+#define GEMM_CB ((size_t)256)
+
+static void gemm_rows(void *p, size_t b0, size_t b1) {
     gemm_ctx *g = (gemm_ctx *)p;
     const size_t M = g->M, N = g->N, K = g->K;
-    double *acc = (double *)malloc(N * sizeof(double));
-    if (!acc) abort();
-    for (size_t i = i0; i < i1; i++) {
-        if (!g->tb) {
-            /* i-k-j order: a contiguous sweep over a row of B. */
-            memset(acc, 0, N * sizeof(double));
-            for (size_t k = 0; k < K; k++) {
-                double a = g->ta ? (double)g->A[k * M + i]
-                                 : (double)g->A[i * K + k];
-                const float *brow = g->B + k * N;
-                for (size_t j = 0; j < N; j++) acc[j] += a * (double)brow[j];
-            }
-        } else {
-            /* B stored [N,K]: each output is a contiguous dot product. */
-            for (size_t j = 0; j < N; j++) {
-                const float *bcol = g->B + j * K;
-                double s = 0.0;
-                if (!g->ta) {
-                    const float *arow = g->A + i * K;
-                    for (size_t k = 0; k < K; k++)
-                        s += (double)arow[k] * (double)bcol[k];
-                } else {
-                    for (size_t k = 0; k < K; k++)
-                        s += (double)g->A[k * M + i] * (double)bcol[k];
+    double acc[GEMM_RB][GEMM_CB];
+    for (size_t blk = b0; blk < b1; blk++) {
+        const size_t i0 = blk * GEMM_RB, ni = i0 + GEMM_RB <= M ? GEMM_RB : M - i0;
+        for (size_t j0 = 0; j0 < N; j0 += GEMM_CB) {
+            const size_t nj = j0 + GEMM_CB <= N ? GEMM_CB : N - j0;
+            for (size_t ii = 0; ii < ni; ii++)
+                for (size_t jj = 0; jj < nj; jj++) acc[ii][jj] = 0.0;
+            if (!g->tb) {
+                for (size_t k = 0; k < K; k++) {
+                    const float *brow = g->B + k * N + j0;
+                    for (size_t ii = 0; ii < ni; ii++) {
+                        const size_t i = i0 + ii;
+                        const double a = g->ta ? (double)g->A[k * M + i]
+                                               : (double)g->A[i * K + k];
+                        for (size_t jj = 0; jj < nj; jj++) acc[ii][jj] += a * (double)brow[jj];
+                    }
                 }
-                acc[j] = s;
+            } else {
+                /* B stored [N,K]: each output is a contiguous dot product. */
+                for (size_t ii = 0; ii < ni; ii++) {
+                    const size_t i = i0 + ii;
+                    for (size_t jj = 0; jj < nj; jj++) {
+                        const float *bcol = g->B + (j0 + jj) * K;
+                        double s2 = 0.0;
+                        for (size_t k = 0; k < K; k++) {
+                            const double a = g->ta ? (double)g->A[k * M + i]
+                                                   : (double)g->A[i * K + k];
+                            s2 += a * (double)bcol[k];
+                        }
+                        acc[ii][jj] = s2;
+                    }
+                }
+            }
+            for (size_t ii = 0; ii < ni; ii++) {
+                const size_t i = i0 + ii;
+                if (g->C)
+                    for (size_t jj = 0; jj < nj; jj++) g->C[i * N + j0 + jj] = (float)acc[ii][jj];
+                if (g->C64)
+                    for (size_t jj = 0; jj < nj; jj++) g->C64[i * N + j0 + jj] = acc[ii][jj];
             }
         }
-        if (g->C)
-            for (size_t j = 0; j < N; j++) g->C[i * N + j] = (float)acc[j];
-        if (g->C64)
-            for (size_t j = 0; j < N; j++) g->C64[i * N + j] = acc[j];
     }
-    free(acc);
 }
 
 void orc_gemm(const float *A, const float *B, float *C, size_t M, size_t N,
               size_t K, int trans_a, int trans_b) {
     gemm_ctx g = {A, B, C, NULL, M, N, K, trans_a, trans_b};
-    parallel_rows(M, gemm_rows, &g);
+    parallel_rows((M + GEMM_RB - 1) / GEMM_RB, gemm_rows, &g);
 }
 
 void orc_gemm_f64(const float *A, const float *B, double *C, size_t M,
                   size_t N, size_t K, int trans_a, int trans_b) {
     gemm_ctx g = {A, B, NULL, C, M, N, K, trans_a, trans_b};
-    parallel_rows(M, gemm_rows, &g);
+    parallel_rows((M + GEMM_RB - 1) / GEMM_RB, gemm_rows, &g);
 }
 
 /* -------------------------------------------------------------- transpose */
 
+typedef struct {
+    const float *in;
+    float *out;
+    size_t rows, cols;
+} transpose_ctx;
+
+/* Bands of 32 input rows, 32 x 32 blocks within a band (pure data
+ * movement: any order gives the same result). */
+static void transpose_bands(void *p, size_t b0, size_t b1) {
+    transpose_ctx *t = (transpose_ctx *)p;
+    for (size_t b = b0; b < b1; b++) {
+        const size_t r0 = b * 32, r1 = r0 + 32 < t->rows ? r0 + 32 : t->rows;
+        for (size_t c0 = 0; c0 < t->cols; c0 += 32) {
+            const size_t c1 = c0 + 32 < t->cols ? c0 + 32 : t->cols;
+            for (size_t r = r0; r < r1; r++)
+                for (size_t c = c0; c < c1; c++) t->out[c * t->rows + r] = t->in[r * t->cols + c];
+        }
+    }
+}
+
 void orc_transpose(const float *in, float *out, size_t rows, size_t cols) {
     /* layout.rs:29,46-51: out[c * rows + r] = in[r * cols + c]. */
-    for (size_t r = 0; r < rows; r++)
-        for (size_t c = 0; c < cols; c++) out[c * rows + r] = in[r * cols + c];
+    transpose_ctx t = {in, out, rows, cols};
+    parallel_rows((rows + 31) / 32, transpose_bands, &t);
 }
 
 /* --------------------------------------------------------------- row ops */
@@ -356,12 +390,32 @@ static float apply_binary(float l, float r, int op) {
     }
 }
 
+/* Element-wise ops run over chunks of ELEM_CHUNK elements on the worker
+ * threads; each element is computed alone, so the split changes nothing. */
+#define ELEM_CHUNK ((size_t)65536)
+
+typedef struct {
+    const float *l, *r;
+    float *o;
+    size_t n;
+    int op;
+    float p0;
+} elem_ctx;
+
+static void binary_chunks(void *p, size_t c0, size_t c1) {
+    elem_ctx *e = (elem_ctx *)p;
+    const size_t i1 = c1 * ELEM_CHUNK < e->n ? c1 * ELEM_CHUNK : e->n;
+    for (size_t i = c0 * ELEM_CHUNK; i < i1; i++) e->o[i] = apply_binary(e->l[i], e->r[i], e->op);
+}
+
 void orc_binary(const float *l, const float *r, float *o, size_t n, int op) {
-    for (size_t i = 0; i < n; i++) o[i] = apply_binary(l[i], r[i], op);
+    elem_ctx e = {l, r, o, n, op, 0.f};
+    parallel_rows((n + ELEM_CHUNK - 1) / ELEM_CHUNK, binary_chunks, &e);
 }
 
 void orc_binary_assign(float *t, const float *r, size_t n, int op) {
-    for (size_t i = 0; i < n; i++) t[i] = apply_binary(t[i], r[i], op);
+    elem_ctx e = {t, r, t, n, op, 0.f};
+    parallel_rows((n + ELEM_CHUNK - 1) / ELEM_CHUNK, binary_chunks, &e);
 }
 
 /* row.rs:179-191: M[i] = M[i] op row[i mod cols]. */
@@ -404,14 +458,29 @@ static float map_one(float x, int op, float p0) {
     }
 }
 
+static void map_chunks(void *p, size_t c0, size_t c1) {
+    elem_ctx *e = (elem_ctx *)p;
+    const size_t i1 = c1 * ELEM_CHUNK < e->n ? c1 * ELEM_CHUNK : e->n;
+    for (size_t i = c0 * ELEM_CHUNK; i < i1; i++) e->o[i] = map_one(e->o[i], e->op, e->p0);
+}
+
 void orc_map(float *x, size_t n, int op, float p0) {
-    for (size_t i = 0; i < n; i++) x[i] = map_one(x[i], op, p0);
+    elem_ctx e = {NULL, NULL, x, n, op, p0};
+    parallel_rows((n + ELEM_CHUNK - 1) / ELEM_CHUNK, map_chunks, &e);
+}
+
+static void activation_backward_chunks(void *p, size_t c0, size_t c1) {
+    elem_ctx *e = (elem_ctx *)p;
+    const size_t i1 = c1 * ELEM_CHUNK < e->n ? c1 * ELEM_CHUNK : e->n;
+    /* derivative = act'(z) rounded to f32, then gradient * derivative. */
+    for (size_t i = c0 * ELEM_CHUNK; i < i1; i++)
+        e->o[i] = e->l[i] * map_one(e->r[i], e->op, 0.f);
 }
 
 void orc_activation_backward(const float *dy, const float *z, float *g,
                              size_t n, int derivative_op) {
-    /* derivative = act'(z) rounded to f32, then gradient * derivative. */
-    for (size_t i = 0; i < n; i++) g[i] = dy[i] * map_one(z[i], derivative_op, 0.f);
+    elem_ctx e = {dy, z, g, n, derivative_op, 0.f};
+    parallel_rows((n + ELEM_CHUNK - 1) / ELEM_CHUNK, activation_backward_chunks, &e);
 }
 
 /* ------------------------------------------------------------- reductions */

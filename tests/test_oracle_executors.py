@@ -169,3 +169,44 @@ def test_c_mirror_block_forward_matches_f64_executor(rms):
     ref, _ = ex.transformer_forward(p, X, ex.RMS if rms else ex.LAYER)
     assert got.shape == (S, O)
     assert np.max(np.abs(got - ref)) <= 1e-5 * max(1.0, np.abs(ref).max())
+
+
+@pytest.mark.parametrize("rms,affine,bias", [(False, True, True), (True, True, True),
+                                             (False, False, True), (True, False, False)])
+def test_c_mirror_training_step_matches_f64_executor(rms, affine, bias):
+    """The C-kernel composition of the training step
+    (oracle.transformer_training_step, timed by bench.py as the C5 host
+    baseline) equals the f64 executor oracle to f32 rounding on the output,
+    the input gradient and every parameter gradient, and each new parameter
+    is the old one minus lr times its gradient with the reference's two
+    roundings (scale, then subtract)."""
+    from oracle import oracle as orc
+
+    S, H, F, O = 24, 16, 40, 12
+    p64 = params(S, H, F, O, seed=5, affine=affine, bias=bias)
+    if rms:
+        p64["BE1"] = p64["BE2"] = None
+    p = {k: (None if v is None else v.astype(np.float32)) for k, v in p64.items()}
+    X = rnd(11, S, H, scale=1.0).astype(np.float32)
+    dY = rnd(12, S, O, scale=1.0).astype(np.float32)
+    lr = np.float32(0.01)
+    kind = ex.RMS if rms else ex.LAYER
+    out, dx, grads, new = orc.transformer_training_step(p, X, dY, float(lr), rms=rms)
+    ref, cache = ex.transformer_forward(p, X, kind)
+    rdx, rg = ex.transformer_backward(p, cache, dY, kind)
+
+    def close(a, b):
+        return np.max(np.abs(a - b)) <= 1e-5 * max(1.0, np.abs(b).max())
+
+    assert close(out, ref)
+    assert close(dx, rdx)
+    for k in p:
+        if p[k] is None:
+            assert grads.get(k) is None, k
+            continue
+        if k == "BK":
+            # identically zero in exact arithmetic (softmax shift invariance)
+            assert np.max(np.abs(grads[k])) <= 1e-5 * max(1.0, np.abs(rg["BV"]).max())
+        else:
+            assert close(grads[k], rg[k]), k
+        assert np.array_equal(new[k], p[k] - lr * grads[k]), k
