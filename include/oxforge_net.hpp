@@ -764,8 +764,12 @@ public:
                             Matrix& row_sumsq, CudaRuntime& rt);
     // With `input_gradient` given, the returned gradient is written there
     // (same shape as the attention input) and an empty Matrix is returned.
+    // With `position` given (the training block's position matrix, same
+    // shape), the product that completes the input gradient dXp also applies
+    // position -= learning_rate * dXp (encoder.rs:180-184) in its epilogue.
     Matrix backward_self(const Matrix& output_gradient, float learning_rate, CudaRuntime& rt,
-                         TransformerGrads* grads = nullptr, Matrix* input_gradient = nullptr);
+                         TransformerGrads* grads = nullptr, Matrix* input_gradient = nullptr,
+                         Matrix* position = nullptr);
     void normalize(Matrix& m, CudaRuntime& rt, const Normalization* norm = nullptr) const;
     Normalization& normalization() { return norm_; }
     QkvProjection& qkv() { return qkv_; }

@@ -835,7 +835,7 @@ Matrix Attention::forward_self_training(Matrix input, CudaRuntime& rt) {
 
 Matrix Attention::backward_self(const Matrix& output_gradient, float learning_rate,
                                 CudaRuntime& rt, TransformerGrads* grads,
-                                Matrix* input_gradient) {
+                                Matrix* input_gradient, Matrix* position) {
     // attention.rs:283-321 with the QKV part of attention.rs:104-144.
     require(cache_.has_value(), "attention forward must run before backward");
     Cache& c = *cache_;
@@ -930,8 +930,43 @@ Matrix Attention::backward_self(const Matrix& output_gradient, float learning_ra
     }
 
     // QkvProjection::backward_self: per projection dX accumulates and W, b
-    // are updated (dW, db kept when grads are requested).
-    std::optional<Matrix> projection_gradient;
+    // are updated (dW, db kept when grads are requested).  The input
+    // gradient dXp = R + sum_i G_i W_i^T (attention.rs:104-144 plus the
+    // residual path) accumulates onto R in place; the last product writes
+    // dXp to its target and, with `position`, also takes the position
+    // matrix's SGD step from it (pre_out = dXp, C = position updated).
+    if (input_gradient)
+        require(input_gradient->rows() == residual_gradient.rows() &&
+                    input_gradient->cols() == residual_gradient.cols(),
+                "input gradient shape");
+    if (position)
+        require(position->rows() == residual_gradient.rows() &&
+                    position->cols() == residual_gradient.cols(),
+                "position gradient shape");
+    Matrix owned_result;
+    Matrix* target = input_gradient;
+    if (!target) {
+        owned_result = rt.new_uninit_matrix(residual_gradient.rows(), residual_gradient.cols());
+        target = &owned_result;
+    }
+    auto accumulate_input_gradient = [&](Linear& lin, const Matrix& g, bool last) {
+        if (!last) {
+            lin.input_gradient_accumulate(g, residual_gradient, rt, nullptr);
+            return;
+        }
+        require(g.cols() == lin.weights().cols(), "gradient.cols() == weights.cols()");
+        forge_gemm_epilogue ep = plain_epilogue();
+        ep.residual = residual_gradient.slice();
+        forge_slice out = target->slice();
+        if (position) {
+            ep.pre_out = target->slice();
+            ep.update = 1;
+            ep.update_scale = learning_rate;
+            out = position->slice();
+        }
+        rt.gemm_ex(nullptr, false, true, g, lin.weights(), out, g.rows(), lin.weights().rows(),
+                   lin.weights().cols(), ep);
+    };
     Linear* linears[3] = {&qkv_.query(), &qkv_.key(), &qkv_.value()};
     const Matrix* projected[3] = {&query_gradient, &key_gradient, &value_gradient};
     // With identity projections of one weight shape whose biases (if any)
@@ -949,10 +984,7 @@ Matrix Attention::backward_self(const Matrix& output_gradient, float learning_ra
         forge_gemm_problem probs[3];
         for (int i = 0; i < 3; i++) {
             Linear& lin = *linears[i];
-            if (!projection_gradient)
-                projection_gradient = lin.input_gradient(*projected[i], rt, nullptr);
-            else
-                lin.input_gradient_accumulate(*projected[i], *projection_gradient, rt, nullptr);
+            accumulate_input_gradient(lin, *projected[i], i == 2);
             Matrix* wg = nullptr;
             if (grads) {
                 grads->weights[i] =
@@ -979,8 +1011,7 @@ Matrix Attention::backward_self(const Matrix& output_gradient, float learning_ra
             g = &*g_owned;
         }
         const bool defer_bias = lin.bias() && !db && !bias_taken[i];
-        if (!projection_gradient) projection_gradient = lin.input_gradient(*g, rt, nullptr);
-        else lin.input_gradient_accumulate(*g, *projection_gradient, rt, nullptr);
+        accumulate_input_gradient(lin, *g, i == 2);
         Matrix* wg = nullptr;
         if (grads) {
             grads->weights[i] = rt.new_uninit_matrix(lin.weights().rows(), lin.weights().cols());
@@ -994,18 +1025,7 @@ Matrix Attention::backward_self(const Matrix& output_gradient, float learning_ra
                            /*bias_step=*/!bias_taken[i]);
         if (grads) grads->biases[i] = std::move(db);
     }
-    if (input_gradient) {
-        require(input_gradient->rows() == residual_gradient.rows() &&
-                    input_gradient->cols() == residual_gradient.cols(),
-                "input gradient shape");
-        check(forge_binary(rt.raw(), nullptr, residual_gradient.slice(),
-                           projection_gradient->slice(), input_gradient->slice(),
-                           residual_gradient.len(), FORGE_ADD),
-              "attention input gradient");
-        return Matrix();
-    }
-    residual_gradient.binary_assign(*projection_gradient, BinaryOp::Add, rt);
-    return residual_gradient;
+    return owned_result;
 }
 
 // ============================================= transformer metadata / data
@@ -1320,19 +1340,13 @@ Matrix TrainingTransformer::backward_impl(const Matrix& output_gradient, float l
     second_gradient = Matrix();
 
     // Attention (fills grads->weights[0..3) and the first norm).
-    Matrix positioned_owned =
-        attention_.backward_self(first_output_gradient, learning_rate, rt, grads, input_gradient);
-    Matrix& positioned_gradient = input_gradient ? *input_gradient : positioned_owned;
-
     // Position matrix: P -= lr * dXp (encoder.rs:180-184: clone, scale,
-    // subtract) as one fused update.  dXp is not scaled in place, so it is
-    // returned as the input gradient without the reference's clone.
-    require(position_.rows() == positioned_gradient.rows() &&
-                position_.cols() == positioned_gradient.cols(),
-            "position gradient shape");
-    check(forge_sgd_update(rt.raw(), nullptr, position_.slice(), positioned_gradient.slice(),
-                           position_.len(), learning_rate),
-          "position update");
+    // subtract, the same two roundings) in the epilogue of the product that
+    // completes dXp.  dXp is not scaled in place, so it is returned as the
+    // input gradient without the reference's clone.
+    Matrix positioned_owned = attention_.backward_self(first_output_gradient, learning_rate, rt,
+                                                       grads, input_gradient, &position_);
+    Matrix& positioned_gradient = input_gradient ? *input_gradient : positioned_owned;
     if (grads) grads->position = rt.clone_matrix(positioned_gradient);
     return positioned_owned;
 }
