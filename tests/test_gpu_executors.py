@@ -361,27 +361,30 @@ def test_transformer_training_step(rt, name, S, H, F, O, norm, bias, affine):
                           (net.LAYER, True, False, 64 * 160 * 4)])
 def test_training_step_without_gradients_updates_the_same(rt, norm, bias, affine, score_bytes):
     """A step that keeps no gradients (the bias sums then feed only the SGD
-    step, the Q/K/V weight updates write no dW) leaves every parameter bit
-    for bit where the step that returns the gradients leaves it, unchunked
-    and chunked (64-row chunks of a 160-row sequence)."""
+    step, the Q/K/V weight updates write no dW), and one that also returns
+    no input gradient (the library then owns dXp), leave every parameter
+    bit for bit where the step that returns the gradients leaves it,
+    unchunked and chunked (64-row chunks of a 160-row sequence)."""
     S, H, F, O = 160, 64, 192, 48
     say(f"training without gradients norm={norm} bias={bias} chunked={score_bytes}")
     p = make_params(S, H, F, O, 70, bias=bias, affine=affine, norm=norm)
     X, dY = synth.normal((S, H), 71), synth.normal((S, O), 72)
-    models = [net.Transformer(rt, p, S, H, F, O, norm, net.ENCODER_TRAINING) for _ in range(2)]
+    models = [net.Transformer(rt, p, S, H, F, O, norm, net.ENCODER_TRAINING) for _ in range(3)]
     dxs = []
-    for want, T in zip((True, False), models):
+    for (want, keep_dx), T in zip(((True, True), (False, True), (False, False)), models):
         if score_bytes:
             T.set_score_bytes(score_bytes)
         T.forward(rt.array(X))
-        dx = rt.empty((S, H))
+        dx = rt.empty((S, H)) if keep_dx else None
         T.backward(rt.array(dY), 1e-3, dx, want_grads=want)
-        dxs.append(dx.numpy())
+        if keep_dx:
+            dxs.append(dx.numpy())
     assert np.array_equal(dxs[0], dxs[1])
     for k in net.TP_SLOTS:
         if p.get(k) is None:
             continue
-        assert np.array_equal(models[0].param(k), models[1].param(k)), k
+        for T in models[1:]:
+            assert np.array_equal(models[0].param(k), T.param(k)), k
     for T in models:
         T.close()
 
