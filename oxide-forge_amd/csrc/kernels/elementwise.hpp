@@ -259,7 +259,7 @@ __device__ __forceinline__ void store_count(unsigned* out, unsigned long long t)
 }
 
 // Count of positions where l != r (compare_vectors, reduction.rs:132-174,
-// but over every element; the reference keeps only block 0's verdict).
+// but over every element; the reference keeps only block 0's count).
 // Counts are integers throughout: per-workgroup partials in `part` (u32),
 // summed in u64 by count_final_body.  With one workgroup the kernel writes
 // the count itself (store_count).

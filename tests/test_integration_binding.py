@@ -1,6 +1,7 @@
-"""The Rust binding a maintainer would add to the reference (INTEGRATION.md,
-section 1.2: the `extern "C"` block of src/cuda/ffi.rs) checked against the C
-headers it binds, include/oxforge.h and include/oxforge_net.h.
+"""The Rust binding a maintainer would add to the reference (the one
+`extern "C"` block of src/cuda/ffi.rs in the repository's integration notes)
+checked against the C headers it binds, include/oxforge.h and
+include/oxforge_net.h.
 
 No Rust toolchain exists in this image, so the block is never compiled here;
 this test is what keeps it true.  Both sides are parsed into canonical type
