@@ -497,11 +497,14 @@ def profile_workload(rt, name, steps, warmup):
         ys = [rt.empty((C, R)) for _ in range(2)]
         ms = time_launches(rt, lambda i: rt.transpose(xs[i % 2], ys[i % 2], R, C), steps, warmup)
         return {"workload": name, "ms": round(ms, 5)}
-    if name in ("c4", "c5"):
-        if name == "c4":
+    if name in ("c4", "c4streams", "c5"):
+        if name in ("c4", "c4streams"):
+            # c4streams: the same forward with Q, K and V on three forked
+            # streams (attention.rs:65-102) instead of one batched launch.
             S, H, F, O = 2048, 1024, 4096, 1024
             T = net.Transformer(rt, transformer_params(S, H, F, O, 4, False), S, H, F, O,
-                                net.RMS, net.ENCODER_INFERENCE, qkv_streams=False)
+                                net.RMS, net.ENCODER_INFERENCE,
+                                qkv_streams=name == "c4streams")
             X, Y = rt.array(synth.normal((S, H), 4)), rt.empty((S, O))
             ms = time_launches(rt, lambda i: T.forward(X, Y), steps, warmup)
         else:
@@ -666,7 +669,8 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--profile", default=None,
                     help="run only one workload (gemm4096, gemm8192x1024, gemms, ksweep, copy, "
-                         "transpose, rows, rows65536, sumcols, c4, c5) for rocprofv3, or vendor "
+                         "transpose, rows, rows65536, sumcols, c4, c4streams, c5) for rocprofv3, "
+                         "or vendor "
                          "(torch.mm "
                          "on the same GEMM shapes, in a process without this build's runtime)")
     args = ap.parse_args()
