@@ -552,6 +552,35 @@ def profile_workload(rt, name, steps, warmup):
                 b.recycle()
         return {"workload": name, "loads": os.environ.get("OXFORGE_SUMCOL_LOADS", "default"),
                 "blocks": os.environ.get("OXFORGE_SUMCOL_BLOCKS", "default"), "results": res}
+    if name == "dsfold":
+        # The C5 attention backward's softmax step both ways, kernel by
+        # kernel: the plain dP product, the softmax backward over P and dP,
+        # and the LayerNorm backward (gamma/beta, their SGD steps) -- against
+        # the dP product that stores dS in its epilogue and the LayerNorm
+        # backward that also writes the row term.  P rotates over four
+        # [S, S] matrices (256 MiB) so the MALL cannot serve it.
+        S, H = 4096, 2048
+        s = 1.0 / H ** 0.5
+        R, V = rt.array(synth.normal((S, H), 1)), rt.array(synth.normal((S, H), 2))
+        Ps = rotating(rt, (S, S), 4, 3)
+        dP, dS = rt.empty((S, S)), rt.empty((S, S))
+        X, dY, Xin = (rt.array(synth.normal((S, H), k)) for k in (9, 10, 12))
+        dX, dot = rt.empty((S, H)), rt.empty((S,))
+        g, b = rt.array(synth.normal((H,), 11, 1.0, 0.1)), rt.array(synth.normal((H,), 13))
+        dg, db = rt.empty((H,)), rt.empty((H,))
+        cases = {
+            "dP product": lambda i: rt.gemm_ex(R, V, dP, S, S, H, trans_b=True),
+            "softmax backward": lambda i: rt.softmax_rows_bwd_scaled(Ps[i % 4], dP, dS, S, S, s),
+            "layer norm backward": lambda i: rt.layer_norm_bwd_sgd(
+                X, dY, dX, S, H, 0.0, gamma=g, beta=b, dgamma=dg, dbeta=db),
+            "dS product": lambda i: rt.gemm_ex(R, V, dS, S, S, H, trans_b=True, alpha=s,
+                                               row_sub=dot, aux_mul=Ps[i % 4]),
+            "layer norm backward + row dot": lambda i: rt.layer_norm_bwd_sgd_dot(
+                X, dY, dX, Xin, dot, S, H, 0.0, dot_scale=s, gamma=g, beta=b, dgamma=dg,
+                dbeta=db),
+        }
+        res = {k: round(time_launches(rt, fn, steps, warmup) * 1e3, 2) for k, fn in cases.items()}
+        return {"workload": name, "us": res}
     raise SystemExit(f"unknown profile workload {name}")
 
 
@@ -669,7 +698,8 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--profile", default=None,
                     help="run only one workload (gemm4096, gemm8192x1024, gemms, ksweep, copy, "
-                         "transpose, rows, rows65536, sumcols, c4, c4streams, c5) for rocprofv3, "
+                         "transpose, rows, rows65536, sumcols, dsfold, c4, c4streams, c5) for "
+                         "rocprofv3, "
                          "or vendor "
                          "(torch.mm "
                          "on the same GEMM shapes, in a process without this build's runtime)")

@@ -265,6 +265,12 @@ typedef struct forge_gemm_epilogue {
     forge_slice col_sums_out;
     forge_slice col_sums_param;
     float col_sums_lr;
+    /* [M] or {NULL,0}: Z = Z - row_sub[r] right after alpha (and the
+     * row_div divide).  With alpha = s, row_sub = s * D and aux_mul = P on
+     * the product dP = dO V^T this forms the softmax backward
+     * dS = P * (dP - D) * s (row.rs:216-236, D_r = sum_j P_rj dP_rj) in the
+     * product's epilogue, D coming from forge_*_norm_bwd_sgd_dot.          */
+    forge_slice row_sub;
 } forge_gemm_epilogue;
 
 forge_status forge_gemm_ex_f32(forge_runtime *rt, forge_stream *stream,
@@ -399,6 +405,23 @@ forge_status forge_layer_norm_bwd_sgd(forge_runtime *rt, forge_stream *stream,
                                       forge_slice beta, forge_slice dx,
                                       forge_slice dgamma, forge_slice dbeta,
                                       size_t rows, size_t cols, float eps, float lr);
+/* forge_layer_norm_bwd_sgd that also writes, for each row r,
+ *   dot[r] = dot_scale * sum_c dx[r, c] * (x[r, c] - sub[r, c]).
+ * Used by the attention backward (attention.rs:283-321): with x the
+ * attention's pre-norm output P V + X, sub its residual input X and dx the
+ * gradient at that output (dO), dot is dot_scale * sum_c dO_rc (P V)_rc =
+ * dot_scale * sum_j P_rj dP_rj with dP = dO V^T -- the row term of the
+ * softmax backward (row.rs:216-236) from the [S, H] operands instead of the
+ * [S, S] ones, so the dP product can form dS in its epilogue
+ * (forge_gemm_epilogue row_sub).  dx and the column sums are those of
+ * forge_layer_norm_bwd_sgd, bit for bit.  sub [rows, cols] may not overlap
+ * dx, nor dot [rows] any matrix operand (FORGE_EINVAL). */
+forge_status forge_layer_norm_bwd_sgd_dot(forge_runtime *rt, forge_stream *stream,
+                                          forge_slice x, forge_slice dy, forge_slice gamma,
+                                          forge_slice beta, forge_slice dx,
+                                          forge_slice dgamma, forge_slice dbeta,
+                                          forge_slice sub, forge_slice dot, size_t rows,
+                                          size_t cols, float eps, float lr, float dot_scale);
 /* forge_layer_norm_bwd that allocates nothing.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
@@ -440,6 +463,12 @@ forge_status forge_rms_norm_bwd_sgd(forge_runtime *rt, forge_stream *stream,
                                     forge_slice x, forge_slice dy, forge_slice gamma,
                                     forge_slice dx, forge_slice dgamma, size_t rows,
                                     size_t cols, float eps, float lr);
+/* forge_rms_norm_bwd_sgd with the row dot of forge_layer_norm_bwd_sgd_dot. */
+forge_status forge_rms_norm_bwd_sgd_dot(forge_runtime *rt, forge_stream *stream,
+                                        forge_slice x, forge_slice dy, forge_slice gamma,
+                                        forge_slice dx, forge_slice dgamma, forge_slice sub,
+                                        forge_slice dot, size_t rows, size_t cols, float eps,
+                                        float lr, float dot_scale);
 
 /* matrix_binary / vector_binary (matrix.rs:194-219 -> elementwise.rs:45-56):
  * o = l op r over n elements.  Bit-exact. */

@@ -701,9 +701,13 @@ struct Normalization {
     Matrix backward(const Matrix& input, const Matrix& output_gradient, CudaRuntime& rt,
                     Vector* dgamma = nullptr, Vector* dbeta = nullptr) const;
     // backward, then the SGD step of this norm's gamma/beta (when present)
-    // in the same final pass; dgamma/dbeta optional gradient outputs.
+    // in the same final pass; dgamma/dbeta optional gradient outputs.  With
+    // dot_sub and dot, also dot[r] = dot_scale * sum_c dx[r,c] *
+    // (input[r,c] - dot_sub[r,c]) (forge_layer_norm_bwd_sgd_dot).
     Matrix backward_step(const Matrix& input, const Matrix& output_gradient, float learning_rate,
-                         CudaRuntime& rt, Vector* dgamma = nullptr, Vector* dbeta = nullptr);
+                         CudaRuntime& rt, Vector* dgamma = nullptr, Vector* dbeta = nullptr,
+                         const Matrix* dot_sub = nullptr, Vector* dot = nullptr,
+                         float dot_scale = 1.0f);
 };
 
 // QkvProjection (attention.rs:15-144).  With `streams` (three streams of

@@ -67,9 +67,12 @@ struct GemmArgs {
     // wave's TM rows (the unguarded tiles only; TM = the tile's rows per
     // wave).
     float* col_part;
+    // [M] or null: Z = Z - row_sub[r] after alpha and the row_div divide
+    // (the softmax backward's row term, folded into the dP product).
+    const float* row_sub;
 };
 // The host fills the same layout (runtime.cpp GemmArgs).
-static_assert(sizeof(GemmArgs) == 168, "kernel argument layout");
+static_assert(sizeof(GemmArgs) == 176, "kernel argument layout");
 
 constexpr int GEMM_GROUP_M = 8;
 constexpr int LDS_PAD = 4;
@@ -109,13 +112,15 @@ struct GemmBatchArgs {
 };
 
 // The fused epilogue on one element z of the product at (row, col), idx =
-// row * ldc + col: alpha, bias, residual, aux multiply (or act'(aux)),
-// pre-activation store, activation, then store or SGD update.  Each step is
-// one rounded f32 operation in the reference's launch order.
+// row * ldc + col: alpha, row divide, row subtrahend, bias, residual, aux
+// multiply (or act'(aux)), pre-activation store, activation, then store or
+// SGD update.  Each step is one rounded f32 operation in the reference's
+// launch order.
 __device__ __forceinline__ void gemm_epilogue_store(const GemmArgs& p, long long idx, int row,
                                                     int col, float z) {
     if (p.alpha != 1.0f) z = p.alpha * z;
     if (p.row_d && (p.row_div & 1)) z = z / p.row_d[row];
+    if (p.row_sub) z = z - p.row_sub[row];
     if (p.bias) z = z + p.bias[col];
     if (p.residual) z = z + ((p.row_d && (p.row_div & 2)) ? p.residual[idx] / p.row_d[row]
                                                           : p.residual[idx]);
@@ -321,11 +326,15 @@ __device__ __forceinline__ void gemm_body_guarded(const GemmArgs& p, int logical
                 // the block's accumulators, each under one uniform branch:
                 // the optional steps neither multiply the unrolled code nor
                 // keep more than one block's operands live.  Per element the
-                // order (alpha, bias, residual, aux, pre_out, activation, store
-                // or update) is that of gemm_epilogue_store.
+                // order (alpha, row divide, row subtrahend, bias, residual,
+                // aux, pre_out, activation, store or update) is that of
+                // gemm_epilogue_store.
                 if (p.alpha != 1.0f) FORGE_EPI_EACH(a[r] = p.alpha * a[r]);
                 if (p.row_d && (p.row_div & 1)) {
                     FORGE_EPI_EACH(a[r] = a[r] / p.row_d[row]);
+                }
+                if (p.row_sub) {
+                    FORGE_EPI_EACH(a[r] = a[r] - p.row_sub[row]);
                 }
                 if (p.bias && col < p.N) {
                     const float b = p.bias[col];
@@ -385,9 +394,17 @@ __device__ __forceinline__ void splitk_reduce_body(const float* __restrict__ P, 
     const long long MN = (long long)p.M * p.N;
     constexpr int W = VEC ? 4 : 1;  // VEC requires N % 4 == 0 and a 16-byte aligned P
     const long long stride = (long long)gridDim.x * SPLITK_THREADS * W;
-    for (long long e = ((long long)blockIdx.x * SPLITK_THREADS + threadIdx.x) * W; e < MN;
-         e += stride) {
-        const int row = (int)(e / p.N), col0 = (int)(e % p.N);
+    // (row, col0) of e, advanced with the grid stride without a 64-bit
+    // division per step (which, with the epilogue's operands, would exceed
+    // the scalar registers).
+    long long e = ((long long)blockIdx.x * SPLITK_THREADS + threadIdx.x) * W;
+    int row = (int)(e / p.N), col0 = (int)(e % p.N);
+    const int srow = (int)(stride / p.N), scol = (int)(stride % p.N);
+    for (; e < MN; e += stride, row += srow, col0 += scol) {
+        if (col0 >= p.N) {
+            col0 -= p.N;
+            row++;
+        }
         float z[W];
         if constexpr (VEC) {
             // All slices are loaded before the sum (up to 8 in flight), then

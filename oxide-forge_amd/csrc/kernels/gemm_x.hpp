@@ -242,19 +242,21 @@ struct XReads {
 };
 
 // Fused epilogue of one 128-bit group of C at flat index idx, column col:
-// the operands (residual, aux, old C) are loaded first so a batch of groups
-// has its reads in flight together, then per element alpha, bias,
-// residual, aux (or act'(aux)), pre-activation store, activation, and store
-// or SGD update -- the order of gemm_epilogue_store, each one rounded f32
-// operation.
+// the operands (residual, aux, old C, the row subtrahend) are loaded first so
+// a batch of groups has its reads in flight together, then per element
+// alpha, row divide, row subtrahend, bias, residual, aux (or act'(aux)),
+// pre-activation store, activation, and store or SGD update -- the order of
+// gemm_epilogue_store, each one rounded f32 operation.
 template <bool EPI>
-__device__ __forceinline__ void x_epi_load(const GemmArgs& p, long long idx, f4& res, f4& mul,
-                                           f4& old) {
+__device__ __forceinline__ void x_epi_load(const GemmArgs& p, long long idx, int row, f4& res,
+                                           f4& mul, f4& old, float& sub) {
     res = mul = old = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    sub = 0.0f;
     if constexpr (EPI) {
         if (p.residual) res = *reinterpret_cast<const f4*>(p.residual + idx);
         if (p.aux) mul = *reinterpret_cast<const f4*>(p.aux + idx);
         if (p.update) old = *reinterpret_cast<const f4*>(p.C + idx);
+        if (p.row_sub) sub = p.row_sub[row];
     }
 }
 
@@ -322,7 +324,7 @@ struct XRowStats {
 template <bool EPI, int NB, bool STATS = false>
 __device__ __forceinline__ void x_epi_store(const GemmArgs& p, const f4 (&z)[NB],
                                             const f4 (&res)[NB], const f4 (&mul)[NB],
-                                            const f4 (&old)[NB], f4 bias,
+                                            const f4 (&old)[NB], const float (&sub)[NB], f4 bias,
                                             const long long (&idx)[NB], const XRowStats<NB>& rs,
                                             int lane_col, float (&cs)[4]) {
     float y[4 * NB];
@@ -342,6 +344,9 @@ __device__ __forceinline__ void x_epi_store(const GemmArgs& p, const f4 (&z)[NB]
 #pragma unroll
                 for (int i = 0; i < 4 * NB; i++) y[i] = y[i] * rs.rinv[i / 4];
         }
+        if (p.row_sub)
+#pragma unroll
+            for (int i = 0; i < 4 * NB; i++) y[i] = y[i] - sub[i / 4];
         if (p.bias)
 #pragma unroll
             for (int u = 0; u < NB; u++) {
@@ -702,6 +707,7 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
         // Loads of a batch first, so NB global reads per operand are in
         // flight together.
         f4 z[NB], res[NB], mul[NB], old[NB];
+        float sub[NB];
         long long idx[NB];
         XRowStats<NB> rs;
 #pragma unroll
@@ -715,9 +721,9 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
             if constexpr (STATS) {
                 if (p.row_part) rs.rinv[u] = smem_all[SMEM + a_off + rr];
             }
-            x_epi_load<EPI>(p, idx[u], res[u], mul[u], old[u]);
+            x_epi_load<EPI>(p, idx[u], row0 + rr, res[u], mul[u], old[u], sub[u]);
         }
-        x_epi_store<EPI, NB, STATS>(p, z, res, mul, old, bias4, idx, rs, lane_col, cs);
+        x_epi_store<EPI, NB, STATS>(p, z, res, mul, old, sub, bias4, idx, rs, lane_col, cs);
     }
     if constexpr (STATS) {
         if (p.col_part) {

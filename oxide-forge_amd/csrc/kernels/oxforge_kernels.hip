@@ -148,7 +148,7 @@ GEMM_GUARDED_KERNEL(forge_gemm_nn_64x64x16_2x2_g, 64, 64, 16, 2, 2, false, false
 // The runtime launches them with WAVES * 64 threads.
 #define ROW_PARTIAL_KERNEL(NAME, OP, VPT, W, PF)                                         \
     FORGE_KERNEL void __launch_bounds__(W * 64) NAME(RowArgs a) {                        \
-        row_kernel_reg<OP, VPT, true, W, PF>(a);                                         \
+        row_kernel_reg<OP, VPT, true, W, false, PF>(a);                                  \
     }
 #define ROW_PARTIAL_KERNELS(OPNAME, OP)                                                  \
     ROW_PARTIAL_KERNEL(forge_row_##OPNAME##_v1_p, OP, 1, ROW_PARTIAL_WAVES, true)        \
@@ -165,6 +165,29 @@ ROW_KERNELS(layer_norm_bwd, ROW_LAYER_NORM_BWD)
 ROW_KERNELS(rms_norm_bwd, ROW_RMS_NORM_BWD)
 ROW_PARTIAL_KERNELS(layer_norm_bwd, ROW_LAYER_NORM_BWD)
 ROW_PARTIAL_KERNELS(rms_norm_bwd, ROW_RMS_NORM_BWD)
+// _d: the norm backward instances above that also write the row dot
+// (RowArgs::dot), without the next-row prefetch.
+#define ROW_DOT_KERNEL(NAME, OP, VPT)                                                    \
+    FORGE_KERNEL void __launch_bounds__(256) NAME(RowArgs a) {                           \
+        row_kernel_reg<OP, VPT, false, ROW_WAVES, true>(a);                              \
+    }
+#define ROW_PARTIAL_DOT_KERNEL(NAME, OP, VPT, W)                                         \
+    FORGE_KERNEL void __launch_bounds__(W * 64) NAME(RowArgs a) {                        \
+        row_kernel_reg<OP, VPT, true, W, true, false>(a);                                \
+    }
+#define ROW_DOT_KERNELS(OPNAME, OP)                                                      \
+    ROW_DOT_KERNEL(forge_row_##OPNAME##_v1_d, OP, 1)                                     \
+    ROW_DOT_KERNEL(forge_row_##OPNAME##_v2_d, OP, 2)                                     \
+    ROW_DOT_KERNEL(forge_row_##OPNAME##_v4_d, OP, 4)                                     \
+    ROW_DOT_KERNEL(forge_row_##OPNAME##_v8_d, OP, 8)                                     \
+    ROW_DOT_KERNEL(forge_row_##OPNAME##_v16_d, OP, 16)                                   \
+    ROW_PARTIAL_DOT_KERNEL(forge_row_##OPNAME##_v1_p_d, OP, 1, ROW_PARTIAL_WAVES)        \
+    ROW_PARTIAL_DOT_KERNEL(forge_row_##OPNAME##_v2_p_d, OP, 2, ROW_PARTIAL_WAVES)        \
+    ROW_PARTIAL_DOT_KERNEL(forge_row_##OPNAME##_v4_p_d, OP, 4, ROW_PARTIAL_WAVES)        \
+    ROW_PARTIAL_DOT_KERNEL(forge_row_##OPNAME##_v4_p4_d, OP, 4, 4)                       \
+    ROW_PARTIAL_DOT_KERNEL(forge_row_##OPNAME##_v8_p_d, OP, 8, ROW_PARTIAL_WAVES)
+ROW_DOT_KERNELS(layer_norm_bwd, ROW_LAYER_NORM_BWD)
+ROW_DOT_KERNELS(rms_norm_bwd, ROW_RMS_NORM_BWD)
 
 
 // ------------------------------------------------------------ elementwise

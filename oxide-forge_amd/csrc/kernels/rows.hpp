@@ -36,6 +36,14 @@ struct RowArgs {
     float scale;         // softmax backward: dx *= scale (1 = reference kernel)
     int nt_stores;       // 1: non-temporal stores at any size (set by the host)
     int lds_params;      // 1: LayerNorm forward stages gamma/beta in LDS (set by the host)
+    // Norm backward row dot (the _d instances and the looping path):
+    // dot[r] = dscale * sum_c dx[r, c] * (x[r, c] - dsub[r, c]).  With x the
+    // attention output plus its residual input and dsub that input, x - dsub
+    // is the attention output O = P V and the dot is the softmax backward's
+    // row term sum_j P_rj dP_rj = sum_c dO_rc O_rc (dP = dO V^T).
+    const float* dsub;   // [rows, cols] or null
+    float* dot;          // [rows] or null
+    float dscale;
 };
 
 enum RowOp {
@@ -104,8 +112,8 @@ __device__ __forceinline__ void row_mask(const bool* ok, float4* v, float4* g) {
 // grid-stride.  The partial-producing backward kernels with at most 8 waves
 // walk several rows per wave, so they prefetch the next row's registers
 // before reducing the current one.
-template <int OP, int VPT, bool PARTIALS, int WAVES = ROW_WAVES,
-          bool PREFETCH = PARTIALS && WAVES <= 8>
+template <int OP, int VPT, bool PARTIALS, int WAVES = ROW_WAVES, bool DOT = false,
+          bool PREFETCH = PARTIALS && WAVES <= 8 && !DOT>
 __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
     const int lane = lane_id();
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // scalar
@@ -192,6 +200,8 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
     };
     static_assert(!PARTIALS || OP == ROW_LAYER_NORM_BWD || OP == ROW_RMS_NORM_BWD,
                   "only the norm backward kernels produce column partials");
+    static_assert(!DOT || OP == ROW_LAYER_NORM_BWD || OP == ROW_RMS_NORM_BWD,
+                  "only the norm backward kernels produce the row dot");
     // The backward's g = dy * gamma for float4 group i of the current row;
     // past cols (ok false) it is 0 and gamma is not read.  Kept in registers
     // between the two passes where that fits: at 8 float4 per lane the
@@ -227,7 +237,7 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
     if (PREFETCH && row < a.rows) row_load<OP, VPT, BWD>(a, row, lane, nv, ng);
     for (; row < a.rows; row += stride) {
         const long long base = (long long)row * cols;
-        float4 v[VPT], g[BWD ? VPT : 1];
+        float4 v[VPT], g[BWD ? VPT : 1], ds[DOT ? VPT : 1];
         bool ok[VPT];
 #pragma unroll
         for (int i = 0; i < VPT; i++) ok[i] = (i * 64 + lane) * 4 < cols;
@@ -241,12 +251,24 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
             if (row + stride < a.rows) row_load<OP, VPT, BWD>(a, row + stride, lane, nv, ng);
         } else {
             row_load<OP, VPT, BWD>(a, row, lane, v, g);
+            if constexpr (DOT) {
+                // The row dot's subtrahend, issued behind the row's own loads
+                // and first used after the row's first reduction.  DOT
+                // instances do not prefetch: at 8 float4 per lane these
+                // registers take the prefetch's place.
+#pragma unroll
+                for (int i = 0; i < VPT; i++) {
+                    const int c = (i * 64 + lane) * 4;
+                    ds[i] = load_stream(a.dsub + base + (c < cols ? c : 0));
+                }
+            }
             if constexpr (LATE_PRELOAD) {
                 if (first) preload();
                 first = false;
             }
             row_mask<OP, VPT, BWD>(ok, v, g);
         }
+        float dd = 0.0f;  // DOT: this lane's part of the row dot
 
         if constexpr (OP == ROW_SOFTMAX) {
             // row.rs:64-112: max, exp(x - max), sum, normalise.
@@ -283,6 +305,10 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
 #pragma unroll
             for (int i = 0; i < VPT; i++) {
                 if (ok[i]) {
+                    // The row dot's x - dsub, while v still holds x.
+                    if constexpr (DOT)
+                        F4_APPLY(ds[i], ds[i], v[i].x - ds[i].x, v[i].y - ds[i].y,
+                                 v[i].z - ds[i].z, v[i].w - ds[i].w);
                     const float dx0 = v[i].x - mean, dx1 = v[i].y - mean;
                     const float dx2 = v[i].z - mean, dx3 = v[i].w - mean;
                     v[i] = make_float4(dx0, dx1, dx2, dx3);
@@ -343,6 +369,8 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                              scale * fmaf(v[i].z, nsb, fmaf(n, gi.z, nsa)),
                              scale * fmaf(v[i].w, nsb, fmaf(n, gi.w, nsa)));
                     store_f4(a.y + base + c, o, nt);
+                    if constexpr (DOT)
+                        dd += fmaf(o.x, ds[i].x, o.y * ds[i].y) + fmaf(o.z, ds[i].z, o.w * ds[i].w);
                     if constexpr (PARTIALS) {
                         pg[i].x = fmaf(g[i].x, v[i].x, pg[i].x);
                         pg[i].y = fmaf(g[i].y, v[i].y, pg[i].y);
@@ -418,6 +446,12 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                 F4_APPLY(o, v[i], fmaf(v[i].x, ncorr, gi.x * inv), fmaf(v[i].y, ncorr, gi.y * inv),
                          fmaf(v[i].z, ncorr, gi.z * inv), fmaf(v[i].w, ncorr, gi.w * inv));
                 store_f4(a.y + base + c, o, nt);
+                if constexpr (DOT) {
+                    // v holds x: the row dot's x - dsub, then its products.
+                    F4_APPLY(ds[i], ds[i], v[i].x - ds[i].x, v[i].y - ds[i].y, v[i].z - ds[i].z,
+                             v[i].w - ds[i].w);
+                    dd += fmaf(o.x, ds[i].x, o.y * ds[i].y) + fmaf(o.z, ds[i].z, o.w * ds[i].w);
+                }
                 if constexpr (PARTIALS) {
                     pg[i].x = fmaf(g[i].x, v[i].x * inv, pg[i].x);
                     pg[i].y = fmaf(g[i].y, v[i].y * inv, pg[i].y);
@@ -425,6 +459,10 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
                     pg[i].w = fmaf(g[i].w, v[i].w * inv, pg[i].w);
                 }
             }
+        }
+        if constexpr (DOT) {
+            dd = wave_sum(dd);
+            if (lane == 0) a.dot[row] = a.dscale * dd;
         }
     }
 
@@ -457,6 +495,7 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
 }
 
 // Looping path: any cols and alignment, scalar accesses, one wave per row.
+// The norm backward's row dot (RowArgs::dot) is taken here when dot is set.
 template <int OP>
 __device__ __forceinline__ void row_kernel_loop(const RowArgs& a) {
     const int lane = lane_id();
@@ -513,12 +552,19 @@ __device__ __forceinline__ void row_kernel_loop(const RowArgs& a) {
                 sa = wave_sum(sa);
                 sb = wave_sum(sb);
                 const float scale = rstd / n;
+                float dd = 0.0f;
                 for (int c = lane; c < cols; c += 64) {
                     const float xh = (x[c] - mean) * rstd;
                     const float gg = a.gamma ? dy[c] * a.gamma[c] : dy[c];
-                    y[c] = scale * (n * gg - sa - xh * sb);
+                    const float o = scale * (n * gg - sa - xh * sb);
+                    if (a.dot) dd = fmaf(o, x[c] - a.dsub[(long long)row * cols + c], dd);
+                    y[c] = o;
                     if (a.pgamma) a.pgamma[prow + c] += dy[c] * xh;
                     if (a.pbeta) a.pbeta[prow + c] += dy[c];
+                }
+                if (a.dot) {
+                    dd = wave_sum(dd);
+                    if (lane == 0) a.dot[row] = a.dscale * dd;
                 }
             }
         } else if constexpr (OP == ROW_RMS_NORM) {
@@ -550,10 +596,17 @@ __device__ __forceinline__ void row_kernel_loop(const RowArgs& a) {
             const float rms = sqrtf(q / n + a.eps);
             const float inv = 1.0f / rms;
             const float corr = d / n * inv * inv * inv;
+            float dd = 0.0f;
             for (int c = lane; c < cols; c += 64) {
                 const float gg = a.gamma ? dy[c] * a.gamma[c] : dy[c];
-                y[c] = gg * inv - x[c] * corr;
+                const float o = gg * inv - x[c] * corr;
+                if (a.dot) dd = fmaf(o, x[c] - a.dsub[(long long)row * cols + c], dd);
+                y[c] = o;
                 if (a.pgamma) a.pgamma[prow + c] += dy[c] * (x[c] * inv);
+            }
+            if (a.dot) {
+                dd = wave_sum(dd);
+                if (lane == 0) a.dot[row] = a.dscale * dd;
             }
         }
     }

@@ -42,13 +42,14 @@ static void sgd_vector(CudaRuntime& rt, Vector& param, const Vector& grad, float
 static Matrix norm_backward_step(Normalization& norm, const Matrix& input,
                                  const Matrix& output_gradient, float lr, CudaRuntime& rt,
                                  bool want, std::optional<Vector>* out_gamma,
-                                 std::optional<Vector>* out_beta) {
+                                 std::optional<Vector>* out_beta, const Matrix* dot_sub = nullptr,
+                                 Vector* dot = nullptr, float dot_scale = 1.0f) {
     const size_t cols = input.cols();
     std::optional<Vector> dg, db;
     if (want) dg = Vector(rt.get_uninit_buffer(cols));
     if (norm.kind == NormType::Layer && want) db = Vector(rt.get_uninit_buffer(cols));
     Matrix dx = norm.backward_step(input, output_gradient, lr, rt, dg ? &*dg : nullptr,
-                                   db ? &*db : nullptr);
+                                   db ? &*db : nullptr, dot_sub, dot, dot_scale);
     if (want) {
         *out_gamma = std::move(dg);
         *out_beta = std::move(db);
@@ -585,23 +586,40 @@ Matrix Normalization::backward(const Matrix& input, const Matrix& output_gradien
 
 Matrix Normalization::backward_step(const Matrix& input, const Matrix& output_gradient,
                                     float learning_rate, CudaRuntime& rt, Vector* dgamma,
-                                    Vector* dbeta) {
+                                    Vector* dbeta, const Matrix* dot_sub, Vector* dot,
+                                    float dot_scale) {
     require(input.rows() == output_gradient.rows() && input.cols() == output_gradient.cols(),
             "norm backward shapes");
+    require(!dot_sub == !dot, "row dot needs both dot_sub and dot");
+    if (dot_sub)
+        require(dot_sub->rows() == input.rows() && dot_sub->cols() == input.cols() &&
+                    dot->len() == input.rows(),
+                "row dot shapes");
     Matrix out = rt.new_uninit_matrix(input.rows(), input.cols());
     forge_slice g = gamma ? gamma->slice() : forge_slice{nullptr, 0};
     forge_slice b = beta ? beta->slice() : forge_slice{nullptr, 0};
     forge_slice dg = dgamma ? dgamma->slice() : forge_slice{nullptr, 0};
     forge_slice db = dbeta ? dbeta->slice() : forge_slice{nullptr, 0};
-    if (kind == NormType::Layer)
-        check(forge_layer_norm_bwd_sgd(rt.raw(), nullptr, input.slice(), output_gradient.slice(), g,
-                                       b, out.slice(), dg, db, input.rows(), input.cols(), eps,
-                                       learning_rate),
+    const size_t rows = input.rows(), cols = input.cols();
+    if (kind == NormType::Layer && dot_sub)
+        check(forge_layer_norm_bwd_sgd_dot(rt.raw(), nullptr, input.slice(),
+                                           output_gradient.slice(), g, b, out.slice(), dg, db,
+                                           dot_sub->slice(), dot->slice(), rows, cols, eps,
+                                           learning_rate, dot_scale),
               "layer_norm_backward");
+    else if (kind == NormType::Layer)
+        check(forge_layer_norm_bwd_sgd(rt.raw(), nullptr, input.slice(), output_gradient.slice(), g,
+                                       b, out.slice(), dg, db, rows, cols, eps, learning_rate),
+              "layer_norm_backward");
+    else if (dot_sub)
+        check(forge_rms_norm_bwd_sgd_dot(rt.raw(), nullptr, input.slice(),
+                                         output_gradient.slice(), g, out.slice(), dg,
+                                         dot_sub->slice(), dot->slice(), rows, cols, eps,
+                                         learning_rate, dot_scale),
+              "rms_norm_backward");
     else
         check(forge_rms_norm_bwd_sgd(rt.raw(), nullptr, input.slice(), output_gradient.slice(), g,
-                                     out.slice(), dg, input.rows(), input.cols(), eps,
-                                     learning_rate),
+                                     out.slice(), dg, rows, cols, eps, learning_rate),
               "rms_norm_backward");
     return out;
 }
@@ -844,43 +862,58 @@ Matrix Attention::backward_self(const Matrix& output_gradient, float learning_ra
         grads->weights.resize(3);
         grads->biases.resize(3);
     }
-    Matrix residual_gradient =
-        norm_backward_step(norm_, c.pre_norm, output_gradient, learning_rate, rt, grads != nullptr,
-                           grads ? &grads->norm1_gamma : nullptr,
-                           grads ? &grads->norm1_beta : nullptr);
-
     const size_t D = c.query.cols();
+    const float scale = score_scale(D);
+    // The softmax backward dS = P * (dP - D) * scale (row.rs:216-236) needs
+    // each row's D_r = sum_j P_rj dP_rj over the whole [S, Sk] row.  With
+    // dP = R V^T that is sum_c R_rc (P V)_rc, and P V = pre_norm - input (the
+    // forward's A V product took the input as its residual): the norm
+    // backward that forms R also writes scale * D from the [S, H] operands
+    // it streams, and each dP product then forms dS in its epilogue
+    // (scale * dP - scale * D, times P) -- no [S, Sk] dP matrix and no
+    // softmax backward pass.
+    const bool fold_ds = S > 0 && Sk > 0;
+    std::optional<Vector> row_term;
+    if (fold_ds) row_term = Vector(rt.get_uninit_buffer(S));
+    Matrix residual_gradient = norm_backward_step(
+        norm_, c.pre_norm, output_gradient, learning_rate, rt, grads != nullptr,
+        grads ? &grads->norm1_gamma : nullptr, grads ? &grads->norm1_beta : nullptr,
+        fold_ds ? &c.input : nullptr, fold_ds ? &*row_term : nullptr, scale);
+    // The dS product: dP rows r0 .. r0 + n - 1 against the P rows `p`.
+    auto score_gradient_epilogue = [&](forge_slice p, size_t r0, size_t n) {
+        forge_gemm_epilogue ep = plain_epilogue();
+        ep.alpha = scale;
+        ep.row_sub = forge_slice{row_term->buffer().ptr() + r0, n};
+        ep.aux_mul = p;
+        return ep;
+    };
+
     Matrix query_gradient, key_gradient, value_gradient;
     bool bias_taken[3] = {false, false, false};  // bias gradient and step already taken
     if (c.probabilities.len() == 0 && S > 0 && Sk > 0) {
         // Chunked: per chunk of query rows, P recomputed as in the forward,
-        // then dP = R V^T, dV += P^T R, dS = softmax_bwd(P, dP) / sqrt(d),
+        // then dS = P * (R V^T - D) / sqrt(d) (one product), dV += P^T R,
         // dQ = dS K, dK += dS^T Q; dV and dK sum the chunks in order.
         const size_t chunk = score_chunk_rows(S, Sk, max_score_bytes_);
         const size_t cr = std::min(chunk, S);
-        Matrix p_c = rt.new_uninit_matrix(cr, Sk), dp_c = rt.new_uninit_matrix(cr, Sk),
-               ds_c = rt.new_uninit_matrix(cr, Sk);
+        Matrix p_c = rt.new_uninit_matrix(cr, Sk), ds_c = rt.new_uninit_matrix(cr, Sk);
         query_gradient = rt.new_uninit_matrix(S, D);
         key_gradient = rt.new_uninit_matrix(Sk, D);
         value_gradient = rt.new_uninit_matrix(Sk, H);
-        const float scale = score_scale(D);
         for (size_t r0 = 0; r0 < S; r0 += chunk) {
             const size_t n = std::min(chunk, S - r0);
-            const forge_slice ps{p_c.buffer().ptr(), n * Sk}, dps{dp_c.buffer().ptr(), n * Sk},
-                dss{ds_c.buffer().ptr(), n * Sk};
+            const forge_slice ps{p_c.buffer().ptr(), n * Sk}, dss{ds_c.buffer().ptr(), n * Sk};
             forge_gemm_epilogue ep = plain_epilogue();
             ep.alpha = scale;
             gemm_slices(rt, false, true, rows_of(c.query, r0, n), c.key.slice(), ps, n, Sk, D, ep,
                         "attention scores");
             check(forge_softmax_rows(rt.raw(), nullptr, ps, n, Sk), "softmax_rows");
-            gemm_slices(rt, false, true, rows_of(residual_gradient, r0, n), c.value.slice(), dps,
-                        n, Sk, H, plain_epilogue(), "dP");
+            gemm_slices(rt, false, true, rows_of(residual_gradient, r0, n), c.value.slice(), dss,
+                        n, Sk, H, score_gradient_epilogue(ps, r0, n), "dS");
             forge_gemm_epilogue acc = plain_epilogue();
             if (r0 > 0) acc.residual = value_gradient.slice();
             gemm_slices(rt, true, false, ps, rows_of(residual_gradient, r0, n),
                         value_gradient.slice(), Sk, H, n, acc, "dV");
-            check(forge_softmax_rows_bwd_scaled(rt.raw(), nullptr, ps, dps, dss, n, Sk, scale),
-                  "softmax_rows_backward");
             gemm_slices(rt, false, false, dss, c.key.slice(), rows_of(query_gradient, r0, n), n,
                         D, Sk, plain_epilogue(), "dQ");
             forge_gemm_epilogue acck = plain_epilogue();
@@ -905,20 +938,14 @@ Matrix Attention::backward_self(const Matrix& output_gradient, float learning_ra
             bias_taken[i] = true;
             return ep;
         };
-        // dP = R V^T (NT), dV = P^T R (TN).
-        Matrix probabilities_gradient = rt.new_uninit_matrix(S, Sk);
-        rt.gemm_ex(nullptr, false, true, residual_gradient, c.value, probabilities_gradient.slice(),
-                   S, Sk, H, plain_epilogue());
+        // dS = P * (R V^T - D) / sqrt(d) (NT, softmax backward in the
+        // epilogue), dV = P^T R (TN).
+        Matrix score_gradient = rt.new_uninit_matrix(S, Sk);
+        rt.gemm_ex(nullptr, false, true, residual_gradient, c.value, score_gradient.slice(), S, Sk,
+                   H, score_gradient_epilogue(c.probabilities.slice(), 0, S));
         value_gradient = rt.new_uninit_matrix(Sk, H);
         rt.gemm_ex(nullptr, true, false, c.probabilities, residual_gradient, value_gradient.slice(),
                    Sk, H, S, bias_sums(2));
-        // dS = softmax_bwd(P, dP) / sqrt(d), fused.
-        Matrix score_gradient = rt.new_uninit_matrix(S, Sk);
-        check(forge_softmax_rows_bwd_scaled(rt.raw(), nullptr, c.probabilities.slice(),
-                                            probabilities_gradient.slice(), score_gradient.slice(),
-                                            S, Sk, score_scale(c.query.cols())),
-              "softmax_rows_backward");
-        probabilities_gradient = Matrix();
         // dQ = dS K (NN), dK = dS^T Q (TN).
         query_gradient = rt.new_uninit_matrix(S, D);
         rt.gemm_ex(nullptr, false, false, score_gradient, c.key, query_gradient.slice(), S, D, Sk,

@@ -71,8 +71,9 @@ struct GemmArgs {
     int row_div;
     float* row_sq;
     float* col_part;
+    const float* row_sub;
 };
-static_assert(sizeof(GemmArgs) == 168, "kernel argument layout of forge::GemmArgs");
+static_assert(sizeof(GemmArgs) == 176, "kernel argument layout of forge::GemmArgs");
 
 // Must match forge::GemmBatchArgs in csrc/kernels/gemm.hpp.
 constexpr int GEMM_BATCH_MAX = 8;
@@ -96,6 +97,9 @@ struct RowArgs {
     float scale;
     int nt_stores = 0;   // set by row_launch
     int lds_params = 0;  // set by row_launch
+    const float* dsub = nullptr;  // norm backward row dot
+    float* dot = nullptr;
+    float dscale = 1.0f;
 };
 
 // LayerNorm forward stages gamma/beta in LDS below this many elements
@@ -853,7 +857,9 @@ forge_status gemm_args(int ta, int tb, forge_slice A, forge_slice B, forge_slice
         FORGE_TRY(need_opt(ep->row_sumsq_out, M * ((N + 31) / 32), "gemm row_sumsq_out"));
         FORGE_TRY(need_opt(ep->col_sums_out, N, "gemm col_sums_out"));
         FORGE_TRY(need_opt(ep->col_sums_param, N, "gemm col_sums_param"));
+        FORGE_TRY(need_opt(ep->row_sub, M, "gemm row_sub"));
         a.row_sq = ep->row_sumsq_out.ptr;
+        a.row_sub = ep->row_sub.ptr;
     }
     *out = a;
     *aligned = al;
@@ -1254,7 +1260,11 @@ forge_status row_launch(forge_runtime* rt, forge_stream* s, const char* op, RowA
     const ColSumOut og{dgamma, sgd.gamma, sgd.lr}, ob{dbeta, sgd.beta, sgd.lr};
     const bool want_g = dgamma || sgd.gamma, want_b = dbeta || sgd.beta;
     bool aligned = aligned16(a.x) && aligned16(a.y) && (!a.dy || aligned16(a.dy)) &&
-                   (!a.gamma || aligned16(a.gamma)) && (!a.beta || aligned16(a.beta));
+                   (!a.gamma || aligned16(a.gamma)) && (!a.beta || aligned16(a.beta)) &&
+                   (!a.dsub || aligned16(a.dsub));
+    // The row dot (norm backward): the register path's _d instances; the
+    // looping path takes it at run time.
+    const char* dsuf = a.dot ? "_d" : "";
     int vpt = row_vpt((size_t)a.cols, aligned);
     const bool partials = want_g || want_b;
     if (partials && vpt > 8) vpt = 0;  // register path with partials: <= 8 float4
@@ -1294,11 +1304,12 @@ forge_status row_launch(forge_runtime* rt, forge_stream* s, const char* op, RowA
         a.pgamma = want_g ? ws : nullptr;
         a.pbeta = want_b ? ws + per : nullptr;
         if (vpt) shmem = (size_t)waves * (size_t)a.cols * sizeof(float);
-        if (vpt) snprintf(name, sizeof name, "forge_row_%s_v%d_p%s", op, vpt, p4 ? "4" : "");
+        if (vpt)
+            snprintf(name, sizeof name, "forge_row_%s_v%d_p%s%s", op, vpt, p4 ? "4" : "", dsuf);
         else snprintf(name, sizeof name, "forge_row_%s_loop", op);
     } else {
         grid = std::min<unsigned>(blocks_needed, 1u << 20);
-        if (vpt) snprintf(name, sizeof name, "forge_row_%s_v%d", op, vpt);
+        if (vpt) snprintf(name, sizeof name, "forge_row_%s_v%d%s", op, vpt, dsuf);
         else snprintf(name, sizeof name, "forge_row_%s_loop", op);
     }
     if (shmem > rt->lds_bytes)
@@ -1644,12 +1655,34 @@ extern "C" forge_status forge_layer_norm_bwd(forge_runtime* rt, forge_stream* s,
                                0);
 }
 
-extern "C" forge_status forge_layer_norm_bwd_sgd(forge_runtime* rt, forge_stream* s,
-                                                 forge_slice x, forge_slice dy,
-                                                 forge_slice gamma, forge_slice beta,
-                                                 forge_slice dx, forge_slice dgamma,
-                                                 forge_slice dbeta, size_t rows, size_t cols,
-                                                 float eps, float lr) {
+// The norm backward's row dot operands (forge_*_norm_bwd_sgd_dot): sub
+// [rows, cols] is disjoint from dx, dot [rows] from every matrix operand.
+static forge_status row_dot_args(forge_slice x, forge_slice dy, forge_slice dx, forge_slice sub,
+                                 forge_slice dot, size_t rows, size_t cols, float dscale,
+                                 RowArgs* a) {
+    const size_t n = rows * cols;
+    FORGE_TRY(need(sub, n, "norm_bwd row-dot sub"));
+    FORGE_TRY(need(dot, rows, "norm_bwd row-dot dot"));
+    auto overlap = [](const float* p, size_t pn, const float* q, size_t qn) {
+        return pn && qn && p < q + qn && q < p + pn;
+    };
+    if (overlap(sub.ptr, n, dx.ptr, n))
+        return fail(FORGE_EINVAL, "norm_bwd row-dot: sub overlaps dx");
+    for (forge_slice m : {x, dy, dx, sub})
+        if (overlap(dot.ptr, rows, m.ptr, n))
+            return fail(FORGE_EINVAL, "norm_bwd row-dot: dot overlaps a matrix operand");
+    a->dsub = sub.ptr;
+    a->dot = dot.ptr;
+    a->dscale = dscale;
+    return FORGE_OK;
+}
+
+static forge_status layer_norm_bwd_sgd_impl(forge_runtime* rt, forge_stream* s, forge_slice x,
+                                            forge_slice dy, forge_slice gamma, forge_slice beta,
+                                            forge_slice dx, forge_slice dgamma, forge_slice dbeta,
+                                            size_t rows, size_t cols, float eps, float lr,
+                                            const forge_slice* sub, forge_slice dot,
+                                            float dscale) {
     if (!rt) return fail(FORGE_EINVAL, "runtime is null");
     FORGE_TRY(check_rows(rows, cols));
     FORGE_TRY(need(x, rows * cols, "layer_norm_bwd x"));
@@ -1660,11 +1693,33 @@ extern "C" forge_status forge_layer_norm_bwd_sgd(forge_runtime* rt, forge_stream
     FORGE_TRY(need_opt(dgamma, cols, "layer_norm_bwd dgamma"));
     FORGE_TRY(need_opt(dbeta, cols, "layer_norm_bwd dbeta"));
     RowArgs a{x.ptr, dx.ptr, dy.ptr, gamma.ptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, eps, 1.0f};
+    if (sub) FORGE_TRY(row_dot_args(x, dy, dx, *sub, dot, rows, cols, dscale, &a));
     NormSgd sgd;
     sgd.gamma = gamma.ptr;
     sgd.beta = beta.ptr;
     sgd.lr = lr;
     return row_launch(rt, s, "layer_norm_bwd", a, dgamma.ptr, dbeta.ptr, nullptr, 0, sgd);
+}
+
+extern "C" forge_status forge_layer_norm_bwd_sgd(forge_runtime* rt, forge_stream* s,
+                                                 forge_slice x, forge_slice dy,
+                                                 forge_slice gamma, forge_slice beta,
+                                                 forge_slice dx, forge_slice dgamma,
+                                                 forge_slice dbeta, size_t rows, size_t cols,
+                                                 float eps, float lr) {
+    return layer_norm_bwd_sgd_impl(rt, s, x, dy, gamma, beta, dx, dgamma, dbeta, rows, cols, eps,
+                                   lr, nullptr, forge_slice{nullptr, 0}, 1.0f);
+}
+
+extern "C" forge_status forge_layer_norm_bwd_sgd_dot(forge_runtime* rt, forge_stream* s,
+                                                     forge_slice x, forge_slice dy,
+                                                     forge_slice gamma, forge_slice beta,
+                                                     forge_slice dx, forge_slice dgamma,
+                                                     forge_slice dbeta, forge_slice sub,
+                                                     forge_slice dot, size_t rows, size_t cols,
+                                                     float eps, float lr, float dot_scale) {
+    return layer_norm_bwd_sgd_impl(rt, s, x, dy, gamma, beta, dx, dgamma, dbeta, rows, cols, eps,
+                                   lr, &sub, dot, dot_scale);
 }
 
 extern "C" forge_status forge_layer_norm_bwd_noalloc(forge_runtime* rt, forge_stream* s,
@@ -1714,10 +1769,11 @@ extern "C" forge_status forge_rms_norm_bwd(forge_runtime* rt, forge_stream* s, f
     return row_launch(rt, s, "rms_norm_bwd", a, dgamma.ptr, nullptr);
 }
 
-extern "C" forge_status forge_rms_norm_bwd_sgd(forge_runtime* rt, forge_stream* s, forge_slice x,
-                                               forge_slice dy, forge_slice gamma, forge_slice dx,
-                                               forge_slice dgamma, size_t rows, size_t cols,
-                                               float eps, float lr) {
+static forge_status rms_norm_bwd_sgd_impl(forge_runtime* rt, forge_stream* s, forge_slice x,
+                                          forge_slice dy, forge_slice gamma, forge_slice dx,
+                                          forge_slice dgamma, size_t rows, size_t cols, float eps,
+                                          float lr, const forge_slice* sub, forge_slice dot,
+                                          float dscale) {
     if (!rt) return fail(FORGE_EINVAL, "runtime is null");
     FORGE_TRY(check_rows(rows, cols));
     FORGE_TRY(need(x, rows * cols, "rms_norm_bwd x"));
@@ -1726,10 +1782,29 @@ extern "C" forge_status forge_rms_norm_bwd_sgd(forge_runtime* rt, forge_stream* 
     FORGE_TRY(need_opt(gamma, cols, "rms_norm_bwd gamma"));
     FORGE_TRY(need_opt(dgamma, cols, "rms_norm_bwd dgamma"));
     RowArgs a{x.ptr, dx.ptr, dy.ptr, gamma.ptr, nullptr, nullptr, nullptr, (int)rows, (int)cols, eps, 1.0f};
+    if (sub) FORGE_TRY(row_dot_args(x, dy, dx, *sub, dot, rows, cols, dscale, &a));
     NormSgd sgd;
     sgd.gamma = gamma.ptr;
     sgd.lr = lr;
     return row_launch(rt, s, "rms_norm_bwd", a, dgamma.ptr, nullptr, nullptr, 0, sgd);
+}
+
+extern "C" forge_status forge_rms_norm_bwd_sgd(forge_runtime* rt, forge_stream* s, forge_slice x,
+                                               forge_slice dy, forge_slice gamma, forge_slice dx,
+                                               forge_slice dgamma, size_t rows, size_t cols,
+                                               float eps, float lr) {
+    return rms_norm_bwd_sgd_impl(rt, s, x, dy, gamma, dx, dgamma, rows, cols, eps, lr, nullptr,
+                                 forge_slice{nullptr, 0}, 1.0f);
+}
+
+extern "C" forge_status forge_rms_norm_bwd_sgd_dot(forge_runtime* rt, forge_stream* s,
+                                                   forge_slice x, forge_slice dy,
+                                                   forge_slice gamma, forge_slice dx,
+                                                   forge_slice dgamma, forge_slice sub,
+                                                   forge_slice dot, size_t rows, size_t cols,
+                                                   float eps, float lr, float dot_scale) {
+    return rms_norm_bwd_sgd_impl(rt, s, x, dy, gamma, dx, dgamma, rows, cols, eps, lr, &sub, dot,
+                                 dot_scale);
 }
 
 extern "C" forge_status forge_binary(forge_runtime* rt, forge_stream* s, forge_slice l,

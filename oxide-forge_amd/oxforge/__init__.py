@@ -88,11 +88,12 @@ def _sl(a) -> Slice:
 def _epilogue(alpha=1.0, bias=None, residual=None, aux_mul=None, pre_out=None,
               activation=ACT_IDENTITY, update=False, update_scale=0.0, aux_activation=0,
               row_parts_in=None, row_parts=0, row_n=0, row_eps=1e-5, row_div=0,
-              row_sumsq_out=None, col_sums_out=None, col_sums_param=None, col_sums_lr=0.0):
+              row_sumsq_out=None, col_sums_out=None, col_sums_param=None, col_sums_lr=0.0,
+              row_sub=None):
     return GemmEpilogue(alpha, _sl(bias), _sl(residual), _sl(aux_mul), _sl(pre_out), activation,
                         1 if update else 0, update_scale, aux_activation, _sl(row_parts_in),
                         row_parts, row_n, row_eps, row_div, _sl(row_sumsq_out), _sl(col_sums_out),
-                        _sl(col_sums_param), col_sums_lr)
+                        _sl(col_sums_param), col_sums_lr, _sl(row_sub))
 
 
 class Runtime:
@@ -216,7 +217,7 @@ class Runtime:
         """forge_gemm_ex_f32; epilogue keywords as _epilogue (alpha, bias,
         residual, aux_mul, pre_out, activation, update, update_scale,
         aux_activation, row_parts_in, row_parts, row_n, row_eps, row_div,
-        row_sumsq_out, col_sums_out, col_sums_param, col_sums_lr)."""
+        row_sumsq_out, col_sums_out, col_sums_param, col_sums_lr, row_sub)."""
         ep = _epilogue(**epilogue)
         call("forge_gemm_ex_f32", self.handle, stream, int(trans_a), int(trans_b), A.slice,
              B.slice, C.slice, M, N, K, byref(ep))
@@ -286,6 +287,20 @@ class Runtime:
                          stream=None) -> None:
         call("forge_rms_norm_bwd_sgd", self.handle, stream, x.slice, dy.slice, _sl(gamma),
              dx.slice, _sl(dgamma), rows, cols, eps, lr)
+
+    def layer_norm_bwd_sgd_dot(self, x, dy, dx, sub, dot, rows, cols, lr, dot_scale=1.0,
+                               gamma=None, beta=None, dgamma=None, dbeta=None, eps=1e-5,
+                               stream=None) -> None:
+        """layer_norm_bwd_sgd plus dot[r] = dot_scale * sum_c dx[r,c] (x[r,c] - sub[r,c])."""
+        call("forge_layer_norm_bwd_sgd_dot", self.handle, stream, x.slice, dy.slice, _sl(gamma),
+             _sl(beta), dx.slice, _sl(dgamma), _sl(dbeta), _sl(sub), _sl(dot), rows, cols, eps,
+             lr, dot_scale)
+
+    def rms_norm_bwd_sgd_dot(self, x, dy, dx, sub, dot, rows, cols, lr, dot_scale=1.0,
+                             gamma=None, dgamma=None, eps=1e-5, stream=None) -> None:
+        """rms_norm_bwd_sgd plus the row dot of layer_norm_bwd_sgd_dot."""
+        call("forge_rms_norm_bwd_sgd_dot", self.handle, stream, x.slice, dy.slice, _sl(gamma),
+             dx.slice, _sl(dgamma), _sl(sub), _sl(dot), rows, cols, eps, lr, dot_scale)
 
     def sum_cols_sgd(self, m, rows, cols, lr, out=None, param=None, stream=None) -> None:
         call("forge_sum_cols_sgd", self.handle, stream, m.slice, rows, cols, _sl(out), _sl(param),

@@ -79,6 +79,7 @@ class GemmEpilogue(ctypes.Structure):
         ("col_sums_out", Slice),
         ("col_sums_param", Slice),
         ("col_sums_lr", c_float),
+        ("row_sub", Slice),
     ]
 
 
@@ -150,6 +151,10 @@ SIGNATURES = {
                                  c_size_t, c_float, c_float],
     "forge_rms_norm_bwd_sgd": [RT, ST, Slice, Slice, Slice, Slice, Slice, c_size_t, c_size_t,
                                c_float, c_float],
+    "forge_layer_norm_bwd_sgd_dot": [RT, ST, Slice, Slice, Slice, Slice, Slice, Slice, Slice,
+                                     Slice, Slice, c_size_t, c_size_t, c_float, c_float, c_float],
+    "forge_rms_norm_bwd_sgd_dot": [RT, ST, Slice, Slice, Slice, Slice, Slice, Slice, Slice,
+                                   c_size_t, c_size_t, c_float, c_float, c_float],
     "forge_sum_cols_sgd": [RT, ST, Slice, c_size_t, c_size_t, Slice, Slice, c_float],
     "forge_rms_norm_rows": [RT, ST, Slice, Slice, c_size_t, c_size_t, c_float],
     "forge_rms_norm_rows_out": [RT, ST, Slice, Slice, Slice, c_size_t, c_size_t, c_float],

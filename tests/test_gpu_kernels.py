@@ -592,6 +592,83 @@ def test_norm_bwd_sgd_matches_separate_launches(rt, rows, cols):
     assert np.array_equal(fdg.numpy(), rdg.numpy()) and np.array_equal(g1.numpy(), g0.numpy())
 
 
+@pytest.mark.parametrize("rows,cols", [(513, 64), (300, 500), (257, 1000), (4096, 2048),
+                                       (96, 4096), (65536, 1024), (77, 1001), (0, 64)])
+def test_norm_bwd_row_dot(rt, rows, cols):
+    """forge_layer_norm_bwd_sgd_dot / forge_rms_norm_bwd_sgd_dot (the
+    attention backward's softmax row term): dx, the gradients and the
+    updated parameters bit for bit those of the _sgd entry points, with
+    gamma/beta (the column-partial instances) and without (the plain ones);
+    dot[r] = s * sum_c dx[r,c] (x[r,c] - sub[r,c]) from the returned dx within
+    (cols + 8) u |s| sum_c |dx| |x - sub| of the f64 value (one rounding for
+    x - sub, one per product, at most cols - 1 in the sum, one for s), and
+    nothing written past `rows`.  The widths take every register instance
+    (1, 2, 4, 8 and 16 float4 per lane; the four-wave partial instance at
+    65536 rows) and the looping path (1001 columns, and 4096 with gamma)."""
+    say(f"norm bwd row dot {rows}x{cols}")
+    u = 2.0 ** -24
+    x = synth.normal((max(rows, 1), cols), 163)[:rows]
+    dy = synth.normal((max(rows, 1), cols), 164)[:rows]
+    sub = synth.normal((max(rows, 1), cols), 167)[:rows]
+    gam, bet = synth.normal((cols,), 165, 1.0, 0.1), synth.normal((cols,), 166, 0.0, 0.1)
+    lr, s = 1e-3, 1.0 / np.sqrt(cols)
+    n = rows * cols
+    dev = (lambda a: rt.array(np.ascontiguousarray(a))) if n else (lambda a: rt.empty((0,)))
+    dX, dDY, dSUB = dev(x), dev(dy), dev(sub)
+    rdx, fdx = rt.empty((max(n, 1),)), rt.empty((max(n, 1),))
+    for norm in ("layer", "rms"):
+        for params in (True, False):
+            say(f"  {norm} params={params}")
+            g0, b0, g1, b1 = (rt.array(v) for v in (gam, bet, gam, bet))
+            rdg, rdb, fdg, fdb = (rt.empty((cols,)) for _ in range(4))
+            dot = rt.array(np.full(rows + 1, np.nan, np.float32))
+            if norm == "layer":
+                kw = dict(gamma=g0, beta=b0, dgamma=rdg, dbeta=rdb) if params else {}
+                rt.layer_norm_bwd_sgd(dX, dDY, rdx, rows, cols, lr, **kw)
+                kw = dict(gamma=g1, beta=b1, dgamma=fdg, dbeta=fdb) if params else {}
+                rt.layer_norm_bwd_sgd_dot(dX, dDY, fdx, dSUB, dot, rows, cols, lr, dot_scale=s,
+                                          **kw)
+            else:
+                kw = dict(gamma=g0, dgamma=rdg) if params else {}
+                rt.rms_norm_bwd_sgd(dX, dDY, rdx, rows, cols, lr, **kw)
+                kw = dict(gamma=g1, dgamma=fdg) if params else {}
+                rt.rms_norm_bwd_sgd_dot(dX, dDY, fdx, dSUB, dot, rows, cols, lr, dot_scale=s,
+                                        **kw)
+            got_dx = fdx.numpy()[:n]
+            assert np.array_equal(got_dx, rdx.numpy()[:n])
+            if params:
+                for a, b in ((fdg, rdg), (g1, g0)) + (((fdb, rdb), (b1, b0))
+                                                      if norm == "layer" else ()):
+                    assert np.array_equal(a.numpy(), b.numpy())
+            got = dot.numpy()
+            assert np.isnan(got[rows])
+            if rows:
+                d64 = got_dx.reshape(rows, cols).astype(np.float64)
+                w = x.astype(np.float64) - sub.astype(np.float64)
+                ref = s * (d64 * w).sum(axis=1)
+                bound = (cols + 8) * u * s * (np.abs(d64) * np.abs(w)).sum(axis=1)
+                err = np.abs(got[:rows] - ref)
+                assert np.all(err <= bound), float(np.max(err / bound))
+
+
+def test_norm_bwd_row_dot_rejects_overlaps(rt):
+    """The row dot's operands: sub may not overlap dx (not even be it), nor
+    dot any matrix operand."""
+    rows, cols = 64, 256
+    x, dy = rt.array(synth.normal((rows, cols), 1)), rt.array(synth.normal((rows, cols), 2))
+    sub = rt.array(synth.normal((rows, cols), 3))
+    big = rt.empty((rows * cols + rows,))
+    dx = big.view(0, (rows, cols))
+    for args in ((sub, big.view(cols, (rows,))),            # dot inside dx
+                 (big.view(rows, (rows, cols)), rt.empty((rows,))),  # sub across dx
+                 (dx, rt.empty((rows,))),                    # sub is dx
+                 (sub, sub.view(5, (rows,)))):               # dot inside sub
+        with pytest.raises(oxforge.ForgeError):
+            rt.layer_norm_bwd_sgd_dot(x, dy, dx, args[0], args[1], rows, cols, 1e-3)
+        with pytest.raises(oxforge.ForgeError):
+            rt.rms_norm_bwd_sgd_dot(x, dy, dx, args[0], args[1], rows, cols, 1e-3)
+
+
 # ------------------------------------------------------------ elementwise
 OPS = [(oxforge.ADD, np.add), (oxforge.SUB, np.subtract), (oxforge.MUL, np.multiply),
        (oxforge.DIV, np.divide)]
@@ -999,6 +1076,40 @@ def test_gemm_every_tile_instance(rt, tile, ta, tb):
     if "_x" in tile:  # unguarded tiles refuse shapes they do not divide
         with pytest.raises(oxforge.ForgeError):
             rt.gemm_ex_tile(tile, dA, dB, dZ, M - 1, N, K, trans_a=ta, trans_b=tb)
+
+
+@pytest.mark.parametrize("tile", TILES + [None])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_epilogue_row_subtrahend(rt, tile, ta, tb):
+    """forge_gemm_epilogue row_sub (the softmax backward formed in the dP
+    product: alpha = s, row_sub = s D, aux_mul = P): Y = ((alpha Z - r_row)
+    + bias + residual) * aux bit for bit the same f32 steps applied to the
+    plain product Z, on every tile instance, and through the dispatcher at a
+    split-K shape (256x128x2048, the reduction kernel's epilogue) and a
+    guarded one (50x70x33)."""
+    shapes = [(256, 128, 2048), (50, 70, 33)] if tile is None else \
+        [tuple(2 * int(x) for x in tile.split("x")[:2]) + (192,)]
+    run = (lambda *a, **k: rt.gemm_ex(*a, **k)) if tile is None else \
+        (lambda *a, **k: rt.gemm_ex_tile(tile, *a, **k))
+    for M, N, K in shapes:
+        say(f"gemm row_sub tile={tile} ta={ta} tb={tb} {M}x{N}x{K}")
+        A = synth.uniform((K, M) if ta else (M, K), 41)
+        B = synth.uniform((N, K) if tb else (K, N), 42)
+        r, bias = synth.uniform((M,), 43), synth.uniform((N,), 44)
+        res, aux = synth.uniform((M, N), 45), synth.uniform((M, N), 46)
+        dA, dB, dr, dbias, dres, daux = (rt.array(v) for v in (A, B, r, bias, res, aux))
+        dZ, dY, dY2 = rt.empty((M, N)), rt.empty((M, N)), rt.empty((M, N))
+        run(dA, dB, dZ, M, N, K, trans_a=ta, trans_b=tb)
+        Z = dZ.numpy()
+        alpha = np.float32(1.0 / np.sqrt(64.0) + 0.01)
+        run(dA, dB, dY, M, N, K, trans_a=ta, trans_b=tb, alpha=float(alpha), row_sub=dr,
+            aux_mul=daux)
+        assert np.array_equal(dY.numpy(), (alpha * Z - r[:, None]) * aux)
+        run(dA, dB, dY2, M, N, K, trans_a=ta, trans_b=tb, alpha=float(alpha), row_sub=dr,
+            bias=dbias, residual=dres, aux_mul=daux)
+        assert np.array_equal(dY2.numpy(), (((alpha * Z - r[:, None]) + bias) + res) * aux)
+    with pytest.raises(oxforge.ForgeError):  # row_sub shorter than M
+        run(dA, dB, dY, M, N, K, trans_a=ta, trans_b=tb, row_sub=rt.empty((M - 1,)))
 
 
 U32 = 2.0 ** -24
