@@ -247,7 +247,7 @@ struct XReads {
 // alpha, row divide, row subtrahend, bias, residual, aux (or act'(aux)),
 // pre-activation store, activation, and store or SGD update -- the order of
 // gemm_epilogue_store, each one rounded f32 operation.
-template <bool EPI>
+template <bool EPI, bool ROWSUB>
 __device__ __forceinline__ void x_epi_load(const GemmArgs& p, long long idx, int row, f4& res,
                                            f4& mul, f4& old, float& sub) {
     res = mul = old = f4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -256,7 +256,9 @@ __device__ __forceinline__ void x_epi_load(const GemmArgs& p, long long idx, int
         if (p.residual) res = *reinterpret_cast<const f4*>(p.residual + idx);
         if (p.aux) mul = *reinterpret_cast<const f4*>(p.aux + idx);
         if (p.update) old = *reinterpret_cast<const f4*>(p.C + idx);
-        if (p.row_sub) sub = p.row_sub[row];
+        if constexpr (ROWSUB) {
+            if (p.row_sub) sub = p.row_sub[row];
+        }
     }
 }
 
@@ -321,7 +323,7 @@ struct XRowStats {
     int row[NB];
 };
 
-template <bool EPI, int NB, bool STATS = false>
+template <bool EPI, int NB, bool STATS = false, bool ROWSUB = false>
 __device__ __forceinline__ void x_epi_store(const GemmArgs& p, const f4 (&z)[NB],
                                             const f4 (&res)[NB], const f4 (&mul)[NB],
                                             const f4 (&old)[NB], const float (&sub)[NB], f4 bias,
@@ -344,9 +346,12 @@ __device__ __forceinline__ void x_epi_store(const GemmArgs& p, const f4 (&z)[NB]
 #pragma unroll
                 for (int i = 0; i < 4 * NB; i++) y[i] = y[i] * rs.rinv[i / 4];
         }
-        if (p.row_sub)
+        // The row subtrahend (the _r instances only).
+        if constexpr (ROWSUB) {
+            if (p.row_sub)
 #pragma unroll
-            for (int i = 0; i < 4 * NB; i++) y[i] = y[i] - sub[i / 4];
+                for (int i = 0; i < 4 * NB; i++) y[i] = y[i] - sub[i / 4];
+        }
         if (p.bias)
 #pragma unroll
             for (int u = 0; u < NB; u++) {
@@ -433,9 +438,10 @@ __device__ __forceinline__ void x_epi_store(const GemmArgs& p, const f4 (&z)[NB]
 #endif
 
 template <int BM, int BN, int BK, bool TA, bool TB, bool EPI, int WM = 2, int WN = 2,
-          bool STATS = false>
+          bool STATS = false, bool ROWSUB = false>
 __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     static_assert(EPI || !STATS, "row statistics ride on the fused epilogue");
+    static_assert(!ROWSUB || STATS, "the row subtrahend rides on the statistics instances");
     constexpr int NW = WM * WN;  // waves: WM x WN sub-tiles of TM x TN
     constexpr int TM = BM / WM, TN = BN / WN;
     // MFMA block: 16 x 16 (v_mfma_f32_16x16x4_f32, four k per instruction,
@@ -721,9 +727,10 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
             if constexpr (STATS) {
                 if (p.row_part) rs.rinv[u] = smem_all[SMEM + a_off + rr];
             }
-            x_epi_load<EPI>(p, idx[u], row0 + rr, res[u], mul[u], old[u], sub[u]);
+            x_epi_load<EPI, ROWSUB>(p, idx[u], row0 + rr, res[u], mul[u], old[u], sub[u]);
         }
-        x_epi_store<EPI, NB, STATS>(p, z, res, mul, old, sub, bias4, idx, rs, lane_col, cs);
+        x_epi_store<EPI, NB, STATS, ROWSUB>(p, z, res, mul, old, sub, bias4, idx, rs, lane_col,
+                                            cs);
     }
     if constexpr (STATS) {
         if (p.col_part) {
@@ -742,9 +749,10 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
 }
 
 template <int BM, int BN, int BK, bool TA, bool TB, bool EPI, int WM = 2, int WN = 2,
-          bool STATS = false>
+          bool STATS = false, bool ROWSUB = false>
 __device__ __forceinline__ void gemm_single_x(const GemmArgs& p) {
-    gemm_body_x<BM, BN, BK, TA, TB, EPI, WM, WN, STATS>(p, xcd_logical(blockIdx.x, gridDim.x));
+    gemm_body_x<BM, BN, BK, TA, TB, EPI, WM, WN, STATS, ROWSUB>(p,
+                                                                xcd_logical(blockIdx.x, gridDim.x));
 }
 
 template <int BM, int BN, int BK, bool TA, bool TB, int WM = 2, int WN = 2>

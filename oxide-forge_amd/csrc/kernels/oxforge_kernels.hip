@@ -62,6 +62,24 @@ GEMM_STATS_FAMILY(nt, false, true)
 GEMM_STATS_FAMILY(tn, true, false)
 GEMM_STATS_FAMILY(tt, true, true)
 
+// Row-subtrahend instances (forge_gemm_<ab>_<tile>_r): the statistics
+// instances plus forge_gemm_epilogue row_sub (the softmax backward formed in
+// the dP product).  Separate again, so the _e and _s kernels stay as they
+// are (with row_sub in them the C4 forward ran 0.9-1.4 us slower).
+#define GEMM_X_ROWSUB_KERNEL(NAME, BM, BN, BK, TA, TB)                              \
+    FORGE_KERNEL void __launch_bounds__(256, GEMM_X_OCC(BM, BN, BK)) NAME(GemmArgs p) { \
+        gemm_single_x<BM, BN, BK, TA, TB, true, 2, 2, true, true>(p);               \
+    }
+#define GEMM_ROWSUB_FAMILY(AB, TA, TB)                                                  \
+    GEMM_X_ROWSUB_KERNEL(forge_gemm_##AB##_128x128x32_x_r, 128, 128, 32, TA, TB)       \
+    GEMM_X_ROWSUB_KERNEL(forge_gemm_##AB##_128x64x32_x_r, 128, 64, 32, TA, TB)         \
+    GEMM_X_ROWSUB_KERNEL(forge_gemm_##AB##_64x128x32_x_r, 64, 128, 32, TA, TB)         \
+    GEMM_X_ROWSUB_KERNEL(forge_gemm_##AB##_64x64x32_x_r, 64, 64, 32, TA, TB)
+GEMM_ROWSUB_FAMILY(nn, false, false)
+GEMM_ROWSUB_FAMILY(nt, false, true)
+GEMM_ROWSUB_FAMILY(tn, true, false)
+GEMM_ROWSUB_FAMILY(tt, true, true)
+
 // Batched instances (forge_gemm_batch_<ab>_<tile>): several same-shape
 // products per launch, each with its own operands and epilogue.  They serve
 // the Q/K/V projections, forge_gemm_batch_f32 and the K slices of split-K
@@ -111,6 +129,14 @@ GEMM_X8_STATS_KERNEL(forge_gemm_nn_64x128x32_x8_s, false, false)
 GEMM_X8_STATS_KERNEL(forge_gemm_nt_64x128x32_x8_s, false, true)
 GEMM_X8_STATS_KERNEL(forge_gemm_tn_64x128x32_x8_s, true, false)
 GEMM_X8_STATS_KERNEL(forge_gemm_tt_64x128x32_x8_s, true, true)
+#define GEMM_X8_ROWSUB_KERNEL(NAME, TA, TB)                                         \
+    FORGE_KERNEL void __launch_bounds__(512, 1) NAME(GemmArgs p) {                  \
+        gemm_single_x<64, 128, 32, TA, TB, true, 4, 2, true, true>(p);             \
+    }
+GEMM_X8_ROWSUB_KERNEL(forge_gemm_nn_64x128x32_x8_r, false, false)
+GEMM_X8_ROWSUB_KERNEL(forge_gemm_nt_64x128x32_x8_r, false, true)
+GEMM_X8_ROWSUB_KERNEL(forge_gemm_tn_64x128x32_x8_r, true, false)
+GEMM_X8_ROWSUB_KERNEL(forge_gemm_tt_64x128x32_x8_r, true, true)
 #define GEMM_X8_BATCH_KERNEL(NAME, TA, TB)                                            \
     FORGE_KERNEL void __launch_bounds__(512, 1) NAME(GemmBatchArgs b) {               \
         gemm_batch_x<64, 128, 32, TA, TB, 4, 2>(b);                                 \

@@ -668,18 +668,22 @@ constexpr int kUnguardedCount = 6;
 // as 512 tiles of 64x128 at 139.
 constexpr double kSingleWorkgroupFactor = 0.96;
 
-enum class GemmKind { Plain, Epilogue, Batch, Stats };
+enum class GemmKind { Plain, Epilogue, Batch, Stats, RowSub };
 
 // Kernel that runs a tile: plain NN (forge_gemm_nn_<tile>), fused epilogue
 // (forge_gemm_<ab>_<tile>_e), fused epilogue with row statistics and column
-// sums (forge_gemm_<ab>_<tile>_s) or batched (forge_gemm_batch_<ab>_<tile>).
+// sums (forge_gemm_<ab>_<tile>_s), the same with the row subtrahend
+// (forge_gemm_<ab>_<tile>_r) or batched (forge_gemm_batch_<ab>_<tile>).
 void gemm_kernel_name(char* out, size_t cap, GemmKind kind, int ta, int tb,
                       const GemmConfig& cfg) {
     if (kind == GemmKind::Batch)
         snprintf(out, cap, "forge_gemm_batch_%s_%s", gemm_ab(ta, tb), cfg.tag);
     else
         snprintf(out, cap, "forge_gemm_%s_%s%s", gemm_ab(ta, tb), cfg.tag,
-                 kind == GemmKind::Epilogue ? "_e" : kind == GemmKind::Stats ? "_s" : "");
+                 kind == GemmKind::Epilogue ? "_e"
+                 : kind == GemmKind::Stats  ? "_s"
+                 : kind == GemmKind::RowSub ? "_r"
+                                            : "");
 }
 
 // Workgroups of a kernel that one CU holds at once (its registers and LDS),
@@ -866,9 +870,12 @@ forge_status gemm_args(int ta, int tb, forge_slice A, forge_slice B, forge_slice
     return FORGE_OK;
 }
 
+// Epilogues that need the statistics instances on the unguarded tiles (_s,
+// or _r with the row subtrahend): row statistics, column sums, row_sub.  The
+// plain fused instances (_e) carry none of that code.
 bool gemm_has_stats(const forge_gemm_epilogue* ep) {
     return ep && (ep->row_parts_in.ptr || ep->row_sumsq_out.ptr || ep->col_sums_out.ptr ||
-                  ep->col_sums_param.ptr);
+                  ep->col_sums_param.ptr || ep->row_sub.ptr);
 }
 
 // Split-K: `splits` K slices of the product as one batched launch writing
@@ -1026,7 +1033,8 @@ forge_status gemm_dispatch(forge_runtime* rt, forge_stream* s, int ta, int tb, f
     if (M == 0 || N == 0) return gemm_stats_empty(rt, s, ep, N);
     const GemmConfig* split_cfg = nullptr;
     const int splits = choose_splits(rt, ta, tb, M, N, K, aligned, &split_cfg);
-    const GemmKind kind = gemm_has_stats(ep)            ? GemmKind::Stats
+    const GemmKind kind = ep && ep->row_sub.ptr        ? GemmKind::RowSub
+                          : gemm_has_stats(ep)            ? GemmKind::Stats
                           : plain_name && !ta && !tb ? GemmKind::Plain
                                                      : GemmKind::Epilogue;
     const GemmPlan plan = splits > 1 ? GemmPlan{split_cfg, 0}
@@ -1044,10 +1052,11 @@ forge_status gemm_dispatch(forge_runtime* rt, forge_stream* s, int ta, int tb, f
     } else {
         char name[96];
         // The guarded tile has no statistics instance: its fused kernel
-        // divides by row_d per element and the sums come from C.
-        gemm_kernel_name(name, sizeof name, xtile || kind != GemmKind::Stats ? kind
-                                                                              : GemmKind::Epilogue,
-                         ta, tb, cfg);
+        // divides by row_d and subtracts row_sub per element, and the sums
+        // come from C.
+        const bool stats_kind = kind == GemmKind::Stats || kind == GemmKind::RowSub;
+        gemm_kernel_name(name, sizeof name, xtile || !stats_kind ? kind : GemmKind::Epilogue, ta,
+                         tb, cfg);
         size_t shmem = 0;
         if (plan.cap) FORGE_TRY(occupancy_cap_shmem(rt, name, plan.cap, &shmem));
         unsigned tiles = (unsigned)(((M + cfg.bm - 1) / cfg.bm) * ((N + cfg.bn - 1) / cfg.bn));
@@ -1480,7 +1489,10 @@ extern "C" forge_status forge_gemm_ex_f32_tile(forge_runtime* rt, forge_stream* 
     FORGE_TRY(gemm_stats_prepare(rt, s, ep, a, xtile, *cfg, ws, &w));
     char name[96];
     snprintf(name, sizeof name, "forge_gemm_%s_%s_%s", gemm_ab(trans_a, trans_b), cfg->tag,
-             xtile && gemm_has_stats(ep) ? "s" : "e");
+             !xtile                        ? "e"
+             : ep && ep->row_sub.ptr       ? "r"
+             : gemm_has_stats(ep)          ? "s"
+                                           : "e");
     size_t shmem = 0;
     if (cap) FORGE_TRY(occupancy_cap_shmem(rt, name, cap, &shmem));
     const unsigned tiles =
