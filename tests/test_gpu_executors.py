@@ -277,32 +277,37 @@ def test_query_chunked_attention_forward_with_split_products(rt):
     assert rel(yc, ref) <= TOL
 
 
-@pytest.mark.parametrize("S,chunk_rows", [(320, 64), (320, 128), (512, 192)])
-def test_query_chunked_attention_training_step(rt, S, chunk_rows):
+@pytest.mark.parametrize("S,chunk_rows,norm", [(320, 64, net.LAYER), (320, 128, net.LAYER),
+                                              (512, 192, net.LAYER), (320, 64, net.RMS)])
+def test_query_chunked_attention_training_step(rt, S, chunk_rows, norm):
     """Training with the score budget below seq x seq: the forward keeps no
     probabilities and backward recomputes them per chunk (dV and dK summed
-    over the chunks in order).  The forward output is bit-identical to the
-    unchunked step; dX and every parameter gradient match the f64 oracle, and
-    the unchunked step's to within 1e-5 relative."""
+    over the chunks in order; each chunk's dS formed in its dP product from
+    the row term the norm backward wrote for all rows).  The forward output
+    is bit-identical to the unchunked step; dX and every parameter gradient
+    match the f64 oracle, and the unchunked step's to within 1e-5
+    relative."""
     H, F, O = 64, 128, 48
-    say(f"chunked attention training S={S} chunk={chunk_rows}")
-    p = make_params(S, H, F, O, 43, bias=True, affine=True, norm=net.LAYER)
+    say(f"chunked attention training S={S} chunk={chunk_rows} norm={norm}")
+    p = make_params(S, H, F, O, 43, bias=True, affine=True, norm=norm)
     X = synth.normal((S, H), 10)
     dY = synth.normal((S, O), 11)
     lr = 1e-3
-    Tc = net.Transformer(rt, p, S, H, F, O, net.LAYER, net.ENCODER_TRAINING)
-    Tu = net.Transformer(rt, p, S, H, F, O, net.LAYER, net.ENCODER_TRAINING)
+    Tc = net.Transformer(rt, p, S, H, F, O, norm, net.ENCODER_TRAINING)
+    Tu = net.Transformer(rt, p, S, H, F, O, norm, net.ENCODER_TRAINING)
     Tc.set_score_bytes(chunk_rows * S * 4)
     yc, yu = Tc.forward(rt.array(X)).numpy(), Tu.forward(rt.array(X)).numpy()
     assert np.array_equal(yc, yu)
     dxc, dxu = rt.empty((S, H)), rt.empty((S, H))
     gc = Tc.backward(rt.array(dY), lr, dxc, want_grads=True)
     gu = Tu.backward(rt.array(dY), lr, dxu, want_grads=True)
-    _, cache = ex.transformer_forward(p, X, net.LAYER)
-    rdX, rg = ex.transformer_backward(p, cache, dY, net.LAYER)
+    _, cache = ex.transformer_forward(p, X, norm)
+    rdX, rg = ex.transformer_backward(p, cache, dY, norm)
     assert rel(dxc.numpy(), rdX) <= TOL
     assert rel(dxc.numpy(), dxu.numpy()) <= 1e-5
     for k in net.TP_SLOTS:
+        if rg.get(k) is None or p.get(k) is None:
+            continue
         g = gc[k].numpy()
         if k == "BK":
             assert np.max(np.abs(g)) / np.max(np.abs(rg["BV"])) <= TOL
