@@ -1254,8 +1254,11 @@ forge_status row_launch(forge_runtime* rt, forge_stream* s, const char* op, RowA
                         size_t scratch_len = 0, NormSgd sgd = NormSgd()) {
     if (a.rows == 0 || a.cols == 0) {
         // No rows: zero gradients, and the SGD step leaves the parameters.
+        // Empty rows: each row dot is zero.
         if (dgamma) FORGE_TRY(forge_fill(rt, s, forge_slice{dgamma, (size_t)a.cols}, 0.0f));
         if (dbeta) FORGE_TRY(forge_fill(rt, s, forge_slice{dbeta, (size_t)a.cols}, 0.0f));
+        if (a.dot && a.rows > 0)
+            FORGE_TRY(forge_fill(rt, s, forge_slice{a.dot, (size_t)a.rows}, 0.0f));
         return FORGE_OK;
     }
     // The softmax and RMSNorm forward kernels store non-temporally at every

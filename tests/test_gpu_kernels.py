@@ -593,7 +593,7 @@ def test_norm_bwd_sgd_matches_separate_launches(rt, rows, cols):
 
 
 @pytest.mark.parametrize("rows,cols", [(513, 64), (300, 500), (257, 1000), (4096, 2048),
-                                       (96, 4096), (65536, 1024), (77, 1001), (0, 64)])
+                                       (96, 4096), (65536, 1024), (77, 1001), (0, 64), (7, 0)])
 def test_norm_bwd_row_dot(rt, rows, cols):
     """forge_layer_norm_bwd_sgd_dot / forge_rms_norm_bwd_sgd_dot (the
     attention backward's softmax row term): dx, the gradients and the
@@ -604,14 +604,15 @@ def test_norm_bwd_row_dot(rt, rows, cols):
     x - sub, one per product, at most cols - 1 in the sum, one for s), and
     nothing written past `rows`.  The widths take every register instance
     (1, 2, 4, 8 and 16 float4 per lane; the four-wave partial instance at
-    65536 rows) and the looping path (1001 columns, and 4096 with gamma)."""
+    65536 rows) and the looping path (1001 columns, and 4096 with gamma);
+    rows of no columns have a zero dot."""
     say(f"norm bwd row dot {rows}x{cols}")
     u = 2.0 ** -24
     x = synth.normal((max(rows, 1), cols), 163)[:rows]
     dy = synth.normal((max(rows, 1), cols), 164)[:rows]
     sub = synth.normal((max(rows, 1), cols), 167)[:rows]
     gam, bet = synth.normal((cols,), 165, 1.0, 0.1), synth.normal((cols,), 166, 0.0, 0.1)
-    lr, s = 1e-3, 1.0 / np.sqrt(cols)
+    lr, s = 1e-3, 1.0 / np.sqrt(max(cols, 1))
     n = rows * cols
     dev = (lambda a: rt.array(np.ascontiguousarray(a))) if n else (lambda a: rt.empty((0,)))
     dX, dDY, dSUB = dev(x), dev(dy), dev(sub)
