@@ -67,9 +67,11 @@ def dispatcher_kernel_names():
     for ab in ("nn", "nt", "tn", "tt"):
         for tag in tiles + ("64x64x16_2x2_g",):
             names.append(f"forge_gemm_{ab}_{tag}_e")
-        # row statistics / column sums instances of the unguarded tiles
+        # row statistics / column sums instances of the unguarded tiles, and
+        # the same with the row subtrahend
         for tag in tiles + ("64x128x32_x8",):
             names.append(f"forge_gemm_{ab}_{tag}_s")
+            names.append(f"forge_gemm_{ab}_{tag}_r")
     for tag in tiles + ("128x256x32_x", "64x64x16_2x2_g"):
         names.append(f"forge_gemm_nn_{tag}")
     # batched (forge_gemm_batch_f32, Q/K/V and split-K slices): every layout
@@ -88,7 +90,11 @@ def dispatcher_kernel_names():
     for op in ("layer_norm_bwd", "rms_norm_bwd"):
         for v in (1, 2, 4, 8):
             names.append(f"forge_row_{op}_v{v}_p")
+            names.append(f"forge_row_{op}_v{v}_p_d")
+        for v in (1, 2, 4, 8, 16):
+            names.append(f"forge_row_{op}_v{v}_d")
         names.append(f"forge_row_{op}_v4_p4")
+        names.append(f"forge_row_{op}_v4_p4_d")
     for op in ("add", "sub", "mul", "div"):
         for k in ("binary", "binary_assign", "by_rows"):
             for s in ("v", "s"):
