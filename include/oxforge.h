@@ -279,6 +279,23 @@ forge_status forge_gemm_ex_f32(forge_runtime *rt, forge_stream *stream,
                                size_t N, size_t K,
                                const forge_gemm_epilogue *epilogue);
 
+/* The sum of count (1 to 3) products under one fused epilogue:
+ *   C = epilogue(sum_z op(A_z) op(B_z)),
+ * each A_z [M, K] and B_z [K, N] after op (trans_a / trans_b as in
+ * forge_gemm_ex_f32).  It replaces the reference's chain of input-gradient
+ * products that accumulate onto one matrix (QkvProjection::backward_self's
+ * dX += G_i W_i^T for Q, K and V, attention.rs:104-144): one launch, one
+ * read and one write of C instead of one per product.  The result is
+ * bit-identical to forge_gemm_ex_f32 on the operands concatenated along K
+ * (K' = count K): with an unguarded tile, no K split and no row statistics
+ * or column sums in the epilogue it is one launch whose slabs come from
+ * each product in turn; otherwise the operands are first copied into that
+ * concatenation. */
+forge_status forge_gemm_sum_f32(forge_runtime *rt, forge_stream *stream, int trans_a,
+                                int trans_b, size_t count, const forge_slice *A,
+                                const forge_slice *B, forge_slice C, size_t M, size_t N,
+                                size_t K, const forge_gemm_epilogue *epilogue);
+
 /* Tuning entry point (no reference counterpart): forge_gemm_f32 with an
  * explicit plain tile instance: "<BM>x<BN>x<BK>_x" for the unguarded
  * four-wave tiles (128x256x32, 128x128x32, 128x64x32, 64x128x32, 64x64x32),

@@ -70,9 +70,18 @@ struct GemmArgs {
     // [M] or null: Z = Z - row_sub[r] after alpha and the row_div divide
     // (the softmax backward's row term, folded into the dP product).
     const float* row_sub;
+    // K segments (the _k instances): the product is sum_s op(A_s) op(B_s)
+    // over K / k_seg segments of k_seg each, A_0 = A, B_0 = B, then A1/B1
+    // and A2/B2, every segment with the pitches lda / ldb -- the product of
+    // the operands concatenated along K, in the same sum order.
+    const float* A1;
+    const float* A2;
+    const float* B1;
+    const float* B2;
+    int k_seg;
 };
 // The host fills the same layout (runtime.cpp GemmArgs).
-static_assert(sizeof(GemmArgs) == 176, "kernel argument layout");
+static_assert(sizeof(GemmArgs) == 216, "kernel argument layout");
 
 constexpr int GEMM_GROUP_M = 8;
 constexpr int LDS_PAD = 4;

@@ -438,7 +438,7 @@ __device__ __forceinline__ void x_epi_store(const GemmArgs& p, const f4 (&z)[NB]
 #endif
 
 template <int BM, int BN, int BK, bool TA, bool TB, bool EPI, int WM = 2, int WN = 2,
-          bool STATS = false, bool ROWSUB = false>
+          bool STATS = false, bool ROWSUB = false, bool SEGK = false>
 __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     static_assert(EPI || !STATS, "row statistics ride on the fused epilogue");
     static_assert(!ROWSUB || STATS, "the row subtrahend rides on the statistics instances");
@@ -491,6 +491,27 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
     const long long b_kstride = TB ? BK : (long long)BK * p.ldb;
     const float* a_base = TA ? p.A + m0 : p.A + (long long)m0 * p.lda;
     const float* b_base = TB ? p.B + (long long)n0 * p.ldb : p.B + n0;
+    // K segments (SEGK): slab k of segment s reads A_s / B_s at k - s * kts.
+    // The address is segment 0's plus a delta selected by integer masks, so
+    // the main loop stays one branch-free instruction stream (a branch there
+    // moves the accumulators out of registers).  Up to three segments; with
+    // two, k never reaches 2 * kts.
+    const int kts = SEGK ? p.k_seg / BK : KT;
+    long long da1 = 0, da2 = 0, db1 = 0, db2 = 0;  // in floats
+    if constexpr (SEGK) {
+        auto delta = [](const float* seg, const float* base) {
+            return (long long)((reinterpret_cast<intptr_t>(seg) -
+                                reinterpret_cast<intptr_t>(base)) / (intptr_t)sizeof(float));
+        };
+        const long long am0 = TA ? m0 : (long long)m0 * p.lda;
+        const long long bn0 = TB ? (long long)n0 * p.ldb : n0;
+        da1 = delta(p.A1 + am0, a_base) - (long long)kts * a_kstride;
+        db1 = delta(p.B1 + bn0, b_base) - (long long)kts * b_kstride;
+        if (p.A2) {
+            da2 = delta(p.A2 + am0, a_base) - 2LL * kts * a_kstride - da1;
+            db2 = delta(p.B2 + bn0, b_base) - 2LL * kts * b_kstride - db1;
+        }
+    }
 
     vacc acc[FM][FN];
 #pragma unroll
@@ -514,8 +535,16 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
 
     auto issue = [&](int k_slab, int stage) {
         float* d = smem + stage * STAGE;
-        dma_a.load(d, a_base + k_slab * a_kstride, p.lda, wave);
-        dma_b.load(d + A_ELEMS, b_base + k_slab * b_kstride, p.ldb, wave);
+        if constexpr (SEGK) {
+            const long long m1 = -(long long)(k_slab >= kts);
+            const long long m2 = -(long long)(k_slab >= 2 * kts);
+            dma_a.load(d, a_base + k_slab * a_kstride + (da1 & m1) + (da2 & m2), p.lda, wave);
+            dma_b.load(d + A_ELEMS, b_base + k_slab * b_kstride + (db1 & m1) + (db2 & m2), p.ldb,
+                       wave);
+        } else {
+            dma_a.load(d, a_base + k_slab * a_kstride, p.lda, wave);
+            dma_b.load(d + A_ELEMS, b_base + k_slab * b_kstride, p.ldb, wave);
+        }
     };
     auto frags = [&](int stage, int chunk, int slot) {
         rd_a.load(smem_all, stage, chunk, fa[slot]);
@@ -749,10 +778,10 @@ __device__ __forceinline__ void gemm_body_x(const GemmArgs& p, int logical) {
 }
 
 template <int BM, int BN, int BK, bool TA, bool TB, bool EPI, int WM = 2, int WN = 2,
-          bool STATS = false, bool ROWSUB = false>
+          bool STATS = false, bool ROWSUB = false, bool SEGK = false>
 __device__ __forceinline__ void gemm_single_x(const GemmArgs& p) {
-    gemm_body_x<BM, BN, BK, TA, TB, EPI, WM, WN, STATS, ROWSUB>(p,
-                                                                xcd_logical(blockIdx.x, gridDim.x));
+    gemm_body_x<BM, BN, BK, TA, TB, EPI, WM, WN, STATS, ROWSUB, SEGK>(
+        p, xcd_logical(blockIdx.x, gridDim.x));
 }
 
 template <int BM, int BN, int BK, bool TA, bool TB, int WM = 2, int WN = 2>

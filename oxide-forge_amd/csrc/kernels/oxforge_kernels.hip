@@ -80,6 +80,23 @@ GEMM_ROWSUB_FAMILY(nt, false, true)
 GEMM_ROWSUB_FAMILY(tn, true, false)
 GEMM_ROWSUB_FAMILY(tt, true, true)
 
+// K-segment instances (forge_gemm_<ab>_<tile>_k): the fused epilogue over a
+// sum of two or three products (forge_gemm_sum_f32), each segment's slabs
+// read from its own operands.
+#define GEMM_X_SEGK_KERNEL(NAME, BM, BN, BK, TA, TB)                                \
+    FORGE_KERNEL void __launch_bounds__(256, GEMM_X_OCC(BM, BN, BK)) NAME(GemmArgs p) { \
+        gemm_single_x<BM, BN, BK, TA, TB, true, 2, 2, false, false, true>(p);       \
+    }
+#define GEMM_SEGK_FAMILY(AB, TA, TB)                                                    \
+    GEMM_X_SEGK_KERNEL(forge_gemm_##AB##_128x128x32_x_k, 128, 128, 32, TA, TB)         \
+    GEMM_X_SEGK_KERNEL(forge_gemm_##AB##_128x64x32_x_k, 128, 64, 32, TA, TB)           \
+    GEMM_X_SEGK_KERNEL(forge_gemm_##AB##_64x128x32_x_k, 64, 128, 32, TA, TB)           \
+    GEMM_X_SEGK_KERNEL(forge_gemm_##AB##_64x64x32_x_k, 64, 64, 32, TA, TB)
+GEMM_SEGK_FAMILY(nn, false, false)
+GEMM_SEGK_FAMILY(nt, false, true)
+GEMM_SEGK_FAMILY(tn, true, false)
+GEMM_SEGK_FAMILY(tt, true, true)
+
 // Batched instances (forge_gemm_batch_<ab>_<tile>): several same-shape
 // products per launch, each with its own operands and epilogue.  They serve
 // the Q/K/V projections, forge_gemm_batch_f32 and the K slices of split-K

@@ -976,31 +976,39 @@ Matrix Attention::backward_self(const Matrix& output_gradient, float learning_ra
         owned_result = rt.new_uninit_matrix(residual_gradient.rows(), residual_gradient.cols());
         target = &owned_result;
     }
+    // The epilogue of the product that completes dXp (residual R, and with
+    // `position` the store of dXp and the position step), and its output.
+    auto final_epilogue = [&](forge_slice* out) {
+        forge_gemm_epilogue ep = plain_epilogue();
+        ep.residual = residual_gradient.slice();
+        *out = target->slice();
+        if (position) {
+            ep.pre_out = target->slice();
+            ep.update = 1;
+            ep.update_scale = learning_rate;
+            *out = position->slice();
+        }
+        return ep;
+    };
     auto accumulate_input_gradient = [&](Linear& lin, const Matrix& g, bool last) {
         if (!last) {
             lin.input_gradient_accumulate(g, residual_gradient, rt, nullptr);
             return;
         }
         require(g.cols() == lin.weights().cols(), "gradient.cols() == weights.cols()");
-        forge_gemm_epilogue ep = plain_epilogue();
-        ep.residual = residual_gradient.slice();
-        forge_slice out = target->slice();
-        if (position) {
-            ep.pre_out = target->slice();
-            ep.update = 1;
-            ep.update_scale = learning_rate;
-            out = position->slice();
-        }
+        forge_slice out;
+        const forge_gemm_epilogue ep = final_epilogue(&out);
         rt.gemm_ex(nullptr, false, true, g, lin.weights(), out, g.rows(), lin.weights().rows(),
                    lin.weights().cols(), ep);
     };
     Linear* linears[3] = {&qkv_.query(), &qkv_.key(), &qkv_.value()};
     const Matrix* projected[3] = {&query_gradient, &key_gradient, &value_gradient};
     // With identity projections of one weight shape whose biases (if any)
-    // took their step in the epilogues above, the three weight updates are
-    // one batched launch after the three input gradients.  Each input
-    // gradient reads only its own W, so the order of updates and input
-    // gradients does not change a result.
+    // took their step in the epilogues above, dXp = R + sum_i G_i W_i^T is
+    // one product over three K segments (one read and one write of R's size
+    // instead of three of each), and the three weight updates are one
+    // batched launch after it.  Each input gradient reads only its own W, so
+    // the order of updates and input gradients does not change a result.
     bool batch = true;
     for (int i = 0; i < 3; i++)
         batch = batch && !linears[i]->needs_pre_activation() &&
@@ -1008,10 +1016,22 @@ Matrix Attention::backward_self(const Matrix& output_gradient, float learning_ra
                 linears[i]->weights().rows() == linears[0]->weights().rows() &&
                 linears[i]->weights().cols() == linears[0]->weights().cols();
     if (batch) {
+        forge_slice gs[3], ws[3];
+        for (int i = 0; i < 3; i++) {
+            require(projected[i]->cols() == linears[i]->weights().cols(),
+                    "gradient.cols() == weights.cols()");
+            gs[i] = projected[i]->slice();
+            ws[i] = linears[i]->weights().slice();
+        }
+        forge_slice out;
+        const forge_gemm_epilogue ep = final_epilogue(&out);
+        check(forge_gemm_sum_f32(rt.raw(), nullptr, 0, 1, 3, gs, ws, out, projected[0]->rows(),
+                                 linears[0]->weights().rows(), linears[0]->weights().cols(),
+                                 &ep),
+              "qkv input gradients");
         forge_gemm_problem probs[3];
         for (int i = 0; i < 3; i++) {
             Linear& lin = *linears[i];
-            accumulate_input_gradient(lin, *projected[i], i == 2);
             Matrix* wg = nullptr;
             if (grads) {
                 grads->weights[i] =

@@ -72,8 +72,13 @@ struct GemmArgs {
     float* row_sq;
     float* col_part;
     const float* row_sub;
+    const float* A1;
+    const float* A2;
+    const float* B1;
+    const float* B2;
+    int k_seg;
 };
-static_assert(sizeof(GemmArgs) == 176, "kernel argument layout of forge::GemmArgs");
+static_assert(sizeof(GemmArgs) == 216, "kernel argument layout of forge::GemmArgs");
 
 // Must match forge::GemmBatchArgs in csrc/kernels/gemm.hpp.
 constexpr int GEMM_BATCH_MAX = 8;
@@ -668,12 +673,13 @@ constexpr int kUnguardedCount = 6;
 // as 512 tiles of 64x128 at 139.
 constexpr double kSingleWorkgroupFactor = 0.96;
 
-enum class GemmKind { Plain, Epilogue, Batch, Stats, RowSub };
+enum class GemmKind { Plain, Epilogue, Batch, Stats, RowSub, SegK };
 
 // Kernel that runs a tile: plain NN (forge_gemm_nn_<tile>), fused epilogue
 // (forge_gemm_<ab>_<tile>_e), fused epilogue with row statistics and column
 // sums (forge_gemm_<ab>_<tile>_s), the same with the row subtrahend
-// (forge_gemm_<ab>_<tile>_r) or batched (forge_gemm_batch_<ab>_<tile>).
+// (forge_gemm_<ab>_<tile>_r), fused epilogue over K segments
+// (forge_gemm_<ab>_<tile>_k) or batched (forge_gemm_batch_<ab>_<tile>).
 void gemm_kernel_name(char* out, size_t cap, GemmKind kind, int ta, int tb,
                       const GemmConfig& cfg) {
     if (kind == GemmKind::Batch)
@@ -683,6 +689,7 @@ void gemm_kernel_name(char* out, size_t cap, GemmKind kind, int ta, int tb,
                  kind == GemmKind::Epilogue ? "_e"
                  : kind == GemmKind::Stats  ? "_s"
                  : kind == GemmKind::RowSub ? "_r"
+                 : kind == GemmKind::SegK   ? "_k"
                                             : "");
 }
 
@@ -1532,6 +1539,84 @@ extern "C" forge_status forge_gemm_kernel_name(forge_runtime* rt, int trans_a, i
     }
     if (n < 0 || (size_t)n >= cap) return fail(FORGE_EINVAL, "name buffer of %zu bytes too small", cap);
     return FORGE_OK;
+}
+
+// Copies count operands of rows x cols (row-major, pitch cols) side by side
+// into dst [rows, count * cols] (concatenation along the columns).
+static forge_status concat_cols(forge_runtime* rt, forge_stream* s, float* dst,
+                                const forge_slice* src, size_t count, size_t rows, size_t cols) {
+    for (size_t z = 0; z < count; z++)
+        HIP_TRY(hipMemcpy2DAsync(dst + z * cols, count * cols * sizeof(float), src[z].ptr,
+                                 cols * sizeof(float), cols * sizeof(float), rows,
+                                 hipMemcpyDeviceToDevice, pick(rt, s)->stream));
+    return FORGE_OK;
+}
+
+extern "C" forge_status forge_gemm_sum_f32(forge_runtime* rt, forge_stream* s, int trans_a,
+                                           int trans_b, size_t count, const forge_slice* A,
+                                           const forge_slice* B, forge_slice C, size_t M,
+                                           size_t N, size_t K, const forge_gemm_epilogue* ep) {
+    if (!rt) return fail(FORGE_EINVAL, "runtime is null");
+    if (count < 1 || count > 3) return fail(FORGE_EINVAL, "gemm_sum count %zu is not 1-3", count);
+    if (!A || !B) return fail(FORGE_EINVAL, "gemm_sum operands are null");
+    const int ta = trans_a != 0, tb = trans_b != 0;
+    GemmArgs a{};
+    bool aligned = true;
+    for (size_t z = 0; z < count; z++) {
+        GemmArgs az{};
+        bool al = false;
+        FORGE_TRY(gemm_args(ta, tb, A[z], B[z], C, M, N, K, ep, &az, &al));
+        aligned = aligned && al;
+        if (z == 0) a = az;
+    }
+    if (count == 1 || M == 0 || N == 0)
+        return gemm_dispatch(rt, s, ta, tb, A[0], B[0], C, M, N, K, ep, false);
+    const size_t Kt = count * K;
+    if (!fits_int(Kt)) return fail(FORGE_EINVAL, "gemm_sum K exceeds 2^31-1");
+    // One launch over the K segments when an unguarded tile takes the whole
+    // product unsplit, with no statistics in its epilogue; else the
+    // operands are concatenated along K and the product runs as one GEMM.
+    // Both give the result of forge_gemm_ex_f32 on the concatenation.
+    if (M && N && aligned && K % 32 == 0 && !gemm_has_stats(ep)) {
+        const GemmConfig* split_cfg = nullptr;
+        if (choose_splits(rt, ta, tb, M, N, Kt, true, &split_cfg) == 1) {
+            const GemmPlan plan = choose_gemm(rt, ta, tb, M, N, Kt, true, GemmKind::SegK);
+            if (plan.cfg != &kGuard64) {
+                const GemmConfig& cfg = *plan.cfg;
+                a.K = (int)Kt;
+                a.k_seg = (int)K;
+                a.A1 = A[1].ptr;
+                a.B1 = B[1].ptr;
+                a.A2 = count > 2 ? A[2].ptr : nullptr;
+                a.B2 = count > 2 ? B[2].ptr : nullptr;
+                char name[96];
+                gemm_kernel_name(name, sizeof name, GemmKind::SegK, ta, tb, cfg);
+                size_t shmem = 0;
+                if (plan.cap) FORGE_TRY(occupancy_cap_shmem(rt, name, plan.cap, &shmem));
+                const unsigned tiles = (unsigned)((M / cfg.bm) * (N / cfg.bn));
+                void* args[] = {&a};
+                return launch(rt, s, name, dim3(tiles), dim3(cfg.threads), shmem, args);
+            }
+        }
+    }
+    // Concatenation along K: op(A) [M, K] segments side by side (rows of A
+    // stacked when A is stored transposed), op(B) [K, N] segments stacked
+    // (side by side when B is stored transposed).
+    forge_slice ac{}, bc{};
+    FORGE_TRY(forge_alloc(rt, Kt * M, &ac));
+    FORGE_TRY(forge_alloc(rt, Kt * N, &bc));
+    forge_status st = FORGE_OK;
+    for (size_t z = 0; z < count && st == FORGE_OK; z++) {
+        if (ta) st = forge_memcpy_d2d(rt, s, forge_slice{ac.ptr + z * K * M, K * M}, A[z], K * M);
+        if (!tb && st == FORGE_OK)
+            st = forge_memcpy_d2d(rt, s, forge_slice{bc.ptr + z * K * N, K * N}, B[z], K * N);
+    }
+    if (st == FORGE_OK && !ta) st = concat_cols(rt, s, ac.ptr, A, count, M, K);
+    if (st == FORGE_OK && tb) st = concat_cols(rt, s, bc.ptr, B, count, N, K);
+    if (st == FORGE_OK) st = gemm_dispatch(rt, s, ta, tb, ac, bc, C, M, N, Kt, ep, false);
+    forge_recycle(rt, ac);
+    forge_recycle(rt, bc);
+    return st;
 }
 
 extern "C" forge_status forge_gemm_batch_f32(forge_runtime* rt, forge_stream* s, int trans_a,

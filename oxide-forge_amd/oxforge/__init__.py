@@ -222,6 +222,16 @@ class Runtime:
         call("forge_gemm_ex_f32", self.handle, stream, int(trans_a), int(trans_b), A.slice,
              B.slice, C.slice, M, N, K, byref(ep))
 
+    def gemm_sum(self, As, Bs, C, M, N, K, trans_a=False, trans_b=False, stream=None,
+                 **epilogue) -> None:
+        """forge_gemm_sum_f32: C = epilogue(sum_z op(As[z]) op(Bs[z]))."""
+        n = len(As)
+        arr_a = (_lib.Slice * max(1, n))(*[a.slice for a in As])
+        arr_b = (_lib.Slice * max(1, n))(*[b.slice for b in Bs])
+        ep = _epilogue(**epilogue)
+        call("forge_gemm_sum_f32", self.handle, stream, int(trans_a), int(trans_b), n, arr_a,
+             arr_b, C.slice, M, N, K, byref(ep))
+
     def gemm_batch(self, problems, M, N, K, trans_a=False, trans_b=False, stream=None) -> None:
         """problems: [(A, B, C, dict of gemm_ex epilogue keywords), ...]."""
         arr = (_lib.GemmProblem * max(1, len(problems)))()

@@ -127,6 +127,8 @@ SIGNATURES = {
     "forge_gemm_f32": [RT, ST, Slice, Slice, Slice, c_size_t, c_size_t, c_size_t],
     "forge_gemm_ex_f32": [RT, ST, c_int, c_int, Slice, Slice, Slice, c_size_t, c_size_t,
                           c_size_t, POINTER(GemmEpilogue)],
+    "forge_gemm_sum_f32": [RT, ST, c_int, c_int, c_size_t, POINTER(Slice), POINTER(Slice), Slice,
+                           c_size_t, c_size_t, c_size_t, POINTER(GemmEpilogue)],
     "forge_gemm_f32_tile": [RT, ST, c_char_p, Slice, Slice, Slice, c_size_t, c_size_t,
                             c_size_t],
     "forge_gemm_f32_split": [RT, ST, c_char_p, c_int, Slice, Slice, Slice, c_size_t, c_size_t,

@@ -72,6 +72,9 @@ def dispatcher_kernel_names():
         for tag in tiles + ("64x128x32_x8",):
             names.append(f"forge_gemm_{ab}_{tag}_s")
             names.append(f"forge_gemm_{ab}_{tag}_r")
+        # fused epilogue over K segments (forge_gemm_sum_f32)
+        for tag in tiles:
+            names.append(f"forge_gemm_{ab}_{tag}_k")
     for tag in tiles + ("128x256x32_x", "64x64x16_2x2_g"):
         names.append(f"forge_gemm_nn_{tag}")
     # batched (forge_gemm_batch_f32, Q/K/V and split-K slices): every layout

@@ -1113,6 +1113,64 @@ def test_gemm_epilogue_row_subtrahend(rt, tile, ta, tb):
         run(dA, dB, dY, M, N, K, trans_a=ta, trans_b=tb, row_sub=rt.empty((M - 1,)))
 
 
+def _concat_k(mats, trans):
+    """op(X_z) [rows, K] side by side along K, in the stored layout: stored
+    [rows, K] concatenates columns, stored transposed [K, rows] stacks."""
+    return np.ascontiguousarray(np.concatenate(mats, axis=0 if trans else 1))
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("count", [2, 3])
+def test_gemm_sum_equals_product_of_concatenation(rt, ta, tb, count):
+    """forge_gemm_sum_f32: C = epilogue(sum_z op(A_z) op(B_z)) equals
+    forge_gemm_ex_f32 on the operands concatenated along K bit for bit: on
+    the one-launch K-segment path (256x128, K = 192 per product; bias,
+    residual, GELU and pre-activation store; the SGD update form), and on
+    the concatenating path (a guarded 50x70x33 shape, a 64x128x4096 shape the
+    dispatcher splits in K, and an epilogue with column sums).  The GEMM bar
+    of the f64 sum holds too."""
+    shapes = [(256, 128, 192, "fused"), (256, 128, 192, "update"), (50, 70, 33, "fused"),
+              (64, 128, 4096, "plain"), (256, 128, 192, "colsums")]
+    for M, N, K, mode in shapes:
+        say(f"gemm_sum count={count} ta={ta} tb={tb} {M}x{N}x{K} {mode}")
+        As = [synth.uniform((K, M) if ta else (M, K), 400 + z) for z in range(count)]
+        Bs = [synth.uniform((N, K) if tb else (K, N), 410 + z) for z in range(count)]
+        bias, res = synth.uniform((N,), 420), synth.uniform((M, N), 421)
+        W0 = synth.uniform((M, N), 422)
+        dA, dB = [rt.array(a) for a in As], [rt.array(b) for b in Bs]
+        dAc, dBc = rt.array(_concat_k(As, ta)), rt.array(_concat_k(Bs, not tb))
+        kw = {}
+        if mode == "fused":
+            kw = dict(bias=rt.array(bias), residual=rt.array(res),
+                      activation=oxforge.ACT_GELU)
+        outs = []
+        for run in ("sum", "concat"):
+            C = rt.array(W0) if mode == "update" else rt.empty((M, N))
+            pre = rt.empty((M, N)) if mode == "fused" else None
+            ex = dict(kw)
+            if pre is not None:
+                ex["pre_out"] = pre
+            if mode == "update":
+                ex.update(update=True, update_scale=1e-3)
+            cs = rt.empty((N,)) if mode == "colsums" else None
+            if cs is not None:
+                ex["col_sums_out"] = cs
+            if run == "sum":
+                rt.gemm_sum(dA, dB, C, M, N, K, trans_a=ta, trans_b=tb, **ex)
+            else:
+                rt.gemm_ex(dAc, dBc, C, M, N, count * K, trans_a=ta, trans_b=tb, **ex)
+            outs.append([C.numpy()] + ([pre.numpy()] if pre is not None else []) +
+                        ([cs.numpy()] if cs is not None else []))
+        for a, b in zip(outs[0], outs[1]):
+            assert np.array_equal(a, b), mode
+        if mode == "plain":
+            ref = sum(orc.gemm_f64(a, b, ta, tb) for a, b in zip(As, Bs))
+            assert np.max(np.abs(outs[0][0] - ref)) / np.max(np.abs(ref)) <= 1e-4
+    with pytest.raises(oxforge.ForgeError):  # four products
+        rt.gemm_sum(dA + dA[:4 - count], dB + dB[:4 - count], C, M, N, K, trans_a=ta,
+                    trans_b=tb)
+
+
 U32 = 2.0 ** -24
 
 
