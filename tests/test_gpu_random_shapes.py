@@ -101,6 +101,44 @@ def test_gemm_random_shapes(rt, seed):
             d.recycle()
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_gemm_sum_random_shapes(rt, seed):
+    """forge_gemm_sum_f32 over random shapes, layouts, counts (2 or 3) and
+    epilogues (bias, residual, ReLU): bit for bit forge_gemm_ex_f32 on the
+    operands concatenated along K, whichever path the shape takes (the
+    K-segment launch for tile-aligned shapes, the concatenating one for the
+    rest and for K splits)."""
+    rng = np.random.default_rng(5000 + seed)
+    for case in range(12):
+        aligned = rng.random() < 0.5
+        if aligned:
+            M, N = 64 * int(rng.integers(1, 9)), 64 * int(rng.integers(1, 9))
+            K = 32 * int(rng.integers(1, 40))
+        else:
+            M, N, K = _dim(rng, 300), _dim(rng, 300), _dim(rng, 400)
+        count = int(rng.integers(2, 4))
+        ta, tb = int(rng.integers(0, 2)), int(rng.integers(0, 2))
+        say(f"seed {seed} case {case}: sum of {count} {M}x{N}x{K} ta={ta} tb={tb}")
+        As = [synth.uniform((K, M) if ta else (M, K), seed * 100 + case * 7 + z)
+              for z in range(count)]
+        Bs = [synth.uniform((N, K) if tb else (K, N), seed * 100 + case * 7 + 50 + z)
+              for z in range(count)]
+        Ac = np.ascontiguousarray(np.concatenate(As, axis=0 if ta else 1))
+        Bc = np.ascontiguousarray(np.concatenate(Bs, axis=1 if tb else 0))
+        ep = {}
+        if rng.random() < 0.5:
+            ep["bias"] = rt.array(synth.uniform((N,), 7))
+        if rng.random() < 0.5:
+            ep["residual"] = rt.array(synth.uniform((M, N), 8))
+        ep["activation"] = int(rng.choice([oxforge.ACT_IDENTITY, oxforge.ACT_RELU]))
+        dC1, dC2 = rt.empty((M, N)), rt.empty((M, N))
+        rt.gemm_sum([rt.array(a) for a in As], [rt.array(b) for b in Bs], dC1, M, N, K,
+                    trans_a=bool(ta), trans_b=bool(tb), **ep)
+        rt.gemm_ex(rt.array(Ac), rt.array(Bc), dC2, M, N, count * K, trans_a=bool(ta),
+                   trans_b=bool(tb), **ep)
+        assert np.array_equal(dC1.numpy(), dC2.numpy()), (M, N, K, count, ta, tb)
+
+
 @pytest.mark.parametrize("seed", range(6))
 def test_row_kernels_random_shapes(rt, seed):
     rng = np.random.default_rng(2000 + seed)
