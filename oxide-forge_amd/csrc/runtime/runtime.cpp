@@ -1569,7 +1569,9 @@ extern "C" forge_status forge_gemm_sum_f32(forge_runtime* rt, forge_stream* s, i
         aligned = aligned && al;
         if (z == 0) a = az;
     }
-    if (count == 1 || M == 0 || N == 0)
+    // One product, or an empty one (no rows, columns or K: the epilogue of
+    // zeros), is the plain fused product.
+    if (count == 1 || M == 0 || N == 0 || K == 0)
         return gemm_dispatch(rt, s, ta, tb, A[0], B[0], C, M, N, K, ep, false);
     const size_t Kt = count * K;
     if (!fits_int(Kt)) return fail(FORGE_EINVAL, "gemm_sum K exceeds 2^31-1");

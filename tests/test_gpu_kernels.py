@@ -1169,6 +1169,14 @@ def test_gemm_sum_equals_product_of_concatenation(rt, ta, tb, count):
     with pytest.raises(oxforge.ForgeError):  # four products
         rt.gemm_sum(dA + dA[:4 - count], dB + dB[:4 - count], C, M, N, K, trans_a=ta,
                     trans_b=tb)
+    # one product is the fused product itself; K = 0 gives the epilogue of zeros
+    C1, C2 = rt.empty((M, N)), rt.empty((M, N))
+    rt.gemm_sum(dA[:1], dB[:1], C1, M, N, K, trans_a=ta, trans_b=tb, bias=rt.array(bias))
+    rt.gemm_ex(dA[0], dB[0], C2, M, N, K, trans_a=ta, trans_b=tb, bias=rt.array(bias))
+    assert np.array_equal(C1.numpy(), C2.numpy())
+    empty = [rt.empty((0,)) for _ in range(count)]
+    rt.gemm_sum(empty, empty, C1, M, N, 0, trans_a=ta, trans_b=tb, bias=rt.array(bias))
+    assert np.array_equal(C1.numpy(), np.broadcast_to(bias, (M, N)))
 
 
 U32 = 2.0 ** -24
