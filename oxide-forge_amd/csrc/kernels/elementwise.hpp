@@ -474,7 +474,12 @@ __device__ __forceinline__ void sum_cols_final_v_body(const float* __restrict__ 
 // finish adds the partial rows, needs every workgroup to release its
 // partial row at agent scope first; on gfx950 that release writes back the
 // XCD's L2, and the launch took 25-43 us at [4096,1024] against 7.7 us for
-// the two launches, so the partial rows go through a kernel boundary.
+// the two launches, so the partial rows go through a kernel boundary.  A
+// one-launch form without partial rows, each workgroup owning a strip of 4,
+// 8 or 16 columns over every row (about 256 strips), took 12.0-16.4 us at
+// [4096,1024] and 15.3-20.5 us at [4096,2048] against 7.4 and 9.9 us: its
+// lanes read 16-64 bytes per row, and those narrow strided requests cost
+// more than the boundary.
 constexpr int SUMCOL1_THREADS = 256;
 constexpr int SUMCOL1_COLS = 64;
 constexpr int SUMCOL1_SLOTS = SUMCOL1_THREADS / (SUMCOL1_COLS / 4);

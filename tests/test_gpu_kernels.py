@@ -779,12 +779,14 @@ def test_sum_rows_cols(rt, rows, cols):
 
 
 # The float4 first pass of the column sums (more than 512 rows, 16-byte
-# aligned float4 columns and outputs): a partial last column group (100
-# columns), a short last chunk (1000 rows), a single chunk that stores the
-# sums itself (65600 columns), and the tall shapes.  Repeated calls, and
-# calls on forked streams with their own workspaces, agree bit for bit.
+# aligned float4 columns and outputs): partial last column groups (100, 1500
+# and 2052 columns), a short last chunk (1000 rows), four columns, a single
+# chunk that stores the sums itself (65600 columns), and the tall shapes.
+# Repeated calls, and calls on forked streams with their own workspaces,
+# agree bit for bit.
 @pytest.mark.parametrize("rows,cols", [(1000, 100), (513, 4), (520, 65600), (65536, 1024),
-                                       (4096, 2048)])
+                                       (4096, 2048), (700, 1500), (2000, 2052), (8192, 1024),
+                                       (8193, 1024)])
 def test_sum_cols_float4_first_pass(rt, rows, cols):
     say(f"sum_cols float4 first pass {rows}x{cols}")
     mf = synth.normal((rows, cols), 9)
