@@ -666,7 +666,15 @@ const GemmConfig kGuard64 = {"64x64x16_2x2_g", 64, 64, 16, 256};
 // 0.3-1%.
 const GemmConfig* const kUnguarded[] = {&kTile128x256, &kTile128x128, &kTile128x64,
                                         &kTile64x128, &kTile64x64, &kTile64x128w8};
-const double kTileEfficiency[] = {0.975, 1.0, 0.98, 0.985, 0.94, 1.005};
+// From K = 2048 on, 128x128 scores below 64x128 (tile_efficiency), so
+// longer products whose tiles balance either way take 64x128: in the C5
+// step (K 2048-8192) that measured 11,243 against 11,272 us by kernel trace
+// on one box (two traces each; six of the nine products with K >= 4096
+// gained 2-8 us, the two 4096x8192x2048 products lost 3-7 us) and 11.220
+// against 11.255 ms in six ABBA pairs of bench runs, each pair faster.  Up to K = 1024 128x128 keeps 1.0:
+// the C4 FFN up-projection (K 1024) as 64x128 made the C4 forward about
+// 0.5 us slower in three of four pairs.
+const double kTileEfficiency[] = {0.975, 0.98, 0.98, 0.985, 0.94, 1.005};
 constexpr int kUnguardedCount = 6;
 // A CU that holds a single four-wave workgroup has one wave per SIMD, which
 // hides less: 2048x2048x1024 as 256 tiles of 128x128 runs at 133 TFLOP/s,
@@ -730,6 +738,26 @@ struct GemmPlan {
     int cap;
 };
 
+// Tile i's factor for a product of depth K: kTileEfficiency (128x128 at
+// 1.0 up to K = 1024), or the comma-separated factors of $OXFORGE_GEMM_EFF
+// in the order of kUnguarded (a tuning knob).
+double tile_efficiency(int i, size_t K) {
+    static const std::vector<double> env = [] {
+        std::vector<double> v;
+        if (const char* e = getenv("OXFORGE_GEMM_EFF")) {
+            char* end = nullptr;
+            for (const char* p = e; *p; p = *end ? end + 1 : end) {
+                v.push_back(strtod(p, &end));
+                if (end == p) break;
+            }
+        }
+        return v;
+    }();
+    if ((size_t)i < env.size()) return env[(size_t)i];
+    if (kUnguarded[i] == &kTile128x128 && K <= 1024) return 1.0;
+    return kTileEfficiency[i];
+}
+
 // Tile choice: the best efficiency x balance over the tiles and, for each,
 // the number c of workgroups a CU may hold (from what fits down to one).
 // t tiles that all fit at once (t <= CUs * c) spread over the CUs, balance
@@ -740,11 +768,12 @@ struct GemmPlan {
 // a single four-wave workgroup scores kSingleWorkgroupFactor less (an
 // eight-wave one does not: it has two waves per SIMD).  Ties go to the
 // larger tile, then to the larger c.  Results on the C3-C5 shapes: plain
-// 4096^3 and 8192x1024x4096 -> the eight-wave 64x128; fused 2048x4096 and
-// the C5 products -> 128x128; 2048x2048 and 2048x1024 products -> 64x128
-// (the three C4 Q/K/V products of one batch: 768 tiles at three per CU).  Unaligned shapes and shapes the
-// tiles do not divide take the bounds-guarded 64x64 tile.  `count`
-// same-shape products share the launch (kind Batch).
+// 4096^3 and 8192x1024x4096 -> the eight-wave 64x128; the C4 FFN
+// up-projection -> 128x128; the other fused and batched C4 and C5 products
+// -> 64x128 (the three C4 Q/K/V products of one batch: 768 tiles at three
+// per CU).  Unaligned shapes and shapes the tiles do not
+// divide take the bounds-guarded 64x64 tile.  `count` same-shape products
+// share the launch (kind Batch).
 GemmPlan choose_gemm(forge_runtime* rt, int ta, int tb, size_t M, size_t N, size_t K,
                      bool aligned, GemmKind kind, size_t count = 1) {
     const size_t cus = rt->cu_count > 0 ? (size_t)rt->cu_count : 256;
@@ -768,7 +797,7 @@ GemmPlan choose_gemm(forge_runtime* rt, int ta, int tb, size_t M, size_t N, size
             // (an eight-wave workgroup alone on a CU still has two waves per SIMD)
             const bool single = g.threads == 256 && occ > 1 && (c == 1 || per_cu == 1);
             const double score =
-                kTileEfficiency[i] * balance * (single ? kSingleWorkgroupFactor : 1.0);
+                tile_efficiency(i, K) * balance * (single ? kSingleWorkgroupFactor : 1.0);
             if (score > best_score + 1e-9) {
                 best = {&g, c == occ ? 0 : c};
                 best_score = score;
