@@ -663,7 +663,10 @@ const GemmConfig kGuard64 = {"64x64x16_2x2_g", 64, 64, 16, 256};
 // both ways) and the C5 step 0.5% slower (11.54 against 11.48 ms); batched
 // Q/K/V lost 7% (98.3 against 92.0 us at C4), and TN products, whose
 // transposed A it reads 32 bits at a time (16-row wave sub-tiles), lost
-// 0.3-1%.
+// 0.3-1%.  Measured again with the fused NN and NT products (not TN, not
+// the K-segmented one) on the eight-wave tile, in ABBA pairs on one box:
+// C4 0.5393-0.5397 against 0.5165-0.5191 ms, C5 11.266-11.301 against
+// 11.224-11.287 ms.
 const GemmConfig* const kUnguarded[] = {&kTile128x256, &kTile128x128, &kTile128x64,
                                         &kTile64x128, &kTile64x64, &kTile64x128w8};
 // From K = 2048 on, 128x128 scores below 64x128 (tile_efficiency), so
