@@ -676,7 +676,9 @@ const GemmConfig* const kUnguarded[] = {&kTile128x256, &kTile128x128, &kTile128x
 // gained 2-8 us, the two 4096x8192x2048 products lost 3-7 us) and 11.220
 // against 11.255 ms in six ABBA pairs of bench runs, each pair faster.  Up to K = 1024 128x128 keeps 1.0:
 // the C4 FFN up-projection (K 1024) as 64x128 made the C4 forward about
-// 0.5 us slower in three of four pairs.
+// 0.5 us slower in three of four pairs.  Two variants measured within the
+// noise of eight pairs each: 128x128 at 1.0 up to K = 2048 (C5 -7 us), and
+// the batched C5 products held to two workgroups per CU (-6 us).
 const double kTileEfficiency[] = {0.975, 0.98, 0.98, 0.985, 0.94, 1.005};
 constexpr int kUnguardedCount = 6;
 // A CU that holds a single four-wave workgroup has one wave per SIMD, which
