@@ -226,7 +226,7 @@ __device__ __forceinline__ void row_kernel_reg(const RowArgs& a) {
     }
 
     // Non-temporal stores from STREAM_NT_MIN on, or at any size when the
-    // host asks (RowArgs::nt_stores: the softmax and RMSNorm forward).
+    // host asks (RowArgs::nt_stores: the forward kernels).
     const bool nt = a.nt_stores || (long long)a.rows * cols >= STREAM_NT_MIN;
     // Prefetch the next row when a wave walks several rows (the partial
     // kernels, whose grid is capped at one workgroup per CU).  Wider

@@ -1302,12 +1302,15 @@ forge_status row_launch(forge_runtime* rt, forge_stream* s, const char* op, RowA
             FORGE_TRY(forge_fill(rt, s, forge_slice{a.dot, (size_t)a.rows}, 0.0f));
         return FORGE_OK;
     }
-    // The softmax and RMSNorm forward kernels store non-temporally at every
-    // size: at [4096,1024] softmax 7.29 -> 6.32 us and RMSNorm 7.86 ->
-    // 7.15 us; LayerNorm forward was unchanged and the backward kernels
-    // 1-2% slower with it, so they, like everything else, store
-    // non-temporally from 64 MiB on.
-    a.nt_stores = (strcmp(op, "softmax") == 0 || strcmp(op, "rms_norm") == 0) ? 1 : 0;
+    // The forward kernels store non-temporally at every size: at
+    // [4096,1024] softmax 7.29 -> 6.32 us, RMSNorm 7.86 -> 7.15 us, and
+    // LayerNorm (with gamma/beta staged in LDS) 7.65-7.68 -> 6.89-6.90 us,
+    // 14.8 -> 13.4 us at [4096,2048].  The backward kernels, like
+    // everything else, store non-temporally from 64 MiB on: at [4096,1024]
+    // non-temporal stores made the softmax backward 0.3 us slower and the
+    // norm backward kernels at most 0.2 us faster.
+    a.nt_stores = (strcmp(op, "softmax") == 0 || strcmp(op, "rms_norm") == 0 ||
+                   strcmp(op, "layer_norm") == 0) ? 1 : 0;
     a.lds_params =
         (strcmp(op, "layer_norm") == 0 && (long long)a.rows * a.cols < kRowLdsParamsMax) ? 1 : 0;
     const ColSumOut og{dgamma, sgd.gamma, sgd.lr}, ob{dbeta, sgd.beta, sgd.lr};
