@@ -1290,6 +1290,9 @@ struct NormSgd {
     float lr = 0.0f;
 };
 
+// Elements from which the norm backward kernels store non-temporally.
+constexpr long long kNormBwdNtMin = 8ll << 20;
+
 forge_status row_launch(forge_runtime* rt, forge_stream* s, const char* op, RowArgs a,
                         float* dgamma, float* dbeta, float* scratch = nullptr,
                         size_t scratch_len = 0, NormSgd sgd = NormSgd()) {
@@ -1306,11 +1309,16 @@ forge_status row_launch(forge_runtime* rt, forge_stream* s, const char* op, RowA
     // [4096,1024] softmax 7.29 -> 6.32 us, RMSNorm 7.86 -> 7.15 us, and
     // LayerNorm (with gamma/beta staged in LDS) 7.65-7.68 -> 6.89-6.90 us,
     // 14.8 -> 13.4 us at [4096,2048].  The backward kernels, like
-    // everything else, store non-temporally from 64 MiB on: at [4096,1024]
-    // non-temporal stores made the softmax backward 0.3 us slower and the
-    // norm backward kernels at most 0.2 us faster.
+    // everything else, store non-temporally from 64 MiB on, the norm
+    // backward kernels from 32 MiB: at [4096,2048] (with dgamma/dbeta) the
+    // LayerNorm backward took 25.3 against 27.2 us with them and the RMSNorm
+    // backward 22.6 against 24.6 us, at [4096,1024] 14.9 against 14.5 and
+    // 13.4 against 13.0 us; the softmax backward was 0.3 us slower at
+    // [4096,1024].
     a.nt_stores = (strcmp(op, "softmax") == 0 || strcmp(op, "rms_norm") == 0 ||
-                   strcmp(op, "layer_norm") == 0) ? 1 : 0;
+                   strcmp(op, "layer_norm") == 0 ||
+                   (strstr(op, "norm_bwd") && (long long)a.rows * a.cols >= kNormBwdNtMin))
+                      ? 1 : 0;
     a.lds_params =
         (strcmp(op, "layer_norm") == 0 && (long long)a.rows * a.cols < kRowLdsParamsMax) ? 1 : 0;
     const ColSumOut og{dgamma, sgd.gamma, sgd.lr}, ob{dbeta, sgd.beta, sgd.lr};
