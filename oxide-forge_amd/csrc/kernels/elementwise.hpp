@@ -671,6 +671,11 @@ __device__ __forceinline__ void reduce_body(const float* __restrict__ x, long lo
 // (about 5.2 against 4.8 TB/s at [8192, 4096]); TC = 64 serves every other
 // shape, GUARD for edges and unaligned views.
 constexpr int TR_ROWS = 64;
+// Transposes from TR_NT_MIN floats (16 MiB) on store non-temporally: at
+// [8192, 4096] 39.9-40.0 us against 51.1-51.3 us with cached stores (and
+// 42.7-43.0 us with non-temporal loads instead, 49.9-50.5 us with both), in
+// three rounds on one device.  Smaller ones keep cached stores.
+constexpr long long TR_NT_MIN = 4ll << 20;
 
 template <int TC, bool GUARD>
 __device__ __forceinline__ void transpose_body(const float* __restrict__ in,
@@ -685,6 +690,7 @@ __device__ __forceinline__ void transpose_body(const float* __restrict__ in,
     const int r0 = tr * TR_ROWS, c0 = tc * TC;
     const int sub = t & 15;  // float4 slot inside 64 columns
     const int rr = t >> 4;   // 0..15
+    const bool nt = (long long)rows * cols >= TR_NT_MIN;
     float4 v[4 * Q];
 #pragma unroll
     for (int i = 0; i < 4 * Q; i++) {
@@ -719,7 +725,7 @@ __device__ __forceinline__ void transpose_body(const float* __restrict__ in,
         w.w = tile[(lr + 3) * P + lc];
         const int orow = c0 + lc, ocol = r0 + lr;
         if constexpr (!GUARD) {
-            *reinterpret_cast<float4*>(out + (long long)orow * rows + ocol) = w;
+            store_f4(out + (long long)orow * rows + ocol, w, nt);
         } else if (orow < cols) {
             float* p = out + (long long)orow * rows + ocol;
             if (ocol + 0 < rows) p[0] = w.x;
